@@ -1,0 +1,178 @@
+/*
+ * lq8.h -- C ABI of the MI355X (gfx950) Q8_0 quantized-weight path.
+ *
+ * Drop-in boundary for lluda-inference's linear layers.  Each entry point
+ * names the reference interface it replaces (paths relative to the
+ * reference crate root, lluda-inference/).  Plain pointers and sizes only.
+ *
+ * Conventions
+ *   - Every function returns lq8_status; on failure lq8_last_error() holds a
+ *     message for the calling thread.  There is never a silent CPU fallback
+ *     (GPU_DESIGN_PRINCIPLES.md:5-45): no device -> LQ8_ERR_NO_DEVICE.
+ *   - Q8_0 host blocks are GGUF block_q8_0: 2-byte little-endian f16 scale d
+ *     followed by 32 int8 codes (34 bytes per 32 values).  Value = d * q.
+ *   - A weight W is [n_out, k_in] row-major, as Linear stores it
+ *     (src/attention.rs:30-35); linear forward computes y = x W^T.
+ *   - *_device functions take device pointers and enqueue on the context's
+ *     stream without synchronizing; the others take host pointers and block.
+ *   - One context = one HIP stream.  Calls on one context must not overlap
+ *     from several threads; distinct contexts are independent.  Weight
+ *     handles are immutable after upload.
+ */
+#ifndef LQ8_H
+#define LQ8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Mirrors LludaError kinds (src/error.rs:17-97). */
+typedef enum {
+    LQ8_OK = 0,
+    LQ8_ERR_SHAPE_MISMATCH = 1,   /* LludaError::ShapeMismatch */
+    LQ8_ERR_DTYPE_MISMATCH = 2,   /* LludaError::DTypeMismatch */
+    LQ8_ERR_DIM_OUT_OF_RANGE = 3, /* LludaError::DimOutOfRange */
+    LQ8_ERR_INVALID_ARG = 4,      /* LludaError::Msg (bad argument, null, stale handle) */
+    LQ8_ERR_NO_DEVICE = 5,        /* GPU init failure (src/gpu/mod.rs:167-174 panics; here an error) */
+    LQ8_ERR_DEVICE = 6,           /* HIP runtime error */
+    LQ8_ERR_OUT_OF_MEMORY = 7,
+    LQ8_ERR_MODEL = 8             /* LludaError::Model */
+} lq8_status;
+
+typedef struct lq8_ctx lq8_ctx;
+typedef struct lq8_weight lq8_weight;
+typedef struct lq8_model lq8_model;
+
+#define LQ8_QK 32
+#define LQ8_BLOCK_BYTES 34
+
+/* ---- library / errors ------------------------------------------------- */
+const char* lq8_version(void);
+/* Thread-local message of the last failure (src/error.rs Display). */
+const char* lq8_last_error(void);
+lq8_status lq8_device_count(int* count);
+
+/* ---- host Q8_0 format (no device needed) -------------------------------
+ * Replaces: the planned GGUF Q8_0 quantizer
+ * (docs/architecture/arch-2026-01-31-qwen3-omni-q8-rust.md:36-39,275-279). */
+size_t lq8_q8_0_bytes(size_t n);
+lq8_status lq8_quantize_q8_0(const float* x, size_t n, void* blocks_out);
+lq8_status lq8_dequantize_q8_0(const void* blocks, size_t n, float* y);
+
+/* ---- context -----------------------------------------------------------
+ * Replaces: gpu::get_context / init (src/gpu/mod.rs:129-178). */
+lq8_status lq8_init(int device, lq8_ctx** out);
+lq8_status lq8_shutdown(lq8_ctx* ctx);
+lq8_status lq8_synchronize(lq8_ctx* ctx);
+lq8_status lq8_device_alloc(lq8_ctx* ctx, size_t bytes, void** dptr);
+lq8_status lq8_device_free(lq8_ctx* ctx, void* dptr);
+lq8_status lq8_copy_to_device(lq8_ctx* ctx, void* dst, const void* src, size_t bytes);
+lq8_status lq8_copy_to_host(lq8_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* HIP-event timer on the context stream (the reference's PROFILE timings,
+ * src/tensor.rs:824-885, measured on the device instead of wall clock). */
+lq8_status lq8_timer_start(lq8_ctx* ctx);
+lq8_status lq8_timer_stop(lq8_ctx* ctx, float* elapsed_ms);
+
+/* ---- weights -----------------------------------------------------------
+ * Replaces: Linear::new (src/attention.rs:63-71) taking ownership of a
+ * weight Tensor; here the weight is uploaded once and repacked into the
+ * device layout (the reference re-uploads per call, src/gpu/gemv.rs:347-411). */
+lq8_status lq8_weight_upload(lq8_ctx* ctx, const void* blocks, size_t n_out, size_t k_in, lq8_weight** out);
+/* Quantizes f32 [n_out, k_in] on the device (bit-exact with lq8_quantize_q8_0). */
+lq8_status lq8_weight_quantize_upload(lq8_ctx* ctx, const float* w, size_t n_out, size_t k_in, lq8_weight** out);
+/* Device N(0, std) weights from a counter-based generator, quantized on the device. */
+lq8_status lq8_weight_random(lq8_ctx* ctx, size_t n_out, size_t k_in, uint64_t seed, uint64_t stream, float std,
+                             lq8_weight** out);
+lq8_status lq8_weight_download(lq8_ctx* ctx, const lq8_weight* w, void* blocks_out);
+lq8_status lq8_weight_shape(const lq8_weight* w, size_t* n_out, size_t* k_in);
+lq8_status lq8_weight_free(lq8_weight* w);
+
+/* ---- device quantize / dequantize ---------------------------------------
+ * Activation quantizer of the W8A8 path, as a standalone op: d_x f32 [n] ->
+ * d_blocks AoS Q8_0 on the device.  Bit-exact with lq8_quantize_q8_0. */
+lq8_status lq8_quantize_q8_0_device(lq8_ctx* ctx, const float* d_x, size_t n, void* d_blocks);
+/* Rows [row0, row0+nrows) of W dequantized to f32 [nrows, k_in]: the
+ * Embedding::forward row gather on a Q8_0 table (src/embedding.rs:137-152). */
+lq8_status lq8_weight_dequantize_rows_device(lq8_ctx* ctx, const lq8_weight* w, size_t row0, size_t nrows,
+                                             float* d_y);
+
+/* ---- linear forward ------------------------------------------------------
+ * Replaces: Linear::forward (src/attention.rs:101-136) and the 2-D
+ * Tensor::matmul it calls (src/tensor.rs:804-817, 898-981, 2716-2753;
+ * GPU: src/gpu/gemv.rs:294, src/gpu/gemm.rs:295).  y[m, n_out] = x[m, k_in] W^T,
+ * f32 in and out.  m == 1: W8A32 GEMV.  m > 1: activations quantized to
+ * Q8_0 per row, W8A8 int8 MFMA GEMM, int32 per block, f32 rescale. */
+lq8_status lq8_linear_forward(lq8_ctx* ctx, const lq8_weight* w, const float* x, size_t m, float* y);
+lq8_status lq8_linear_forward_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m, float* d_y);
+/* The two kernels behind it, callable directly (any m for the GEMM). */
+lq8_status lq8_gemv_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, float* d_y);
+lq8_status lq8_gemm_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m, float* d_y);
+
+/* Independent GEMVs in one launch (routed MoE experts; a batch of linear
+ * layers).  No reference counterpart: the reference runs one matmul per call. */
+typedef struct {
+    const lq8_weight* w;
+    const float* x; /* device, k_in floats */
+    float* y;       /* device, n_out floats */
+} lq8_gemv_problem;
+lq8_status lq8_gemv_grouped_device(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t count);
+
+/* Benchmark harness (examples/benchmark_gemv.rs:13-99 measured on the device):
+ * runs `reps` passes over the problems on the context stream and returns the
+ * device time in ms.  mode 0: one launch per problem; 1: one grouped launch
+ * per pass; 2: mode 0 replayed from a HIP graph; 3: per-launch HIP-event
+ * pairs, returning the sum of the launches' own intervals. */
+lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t count, int mode, int reps,
+                          float* ms);
+
+/* ---- Qwen3 model ---------------------------------------------------------
+ * Replaces: Qwen3ForCausalLM::load/forward/clear_kv_cache
+ * (src/model.rs:273-302, 345-372, 396-398) and generate() with greedy
+ * sampling (src/generate.rs:611-664, 153-174). */
+typedef struct {
+    uint32_t vocab_size, hidden_size, intermediate_size, num_layers;
+    uint32_t num_heads, num_kv_heads, head_dim, max_positions;
+    float rms_norm_eps;
+    double rope_theta;
+} lq8_qwen3_config;
+
+/* Tensor table (host pointers), the same order everywhere:
+ *   [0] model.embed_tokens.weight   Q8_0 [vocab, hidden] (tied lm_head)
+ *   [1] model.norm.weight           f32  [hidden]
+ *   layer l, base 2 + 11*l:
+ *   +0 input_layernorm f32 [hidden]   +1 post_attention_layernorm f32 [hidden]
+ *   +2 self_attn.q_norm f32 [head_dim] +3 self_attn.k_norm f32 [head_dim]
+ *   +4 q_proj +5 k_proj +6 v_proj +7 o_proj +8 gate_proj +9 up_proj +10 down_proj (Q8_0)
+ * (weight names: src/model.rs:439-538). */
+size_t lq8_model_tensor_count(const lq8_qwen3_config* cfg);
+lq8_status lq8_model_tensor_bytes(const lq8_qwen3_config* cfg, size_t index, size_t* bytes);
+lq8_status lq8_model_create(lq8_ctx* ctx, const lq8_qwen3_config* cfg, const void* const* tensors,
+                            lq8_model** out);
+/* Random init as HF does: Linear/Embedding N(0, std) from a seeded counter
+ * generator (quantized on the device), RMSNorm weights 1. */
+lq8_status lq8_model_create_random(lq8_ctx* ctx, const lq8_qwen3_config* cfg, uint64_t seed, float std,
+                                   lq8_model** out);
+lq8_status lq8_model_export_tensor(lq8_model* m, size_t index, void* host_out);
+lq8_status lq8_model_clear_kv_cache(lq8_model* m);
+/* logits: host f32 [vocab] for the last position (or NULL). offset must equal
+ * the number of cached positions (prefill_len + generated - 1 in generate()). */
+lq8_status lq8_model_forward(lq8_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits);
+
+typedef struct {
+    double prefill_ms;      /* prompt forward + first token, device time */
+    double decode_ms;       /* the max_new-1 single-token steps, device time */
+    double decode_tokens_per_s;
+    uint32_t used_graph;    /* 1 if the decode step ran as a replayed HIP graph */
+} lq8_gen_stats;
+/* Greedy generation; the token loop stays on the device.  out_tokens: max_new. */
+lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                               uint32_t* out_tokens, lq8_gen_stats* stats);
+lq8_status lq8_model_free(lq8_model* m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LQ8_H */

@@ -1,0 +1,598 @@
+/*
+ * lq8_oracle.c -- CPU oracle for the Q8_0 quantized-weight hot path of
+ * lluda-inference (TEST INFRASTRUCTURE: loaded only by tests/, by
+ * __graft_entry__.smoke() and by bench.py's cpu_baseline leg, always as the
+ * checker, never as the thing shipped or measured as the product).
+ *
+ * What it restates
+ *   - Q8_0 (GGUF block_q8_0: f16 scale + 32 int8 codes, 34 bytes) quantize /
+ *     dequantize.  The reference names this format as its plan
+ *     (README.md:24,32; docs/architecture/arch-2026-01-31-qwen3-omni-q8-rust.md:36-39,275-279)
+ *     and places the arithmetic in candle-core's GGML quantized module
+ *     (arch-2026-01-31-qwen3-bf16-first.md:309-315), which is not vendored.
+ *     Published algorithm restated: amax = max|x| (NaN ignored, as f32::max),
+ *     d = amax/127, id = d ? 1/d : 0, q = round_half_away(x*id) saturated to
+ *     int8 (NaN -> 0), scale stored as f16 (round to nearest even).
+ *   - Linear::forward (lluda-inference/src/attention.rs:101-136) on a Q8_0
+ *     weight: y[m, n] = x[m, :] . W[n, :].  M == 1 is a W8A32 GEMV, M > 1
+ *     quantizes the activation rows and runs a W8A8 GEMM with exact int32 per
+ *     block and an f32 rescale.
+ *   - The Qwen3 decoder numerics around it: RmsNorm (src/rms_norm.rs:123-177,
+ *     bf16 input and output rounding), RoPE (src/rope.rs:77-128,245-303),
+ *     GQA attention (src/attention.rs:318-403, 426-456), softmax
+ *     (src/tensor.rs:1913-1935), SiLU (src/tensor.rs:1955-1990), residual adds
+ *     (src/transformer.rs:180-204), last-token lm_head (src/model.rs:345-372),
+ *     greedy argmax with last-index ties (src/tensor.rs:2451-2480,
+ *     src/generate.rs:153-174, 611-664).
+ *
+ * Canonical orders (the HIP kernels follow exactly these, so results match
+ * bit for bit; the reference's own sums are plain sequential loops, available
+ * here through orc_set_sequential_sums(1) for comparison):
+ *   GEMV   per row: p_b = fmaf-chain over the 32 codes of block b (j = 0..31,
+ *          from 0); blocks are grouped by 8; a_g = fmaf(p_b, d_b, a_g) in block
+ *          order from 0; y = y + a_g in group order from 0.
+ *   GEMM   per (m, n): I_b = exact int32 sum of the 32 code products;
+ *          s_b = f32(dw_b) * f32(dx_b) (exact); a_g = fmaf((float)I_b, s_b, a_g)
+ *          within a group of 8 blocks; y = y + a_g in group order.
+ *   SUM64  (RMSNorm sum of squares, softmax denominator): lane l in 0..63
+ *          accumulates elements l, l+64, l+128, ... in order from 0; then the
+ *          64 partials are folded with distances 32, 16, 8, 4, 2, 1
+ *          (v[l] = v[l] + v[l+d]).
+ *   dot products inside attention (q.k over head_dim, p.v over positions)
+ *          are sequential, exactly as the reference's matmul_4d
+ *          (src/tensor.rs:2846-2915).
+ *   exp    orc_expf: double-precision Cody-Waite reduction + degree-13 Taylor
+ *          polynomial, rounded once to float.  Agrees with a correctly rounded
+ *          expf except in rare last-bit cases.
+ *
+ * Build: gcc -O2 -ffp-contract=off -fno-fast-math (Rust never contracts a*b+c).
+ */
+#include "lq8_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_seq_sums = 0;
+void orc_set_sequential_sums(int on) { g_seq_sums = on ? 1 : 0; }
+
+/* Thread count of the parallel loops (each output is still summed by one
+ * thread in the fixed order, so results do not depend on it). */
+void orc_set_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+
+/* ------------------------------------------------------------------------ */
+/* scalar numerics                                                          */
+/* ------------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* IEEE binary16, round to nearest even, with subnormals, overflow to inf. */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) {
+        if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+        return (uint16_t)(sign | 0x7C00u);
+    }
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* >= 65520 */
+    if (ax >= 0x38800000u) {                                   /* >= 2^-14: normal */
+        uint32_t mant = ax & 0x7FFFFFu;
+        uint32_t e = (ax >> 23) - 127u + 15u;
+        uint32_t h = (e << 10) | (mant >> 13);
+        uint32_t rem = mant & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    if (ax < 0x33000000u) return (uint16_t)sign; /* < 2^-25 */
+    {
+        uint32_t mant = (ax & 0x7FFFFFu) | 0x800000u;
+        int e = (int)(ax >> 23) - 127; /* -25 .. -15 */
+        int s = -e - 1;                /* 14 .. 24 */
+        uint32_t h = mant >> s;
+        uint32_t rem = mant & ((1u << s) - 1u);
+        uint32_t half = 1u << (s - 1);
+        if (rem > half || (rem == half && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    if (e == 0x1Fu) return u2f(sign | 0x7F800000u | (m << 13));
+    if (e == 0) {
+        /* subnormal or zero: m * 2^-24, exact in f32 */
+        float v = (float)m * 5.9604644775390625e-8f;
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* src/bf16.rs:112-131: bits + 0x7FFF + lsb, keep the top 16 bits. */
+float orc_bf16_round(float x) {
+    uint32_t b = f2u(x);
+    uint32_t bias = 0x7FFFu + ((b >> 16) & 1u);
+    return u2f(((b + bias) >> 16) << 16);
+}
+
+/* exp in double, rounded once to float.  Every step is an IEEE operation
+ * (fma, mul, add, rint, ldexp), so any IEEE machine gets the same bits. */
+float orc_expf(float xf) {
+    if (xf != xf) return xf;
+    if (xf > 89.0f) return INFINITY;
+    if (xf < -110.0f) return 0.0f;
+    double x = (double)xf;
+    double k = rint(x * 1.4426950408889634074);
+    double r = fma(-k, 6.93147180369123816490e-01, x);  /* ln2 hi */
+    r = fma(-k, 1.90821492927058770002e-10, r);         /* ln2 lo */
+    double p = 1.0 / 6227020800.0;                       /* 1/13! */
+    p = fma(p, r, 1.0 / 479001600.0);
+    p = fma(p, r, 1.0 / 39916800.0);
+    p = fma(p, r, 1.0 / 3628800.0);
+    p = fma(p, r, 1.0 / 362880.0);
+    p = fma(p, r, 1.0 / 40320.0);
+    p = fma(p, r, 1.0 / 5040.0);
+    p = fma(p, r, 1.0 / 720.0);
+    p = fma(p, r, 1.0 / 120.0);
+    p = fma(p, r, 1.0 / 24.0);
+    p = fma(p, r, 1.0 / 6.0);
+    p = fma(p, r, 0.5);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    return (float)ldexp(p, (int)k);
+}
+
+void orc_f32_to_f16_n(const float* x, uint16_t* h, size_t n) { for (size_t i = 0; i < n; i++) h[i] = orc_f32_to_f16(x[i]); }
+void orc_f16_to_f32_n(const uint16_t* h, float* x, size_t n) { for (size_t i = 0; i < n; i++) x[i] = orc_f16_to_f32(h[i]); }
+void orc_bf16_round_n(const float* x, float* y, size_t n) { for (size_t i = 0; i < n; i++) y[i] = orc_bf16_round(x[i]); }
+void orc_expf_n(const float* x, float* y, size_t n) { for (size_t i = 0; i < n; i++) y[i] = orc_expf(x[i]); }
+
+/* SUM64 canonical order over v[0..n) (see header comment). */
+static float sum64(const float* v, size_t n) {
+    if (g_seq_sums) {
+        float s = 0.0f;
+        for (size_t i = 0; i < n; i++) s = s + v[i];
+        return s;
+    }
+    float p[64];
+    for (int l = 0; l < 64; l++) {
+        float a = 0.0f;
+        for (size_t i = (size_t)l; i < n; i += 64) a = a + v[i];
+        p[l] = a;
+    }
+    for (int d = 32; d >= 1; d >>= 1)
+        for (int l = 0; l < d; l++) p[l] = p[l] + p[l + d];
+    return p[0];
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q8_0 format                                                              */
+/* ------------------------------------------------------------------------ */
+
+static inline int8_t sat_i8(float v) {
+    if (v != v) return 0;
+    if (v >= 127.0f) return 127;
+    if (v <= -128.0f) return -128;
+    return (int8_t)v;
+}
+
+static void quantize_block(const float* x, uint16_t* d16, int8_t* q, float* d32) {
+    float amax = 0.0f;
+    for (int j = 0; j < ORC_QK; j++) {
+        float v = fabsf(x[j]);
+        if (v > amax) amax = v;
+    }
+    float d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    *d16 = orc_f32_to_f16(d);
+    if (d32) *d32 = d;
+    for (int j = 0; j < ORC_QK; j++) q[j] = sat_i8(roundf(x[j] * id));
+}
+
+int orc_quantize_q8_0(const float* x, size_t n, uint8_t* blocks) {
+    if (n % ORC_QK) return 1;
+    for (size_t b = 0; b < n / ORC_QK; b++) {
+        uint16_t d16;
+        int8_t q[ORC_QK];
+        quantize_block(x + b * ORC_QK, &d16, q, NULL);
+        uint8_t* o = blocks + b * ORC_BLOCK_BYTES;
+        o[0] = (uint8_t)(d16 & 0xFF);
+        o[1] = (uint8_t)(d16 >> 8);
+        memcpy(o + 2, q, ORC_QK);
+    }
+    return 0;
+}
+
+static inline float blk_scale(const uint8_t* blk) {
+    return orc_f16_to_f32((uint16_t)(blk[0] | ((uint16_t)blk[1] << 8)));
+}
+
+int orc_dequantize_q8_0(const uint8_t* blocks, size_t n, float* y) {
+    if (n % ORC_QK) return 1;
+    for (size_t b = 0; b < n / ORC_QK; b++) {
+        const uint8_t* blk = blocks + b * ORC_BLOCK_BYTES;
+        float d = blk_scale(blk);
+        const int8_t* q = (const int8_t*)(blk + 2);
+        for (int j = 0; j < ORC_QK; j++) y[b * ORC_QK + j] = d * (float)q[j];
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q8_0 GEMV (W8A32) and GEMM (W8A8)                                        */
+/* ------------------------------------------------------------------------ */
+
+static float gemv_row(const uint8_t* row, size_t nb, const float* x) {
+    if (g_seq_sums) {
+        /* matmul_2d (src/tensor.rs:2740-2750) over the dequantized row */
+        float s = 0.0f;
+        for (size_t b = 0; b < nb; b++) {
+            const uint8_t* blk = row + b * ORC_BLOCK_BYTES;
+            float d = blk_scale(blk);
+            const int8_t* q = (const int8_t*)(blk + 2);
+            for (int j = 0; j < ORC_QK; j++) s = s + (d * (float)q[j]) * x[b * ORC_QK + j];
+        }
+        return s;
+    }
+    float y = 0.0f;
+    for (size_t g = 0; g < nb; g += ORC_GROUP_BLOCKS) {
+        float a = 0.0f;
+        size_t ge = g + ORC_GROUP_BLOCKS < nb ? g + ORC_GROUP_BLOCKS : nb;
+        for (size_t b = g; b < ge; b++) {
+            const uint8_t* blk = row + b * ORC_BLOCK_BYTES;
+            const int8_t* q = (const int8_t*)(blk + 2);
+            const float* xb = x + b * ORC_QK;
+            float p = 0.0f;
+            for (int j = 0; j < ORC_QK; j++) p = fmaf((float)q[j], xb[j], p);
+            a = fmaf(p, blk_scale(blk), a);
+        }
+        y = y + a;
+    }
+    return y;
+}
+
+int orc_gemv_q8_0(const uint8_t* w, size_t n_out, size_t k_in, const float* x, float* y) {
+    if (k_in == 0 || k_in % ORC_QK || n_out == 0) return 1;
+    size_t nb = k_in / ORC_QK;
+    long long nn = (long long)n_out;
+#pragma omp parallel for schedule(static)
+    for (long long n = 0; n < nn; n++) y[n] = gemv_row(w + (size_t)n * nb * ORC_BLOCK_BYTES, nb, x);
+    return 0;
+}
+
+int orc_gemm_q8_0(const uint8_t* w, size_t n_out, size_t k_in, const float* x, size_t m, float* y) {
+    if (k_in == 0 || k_in % ORC_QK || n_out == 0 || m == 0) return 1;
+    size_t nb = k_in / ORC_QK;
+    /* activation rows -> Q8_0 (codes + f16 scales), same quantizer as weights */
+    int8_t* xq = (int8_t*)malloc(m * k_in);
+    float* xd = (float*)malloc(m * nb * sizeof(float));
+    if (!xq || !xd) { free(xq); free(xd); return 2; }
+    for (size_t r = 0; r < m; r++)
+        for (size_t b = 0; b < nb; b++) {
+            uint16_t d16;
+            quantize_block(x + r * k_in + b * ORC_QK, &d16, xq + r * k_in + b * ORC_QK, NULL);
+            xd[r * nb + b] = orc_f16_to_f32(d16);
+        }
+    long long total = (long long)(m * n_out);
+#pragma omp parallel for schedule(static)
+    for (long long t = 0; t < total; t++) {
+        size_t r = (size_t)t / n_out, n = (size_t)t % n_out;
+        const uint8_t* row = w + n * nb * ORC_BLOCK_BYTES;
+        const int8_t* xr = xq + r * k_in;
+        float acc = 0.0f;
+        for (size_t g = 0; g < nb; g += ORC_GROUP_BLOCKS) {
+            float a = 0.0f;
+            size_t ge = g + ORC_GROUP_BLOCKS < nb ? g + ORC_GROUP_BLOCKS : nb;
+            for (size_t b = g; b < ge; b++) {
+                const uint8_t* blk = row + b * ORC_BLOCK_BYTES;
+                const int8_t* q = (const int8_t*)(blk + 2);
+                int32_t isum = 0;
+                for (int j = 0; j < ORC_QK; j++) isum += (int32_t)q[j] * (int32_t)xr[b * ORC_QK + j];
+                float s = blk_scale(blk) * xd[r * nb + b];
+                if (g_seq_sums) acc = acc + (float)isum * s;
+                else a = fmaf((float)isum, s, a);
+            }
+            if (!g_seq_sums) acc = acc + a;
+        }
+        y[r * n_out + n] = acc;
+    }
+    free(xq);
+    free(xd);
+    return 0;
+}
+
+int orc_linear_forward(const uint8_t* w, size_t n_out, size_t k_in, const float* x, size_t m, float* y) {
+    if (m == 1) return orc_gemv_q8_0(w, n_out, k_in, x, y);
+    return orc_gemm_q8_0(w, n_out, k_in, x, m, y);
+}
+
+/* ------------------------------------------------------------------------ */
+/* support ops                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* src/rms_norm.rs:143-176: input rounded to bf16, sum of squares, mean,
+ * inv = 1/sqrt(mean + eps), out = bf16((x*inv)*w). */
+static void rms_norm_row(const float* x, const float* w, size_t dim, float eps, float* y, float* scratch) {
+    for (size_t i = 0; i < dim; i++) {
+        float v = orc_bf16_round(x[i]);
+        scratch[i] = v * v;
+    }
+    float ss = sum64(scratch, dim);
+    float mean = ss / (float)dim;
+    float inv = 1.0f / sqrtf(mean + eps);
+    for (size_t i = 0; i < dim; i++) {
+        float v = orc_bf16_round(x[i]);
+        y[i] = orc_bf16_round((v * inv) * orc_bf16_round(w[i]));
+    }
+}
+
+int orc_rms_norm(const float* x, const float* weight, size_t rows, size_t dim, float eps, float* y) {
+    if (dim == 0) return 1;
+    float* scratch = (float*)malloc(dim * sizeof(float));
+    if (!scratch) return 2;
+    for (size_t r = 0; r < rows; r++) rms_norm_row(x + r * dim, weight, dim, eps, y + r * dim, scratch);
+    free(scratch);
+    return 0;
+}
+
+/* src/rope.rs:77-128: inv_freq[i] = 1/theta^(2i/rope_dim) (f64), each
+ * frequency stored twice, cos/sin evaluated in f64 and cast to f32.
+ * Tables are [max_pos][head_dim/2]. */
+int orc_rope_tables(size_t head_dim, size_t max_pos, double theta, float* cos_t, float* sin_t) {
+    if (head_dim % 4) return 1;
+    size_t rope_dim = head_dim / 2, half = rope_dim / 2;
+    double* inv_freq = (double*)malloc(half * sizeof(double));
+    if (!inv_freq) return 2;
+    for (size_t i = 0; i < half; i++) inv_freq[i] = 1.0 / pow(theta, (double)(2 * i) / (double)rope_dim);
+    for (size_t p = 0; p < max_pos; p++)
+        for (size_t i = 0; i < half; i++) {
+            double f = (double)p * inv_freq[i];
+            float c = (float)cos(f), s = (float)sin(f);
+            cos_t[p * rope_dim + 2 * i] = c;
+            cos_t[p * rope_dim + 2 * i + 1] = c;
+            sin_t[p * rope_dim + 2 * i] = s;
+            sin_t[p * rope_dim + 2 * i + 1] = s;
+        }
+    free(inv_freq);
+    return 0;
+}
+
+/* src/rope.rs:270-297: out[d] = x[d]*c - x[d+R]*s, out[d+R] = x[d+R]*c + x[d]*s
+ * with R = head_dim/2 and c, s taken at column 2*(d/2) of the table.
+ * x is [heads][seq][head_dim]; positions are offset + l. */
+int orc_rope_apply(const float* x, size_t heads, size_t seq, size_t head_dim, const float* cos_t,
+                   const float* sin_t, size_t offset, float* y) {
+    size_t R = head_dim / 2;
+    for (size_t h = 0; h < heads; h++)
+        for (size_t l = 0; l < seq; l++) {
+            const float* xr = x + (h * seq + l) * head_dim;
+            float* yr = y + (h * seq + l) * head_dim;
+            const float* c = cos_t + (offset + l) * R;
+            const float* s = sin_t + (offset + l) * R;
+            for (size_t d = 0; d < R; d++) {
+                float cv = c[d & ~(size_t)1], sv = s[d & ~(size_t)1];
+                float x1 = xr[d], x2 = xr[d + R];
+                yr[d] = x1 * cv - x2 * sv;
+                yr[d + R] = x2 * cv + x1 * sv;
+            }
+        }
+    return 0;
+}
+
+/* src/tensor.rs:1967-1978 (f32 branch). */
+float orc_silu(float x) { return x / (1.0f + orc_expf(-x)); }
+
+/* Iterator::max_by keeps the last of equal maxima (src/tensor.rs:2475-2480). */
+uint32_t orc_argmax_last(const float* x, size_t n) {
+    size_t best = 0;
+    for (size_t i = 1; i < n; i++)
+        if (!(x[i] < x[best])) best = i;
+    return (uint32_t)best;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Qwen3 model (src/model.rs, src/transformer.rs, src/attention.rs, src/mlp.rs) */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    const float *in_norm, *post_norm, *q_norm, *k_norm;
+    const uint8_t *q, *k, *v, *o, *gate, *up, *down;
+} orc_layer;
+
+struct orc_model {
+    orc_qwen3_config c;
+    const uint8_t* embed;
+    const float* final_norm;
+    orc_layer* layers;
+    float *cos_t, *sin_t;
+    float *kc, *vc; /* [layer][kv_head][max_pos][head_dim] */
+    size_t kv_len;
+};
+
+orc_model* orc_model_new(const orc_qwen3_config* cfg, const void* const* t) {
+    orc_model* m = (orc_model*)calloc(1, sizeof(orc_model));
+    if (!m) return NULL;
+    m->c = *cfg;
+    m->embed = (const uint8_t*)t[0];
+    m->final_norm = (const float*)t[1];
+    m->layers = (orc_layer*)calloc(cfg->num_layers, sizeof(orc_layer));
+    size_t hd = cfg->head_dim, R = hd / 2;
+    m->cos_t = (float*)malloc((size_t)cfg->max_positions * R * sizeof(float));
+    m->sin_t = (float*)malloc((size_t)cfg->max_positions * R * sizeof(float));
+    size_t kvsz = (size_t)cfg->num_layers * cfg->num_kv_heads * cfg->max_positions * hd;
+    m->kc = (float*)calloc(kvsz, sizeof(float));
+    m->vc = (float*)calloc(kvsz, sizeof(float));
+    if (!m->layers || !m->cos_t || !m->sin_t || !m->kc || !m->vc) { orc_model_free(m); return NULL; }
+    for (uint32_t l = 0; l < cfg->num_layers; l++) {
+        const void* const* b = t + 2 + 11 * (size_t)l;
+        orc_layer* L = &m->layers[l];
+        L->in_norm = (const float*)b[0]; L->post_norm = (const float*)b[1];
+        L->q_norm = (const float*)b[2]; L->k_norm = (const float*)b[3];
+        L->q = (const uint8_t*)b[4]; L->k = (const uint8_t*)b[5]; L->v = (const uint8_t*)b[6];
+        L->o = (const uint8_t*)b[7]; L->gate = (const uint8_t*)b[8]; L->up = (const uint8_t*)b[9];
+        L->down = (const uint8_t*)b[10];
+    }
+    orc_rope_tables(hd, cfg->max_positions, cfg->rope_theta, m->cos_t, m->sin_t);
+    return m;
+}
+
+void orc_model_free(orc_model* m) {
+    if (!m) return;
+    free(m->layers); free(m->cos_t); free(m->sin_t); free(m->kc); free(m->vc);
+    free(m);
+}
+
+void orc_model_clear_kv_cache(orc_model* m) { m->kv_len = 0; }
+
+/* One q-head attention row: q [hd], visible positions 0..L-1 of kv head kvh.
+ * src/attention.rs:374-394: scores = q.k (sequential over d), * 1/sqrt(hd),
+ * softmax (max, exp(x-max), sum, divide), then p.v sequential over positions. */
+static void attend(const orc_model* m, size_t layer, size_t kvh, const float* q, size_t L, float* out, float* sc) {
+    const orc_qwen3_config* c = &m->c;
+    size_t hd = c->head_dim, P = c->max_positions;
+    const float* K = m->kc + ((layer * c->num_kv_heads + kvh) * P) * hd;
+    const float* V = m->vc + ((layer * c->num_kv_heads + kvh) * P) * hd;
+    float scale = 1.0f / sqrtf((float)hd);
+    float mx = -INFINITY;
+    for (size_t j = 0; j < L; j++) {
+        float s = 0.0f;
+        for (size_t d = 0; d < hd; d++) s = s + q[d] * K[j * hd + d];
+        s = s * scale;
+        sc[j] = s;
+        if (s > mx) mx = s;
+    }
+    for (size_t j = 0; j < L; j++) sc[j] = orc_expf(sc[j] - mx);
+    float sum = sum64(sc, L);
+    for (size_t j = 0; j < L; j++) sc[j] = sc[j] / sum;
+    for (size_t d = 0; d < hd; d++) {
+        float o = 0.0f;
+        for (size_t j = 0; j < L; j++) o = o + sc[j] * V[j * hd + d];
+        out[d] = o;
+    }
+}
+
+int orc_model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits) {
+    const orc_qwen3_config* c = &m->c;
+    if (n == 0) return 1;
+    if (offset != m->kv_len || offset + n > c->max_positions) return 3;
+    size_t Hd = c->hidden_size, I = c->intermediate_size, hd = c->head_dim;
+    size_t NH = c->num_heads, NKV = c->num_kv_heads, P = c->max_positions;
+    size_t QD = NH * hd, KD = NKV * hd, R = hd / 2, groups = NH / NKV;
+    size_t nbh = Hd / ORC_QK;
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= c->vocab_size) return 3;
+
+    float* H = (float*)malloc(n * Hd * sizeof(float));
+    float* X = (float*)malloc(n * (Hd > QD ? Hd : QD) * sizeof(float));
+    float* Q = (float*)malloc(n * QD * sizeof(float));
+    float* K = (float*)malloc(n * KD * sizeof(float));
+    float* Vv = (float*)malloc(n * KD * sizeof(float));
+    float* A = (float*)malloc(n * QD * sizeof(float));
+    float* O = (float*)malloc(n * Hd * sizeof(float));
+    float* G = (float*)malloc(n * I * sizeof(float));
+    float* U = (float*)malloc(n * I * sizeof(float));
+    float* scratch = (float*)malloc((P > Hd ? P : Hd) * sizeof(float) * 2);
+    float* tmp = (float*)malloc(hd * sizeof(float));
+    if (!H || !X || !Q || !K || !Vv || !A || !O || !G || !U || !scratch || !tmp) {
+        free(H); free(X); free(Q); free(K); free(Vv); free(A); free(O); free(G); free(U); free(scratch); free(tmp);
+        return 2;
+    }
+    /* Embedding::forward (src/embedding.rs:137-152): row gather; rows are
+     * dequantized Q8_0, exact in f32. */
+    for (size_t i = 0; i < n; i++)
+        orc_dequantize_q8_0(m->embed + (size_t)ids[i] * nbh * ORC_BLOCK_BYTES, Hd, H + i * Hd);
+
+    for (size_t l = 0; l < c->num_layers; l++) {
+        const orc_layer* L = &m->layers[l];
+        orc_rms_norm(H, L->in_norm, n, Hd, c->rms_norm_eps, X);
+        orc_linear_forward(L->q, QD, Hd, X, n, Q);
+        orc_linear_forward(L->k, KD, Hd, X, n, K);
+        orc_linear_forward(L->v, KD, Hd, X, n, Vv);
+        /* per-head q/k RmsNorm then RoPE (src/attention.rs:350-364) */
+        for (size_t i = 0; i < n; i++) {
+            size_t pos = offset + i;
+            const float* cs = m->cos_t + pos * R;
+            const float* sn = m->sin_t + pos * R;
+            for (size_t h = 0; h < NH + NKV; h++) {
+                int isq = h < NH;
+                float* src = isq ? Q + i * QD + h * hd : K + i * KD + (h - NH) * hd;
+                rms_norm_row(src, isq ? L->q_norm : L->k_norm, hd, c->rms_norm_eps, tmp, scratch);
+                float* dst;
+                if (isq) dst = src;
+                else dst = m->kc + ((l * NKV + (h - NH)) * P + pos) * hd;
+                for (size_t d = 0; d < R; d++) {
+                    float cv = cs[d & ~(size_t)1], sv = sn[d & ~(size_t)1];
+                    float x1 = tmp[d], x2 = tmp[d + R];
+                    dst[d] = x1 * cv - x2 * sv;
+                    dst[d + R] = x2 * cv + x1 * sv;
+                }
+            }
+            for (size_t h = 0; h < NKV; h++)
+                memcpy(m->vc + ((l * NKV + h) * P + pos) * hd, Vv + i * KD + h * hd, hd * sizeof(float));
+        }
+        long long work = (long long)(n * NH);
+#pragma omp parallel
+        {
+            float* sc = (float*)malloc((offset + n) * sizeof(float));
+#pragma omp for schedule(static)
+            for (long long t = 0; t < work; t++) {
+                size_t i = (size_t)t / NH, h = (size_t)t % NH;
+                attend(m, l, h / groups, Q + i * QD + h * hd, offset + i + 1, A + i * QD + h * hd, sc);
+            }
+            free(sc);
+        }
+        orc_linear_forward(L->o, Hd, QD, A, n, O);
+        for (size_t t = 0; t < n * Hd; t++) H[t] = H[t] + O[t];
+        orc_rms_norm(H, L->post_norm, n, Hd, c->rms_norm_eps, X);
+        orc_linear_forward(L->gate, I, Hd, X, n, G);
+        orc_linear_forward(L->up, I, Hd, X, n, U);
+        for (size_t t = 0; t < n * I; t++) G[t] = orc_silu(G[t]) * U[t];
+        orc_linear_forward(L->down, Hd, I, G, n, O);
+        for (size_t t = 0; t < n * Hd; t++) H[t] = H[t] + O[t];
+    }
+    m->kv_len = offset + n;
+    /* final norm of the last position, then lm_head GEMV (src/model.rs:357-371) */
+    orc_rms_norm(H + (n - 1) * Hd, m->final_norm, 1, Hd, c->rms_norm_eps, X);
+    orc_gemv_q8_0(m->embed, c->vocab_size, Hd, X, logits);
+    free(H); free(X); free(Q); free(K); free(Vv); free(A); free(O); free(G); free(U); free(scratch); free(tmp);
+    return 0;
+}
+
+/* src/generate.rs:611-664 with the greedy sampler; no EOS stop. */
+int orc_generate_greedy(orc_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                        uint32_t* out_tokens, float* out_margins) {
+    if (n_prompt == 0 || max_new == 0) return 1;
+    float* logits = (float*)malloc((size_t)m->c.vocab_size * sizeof(float));
+    if (!logits) return 2;
+    orc_model_clear_kv_cache(m);
+    int rc = 0;
+    uint32_t tok = 0;
+    for (size_t t = 0; t < max_new; t++) {
+        if (t == 0) rc = orc_model_forward(m, prompt, n_prompt, 0, logits);
+        else rc = orc_model_forward(m, &tok, 1, n_prompt + t - 1, logits);
+        if (rc) break;
+        tok = orc_argmax_last(logits, m->c.vocab_size);
+        out_tokens[t] = tok;
+        if (out_margins) {
+            float best = logits[tok], second = -INFINITY;
+            for (size_t i = 0; i < m->c.vocab_size; i++)
+                if (i != tok && logits[i] > second) second = logits[i];
+            out_margins[t] = best - second;
+        }
+    }
+    free(logits);
+    return rc;
+}

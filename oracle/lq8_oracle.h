@@ -1,0 +1,85 @@
+/*
+ * lq8_oracle.h -- CPU oracle for the Q8_0 hot path (TEST INFRASTRUCTURE).
+ *
+ * This library is the parity checker.  Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may load it.  The shipped library
+ * (liblq8.so) never links, loads or calls it.
+ *
+ * Every float operation below is written out in a fixed order so that the
+ * HIP kernels, which follow the same orders, reproduce the results bit for
+ * bit.  The orders are documented per function in lq8_oracle.c.
+ */
+#ifndef LQ8_ORACLE_H
+#define LQ8_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORC_QK 32          /* elements per Q8_0 block */
+#define ORC_BLOCK_BYTES 34 /* f16 scale + 32 int8 codes (GGUF block_q8_0) */
+#define ORC_GROUP_BLOCKS 8 /* blocks per accumulation group */
+
+/* ---- scalar numerics ---- */
+uint16_t orc_f32_to_f16(float x);
+float orc_f16_to_f32(uint16_t h);
+float orc_bf16_round(float x);
+float orc_expf(float x);
+void orc_f32_to_f16_n(const float* x, uint16_t* h, size_t n);
+void orc_f16_to_f32_n(const uint16_t* h, float* x, size_t n);
+void orc_bf16_round_n(const float* x, float* y, size_t n);
+void orc_expf_n(const float* x, float* y, size_t n);
+
+/* 0 = canonical orders (what the GPU computes), 1 = the reference's plain
+ * sequential sums.  Global switch, used only to compare the two. */
+void orc_set_sequential_sums(int on);
+void orc_set_threads(int n);
+
+/* ---- Q8_0 format ---- */
+int orc_quantize_q8_0(const float* x, size_t n, uint8_t* blocks);
+int orc_dequantize_q8_0(const uint8_t* blocks, size_t n, float* y);
+
+/* ---- Q8_0 matmul, W[n_out, k_in] in AoS blocks ---- */
+int orc_gemv_q8_0(const uint8_t* w, size_t n_out, size_t k_in, const float* x, float* y);
+int orc_gemm_q8_0(const uint8_t* w, size_t n_out, size_t k_in, const float* x, size_t m, float* y);
+int orc_linear_forward(const uint8_t* w, size_t n_out, size_t k_in, const float* x, size_t m, float* y);
+
+/* ---- support ops ---- */
+int orc_rms_norm(const float* x, const float* weight, size_t rows, size_t dim, float eps, float* y);
+int orc_rope_tables(size_t head_dim, size_t max_pos, double theta, float* cos_t, float* sin_t);
+int orc_rope_apply(const float* x, size_t heads, size_t seq, size_t head_dim, const float* cos_t,
+                   const float* sin_t, size_t offset, float* y);
+float orc_silu(float x);
+uint32_t orc_argmax_last(const float* x, size_t n);
+
+/* ---- Qwen3 model ---- */
+typedef struct {
+    uint32_t vocab_size, hidden_size, intermediate_size, num_layers;
+    uint32_t num_heads, num_kv_heads, head_dim, max_positions;
+    float rms_norm_eps;
+    double rope_theta;
+} orc_qwen3_config;
+
+/* Tensor table order (pointers are copied, not the data):
+ *   [0] embed_tokens Q8_0 [vocab, hidden] (tied lm_head)
+ *   [1] final norm f32 [hidden]
+ *   per layer l, base = 2 + 11*l:
+ *   +0 input_layernorm f32 [hidden]   +1 post_attention_layernorm f32 [hidden]
+ *   +2 q_norm f32 [head_dim]           +3 k_norm f32 [head_dim]
+ *   +4 q_proj Q8_0  +5 k_proj  +6 v_proj  +7 o_proj
+ *   +8 gate_proj    +9 up_proj +10 down_proj                               */
+typedef struct orc_model orc_model;
+orc_model* orc_model_new(const orc_qwen3_config* cfg, const void* const* tensors);
+void orc_model_free(orc_model* m);
+void orc_model_clear_kv_cache(orc_model* m);
+int orc_model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits);
+int orc_generate_greedy(orc_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                        uint32_t* out_tokens, float* out_margins);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,252 @@
+"""ctypes wrapper of the CPU oracle (TEST INFRASTRUCTURE).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, and only as the checker.  The shipped library never uses it.
+Build with ``make -C oracle`` (done by __graft_entry__.build()).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "liblq8_oracle.so")
+
+QK = 32
+BLOCK_BYTES = 34
+
+
+class OrcConfig(C.Structure):
+    _fields_ = [
+        ("vocab_size", C.c_uint32), ("hidden_size", C.c_uint32), ("intermediate_size", C.c_uint32),
+        ("num_layers", C.c_uint32), ("num_heads", C.c_uint32), ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32), ("max_positions", C.c_uint32), ("rms_norm_eps", C.c_float),
+        ("rope_theta", C.c_double),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} not built (make -C oracle)")
+        L = C.CDLL(LIB_PATH)
+        vp, sz = C.c_void_p, C.c_size_t
+        sigs = {
+            "orc_f32_to_f16": (C.c_uint16, [C.c_float]),
+            "orc_f16_to_f32": (C.c_float, [C.c_uint16]),
+            "orc_bf16_round": (C.c_float, [C.c_float]),
+            "orc_expf": (C.c_float, [C.c_float]),
+            "orc_f32_to_f16_n": (None, [vp, vp, sz]),
+            "orc_f16_to_f32_n": (None, [vp, vp, sz]),
+            "orc_bf16_round_n": (None, [vp, vp, sz]),
+            "orc_expf_n": (None, [vp, vp, sz]),
+            "orc_set_sequential_sums": (None, [C.c_int]),
+            "orc_set_threads": (None, [C.c_int]),
+            "orc_quantize_q8_0": (C.c_int, [vp, sz, vp]),
+            "orc_dequantize_q8_0": (C.c_int, [vp, sz, vp]),
+            "orc_gemv_q8_0": (C.c_int, [vp, sz, sz, vp, vp]),
+            "orc_gemm_q8_0": (C.c_int, [vp, sz, sz, vp, sz, vp]),
+            "orc_linear_forward": (C.c_int, [vp, sz, sz, vp, sz, vp]),
+            "orc_rms_norm": (C.c_int, [vp, vp, sz, sz, C.c_float, vp]),
+            "orc_rope_tables": (C.c_int, [sz, sz, C.c_double, vp, vp]),
+            "orc_rope_apply": (C.c_int, [vp, sz, sz, sz, vp, vp, sz, vp]),
+            "orc_silu": (C.c_float, [C.c_float]),
+            "orc_argmax_last": (C.c_uint32, [vp, sz]),
+            "orc_model_new": (vp, [C.POINTER(OrcConfig), vp]),
+            "orc_model_free": (None, [vp]),
+            "orc_model_clear_kv_cache": (None, [vp]),
+            "orc_model_forward": (C.c_int, [vp, vp, sz, sz, vp]),
+            "orc_generate_greedy": (C.c_int, [vp, vp, sz, sz, vp, vp]),
+        }
+        for name, (res, args) in sigs.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return C.c_void_p(a.ctypes.data)
+
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size, dtype=np.uint16)
+    lib().orc_f32_to_f16_n(_p(x), _p(out), x.size)
+    return out
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16).reshape(-1)
+    out = np.empty(h.size, dtype=np.float32)
+    lib().orc_f16_to_f32_n(_p(h), _p(out), h.size)
+    return out
+
+
+def bf16_round(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size, dtype=np.float32)
+    lib().orc_bf16_round_n(_p(x), _p(out), x.size)
+    return out
+
+
+def expf(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size, dtype=np.float32)
+    lib().orc_expf_n(_p(x), _p(out), x.size)
+    return out
+
+
+def set_sequential_sums(on: bool) -> None:
+    lib().orc_set_sequential_sums(1 if on else 0)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def quantize_q8_0(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size // QK * BLOCK_BYTES, dtype=np.uint8)
+    if lib().orc_quantize_q8_0(_p(x), x.size, _p(out)):
+        raise ValueError("n must be a multiple of 32")
+    return out
+
+
+def dequantize_q8_0(blocks, n: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    if lib().orc_dequantize_q8_0(_p(blocks), n, _p(out)):
+        raise ValueError("n must be a multiple of 32")
+    return out
+
+
+def gemv_q8_0(blocks, n_out: int, k_in: int, x) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(n_out, dtype=np.float32)
+    if lib().orc_gemv_q8_0(_p(blocks), n_out, k_in, _p(x), _p(y)):
+        raise ValueError("bad shape")
+    return y
+
+
+def gemm_q8_0(blocks, n_out: int, k_in: int, x) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.size // k_in
+    y = np.empty((m, n_out), dtype=np.float32)
+    if lib().orc_gemm_q8_0(_p(blocks), n_out, k_in, _p(x), m, _p(y)):
+        raise ValueError("bad shape")
+    return y
+
+
+def linear_forward(blocks, n_out: int, k_in: int, x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m = x.size // k_in
+    y = np.empty((m, n_out), dtype=np.float32)
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    if lib().orc_linear_forward(_p(blocks), n_out, k_in, _p(x), m, _p(y)):
+        raise ValueError("bad shape")
+    return y
+
+
+def rms_norm(x, weight, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    dim = w.size
+    y = np.empty_like(x)
+    lib().orc_rms_norm(_p(x), _p(w), x.size // dim, dim, eps, _p(y))
+    return y
+
+
+def rope_tables(head_dim: int, max_pos: int, theta: float):
+    R = head_dim // 2
+    c = np.empty((max_pos, R), dtype=np.float32)
+    s = np.empty((max_pos, R), dtype=np.float32)
+    if lib().orc_rope_tables(head_dim, max_pos, theta, _p(c), _p(s)):
+        raise ValueError("head_dim must be a multiple of 4")
+    return c, s
+
+
+def rope_apply(x, cos_t, sin_t, offset: int) -> np.ndarray:
+    """x: [heads, seq, head_dim]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    h, l, d = x.shape
+    y = np.empty_like(x)
+    lib().orc_rope_apply(_p(x), h, l, d, _p(np.ascontiguousarray(cos_t)), _p(np.ascontiguousarray(sin_t)), offset,
+                         _p(y))
+    return y
+
+
+def silu(x: float) -> float:
+    return lib().orc_silu(x)
+
+
+def argmax_last(x) -> int:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return int(lib().orc_argmax_last(_p(x), x.size))
+
+
+class Model:
+    """Oracle Qwen3ForCausalLM over host tensors in the include/lq8.h table order."""
+
+    def __init__(self, cfg, tensors: Sequence[np.ndarray]):
+        self.cfg = cfg
+        self._keep = [np.ascontiguousarray(t) for t in tensors]
+        arr = (C.c_void_p * len(self._keep))(*[t.ctypes.data for t in self._keep])
+        self._c = OrcConfig(cfg.vocab_size, cfg.hidden_size, cfg.intermediate_size, cfg.num_hidden_layers,
+                            cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim,
+                            cfg.max_position_embeddings, cfg.rms_norm_eps, cfg.rope_theta)
+        self.h = lib().orc_model_new(C.byref(self._c), arr)
+        if not self.h:
+            raise MemoryError("oracle model allocation failed")
+
+    def close(self):
+        if self.h:
+            lib().orc_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def clear_kv_cache(self):
+        lib().orc_model_clear_kv_cache(self.h)
+
+    def forward(self, ids, offset: int) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        logits = np.empty(self.cfg.vocab_size, dtype=np.float32)
+        rc = lib().orc_model_forward(self.h, _p(ids), ids.size, offset, _p(logits))
+        if rc:
+            raise ValueError(f"oracle forward failed ({rc})")
+        return logits
+
+    def generate_greedy(self, prompt, max_new: int):
+        ids = np.ascontiguousarray(prompt, dtype=np.uint32)
+        toks = np.empty(max_new, dtype=np.uint32)
+        margins = np.empty(max_new, dtype=np.float32)
+        rc = lib().orc_generate_greedy(self.h, _p(ids), ids.size, max_new, _p(toks), _p(margins))
+        if rc:
+            raise ValueError(f"oracle generate failed ({rc})")
+        return toks, margins
+
+
+def random_q8_tensors(cfg, seed: int, std: float = 0.02):
+    """Small random model in table order (numpy normal draws, oracle quantizer)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(cfg.tensor_count()):
+        kind, shape = cfg.tensor_shape(i)
+        if kind == "f32":
+            out.append(np.ones(shape, dtype=np.float32))
+        else:
+            w = (rng.standard_normal(shape) * std).astype(np.float32)
+            out.append(quantize_q8_0(w))
+    return out

@@ -1,0 +1,535 @@
+// model.hip -- Qwen3ForCausalLM on Q8_0 weights (src/model.rs, src/transformer.rs,
+// src/attention.rs, src/mlp.rs, src/generate.rs of the reference crate).
+//
+// Weights live once in HBM in the tiled Q8_0 layout.  q/k/v and gate/up are
+// stored as one concatenated weight each (rows are independent, so the
+// results are those of the separate projections).  Decode (one position)
+// runs 6 kernels per layer:
+//   rmsnorm+qkv GEMV | q/k-norm+RoPE+KV append | attention |
+//   o GEMV + residual | rmsnorm+gate/up GEMV | silu*up + down GEMV + residual
+// Prefill (n > 1 positions) quantizes activations and uses the MFMA GEMM.
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "lq8_internal.h"
+
+using namespace lq8;
+
+namespace {
+
+struct Layer {
+    lq8_weight *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
+    float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+};
+
+}  // namespace
+
+struct lq8_model {
+    lq8_ctx* ctx = nullptr;
+    lq8_qwen3_config c{};
+    size_t QD = 0, KD = 0, QKV = 0;
+    lq8_weight* embed = nullptr;
+    float* final_norm = nullptr;
+    std::vector<Layer> layers;
+    float *cos_t = nullptr, *sin_t = nullptr;
+    float *kc = nullptr, *vc = nullptr;  // [layer][kv_head][head_dim][pos] / [layer][kv_head][pos][head_dim]
+    size_t kv_len = 0;
+    // single-position buffers
+    float *h = nullptr, *qkv = nullptr, *qr = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
+    uint32_t* d_ids = nullptr;
+    size_t ids_cap = 0;
+    int *d_pos = nullptr, *d_step = nullptr;
+    uint32_t *d_tok = nullptr, *d_tokens = nullptr;
+    size_t tokens_cap = 0;
+    // prefill buffers, capacity in rows
+    size_t pf_cap = 0;
+    float *P_h = nullptr, *P_x = nullptr, *P_qkv = nullptr, *P_qr = nullptr, *P_attn = nullptr, *P_gu = nullptr,
+          *P_act = nullptr, *P_xs = nullptr;
+    int8_t* P_xq = nullptr;
+    hipGraphExec_t graph = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+};
+
+namespace {
+
+lq8_status validate(const lq8_qwen3_config* c) {
+    if (!c) return fail(LQ8_ERR_INVALID_ARG, "config is null");
+    if (!c->vocab_size || !c->hidden_size || !c->intermediate_size || !c->num_layers || !c->num_heads ||
+        !c->num_kv_heads || !c->head_dim || !c->max_positions)
+        return fail(LQ8_ERR_MODEL, "config: zero dimension");
+    if (c->num_heads % c->num_kv_heads) return fail(LQ8_ERR_MODEL, "num_heads must be divisible by num_kv_heads");
+    if (c->hidden_size % 32 || c->intermediate_size % 32)
+        return fail(LQ8_ERR_MODEL, "hidden and intermediate sizes must be multiples of 32 (Q8_0 blocks)");
+    if (c->head_dim % 128 || c->head_dim > 512) return fail(LQ8_ERR_MODEL, "head_dim must be 128, 256 or 384/512");
+    if (c->max_positions > 8192) return fail(LQ8_ERR_MODEL, "max_positions > 8192 not supported");
+    if (c->hidden_size > 16384 || c->intermediate_size > 16384 || c->num_heads * c->head_dim > 16384)
+        return fail(LQ8_ERR_MODEL, "dimensions above 16384 not supported");
+    return LQ8_OK;
+}
+
+template <typename T>
+lq8_status dalloc(T** p, size_t count) {
+    LQ8_HIP(hipMalloc((void**)p, count * sizeof(T) + 16));
+    return LQ8_OK;
+}
+
+void release(lq8_model* m) {
+    if (!m) return;
+    registry_remove(m);
+    auto F = [](void* p) { if (p) (void)hipFree(p); };
+    if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    if (m->e0) (void)hipEventDestroy(m->e0);
+    if (m->e1) (void)hipEventDestroy(m->e1);
+    if (m->e2) (void)hipEventDestroy(m->e2);
+    weight_release(m->embed);
+    F(m->final_norm);
+    for (auto& L : m->layers) {
+        weight_release(L.qkv); weight_release(L.o); weight_release(L.gu); weight_release(L.down);
+        F(L.in_norm); F(L.post_norm); F(L.q_norm); F(L.k_norm);
+    }
+    F(m->cos_t); F(m->sin_t); F(m->kc); F(m->vc);
+    F(m->h); F(m->qkv); F(m->qr); F(m->attn); F(m->gu); F(m->logits);
+    F(m->d_ids); F(m->d_pos); F(m->d_step); F(m->d_tok); F(m->d_tokens);
+    F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_act); F(m->P_xs); F(m->P_xq);
+    delete m;
+}
+
+// Allocate weights (uninitialised), norms, tables, caches and decode buffers.
+lq8_status build_skeleton(lq8_ctx* ctx, const lq8_qwen3_config* c, lq8_model* m) {
+    m->ctx = ctx;
+    m->c = *c;
+    const size_t Hd = c->hidden_size, I = c->intermediate_size, hd = c->head_dim, P = c->max_positions;
+    m->QD = (size_t)c->num_heads * hd;
+    m->KD = (size_t)c->num_kv_heads * hd;
+    m->QKV = m->QD + 2 * m->KD;
+    lq8_status st;
+    if ((st = weight_alloc(ctx, c->vocab_size, Hd, &m->embed))) return st;
+    if ((st = dalloc(&m->final_norm, Hd))) return st;
+    m->layers.resize(c->num_layers);
+    for (auto& L : m->layers) {
+        if ((st = weight_alloc(ctx, m->QKV, Hd, &L.qkv))) return st;
+        if ((st = weight_alloc(ctx, Hd, m->QD, &L.o))) return st;
+        if ((st = weight_alloc(ctx, 2 * I, Hd, &L.gu))) return st;
+        if ((st = weight_alloc(ctx, Hd, I, &L.down))) return st;
+        if ((st = dalloc(&L.in_norm, Hd)) || (st = dalloc(&L.post_norm, Hd)) || (st = dalloc(&L.q_norm, hd)) ||
+            (st = dalloc(&L.k_norm, hd)))
+            return st;
+    }
+    // RoPE tables (src/rope.rs:77-128): f64 math, cast to f32, each frequency twice.
+    const size_t R = hd / 2, half = R / 2;
+    std::vector<float> ct(P * R), stbl(P * R);
+    std::vector<double> inv(half);
+    for (size_t i = 0; i < half; i++) inv[i] = 1.0 / std::pow(c->rope_theta, (double)(2 * i) / (double)R);
+    for (size_t p = 0; p < P; p++)
+        for (size_t i = 0; i < half; i++) {
+            double f = (double)p * inv[i];
+            float cv = (float)std::cos(f), sv = (float)std::sin(f);
+            ct[p * R + 2 * i] = ct[p * R + 2 * i + 1] = cv;
+            stbl[p * R + 2 * i] = stbl[p * R + 2 * i + 1] = sv;
+        }
+    if ((st = dalloc(&m->cos_t, P * R)) || (st = dalloc(&m->sin_t, P * R))) return st;
+    LQ8_HIP(hipMemcpy(m->cos_t, ct.data(), P * R * sizeof(float), hipMemcpyHostToDevice));
+    LQ8_HIP(hipMemcpy(m->sin_t, stbl.data(), P * R * sizeof(float), hipMemcpyHostToDevice));
+    const size_t kv = (size_t)c->num_layers * c->num_kv_heads * hd * P;
+    if ((st = dalloc(&m->kc, kv)) || (st = dalloc(&m->vc, kv))) return st;
+    LQ8_HIP(hipMemset(m->kc, 0, kv * sizeof(float)));
+    LQ8_HIP(hipMemset(m->vc, 0, kv * sizeof(float)));
+    if ((st = dalloc(&m->h, Hd)) || (st = dalloc(&m->qkv, m->QKV)) || (st = dalloc(&m->qr, m->QD)) ||
+        (st = dalloc(&m->attn, m->QD)) || (st = dalloc(&m->gu, 2 * I)) || (st = dalloc(&m->logits, c->vocab_size)) ||
+        (st = dalloc(&m->d_pos, 1)) || (st = dalloc(&m->d_step, 1)) || (st = dalloc(&m->d_tok, 1)))
+        return st;
+    LQ8_HIP(hipEventCreate(&m->e0));
+    LQ8_HIP(hipEventCreate(&m->e1));
+    LQ8_HIP(hipEventCreate(&m->e2));
+    return LQ8_OK;
+}
+
+lq8_status fill_norm(float* d, size_t n, const float* host) {
+    if (host) {
+        LQ8_HIP(hipMemcpy(d, host, n * sizeof(float), hipMemcpyHostToDevice));
+    } else {
+        std::vector<float> ones(n, 1.0f);
+        LQ8_HIP(hipMemcpy(d, ones.data(), n * sizeof(float), hipMemcpyHostToDevice));
+    }
+    return LQ8_OK;
+}
+
+// Tensor index -> (weight, first row, rows) or norm buffer.
+struct TensorRef {
+    lq8_weight* w = nullptr;
+    size_t row0 = 0, rows = 0;
+    float* norm = nullptr;
+    size_t norm_len = 0;
+};
+
+TensorRef tensor_ref(lq8_model* m, size_t idx) {
+    TensorRef t;
+    const size_t Hd = m->c.hidden_size, I = m->c.intermediate_size, hd = m->c.head_dim;
+    if (idx == 0) { t.w = m->embed; t.rows = m->c.vocab_size; return t; }
+    if (idx == 1) { t.norm = m->final_norm; t.norm_len = Hd; return t; }
+    size_t l = (idx - 2) / 11, k = (idx - 2) % 11;
+    Layer& L = m->layers[l];
+    switch (k) {
+        case 0: t.norm = L.in_norm; t.norm_len = Hd; break;
+        case 1: t.norm = L.post_norm; t.norm_len = Hd; break;
+        case 2: t.norm = L.q_norm; t.norm_len = hd; break;
+        case 3: t.norm = L.k_norm; t.norm_len = hd; break;
+        case 4: t.w = L.qkv; t.row0 = 0; t.rows = m->QD; break;
+        case 5: t.w = L.qkv; t.row0 = m->QD; t.rows = m->KD; break;
+        case 6: t.w = L.qkv; t.row0 = m->QD + m->KD; t.rows = m->KD; break;
+        case 7: t.w = L.o; t.rows = Hd; break;
+        case 8: t.w = L.gu; t.row0 = 0; t.rows = I; break;
+        case 9: t.w = L.gu; t.row0 = I; t.rows = I; break;
+        default: t.w = L.down; t.rows = Hd; break;
+    }
+    return t;
+}
+
+lq8_status ensure_ids(lq8_model* m, size_t n) {
+    if (n > m->ids_cap) {
+        if (m->d_ids) LQ8_HIP(hipFree(m->d_ids));
+        m->d_ids = nullptr;
+        lq8_status st = dalloc(&m->d_ids, n);
+        if (st) return st;
+        m->ids_cap = n;
+    }
+    return LQ8_OK;
+}
+
+lq8_status ensure_prefill(lq8_model* m, size_t n) {
+    if (n <= m->pf_cap) return LQ8_OK;
+    LQ8_HIP(hipStreamSynchronize(m->ctx->stream));
+    auto F = [](float*& p) { if (p) (void)hipFree(p); p = nullptr; };
+    F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_act); F(m->P_xs);
+    if (m->P_xq) (void)hipFree(m->P_xq);
+    m->P_xq = nullptr;
+    m->pf_cap = 0;
+    const size_t Hd = m->c.hidden_size, I = m->c.intermediate_size;
+    const size_t kmax = std::max(Hd, std::max(m->QD, (size_t)I));
+    const size_t mt = (n + 63) / 64;
+    lq8_status st;
+    if ((st = dalloc(&m->P_h, n * Hd)) || (st = dalloc(&m->P_x, n * Hd)) || (st = dalloc(&m->P_qkv, n * m->QKV)) ||
+        (st = dalloc(&m->P_qr, n * m->QD)) || (st = dalloc(&m->P_attn, n * m->QD)) ||
+        (st = dalloc(&m->P_gu, n * 2 * I)) || (st = dalloc(&m->P_act, n * I)) ||
+        (st = dalloc(&m->P_xs, mt * (kmax / 32) * 64)) || (st = dalloc(&m->P_xq, mt * (kmax / 32) * 2048)))
+        return st;
+    m->pf_cap = n;
+    return LQ8_OK;
+}
+
+// One position through the decoder (src/model.rs:170-195 with L = 1) and the
+// lm_head GEMV; the token id comes from device memory.
+lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, int pos_base) {
+    hipStream_t s = m->ctx->stream;
+    const lq8_qwen3_config& c = m->c;
+    const int Hd = (int)c.hidden_size, I = (int)c.intermediate_size;
+    const size_t layer_kv = (size_t)c.num_kv_heads * c.head_dim * c.max_positions;
+    lq8_status st;
+    if ((st = launch_dequant_rows(s, m->embed, d_id, 0, 1, m->h))) return st;
+    for (size_t l = 0; l < m->layers.size(); l++) {
+        Layer& L = m->layers[l];
+        GemvLaunch g1{L.qkv->codes, L.qkv->scales, m->h, L.in_norm, c.rms_norm_eps, m->qkv, nullptr, (int)m->QKV, Hd};
+        if ((st = launch_gemv(s, XS_RMSNORM, g1))) return st;
+        QkRopeLaunch qr{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->qr, m->kc + l * layer_kv,
+                        m->vc + l * layer_kv, d_pos, pos_base, 1, (int)c.num_heads, (int)c.num_kv_heads,
+                        (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps};
+        if ((st = launch_qk_rope_kv(s, qr))) return st;
+        AttnLaunch at{m->qr, m->kc + l * layer_kv, m->vc + l * layer_kv, m->attn, d_pos, pos_base, 1,
+                      (int)c.num_heads, (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions,
+                      1.0f / std::sqrt((float)c.head_dim)};
+        if ((st = launch_attention(s, at))) return st;
+        GemvLaunch g2{L.o->codes, L.o->scales, m->attn, nullptr, 0.0f, m->h, m->h, Hd, (int)m->QD};
+        if ((st = launch_gemv(s, XS_PLAIN, g2))) return st;
+        GemvLaunch g3{L.gu->codes, L.gu->scales, m->h, L.post_norm, c.rms_norm_eps, m->gu, nullptr, 2 * I, Hd};
+        if ((st = launch_gemv(s, XS_RMSNORM, g3))) return st;
+        GemvLaunch g4{L.down->codes, L.down->scales, m->gu, nullptr, 0.0f, m->h, m->h, Hd, I};
+        if ((st = launch_gemv(s, XS_SILU, g4))) return st;
+    }
+    GemvLaunch g5{m->embed->codes, m->embed->scales, m->h, m->final_norm, c.rms_norm_eps, m->logits, nullptr,
+                  (int)c.vocab_size, Hd};
+    return launch_gemv(s, XS_RMSNORM, g5);
+}
+
+lq8_status quant_gemm(lq8_model* m, const float* x, int n, const lq8_weight* w, float* y, const float* resid) {
+    hipStream_t s = m->ctx->stream;
+    lq8_status st = launch_quantize_act(s, x, n, (int)w->k_in, m->P_xq, m->P_xs);
+    if (st) return st;
+    return launch_gemm(s, m->P_xq, m->P_xs, n, w, y, resid, (int)w->n_out, 0);
+}
+
+// n positions starting at pos_base (src/model.rs:170-195), then the last
+// position's logits.
+lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base) {
+    hipStream_t s = m->ctx->stream;
+    const lq8_qwen3_config& c = m->c;
+    const int Hd = (int)c.hidden_size, I = (int)c.intermediate_size;
+    const size_t layer_kv = (size_t)c.num_kv_heads * c.head_dim * c.max_positions;
+    lq8_status st;
+    if ((st = launch_dequant_rows(s, m->embed, m->d_ids, 0, n, m->P_h))) return st;
+    for (size_t l = 0; l < m->layers.size(); l++) {
+        Layer& L = m->layers[l];
+        if ((st = launch_rms_norm_rows(s, m->P_h, L.in_norm, n, Hd, c.rms_norm_eps, m->P_x))) return st;
+        if ((st = quant_gemm(m, m->P_x, n, L.qkv, m->P_qkv, nullptr))) return st;
+        QkRopeLaunch qr{m->P_qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->P_qr, m->kc + l * layer_kv,
+                        m->vc + l * layer_kv, nullptr, pos_base, n, (int)c.num_heads, (int)c.num_kv_heads,
+                        (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps};
+        if ((st = launch_qk_rope_kv(s, qr))) return st;
+        AttnLaunch at{m->P_qr, m->kc + l * layer_kv, m->vc + l * layer_kv, m->P_attn, nullptr, pos_base, n,
+                      (int)c.num_heads, (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions,
+                      1.0f / std::sqrt((float)c.head_dim)};
+        if ((st = launch_attention(s, at))) return st;
+        if ((st = quant_gemm(m, m->P_attn, n, L.o, m->P_h, m->P_h))) return st;
+        if ((st = launch_rms_norm_rows(s, m->P_h, L.post_norm, n, Hd, c.rms_norm_eps, m->P_x))) return st;
+        if ((st = quant_gemm(m, m->P_x, n, L.gu, m->P_gu, nullptr))) return st;
+        if ((st = launch_silu_mul(s, m->P_gu, n, I, m->P_act))) return st;
+        if ((st = quant_gemm(m, m->P_act, n, L.down, m->P_h, m->P_h))) return st;
+    }
+    // final norm + lm_head on the last position only (src/model.rs:357-371)
+    GemvLaunch g{m->embed->codes, m->embed->scales, m->P_h + (size_t)(n - 1) * Hd, m->final_norm, c.rms_norm_eps,
+                 m->logits, nullptr, (int)c.vocab_size, Hd};
+    return launch_gemv(s, XS_RMSNORM, g);
+}
+
+lq8_status capture_decode_graph(lq8_model* m) {
+    if (m->graph) return LQ8_OK;
+    hipStream_t s = m->ctx->stream;
+    hipGraph_t g = nullptr;
+    LQ8_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
+    lq8_status st = enqueue_decode(m, m->d_tok, m->d_pos, 0);
+    if (!st) st = launch_argmax_step(s, m->logits, (int)m->c.vocab_size, m->d_tok, m->d_tokens, m->d_pos, m->d_step);
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (st) {
+        if (g) (void)hipGraphDestroy(g);
+        return st;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        m->graph = nullptr;
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    return LQ8_OK;
+}
+
+}  // namespace
+
+#define CHECK_M(m) \
+    if (!registry_has(m)) return fail(LQ8_ERR_INVALID_ARG, "invalid or released model handle")
+
+extern "C" {
+
+size_t lq8_model_tensor_count(const lq8_qwen3_config* cfg) { return cfg ? 2 + 11 * (size_t)cfg->num_layers : 0; }
+
+lq8_status lq8_model_tensor_bytes(const lq8_qwen3_config* c, size_t idx, size_t* bytes) {
+    if (!c || !bytes) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (idx >= lq8_model_tensor_count(c)) return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "tensor index out of range");
+    const size_t Hd = c->hidden_size, I = c->intermediate_size, hd = c->head_dim;
+    const size_t QD = c->num_heads * hd, KD = c->num_kv_heads * hd;
+    auto q8 = [](size_t r, size_t k) { return r * (k / 32) * 34; };
+    if (idx == 0) { *bytes = q8(c->vocab_size, Hd); return LQ8_OK; }
+    if (idx == 1) { *bytes = Hd * 4; return LQ8_OK; }
+    switch ((idx - 2) % 11) {
+        case 0: case 1: *bytes = Hd * 4; break;
+        case 2: case 3: *bytes = hd * 4; break;
+        case 4: *bytes = q8(QD, Hd); break;
+        case 5: case 6: *bytes = q8(KD, Hd); break;
+        case 7: *bytes = q8(Hd, QD); break;
+        case 8: case 9: *bytes = q8(I, Hd); break;
+        default: *bytes = q8(Hd, I); break;
+    }
+    return LQ8_OK;
+}
+
+lq8_status lq8_model_create(lq8_ctx* ctx, const lq8_qwen3_config* cfg, const void* const* tensors, lq8_model** out) {
+    if (!registry_has(ctx)) return fail(LQ8_ERR_INVALID_ARG, "invalid context handle");
+    if (!tensors || !out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    lq8_status st = validate(cfg);
+    if (st) return st;
+    size_t count = lq8_model_tensor_count(cfg);
+    for (size_t i = 0; i < count; i++)
+        if (!tensors[i]) return fail(LQ8_ERR_INVALID_ARG, "null tensor in table");
+    LQ8_HIP(hipSetDevice(ctx->device));
+    lq8_model* m = new lq8_model();
+    registry_add(m);
+    if ((st = build_skeleton(ctx, cfg, m))) { release(m); return st; }
+    void* tmp = nullptr;
+    size_t tmp_cap = 0;
+    for (size_t i = 0; i < count && !st; i++) {
+        TensorRef t = tensor_ref(m, i);
+        if (t.norm) { st = fill_norm(t.norm, t.norm_len, (const float*)tensors[i]); continue; }
+        size_t bytes = t.rows * t.w->nb * BLOCK_BYTES;
+        if (bytes > tmp_cap) {
+            if (tmp) (void)hipFree(tmp);
+            tmp = nullptr;
+            hipError_t e = hipMalloc(&tmp, bytes);
+            if (e != hipSuccess) { st = hip_fail(e, "staging"); break; }
+            tmp_cap = bytes;
+        }
+        hipError_t e = hipMemcpy(tmp, tensors[i], bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) { st = hip_fail(e, "tensor upload"); break; }
+        st = launch_repack_aos(ctx->stream, (const uint8_t*)tmp, t.rows, t.w->nb, t.row0, t.w);
+        if (!st) {
+            e = hipStreamSynchronize(ctx->stream);
+            if (e != hipSuccess) st = hip_fail(e, "tensor repack");
+        }
+    }
+    if (tmp) (void)hipFree(tmp);
+    if (st) { release(m); return st; }
+    *out = m;
+    return LQ8_OK;
+}
+
+lq8_status lq8_model_create_random(lq8_ctx* ctx, const lq8_qwen3_config* cfg, uint64_t seed, float stddev,
+                                   lq8_model** out) {
+    if (!registry_has(ctx)) return fail(LQ8_ERR_INVALID_ARG, "invalid context handle");
+    if (!out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    lq8_status st = validate(cfg);
+    if (st) return st;
+    LQ8_HIP(hipSetDevice(ctx->device));
+    lq8_model* m = new lq8_model();
+    registry_add(m);
+    if ((st = build_skeleton(ctx, cfg, m))) { release(m); return st; }
+    size_t count = lq8_model_tensor_count(cfg);
+    for (size_t i = 0; i < count && !st; i++) {
+        TensorRef t = tensor_ref(m, i);
+        if (t.norm) st = fill_norm(t.norm, t.norm_len, nullptr);
+        else st = launch_random_weight(ctx->stream, t.w, t.row0, t.rows, seed, i, stddev);
+    }
+    if (!st) {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) st = hip_fail(e, "random init");
+    }
+    if (st) { release(m); return st; }
+    *out = m;
+    return LQ8_OK;
+}
+
+lq8_status lq8_model_export_tensor(lq8_model* m, size_t idx, void* host_out) {
+    CHECK_M(m);
+    if (!host_out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (idx >= lq8_model_tensor_count(&m->c)) return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "tensor index out of range");
+    TensorRef t = tensor_ref(m, idx);
+    hipStream_t s = m->ctx->stream;
+    if (t.norm) {
+        LQ8_HIP(hipMemcpyAsync(host_out, t.norm, t.norm_len * sizeof(float), hipMemcpyDeviceToHost, s));
+        LQ8_HIP(hipStreamSynchronize(s));
+        return LQ8_OK;
+    }
+    size_t bytes = t.rows * t.w->nb * BLOCK_BYTES;
+    void* tmp = nullptr;
+    LQ8_HIP(hipMalloc(&tmp, bytes));
+    lq8_status st = launch_unpack_aos(s, t.w, t.row0, t.rows, (uint8_t*)tmp);
+    hipError_t e = st ? hipSuccess : hipMemcpyAsync(host_out, tmp, bytes, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(tmp);
+    if (st) return st;
+    if (e != hipSuccess) return hip_fail(e, "tensor export");
+    return LQ8_OK;
+}
+
+lq8_status lq8_model_clear_kv_cache(lq8_model* m) {
+    CHECK_M(m);
+    m->kv_len = 0;
+    return LQ8_OK;
+}
+
+lq8_status lq8_model_forward(lq8_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits) {
+    CHECK_M(m);
+    if (!ids || n == 0) return fail(LQ8_ERR_INVALID_ARG, "input_ids cannot be empty");
+    if (offset != m->kv_len)
+        return fail(LQ8_ERR_INVALID_ARG, "offset must equal the number of cached positions");
+    if (offset + n > m->c.max_positions) return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "positions exceed max_positions");
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= m->c.vocab_size) return fail(LQ8_ERR_INVALID_ARG, "token id out of range for vocab_size");
+    LQ8_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    lq8_status st;
+    if ((st = ensure_ids(m, n))) return st;
+    LQ8_HIP(hipMemcpyAsync(m->d_ids, ids, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    if (n == 1) {
+        st = enqueue_decode(m, m->d_ids, nullptr, (int)offset);
+    } else {
+        if ((st = ensure_prefill(m, n))) return st;
+        st = enqueue_prefill(m, (int)n, (int)offset);
+    }
+    if (st) return st;
+    if (logits)
+        LQ8_HIP(hipMemcpyAsync(logits, m->logits, m->c.vocab_size * sizeof(float), hipMemcpyDeviceToHost, s));
+    LQ8_HIP(hipStreamSynchronize(s));
+    m->kv_len = offset + n;
+    return LQ8_OK;
+}
+
+lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                               uint32_t* out_tokens, lq8_gen_stats* stats) {
+    CHECK_M(m);
+    if (!prompt || n_prompt == 0) return fail(LQ8_ERR_INVALID_ARG, "empty prompt");
+    if (max_new == 0 || !out_tokens) return fail(LQ8_ERR_INVALID_ARG, "max_new must be positive");
+    if (n_prompt + max_new - 1 > m->c.max_positions)
+        return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "prompt + generated tokens exceed max_positions");
+    for (size_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= m->c.vocab_size) return fail(LQ8_ERR_INVALID_ARG, "token id out of range for vocab_size");
+    LQ8_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    lq8_status st;
+    if ((st = ensure_ids(m, n_prompt))) return st;
+    if (max_new > m->tokens_cap) {
+        if (m->d_tokens) LQ8_HIP(hipFree(m->d_tokens));
+        m->d_tokens = nullptr;
+        if ((st = dalloc(&m->d_tokens, max_new))) return st;
+        m->tokens_cap = max_new;
+        if (m->graph) { (void)hipGraphExecDestroy(m->graph); m->graph = nullptr; }
+    }
+    if (n_prompt > 1 && (st = ensure_prefill(m, n_prompt))) return st;
+    const bool use_graph = std::getenv("LQ8_NO_GRAPH") == nullptr;
+    if (use_graph && max_new > 1 && (st = capture_decode_graph(m))) return st;
+    // clear_kv_cache (src/generate.rs:618), then prefill at offset 0
+    m->kv_len = 0;
+    const int zero = 0, pos0 = (int)n_prompt - 1;
+    LQ8_HIP(hipMemcpyAsync(m->d_ids, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    LQ8_HIP(hipMemcpyAsync(m->d_step, &zero, sizeof(int), hipMemcpyHostToDevice, s));
+    LQ8_HIP(hipMemcpyAsync(m->d_pos, &pos0, sizeof(int), hipMemcpyHostToDevice, s));
+    LQ8_HIP(hipEventRecord(m->e0, s));
+    st = n_prompt == 1 ? enqueue_decode(m, m->d_ids, nullptr, 0) : enqueue_prefill(m, (int)n_prompt, 0);
+    if (st) return st;
+    // first token from the prefill logits; d_pos becomes n_prompt
+    if ((st = launch_argmax_step(s, m->logits, (int)m->c.vocab_size, m->d_tok, m->d_tokens, m->d_pos, m->d_step)))
+        return st;
+    LQ8_HIP(hipEventRecord(m->e1, s));
+    for (size_t t = 1; t < max_new; t++) {
+        if (use_graph) {
+            LQ8_HIP(hipGraphLaunch(m->graph, s));
+        } else {
+            if ((st = enqueue_decode(m, m->d_tok, m->d_pos, 0))) return st;
+            if ((st = launch_argmax_step(s, m->logits, (int)m->c.vocab_size, m->d_tok, m->d_tokens, m->d_pos,
+                                         m->d_step)))
+                return st;
+        }
+    }
+    LQ8_HIP(hipEventRecord(m->e2, s));
+    LQ8_HIP(hipMemcpyAsync(out_tokens, m->d_tokens, max_new * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    LQ8_HIP(hipStreamSynchronize(s));
+    m->kv_len = n_prompt + max_new - 1;
+    if (stats) {
+        float a = 0, b = 0;
+        LQ8_HIP(hipEventElapsedTime(&a, m->e0, m->e1));
+        LQ8_HIP(hipEventElapsedTime(&b, m->e1, m->e2));
+        stats->prefill_ms = a;
+        stats->decode_ms = b;
+        stats->decode_tokens_per_s = (max_new > 1 && b > 0) ? (double)(max_new - 1) / (b * 1e-3) : 0.0;
+        stats->used_graph = use_graph ? 1u : 0u;
+    }
+    return LQ8_OK;
+}
+
+lq8_status lq8_model_free(lq8_model* m) {
+    CHECK_M(m);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    release(m);
+    return LQ8_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,594 @@
+// runtime.hip -- context, weights, linear forward: the C ABI of include/lq8.h
+// (model entry points live in model.hip).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <unordered_set>
+#include <vector>
+
+#include "lq8_internal.h"
+
+namespace lq8 {
+
+namespace {
+thread_local std::string g_last_error;
+std::mutex g_reg_mu;
+std::unordered_set<const void*>& registry() {
+    static std::unordered_set<const void*> s;
+    return s;
+}
+}  // namespace
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+lq8_status fail(lq8_status st, const std::string& msg) {
+    g_last_error = msg;
+    return st;
+}
+
+lq8_status hip_fail(hipError_t e, const char* what) {
+    std::string m = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+    if (e == hipErrorOutOfMemory) return fail(LQ8_ERR_OUT_OF_MEMORY, m);
+    if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) return fail(LQ8_ERR_NO_DEVICE, m);
+    return fail(LQ8_ERR_DEVICE, m);
+}
+
+void registry_add(const void* p) {
+    std::lock_guard<std::mutex> g(g_reg_mu);
+    registry().insert(p);
+}
+void registry_remove(const void* p) {
+    std::lock_guard<std::mutex> g(g_reg_mu);
+    registry().erase(p);
+}
+bool registry_has(const void* p) {
+    std::lock_guard<std::mutex> g(g_reg_mu);
+    return p && registry().count(p) != 0;
+}
+
+lq8_status ctx_scratch(lq8_ctx* ctx, size_t bytes, void** out) {
+    if (bytes > ctx->scratch_bytes) {
+        LQ8_HIP(hipStreamSynchronize(ctx->stream));
+        if (ctx->scratch) LQ8_HIP(hipFree(ctx->scratch));
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+        size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+        LQ8_HIP(hipMalloc(&ctx->scratch, want));
+        ctx->scratch_bytes = want;
+    }
+    *out = ctx->scratch;
+    return LQ8_OK;
+}
+
+lq8_status weight_alloc(lq8_ctx* ctx, size_t n_out, size_t k_in, lq8_weight** out) {
+    if (n_out == 0 || k_in == 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "weight: zero dimension");
+    if (k_in % QK) return fail(LQ8_ERR_SHAPE_MISMATCH, "weight: k_in must be a multiple of 32 (Q8_0 block)");
+    if (n_out > (size_t)INT32_MAX || k_in > (size_t)INT32_MAX) return fail(LQ8_ERR_SHAPE_MISMATCH, "weight: too large");
+    lq8_weight* w = new lq8_weight();
+    w->ctx = ctx;
+    w->n_out = n_out;
+    w->k_in = k_in;
+    w->nb = k_in / QK;
+    w->tiles = (n_out + TILE_ROWS - 1) / TILE_ROWS;
+    size_t code_bytes = w->tiles * w->nb * 2048, scale_bytes = w->tiles * w->nb * 64 * sizeof(uint16_t);
+    hipError_t e = hipMalloc(&w->codes, code_bytes);
+    if (e == hipSuccess) e = hipMalloc(&w->scales, scale_bytes);
+    // padded rows are zero so every kernel can read whole tiles
+    if (e == hipSuccess) e = hipMemsetAsync(w->codes, 0, code_bytes, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(w->scales, 0, scale_bytes, ctx->stream);
+    if (e != hipSuccess) {
+        weight_release(w);
+        return hip_fail(e, "weight allocation");
+    }
+    registry_add(w);
+    *out = w;
+    return LQ8_OK;
+}
+
+void weight_release(lq8_weight* w) {
+    if (!w) return;
+    registry_remove(w);
+    if (w->codes) (void)hipFree(w->codes);
+    if (w->scales) (void)hipFree(w->scales);
+    delete w;
+}
+
+// ---- host Q8_0 quantizer (same algorithm as the device quantizer) ---------
+
+static inline uint32_t f2u(float f) { uint32_t u; std::memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; std::memcpy(&f, &u, 4); return f; }
+
+uint16_t host_f32_to_f16(float f) {
+    uint32_t x = f2u(f), sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | (ax > 0x7F800000u ? 0x7E00u | ((ax >> 13) & 0x3FFu) : 0x7C00u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    if (ax >= 0x38800000u) {
+        uint32_t m = ax & 0x7FFFFFu, h = (((ax >> 23) - 112u) << 10) | (m >> 13), rem = m & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    if (ax < 0x33000000u) return (uint16_t)sign;
+    uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+    int s = 126 - (int)(ax >> 23);
+    uint32_t h = m >> s, rem = m & ((1u << s) - 1u), half = 1u << (s - 1);
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+float host_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    if (e == 0x1Fu) return u2f(sign | 0x7F800000u | (m << 13));
+    if (e == 0) {
+        float v = (float)m * 5.9604644775390625e-8f;
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+}  // namespace lq8
+
+using namespace lq8;
+
+#define CHECK_CTX(ctx) \
+    if (!registry_has(ctx)) return fail(LQ8_ERR_INVALID_ARG, "invalid or released context handle")
+#define CHECK_W(w) \
+    if (!registry_has(w)) return fail(LQ8_ERR_INVALID_ARG, "invalid or released weight handle")
+
+static lq8_status set_device(lq8_ctx* ctx) {
+    LQ8_HIP(hipSetDevice(ctx->device));
+    return LQ8_OK;
+}
+
+extern "C" {
+
+const char* lq8_version(void) { return "lq8 0.1.0 (gfx950, Q8_0)"; }
+
+const char* lq8_last_error(void) { return g_last_error.c_str(); }
+
+lq8_status lq8_device_count(int* count) {
+    if (!count) return fail(LQ8_ERR_INVALID_ARG, "count is null");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) n = 0;
+    *count = n;
+    return LQ8_OK;
+}
+
+size_t lq8_q8_0_bytes(size_t n) { return (n / QK) * BLOCK_BYTES; }
+
+lq8_status lq8_quantize_q8_0(const float* x, size_t n, void* blocks_out) {
+    if ((!x || !blocks_out) && n) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (n % QK) return fail(LQ8_ERR_SHAPE_MISMATCH, "quantize: n must be a multiple of 32");
+    uint8_t* o = (uint8_t*)blocks_out;
+    for (size_t b = 0; b < n / QK; b++) {
+        const float* xb = x + b * QK;
+        float amax = 0.0f;
+        for (int j = 0; j < QK; j++) {
+            float v = std::fabs(xb[j]);
+            if (v > amax) amax = v;
+        }
+        float d = amax / 127.0f;
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint16_t d16 = host_f32_to_f16(d);
+        uint8_t* ob = o + b * BLOCK_BYTES;
+        ob[0] = (uint8_t)(d16 & 0xFF);
+        ob[1] = (uint8_t)(d16 >> 8);
+        for (int j = 0; j < QK; j++) {
+            float v = std::round(xb[j] * id);
+            int q = (v != v) ? 0 : (v >= 127.0f ? 127 : (v <= -128.0f ? -128 : (int)v));
+            ob[2 + j] = (uint8_t)(int8_t)q;
+        }
+    }
+    return LQ8_OK;
+}
+
+lq8_status lq8_dequantize_q8_0(const void* blocks, size_t n, float* y) {
+    if ((!blocks || !y) && n) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (n % QK) return fail(LQ8_ERR_SHAPE_MISMATCH, "dequantize: n must be a multiple of 32");
+    const uint8_t* in = (const uint8_t*)blocks;
+    for (size_t b = 0; b < n / QK; b++) {
+        const uint8_t* blk = in + b * BLOCK_BYTES;
+        float d = host_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int j = 0; j < QK; j++) y[b * QK + j] = d * (float)(int8_t)blk[2 + j];
+    }
+    return LQ8_OK;
+}
+
+lq8_status lq8_init(int device, lq8_ctx** out) {
+    if (!out) return fail(LQ8_ERR_INVALID_ARG, "out is null");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return fail(LQ8_ERR_NO_DEVICE, "no HIP device available (no fallback: the Q8_0 path requires a GPU)");
+    if (device < 0 || device >= n) return fail(LQ8_ERR_NO_DEVICE, "device index out of range");
+    LQ8_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    LQ8_HIP(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(LQ8_ERR_NO_DEVICE, std::string("device is ") + prop.gcnArchName + ", this library targets gfx950");
+    lq8_ctx* ctx = new lq8_ctx();
+    ctx->device = device;
+    ctx->num_cus = prop.multiProcessorCount;
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->t0);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->t1);
+    if (e != hipSuccess) {
+        if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return hip_fail(e, "context creation");
+    }
+    registry_add(ctx);
+    *out = ctx;
+    return LQ8_OK;
+}
+
+lq8_status lq8_shutdown(lq8_ctx* ctx) {
+    CHECK_CTX(ctx);
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    registry_remove(ctx);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->problems) (void)hipFree(ctx->problems);
+    (void)hipEventDestroy(ctx->t0);
+    (void)hipEventDestroy(ctx->t1);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return LQ8_OK;
+}
+
+lq8_status lq8_synchronize(lq8_ctx* ctx) {
+    CHECK_CTX(ctx);
+    LQ8_HIP(hipStreamSynchronize(ctx->stream));
+    return LQ8_OK;
+}
+
+lq8_status lq8_device_alloc(lq8_ctx* ctx, size_t bytes, void** dptr) {
+    CHECK_CTX(ctx);
+    if (!dptr) return fail(LQ8_ERR_INVALID_ARG, "dptr is null");
+    if (set_device(ctx)) return LQ8_ERR_DEVICE;
+    LQ8_HIP(hipMalloc(dptr, bytes ? bytes : 1));
+    return LQ8_OK;
+}
+
+lq8_status lq8_device_free(lq8_ctx* ctx, void* dptr) {
+    CHECK_CTX(ctx);
+    LQ8_HIP(hipStreamSynchronize(ctx->stream));
+    LQ8_HIP(hipFree(dptr));
+    return LQ8_OK;
+}
+
+lq8_status lq8_copy_to_device(lq8_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    CHECK_CTX(ctx);
+    LQ8_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    LQ8_HIP(hipStreamSynchronize(ctx->stream));
+    return LQ8_OK;
+}
+
+lq8_status lq8_copy_to_host(lq8_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    CHECK_CTX(ctx);
+    LQ8_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    LQ8_HIP(hipStreamSynchronize(ctx->stream));
+    return LQ8_OK;
+}
+
+lq8_status lq8_timer_start(lq8_ctx* ctx) {
+    CHECK_CTX(ctx);
+    LQ8_HIP(hipEventRecord(ctx->t0, ctx->stream));
+    return LQ8_OK;
+}
+
+lq8_status lq8_timer_stop(lq8_ctx* ctx, float* elapsed_ms) {
+    CHECK_CTX(ctx);
+    if (!elapsed_ms) return fail(LQ8_ERR_INVALID_ARG, "elapsed_ms is null");
+    LQ8_HIP(hipEventRecord(ctx->t1, ctx->stream));
+    LQ8_HIP(hipEventSynchronize(ctx->t1));
+    LQ8_HIP(hipEventElapsedTime(elapsed_ms, ctx->t0, ctx->t1));
+    return LQ8_OK;
+}
+
+// ---- weights -------------------------------------------------------------------
+
+lq8_status lq8_weight_upload(lq8_ctx* ctx, const void* blocks, size_t n_out, size_t k_in, lq8_weight** out) {
+    CHECK_CTX(ctx);
+    if (!blocks || !out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (set_device(ctx)) return LQ8_ERR_DEVICE;
+    lq8_weight* w = nullptr;
+    lq8_status st = weight_alloc(ctx, n_out, k_in, &w);
+    if (st) return st;
+    size_t bytes = n_out * (k_in / QK) * BLOCK_BYTES;
+    void* tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, bytes);
+    if (e == hipSuccess) e = hipMemcpyAsync(tmp, blocks, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) {
+        if (tmp) (void)hipFree(tmp);
+        weight_release(w);
+        return hip_fail(e, "weight upload");
+    }
+    st = launch_repack_aos(ctx->stream, (const uint8_t*)tmp, n_out, w->nb, 0, w);
+    e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(tmp);
+    if (st || e != hipSuccess) {
+        weight_release(w);
+        return st ? st : hip_fail(e, "weight repack");
+    }
+    *out = w;
+    return LQ8_OK;
+}
+
+lq8_status lq8_weight_quantize_upload(lq8_ctx* ctx, const float* src, size_t n_out, size_t k_in, lq8_weight** out) {
+    CHECK_CTX(ctx);
+    if (!src || !out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (set_device(ctx)) return LQ8_ERR_DEVICE;
+    lq8_weight* w = nullptr;
+    lq8_status st = weight_alloc(ctx, n_out, k_in, &w);
+    if (st) return st;
+    size_t bytes = n_out * k_in * sizeof(float);
+    void* tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, bytes);
+    if (e == hipSuccess) e = hipMemcpyAsync(tmp, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) {
+        if (tmp) (void)hipFree(tmp);
+        weight_release(w);
+        return hip_fail(e, "weight upload");
+    }
+    st = launch_quantize_weight_f32(ctx->stream, (const float*)tmp, n_out, 0, w);
+    e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(tmp);
+    if (st || e != hipSuccess) {
+        weight_release(w);
+        return st ? st : hip_fail(e, "weight quantize");
+    }
+    *out = w;
+    return LQ8_OK;
+}
+
+lq8_status lq8_weight_random(lq8_ctx* ctx, size_t n_out, size_t k_in, uint64_t seed, uint64_t stream, float stddev,
+                             lq8_weight** out) {
+    CHECK_CTX(ctx);
+    if (!out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (set_device(ctx)) return LQ8_ERR_DEVICE;
+    lq8_weight* w = nullptr;
+    lq8_status st = weight_alloc(ctx, n_out, k_in, &w);
+    if (st) return st;
+    st = launch_random_weight(ctx->stream, w, 0, n_out, seed, stream, stddev);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (st || e != hipSuccess) {
+        weight_release(w);
+        return st ? st : hip_fail(e, "random weight");
+    }
+    *out = w;
+    return LQ8_OK;
+}
+
+lq8_status lq8_weight_download(lq8_ctx* ctx, const lq8_weight* w, void* blocks_out) {
+    CHECK_CTX(ctx);
+    CHECK_W(w);
+    if (!blocks_out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    size_t bytes = w->n_out * w->nb * BLOCK_BYTES;
+    void* tmp = nullptr;
+    LQ8_HIP(hipMalloc(&tmp, bytes));
+    lq8_status st = launch_unpack_aos(ctx->stream, w, 0, w->n_out, (uint8_t*)tmp);
+    hipError_t e = st ? hipSuccess : hipMemcpyAsync(blocks_out, tmp, bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(tmp);
+    if (st) return st;
+    if (e != hipSuccess) return hip_fail(e, "weight download");
+    return LQ8_OK;
+}
+
+lq8_status lq8_weight_shape(const lq8_weight* w, size_t* n_out, size_t* k_in) {
+    CHECK_W(w);
+    if (n_out) *n_out = w->n_out;
+    if (k_in) *k_in = w->k_in;
+    return LQ8_OK;
+}
+
+lq8_status lq8_weight_free(lq8_weight* w) {
+    CHECK_W(w);
+    (void)hipStreamSynchronize(w->ctx->stream);
+    weight_release(w);
+    return LQ8_OK;
+}
+
+lq8_status lq8_quantize_q8_0_device(lq8_ctx* ctx, const float* d_x, size_t n, void* d_blocks) {
+    CHECK_CTX(ctx);
+    if ((!d_x || !d_blocks) && n) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (n % QK) return fail(LQ8_ERR_SHAPE_MISMATCH, "quantize: n must be a multiple of 32");
+    return launch_quantize_aos(ctx->stream, d_x, n / QK, (uint8_t*)d_blocks);
+}
+
+lq8_status lq8_weight_dequantize_rows_device(lq8_ctx* ctx, const lq8_weight* w, size_t row0, size_t nrows,
+                                             float* d_y) {
+    CHECK_CTX(ctx);
+    CHECK_W(w);
+    if (!d_y) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (row0 > w->n_out || nrows > w->n_out - row0) return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "rows out of range");
+    return launch_dequant_rows(ctx->stream, w, nullptr, row0, nrows, d_y);
+}
+
+// ---- linear forward --------------------------------------------------------------
+
+lq8_status lq8_gemv_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, float* d_y) {
+    CHECK_CTX(ctx);
+    CHECK_W(w);
+    if (!d_x || !d_y) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (((uintptr_t)d_x & 15) != 0) return fail(LQ8_ERR_INVALID_ARG, "x must be 16-byte aligned");
+    GemvLaunch a{w->codes, w->scales, d_x, nullptr, 0.0f, d_y, nullptr, (int)w->n_out, (int)w->k_in};
+    return launch_gemv(ctx->stream, XS_PLAIN, a);
+}
+
+lq8_status lq8_gemm_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m, float* d_y) {
+    CHECK_CTX(ctx);
+    CHECK_W(w);
+    if (!d_x || !d_y) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (m == 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemm: m must be positive");
+    if (m > (size_t)INT32_MAX / 2) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemm: m too large");
+    if (((uintptr_t)d_x & 15) != 0) return fail(LQ8_ERR_INVALID_ARG, "x must be 16-byte aligned");
+    size_t mt = (m + 63) / 64;
+    size_t code_bytes = mt * w->nb * 2048, scale_bytes = mt * w->nb * 64 * sizeof(float);
+    void* sc = nullptr;
+    lq8_status st = ctx_scratch(ctx, code_bytes + scale_bytes, &sc);
+    if (st) return st;
+    int8_t* xq = (int8_t*)sc;
+    float* xs = (float*)((char*)sc + code_bytes);
+    st = launch_quantize_act(ctx->stream, d_x, (int)m, (int)w->k_in, xq, xs);
+    if (st) return st;
+    return launch_gemm(ctx->stream, xq, xs, (int)m, w, d_y, nullptr, (int)w->n_out, 0);
+}
+
+lq8_status lq8_linear_forward_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m, float* d_y) {
+    if (m == 1) return lq8_gemv_q8_0_device(ctx, w, d_x, d_y);
+    return lq8_gemm_q8_0_device(ctx, w, d_x, m, d_y);
+}
+
+lq8_status lq8_linear_forward(lq8_ctx* ctx, const lq8_weight* w, const float* x, size_t m, float* y) {
+    CHECK_CTX(ctx);
+    CHECK_W(w);
+    if (!x || !y) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (m == 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "linear: m must be positive");
+    if (set_device(ctx)) return LQ8_ERR_DEVICE;
+    size_t xb = m * w->k_in * sizeof(float), yb = m * w->n_out * sizeof(float);
+    void *dx = nullptr, *dy = nullptr;
+    hipError_t e = hipMalloc(&dx, xb);
+    if (e == hipSuccess) e = hipMalloc(&dy, yb);
+    if (e == hipSuccess) e = hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream);
+    lq8_status st = LQ8_OK;
+    if (e == hipSuccess) st = lq8_linear_forward_device(ctx, w, (const float*)dx, m, (float*)dy);
+    if (e == hipSuccess && !st) e = hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (dx) (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+    if (st) return st;
+    if (e != hipSuccess) return hip_fail(e, "linear forward");
+    return LQ8_OK;
+}
+
+lq8_status lq8_gemv_grouped_device(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t count) {
+    CHECK_CTX(ctx);
+    if (count == 0) return LQ8_OK;
+    if (!problems) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (count > 65536) return fail(LQ8_ERR_INVALID_ARG, "too many problems");
+    std::vector<GemvProblemDev> host(count);
+    size_t tiles = 0;
+    int max_k = 0;
+    for (size_t i = 0; i < count; i++) {
+        const lq8_gemv_problem& p = problems[i];
+        if (!registry_has(p.w)) return fail(LQ8_ERR_INVALID_ARG, "invalid weight handle in problem list");
+        if (!p.x || !p.y) return fail(LQ8_ERR_INVALID_ARG, "null pointer in problem list");
+        if (((uintptr_t)p.x & 15) != 0) return fail(LQ8_ERR_INVALID_ARG, "x must be 16-byte aligned");
+        if (p.w->k_in > 16384) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k > 16384 not supported");
+        host[i] = GemvProblemDev{p.w->codes, p.w->scales, p.x, p.y, (int)p.w->n_out, (int)p.w->k_in, (int)tiles, 0};
+        tiles += p.w->tiles;
+        if ((int)p.w->k_in > max_k) max_k = (int)p.w->k_in;
+    }
+    if (tiles > (size_t)INT32_MAX) return fail(LQ8_ERR_SHAPE_MISMATCH, "too many tiles");
+    size_t bytes = count * sizeof(GemvProblemDev);
+    if (bytes > ctx->problems_bytes) {
+        LQ8_HIP(hipStreamSynchronize(ctx->stream));
+        if (ctx->problems) LQ8_HIP(hipFree(ctx->problems));
+        ctx->problems = nullptr;
+        LQ8_HIP(hipMalloc(&ctx->problems, bytes));
+        ctx->problems_bytes = bytes;
+    }
+    LQ8_HIP(hipMemcpyAsync(ctx->problems, host.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
+    // the host vector dies at return: wait for the copy to finish reading it
+    LQ8_HIP(hipStreamSynchronize(ctx->stream));
+    return launch_gemv_grouped(ctx->stream, (const GemvProblemDev*)ctx->problems, (int)count, (int)tiles, max_k);
+}
+
+lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t count, int mode, int reps,
+                          float* ms) {
+    CHECK_CTX(ctx);
+    if (!problems || !count || reps <= 0 || !ms) return fail(LQ8_ERR_INVALID_ARG, "bad benchmark arguments");
+    std::vector<GemvLaunch> L(count);
+    for (size_t i = 0; i < count; i++) {
+        const lq8_gemv_problem& p = problems[i];
+        if (!registry_has(p.w)) return fail(LQ8_ERR_INVALID_ARG, "invalid weight handle in problem list");
+        if (!p.x || !p.y || ((uintptr_t)p.x & 15)) return fail(LQ8_ERR_INVALID_ARG, "bad x / y pointer");
+        L[i] = GemvLaunch{p.w->codes, p.w->scales, p.x, nullptr, 0.0f, p.y, nullptr, (int)p.w->n_out, (int)p.w->k_in};
+    }
+    hipStream_t s = ctx->stream;
+    lq8_status st = LQ8_OK;
+    if (mode == 0 || mode == 2) {  // one launch per problem (2: replayed as a HIP graph)
+        hipGraphExec_t exec = nullptr;
+        if (mode == 2) {
+            hipGraph_t g = nullptr;
+            LQ8_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
+            for (size_t i = 0; i < count && !st; i++) st = launch_gemv(s, XS_PLAIN, L[i]);
+            hipError_t e = hipStreamEndCapture(s, &g);
+            if (st) { if (g) (void)hipGraphDestroy(g); return st; }
+            if (e != hipSuccess) return hip_fail(e, "capture");
+            e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (e != hipSuccess) return hip_fail(e, "instantiate");
+        }
+        LQ8_HIP(hipEventRecord(ctx->t0, s));
+        for (int r = 0; r < reps && !st; r++) {
+            if (exec) {
+                hipError_t e = hipGraphLaunch(exec, s);
+                if (e != hipSuccess) st = hip_fail(e, "graph launch");
+            } else {
+                for (size_t i = 0; i < count && !st; i++) st = launch_gemv(s, XS_PLAIN, L[i]);
+            }
+        }
+        LQ8_HIP(hipEventRecord(ctx->t1, s));
+        LQ8_HIP(hipEventSynchronize(ctx->t1));
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (st) return st;
+        LQ8_HIP(hipEventElapsedTime(ms, ctx->t0, ctx->t1));
+        return LQ8_OK;
+    }
+    if (mode == 1) {  // all problems in one grouped launch
+        std::vector<GemvProblemDev> host(count);
+        size_t tiles = 0;
+        int max_k = 0;
+        for (size_t i = 0; i < count; i++) {
+            const lq8_gemv_problem& p = problems[i];
+            host[i] = GemvProblemDev{p.w->codes, p.w->scales, p.x, p.y, (int)p.w->n_out, (int)p.w->k_in, (int)tiles, 0};
+            tiles += p.w->tiles;
+            max_k = std::max(max_k, (int)p.w->k_in);
+        }
+        size_t bytes = count * sizeof(GemvProblemDev);
+        void* d = nullptr;
+        LQ8_HIP(hipMalloc(&d, bytes));
+        hipError_t e = hipMemcpy(d, host.data(), bytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipEventRecord(ctx->t0, s);
+        for (int r = 0; r < reps && e == hipSuccess && !st; r++)
+            st = launch_gemv_grouped(s, (const GemvProblemDev*)d, (int)count, (int)tiles, max_k);
+        if (e == hipSuccess) e = hipEventRecord(ctx->t1, s);
+        if (e == hipSuccess) e = hipEventSynchronize(ctx->t1);
+        (void)hipFree(d);
+        if (st) return st;
+        if (e != hipSuccess) return hip_fail(e, "grouped benchmark");
+        LQ8_HIP(hipEventElapsedTime(ms, ctx->t0, ctx->t1));
+        return LQ8_OK;
+    }
+    if (mode == 3) {  // per-launch event pairs: sum of the launches' own intervals
+        std::vector<hipEvent_t> ev(2 * count);
+        for (auto& e : ev) LQ8_HIP(hipEventCreate(&e));
+        double total = 0.0;
+        for (int r = 0; r < reps && !st; r++) {
+            for (size_t i = 0; i < count && !st; i++) {
+                (void)hipEventRecord(ev[2 * i], s);
+                st = launch_gemv(s, XS_PLAIN, L[i]);
+                (void)hipEventRecord(ev[2 * i + 1], s);
+            }
+            if (st) break;
+            hipError_t e = hipEventSynchronize(ev[2 * count - 1]);
+            if (e != hipSuccess) { st = hip_fail(e, "event sync"); break; }
+            for (size_t i = 0; i < count; i++) {
+                float t = 0;
+                (void)hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]);
+                total += t;
+            }
+        }
+        for (auto& e : ev) (void)hipEventDestroy(e);
+        if (st) return st;
+        *ms = (float)total;
+        return LQ8_OK;
+    }
+    return fail(LQ8_ERR_INVALID_ARG, "unknown benchmark mode");
+}
+
+}  // extern "C"

@@ -1,0 +1,446 @@
+"""Host-side mirror of lluda-inference's linear-layer / model API over liblq8.so.
+
+The reference exposes ``Linear::new(weight)`` / ``Linear::forward(x)``
+(src/attention.rs:63-136), ``Tensor::matmul`` (src/tensor.rs:804),
+``Qwen3ForCausalLM::{load, forward, clear_kv_cache}`` (src/model.rs:273-398)
+and ``generate`` (src/generate.rs:611-664).  This module keeps those names and
+argument meanings on top of the C ABI in include/lq8.h.  Errors surface as
+``LludaError`` subclasses named after the reference's error kinds
+(src/error.rs:17-97).  There is no CPU fallback: without the shared library or
+without a gfx950 device every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liblq8.so")
+
+QK = 32
+BLOCK_BYTES = 34
+
+
+class LludaError(RuntimeError):
+    """Base error; ``status`` is the lq8_status code."""
+
+    status = -1
+
+    def __init__(self, msg: str, status: int | None = None):
+        super().__init__(msg)
+        if status is not None:
+            self.status = status
+
+
+class ShapeMismatch(LludaError):
+    status = 1
+
+
+class DTypeMismatch(LludaError):
+    status = 2
+
+
+class DimOutOfRange(LludaError):
+    status = 3
+
+
+class InvalidArgument(LludaError):
+    status = 4
+
+
+class NoDevice(LludaError):
+    status = 5
+
+
+class DeviceError(LludaError):
+    status = 6
+
+
+class OutOfMemory(LludaError):
+    status = 7
+
+
+class ModelError(LludaError):
+    status = 8
+
+
+_ERRORS = {c.status: c for c in (ShapeMismatch, DTypeMismatch, DimOutOfRange, InvalidArgument, NoDevice,
+                                  DeviceError, OutOfMemory, ModelError)}
+
+
+class Qwen3ConfigC(C.Structure):
+    _fields_ = [
+        ("vocab_size", C.c_uint32), ("hidden_size", C.c_uint32), ("intermediate_size", C.c_uint32),
+        ("num_layers", C.c_uint32), ("num_heads", C.c_uint32), ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32), ("max_positions", C.c_uint32), ("rms_norm_eps", C.c_float),
+        ("rope_theta", C.c_double),
+    ]
+
+
+class GemvProblemC(C.Structure):
+    _fields_ = [("w", C.c_void_p), ("x", C.c_void_p), ("y", C.c_void_p)]
+
+
+class GenStatsC(C.Structure):
+    _fields_ = [("prefill_ms", C.c_double), ("decode_ms", C.c_double), ("decode_tokens_per_s", C.c_double),
+                ("used_graph", C.c_uint32)]
+
+
+_lib: Optional[C.CDLL] = None
+
+# (name, restype, argtypes) of every exported entry point.
+_SIGS = [
+    ("lq8_version", C.c_char_p, []),
+    ("lq8_last_error", C.c_char_p, []),
+    ("lq8_device_count", C.c_int, [C.POINTER(C.c_int)]),
+    ("lq8_q8_0_bytes", C.c_size_t, [C.c_size_t]),
+    ("lq8_quantize_q8_0", C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("lq8_dequantize_q8_0", C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("lq8_init", C.c_int, [C.c_int, C.POINTER(C.c_void_p)]),
+    ("lq8_shutdown", C.c_int, [C.c_void_p]),
+    ("lq8_synchronize", C.c_int, [C.c_void_p]),
+    ("lq8_device_alloc", C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p)]),
+    ("lq8_device_free", C.c_int, [C.c_void_p, C.c_void_p]),
+    ("lq8_copy_to_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    ("lq8_copy_to_host", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    ("lq8_timer_start", C.c_int, [C.c_void_p]),
+    ("lq8_timer_stop", C.c_int, [C.c_void_p, C.POINTER(C.c_float)]),
+    ("lq8_weight_upload", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_void_p)]),
+    ("lq8_weight_quantize_upload", C.c_int,
+     [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_void_p)]),
+    ("lq8_weight_random", C.c_int,
+     [C.c_void_p, C.c_size_t, C.c_size_t, C.c_uint64, C.c_uint64, C.c_float, C.POINTER(C.c_void_p)]),
+    ("lq8_weight_download", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    ("lq8_weight_shape", C.c_int, [C.c_void_p, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    ("lq8_weight_free", C.c_int, [C.c_void_p]),
+    ("lq8_quantize_q8_0_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("lq8_weight_dequantize_rows_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
+    ("lq8_linear_forward", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("lq8_linear_forward_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("lq8_gemv_q8_0_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    ("lq8_gemm_q8_0_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("lq8_gemv_grouped_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    ("lq8_bench_gemv", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.POINTER(C.c_float)]),
+    ("lq8_model_tensor_count", C.c_size_t, [C.POINTER(Qwen3ConfigC)]),
+    ("lq8_model_tensor_bytes", C.c_int, [C.POINTER(Qwen3ConfigC), C.c_size_t, C.POINTER(C.c_size_t)]),
+    ("lq8_model_create", C.c_int, [C.c_void_p, C.POINTER(Qwen3ConfigC), C.c_void_p, C.POINTER(C.c_void_p)]),
+    ("lq8_model_create_random", C.c_int,
+     [C.c_void_p, C.POINTER(Qwen3ConfigC), C.c_uint64, C.c_float, C.POINTER(C.c_void_p)]),
+    ("lq8_model_export_tensor", C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("lq8_model_clear_kv_cache", C.c_int, [C.c_void_p]),
+    ("lq8_model_forward", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
+    ("lq8_generate_greedy", C.c_int,
+     [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.POINTER(GenStatsC)]),
+    ("lq8_model_free", C.c_int, [C.c_void_p]),
+]
+
+EXPORTED = [s[0] for s in _SIGS]
+
+
+def lib() -> C.CDLL:
+    """Load liblq8.so (built in-tree).  Raises if it was not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise LludaError(f"{LIB_PATH} not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in _SIGS:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        msg = lib().lq8_last_error().decode(errors="replace")
+        raise _ERRORS.get(status, LludaError)(msg, status)
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    return C.c_void_p(a.ctypes.data)
+
+
+def version() -> str:
+    return lib().lq8_version().decode()
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    _check(lib().lq8_device_count(C.byref(n)))
+    return n.value
+
+
+# ---- host Q8_0 format ----------------------------------------------------------
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    """f32 array (size multiple of 32) -> uint8 AoS blocks (34 bytes each)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size // QK * BLOCK_BYTES, dtype=np.uint8)
+    _check(lib().lq8_quantize_q8_0(_ptr(x), x.size, _ptr(out)))
+    return out
+
+
+def dequantize_q8_0(blocks: np.ndarray, n: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    y = np.empty(n, dtype=np.float32)
+    _check(lib().lq8_dequantize_q8_0(_ptr(blocks), n, _ptr(y)))
+    return y
+
+
+# ---- device context and buffers ----------------------------------------------------
+
+class Context:
+    """One device + one stream (the reference's global GPU context, src/gpu/mod.rs:129-178)."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        _check(lib().lq8_init(device, C.byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            _check(lib().lq8_shutdown(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def synchronize(self) -> None:
+        _check(lib().lq8_synchronize(self.handle))
+
+    def timer_start(self) -> None:
+        _check(lib().lq8_timer_start(self.handle))
+
+    def timer_stop(self) -> float:
+        ms = C.c_float(0.0)
+        _check(lib().lq8_timer_stop(self.handle, C.byref(ms)))
+        return ms.value
+
+
+class DeviceBuffer:
+    """A device allocation with explicit host copies (no implicit transfers)."""
+
+    def __init__(self, ctx: Context, nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        _check(lib().lq8_device_alloc(ctx.handle, self.nbytes, C.byref(p)))
+        self.ptr = p
+
+    @classmethod
+    def from_array(cls, ctx: Context, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(ctx, a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise ShapeMismatch("upload larger than buffer")
+        _check(lib().lq8_copy_to_device(self.ctx.handle, self.ptr, _ptr(a), a.nbytes))
+
+    def download(self, dtype, count: int) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        if out.nbytes > self.nbytes:
+            raise ShapeMismatch("download larger than buffer")
+        _check(lib().lq8_copy_to_host(self.ctx.handle, _ptr(out), self.ptr, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            _check(lib().lq8_device_free(self.ctx.handle, self.ptr))
+            self.ptr = None
+
+
+class Q8Weight:
+    """A Q8_0 weight [n_out, k_in] resident on the device (uploaded once)."""
+
+    def __init__(self, ctx: Context, handle: C.c_void_p):
+        self.ctx = ctx
+        self.handle = handle
+        n, k = C.c_size_t(), C.c_size_t()
+        _check(lib().lq8_weight_shape(handle, C.byref(n), C.byref(k)))
+        self.n_out, self.k_in = n.value, k.value
+
+    @classmethod
+    def from_blocks(cls, ctx: Context, blocks: np.ndarray, n_out: int, k_in: int) -> "Q8Weight":
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        if blocks.size != n_out * (k_in // QK) * BLOCK_BYTES:
+            raise ShapeMismatch(f"expected {n_out * (k_in // QK) * BLOCK_BYTES} bytes, got {blocks.size}")
+        h = C.c_void_p()
+        _check(lib().lq8_weight_upload(ctx.handle, _ptr(blocks), n_out, k_in, C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def quantize(cls, ctx: Context, w: np.ndarray) -> "Q8Weight":
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        if w.ndim != 2:
+            raise ShapeMismatch("weight must be 2-D [out_features, in_features]")
+        h = C.c_void_p()
+        _check(lib().lq8_weight_quantize_upload(ctx.handle, _ptr(w), w.shape[0], w.shape[1], C.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def random(cls, ctx: Context, n_out: int, k_in: int, seed: int, stream: int = 0, std: float = 0.02):
+        h = C.c_void_p()
+        _check(lib().lq8_weight_random(ctx.handle, n_out, k_in, seed, stream, std, C.byref(h)))
+        return cls(ctx, h)
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.n_out * (self.k_in // QK) * BLOCK_BYTES, dtype=np.uint8)
+        _check(lib().lq8_weight_download(self.ctx.handle, self.handle, _ptr(out)))
+        return out
+
+    def free(self) -> None:
+        if self.handle:
+            _check(lib().lq8_weight_free(self.handle))
+            self.handle = None
+
+
+class Linear:
+    """``Linear`` of src/attention.rs:33-137 on a Q8_0 weight: y = x @ W^T."""
+
+    def __init__(self, weight: Q8Weight):
+        self.weight = weight
+
+    @classmethod
+    def new(cls, weight: Q8Weight) -> "Linear":
+        return cls(weight)
+
+    def forward(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim < 1 or x.shape[-1] != self.weight.k_in:
+            raise ShapeMismatch(f"expected last dim {self.weight.k_in}, got {x.shape}")
+        m = int(np.prod(x.shape[:-1])) if x.ndim > 1 else 1
+        y = np.empty((m, self.weight.n_out), dtype=np.float32)
+        _check(lib().lq8_linear_forward(self.weight.ctx.handle, self.weight.handle, _ptr(x), m, _ptr(y)))
+        return y.reshape(tuple(x.shape[:-1]) + (self.weight.n_out,))
+
+    def forward_device(self, x: DeviceBuffer, m: int, y: DeviceBuffer) -> None:
+        _check(lib().lq8_linear_forward_device(self.weight.ctx.handle, self.weight.handle, x.ptr, m, y.ptr))
+
+
+# ---- Qwen3 -------------------------------------------------------------------
+
+@dataclass
+class Qwen3Config:
+    """The fields of Qwen3Config (src/config.rs:15-82) that the decoder uses."""
+
+    vocab_size: int = 151936
+    hidden_size: int = 1024
+    intermediate_size: int = 3072
+    num_hidden_layers: int = 28
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    max_position_embeddings: int = 4096
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+
+    def c(self) -> Qwen3ConfigC:
+        return Qwen3ConfigC(self.vocab_size, self.hidden_size, self.intermediate_size, self.num_hidden_layers,
+                            self.num_attention_heads, self.num_key_value_heads, self.head_dim,
+                            self.max_position_embeddings, self.rms_norm_eps, self.rope_theta)
+
+    def tensor_count(self) -> int:
+        return 2 + 11 * self.num_hidden_layers
+
+    def tensor_shape(self, idx: int):
+        """(kind, shape) of tensor ``idx`` in the table order of include/lq8.h."""
+        H, I, hd = self.hidden_size, self.intermediate_size, self.head_dim
+        QD, KD = self.num_attention_heads * hd, self.num_key_value_heads * hd
+        if idx == 0:
+            return "q8", (self.vocab_size, H)
+        if idx == 1:
+            return "f32", (H,)
+        k = (idx - 2) % 11
+        return [("f32", (H,)), ("f32", (H,)), ("f32", (hd,)), ("f32", (hd,)), ("q8", (QD, H)), ("q8", (KD, H)),
+                ("q8", (KD, H)), ("q8", (H, QD)), ("q8", (I, H)), ("q8", (I, H)), ("q8", (H, I))][k]
+
+
+def qwen3_0_6b(max_positions: int = 4096) -> Qwen3Config:
+    return Qwen3Config(max_position_embeddings=max_positions)
+
+
+class Qwen3ForCausalLM:
+    """src/model.rs:245-398 on Q8_0 weights."""
+
+    def __init__(self, ctx: Context, cfg: Qwen3Config, handle: C.c_void_p):
+        self.ctx, self.cfg, self.handle = ctx, cfg, handle
+        self._c = cfg.c()
+
+    @classmethod
+    def load(cls, ctx: Context, cfg: Qwen3Config, tensors: Sequence[np.ndarray]) -> "Qwen3ForCausalLM":
+        """From host tensors (Q8_0 AoS blocks or f32 norms) in table order."""
+        if len(tensors) != cfg.tensor_count():
+            raise ModelError(f"expected {cfg.tensor_count()} tensors, got {len(tensors)}")
+        keep = [np.ascontiguousarray(t) for t in tensors]
+        arr = (C.c_void_p * len(keep))(*[t.ctypes.data for t in keep])
+        h = C.c_void_p()
+        c = cfg.c()
+        _check(lib().lq8_model_create(ctx.handle, C.byref(c), arr, C.byref(h)))
+        return cls(ctx, cfg, h)
+
+    @classmethod
+    def random(cls, ctx: Context, cfg: Qwen3Config, seed: int, std: float = 0.02) -> "Qwen3ForCausalLM":
+        h = C.c_void_p()
+        c = cfg.c()
+        _check(lib().lq8_model_create_random(ctx.handle, C.byref(c), seed, std, C.byref(h)))
+        return cls(ctx, cfg, h)
+
+    def export_tensor(self, idx: int) -> np.ndarray:
+        nb = C.c_size_t()
+        _check(lib().lq8_model_tensor_bytes(C.byref(self._c), idx, C.byref(nb)))
+        kind, _ = self.cfg.tensor_shape(idx)
+        out = np.empty(nb.value // 4 if kind == "f32" else nb.value, dtype=np.float32 if kind == "f32" else np.uint8)
+        _check(lib().lq8_model_export_tensor(self.handle, idx, _ptr(out)))
+        return out
+
+    def export_all(self):
+        return [self.export_tensor(i) for i in range(self.cfg.tensor_count())]
+
+    def clear_kv_cache(self) -> None:
+        _check(lib().lq8_model_clear_kv_cache(self.handle))
+
+    def forward(self, input_ids: Sequence[int], offset: int) -> np.ndarray:
+        ids = np.ascontiguousarray(input_ids, dtype=np.uint32)
+        logits = np.empty(self.cfg.vocab_size, dtype=np.float32)
+        _check(lib().lq8_model_forward(self.handle, _ptr(ids), ids.size, offset, _ptr(logits)))
+        return logits
+
+    def generate_greedy(self, prompt: Sequence[int], max_new_tokens: int):
+        ids = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(max_new_tokens, dtype=np.uint32)
+        st = GenStatsC()
+        _check(lib().lq8_generate_greedy(self.handle, _ptr(ids), ids.size, max_new_tokens, _ptr(out), C.byref(st)))
+        return out, {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
+                     "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph)}
+
+    def free(self) -> None:
+        if self.handle:
+            _check(lib().lq8_model_free(self.handle))
+            self.handle = None
+
+
+def gemv_grouped_device(ctx: Context, problems) -> None:
+    """problems: iterable of (Q8Weight, DeviceBuffer x, DeviceBuffer y)."""
+    arr = (GemvProblemC * len(problems))(*[GemvProblemC(w.handle, x.ptr, y.ptr) for (w, x, y) in problems])
+    _check(lib().lq8_gemv_grouped_device(ctx.handle, arr, len(problems)))
+
+
+def bench_gemv(ctx: Context, problems, mode: int, reps: int) -> float:
+    """Device ms for ``reps`` passes over (Q8Weight, x, y) problems (see lq8_bench_gemv)."""
+    arr = (GemvProblemC * len(problems))(*[GemvProblemC(w.handle, x.ptr, y.ptr) for (w, x, y) in problems])
+    ms = C.c_float(0.0)
+    _check(lib().lq8_bench_gemv(ctx.handle, arr, len(problems), mode, reps, C.byref(ms)))
+    return ms.value

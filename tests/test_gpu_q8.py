@@ -1,0 +1,227 @@
+"""GPU parity of the Q8_0 kernels against the CPU oracle, through the C ABI.
+
+Bar: quantized codes and scales bit-exact; GEMV / GEMM outputs bit-exact with
+the oracle (the kernels follow the oracle's accumulation order) and, as the
+stated contract, within 1e-3 relative error (f32 accumulation).
+"""
+import numpy as np
+import pytest
+
+import lq8
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3  # matvec/matmul tolerance of the contract (f32 accumulation)
+
+
+def rel_err(y, ref):
+    scale = max(float(np.max(np.abs(ref))), float(np.sqrt(np.mean(ref.astype(np.float64) ** 2))), 1e-30)
+    return float(np.max(np.abs(y.astype(np.float64) - ref))) / scale
+
+
+def assert_parity(y, ref):
+    assert y.shape == ref.shape
+    assert rel_err(y, ref) <= REL_TOL
+    bad = np.flatnonzero(y.view(np.uint32) != ref.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} elements differ from the oracle, first at {bad[:5]}: {y.ravel()[bad[:5]]} vs {ref.ravel()[bad[:5]]}"
+
+
+def normal(shape, std, seed):
+    return (np.random.default_rng(seed).standard_normal(shape) * std).astype(np.float32)
+
+
+def edge_blocks():
+    """Blocks that pin the quantizer's special cases."""
+    rows = []
+    rows.append(np.zeros(32, np.float32))                                  # d = 0, codes 0
+    t = np.zeros(32, np.float32); t[0] = 127.0; t[1:8] = [0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 126.5]
+    rows.append(t)                                                         # d = 1: ties round away from zero
+    rows.append(np.full(32, -3.0, np.float32))                             # all equal negative -> -127
+    t = np.linspace(-1e-6, 1e-6, 32).astype(np.float32); rows.append(t)   # f16 subnormal scale
+    t = np.linspace(-1e-38, 2e-38, 32).astype(np.float32); rows.append(t) # f32-subnormal scale, 1/d overflows
+    t = np.ones(32, np.float32) * 7e6; t[3] = -9e6; rows.append(t)         # f16 scale overflow to inf
+    t = normal(32, 1.0, 5); t[7] = np.nan; rows.append(t)                  # NaN ignored by amax, coded 0
+    t = normal(32, 1.0, 6); t[9] = np.inf; rows.append(t)                  # inf
+    return np.concatenate(rows)
+
+
+def test_device_quantizer_bit_exact(ctx):
+    x = np.concatenate([normal(32 * 4096, 1.0, 1), normal(32 * 1024, 0.02, 2), edge_blocks()])
+    ref = oracle.quantize_q8_0(x)
+    host = lq8.quantize_q8_0(x)
+    assert np.array_equal(host, ref)
+    dx = lq8.DeviceBuffer.from_array(ctx, x)
+    db = lq8.DeviceBuffer(ctx, ref.size)
+    lq8._check(lq8.lib().lq8_quantize_q8_0_device(ctx.handle, dx.ptr, x.size, db.ptr))
+    got = db.download(np.uint8, ref.size)
+    dx.free(); db.free()
+    bad = np.flatnonzero(got != ref)
+    assert bad.size == 0, f"blocks differ at bytes {bad[:8]} (block {bad[0] // 34})"
+
+
+def test_weight_upload_download_roundtrip(ctx):
+    n, k = 200, 96  # ragged: 200 rows is not a multiple of the 64-row tile
+    blocks = oracle.quantize_q8_0(normal((n, k), 0.02, 3))
+    w = lq8.Q8Weight.from_blocks(ctx, blocks, n, k)
+    assert np.array_equal(w.download(), blocks)
+    w.free()
+    wf = normal((n, k), 0.5, 4)
+    w2 = lq8.Q8Weight.quantize(ctx, wf)
+    assert np.array_equal(w2.download(), oracle.quantize_q8_0(wf))
+    w2.free()
+
+
+def test_dequantize_rows_exact(ctx):
+    n, k = 130, 64
+    blocks = oracle.quantize_q8_0(normal((n, k), 0.02, 8))
+    w = lq8.Q8Weight.from_blocks(ctx, blocks, n, k)
+    y = lq8.DeviceBuffer(ctx, 5 * k * 4)
+    lq8._check(lq8.lib().lq8_weight_dequantize_rows_device(ctx.handle, w.handle, 120, 5, y.ptr))
+    got = y.download(np.float32, 5 * k)
+    ref = oracle.dequantize_q8_0(blocks, n * k).reshape(n, k)[120:125].ravel()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    y.free(); w.free()
+
+
+def gemv_case(ctx, n, k, seed, x_std=1.0):
+    blocks = oracle.quantize_q8_0(normal((n, k), 0.02, seed))
+    x = normal(k, x_std, seed + 1000)
+    w = lq8.Q8Weight.from_blocks(ctx, blocks, n, k)
+    dx = lq8.DeviceBuffer.from_array(ctx, x)
+    dy = lq8.DeviceBuffer(ctx, n * 4)
+    lq8._check(lq8.lib().lq8_gemv_q8_0_device(ctx.handle, w.handle, dx.ptr, dy.ptr))
+    y = dy.download(np.float32, n)
+    dx.free(); dy.free(); w.free()
+    return y, oracle.gemv_q8_0(blocks, n, k, x)
+
+
+def test_gemv_config1_3072x1024(ctx):
+    y, ref = gemv_case(ctx, 3072, 1024, 11)
+    assert_parity(y, ref)
+
+
+@pytest.mark.parametrize("n,k", [(2048, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (1024, 3072)])
+def test_gemv_qwen3_layer_shapes(ctx, n, k):
+    y, ref = gemv_case(ctx, n, k, n + k)
+    assert_parity(y, ref)
+
+
+def test_gemv_lm_head_151936x1024(ctx):
+    y, ref = gemv_case(ctx, 151936, 1024, 99)
+    assert_parity(y, ref)
+
+
+@pytest.mark.parametrize("n,k", [(1, 32), (65, 96), (100, 288), (7, 8192), (64, 4096), (3, 160)])
+def test_gemv_edge_shapes(ctx, n, k):
+    y, ref = gemv_case(ctx, n, k, 7 * n + k)
+    assert_parity(y, ref)
+
+
+def test_gemv_known_answer(ctx):
+    """test_linear_forward (src/attention.rs:605) on Q8_0-exact weights.
+
+    Each weight row holds 127 in its last slot, so d = 1 and the codes are the
+    integers themselves; x is zero there.  x @ W^T = [14, 32] exactly, as in
+    the reference test, and [14, 32, 50, 68] for src/gpu/gemv.rs:543.
+    """
+    k = 32
+    W = np.zeros((4, k), np.float32)
+    W[:, :3] = [[1, 2, 3], [4, 5, 6], [7, 8, 9], [10, 11, 12]]
+    W[:, -1] = 127.0
+    x = np.zeros(k, np.float32)
+    x[:3] = [1, 2, 3]
+    w = lq8.Q8Weight.quantize(ctx, W)
+    y = lq8.Linear.new(w).forward(x.reshape(1, k))
+    assert y.shape == (1, 4)
+    assert y.ravel().tolist() == [14.0, 32.0, 50.0, 68.0]
+    w.free()
+
+
+def gemm_case(ctx, m, n, k, seed):
+    blocks = oracle.quantize_q8_0(normal((n, k), 0.02, seed))
+    x = normal((m, k), 1.0, seed + 1)
+    w = lq8.Q8Weight.from_blocks(ctx, blocks, n, k)
+    dx = lq8.DeviceBuffer.from_array(ctx, x)
+    dy = lq8.DeviceBuffer(ctx, m * n * 4)
+    lq8._check(lq8.lib().lq8_gemm_q8_0_device(ctx.handle, w.handle, dx.ptr, m, dy.ptr))
+    y = dy.download(np.float32, m * n).reshape(m, n)
+    dx.free(); dy.free(); w.free()
+    return y, oracle.gemm_q8_0(blocks, n, k, x)
+
+
+@pytest.mark.parametrize("n,k", [(3072, 1024), (1024, 3072)])
+def test_gemm_config3_m512(ctx, n, k):
+    y, ref = gemm_case(ctx, 512, n, k, n)
+    assert_parity(y, ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 64, 32), (3, 100, 96), (63, 130, 288), (65, 64, 1024), (130, 192, 256),
+                                   (1, 96, 64)])
+def test_gemm_ragged(ctx, m, n, k):
+    y, ref = gemm_case(ctx, m, n, k, m * 31 + n)
+    assert_parity(y, ref)
+
+
+def test_gemm_int_blocks_exact(ctx):
+    """Per-block int32 sums are exact: with d_w = d_x = 1 (a 127 in every
+    block) the f32 result is the integer dot product itself."""
+    m, n, k = 64, 64, 256
+    rng = np.random.default_rng(4)
+    qw = rng.integers(-127, 128, (n, k)).astype(np.float32)
+    qx = rng.integers(-127, 128, (m, k)).astype(np.float32)
+    qw[:, ::32] = 127.0
+    qx[:, ::32] = 127.0
+    w = lq8.Q8Weight.quantize(ctx, qw)
+    y = lq8.Linear.new(w).forward(qx)
+    exact = qx.astype(np.int64) @ qw.astype(np.int64).T
+    assert np.array_equal(y.astype(np.int64), exact)
+    w.free()
+
+
+def test_linear_forward_dispatch(ctx):
+    n, k = 256, 512
+    blocks = oracle.quantize_q8_0(normal((n, k), 0.02, 21))
+    lin = lq8.Linear.new(lq8.Q8Weight.from_blocks(ctx, blocks, n, k))
+    x1 = normal((1, 1, k), 1.0, 22)
+    assert_parity(lin.forward(x1).reshape(1, n), oracle.linear_forward(blocks, n, k, x1))
+    x5 = normal((1, 5, k), 1.0, 23)
+    y5 = lin.forward(x5)
+    assert y5.shape == (1, 5, n)
+    assert_parity(y5.reshape(5, n), oracle.linear_forward(blocks, n, k, x5))
+    with pytest.raises(lq8.ShapeMismatch):
+        lin.forward(normal((2, k + 32), 1.0, 1))
+    lin.weight.free()
+
+
+def test_grouped_gemv(ctx):
+    shapes = [(2048, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (1024, 3072), (100, 96)]
+    probs, refs, bufs, ws = [], [], [], []
+    for i, (n, k) in enumerate(shapes):
+        blocks = oracle.quantize_q8_0(normal((n, k), 0.02, 300 + i))
+        x = normal(k, 1.0, 400 + i)
+        w = lq8.Q8Weight.from_blocks(ctx, blocks, n, k)
+        dx, dy = lq8.DeviceBuffer.from_array(ctx, x), lq8.DeviceBuffer(ctx, n * 4)
+        probs.append((w, dx, dy))
+        refs.append(oracle.gemv_q8_0(blocks, n, k, x))
+        bufs += [dx, dy]
+        ws.append(w)
+    lq8.gemv_grouped_device(ctx, probs)
+    for (w, dx, dy), ref in zip(probs, refs):
+        assert_parity(dy.download(np.float32, w.n_out), ref)
+    for b in bufs:
+        b.free()
+    for w in ws:
+        w.free()
+
+
+def test_errors_no_fallback(ctx):
+    with pytest.raises(lq8.ShapeMismatch):
+        lq8.Q8Weight.quantize(ctx, np.zeros((4, 33), np.float32))
+    w = lq8.Q8Weight.random(ctx, 64, 64, seed=1)
+    stale = w.handle
+    w.free()
+    with pytest.raises(lq8.InvalidArgument):
+        lq8._check(lq8.lib().lq8_weight_free(stale))
+    with pytest.raises(lq8.InvalidArgument):
+        lq8._check(lq8.lib().lq8_gemv_q8_0_device(ctx.handle, stale, None, None))
