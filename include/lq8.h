@@ -99,6 +99,14 @@ lq8_status lq8_quantize_q8_0_device(lq8_ctx* ctx, const float* d_x, size_t n, vo
 lq8_status lq8_weight_dequantize_rows_device(lq8_ctx* ctx, const lq8_weight* w, size_t row0, size_t nrows,
                                              float* d_y);
 
+/* ---- decoder ops (device pointers) -----------------------------------------
+ * RmsNorm::forward (src/rms_norm.rs:123-177): rows of dim values, input and
+ * output rounded to bf16 (returned as f32 values), weight rounded to bf16. */
+lq8_status lq8_rms_norm_device(lq8_ctx* ctx, const float* d_x, const float* d_w, size_t rows, size_t dim, float eps,
+                               float* d_y);
+/* Tensor::silu, f32 branch (src/tensor.rs:1955-1990): x / (1 + exp(-x)). */
+lq8_status lq8_silu_device(lq8_ctx* ctx, const float* d_x, size_t n, float* d_y);
+
 /* ---- linear forward ------------------------------------------------------
  * Replaces: Linear::forward (src/attention.rs:101-136) and the 2-D
  * Tensor::matmul it calls (src/tensor.rs:804-817, 898-981, 2716-2753;
@@ -160,6 +168,11 @@ lq8_status lq8_model_clear_kv_cache(lq8_model* m);
 /* logits: host f32 [vocab] for the last position (or NULL). offset must equal
  * the number of cached positions (prefill_len + generated - 1 in generate()). */
 lq8_status lq8_model_forward(lq8_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits);
+/* Qwen3Model::forward_with_intermediates (src/model.rs:201-231) plus the
+ * logits: hidden [num_layers + 1][n][hidden] (embedding output, then each
+ * layer's output), final_norm [n][hidden], logits [vocab] (or NULL). */
+lq8_status lq8_model_forward_with_intermediates(lq8_model* m, const uint32_t* ids, size_t n, size_t offset,
+                                                float* hidden, float* final_norm, float* logits);
 
 typedef struct {
     double prefill_ms;      /* prompt forward + first token, device time */

@@ -484,7 +484,23 @@ static void attend(const orc_model* m, size_t layer, size_t kvh, const float* q,
     }
 }
 
+static int model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits, float* hidden,
+                         float* final_norm);
+
 int orc_model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits) {
+    return model_forward(m, ids, n, offset, logits, NULL, NULL);
+}
+
+/* Qwen3Model::forward_with_intermediates (src/model.rs:201-231): hidden is
+ * [num_layers + 1][n][hidden] (embedding output, then each layer's output),
+ * final_norm is [n][hidden]. */
+int orc_model_forward_with_intermediates(orc_model* m, const uint32_t* ids, size_t n, size_t offset, float* hidden,
+                                         float* final_norm, float* logits) {
+    return model_forward(m, ids, n, offset, logits, hidden, final_norm);
+}
+
+static int model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits, float* hidden,
+                         float* final_norm) {
     const orc_qwen3_config* c = &m->c;
     if (n == 0) return 1;
     if (offset != m->kv_len || offset + n > c->max_positions) return 3;
@@ -514,6 +530,7 @@ int orc_model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t offset
      * dequantized Q8_0, exact in f32. */
     for (size_t i = 0; i < n; i++)
         orc_dequantize_q8_0(m->embed + (size_t)ids[i] * nbh * ORC_BLOCK_BYTES, Hd, H + i * Hd);
+    if (hidden) memcpy(hidden, H, n * Hd * sizeof(float));
 
     for (size_t l = 0; l < c->num_layers; l++) {
         const orc_layer* L = &m->layers[l];
@@ -562,7 +579,9 @@ int orc_model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t offset
         for (size_t t = 0; t < n * I; t++) G[t] = orc_silu(G[t]) * U[t];
         orc_linear_forward(L->down, Hd, I, G, n, O);
         for (size_t t = 0; t < n * Hd; t++) H[t] = H[t] + O[t];
+        if (hidden) memcpy(hidden + (l + 1) * n * Hd, H, n * Hd * sizeof(float));
     }
+    if (final_norm) orc_rms_norm(H, m->final_norm, n, Hd, c->rms_norm_eps, final_norm);
     m->kv_len = offset + n;
     /* final norm of the last position, then lm_head GEMV (src/model.rs:357-371) */
     orc_rms_norm(H + (n - 1) * Hd, m->final_norm, 1, Hd, c->rms_norm_eps, X);

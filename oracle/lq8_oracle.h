@@ -76,6 +76,8 @@ orc_model* orc_model_new(const orc_qwen3_config* cfg, const void* const* tensors
 void orc_model_free(orc_model* m);
 void orc_model_clear_kv_cache(orc_model* m);
 int orc_model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits);
+int orc_model_forward_with_intermediates(orc_model* m, const uint32_t* ids, size_t n, size_t offset, float* hidden,
+                                         float* final_norm, float* logits);
 int orc_generate_greedy(orc_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
                         uint32_t* out_tokens, float* out_margins);
 

@@ -63,6 +63,7 @@ def lib():
             "orc_model_free": (None, [vp]),
             "orc_model_clear_kv_cache": (None, [vp]),
             "orc_model_forward": (C.c_int, [vp, vp, sz, sz, vp]),
+            "orc_model_forward_with_intermediates": (C.c_int, [vp, vp, sz, sz, vp, vp, vp]),
             "orc_generate_greedy": (C.c_int, [vp, vp, sz, sz, vp, vp]),
         }
         for name, (res, args) in sigs.items():
@@ -227,6 +228,17 @@ class Model:
         if rc:
             raise ValueError(f"oracle forward failed ({rc})")
         return logits
+
+    def forward_with_intermediates(self, ids, offset: int):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        n, H = ids.size, self.cfg.hidden_size
+        hidden = np.empty((self.cfg.num_hidden_layers + 1, n, H), dtype=np.float32)
+        fin = np.empty((n, H), dtype=np.float32)
+        logits = np.empty(self.cfg.vocab_size, dtype=np.float32)
+        rc = lib().orc_model_forward_with_intermediates(self.h, _p(ids), n, offset, _p(hidden), _p(fin), _p(logits))
+        if rc:
+            raise ValueError(f"oracle forward failed ({rc})")
+        return hidden, fin, logits
 
     def generate_greedy(self, prompt, max_new: int):
         ids = np.ascontiguousarray(prompt, dtype=np.uint32)

@@ -145,6 +145,7 @@ lq8_status launch_attention(hipStream_t s, const AttnLaunch& a);
 
 lq8_status launch_rms_norm_rows(hipStream_t s, const float* x, const float* w, int rows, int dim, float eps, float* y);
 lq8_status launch_silu_mul(hipStream_t s, const float* gu, int rows, int inter, float* act);
+lq8_status launch_silu(hipStream_t s, const float* x, size_t n, float* y);
 // Argmax with last-index ties over logits[n]; writes tokens_out[*d_step] and
 // *d_tok, then advances *d_pos and *d_step (all device scalars).
 lq8_status launch_argmax_step(hipStream_t s, const float* logits, int n, uint32_t* d_tok, uint32_t* tokens_out,

@@ -221,13 +221,21 @@ lq8_status ensure_prefill(lq8_model* m, size_t n) {
 
 // One position through the decoder (src/model.rs:170-195 with L = 1) and the
 // lm_head GEMV; the token id comes from device memory.
-lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, int pos_base) {
+// trace (optional, host): [0] embedding output, [1 + l] output of layer l, all [n][hidden].
+lq8_status trace_copy(lq8_model* m, float* host, const float* dev, size_t count) {
+    if (!host) return LQ8_OK;
+    LQ8_HIP(hipMemcpyAsync(host, dev, count * sizeof(float), hipMemcpyDeviceToHost, m->ctx->stream));
+    return LQ8_OK;
+}
+
+lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, int pos_base, float* trace = nullptr) {
     hipStream_t s = m->ctx->stream;
     const lq8_qwen3_config& c = m->c;
     const int Hd = (int)c.hidden_size, I = (int)c.intermediate_size;
     const size_t layer_kv = (size_t)c.num_kv_heads * c.head_dim * c.max_positions;
     lq8_status st;
     if ((st = launch_dequant_rows(s, m->embed, d_id, 0, 1, m->h))) return st;
+    if ((st = trace_copy(m, trace, m->h, Hd))) return st;
     for (size_t l = 0; l < m->layers.size(); l++) {
         Layer& L = m->layers[l];
         GemvLaunch g1{L.qkv->codes, L.qkv->scales, m->h, L.in_norm, c.rms_norm_eps, m->qkv, nullptr, (int)m->QKV, Hd};
@@ -246,6 +254,7 @@ lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, 
         if ((st = launch_gemv(s, XS_RMSNORM, g3))) return st;
         GemvLaunch g4{L.down->codes, L.down->scales, m->gu, nullptr, 0.0f, m->h, m->h, Hd, I};
         if ((st = launch_gemv(s, XS_SILU, g4))) return st;
+        if (trace && (st = trace_copy(m, trace + (l + 1) * Hd, m->h, Hd))) return st;
     }
     GemvLaunch g5{m->embed->codes, m->embed->scales, m->h, m->final_norm, c.rms_norm_eps, m->logits, nullptr,
                   (int)c.vocab_size, Hd};
@@ -261,13 +270,14 @@ lq8_status quant_gemm(lq8_model* m, const float* x, int n, const lq8_weight* w, 
 
 // n positions starting at pos_base (src/model.rs:170-195), then the last
 // position's logits.
-lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base) {
+lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base, float* trace = nullptr) {
     hipStream_t s = m->ctx->stream;
     const lq8_qwen3_config& c = m->c;
     const int Hd = (int)c.hidden_size, I = (int)c.intermediate_size;
     const size_t layer_kv = (size_t)c.num_kv_heads * c.head_dim * c.max_positions;
     lq8_status st;
     if ((st = launch_dequant_rows(s, m->embed, m->d_ids, 0, n, m->P_h))) return st;
+    if ((st = trace_copy(m, trace, m->P_h, (size_t)n * Hd))) return st;
     for (size_t l = 0; l < m->layers.size(); l++) {
         Layer& L = m->layers[l];
         if ((st = launch_rms_norm_rows(s, m->P_h, L.in_norm, n, Hd, c.rms_norm_eps, m->P_x))) return st;
@@ -285,6 +295,7 @@ lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base) {
         if ((st = quant_gemm(m, m->P_x, n, L.gu, m->P_gu, nullptr))) return st;
         if ((st = launch_silu_mul(s, m->P_gu, n, I, m->P_act))) return st;
         if ((st = quant_gemm(m, m->P_act, n, L.down, m->P_h, m->P_h))) return st;
+        if (trace && (st = trace_copy(m, trace + (l + 1) * (size_t)n * Hd, m->P_h, (size_t)n * Hd))) return st;
     }
     // final norm + lm_head on the last position only (src/model.rs:357-371)
     GemvLaunch g{m->embed->codes, m->embed->scales, m->P_h + (size_t)(n - 1) * Hd, m->final_norm, c.rms_norm_eps,
@@ -456,6 +467,40 @@ lq8_status lq8_model_forward(lq8_model* m, const uint32_t* ids, size_t n, size_t
         st = enqueue_prefill(m, (int)n, (int)offset);
     }
     if (st) return st;
+    if (logits)
+        LQ8_HIP(hipMemcpyAsync(logits, m->logits, m->c.vocab_size * sizeof(float), hipMemcpyDeviceToHost, s));
+    LQ8_HIP(hipStreamSynchronize(s));
+    m->kv_len = offset + n;
+    return LQ8_OK;
+}
+
+lq8_status lq8_model_forward_with_intermediates(lq8_model* m, const uint32_t* ids, size_t n, size_t offset,
+                                                float* hidden, float* final_norm, float* logits) {
+    CHECK_M(m);
+    if (!ids || n == 0) return fail(LQ8_ERR_INVALID_ARG, "input_ids cannot be empty");
+    if (!hidden || !final_norm) return fail(LQ8_ERR_INVALID_ARG, "null output pointer");
+    if (offset != m->kv_len) return fail(LQ8_ERR_INVALID_ARG, "offset must equal the number of cached positions");
+    if (offset + n > m->c.max_positions) return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "positions exceed max_positions");
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= m->c.vocab_size) return fail(LQ8_ERR_INVALID_ARG, "token id out of range for vocab_size");
+    LQ8_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    const int Hd = (int)m->c.hidden_size;
+    lq8_status st;
+    if ((st = ensure_ids(m, n)) || (st = ensure_prefill(m, n))) return st;
+    LQ8_HIP(hipMemcpyAsync(m->d_ids, ids, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    const float* last;
+    if (n == 1) {
+        st = enqueue_decode(m, m->d_ids, nullptr, (int)offset, hidden);
+        last = m->h;
+    } else {
+        st = enqueue_prefill(m, (int)n, (int)offset, hidden);
+        last = m->P_h;
+    }
+    if (st) return st;
+    // final norm of every position (src/model.rs:194)
+    if ((st = launch_rms_norm_rows(s, last, m->final_norm, (int)n, Hd, m->c.rms_norm_eps, m->P_x))) return st;
+    LQ8_HIP(hipMemcpyAsync(final_norm, m->P_x, n * Hd * sizeof(float), hipMemcpyDeviceToHost, s));
     if (logits)
         LQ8_HIP(hipMemcpyAsync(logits, m->logits, m->c.vocab_size * sizeof(float), hipMemcpyDeviceToHost, s));
     LQ8_HIP(hipStreamSynchronize(s));

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(64) void k_qk_rope_kv(QkRopeLaunch a) {
     }
     acc = wave_sum64(acc);
     const float mean = __fdiv_rn(acc, (float)hd);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(mean + a.eps));
+    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(mean + a.eps));
     for (int t = 0; t < per; t++) y[t] = bf16_round((xb[t] * inv) * bf16_round(w[lane + 64 * t]));
     const float* cs = a.cos_t + (size_t)pos * R;
     const float* sn = a.sin_t + (size_t)pos * R;
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(64) void k_rms_norm_rows(const float* __restrict__ 
     }
     acc = wave_sum64(acc);
     const float mean = __fdiv_rn(acc, (float)dim);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));
+    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(mean + eps));
     float* yr = y + (size_t)r * dim;
     for (int i = lane; i < dim; i += 64) yr[i] = bf16_round((bf16_round(xr[i]) * inv) * bf16_round(w[i]));
 }
@@ -149,6 +149,14 @@ __global__ void k_silu_mul(const float* __restrict__ gu, int rows, int inter, fl
     float g = gu[r * 2 * inter + j], u = gu[r * 2 * inter + inter + j];
     float s = __fdiv_rn(g, 1.0f + expf_cr(-g));
     act[idx] = s * u;
+}
+
+// Tensor::silu f32 branch (src/tensor.rs:1978): x / (1 + exp(-x)).
+__global__ void k_silu(const float* __restrict__ x, size_t n, float* __restrict__ y) {
+    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n) return;
+    float v = x[idx];
+    y[idx] = __fdiv_rn(v, 1.0f + expf_cr(-v));
 }
 
 // Greedy pick (src/generate.rs:153-174): maximum, last index on ties.
@@ -212,6 +220,13 @@ lq8_status launch_rms_norm_rows(hipStream_t s, const float* x, const float* w, i
 lq8_status launch_silu_mul(hipStream_t s, const float* gu, int rows, int inter, float* act) {
     size_t n = (size_t)rows * inter;
     hipLaunchKernelGGL(k_silu_mul, dim3(grid1(n, 256)), dim3(256), 0, s, gu, rows, inter, act);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
+lq8_status launch_silu(hipStream_t s, const float* x, size_t n, float* y) {
+    if (!n) return LQ8_OK;
+    hipLaunchKernelGGL(k_silu, dim3(grid1(n, 256)), dim3(256), 0, s, x, n, y);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

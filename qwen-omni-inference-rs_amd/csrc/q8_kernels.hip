@@ -237,7 +237,7 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, const float
             for (int d = 32; d >= 1; d >>= 1) a = a + __shfl_xor(a, d, 64);
             if (tid == 0) {
                 float mean = __fdiv_rn(a, (float)k);
-                red[0] = __fdiv_rn(1.0f, __fsqrt_rn(mean + eps));
+                red[0] = __fdiv_rn(1.0f, __builtin_sqrtf(mean + eps));
             }
         }
         __syncthreads();

@@ -407,6 +407,23 @@ lq8_status lq8_weight_dequantize_rows_device(lq8_ctx* ctx, const lq8_weight* w, 
     return launch_dequant_rows(ctx->stream, w, nullptr, row0, nrows, d_y);
 }
 
+// ---- decoder ops ------------------------------------------------------------------
+
+lq8_status lq8_rms_norm_device(lq8_ctx* ctx, const float* d_x, const float* d_w, size_t rows, size_t dim, float eps,
+                               float* d_y) {
+    CHECK_CTX(ctx);
+    if (!d_x || !d_w || !d_y) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (dim == 0 || dim > (size_t)INT32_MAX || rows > 0x7FFFFFFF) return fail(LQ8_ERR_SHAPE_MISMATCH, "bad shape");
+    if (rows == 0) return LQ8_OK;
+    return launch_rms_norm_rows(ctx->stream, d_x, d_w, (int)rows, (int)dim, eps, d_y);
+}
+
+lq8_status lq8_silu_device(lq8_ctx* ctx, const float* d_x, size_t n, float* d_y) {
+    CHECK_CTX(ctx);
+    if ((!d_x || !d_y) && n) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    return launch_silu(ctx->stream, d_x, n, d_y);
+}
+
 // ---- linear forward --------------------------------------------------------------
 
 lq8_status lq8_gemv_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, float* d_y) {

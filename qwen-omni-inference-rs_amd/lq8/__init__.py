@@ -119,6 +119,9 @@ _SIGS = [
     ("lq8_weight_free", C.c_int, [C.c_void_p]),
     ("lq8_quantize_q8_0_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("lq8_weight_dequantize_rows_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
+    ("lq8_rms_norm_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_float,
+                                      C.c_void_p]),
+    ("lq8_silu_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("lq8_linear_forward", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("lq8_linear_forward_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("lq8_gemv_q8_0_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
@@ -133,6 +136,8 @@ _SIGS = [
     ("lq8_model_export_tensor", C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
     ("lq8_model_clear_kv_cache", C.c_int, [C.c_void_p]),
     ("lq8_model_forward", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
+    ("lq8_model_forward_with_intermediates", C.c_int,
+     [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p, C.c_void_p]),
     ("lq8_generate_greedy", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.POINTER(GenStatsC)]),
     ("lq8_model_free", C.c_int, [C.c_void_p]),
@@ -260,6 +265,29 @@ class DeviceBuffer:
         if self.ptr:
             _check(lib().lq8_device_free(self.ctx.handle, self.ptr))
             self.ptr = None
+
+
+def rms_norm_device(ctx: "Context", x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """RmsNorm::forward on the device over the rows of x."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    dx, dw = DeviceBuffer.from_array(ctx, x), DeviceBuffer.from_array(ctx, w)
+    dy = DeviceBuffer(ctx, x.nbytes)
+    try:
+        _check(lib().lq8_rms_norm_device(ctx.handle, dx.ptr, dw.ptr, x.size // w.size, w.size, eps, dy.ptr))
+        return dy.download(np.float32, x.size).reshape(x.shape)
+    finally:
+        dx.free(); dw.free(); dy.free()
+
+
+def silu_device(ctx: "Context", x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    dx, dy = DeviceBuffer.from_array(ctx, x), DeviceBuffer(ctx, x.nbytes)
+    try:
+        _check(lib().lq8_silu_device(ctx.handle, dx.ptr, x.size, dy.ptr))
+        return dy.download(np.float32, x.size).reshape(x.shape)
+    finally:
+        dx.free(); dy.free()
 
 
 class Q8Weight:
@@ -417,6 +445,17 @@ class Qwen3ForCausalLM:
         logits = np.empty(self.cfg.vocab_size, dtype=np.float32)
         _check(lib().lq8_model_forward(self.handle, _ptr(ids), ids.size, offset, _ptr(logits)))
         return logits
+
+    def forward_with_intermediates(self, input_ids: Sequence[int], offset: int):
+        """(hidden [layers+1, n, hidden], final_norm [n, hidden], logits [vocab])."""
+        ids = np.ascontiguousarray(input_ids, dtype=np.uint32)
+        n, H = ids.size, self.cfg.hidden_size
+        hidden = np.empty((self.cfg.num_hidden_layers + 1, n, H), dtype=np.float32)
+        fin = np.empty((n, H), dtype=np.float32)
+        logits = np.empty(self.cfg.vocab_size, dtype=np.float32)
+        _check(lib().lq8_model_forward_with_intermediates(self.handle, _ptr(ids), n, offset, _ptr(hidden), _ptr(fin),
+                                                          _ptr(logits)))
+        return hidden, fin, logits
 
     def generate_greedy(self, prompt: Sequence[int], max_new_tokens: int):
         ids = np.ascontiguousarray(prompt, dtype=np.uint32)
