@@ -54,7 +54,11 @@ struct lq8_ctx {
     size_t scratch_bytes = 0;
     void* problems = nullptr;  // device copy of grouped GEMV descriptors
     size_t problems_bytes = 0;
+    float* gemv_partials = nullptr;  // split-K partials of the decode GEMV
+    int* gemv_counters = nullptr;    // per-tile arrival counters, kept at zero
 };
+constexpr long long GEMV_PARTIALS_CAP = 4ll << 20;  // floats
+constexpr int GEMV_COUNTERS_CAP = 1 << 16;
 
 struct lq8_weight {
     lq8_ctx* ctx = nullptr;
@@ -82,8 +86,17 @@ struct GemvLaunch {
     float* y;              // output [n]
     const float* resid;    // if non-null: y = resid + Wx
     int n, k;
+    // split-K combine buffers (from the context); counters are zero between launches
+    float* partials = nullptr;
+    int* counters = nullptr;
+    long long partials_cap = 0;
+    int counters_cap = 0;
 };
 lq8_status launch_gemv(hipStream_t s, XSource xs, const GemvLaunch& a);
+// One workgroup per 64-row tile (all groups in one workgroup, no counters).
+lq8_status launch_gemv_tile_wg(hipStream_t s, XSource xs, const GemvLaunch& a);
+// Point a launch at the context's split-K buffers.
+void gemv_attach(GemvLaunch& a, const lq8_ctx* ctx);
 
 // Grouped GEMV over independent problems (device-side descriptor table).
 struct GemvProblemDev {
@@ -124,7 +137,7 @@ struct QkRopeLaunch {
     const float* cos_t;    // [max_pos][head_dim/2]
     const float* sin_t;
     float* q_out;          // [n][q_dim] normalized, rotated queries
-    float* k_cache_t;      // [kv_heads][head_dim][max_pos] (this layer)
+    float* k_cache;        // [kv_heads][max_pos][head_dim] (this layer)
     float* v_cache;        // [kv_heads][max_pos][head_dim] (this layer)
     const int* d_pos;
     int pos_base, n, num_heads, num_kv_heads, head_dim, max_pos;
@@ -134,7 +147,7 @@ lq8_status launch_qk_rope_kv(hipStream_t s, const QkRopeLaunch& a);
 
 struct AttnLaunch {
     const float* q;        // [n][num_heads*head_dim]
-    const float* k_cache_t;
+    const float* k_cache;
     const float* v_cache;
     float* out;            // [n][num_heads*head_dim]
     const int* d_pos;
@@ -142,6 +155,26 @@ struct AttnLaunch {
     float scale;
 };
 lq8_status launch_attention(hipStream_t s, const AttnLaunch& a);
+
+// Decode attention for one new position (reads the position from d_pos or
+// pos_base): q/k RmsNorm + RoPE + KV append fused into the scores kernel,
+// then softmax and p.v per kv group.
+struct AttnDecodeLaunch {
+    const float* qkv;      // [q_dim + 2*kv_dim]
+    const float* q_norm;
+    const float* k_norm;
+    const float* cos_t;
+    const float* sin_t;
+    float* k_cache;        // [kv_heads][max_pos][head_dim] (this layer)
+    float* v_cache;        // [kv_heads][max_pos][head_dim]
+    float* scores;         // [num_heads][max_pos] scratch
+    float* out;            // [num_heads*head_dim]
+    const int* d_pos;
+    int pos_base, num_heads, num_kv_heads, head_dim, max_pos;
+    float eps, scale;
+};
+lq8_status launch_attention_decode(hipStream_t s, const AttnDecodeLaunch& a);
+bool attention_decode_supported(int num_heads, int num_kv_heads, int head_dim, int max_pos);
 
 lq8_status launch_rms_norm_rows(hipStream_t s, const float* x, const float* w, int rows, int dim, float eps, float* y);
 lq8_status launch_silu_mul(hipStream_t s, const float* gu, int rows, int inter, float* act);

@@ -34,10 +34,12 @@ struct lq8_model {
     float* final_norm = nullptr;
     std::vector<Layer> layers;
     float *cos_t = nullptr, *sin_t = nullptr;
-    float *kc = nullptr, *vc = nullptr;  // [layer][kv_head][head_dim][pos] / [layer][kv_head][pos][head_dim]
+    float *kc = nullptr, *vc = nullptr;  // [layer][kv_head][pos][head_dim] each
     size_t kv_len = 0;
     // single-position buffers
     float *h = nullptr, *qkv = nullptr, *qr = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
+    float* scores = nullptr;  // [num_heads][max_pos] decode attention scores
+    bool fused_attn = false;  // decode attention through launch_attention_decode
     uint32_t* d_ids = nullptr;
     size_t ids_cap = 0;
     int *d_pos = nullptr, *d_step = nullptr;
@@ -90,7 +92,7 @@ void release(lq8_model* m) {
         F(L.in_norm); F(L.post_norm); F(L.q_norm); F(L.k_norm);
     }
     F(m->cos_t); F(m->sin_t); F(m->kc); F(m->vc);
-    F(m->h); F(m->qkv); F(m->qr); F(m->attn); F(m->gu); F(m->logits);
+    F(m->h); F(m->qkv); F(m->qr); F(m->attn); F(m->gu); F(m->logits); F(m->scores);
     F(m->d_ids); F(m->d_pos); F(m->d_step); F(m->d_tok); F(m->d_tokens);
     F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_act); F(m->P_xs); F(m->P_xq);
     delete m;
@@ -138,8 +140,10 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_qwen3_config* c, lq8_model* m)
     LQ8_HIP(hipMemset(m->vc, 0, kv * sizeof(float)));
     if ((st = dalloc(&m->h, Hd)) || (st = dalloc(&m->qkv, m->QKV)) || (st = dalloc(&m->qr, m->QD)) ||
         (st = dalloc(&m->attn, m->QD)) || (st = dalloc(&m->gu, 2 * I)) || (st = dalloc(&m->logits, c->vocab_size)) ||
-        (st = dalloc(&m->d_pos, 1)) || (st = dalloc(&m->d_step, 1)) || (st = dalloc(&m->d_tok, 1)))
+        (st = dalloc(&m->d_pos, 1)) || (st = dalloc(&m->d_step, 1)) || (st = dalloc(&m->d_tok, 1)) ||
+        (st = dalloc(&m->scores, (size_t)c->num_heads * P)))
         return st;
+    m->fused_attn = attention_decode_supported((int)c->num_heads, (int)c->num_kv_heads, (int)hd, (int)P);
     LQ8_HIP(hipEventCreate(&m->e0));
     LQ8_HIP(hipEventCreate(&m->e1));
     LQ8_HIP(hipEventCreate(&m->e2));
@@ -239,25 +243,38 @@ lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, 
     for (size_t l = 0; l < m->layers.size(); l++) {
         Layer& L = m->layers[l];
         GemvLaunch g1{L.qkv->codes, L.qkv->scales, m->h, L.in_norm, c.rms_norm_eps, m->qkv, nullptr, (int)m->QKV, Hd};
+        gemv_attach(g1, m->ctx);
         if ((st = launch_gemv(s, XS_RMSNORM, g1))) return st;
-        QkRopeLaunch qr{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->qr, m->kc + l * layer_kv,
-                        m->vc + l * layer_kv, d_pos, pos_base, 1, (int)c.num_heads, (int)c.num_kv_heads,
-                        (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps};
-        if ((st = launch_qk_rope_kv(s, qr))) return st;
-        AttnLaunch at{m->qr, m->kc + l * layer_kv, m->vc + l * layer_kv, m->attn, d_pos, pos_base, 1,
-                      (int)c.num_heads, (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions,
-                      1.0f / std::sqrt((float)c.head_dim)};
-        if ((st = launch_attention(s, at))) return st;
+        if (m->fused_attn) {
+            AttnDecodeLaunch ad{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->kc + l * layer_kv,
+                                m->vc + l * layer_kv, m->scores, m->attn, d_pos, pos_base, (int)c.num_heads,
+                                (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps,
+                                1.0f / std::sqrt((float)c.head_dim)};
+            if ((st = launch_attention_decode(s, ad))) return st;
+        } else {
+            QkRopeLaunch qr{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->qr, m->kc + l * layer_kv,
+                            m->vc + l * layer_kv, d_pos, pos_base, 1, (int)c.num_heads, (int)c.num_kv_heads,
+                            (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps};
+            if ((st = launch_qk_rope_kv(s, qr))) return st;
+            AttnLaunch at{m->qr, m->kc + l * layer_kv, m->vc + l * layer_kv, m->attn, d_pos, pos_base, 1,
+                          (int)c.num_heads, (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions,
+                          1.0f / std::sqrt((float)c.head_dim)};
+            if ((st = launch_attention(s, at))) return st;
+        }
         GemvLaunch g2{L.o->codes, L.o->scales, m->attn, nullptr, 0.0f, m->h, m->h, Hd, (int)m->QD};
+        gemv_attach(g2, m->ctx);
         if ((st = launch_gemv(s, XS_PLAIN, g2))) return st;
         GemvLaunch g3{L.gu->codes, L.gu->scales, m->h, L.post_norm, c.rms_norm_eps, m->gu, nullptr, 2 * I, Hd};
+        gemv_attach(g3, m->ctx);
         if ((st = launch_gemv(s, XS_RMSNORM, g3))) return st;
         GemvLaunch g4{L.down->codes, L.down->scales, m->gu, nullptr, 0.0f, m->h, m->h, Hd, I};
+        gemv_attach(g4, m->ctx);
         if ((st = launch_gemv(s, XS_SILU, g4))) return st;
         if (trace && (st = trace_copy(m, trace + (l + 1) * Hd, m->h, Hd))) return st;
     }
     GemvLaunch g5{m->embed->codes, m->embed->scales, m->h, m->final_norm, c.rms_norm_eps, m->logits, nullptr,
                   (int)c.vocab_size, Hd};
+    gemv_attach(g5, m->ctx);
     return launch_gemv(s, XS_RMSNORM, g5);
 }
 
@@ -300,6 +317,7 @@ lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base, float* trace = nul
     // final norm + lm_head on the last position only (src/model.rs:357-371)
     GemvLaunch g{m->embed->codes, m->embed->scales, m->P_h + (size_t)(n - 1) * Hd, m->final_norm, c.rms_norm_eps,
                  m->logits, nullptr, (int)c.vocab_size, Hd};
+    gemv_attach(g, m->ctx);
     return launch_gemv(s, XS_RMSNORM, g);
 }
 

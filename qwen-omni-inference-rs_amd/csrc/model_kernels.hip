@@ -56,9 +56,9 @@ __global__ __launch_bounds__(64) void k_qk_rope_kv(QkRopeLaunch a) {
             q[d] = o1;
             q[d + R] = o2;
         } else {
-            float* kt = a.k_cache_t + (size_t)kvh * hd * a.max_pos;
-            kt[(size_t)d * a.max_pos + pos] = o1;
-            kt[(size_t)(d + R) * a.max_pos + pos] = o2;
+            float* kr = a.k_cache + ((size_t)kvh * a.max_pos + pos) * hd;
+            kr[d] = o1;
+            kr[d + R] = o2;
         }
     }
     if (!isq) {
@@ -86,11 +86,11 @@ __global__ __launch_bounds__(256) void k_attention(AttnLaunch a) {
     float* sc = red + 8;
     for (int d = tid; d < hd; d += 256) q[d] = a.q[(size_t)i * QD + h * hd + d];
     __syncthreads();
-    const float* KT = a.k_cache_t + (size_t)kvh * hd * P;
+    const float* K = a.k_cache + (size_t)kvh * P * hd;
     float lmax = -__builtin_huge_valf();
     for (int j = tid; j < L; j += 256) {
         float s = 0.0f;
-        for (int d = 0; d < hd; d++) s = s + q[d] * KT[(size_t)d * P + j];
+        for (int d = 0; d < hd; d++) s = s + q[d] * K[(size_t)j * hd + d];
         s = s * a.scale;
         sc[j] = s;
         lmax = s > lmax ? s : lmax;
@@ -122,6 +122,143 @@ __global__ __launch_bounds__(256) void k_attention(AttnLaunch a) {
         for (int j = 0; j < L; j++) o = o + sc[j] * V[(size_t)j * hd + d];
         a.out[(size_t)i * QD + h * hd + d] = o;
     }
+}
+
+
+// ---- decode attention (one new position) ------------------------------------
+
+// The q-head's query and, when this chunk holds the new position, the new
+// key: RmsNorm per head then RoPE, computed by one wave (lane l holds
+// elements l, l+64, ...).  Same arithmetic as k_qk_rope_kv.
+__device__ __forceinline__ void norm_rope_head(const float* src, const float* w, const float* cs, const float* sn,
+                                               int hd, float eps, float* dst) {
+    const int lane = threadIdx.x & 63, R = hd / 2, per = hd / 64;
+    float xb[8], y[8];
+    float acc = 0.0f;
+    for (int t = 0; t < per; t++) {
+        float v = bf16_round(src[lane + 64 * t]);
+        xb[t] = v;
+        acc = acc + v * v;
+    }
+    acc = wave_sum64(acc);
+    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)hd) + eps));
+    for (int t = 0; t < per; t++) y[t] = bf16_round((xb[t] * inv) * bf16_round(w[lane + 64 * t]));
+    for (int t = 0; t < per / 2; t++) {
+        const int d = lane + 64 * t;
+        const float c = cs[d & ~1], s = sn[d & ~1];
+        const float x1 = y[t], x2 = y[t + per / 2];
+        dst[d] = x1 * c - x2 * s;
+        dst[d + R] = x2 * c + x1 * s;
+    }
+}
+
+// grid (num_heads, max_pos / 64), block 64: scores of 64 positions of one
+// q-head, s_j = (q . k_j sequential over head_dim) * scale.  The workgroup
+// holding the new position also appends its key and value to the cache
+// (the first q-head of each kv group writes; the others recompute the key).
+__global__ __launch_bounds__(64) void k_attn_scores(AttnDecodeLaunch a) {
+    __shared__ float qs[512];
+    __shared__ float ks[512];
+    const int h = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
+    const int hd = a.head_dim, P = a.max_pos, groups = a.num_heads / a.num_kv_heads;
+    const int kvh = h / groups;
+    const int pos = a.d_pos ? *a.d_pos : a.pos_base;
+    const int L = pos + 1;
+    const int p = c * 64 + lane;
+    if (c * 64 >= L) return;
+    const int QD = a.num_heads * hd, KD = a.num_kv_heads * hd;
+    const float* kc = a.k_cache + (size_t)kvh * P * hd;
+    // key row of this lane's position (cached positions only), loaded first
+    float4 kr[32];
+    const bool cached = p < pos;
+    if (cached) {
+        const float4* src = (const float4*)(kc + (size_t)p * hd);
+        for (int t = 0; t < hd / 4; t++) kr[t] = src[t];
+    }
+    const float* cs = a.cos_t + (size_t)pos * (hd / 2);
+    const float* sn = a.sin_t + (size_t)pos * (hd / 2);
+    norm_rope_head(a.qkv + h * hd, a.q_norm, cs, sn, hd, a.eps, qs);
+    const bool has_new = pos >= c * 64 && pos < c * 64 + 64;
+    if (has_new) {
+        norm_rope_head(a.qkv + QD + kvh * hd, a.k_norm, cs, sn, hd, a.eps, ks);
+        __syncthreads();
+        if (h % groups == 0) {
+            float* krow = a.k_cache + ((size_t)kvh * P + pos) * hd;
+            float* vrow = a.v_cache + ((size_t)kvh * P + pos) * hd;
+            const float* v = a.qkv + QD + KD + kvh * hd;
+            for (int d = lane; d < hd; d += 64) {
+                krow[d] = ks[d];
+                vrow[d] = v[d];
+            }
+        }
+    }
+    __syncthreads();
+    if (p >= L) return;
+    float s = 0.0f;
+    if (cached) {
+        for (int t = 0; t < hd / 4; t++) {
+            s = s + qs[4 * t] * kr[t].x;
+            s = s + qs[4 * t + 1] * kr[t].y;
+            s = s + qs[4 * t + 2] * kr[t].z;
+            s = s + qs[4 * t + 3] * kr[t].w;
+        }
+    } else {
+        for (int d = 0; d < hd; d++) s = s + qs[d] * ks[d];
+    }
+    a.scores[(size_t)h * P + p] = s * a.scale;
+}
+
+// grid (num_kv_heads), block 64 * groups * head_dim / 64: softmax of each
+// q-head of the kv group (max, exp(s - max), SUM64, divide), then
+// out[h][d] = sum_j p_j v_j[d] sequentially over j, V staged through LDS in
+// chunks of 32 positions.
+__global__ __launch_bounds__(1024) void k_attn_pv(AttnDecodeLaunch a) {
+    extern __shared__ float sm[];
+    const int kvh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hd = a.head_dim, P = a.max_pos, groups = a.num_heads / a.num_kv_heads;
+    const int L = (a.d_pos ? *a.d_pos : a.pos_base) + 1;
+    const int nt = blockDim.x;
+    float* pr = sm;                  // [groups][P] probabilities
+    float* vt = pr + groups * P;     // [32][hd] staged values
+    // softmax rows: wave w < groups handles q-head kvh*groups + w
+    if (wave < groups) {
+        const int h = kvh * groups + wave;
+        const float* sc = a.scores + (size_t)h * P;
+        float* p = pr + wave * P;
+        float mx = -__builtin_huge_valf();
+        for (int j = lane; j < L; j += 64) {
+            float v = sc[j];
+            p[j] = v;
+            mx = v > mx ? v : mx;
+        }
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            float o = __shfl_xor(mx, d, 64);
+            mx = o > mx ? o : mx;
+        }
+        float acc = 0.0f;
+        for (int j = lane; j < L; j += 64) {
+            float e = expf_cr(p[j] - mx);
+            p[j] = e;
+            acc = acc + e;
+        }
+        acc = wave_sum64(acc);
+        for (int j = lane; j < L; j += 64) p[j] = __fdiv_rn(p[j], acc);
+    }
+    __syncthreads();
+    const int hq = tid / hd, d = tid % hd;          // output element of this thread
+    const float* V = a.v_cache + (size_t)kvh * P * hd;
+    const float* p = pr + hq * P;
+    float o = 0.0f;
+    for (int j0 = 0; j0 < L; j0 += 32) {
+        const int nj = min(32, L - j0);
+        for (int i = tid * 4; i < nj * hd; i += nt * 4) *(float4*)(vt + i) = *(const float4*)(V + (size_t)j0 * hd + i);
+        __syncthreads();
+        if (hq < groups)
+            for (int j = 0; j < nj; j++) o = o + p[j0 + j] * vt[j * hd + d];
+        __syncthreads();
+    }
+    if (hq < groups) a.out[(size_t)(kvh * groups + hq) * hd + d] = o;
 }
 
 // RmsNorm of each row (src/rms_norm.rs:143-176), one wave per row.
@@ -207,6 +344,26 @@ lq8_status launch_attention(hipStream_t s, const AttnLaunch& a) {
     size_t smem = ((size_t)a.head_dim + 8 + (size_t)a.max_pos) * sizeof(float);
     dim3 grid((unsigned)a.num_heads, (unsigned)a.n);
     hipLaunchKernelGGL(k_attention, grid, dim3(256), smem, s, a);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
+
+bool attention_decode_supported(int num_heads, int num_kv_heads, int head_dim, int max_pos) {
+    const long long groups = num_heads / num_kv_heads;
+    const long long lds = (groups * max_pos + 32ll * head_dim) * 4;
+    return head_dim == 128 && groups * head_dim <= 1024 && lds <= 64 * 1024;
+}
+
+lq8_status launch_attention_decode(hipStream_t s, const AttnDecodeLaunch& a) {
+    if (!attention_decode_supported(a.num_heads, a.num_kv_heads, a.head_dim, a.max_pos))
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "decode attention: unsupported head layout");
+    const int groups = a.num_heads / a.num_kv_heads;
+    hipLaunchKernelGGL(k_attn_scores, dim3((unsigned)a.num_heads, (unsigned)((a.max_pos + 63) / 64)), dim3(64), 0, s, a);
+    LQ8_HIP(hipGetLastError());
+    const int threads = ((groups * a.head_dim + 63) / 64) * 64;
+    size_t smem = ((size_t)groups * a.max_pos + 32 * (size_t)a.head_dim) * sizeof(float);
+    hipLaunchKernelGGL(k_attn_pv, dim3((unsigned)a.num_kv_heads), dim3(threads < 256 ? 256 : threads), smem, s, a);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

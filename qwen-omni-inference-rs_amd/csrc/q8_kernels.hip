@@ -399,7 +399,7 @@ inline unsigned grid1(size_t n, unsigned block) { return (unsigned)((n + block -
 
 // ---- launchers ---------------------------------------------------------------
 
-lq8_status launch_gemv(hipStream_t s, XSource xs, const GemvLaunch& a) {
+lq8_status launch_gemv_tile_wg(hipStream_t s, XSource xs, const GemvLaunch& a) {
     if (a.k <= 0 || a.k % 32 || a.n <= 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k must be a positive multiple of 32");
     if (a.k > 16384) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k > 16384 not supported");
     const int nb = a.k / 32, ngroups = (nb + GROUP_BLOCKS - 1) / GROUP_BLOCKS;

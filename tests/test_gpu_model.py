@@ -97,6 +97,21 @@ def test_graph_replays_repeatable(small_pair):
     assert a.tolist() == b.tolist()
 
 
+def test_long_context_config_uses_unfused_attention(ctx):
+    """max_positions 8192 exceeds the fused decode attention's LDS budget, so
+    decode runs the per-head kernels; results still match the oracle."""
+    cfg = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                          num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=8192)
+    model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=9)
+    ref = oracle.Model(cfg, model.export_all())
+    prompt = np.random.default_rng(9).integers(0, cfg.vocab_size, 70).astype(np.uint32)
+    toks, _ = model.generate_greedy(prompt, 10)
+    ref_toks, _ = ref.generate_greedy(prompt, 10)
+    assert toks.tolist() == ref_toks.tolist()
+    model.free()
+    ref.close()
+
+
 def test_qwen3_0_6b_greedy_128_plus_128(ctx):
     """Qwen3-0.6B random-init Q8_0, 128 uniform-random prompt ids, 128 greedy
     tokens: identical to the oracle; the prefill logits are bit-identical."""

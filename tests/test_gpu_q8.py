@@ -225,3 +225,25 @@ def test_errors_no_fallback(ctx):
         lq8._check(lq8.lib().lq8_weight_free(stale))
     with pytest.raises(lq8.InvalidArgument):
         lq8._check(lq8.lib().lq8_gemv_q8_0_device(ctx.handle, stale, None, None))
+
+
+def test_gemv_split_repeated_calls(ctx):
+    """Small-N GEMVs combine group partials across workgroups through device
+    counters; repeated calls (counters reset by the last workgroup) and
+    interleaved shapes give the oracle's bits every time."""
+    cases = []
+    for i, (n, k) in enumerate([(1024, 3072), (64, 2048), (1024, 1024), (200, 768)]):
+        blocks = oracle.quantize_q8_0(normal((n, k), 0.02, 500 + i))
+        x = normal(k, 1.0, 600 + i)
+        w = lq8.Q8Weight.from_blocks(ctx, blocks, n, k)
+        cases.append((w, lq8.DeviceBuffer.from_array(ctx, x), lq8.DeviceBuffer(ctx, 4 * n),
+                      oracle.gemv_q8_0(blocks, n, k, x)))
+    for _ in range(3):
+        for w, dx, dy, ref in cases:
+            lq8._check(lq8.lib().lq8_gemv_q8_0_device(ctx.handle, w.handle, dx.ptr, dy.ptr))
+        for w, dx, dy, ref in cases:
+            assert_parity(dy.download(np.float32, w.n_out), ref)
+    lq8.bench_gemv(ctx, [(w, dx, dy) for w, dx, dy, _ in cases], mode=2, reps=5)
+    for w, dx, dy, ref in cases:
+        assert_parity(dy.download(np.float32, w.n_out), ref)
+        dx.free(); dy.free(); w.free()
