@@ -38,9 +38,11 @@
  *          accumulates elements l, l+64, l+128, ... in order from 0; then the
  *          64 partials are folded with distances 32, 16, 8, 4, 2, 1
  *          (v[l] = v[l] + v[l+d]).
- *   dot products inside attention (q.k over head_dim, p.v over positions)
- *          are sequential, exactly as the reference's matmul_4d
+ *   q.k     sequential over head_dim, as the reference's matmul_4d
  *          (src/tensor.rs:2846-2915).
+ *   PV4    (p.v over positions): chunks of 64 positions, chunk c in set c % 4;
+ *          each set sums its positions in increasing order from 0, then
+ *          out = ((A0 + A1) + A2) + A3.
  *   exp    orc_expf: double-precision Cody-Waite reduction + degree-13 Taylor
  *          polynomial, rounded once to float.  Agrees with a correctly rounded
  *          expf except in rare last-bit cases.
@@ -478,9 +480,25 @@ static void attend(const orc_model* m, size_t layer, size_t kvh, const float* q,
     float sum = sum64(sc, L);
     for (size_t j = 0; j < L; j++) sc[j] = sc[j] / sum;
     for (size_t d = 0; d < hd; d++) {
-        float o = 0.0f;
-        for (size_t j = 0; j < L; j++) o = o + sc[j] * V[j * hd + d];
-        out[d] = o;
+        if (g_seq_sums) {
+            float o = 0.0f;
+            for (size_t j = 0; j < L; j++) o = o + sc[j] * V[j * hd + d];
+            out[d] = o;
+            continue;
+        }
+        /* PV4: positions are cut into chunks of 64; chunk c belongs to set
+         * c % 4.  Each set accumulates its positions in increasing order from
+         * 0; the four set sums are added in set order. */
+        float a[4];
+        for (int st = 0; st < 4; st++) {
+            float o = 0.0f;
+            for (size_t j = (size_t)st * 64; j < L; j += 256) {
+                size_t je = j + 64 < L ? j + 64 : L;
+                for (size_t jj = j; jj < je; jj++) o = o + sc[jj] * V[jj * hd + d];
+            }
+            a[st] = o;
+        }
+        out[d] = ((a[0] + a[1]) + a[2]) + a[3];
     }
 }
 

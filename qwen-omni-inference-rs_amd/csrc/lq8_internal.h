@@ -54,11 +54,7 @@ struct lq8_ctx {
     size_t scratch_bytes = 0;
     void* problems = nullptr;  // device copy of grouped GEMV descriptors
     size_t problems_bytes = 0;
-    float* gemv_partials = nullptr;  // split-K partials of the decode GEMV
-    int* gemv_counters = nullptr;    // per-tile arrival counters, kept at zero
 };
-constexpr long long GEMV_PARTIALS_CAP = 4ll << 20;  // floats
-constexpr int GEMV_COUNTERS_CAP = 1 << 16;
 
 struct lq8_weight {
     lq8_ctx* ctx = nullptr;
@@ -86,17 +82,24 @@ struct GemvLaunch {
     float* y;              // output [n]
     const float* resid;    // if non-null: y = resid + Wx
     int n, k;
-    // split-K combine buffers (from the context); counters are zero between launches
+    // PARTIALS output: group partials [groups][stride] instead of y
     float* partials = nullptr;
-    int* counters = nullptr;
     long long partials_cap = 0;
-    int counters_cap = 0;
+    // input as base + partials: x_i = (x ? x[i] : 0) + ((0 + xp[0][i]) + xp[1][i] + ...)
+    const float* xp = nullptr;
+    int xg = 0;
+    size_t xstride = 0;
+    float* x_out = nullptr;  // RMSNORM source: workgroup 0 stores the combined input here
 };
 lq8_status launch_gemv(hipStream_t s, XSource xs, const GemvLaunch& a);
 // One workgroup per 64-row tile (all groups in one workgroup, no counters).
 lq8_status launch_gemv_tile_wg(hipStream_t s, XSource xs, const GemvLaunch& a);
-// Point a launch at the context's split-K buffers.
-void gemv_attach(GemvLaunch& a, const lq8_ctx* ctx);
+// Row stride of a PARTIALS output and number of groups of a k-wide input.
+size_t gemv_partial_stride(int n);
+int gemv_groups(int k);
+// y = (base ? base : 0) + ((0 + P[0]) + P[1] + ...), elementwise.
+lq8_status launch_combine(hipStream_t s, const float* base, const float* partials, int groups, size_t stride, int n,
+                          float* y);
 
 // Grouped GEMV over independent problems (device-side descriptor table).
 struct GemvProblemDev {
@@ -156,25 +159,29 @@ struct AttnLaunch {
 };
 lq8_status launch_attention(hipStream_t s, const AttnLaunch& a);
 
-// Decode attention for one new position (reads the position from d_pos or
-// pos_base): q/k RmsNorm + RoPE + KV append fused into the scores kernel,
-// then softmax and p.v per kv group.
-struct AttnDecodeLaunch {
-    const float* qkv;      // [q_dim + 2*kv_dim]
+// Attention with head_dim 128 and at most 2 q-heads per kv head, one
+// workgroup per (kv head, query row).  Decode form: qkv_p holds the qkv
+// projection as qkv_g partials of stride qkv_stride; the kernel normalizes
+// and rotates q/k, appends k/v at the position and attends.  Prefill form:
+// q_rows holds normalized, rotated queries and the cache is filled.
+struct AttnGroupLaunch {
+    const float* qkv_p;
+    int qkv_g;
+    size_t qkv_stride;
+    const float* q_rows;
     const float* q_norm;
     const float* k_norm;
     const float* cos_t;
     const float* sin_t;
-    float* k_cache;        // [kv_heads][max_pos][head_dim] (this layer)
-    float* v_cache;        // [kv_heads][max_pos][head_dim]
-    float* scores;         // [num_heads][max_pos] scratch
-    float* out;            // [num_heads*head_dim]
+    float* k_cache;        // [kv_heads][max_pos][128] (this layer)
+    float* v_cache;
+    float* out;            // [n][num_heads * 128]
     const int* d_pos;
-    int pos_base, num_heads, num_kv_heads, head_dim, max_pos;
+    int pos_base, n, num_heads, num_kv_heads, max_pos;
     float eps, scale;
 };
-lq8_status launch_attention_decode(hipStream_t s, const AttnDecodeLaunch& a);
-bool attention_decode_supported(int num_heads, int num_kv_heads, int head_dim, int max_pos);
+lq8_status launch_attention_group(hipStream_t s, const AttnGroupLaunch& a);
+bool attention_group_supported(int num_heads, int num_kv_heads, int head_dim, int max_pos);
 
 lq8_status launch_rms_norm_rows(hipStream_t s, const float* x, const float* w, int rows, int dim, float eps, float* y);
 lq8_status launch_silu_mul(hipStream_t s, const float* gu, int rows, int inter, float* act);

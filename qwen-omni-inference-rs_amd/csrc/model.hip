@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <utility>
 #include <vector>
 
 #include "lq8_internal.h"
@@ -38,8 +39,9 @@ struct lq8_model {
     size_t kv_len = 0;
     // single-position buffers
     float *h = nullptr, *qkv = nullptr, *qr = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
-    float* scores = nullptr;  // [num_heads][max_pos] decode attention scores
-    bool fused_attn = false;  // decode attention through launch_attention_decode
+    float *h2 = nullptr, *tr = nullptr;  // second residual buffer; trace staging
+    float *qkv_p = nullptr, *o_p = nullptr, *gu_p = nullptr, *dn_p = nullptr;  // projection partials
+    bool grouped_attn = false;           // attention through launch_attention_group
     uint32_t* d_ids = nullptr;
     size_t ids_cap = 0;
     int *d_pos = nullptr, *d_step = nullptr;
@@ -92,7 +94,8 @@ void release(lq8_model* m) {
         F(L.in_norm); F(L.post_norm); F(L.q_norm); F(L.k_norm);
     }
     F(m->cos_t); F(m->sin_t); F(m->kc); F(m->vc);
-    F(m->h); F(m->qkv); F(m->qr); F(m->attn); F(m->gu); F(m->logits); F(m->scores);
+    F(m->h); F(m->qkv); F(m->qr); F(m->attn); F(m->gu); F(m->logits);
+    F(m->h2); F(m->tr); F(m->qkv_p); F(m->o_p); F(m->gu_p); F(m->dn_p);
     F(m->d_ids); F(m->d_pos); F(m->d_step); F(m->d_tok); F(m->d_tokens);
     F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_act); F(m->P_xs); F(m->P_xq);
     delete m;
@@ -140,10 +143,17 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_qwen3_config* c, lq8_model* m)
     LQ8_HIP(hipMemset(m->vc, 0, kv * sizeof(float)));
     if ((st = dalloc(&m->h, Hd)) || (st = dalloc(&m->qkv, m->QKV)) || (st = dalloc(&m->qr, m->QD)) ||
         (st = dalloc(&m->attn, m->QD)) || (st = dalloc(&m->gu, 2 * I)) || (st = dalloc(&m->logits, c->vocab_size)) ||
-        (st = dalloc(&m->d_pos, 1)) || (st = dalloc(&m->d_step, 1)) || (st = dalloc(&m->d_tok, 1)) ||
-        (st = dalloc(&m->scores, (size_t)c->num_heads * P)))
+        (st = dalloc(&m->d_pos, 1)) || (st = dalloc(&m->d_step, 1)) || (st = dalloc(&m->d_tok, 1)))
         return st;
-    m->fused_attn = attention_decode_supported((int)c->num_heads, (int)c->num_kv_heads, (int)hd, (int)P);
+    {
+        const int Gh = gemv_groups((int)Hd), Gq = gemv_groups((int)m->QD), Gi = gemv_groups((int)I);
+        const size_t sQKV = gemv_partial_stride((int)m->QKV), sH = gemv_partial_stride((int)Hd);
+        const size_t sGU = gemv_partial_stride((int)(2 * I));
+        if ((st = dalloc(&m->h2, Hd)) || (st = dalloc(&m->tr, Hd)) || (st = dalloc(&m->qkv_p, Gh * sQKV)) ||
+            (st = dalloc(&m->o_p, Gq * sH)) || (st = dalloc(&m->gu_p, Gh * sGU)) || (st = dalloc(&m->dn_p, Gi * sH)))
+            return st;
+    }
+    m->grouped_attn = attention_group_supported((int)c->num_heads, (int)c->num_kv_heads, (int)hd, (int)P);
     LQ8_HIP(hipEventCreate(&m->e0));
     LQ8_HIP(hipEventCreate(&m->e1));
     LQ8_HIP(hipEventCreate(&m->e2));
@@ -232,49 +242,95 @@ lq8_status trace_copy(lq8_model* m, float* host, const float* dev, size_t count)
     return LQ8_OK;
 }
 
-lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, int pos_base, float* trace = nullptr) {
+// Decode dataflow.  The projections write group partials (see gemv.hip)
+// that the next kernel folds in group order while staging its input; the
+// residual stream lives in two buffers used in turn, each combined value
+// (base + finished projection) stored once by the kernel that first needs it.
+lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, int pos_base, float* trace = nullptr,
+                          float* final_hidden = nullptr) {
     hipStream_t s = m->ctx->stream;
     const lq8_qwen3_config& c = m->c;
     const int Hd = (int)c.hidden_size, I = (int)c.intermediate_size;
     const size_t layer_kv = (size_t)c.num_kv_heads * c.head_dim * c.max_positions;
+    const int Gh = gemv_groups(Hd), Gq = gemv_groups((int)m->QD), Gi = gemv_groups(I);
+    const size_t sQKV = gemv_partial_stride((int)m->QKV), sH = gemv_partial_stride(Hd), sGU = gemv_partial_stride(2 * I);
+    const float scale = 1.0f / std::sqrt((float)c.head_dim);
+    float* cur = m->h;
+    float* other = m->h2;
+    const float* pend = nullptr;  // down-projection partials not yet added to cur
+    int pend_g = 0;
     lq8_status st;
-    if ((st = launch_dequant_rows(s, m->embed, d_id, 0, 1, m->h))) return st;
-    if ((st = trace_copy(m, trace, m->h, Hd))) return st;
+    if ((st = launch_dequant_rows(s, m->embed, d_id, 0, 1, cur))) return st;
+    if ((st = trace_copy(m, trace, cur, Hd))) return st;
     for (size_t l = 0; l < m->layers.size(); l++) {
         Layer& L = m->layers[l];
-        GemvLaunch g1{L.qkv->codes, L.qkv->scales, m->h, L.in_norm, c.rms_norm_eps, m->qkv, nullptr, (int)m->QKV, Hd};
-        gemv_attach(g1, m->ctx);
+        // input_layernorm(h) -> q|k|v partials; h = cur + pending down projection
+        GemvLaunch g1{L.qkv->codes, L.qkv->scales, cur, L.in_norm, c.rms_norm_eps, nullptr, nullptr, (int)m->QKV, Hd};
+        g1.partials = m->qkv_p;
+        g1.partials_cap = (long long)(Gh * sQKV);
+        g1.xp = pend;
+        g1.xg = pend_g;
+        g1.xstride = sH;
+        g1.x_out = pend ? other : nullptr;
         if ((st = launch_gemv(s, XS_RMSNORM, g1))) return st;
-        if (m->fused_attn) {
-            AttnDecodeLaunch ad{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->kc + l * layer_kv,
-                                m->vc + l * layer_kv, m->scores, m->attn, d_pos, pos_base, (int)c.num_heads,
-                                (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps,
-                                1.0f / std::sqrt((float)c.head_dim)};
-            if ((st = launch_attention_decode(s, ad))) return st;
+        if (pend) {
+            std::swap(cur, other);
+            pend = nullptr;
+            pend_g = 0;
+        }
+        // attention (q/k norm, RoPE, KV append, scores, softmax, p.v)
+        if (m->grouped_attn) {
+            AttnGroupLaunch at{m->qkv_p, Gh, sQKV, nullptr, L.q_norm, L.k_norm, m->cos_t, m->sin_t,
+                               m->kc + l * layer_kv, m->vc + l * layer_kv, m->attn, d_pos, pos_base, 1,
+                               (int)c.num_heads, (int)c.num_kv_heads, (int)c.max_positions, c.rms_norm_eps, scale};
+            if ((st = launch_attention_group(s, at))) return st;
         } else {
+            if ((st = launch_combine(s, nullptr, m->qkv_p, Gh, sQKV, (int)m->QKV, m->qkv))) return st;
             QkRopeLaunch qr{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->qr, m->kc + l * layer_kv,
                             m->vc + l * layer_kv, d_pos, pos_base, 1, (int)c.num_heads, (int)c.num_kv_heads,
                             (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps};
             if ((st = launch_qk_rope_kv(s, qr))) return st;
             AttnLaunch at{m->qr, m->kc + l * layer_kv, m->vc + l * layer_kv, m->attn, d_pos, pos_base, 1,
-                          (int)c.num_heads, (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions,
-                          1.0f / std::sqrt((float)c.head_dim)};
+                          (int)c.num_heads, (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions, scale};
             if ((st = launch_attention(s, at))) return st;
         }
-        GemvLaunch g2{L.o->codes, L.o->scales, m->attn, nullptr, 0.0f, m->h, m->h, Hd, (int)m->QD};
-        gemv_attach(g2, m->ctx);
+        // o_proj -> partials
+        GemvLaunch g2{L.o->codes, L.o->scales, m->attn, nullptr, 0.0f, nullptr, nullptr, Hd, (int)m->QD};
+        g2.partials = m->o_p;
+        g2.partials_cap = (long long)(Gq * sH);
         if ((st = launch_gemv(s, XS_PLAIN, g2))) return st;
-        GemvLaunch g3{L.gu->codes, L.gu->scales, m->h, L.post_norm, c.rms_norm_eps, m->gu, nullptr, 2 * I, Hd};
-        gemv_attach(g3, m->ctx);
+        // post_attention_layernorm(h + o) -> gate|up partials; h + o stored to other
+        GemvLaunch g3{L.gu->codes, L.gu->scales, cur, L.post_norm, c.rms_norm_eps, nullptr, nullptr, 2 * I, Hd};
+        g3.partials = m->gu_p;
+        g3.partials_cap = (long long)(Gh * sGU);
+        g3.xp = m->o_p;
+        g3.xg = Gq;
+        g3.xstride = sH;
+        g3.x_out = other;
         if ((st = launch_gemv(s, XS_RMSNORM, g3))) return st;
-        GemvLaunch g4{L.down->codes, L.down->scales, m->gu, nullptr, 0.0f, m->h, m->h, Hd, I};
-        gemv_attach(g4, m->ctx);
+        std::swap(cur, other);
+        // down_proj(silu(gate) * up) -> partials, added by the next consumer
+        GemvLaunch g4{L.down->codes, L.down->scales, nullptr, nullptr, 0.0f, nullptr, nullptr, Hd, I};
+        g4.partials = m->dn_p;
+        g4.partials_cap = (long long)(Gi * sH);
+        g4.xp = m->gu_p;
+        g4.xg = Gh;
+        g4.xstride = sGU;
         if ((st = launch_gemv(s, XS_SILU, g4))) return st;
-        if (trace && (st = trace_copy(m, trace + (l + 1) * Hd, m->h, Hd))) return st;
+        pend = m->dn_p;
+        pend_g = Gi;
+        if (trace) {
+            if ((st = launch_combine(s, cur, pend, pend_g, sH, Hd, m->tr))) return st;
+            if ((st = trace_copy(m, trace + (l + 1) * Hd, m->tr, Hd))) return st;
+        }
     }
-    GemvLaunch g5{m->embed->codes, m->embed->scales, m->h, m->final_norm, c.rms_norm_eps, m->logits, nullptr,
+    if (final_hidden && (st = launch_combine(s, cur, pend, pend_g, sH, Hd, final_hidden))) return st;
+    // norm(h) -> lm_head logits
+    GemvLaunch g5{m->embed->codes, m->embed->scales, cur, m->final_norm, c.rms_norm_eps, m->logits, nullptr,
                   (int)c.vocab_size, Hd};
-    gemv_attach(g5, m->ctx);
+    g5.xp = pend;
+    g5.xg = pend_g;
+    g5.xstride = sH;
     return launch_gemv(s, XS_RMSNORM, g5);
 }
 
@@ -303,10 +359,18 @@ lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base, float* trace = nul
                         m->vc + l * layer_kv, nullptr, pos_base, n, (int)c.num_heads, (int)c.num_kv_heads,
                         (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps};
         if ((st = launch_qk_rope_kv(s, qr))) return st;
-        AttnLaunch at{m->P_qr, m->kc + l * layer_kv, m->vc + l * layer_kv, m->P_attn, nullptr, pos_base, n,
-                      (int)c.num_heads, (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions,
-                      1.0f / std::sqrt((float)c.head_dim)};
-        if ((st = launch_attention(s, at))) return st;
+        if (m->grouped_attn) {
+            AttnGroupLaunch at{nullptr, 0, 0, m->P_qr, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->kc + l * layer_kv,
+                               m->vc + l * layer_kv, m->P_attn, nullptr, pos_base, n, (int)c.num_heads,
+                               (int)c.num_kv_heads, (int)c.max_positions, c.rms_norm_eps,
+                               1.0f / std::sqrt((float)c.head_dim)};
+            if ((st = launch_attention_group(s, at))) return st;
+        } else {
+            AttnLaunch at{m->P_qr, m->kc + l * layer_kv, m->vc + l * layer_kv, m->P_attn, nullptr, pos_base, n,
+                          (int)c.num_heads, (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions,
+                          1.0f / std::sqrt((float)c.head_dim)};
+            if ((st = launch_attention(s, at))) return st;
+        }
         if ((st = quant_gemm(m, m->P_attn, n, L.o, m->P_h, m->P_h))) return st;
         if ((st = launch_rms_norm_rows(s, m->P_h, L.post_norm, n, Hd, c.rms_norm_eps, m->P_x))) return st;
         if ((st = quant_gemm(m, m->P_x, n, L.gu, m->P_gu, nullptr))) return st;
@@ -317,7 +381,6 @@ lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base, float* trace = nul
     // final norm + lm_head on the last position only (src/model.rs:357-371)
     GemvLaunch g{m->embed->codes, m->embed->scales, m->P_h + (size_t)(n - 1) * Hd, m->final_norm, c.rms_norm_eps,
                  m->logits, nullptr, (int)c.vocab_size, Hd};
-    gemv_attach(g, m->ctx);
     return launch_gemv(s, XS_RMSNORM, g);
 }
 
@@ -509,8 +572,8 @@ lq8_status lq8_model_forward_with_intermediates(lq8_model* m, const uint32_t* id
     LQ8_HIP(hipMemcpyAsync(m->d_ids, ids, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     const float* last;
     if (n == 1) {
-        st = enqueue_decode(m, m->d_ids, nullptr, (int)offset, hidden);
-        last = m->h;
+        st = enqueue_decode(m, m->d_ids, nullptr, (int)offset, hidden, m->tr);
+        last = m->tr;
     } else {
         st = enqueue_prefill(m, (int)n, (int)offset, hidden);
         last = m->P_h;

@@ -118,119 +118,123 @@ __global__ __launch_bounds__(256) void k_attention(AttnLaunch a) {
     __syncthreads();
     const float* V = a.v_cache + (size_t)kvh * P * hd;
     for (int d = tid; d < hd; d += 256) {
-        float o = 0.0f;
-        for (int j = 0; j < L; j++) o = o + sc[j] * V[(size_t)j * hd + d];
-        a.out[(size_t)i * QD + h * hd + d] = o;
+        // PV4 order: chunk c of 64 positions belongs to set c % 4; sets sum
+        // their positions in order, then ((A0 + A1) + A2) + A3.
+        float s4[4];
+        for (int st = 0; st < 4; st++) {
+            float o = 0.0f;
+            for (int j0 = st * 64; j0 < L; j0 += 256) {
+                const int je = min(j0 + 64, L);
+                for (int j = j0; j < je; j++) o = o + sc[j] * V[(size_t)j * hd + d];
+            }
+            s4[st] = o;
+        }
+        a.out[(size_t)i * QD + h * hd + d] = ((s4[0] + s4[1]) + s4[2]) + s4[3];
     }
 }
 
 
-// ---- decode attention (one new position) ------------------------------------
+// ---- attention, one workgroup per (kv group, query) -------------------------
 
-// The q-head's query and, when this chunk holds the new position, the new
-// key: RmsNorm per head then RoPE, computed by one wave (lane l holds
-// elements l, l+64, ...).  Same arithmetic as k_qk_rope_kv.
-__device__ __forceinline__ void norm_rope_head(const float* src, const float* w, const float* cs, const float* sn,
-                                               int hd, float eps, float* dst) {
-    const int lane = threadIdx.x & 63, R = hd / 2, per = hd / 64;
-    float xb[8], y[8];
+// RmsNorm per head then RoPE of one head vector held by one wave (lane l has
+// elements l and l + 64), exactly as k_qk_rope_kv; src holds the projection
+// as (base +) partials.
+__device__ __forceinline__ void head_norm_rope(const float* src_p, int g_count, size_t stride, const float* w,
+                                               const float* cs, const float* sn, float eps, float* dst) {
+    const int lane = threadIdx.x & 63;
+    float xb[2];
     float acc = 0.0f;
-    for (int t = 0; t < per; t++) {
-        float v = bf16_round(src[lane + 64 * t]);
+    for (int t = 0; t < 2; t++) {
+        float s = 0.0f;
+        for (int g = 0; g < g_count; g++) s = s + src_p[(size_t)g * stride + lane + 64 * t];
+        float v = bf16_round(s);
         xb[t] = v;
         acc = acc + v * v;
     }
     acc = wave_sum64(acc);
-    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)hd) + eps));
-    for (int t = 0; t < per; t++) y[t] = bf16_round((xb[t] * inv) * bf16_round(w[lane + 64 * t]));
-    for (int t = 0; t < per / 2; t++) {
-        const int d = lane + 64 * t;
-        const float c = cs[d & ~1], s = sn[d & ~1];
-        const float x1 = y[t], x2 = y[t + per / 2];
-        dst[d] = x1 * c - x2 * s;
-        dst[d + R] = x2 * c + x1 * s;
-    }
+    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, 128.0f) + eps));
+    const float y0 = bf16_round((xb[0] * inv) * bf16_round(w[lane]));
+    const float y1 = bf16_round((xb[1] * inv) * bf16_round(w[lane + 64]));
+    const float c = cs[lane & ~1], s = sn[lane & ~1];
+    dst[lane] = y0 * c - y1 * s;
+    dst[lane + 64] = y1 * c + y0 * s;
 }
 
-// grid (num_heads, max_pos / 64), block 64: scores of 64 positions of one
-// q-head, s_j = (q . k_j sequential over head_dim) * scale.  The workgroup
-// holding the new position also appends its key and value to the cache
-// (the first q-head of each kv group writes; the others recompute the key).
-__global__ __launch_bounds__(64) void k_attn_scores(AttnDecodeLaunch a) {
-    __shared__ float qs[512];
-    __shared__ float ks[512];
-    const int h = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
-    const int hd = a.head_dim, P = a.max_pos, groups = a.num_heads / a.num_kv_heads;
-    const int kvh = h / groups;
-    const int pos = a.d_pos ? *a.d_pos : a.pos_base;
+// grid (num_kv_heads, n), block G * 512 (G = q-heads per kv head, head_dim 128).
+// Decode (qkv_p set): the query heads and the new key come from the qkv
+// projection partials; the new key and value are appended to the cache and
+// used from LDS.  Prefill (q_rows set): normalized, rotated queries and a
+// filled cache.  Then scores (q.k sequential over d, times scale), softmax
+// (max, exp, SUM64, divide) and p.v in the PV4 order: thread group st of four
+// accumulates the positions of chunks st, st + 4, ... in order, and the four
+// partial sums are added in order.
+__global__ __launch_bounds__(1024) void k_attn_group(AttnGroupLaunch a) {
+    extern __shared__ float sm[];
+    const int kvh = blockIdx.x, i = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.num_heads / a.num_kv_heads, T = G * 512, P = a.max_pos;
+    const int QD = a.num_heads * 128, KD = a.num_kv_heads * 128;
+    const int pos = (a.d_pos ? *a.d_pos : a.pos_base) + i;
     const int L = pos + 1;
-    const int p = c * 64 + lane;
-    if (c * 64 >= L) return;
-    const int QD = a.num_heads * hd, KD = a.num_kv_heads * hd;
-    const float* kc = a.k_cache + (size_t)kvh * P * hd;
-    // key row of this lane's position (cached positions only), loaded first
-    float4 kr[32];
-    const bool cached = p < pos;
-    if (cached) {
-        const float4* src = (const float4*)(kc + (size_t)p * hd);
-        for (int t = 0; t < hd / 4; t++) kr[t] = src[t];
-    }
-    const float* cs = a.cos_t + (size_t)pos * (hd / 2);
-    const float* sn = a.sin_t + (size_t)pos * (hd / 2);
-    norm_rope_head(a.qkv + h * hd, a.q_norm, cs, sn, hd, a.eps, qs);
-    const bool has_new = pos >= c * 64 && pos < c * 64 + 64;
-    if (has_new) {
-        norm_rope_head(a.qkv + QD + kvh * hd, a.k_norm, cs, sn, hd, a.eps, ks);
-        __syncthreads();
-        if (h % groups == 0) {
-            float* krow = a.k_cache + ((size_t)kvh * P + pos) * hd;
-            float* vrow = a.v_cache + ((size_t)kvh * P + pos) * hd;
-            const float* v = a.qkv + QD + KD + kvh * hd;
-            for (int d = lane; d < hd; d += 64) {
-                krow[d] = ks[d];
-                vrow[d] = v[d];
+    float* qs = sm;                  // [G][128]
+    float* kn = qs + G * 128;        // [128] new key
+    float* vn = kn + 128;            // [128] new value
+    float* pr = vn + 128;            // [G][P] scores, then probabilities
+    float* part = pr + G * P;        // [4][G * 128]
+    const bool fused = a.qkv_p != nullptr;
+    if (fused) {
+        const float* cs = a.cos_t + (size_t)pos * 64;
+        const float* sn = a.sin_t + (size_t)pos * 64;
+        if (wave < G) {
+            head_norm_rope(a.qkv_p + (kvh * G + wave) * 128, a.qkv_g, a.qkv_stride, a.q_norm, cs, sn, a.eps,
+                           qs + wave * 128);
+        } else if (wave == G) {
+            head_norm_rope(a.qkv_p + QD + kvh * 128, a.qkv_g, a.qkv_stride, a.k_norm, cs, sn, a.eps, kn);
+            float* krow = a.k_cache + ((size_t)kvh * P + pos) * 128;
+            krow[lane] = kn[lane];
+            krow[lane + 64] = kn[lane + 64];
+        } else if (wave == G + 1) {
+            float* vrow = a.v_cache + ((size_t)kvh * P + pos) * 128;
+            for (int t = 0; t < 2; t++) {
+                float s = 0.0f;
+                for (int g = 0; g < a.qkv_g; g++) s = s + a.qkv_p[(size_t)g * a.qkv_stride + QD + KD + kvh * 128 + lane + 64 * t];
+                vn[lane + 64 * t] = s;
+                vrow[lane + 64 * t] = s;
             }
         }
+    } else {
+        for (int e = tid; e < G * 128; e += T) qs[e] = a.q_rows[(size_t)i * QD + kvh * G * 128 + e];
     }
     __syncthreads();
-    if (p >= L) return;
-    float s = 0.0f;
-    if (cached) {
-        for (int t = 0; t < hd / 4; t++) {
-            s = s + qs[4 * t] * kr[t].x;
-            s = s + qs[4 * t + 1] * kr[t].y;
-            s = s + qs[4 * t + 2] * kr[t].z;
-            s = s + qs[4 * t + 3] * kr[t].w;
+    // scores
+    const float* K = a.k_cache + (size_t)kvh * P * 128;
+    for (int j = tid; j < L; j += T) {
+        float s[8];
+        for (int h = 0; h < G; h++) s[h] = 0.0f;
+        if (fused && j == pos) {
+            for (int d = 0; d < 128; d++)
+                for (int h = 0; h < G; h++) s[h] = s[h] + qs[h * 128 + d] * kn[d];
+        } else {
+            const float4* kr = (const float4*)(K + (size_t)j * 128);
+            for (int t = 0; t < 32; t++) {
+                const float4 k4 = kr[t];
+                for (int h = 0; h < G; h++) {
+                    const float* q = qs + h * 128 + 4 * t;
+                    s[h] = s[h] + q[0] * k4.x;
+                    s[h] = s[h] + q[1] * k4.y;
+                    s[h] = s[h] + q[2] * k4.z;
+                    s[h] = s[h] + q[3] * k4.w;
+                }
+            }
         }
-    } else {
-        for (int d = 0; d < hd; d++) s = s + qs[d] * ks[d];
+        for (int h = 0; h < G; h++) pr[h * P + j] = s[h] * a.scale;
     }
-    a.scores[(size_t)h * P + p] = s * a.scale;
-}
-
-// grid (num_kv_heads), block 64 * groups * head_dim / 64: softmax of each
-// q-head of the kv group (max, exp(s - max), SUM64, divide), then
-// out[h][d] = sum_j p_j v_j[d] sequentially over j, V staged through LDS in
-// chunks of 32 positions.
-__global__ __launch_bounds__(1024) void k_attn_pv(AttnDecodeLaunch a) {
-    extern __shared__ float sm[];
-    const int kvh = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int hd = a.head_dim, P = a.max_pos, groups = a.num_heads / a.num_kv_heads;
-    const int L = (a.d_pos ? *a.d_pos : a.pos_base) + 1;
-    const int nt = blockDim.x;
-    float* pr = sm;                  // [groups][P] probabilities
-    float* vt = pr + groups * P;     // [32][hd] staged values
-    // softmax rows: wave w < groups handles q-head kvh*groups + w
-    if (wave < groups) {
-        const int h = kvh * groups + wave;
-        const float* sc = a.scores + (size_t)h * P;
+    __syncthreads();
+    // softmax per q-head, one wave each
+    if (wave < G) {
         float* p = pr + wave * P;
         float mx = -__builtin_huge_valf();
-        for (int j = lane; j < L; j += 64) {
-            float v = sc[j];
-            p[j] = v;
-            mx = v > mx ? v : mx;
-        }
+        for (int j = lane; j < L; j += 64) mx = p[j] > mx ? p[j] : mx;
 #pragma unroll
         for (int d = 32; d >= 1; d >>= 1) {
             float o = __shfl_xor(mx, d, 64);
@@ -246,19 +250,26 @@ __global__ __launch_bounds__(1024) void k_attn_pv(AttnDecodeLaunch a) {
         for (int j = lane; j < L; j += 64) p[j] = __fdiv_rn(p[j], acc);
     }
     __syncthreads();
-    const int hq = tid / hd, d = tid % hd;          // output element of this thread
-    const float* V = a.v_cache + (size_t)kvh * P * hd;
-    const float* p = pr + hq * P;
-    float o = 0.0f;
-    for (int j0 = 0; j0 < L; j0 += 32) {
-        const int nj = min(32, L - j0);
-        for (int i = tid * 4; i < nj * hd; i += nt * 4) *(float4*)(vt + i) = *(const float4*)(V + (size_t)j0 * hd + i);
-        __syncthreads();
-        if (hq < groups)
-            for (int j = 0; j < nj; j++) o = o + p[j0 + j] * vt[j * hd + d];
-        __syncthreads();
+    // p.v, PV4 order
+    {
+        const int st = tid / (G * 128), r = tid % (G * 128), hq = r / 128, d = r % 128;
+        const float* V = a.v_cache + (size_t)kvh * P * 128;
+        const float* p = pr + hq * P;
+        float o = 0.0f;
+        for (int j0 = st * 64; j0 < L; j0 += 256) {
+            const int je = min(j0 + 64, L);
+            for (int j = j0; j < je; j++) {
+                const float v = (fused && j == pos) ? vn[d] : V[(size_t)j * 128 + d];
+                o = o + p[j] * v;
+            }
+        }
+        part[st * G * 128 + r] = o;
     }
-    if (hq < groups) a.out[(size_t)(kvh * groups + hq) * hd + d] = o;
+    __syncthreads();
+    for (int r = tid; r < G * 128; r += T) {
+        const float o = ((part[r] + part[G * 128 + r]) + part[2 * G * 128 + r]) + part[3 * G * 128 + r];
+        a.out[(size_t)i * QD + kvh * G * 128 + r] = o;
+    }
 }
 
 // RmsNorm of each row (src/rms_norm.rs:143-176), one wave per row.
@@ -349,21 +360,19 @@ lq8_status launch_attention(hipStream_t s, const AttnLaunch& a) {
 }
 
 
-bool attention_decode_supported(int num_heads, int num_kv_heads, int head_dim, int max_pos) {
-    const long long groups = num_heads / num_kv_heads;
-    const long long lds = (groups * max_pos + 32ll * head_dim) * 4;
-    return head_dim == 128 && groups * head_dim <= 1024 && lds <= 64 * 1024;
+bool attention_group_supported(int num_heads, int num_kv_heads, int head_dim, int max_pos) {
+    if (head_dim != 128 || num_heads % num_kv_heads) return false;
+    const long long G = num_heads / num_kv_heads;
+    const long long lds = (G * 128 + 256 + G * max_pos + 4 * G * 128) * 4;
+    return G >= 1 && G <= 2 && lds <= 64 * 1024;
 }
 
-lq8_status launch_attention_decode(hipStream_t s, const AttnDecodeLaunch& a) {
-    if (!attention_decode_supported(a.num_heads, a.num_kv_heads, a.head_dim, a.max_pos))
-        return fail(LQ8_ERR_SHAPE_MISMATCH, "decode attention: unsupported head layout");
-    const int groups = a.num_heads / a.num_kv_heads;
-    hipLaunchKernelGGL(k_attn_scores, dim3((unsigned)a.num_heads, (unsigned)((a.max_pos + 63) / 64)), dim3(64), 0, s, a);
-    LQ8_HIP(hipGetLastError());
-    const int threads = ((groups * a.head_dim + 63) / 64) * 64;
-    size_t smem = ((size_t)groups * a.max_pos + 32 * (size_t)a.head_dim) * sizeof(float);
-    hipLaunchKernelGGL(k_attn_pv, dim3((unsigned)a.num_kv_heads), dim3(threads < 256 ? 256 : threads), smem, s, a);
+lq8_status launch_attention_group(hipStream_t s, const AttnGroupLaunch& a) {
+    if (!attention_group_supported(a.num_heads, a.num_kv_heads, 128, a.max_pos))
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "grouped attention: unsupported head layout");
+    const int G = a.num_heads / a.num_kv_heads;
+    size_t smem = ((size_t)G * 128 + 256 + (size_t)G * a.max_pos + 4 * (size_t)G * 128) * sizeof(float);
+    hipLaunchKernelGGL(k_attn_group, dim3((unsigned)a.num_kv_heads, (unsigned)a.n), dim3(G * 512), smem, s, a);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

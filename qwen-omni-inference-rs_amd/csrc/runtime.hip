@@ -47,13 +47,6 @@ bool registry_has(const void* p) {
     return p && registry().count(p) != 0;
 }
 
-void gemv_attach(GemvLaunch& a, const lq8_ctx* ctx) {
-    a.partials = ctx->gemv_partials;
-    a.counters = ctx->gemv_counters;
-    a.partials_cap = ctx->gemv_partials ? GEMV_PARTIALS_CAP : 0;
-    a.counters_cap = ctx->gemv_counters ? GEMV_COUNTERS_CAP : 0;
-}
-
 lq8_status ctx_scratch(lq8_ctx* ctx, size_t bytes, void** out) {
     if (bytes > ctx->scratch_bytes) {
         LQ8_HIP(hipStreamSynchronize(ctx->stream));
@@ -220,12 +213,7 @@ lq8_status lq8_init(int device, lq8_ctx** out) {
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&ctx->t0);
     if (e == hipSuccess) e = hipEventCreate(&ctx->t1);
-    if (e == hipSuccess) e = hipMalloc(&ctx->gemv_partials, GEMV_PARTIALS_CAP * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc(&ctx->gemv_counters, GEMV_COUNTERS_CAP * sizeof(int));
-    if (e == hipSuccess) e = hipMemset(ctx->gemv_counters, 0, GEMV_COUNTERS_CAP * sizeof(int));
     if (e != hipSuccess) {
-        if (ctx->gemv_partials) (void)hipFree(ctx->gemv_partials);
-        if (ctx->gemv_counters) (void)hipFree(ctx->gemv_counters);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return hip_fail(e, "context creation");
@@ -242,8 +230,6 @@ lq8_status lq8_shutdown(lq8_ctx* ctx) {
     registry_remove(ctx);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->problems) (void)hipFree(ctx->problems);
-    if (ctx->gemv_partials) (void)hipFree(ctx->gemv_partials);
-    if (ctx->gemv_counters) (void)hipFree(ctx->gemv_counters);
     (void)hipEventDestroy(ctx->t0);
     (void)hipEventDestroy(ctx->t1);
     (void)hipStreamDestroy(ctx->stream);
@@ -446,7 +432,6 @@ lq8_status lq8_gemv_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* 
     if (!d_x || !d_y) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
     if (((uintptr_t)d_x & 15) != 0) return fail(LQ8_ERR_INVALID_ARG, "x must be 16-byte aligned");
     GemvLaunch a{w->codes, w->scales, d_x, nullptr, 0.0f, d_y, nullptr, (int)w->n_out, (int)w->k_in};
-    gemv_attach(a, ctx);
     return launch_gemv(ctx->stream, XS_PLAIN, a);
 }
 
@@ -539,7 +524,6 @@ lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t
         if (!registry_has(p.w)) return fail(LQ8_ERR_INVALID_ARG, "invalid weight handle in problem list");
         if (!p.x || !p.y || ((uintptr_t)p.x & 15)) return fail(LQ8_ERR_INVALID_ARG, "bad x / y pointer");
         L[i] = GemvLaunch{p.w->codes, p.w->scales, p.x, nullptr, 0.0f, p.y, nullptr, (int)p.w->n_out, (int)p.w->k_in};
-        gemv_attach(L[i], ctx);
     }
     hipStream_t s = ctx->stream;
     lq8_status st = LQ8_OK;
