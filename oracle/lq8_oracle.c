@@ -28,9 +28,11 @@
  * Canonical orders (the HIP kernels follow exactly these, so results match
  * bit for bit; the reference's own sums are plain sequential loops, available
  * here through orc_set_sequential_sums(1) for comparison):
- *   GEMV   per row: p_b = fmaf-chain over the 32 codes of block b (j = 0..31,
- *          from 0); blocks are grouped by 8; a_g = fmaf(p_b, d_b, a_g) in block
- *          order from 0; y = y + a_g in group order from 0.
+ *   GEMV   per row: for block b, h0_b = fmaf chain over codes j = 0..15 and
+ *          h1_b = fmaf chain over codes j = 16..31 (each from +0, in j order),
+ *          v_b = (h0_b + h1_b) * d_b; then a pairwise tree over the blocks:
+ *          for s = 1, 2, 4, ...: v[i] = v[i] + v[i + s] for i = 0, 2s, 4s, ...
+ *          while i + s < nb; y = v[0].
  *   GEMM   per (m, n): I_b = exact int32 sum of the 32 code products;
  *          s_b = f32(dw_b) * f32(dx_b) (exact); a_g = fmaf((float)I_b, s_b, a_g)
  *          within a group of 8 blocks; y = y + a_g in group order.
@@ -40,9 +42,8 @@
  *          (v[l] = v[l] + v[l+d]).
  *   q.k     sequential over head_dim, as the reference's matmul_4d
  *          (src/tensor.rs:2846-2915).
- *   PV4    (p.v over positions): chunks of 64 positions, chunk c in set c % 4;
- *          each set sums its positions in increasing order from 0, then
- *          out = ((A0 + A1) + A2) + A3.
+ *   ATTN   softmax and p.v over segments of 64 positions with a running
+ *          max / denominator (see attend()).
  *   exp    orc_expf: double-precision Cody-Waite reduction + degree-13 Taylor
  *          polynomial, rounded once to float.  Agrees with a correctly rounded
  *          expf except in rare last-bit cases.
@@ -237,7 +238,10 @@ int orc_dequantize_q8_0(const uint8_t* blocks, size_t n, float* y) {
 /* Q8_0 GEMV (W8A32) and GEMM (W8A8)                                        */
 /* ------------------------------------------------------------------------ */
 
-static float gemv_row(const uint8_t* row, size_t nb, const float* x) {
+#define ORC_MAX_NB 2048 /* k_in <= 65536 */
+
+/* GEMV canonical order (header comment); v is scratch of nb floats. */
+static float gemv_row(const uint8_t* row, size_t nb, const float* x, float* v) {
     if (g_seq_sums) {
         /* matmul_2d (src/tensor.rs:2740-2750) over the dequantized row */
         float s = 0.0f;
@@ -249,29 +253,30 @@ static float gemv_row(const uint8_t* row, size_t nb, const float* x) {
         }
         return s;
     }
-    float y = 0.0f;
-    for (size_t g = 0; g < nb; g += ORC_GROUP_BLOCKS) {
-        float a = 0.0f;
-        size_t ge = g + ORC_GROUP_BLOCKS < nb ? g + ORC_GROUP_BLOCKS : nb;
-        for (size_t b = g; b < ge; b++) {
-            const uint8_t* blk = row + b * ORC_BLOCK_BYTES;
-            const int8_t* q = (const int8_t*)(blk + 2);
-            const float* xb = x + b * ORC_QK;
-            float p = 0.0f;
-            for (int j = 0; j < ORC_QK; j++) p = fmaf((float)q[j], xb[j], p);
-            a = fmaf(p, blk_scale(blk), a);
-        }
-        y = y + a;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = row + b * ORC_BLOCK_BYTES;
+        const int8_t* q = (const int8_t*)(blk + 2);
+        const float* xb = x + b * ORC_QK;
+        float h0 = 0.0f, h1 = 0.0f;
+        for (int j = 0; j < 16; j++) h0 = fmaf((float)q[j], xb[j], h0);
+        for (int j = 16; j < 32; j++) h1 = fmaf((float)q[j], xb[j], h1);
+        v[b] = (h0 + h1) * blk_scale(blk);
     }
-    return y;
+    for (size_t s = 1; s < nb; s *= 2)
+        for (size_t i = 0; i + s < nb; i += 2 * s) v[i] = v[i] + v[i + s];
+    return v[0];
 }
 
 int orc_gemv_q8_0(const uint8_t* w, size_t n_out, size_t k_in, const float* x, float* y) {
-    if (k_in == 0 || k_in % ORC_QK || n_out == 0) return 1;
+    if (k_in == 0 || k_in % ORC_QK || n_out == 0 || k_in / ORC_QK > ORC_MAX_NB) return 1;
     size_t nb = k_in / ORC_QK;
     long long nn = (long long)n_out;
-#pragma omp parallel for schedule(static)
-    for (long long n = 0; n < nn; n++) y[n] = gemv_row(w + (size_t)n * nb * ORC_BLOCK_BYTES, nb, x);
+#pragma omp parallel
+    {
+        float v[ORC_MAX_NB];
+#pragma omp for schedule(static)
+        for (long long n = 0; n < nn; n++) y[n] = gemv_row(w + (size_t)n * nb * ORC_BLOCK_BYTES, nb, x, v);
+    }
     return 0;
 }
 
@@ -460,46 +465,69 @@ void orc_model_free(orc_model* m) {
 void orc_model_clear_kv_cache(orc_model* m) { m->kv_len = 0; }
 
 /* One q-head attention row: q [hd], visible positions 0..L-1 of kv head kvh.
- * src/attention.rs:374-394: scores = q.k (sequential over d), * 1/sqrt(hd),
- * softmax (max, exp(x-max), sum, divide), then p.v sequential over positions. */
+ * src/attention.rs:374-394 computes scores = q.k (sequential over d), times
+ * 1/sqrt(hd), softmax (max, exp(x - max), sum, divide), then p.v.  Here the
+ * positions are taken in segments of 64 (flash-decoding order, the same
+ * arithmetic on every device):
+ *   per segment c: s_j = (q.k_j sequential over d) * scale; m_c = max s_j;
+ *     e_j = exp(s_j - m_c); l_c = SUM64(e); o_c[d] = sum_j e_j * v_j[d] (j in order);
+ *   running (m, num[d], den) from (-inf, 0, 0): m' = max(m, m_c);
+ *     a = exp(m - m'), b = exp(m_c - m'); num = num * a + b * o_c;
+ *     den = den * a + b * l_c; m = m'.
+ *   out[d] = num[d] / den.
+ * With the plain sequential sums switch on, the reference's order is used. */
+#define ORC_ATT_SEG 64
 static void attend(const orc_model* m, size_t layer, size_t kvh, const float* q, size_t L, float* out, float* sc) {
     const orc_qwen3_config* c = &m->c;
     size_t hd = c->head_dim, P = c->max_positions;
     const float* K = m->kc + ((layer * c->num_kv_heads + kvh) * P) * hd;
     const float* V = m->vc + ((layer * c->num_kv_heads + kvh) * P) * hd;
     float scale = 1.0f / sqrtf((float)hd);
-    float mx = -INFINITY;
-    for (size_t j = 0; j < L; j++) {
-        float s = 0.0f;
-        for (size_t d = 0; d < hd; d++) s = s + q[d] * K[j * hd + d];
-        s = s * scale;
-        sc[j] = s;
-        if (s > mx) mx = s;
-    }
-    for (size_t j = 0; j < L; j++) sc[j] = orc_expf(sc[j] - mx);
-    float sum = sum64(sc, L);
-    for (size_t j = 0; j < L; j++) sc[j] = sc[j] / sum;
-    for (size_t d = 0; d < hd; d++) {
-        if (g_seq_sums) {
+    if (g_seq_sums) {
+        float mx = -INFINITY;
+        for (size_t j = 0; j < L; j++) {
+            float s = 0.0f;
+            for (size_t d = 0; d < hd; d++) s = s + q[d] * K[j * hd + d];
+            s = s * scale;
+            sc[j] = s;
+            if (s > mx) mx = s;
+        }
+        float sum = 0.0f;
+        for (size_t j = 0; j < L; j++) { sc[j] = orc_expf(sc[j] - mx); sum = sum + sc[j]; }
+        for (size_t j = 0; j < L; j++) sc[j] = sc[j] / sum;
+        for (size_t d = 0; d < hd; d++) {
             float o = 0.0f;
             for (size_t j = 0; j < L; j++) o = o + sc[j] * V[j * hd + d];
             out[d] = o;
-            continue;
         }
-        /* PV4: positions are cut into chunks of 64; chunk c belongs to set
-         * c % 4.  Each set accumulates its positions in increasing order from
-         * 0; the four set sums are added in set order. */
-        float a[4];
-        for (int st = 0; st < 4; st++) {
-            float o = 0.0f;
-            for (size_t j = (size_t)st * 64; j < L; j += 256) {
-                size_t je = j + 64 < L ? j + 64 : L;
-                for (size_t jj = j; jj < je; jj++) o = o + sc[jj] * V[jj * hd + d];
-            }
-            a[st] = o;
-        }
-        out[d] = ((a[0] + a[1]) + a[2]) + a[3];
+        return;
     }
+    float run_m = -INFINITY, den = 0.0f;
+    for (size_t d = 0; d < hd; d++) out[d] = 0.0f; /* num */
+    for (size_t js = 0; js < L; js += ORC_ATT_SEG) {
+        size_t nj = L - js < ORC_ATT_SEG ? L - js : ORC_ATT_SEG;
+        float mc = -INFINITY;
+        for (size_t j = 0; j < nj; j++) {
+            float s = 0.0f;
+            const float* kr = K + (js + j) * hd;
+            for (size_t d = 0; d < hd; d++) s = s + q[d] * kr[d];
+            s = s * scale;
+            sc[j] = s;
+            if (s > mc) mc = s;
+        }
+        for (size_t j = 0; j < nj; j++) sc[j] = orc_expf(sc[j] - mc);
+        float lc = sum64(sc, nj);
+        float mn = run_m > mc ? run_m : mc;
+        float a = orc_expf(run_m - mn), b = orc_expf(mc - mn);
+        for (size_t d = 0; d < hd; d++) {
+            float o = 0.0f;
+            for (size_t j = 0; j < nj; j++) o = o + sc[j] * V[(js + j) * hd + d];
+            out[d] = out[d] * a + b * o;
+        }
+        den = den * a + b * lc;
+        run_m = mn;
+    }
+    for (size_t d = 0; d < hd; d++) out[d] = out[d] / den;
 }
 
 static int model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits, float* hidden,

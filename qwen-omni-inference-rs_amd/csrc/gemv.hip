@@ -1,26 +1,29 @@
 // gemv.hip -- decode-time Q8_0 GEMV (W8A32) for gfx950.
 //
-// A weight is stored as 64-row tiles; each tile row is cut into groups of 8
-// Q8_0 blocks (256 values, 16 KiB of codes per tile).  One wave owns one
-// (tile, group): lane r streams row r's codes with two coalesced 1 KiB loads
-// per block, keeps them in registers, and accumulates
-//   p_b = fmaf chain over the block's 32 codes,   a_g = fmaf(p_b, d_b, a_g).
-// The row result is y = ((0 + a_0) + a_1) + ... in group order.
+// A workgroup owns TPW consecutive 16-row tiles of W and the whole K range,
+// so every output is final when the workgroup ends (no cross-workgroup
+// reduction: on this chip a device-scope release/acquire costs more than the
+// GEMV body).  The K range of a tile is cut into G groups of CH block pairs
+// (CH = 1, 2 or 4); the (tile, group) items are spread over the waves.  A wave
+// reads a (tile, pair) chunk with one 16-byte load per lane (16 rows x 2
+// blocks = 1 KiB, coalesced).
 //
-// Two output modes:
-//   FINAL     one workgroup per tile, one wave per group; the group partials
-//             meet in LDS and wave 0 writes y (plus an optional residual).
-//   PARTIALS  one single-wave workgroup per (tile, group), so even a
-//             1024-row weight occupies the whole chip; the partials a_g are
-//             written out and the consuming kernel adds them in group order
-//             while it stages its own input (no extra launch, no
-//             cross-workgroup synchronisation).
-// Inputs may themselves arrive as partials: x_i = base_i + S_i with
-// S_i = ((0 + P_0,i) + P_1,i) + ...  (the residual add of the reference,
-// base + projection, with the projection completed first).
+// Issue order inside a workgroup: the loads of the input vector first (into
+// registers), then the weight loads of the wave's first item, then the input
+// transform (RmsNorm, silu * up, attention combine) into LDS.  Memory
+// counters complete in issue order, so the transform waits only for the
+// input and runs while the weights are in flight; every load is
+// unconditional (indices clamped), so all of a wave's loads are in flight
+// together.
 //
-// Every workgroup issues its weight loads before it stages the input, so the
-// HBM latency of the weights overlaps the staging.
+// Summation order per row (the oracle's GEMV order, bit for bit):
+//   h0_b = fmaf chain over codes 0..15 of block b, h1_b over codes 16..31
+//   (from +0, lane (row, half) computes one of them); v_b = (h0_b + h1_b) * d_b;
+//   pairwise tree over blocks: v[i] += v[i + s] for s = 1, 2, 4, ..., i + s < nb.
+// Level s = 1 pairs the two blocks of a chunk (lanes l and l ^ 32), the next
+// levels run in-lane over the CH pairs of a group, the rest over the group
+// sums; every group starts at a multiple of CH (a power of two), so the split
+// follows the tree exactly.
 #include "lq8_internal.h"
 #include "lq8_numerics.h"
 
@@ -29,14 +32,19 @@ namespace lq8 {
 namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int MAX_CH = 4;
+constexpr int MAX_WAVES = 16;
+constexpr int SP = 4;  // input float4s per thread held in registers (the rest load-and-use)
+constexpr int CU = 4;  // attention segments held in registers (256 positions)
+constexpr int EA = 2;  // attention outputs per thread held in registers
 
-enum OutMode : int { OUT_FINAL = 0, OUT_PARTIALS = 1 };
-
-__device__ __forceinline__ float dot16(u32x4 v, const float* __restrict__ x, float p) {
-    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+// fmaf chain over the 16 codes in v against x[0..15], from +0.
+__device__ __forceinline__ float dot16(u32x4 v, const float* __restrict__ x) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float p = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        float4 xv = *(const float4*)(x + 4 * i);
+        const float4 xv = *(const float4*)(x + 4 * i);
         p = fmaf((float)(int8_t)(w[i] & 0xFF), xv.x, p);
         p = fmaf((float)(int8_t)((w[i] >> 8) & 0xFF), xv.y, p);
         p = fmaf((float)(int8_t)((w[i] >> 16) & 0xFF), xv.z, p);
@@ -45,188 +53,455 @@ __device__ __forceinline__ float dot16(u32x4 v, const float* __restrict__ x, flo
     return p;
 }
 
-// Input element i: base_i + (partials summed in group order).
-__device__ __forceinline__ float load_x(const GemvLaunch& a, int i) {
-    if (a.xg == 0) return a.x[i];
-    float s = 0.0f;
-    for (int g = 0; g < a.xg; g++) s = s + a.xp[(size_t)g * a.xstride + i];
-    return a.x ? a.x[i] + s : s;
+__device__ __forceinline__ float4 bf16_round4(float4 v) {
+    return make_float4(bf16_round(v.x), bf16_round(v.y), bf16_round(v.z), bf16_round(v.w));
+}
+__device__ __forceinline__ float silu_mul(float g, float u) { return __fdiv_rn(g, 1.0f + expf_cr(-g)) * u; }
+// RmsNorm output element (src/rms_norm.rs:159-173): bf16((v * inv) * bf16(w)), v = bf16(x)
+__device__ __forceinline__ float4 norm4(float4 v, float4 w, float inv) {
+    return make_float4(bf16_round((v.x * inv) * bf16_round(w.x)), bf16_round((v.y * inv) * bf16_round(w.y)),
+                       bf16_round((v.z * inv) * bf16_round(w.z)), bf16_round((v.w * inv) * bf16_round(w.w)));
 }
 
-// Stage the input range [k0, k1) (relative to k0) into LDS.
-template <int XS, int NT>
-__device__ __forceinline__ void stage_range(const GemvLaunch& a, int k0, int k1, float* xs, float* red) {
-    const int tid = threadIdx.x;
-    if (XS == XS_PLAIN) {
-        if (a.xg == 0) {
-            for (int i = k0 + tid * 4; i < k1; i += NT * 4) *(float4*)(xs + i - k0) = *(const float4*)(a.x + i);
+// Input staging, split into the loads (issued before the weights) and the
+// transform into LDS xs[0, k) (ends with a barrier).
+template <int XS>
+struct Stage {
+    float4 xv[SP] = {}, wv[SP] = {};
+    float mcs[CU] = {}, lcs[CU] = {};
+    float ov[EA][CU] = {};
+
+    // Only waves whose 64 threads reach into the input issue its loads (a
+    // wave-uniform condition, so no lane-divergent branch around a load).
+    __device__ __forceinline__ void load(const GemvArgs& a, int wave) {
+        const int tid = threadIdx.x, nt = blockDim.x, k4 = a.k >> 2;
+        const float* __restrict__ x = a.x;
+        if (XS == XS_PLAIN || XS == XS_RMSNORM || XS == XS_SILU) {
+#pragma unroll
+            for (int e = 0; e < SP; e++) {
+                if (wave * 64 + e * nt < k4) {
+                    const int i4 = min(tid + e * nt, k4 - 1);
+                    xv[e] = *(const float4*)(x + 4 * i4);
+                    if (XS == XS_RMSNORM) wv[e] = *(const float4*)(a.norm_w + 4 * i4);
+                    if (XS == XS_SILU) wv[e] = *(const float4*)(x + a.k + 4 * i4);
+                }
+            }
         } else {
-            for (int i = k0 + tid; i < k1; i += NT) xs[i - k0] = load_x(a, i);
-        }
-    } else if (XS == XS_SILU) {
-        // silu(gate) * up (src/mlp.rs:151-164; silu src/tensor.rs:1978)
-        for (int i = k0 + tid; i < k1; i += NT) {
-            float g = load_x(a, i), u = load_x(a, a.k + i);
-            xs[i - k0] = __fdiv_rn(g, 1.0f + expf_cr(-g)) * u;
-        }
-    } else {
-        // RmsNorm (src/rms_norm.rs:143-176) of the whole input with the SUM64
-        // order; workgroup 0 also stores the (pre-norm) input when asked.
-        if (tid < 64) {
-            float acc = 0.0f;
-            for (int i = tid; i < a.k; i += 64) {
-                float xv = load_x(a, i);
-                if (a.x_out && blockIdx.x == 0) a.x_out[i] = xv;
-                float v = bf16_round(xv);
-                acc = acc + v * v;
+            const int H = a.attn_heads;
+            const int C = (a.d_pos ? *a.d_pos : a.pos_base) / ATT_SEG + 1;
+            const int h = min(tid, H - 1);
+            if (wave * 64 < H) {
+#pragma unroll
+                for (int c = 0; c < CU; c++) {
+                    const float* p = x + ((size_t)min(c, C - 1) * H + h) * ATT_PART_STRIDE;
+                    mcs[c] = p[128];
+                    lcs[c] = p[129];
+                }
             }
 #pragma unroll
-            for (int d = 32; d >= 1; d >>= 1) acc = acc + __shfl_xor(acc, d, 64);
-            if (tid == 0) red[0] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)a.k) + a.eps));
+            for (int e = 0; e < EA; e++) {
+                if (wave * 64 + e * nt < a.k) {
+                    const int i = min(tid + e * nt, a.k - 1);
+#pragma unroll
+                    for (int c = 0; c < CU; c++)
+                        ov[e][c] = x[((size_t)min(c, C - 1) * H + (i >> 7)) * ATT_PART_STRIDE + (i & 127)];
+                }
+            }
         }
-        __syncthreads();
-        const float inv = red[0];
-        for (int i = k0 + tid; i < k1; i += NT)
-            xs[i - k0] = bf16_round((bf16_round(load_x(a, i)) * inv) * bf16_round(a.norm_w[i]));
+    }
+
+    __device__ __forceinline__ void finish(const GemvArgs& a, int wave, float* xs, float* red) {
+        const int tid = threadIdx.x, nt = blockDim.x, k = a.k, k4 = k >> 2;
+        const float* __restrict__ x = a.x;
+        if (XS == XS_PLAIN) {
+#pragma unroll
+            for (int e = 0; e < SP; e++)
+                if (wave * 64 + e * nt < k4 && tid + e * nt < k4) {
+                    const float4 v = xv[e];  // component copy: keeps xv in registers
+                    *(float4*)(xs + 4 * (tid + e * nt)) = make_float4(v.x, v.y, v.z, v.w);
+                }
+            for (int i4 = tid + SP * nt; i4 < k4; i4 += nt) *(float4*)(xs + 4 * i4) = *(const float4*)(x + 4 * i4);
+            __syncthreads();
+        } else if (XS == XS_SILU) {
+            // silu(gate) * up (src/mlp.rs:151-164; silu src/tensor.rs:1978)
+#pragma unroll
+            for (int e = 0; e < SP; e++)
+                if (wave * 64 + e * nt < k4 && tid + e * nt < k4) {
+                    const float4 g = xv[e], u = wv[e];
+                    *(float4*)(xs + 4 * (tid + e * nt)) =
+                        make_float4(silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w));
+                }
+            for (int i4 = tid + SP * nt; i4 < k4; i4 += nt) {
+                const float4 g = *(const float4*)(x + 4 * i4), u = *(const float4*)(x + k + 4 * i4);
+                *(float4*)(xs + 4 * i4) =
+                    make_float4(silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w));
+            }
+            __syncthreads();
+        } else if (XS == XS_RMSNORM) {
+            // RmsNorm (src/rms_norm.rs:143-176): input rounded to bf16; sum of
+            // squares in the SUM64 order (lane l adds elements l, l + 64, ... in
+            // order; the 64 partials fold at distances 32, 16, 8, 4, 2, 1);
+            // inv = 1 / sqrt(sum / k + eps); out = bf16((v * inv) * bf16(w)).
+#pragma unroll
+            for (int e = 0; e < SP; e++)
+                if (wave * 64 + e * nt < k4 && tid + e * nt < k4) *(float4*)(xs + 4 * (tid + e * nt)) = bf16_round4(xv[e]);
+            for (int i4 = tid + SP * nt; i4 < k4; i4 += nt) *(float4*)(xs + 4 * i4) = bf16_round4(*(const float4*)(x + 4 * i4));
+            __syncthreads();
+            if (tid < 64) {
+                float acc = 0.0f;
+                for (int i = tid; i < k; i += 64) {
+                    const float v = xs[i];
+                    acc = acc + v * v;
+                }
+#pragma unroll
+                for (int d = 32; d >= 1; d >>= 1) acc = acc + __shfl_xor(acc, d, 64);
+                if (tid == 0) red[0] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)k) + a.eps));
+            }
+            __syncthreads();
+            const float inv = red[0];
+#pragma unroll
+            for (int e = 0; e < SP; e++)
+                if (wave * 64 + e * nt < k4 && tid + e * nt < k4) {
+                    float4* p = (float4*)(xs + 4 * (tid + e * nt));
+                    *p = norm4(*p, wv[e], inv);
+                }
+            for (int i4 = tid + SP * nt; i4 < k4; i4 += nt) {
+                float4* p = (float4*)(xs + 4 * i4);
+                *p = norm4(*p, *(const float4*)(a.norm_w + 4 * i4), inv);
+            }
+            __syncthreads();
+        } else {
+            // Attention output (src/attention.rs:374-399) from per-segment
+            // partials (o_c, m_c, l_c) of each head, combined in segment order:
+            // m' = max(m, m_c), a = exp(m - m'), b = exp(m_c - m'),
+            // num = num * a + b * o_c, den = den * a + b * l_c; x = num / den.
+            const int H = a.attn_heads;
+            const int C = (a.d_pos ? *a.d_pos : a.pos_base) / ATT_SEG + 1;
+            float* coef = red + 4;                     // [C][H][2]
+            float* dens = coef + a.attn_cmax * H * 2;  // [H]
+            for (int h = tid; h < H; h += nt) {
+                float m = -__builtin_huge_valf(), den = 0.0f;
+                for (int c0 = 0; c0 < C; c0 += CU) {
+                    float mc[CU], lc[CU];
+#pragma unroll
+                    for (int c = 0; c < CU; c++) {
+                        if (c0 == 0 && h == tid) {
+                            mc[c] = mcs[c];
+                            lc[c] = lcs[c];
+                        } else {
+                            const float* p = x + ((size_t)min(c0 + c, C - 1) * H + h) * ATT_PART_STRIDE;
+                            mc[c] = p[128];
+                            lc[c] = p[129];
+                        }
+                    }
+#pragma unroll
+                    for (int c = 0; c < CU; c++) {
+                        if (c0 + c < C) {
+                            const float mn = m > mc[c] ? m : mc[c];
+                            const float ea = expf_cr(m - mn), eb = expf_cr(mc[c] - mn);
+                            coef[((c0 + c) * H + h) * 2] = ea;
+                            coef[((c0 + c) * H + h) * 2 + 1] = eb;
+                            den = den * ea + eb * lc[c];
+                            m = mn;
+                        }
+                    }
+                }
+                dens[h] = den;
+            }
+            __syncthreads();
+            for (int e0 = 0; tid + e0 * nt < k; e0 += EA) {
+#pragma unroll
+                for (int e = 0; e < EA; e++) {
+                    const int i = tid + (e0 + e) * nt;
+                    if (i < k) {
+                        const int h = i >> 7, d = i & 127;
+                        float num = 0.0f;
+                        for (int c0 = 0; c0 < C; c0 += CU) {
+                            float o[CU];
+#pragma unroll
+                            for (int c = 0; c < CU; c++)
+                                o[c] = (c0 == 0 && e0 == 0) ? ov[e][c]
+                                                            : x[((size_t)min(c0 + c, C - 1) * H + h) * ATT_PART_STRIDE + d];
+#pragma unroll
+                            for (int c = 0; c < CU; c++)
+                                if (c0 + c < C)
+                                    num = num * coef[((c0 + c) * H + h) * 2] + coef[((c0 + c) * H + h) * 2 + 1] * o[c];
+                        }
+                        xs[i] = __fdiv_rn(num, dens[h]);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+};
+
+// Pairs per group for a K range of np pairs over up to W waves.
+inline int pick_ch(int np, int w) {
+    int ch = 1;
+    while (ch < MAX_CH && (np + ch - 1) / ch > w) ch *= 2;
+    return ch;
+}
+
+// TPW tiles from tile0 (ntiles of them valid): rows tile*16 .. tile*16+15.
+// LDS: xs [np * 64] (the input, zero over the padding block of an odd nb),
+// gs [ntiles * G][16] group sums, red [4] (+ the XS_ATTN coefficients).
+template <int XS, int EPI, int CH>
+__device__ __forceinline__ void gemv_tiles(const GemvArgs& a, int tile0, int ntiles, float* sm) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar control flow
+    const int W = blockDim.x >> 6;
+    const int nb = a.k >> 5, np = (nb + 1) >> 1;
+    const int G = (np + CH - 1) / CH;
+    const int items = ntiles * G;
+    float* xs = sm;
+    float* gs = sm + np * 64;
+    float* red = gs + items * 16;
+    const int r = lane & 15, part = lane >> 4, bsel = part >> 1, half = part & 1;
+    const int8_t* cbase = a.codes + (size_t)tile0 * np * CHUNK_BYTES + lane * 16;
+    const uint16_t* sbase = a.scales + (size_t)tile0 * 2 * np * 16 + bsel * 16 + r;
+    Stage<XS> st;
+    st.load(a, wave);
+    if ((nb & 1) && threadIdx.x < 32) xs[a.k + threadIdx.x] = 0.0f;  // ordered by the staging barriers
+    // weights of the current item (cv, ds) and the next one (nv, ns)
+    u32x4 cv[CH], nv[CH];
+    uint16_t ds[CH], ns[CH];
+    {
+        const int it0 = min(wave, items - 1);
+        const int t0 = it0 / G, g0 = it0 - t0 * G;
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int c = t0 * np + min(g0 * CH + i, np - 1);  // chunk of (tile t0, group g0)
+            nv[i] = __builtin_nontemporal_load((const u32x4*)(cbase + (size_t)c * CHUNK_BYTES));
+            ns[i] = sbase[(size_t)c * 32];
+        }
+    }
+    st.finish(a, wave, xs, red);
+    for (int item = wave; item < items; item += W) {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            cv[i] = nv[i];
+            ds[i] = ns[i];
+        }
+        if (item + W < items) {
+            const int tn = (item + W) / G, gn = item + W - tn * G;
+#pragma unroll
+            for (int i = 0; i < CH; i++) {
+                const int c = tn * np + min(gn * CH + i, np - 1);
+                nv[i] = __builtin_nontemporal_load((const u32x4*)(cbase + (size_t)c * CHUNK_BYTES));
+                ns[i] = sbase[(size_t)c * 32];
+            }
+        }
+        const int g = item % G;
+        const int cnt = min(CH, np - g * CH);  // valid pairs of this group
+        float v[CH];
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int p = min(g * CH + i, np - 1);
+            const float h = dot16(cv[i], xs + (2 * p + bsel) * 32 + half * 16);
+            const float o = __shfl_xor(h, 16, 64);
+            const float h0 = half ? o : h, h1 = half ? h : o;
+            const float vb = (h0 + h1) * f16_bits_to_f32(ds[i]);
+            const float ov = __shfl_xor(vb, 32, 64);
+            // level s = 1 of the tree: blocks 2p and 2p + 1 (absent when nb is odd)
+            if (2 * p + 1 >= nb) v[i] = bsel ? ov : vb;
+            else v[i] = bsel ? ov + vb : vb + ov;
+        }
+#pragma unroll
+        for (int s = 1; s < CH; s *= 2)
+#pragma unroll
+            for (int i = 0; i + s < CH; i += 2 * s)
+                if (i + s < cnt) v[i] = v[i] + v[i + s];
+        if (lane < 16) gs[item * 16 + lane] = v[0];
+    }
+    __syncthreads();
+    if (wave < ntiles) {
+        // wave t finishes tile tile0 + t: the tree over its G group sums
+        const float* tg = gs + wave * G * 16;
+        float acc = 0.0f;
+        if (G <= 16) {
+            float t[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) t[i] = i < G ? tg[i * 16 + r] : 0.0f;
+#pragma unroll
+            for (int s = 1; s < 16; s *= 2)
+#pragma unroll
+                for (int i = 0; i + s < 16; i += 2 * s)
+                    if (i + s < G) t[i] = t[i] + t[i + s];
+            acc = t[0];
+        } else if (lane < 16) {
+            float* tw = gs + wave * G * 16;
+            for (int s = 1; s < G; s *= 2)
+                for (int i = 0; i + s < G; i += 2 * s) tw[i * 16 + lane] = tw[i * 16 + lane] + tw[(i + s) * 16 + lane];
+            acc = tw[lane];
+        }
+        const int tile = tile0 + wave;
+        const int row = tile * TILE_ROWS + r;
+        const bool valid = lane < 16 && row < a.n;
+        if (EPI == EPI_RESID) {
+            if (valid) a.y[row] = a.resid[row] + acc;
+        } else {
+            if (valid) a.y[row] = acc;
+        }
+        if (EPI == EPI_ARGMAX) {
+            // greedy pick within the tile: maximum, last index on ties
+            float bv = valid ? acc : -__builtin_huge_valf();
+            int bi = valid ? row : -1;
+#pragma unroll
+            for (int d = 8; d >= 1; d >>= 1) {
+                const float ov = __shfl_xor(bv, d, 64);
+                const int oi = __shfl_xor(bi, d, 64);
+                if (ov > bv || (ov == bv && oi > bi)) { bv = ov; bi = oi; }
+            }
+            if (lane == 0) {
+                a.arg_val[tile] = bv;
+                a.arg_idx[tile] = bi;
+            }
+        }
     }
 }
 
-// W waves per workgroup.  FINAL: workgroup = tile, wave = group (W >= groups).
-// PARTIALS: W == 1, workgroup = (tile, group) with tile = blockIdx / groups.
-template <int XS, int W, int MODE>
-__global__ __launch_bounds__(64 * W) void k_gemv2(GemvLaunch a) {
+template <int XS, int EPI, int CH>
+__global__ __launch_bounds__(1024) void k_gemv(GemvArgs a, int tpw) {
     extern __shared__ float smem[];
-    float* xs = smem;  // staged input range
-    const int nb = a.k / 32;
-    const int ngroups = (nb + GROUP_BLOCKS - 1) / GROUP_BLOCKS;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    size_t tile;
-    int g;
-    if (MODE == OUT_PARTIALS) {
-        tile = blockIdx.x / ngroups;
-        g = blockIdx.x % ngroups;
-    } else {
-        tile = blockIdx.x;
-        g = wave;
-    }
-    const int range = MODE == OUT_PARTIALS ? GROUP_BLOCKS * 32 : a.k;
-    float* red = xs + range;  // 4 floats
-    float* part = red + 4;    // W * 64 floats
-    const int b0 = g * GROUP_BLOCKS;
-    const int nblk = g < ngroups ? min(GROUP_BLOCKS, nb - b0) : 0;
-    const int k0 = MODE == OUT_PARTIALS ? b0 * 32 : 0;
-    const int k1 = MODE == OUT_PARTIALS ? min(a.k, k0 + GROUP_BLOCKS * 32) : a.k;
+    const int tiles = (a.n + TILE_ROWS - 1) / TILE_ROWS;
+    const int tile0 = blockIdx.x * tpw;
+    gemv_tiles<XS, EPI, CH>(a, tile0, min(tpw, tiles - tile0), smem);
+}
 
-    const int8_t* cb = a.codes + (tile * nb + b0) * 2048 + lane * 16;
-    const uint16_t* sb = a.scales + (tile * nb + b0) * 64 + lane;
-    float acc = 0.0f;
-    if (nblk == GROUP_BLOCKS) {
-        // weights first: 8 blocks x 2 x 16 bytes per lane, plus the scales
-        u32x4 lo[GROUP_BLOCKS], hi[GROUP_BLOCKS];
-        uint16_t ds[GROUP_BLOCKS];
-#pragma unroll
-        for (int i = 0; i < GROUP_BLOCKS; i++) {
-            lo[i] = __builtin_nontemporal_load((const u32x4*)(cb + i * 2048));
-            hi[i] = __builtin_nontemporal_load((const u32x4*)(cb + i * 2048 + 1024));
-            ds[i] = sb[i * 64];
-        }
-        stage_range<XS, 64 * W>(a, k0, k1, xs, red);
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < GROUP_BLOCKS; i++) {
-            const float* xb = xs + (b0 + i) * 32 - k0;
-            float p = dot16(lo[i], xb, 0.0f);
-            p = dot16(hi[i], xb + 16, p);
-            acc = fmaf(p, f16_bits_to_f32(ds[i]), acc);
-        }
-    } else {
-        // tail group (fewer than 8 blocks) or an idle wave
-        stage_range<XS, 64 * W>(a, k0, k1, xs, red);
-        __syncthreads();
-        for (int i = 0; i < nblk; i++) {
-            u32x4 l = *(const u32x4*)(cb + i * 2048);
-            u32x4 h = *(const u32x4*)(cb + i * 2048 + 1024);
-            const float* xb = xs + (b0 + i) * 32 - k0;
-            float p = dot16(l, xb, 0.0f);
-            p = dot16(h, xb + 16, p);
-            acc = fmaf(p, f16_bits_to_f32(sb[i * 64]), acc);
-        }
+__global__ __launch_bounds__(256) void k_gemv_grouped(const GemvProblemDev* __restrict__ probs, int count) {
+    extern __shared__ float smem[];
+    int lo = 0, hi = count - 1;
+    const int t = blockIdx.x;
+    while (lo < hi) {  // the problem owning this tile (tile_begin ascending)
+        const int mid = (lo + hi + 1) >> 1;
+        if (probs[mid].tile_begin <= t) lo = mid;
+        else hi = mid - 1;
     }
-    if (MODE == OUT_PARTIALS) {
-        const size_t tiles = (size_t)(a.n + TILE_ROWS - 1) / TILE_ROWS;
-        a.partials[(size_t)g * tiles * TILE_ROWS + tile * TILE_ROWS + lane] = acc;
-    } else {
-        part[wave * 64 + lane] = acc;
-        __syncthreads();
-        if (wave == 0) {
-            float y = 0.0f;
-            for (int gg = 0; gg < ngroups; gg++) y = y + part[gg * 64 + lane];
-            const size_t row = tile * TILE_ROWS + lane;
-            if (row < (size_t)a.n) {
-                if (a.resid) y = a.resid[row] + y;
-                a.y[row] = y;
-            }
+    const GemvProblemDev p = probs[lo];
+    GemvArgs a{p.codes, p.scales, p.x, nullptr, p.y, nullptr, nullptr, nullptr, p.n, p.k, 0.0f};
+    // (descriptor k is bounded by GEMV_MAX_K on the host)
+    gemv_tiles<XS_PLAIN, EPI_STORE, MAX_CH>(a, t - p.tile_begin, 1, smem);
+}
+
+// Greedy pick (src/generate.rs:153-174 via src/tensor.rs:2451-2480):
+// maximum over the tiles' partials, last index on ties.
+__global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__ val, const int* __restrict__ idx,
+                                                       int count, uint32_t* d_tok, uint32_t* tokens_out, int* d_pos,
+                                                       int* d_step) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -__builtin_huge_valf();
+    int bi = -1;
+    constexpr int AU = 16;  // entries per thread per pass, loads issued together
+    for (int i0 = tid; i0 < count; i0 += 1024 * AU) {
+        float v[AU];
+        int j[AU];
+#pragma unroll
+        for (int e = 0; e < AU; e++) {
+            const int i = min(i0 + e * 1024, count - 1);
+            v[e] = val[i];
+            j[e] = idx[i];
         }
+#pragma unroll
+        for (int e = 0; e < AU; e++)
+            if (i0 + e * 1024 < count && (v[e] > bv || (v[e] == bv && j[e] > bi))) { bv = v[e]; bi = j[e]; }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const float ov = __shfl_xor(bv, d, 64);
+        const int oi = __shfl_xor(bi, d, 64);
+        if (ov > bv || (ov == bv && oi > bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+            if (sv[w] > bv || (sv[w] == bv && si[w] > bi)) { bv = sv[w]; bi = si[w]; }
+        const uint32_t tok = (uint32_t)(bi < 0 ? 0 : bi);
+        *d_tok = tok;
+        tokens_out[*d_step] = tok;
+        *d_step = *d_step + 1;
+        *d_pos = *d_pos + 1;
     }
 }
 
-__global__ __launch_bounds__(256) void k_combine(const float* __restrict__ base, const float* __restrict__ partials,
-                                                 int groups, size_t stride, int n, float* __restrict__ y) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    float s = 0.0f;
-    for (int g = 0; g < groups; g++) s = s + partials[(size_t)g * stride + i];
-    y[i] = base ? base[i] + s : s;
-}
-
-template <int XS, int W, int MODE>
-lq8_status launch_v2(hipStream_t s, const GemvLaunch& a, unsigned grid) {
-    const int range = MODE == OUT_PARTIALS ? GROUP_BLOCKS * 32 : a.k;
-    size_t smem = (size_t)(range + 4 + W * 64) * sizeof(float);
-    hipLaunchKernelGGL((k_gemv2<XS, W, MODE>), dim3(grid), dim3(64 * W), smem, s, a);
+template <int XS, int EPI>
+lq8_status launch_one(hipStream_t s, const GemvArgs& a) {
+    const int nb = a.k >> 5, np = (nb + 1) >> 1;
+    const int tiles = (a.n + TILE_ROWS - 1) / TILE_ROWS;
+    // Many tiles (lm_head): 4 pairs per item, 4 tiles per 4-wave workgroup
+    // (one staged input serves 64 rows, each wave loops over its items with
+    // the next item's weights prefetched); few tiles: one tile per workgroup
+    // and up to 16 waves to spread it over the CU.
+    int ch, tpw, waves;
+    const int wmax = tiles >= 1024 ? 4 : MAX_WAVES;
+    if (tiles >= 1024) {
+        ch = MAX_CH;
+        tpw = 4;
+    } else {
+        ch = pick_ch(np, MAX_WAVES);
+        tpw = 1;
+    }
+    const int G = (np + ch - 1) / ch;
+    waves = max(tpw, min(wmax, tpw * G));
+    size_t smem = ((size_t)np * 64 + (size_t)tpw * G * 16 + 4) * sizeof(float);
+    if (XS == XS_ATTN) smem += ((size_t)a.attn_cmax * a.attn_heads * 2 + a.attn_heads) * sizeof(float);
+    if (smem > 64 * 1024) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: input staging exceeds 64 KiB of LDS");
+    const dim3 grid((unsigned)((tiles + tpw - 1) / tpw)), block(64 * waves);
+    if (ch == 1) hipLaunchKernelGGL((k_gemv<XS, EPI, 1>), grid, block, smem, s, a, tpw);
+    else if (ch == 2) hipLaunchKernelGGL((k_gemv<XS, EPI, 2>), grid, block, smem, s, a, tpw);
+    else hipLaunchKernelGGL((k_gemv<XS, EPI, 4>), grid, block, smem, s, a, tpw);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
 
 template <int XS>
-lq8_status dispatch(hipStream_t s, const GemvLaunch& a) {
-    const int nb = a.k / 32, ngroups = (nb + GROUP_BLOCKS - 1) / GROUP_BLOCKS;
-    const size_t tiles = (a.n + TILE_ROWS - 1) / TILE_ROWS;
-    if (a.partials) {
-        if (tiles * TILE_ROWS * (size_t)ngroups > (size_t)a.partials_cap)
-            return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: partial buffer too small");
-        return launch_v2<XS, 1, OUT_PARTIALS>(s, a, (unsigned)(tiles * ngroups));
+lq8_status launch_epi(hipStream_t s, Epilogue epi, const GemvArgs& a) {
+    switch (epi) {
+        case EPI_STORE: return launch_one<XS, EPI_STORE>(s, a);
+        case EPI_RESID: return launch_one<XS, EPI_RESID>(s, a);
+        default: return launch_one<XS, EPI_ARGMAX>(s, a);
     }
-    if (a.k > 8192) return launch_gemv_tile_wg(s, (XSource)XS, a);
-    const unsigned grid = (unsigned)tiles;
-    if (ngroups <= 4) return launch_v2<XS, 4, OUT_FINAL>(s, a, grid);
-    if (ngroups <= 8) return launch_v2<XS, 8, OUT_FINAL>(s, a, grid);
-    if (ngroups <= 16) return launch_v2<XS, 16, OUT_FINAL>(s, a, grid);
-    return launch_gemv_tile_wg(s, (XSource)XS, a);
 }
 
 }  // namespace
 
-lq8_status launch_gemv(hipStream_t s, XSource xs, const GemvLaunch& a) {
+lq8_status launch_gemv(hipStream_t s, XSource xs, Epilogue epi, const GemvArgs& a) {
     if (a.k <= 0 || a.k % 32 || a.n <= 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k must be a positive multiple of 32");
-    if (a.k > 16384) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k > 16384 not supported");
+    if (a.k > GEMV_MAX_K) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k above 12288 is not supported");
+    if (epi == EPI_RESID && !a.resid) return fail(LQ8_ERR_INVALID_ARG, "gemv: residual is null");
+    if (epi == EPI_ARGMAX && (!a.arg_val || !a.arg_idx)) return fail(LQ8_ERR_INVALID_ARG, "gemv: argmax buffers are null");
+    if (xs == XS_ATTN && (a.attn_heads * 128 != a.k || a.attn_cmax <= 0))
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: attention input layout does not match k");
     switch (xs) {
-        case XS_PLAIN: return dispatch<XS_PLAIN>(s, a);
-        case XS_RMSNORM: return dispatch<XS_RMSNORM>(s, a);
-        default: return dispatch<XS_SILU>(s, a);
+        case XS_PLAIN: return launch_epi<XS_PLAIN>(s, epi, a);
+        case XS_RMSNORM: return launch_epi<XS_RMSNORM>(s, epi, a);
+        case XS_SILU: return launch_epi<XS_SILU>(s, epi, a);
+        default: return launch_epi<XS_ATTN>(s, epi, a);
     }
 }
 
-lq8_status launch_combine(hipStream_t s, const float* base, const float* partials, int groups, size_t stride, int n,
-                          float* y) {
-    if (n <= 0) return LQ8_OK;
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, base, partials, groups, stride, n,
-                       y);
+lq8_status launch_gemv_grouped(hipStream_t s, const GemvProblemDev* d_probs, int count, int total_tiles,
+                               int max_k) {
+    if (count <= 0 || total_tiles <= 0) return LQ8_OK;
+    // throughput form: 4 waves per tile, 4 pairs per group (a wave loops over groups)
+    const int np = ((max_k >> 5) + 1) >> 1;
+    const int gmax = (np + MAX_CH - 1) / MAX_CH;
+    const size_t smem = ((size_t)np * 64 + (size_t)gmax * 16 + 4) * sizeof(float);
+    hipLaunchKernelGGL(k_gemv_grouped, dim3((unsigned)total_tiles), dim3(256), smem, s, d_probs, count);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
 
-size_t gemv_partial_stride(int n) { return (size_t)((n + TILE_ROWS - 1) / TILE_ROWS) * TILE_ROWS; }
-int gemv_groups(int k) { return (k / 32 + GROUP_BLOCKS - 1) / GROUP_BLOCKS; }
+lq8_status launch_argmax_final(hipStream_t s, const float* arg_val, const int* arg_idx, int count, uint32_t* d_tok,
+                               uint32_t* tokens_out, int* d_pos, int* d_step) {
+    if (count <= 0) return fail(LQ8_ERR_INVALID_ARG, "argmax: empty");
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, s, arg_val, arg_idx, count, d_tok, tokens_out, d_pos,
+                       d_step);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
 
 }  // namespace lq8

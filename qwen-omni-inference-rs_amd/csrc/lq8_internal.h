@@ -1,13 +1,17 @@
 // lq8_internal.h -- shared definitions of the gfx950 Q8_0 library.
 //
 // Device layout of a Q8_0 weight W[n_out, k_in] (nb = k_in / 32 blocks per
-// row, rows padded to a multiple of 64):
-//   codes  [tiles = ceil(n_out/64)][nb][2 halves][64 rows][16 int8]
-//   scales [tiles][nb][64 rows] f16 bits
-// One (tile, block) pair is 2 KiB of codes: lane r of a wave reads row r's
-// codes 0..15 from the first KiB and 16..31 from the second, so both 16-byte
-// loads of a wave are 1 KiB contiguous.  The same layout feeds the MFMA GEMM
-// (32-row halves of a tile are 512-byte contiguous operand slices).
+// row, np = ceil(nb / 2) block pairs; rows grouped into 16-row tiles):
+//   codes  [tiles][np][part 0..3][16 rows][16 int8]      1 KiB per (tile, pair)
+//          part = (block & 1) * 2 + half: codes 16*half .. 16*half + 15 of
+//          block 2*pair + (part >> 1)
+//   scales [tiles][2 * np][16 rows] f16 bits
+// Lane l of a wave reading one (tile, pair) chunk with a 16-byte load gets
+// row l % 16, part l / 16: one 1 KiB coalesced load covers 16 rows x 2
+// blocks.  The same chunk is the A/B operand layout of the int8 MFMA GEMM
+// (rows 0..15 and 16..31 of a 32-row MFMA tile come from two tiles).
+// Padding rows (n_out .. 16 * tiles) and the padding block of an odd nb are
+// zero codes with a zero scale.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -22,9 +26,17 @@ namespace lq8 {
 
 constexpr int QK = 32;
 constexpr int BLOCK_BYTES = 34;
-constexpr int TILE_ROWS = 64;
-constexpr int GROUP_BLOCKS = 8;  // blocks per accumulation group
-constexpr int TILE_BLOCK_BYTES = TILE_ROWS * QK;
+constexpr int TILE_ROWS = 16;
+constexpr int CHUNK_BYTES = 1024;   // one (tile, pair) chunk of codes
+constexpr int GEMM_GROUP = 8;       // blocks per accumulation group of the W8A8 GEMM
+constexpr int GEMV_MAX_K = 12288;  // staged input + group sums stay under 64 KiB of LDS
+
+__host__ __device__ inline size_t code_off(size_t tile, size_t np, size_t b, int half, int r) {
+    return ((tile * np + (b >> 1)) * 64 + ((b & 1) * 2 + half) * 16 + r) * 16;
+}
+__host__ __device__ inline size_t scale_off(size_t tile, size_t np, size_t b, int r) {
+    return (tile * 2 * np + b) * 16 + r;
+}
 
 // ---- error plumbing ------------------------------------------------------
 void set_error(const std::string& msg);
@@ -58,7 +70,7 @@ struct lq8_ctx {
 
 struct lq8_weight {
     lq8_ctx* ctx = nullptr;
-    size_t n_out = 0, k_in = 0, nb = 0, tiles = 0;
+    size_t n_out = 0, k_in = 0, nb = 0, np = 0, tiles = 0;
     int8_t* codes = nullptr;
     uint16_t* scales = nullptr;
 };
@@ -68,38 +80,31 @@ namespace lq8 {
 // Scratch owned by the context; grows on demand (synchronizes before growing).
 lq8_status ctx_scratch(lq8_ctx* ctx, size_t bytes, void** out);
 
-// ---- kernel launchers (kernels.hip) -------------------------------------
-// x-source of a GEMV: plain f32 vector, RMSNorm of a hidden vector, or
-// silu(gate) * up of a concatenated [gate | up] vector.
-enum XSource : int { XS_PLAIN = 0, XS_RMSNORM = 1, XS_SILU = 2 };
+// ---- GEMV (gemv.hip) ---------------------------------------------------------
+// Input x of a GEMV: plain f32 vector, RmsNorm of a hidden vector,
+// silu(gate) * up of a concatenated [gate | up] vector, or the attention
+// output combined from per-segment partials (x = partials, see AttnSegLaunch).
+enum XSource : int { XS_PLAIN = 0, XS_RMSNORM = 1, XS_SILU = 2, XS_ATTN = 3 };
+// Output: y = W x, y = resid + W x, or y = W x plus the per-tile argmax
+// (value, index; last index on ties) of the logits.
+enum Epilogue : int { EPI_STORE = 0, EPI_RESID = 1, EPI_ARGMAX = 2 };
 
-struct GemvLaunch {
+struct GemvArgs {
     const int8_t* codes;
     const uint16_t* scales;
     const float* x;        // XS_PLAIN: x[k]; XS_RMSNORM: hidden[k]; XS_SILU: gu[2k]
     const float* norm_w;   // XS_RMSNORM weight [k]
-    float eps;
-    float* y;              // output [n]
-    const float* resid;    // if non-null: y = resid + Wx
+    float* y;              // [n]
+    const float* resid;    // EPI_RESID: [n]
+    float* arg_val;        // EPI_ARGMAX: [tiles]
+    int* arg_idx;          // EPI_ARGMAX: [tiles]
     int n, k;
-    // PARTIALS output: group partials [groups][stride] instead of y
-    float* partials = nullptr;
-    long long partials_cap = 0;
-    // input as base + partials: x_i = (x ? x[i] : 0) + ((0 + xp[0][i]) + xp[1][i] + ...)
-    const float* xp = nullptr;
-    int xg = 0;
-    size_t xstride = 0;
-    float* x_out = nullptr;  // RMSNORM source: workgroup 0 stores the combined input here
+    float eps;
+    // XS_ATTN: position (device scalar or base), heads, partial rows per segment capacity
+    const int* d_pos = nullptr;
+    int pos_base = 0, attn_heads = 0, attn_cmax = 0;
 };
-lq8_status launch_gemv(hipStream_t s, XSource xs, const GemvLaunch& a);
-// One workgroup per 64-row tile (all groups in one workgroup, no counters).
-lq8_status launch_gemv_tile_wg(hipStream_t s, XSource xs, const GemvLaunch& a);
-// Row stride of a PARTIALS output and number of groups of a k-wide input.
-size_t gemv_partial_stride(int n);
-int gemv_groups(int k);
-// y = (base ? base : 0) + ((0 + P[0]) + P[1] + ...), elementwise.
-lq8_status launch_combine(hipStream_t s, const float* base, const float* partials, int groups, size_t stride, int n,
-                          float* y);
+lq8_status launch_gemv(hipStream_t s, XSource xs, Epilogue epi, const GemvArgs& a);
 
 // Grouped GEMV over independent problems (device-side descriptor table).
 struct GemvProblemDev {
@@ -111,17 +116,23 @@ struct GemvProblemDev {
 };
 lq8_status launch_gemv_grouped(hipStream_t s, const GemvProblemDev* d_probs, int count, int total_tiles,
                                int max_k);
+// Final greedy pick over the per-tile argmax partials: token -> *d_tok and
+// tokens_out[*d_step], then *d_pos and *d_step advance (device scalars).
+lq8_status launch_argmax_final(hipStream_t s, const float* arg_val, const int* arg_idx, int count, uint32_t* d_tok,
+                               uint32_t* tokens_out, int* d_pos, int* d_step);
 
-// Activation quantization into the tiled layout (codes + f32 scales).
+// ---- Q8_0 format, activation quantization, GEMM (q8_kernels.hip) -------------
+// Activation rows x[m, k] -> tiled codes (as a weight) + f32 scales [mtiles][2*np][16].
 lq8_status launch_quantize_act(hipStream_t s, const float* x, int m, int k, int8_t* codes, float* scales32);
+size_t act_code_bytes(int m, int k);
+size_t act_scale_bytes(int m, int k);
 // AoS quantization (public device quantizer).
 lq8_status launch_quantize_aos(hipStream_t s, const float* x, size_t nblocks, uint8_t* blocks);
 // W8A8 GEMM: y[m, n] (+ resid) from tiled activations and a tiled weight.
 lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const float* xs, int m, const lq8_weight* w, float* y,
-                       const float* resid, int ldy, int col0);
+                       const float* resid);
 
-lq8_status launch_repack_aos(hipStream_t s, const uint8_t* aos, size_t n_rows, size_t nb, size_t row0,
-                             const lq8_weight* w);
+lq8_status launch_repack_aos(hipStream_t s, const uint8_t* aos, size_t n_rows, size_t row0, const lq8_weight* w);
 lq8_status launch_unpack_aos(hipStream_t s, const lq8_weight* w, size_t row0, size_t n_rows, uint8_t* aos);
 lq8_status launch_quantize_weight_f32(hipStream_t s, const float* src, size_t n_rows, size_t row0,
                                       const lq8_weight* w);
@@ -129,7 +140,6 @@ lq8_status launch_random_weight(hipStream_t s, const lq8_weight* w, size_t row0,
                                 uint64_t stream, float stddev);
 lq8_status launch_dequant_rows(hipStream_t s, const lq8_weight* w, const uint32_t* d_ids, size_t row0,
                                size_t nrows, float* y);
-
 
 // ---- decoder support kernels (model_kernels.hip) ---------------------------
 // positions: pos_i = (d_pos ? *d_pos : pos_base) + i
@@ -148,48 +158,48 @@ struct QkRopeLaunch {
 };
 lq8_status launch_qk_rope_kv(hipStream_t s, const QkRopeLaunch& a);
 
-struct AttnLaunch {
-    const float* q;        // [n][num_heads*head_dim]
-    const float* k_cache;
-    const float* v_cache;
-    float* out;            // [n][num_heads*head_dim]
-    const int* d_pos;
-    int pos_base, n, num_heads, num_kv_heads, head_dim, max_pos;
-    float scale;
-};
-lq8_status launch_attention(hipStream_t s, const AttnLaunch& a);
+// Attention (head_dim 128, G = num_heads / num_kv_heads <= ATT_MAX_GROUP
+// query heads per kv head), positions in segments of ATT_SEG.
+constexpr int ATT_SEG = 64;
+constexpr int ATT_THREADS = 512;
+constexpr int ATT_F4 = ATT_SEG * 32 / ATT_THREADS;  // float4 of one segment's K (or V) per thread
+constexpr int ATT_PART_STRIDE = 132;                // o_c[128], m_c, l_c, pad
+constexpr int ATT_MAX_GROUP = 16;
+bool attention_supported(int num_heads, int num_kv_heads, int head_dim);
 
-// Attention with head_dim 128 and at most 2 q-heads per kv head, one
-// workgroup per (kv head, query row).  Decode form: qkv_p holds the qkv
-// projection as qkv_g partials of stride qkv_stride; the kernel normalizes
-// and rotates q/k, appends k/v at the position and attends.  Prefill form:
-// q_rows holds normalized, rotated queries and the cache is filled.
-struct AttnGroupLaunch {
-    const float* qkv_p;
-    int qkv_g;
-    size_t qkv_stride;
-    const float* q_rows;
+// Decode: one workgroup per (kv head, segment); normalizes and rotates q/k
+// from the qkv projection, appends k/v at the position, and writes per
+// (segment, q head) partials part[(c * num_heads + h) * ATT_PART_STRIDE]
+// that the o-projection GEMV combines (XS_ATTN).
+struct AttnSegLaunch {
+    const float* qkv;      // [q_dim + 2 * kv_dim]
     const float* q_norm;
     const float* k_norm;
-    const float* cos_t;
+    const float* cos_t;    // [max_pos][64]
     const float* sin_t;
     float* k_cache;        // [kv_heads][max_pos][128] (this layer)
     float* v_cache;
-    float* out;            // [n][num_heads * 128]
+    float* part;           // [ceil(max_pos / ATT_SEG)][num_heads][ATT_PART_STRIDE]
     const int* d_pos;
-    int pos_base, n, num_heads, num_kv_heads, max_pos;
+    int pos_base, num_heads, num_kv_heads, max_pos;
     float eps, scale;
 };
-lq8_status launch_attention_group(hipStream_t s, const AttnGroupLaunch& a);
-bool attention_group_supported(int num_heads, int num_kv_heads, int head_dim, int max_pos);
+lq8_status launch_attention_seg(hipStream_t s, const AttnSegLaunch& a);
+
+// Prefill: one workgroup per (kv head, query row) over a filled cache.
+struct AttnRowsLaunch {
+    const float* q_rows;   // [n][num_heads * 128] normalized, rotated
+    const float* k_cache;
+    const float* v_cache;
+    float* out;            // [n][num_heads * 128]
+    int pos_base, n, num_heads, num_kv_heads, max_pos;
+    float scale;
+};
+lq8_status launch_attention_rows(hipStream_t s, const AttnRowsLaunch& a);
 
 lq8_status launch_rms_norm_rows(hipStream_t s, const float* x, const float* w, int rows, int dim, float eps, float* y);
 lq8_status launch_silu_mul(hipStream_t s, const float* gu, int rows, int inter, float* act);
 lq8_status launch_silu(hipStream_t s, const float* x, size_t n, float* y);
-// Argmax with last-index ties over logits[n]; writes tokens_out[*d_step] and
-// *d_tok, then advances *d_pos and *d_step (all device scalars).
-lq8_status launch_argmax_step(hipStream_t s, const float* logits, int n, uint32_t* d_tok, uint32_t* tokens_out,
-                              int* d_pos, int* d_step);
 
 // ---- allocation helpers ----------------------------------------------------
 lq8_status weight_alloc(lq8_ctx* ctx, size_t n_out, size_t k_in, lq8_weight** out);

@@ -4,9 +4,13 @@
 // Weights live once in HBM in the tiled Q8_0 layout.  q/k/v and gate/up are
 // stored as one concatenated weight each (rows are independent, so the
 // results are those of the separate projections).  Decode (one position)
-// runs 6 kernels per layer:
-//   rmsnorm+qkv GEMV | q/k-norm+RoPE+KV append | attention |
-//   o GEMV + residual | rmsnorm+gate/up GEMV | silu*up + down GEMV + residual
+// runs 5 kernels per layer, each output final when its kernel ends:
+//   RmsNorm + qkv GEMV
+//   attention per (kv head, 64-position segment): q/k RmsNorm, RoPE, KV append
+//   o GEMV on the combined segment partials, + residual
+//   RmsNorm + gate|up GEMV
+//   silu(gate) * up staged into the down GEMV, + residual
+// then RmsNorm + lm_head GEMV with per-tile argmax and one argmax kernel.
 // Prefill (n > 1 positions) quantizes activations and uses the MFMA GEMM.
 #include <cmath>
 #include <cstdlib>
@@ -31,6 +35,7 @@ struct lq8_model {
     lq8_ctx* ctx = nullptr;
     lq8_qwen3_config c{};
     size_t QD = 0, KD = 0, QKV = 0;
+    int cmax = 0;  // attention segments at max_positions
     lq8_weight* embed = nullptr;
     float* final_norm = nullptr;
     std::vector<Layer> layers;
@@ -38,10 +43,9 @@ struct lq8_model {
     float *kc = nullptr, *vc = nullptr;  // [layer][kv_head][pos][head_dim] each
     size_t kv_len = 0;
     // single-position buffers
-    float *h = nullptr, *qkv = nullptr, *qr = nullptr, *attn = nullptr, *gu = nullptr, *logits = nullptr;
-    float *h2 = nullptr, *tr = nullptr;  // second residual buffer; trace staging
-    float *qkv_p = nullptr, *o_p = nullptr, *gu_p = nullptr, *dn_p = nullptr;  // projection partials
-    bool grouped_attn = false;           // attention through launch_attention_group
+    float *h = nullptr, *h2 = nullptr, *qkv = nullptr, *gu = nullptr, *apart = nullptr, *logits = nullptr;
+    float* arg_val = nullptr;
+    int* arg_idx = nullptr;
     uint32_t* d_ids = nullptr;
     size_t ids_cap = 0;
     int *d_pos = nullptr, *d_step = nullptr;
@@ -66,10 +70,12 @@ lq8_status validate(const lq8_qwen3_config* c) {
     if (c->num_heads % c->num_kv_heads) return fail(LQ8_ERR_MODEL, "num_heads must be divisible by num_kv_heads");
     if (c->hidden_size % 32 || c->intermediate_size % 32)
         return fail(LQ8_ERR_MODEL, "hidden and intermediate sizes must be multiples of 32 (Q8_0 blocks)");
-    if (c->head_dim % 128 || c->head_dim > 512) return fail(LQ8_ERR_MODEL, "head_dim must be 128, 256 or 384/512");
+    if (!attention_supported((int)c->num_heads, (int)c->num_kv_heads, (int)c->head_dim))
+        return fail(LQ8_ERR_MODEL, "attention needs head_dim 128 and at most 16 query heads per kv head");
     if (c->max_positions > 8192) return fail(LQ8_ERR_MODEL, "max_positions > 8192 not supported");
-    if (c->hidden_size > 16384 || c->intermediate_size > 16384 || c->num_heads * c->head_dim > 16384)
-        return fail(LQ8_ERR_MODEL, "dimensions above 16384 not supported");
+    if (c->hidden_size > (uint32_t)GEMV_MAX_K || c->intermediate_size > (uint32_t)GEMV_MAX_K ||
+        c->num_heads * c->head_dim > (uint32_t)GEMV_MAX_K)
+        return fail(LQ8_ERR_MODEL, "dimensions above 12288 not supported");
     return LQ8_OK;
 }
 
@@ -94,8 +100,7 @@ void release(lq8_model* m) {
         F(L.in_norm); F(L.post_norm); F(L.q_norm); F(L.k_norm);
     }
     F(m->cos_t); F(m->sin_t); F(m->kc); F(m->vc);
-    F(m->h); F(m->qkv); F(m->qr); F(m->attn); F(m->gu); F(m->logits);
-    F(m->h2); F(m->tr); F(m->qkv_p); F(m->o_p); F(m->gu_p); F(m->dn_p);
+    F(m->h); F(m->h2); F(m->qkv); F(m->gu); F(m->apart); F(m->logits); F(m->arg_val); F(m->arg_idx);
     F(m->d_ids); F(m->d_pos); F(m->d_step); F(m->d_tok); F(m->d_tokens);
     F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_act); F(m->P_xs); F(m->P_xq);
     delete m;
@@ -109,6 +114,7 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_qwen3_config* c, lq8_model* m)
     m->QD = (size_t)c->num_heads * hd;
     m->KD = (size_t)c->num_kv_heads * hd;
     m->QKV = m->QD + 2 * m->KD;
+    m->cmax = (int)((P + ATT_SEG - 1) / ATT_SEG);
     lq8_status st;
     if ((st = weight_alloc(ctx, c->vocab_size, Hd, &m->embed))) return st;
     if ((st = dalloc(&m->final_norm, Hd))) return st;
@@ -129,8 +135,8 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_qwen3_config* c, lq8_model* m)
     for (size_t i = 0; i < half; i++) inv[i] = 1.0 / std::pow(c->rope_theta, (double)(2 * i) / (double)R);
     for (size_t p = 0; p < P; p++)
         for (size_t i = 0; i < half; i++) {
-            double f = (double)p * inv[i];
-            float cv = (float)std::cos(f), sv = (float)std::sin(f);
+            const double f = (double)p * inv[i];
+            const float cv = (float)std::cos(f), sv = (float)std::sin(f);
             ct[p * R + 2 * i] = ct[p * R + 2 * i + 1] = cv;
             stbl[p * R + 2 * i] = stbl[p * R + 2 * i + 1] = sv;
         }
@@ -141,19 +147,12 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_qwen3_config* c, lq8_model* m)
     if ((st = dalloc(&m->kc, kv)) || (st = dalloc(&m->vc, kv))) return st;
     LQ8_HIP(hipMemset(m->kc, 0, kv * sizeof(float)));
     LQ8_HIP(hipMemset(m->vc, 0, kv * sizeof(float)));
-    if ((st = dalloc(&m->h, Hd)) || (st = dalloc(&m->qkv, m->QKV)) || (st = dalloc(&m->qr, m->QD)) ||
-        (st = dalloc(&m->attn, m->QD)) || (st = dalloc(&m->gu, 2 * I)) || (st = dalloc(&m->logits, c->vocab_size)) ||
-        (st = dalloc(&m->d_pos, 1)) || (st = dalloc(&m->d_step, 1)) || (st = dalloc(&m->d_tok, 1)))
+    if ((st = dalloc(&m->h, Hd)) || (st = dalloc(&m->h2, Hd)) || (st = dalloc(&m->qkv, m->QKV)) ||
+        (st = dalloc(&m->gu, 2 * I)) || (st = dalloc(&m->apart, (size_t)m->cmax * c->num_heads * ATT_PART_STRIDE)) ||
+        (st = dalloc(&m->logits, c->vocab_size)) || (st = dalloc(&m->arg_val, m->embed->tiles)) ||
+        (st = dalloc(&m->arg_idx, m->embed->tiles)) || (st = dalloc(&m->d_pos, 1)) || (st = dalloc(&m->d_step, 1)) ||
+        (st = dalloc(&m->d_tok, 1)))
         return st;
-    {
-        const int Gh = gemv_groups((int)Hd), Gq = gemv_groups((int)m->QD), Gi = gemv_groups((int)I);
-        const size_t sQKV = gemv_partial_stride((int)m->QKV), sH = gemv_partial_stride((int)Hd);
-        const size_t sGU = gemv_partial_stride((int)(2 * I));
-        if ((st = dalloc(&m->h2, Hd)) || (st = dalloc(&m->tr, Hd)) || (st = dalloc(&m->qkv_p, Gh * sQKV)) ||
-            (st = dalloc(&m->o_p, Gq * sH)) || (st = dalloc(&m->gu_p, Gh * sGU)) || (st = dalloc(&m->dn_p, Gi * sH)))
-            return st;
-    }
-    m->grouped_attn = attention_group_supported((int)c->num_heads, (int)c->num_kv_heads, (int)hd, (int)P);
     LQ8_HIP(hipEventCreate(&m->e0));
     LQ8_HIP(hipEventCreate(&m->e1));
     LQ8_HIP(hipEventCreate(&m->e2));
@@ -183,7 +182,7 @@ TensorRef tensor_ref(lq8_model* m, size_t idx) {
     const size_t Hd = m->c.hidden_size, I = m->c.intermediate_size, hd = m->c.head_dim;
     if (idx == 0) { t.w = m->embed; t.rows = m->c.vocab_size; return t; }
     if (idx == 1) { t.norm = m->final_norm; t.norm_len = Hd; return t; }
-    size_t l = (idx - 2) / 11, k = (idx - 2) % 11;
+    const size_t l = (idx - 2) / 11, k = (idx - 2) % 11;
     Layer& L = m->layers[l];
     switch (k) {
         case 0: t.norm = L.in_norm; t.norm_len = Hd; break;
@@ -203,6 +202,7 @@ TensorRef tensor_ref(lq8_model* m, size_t idx) {
 
 lq8_status ensure_ids(lq8_model* m, size_t n) {
     if (n > m->ids_cap) {
+        LQ8_HIP(hipStreamSynchronize(m->ctx->stream));
         if (m->d_ids) LQ8_HIP(hipFree(m->d_ids));
         m->d_ids = nullptr;
         lq8_status st = dalloc(&m->d_ids, n);
@@ -221,133 +221,100 @@ lq8_status ensure_prefill(lq8_model* m, size_t n) {
     m->P_xq = nullptr;
     m->pf_cap = 0;
     const size_t Hd = m->c.hidden_size, I = m->c.intermediate_size;
-    const size_t kmax = std::max(Hd, std::max(m->QD, (size_t)I));
-    const size_t mt = (n + 63) / 64;
+    const int kmax = (int)std::max(Hd, std::max(m->QD, (size_t)I));
     lq8_status st;
     if ((st = dalloc(&m->P_h, n * Hd)) || (st = dalloc(&m->P_x, n * Hd)) || (st = dalloc(&m->P_qkv, n * m->QKV)) ||
         (st = dalloc(&m->P_qr, n * m->QD)) || (st = dalloc(&m->P_attn, n * m->QD)) ||
         (st = dalloc(&m->P_gu, n * 2 * I)) || (st = dalloc(&m->P_act, n * I)) ||
-        (st = dalloc(&m->P_xs, mt * (kmax / 32) * 64)) || (st = dalloc(&m->P_xq, mt * (kmax / 32) * 2048)))
+        (st = dalloc(&m->P_xs, act_scale_bytes((int)n, kmax) / sizeof(float))) ||
+        (st = dalloc(&m->P_xq, act_code_bytes((int)n, kmax))))
         return st;
     m->pf_cap = n;
     return LQ8_OK;
 }
 
-// One position through the decoder (src/model.rs:170-195 with L = 1) and the
-// lm_head GEMV; the token id comes from device memory.
-// trace (optional, host): [0] embedding output, [1 + l] output of layer l, all [n][hidden].
 lq8_status trace_copy(lq8_model* m, float* host, const float* dev, size_t count) {
     if (!host) return LQ8_OK;
     LQ8_HIP(hipMemcpyAsync(host, dev, count * sizeof(float), hipMemcpyDeviceToHost, m->ctx->stream));
     return LQ8_OK;
 }
 
-// Decode dataflow.  The projections write group partials (see gemv.hip)
-// that the next kernel folds in group order while staging its input; the
-// residual stream lives in two buffers used in turn, each combined value
-// (base + finished projection) stored once by the kernel that first needs it.
+GemvArgs gemv_args(const lq8_weight* w, const float* x, float* y) {
+    GemvArgs a{w->codes, w->scales, x, nullptr, y, nullptr, nullptr, nullptr, (int)w->n_out, (int)w->k_in, 0.0f};
+    return a;
+}
+
+// One position through the decoder (src/model.rs:170-195 with L = 1) and the
+// lm_head GEMV with per-tile argmax partials; the token id and the position
+// come from device memory (d_pos null: position pos_base).
+// trace (optional, host): [0] embedding output, [1 + l] output of layer l.
 lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, int pos_base, float* trace = nullptr,
                           float* final_hidden = nullptr) {
     hipStream_t s = m->ctx->stream;
     const lq8_qwen3_config& c = m->c;
-    const int Hd = (int)c.hidden_size, I = (int)c.intermediate_size;
+    const int Hd = (int)c.hidden_size;
     const size_t layer_kv = (size_t)c.num_kv_heads * c.head_dim * c.max_positions;
-    const int Gh = gemv_groups(Hd), Gq = gemv_groups((int)m->QD), Gi = gemv_groups(I);
-    const size_t sQKV = gemv_partial_stride((int)m->QKV), sH = gemv_partial_stride(Hd), sGU = gemv_partial_stride(2 * I);
     const float scale = 1.0f / std::sqrt((float)c.head_dim);
-    float* cur = m->h;
-    float* other = m->h2;
-    const float* pend = nullptr;  // down-projection partials not yet added to cur
-    int pend_g = 0;
     lq8_status st;
-    if ((st = launch_dequant_rows(s, m->embed, d_id, 0, 1, cur))) return st;
-    if ((st = trace_copy(m, trace, cur, Hd))) return st;
+    if ((st = launch_dequant_rows(s, m->embed, d_id, 0, 1, m->h))) return st;
+    if ((st = trace_copy(m, trace, m->h, Hd))) return st;
     for (size_t l = 0; l < m->layers.size(); l++) {
         Layer& L = m->layers[l];
-        // input_layernorm(h) -> q|k|v partials; h = cur + pending down projection
-        GemvLaunch g1{L.qkv->codes, L.qkv->scales, cur, L.in_norm, c.rms_norm_eps, nullptr, nullptr, (int)m->QKV, Hd};
-        g1.partials = m->qkv_p;
-        g1.partials_cap = (long long)(Gh * sQKV);
-        g1.xp = pend;
-        g1.xg = pend_g;
-        g1.xstride = sH;
-        g1.x_out = pend ? other : nullptr;
-        if ((st = launch_gemv(s, XS_RMSNORM, g1))) return st;
-        if (pend) {
-            std::swap(cur, other);
-            pend = nullptr;
-            pend_g = 0;
-        }
-        // attention (q/k norm, RoPE, KV append, scores, softmax, p.v)
-        if (m->grouped_attn) {
-            AttnGroupLaunch at{m->qkv_p, Gh, sQKV, nullptr, L.q_norm, L.k_norm, m->cos_t, m->sin_t,
-                               m->kc + l * layer_kv, m->vc + l * layer_kv, m->attn, d_pos, pos_base, 1,
-                               (int)c.num_heads, (int)c.num_kv_heads, (int)c.max_positions, c.rms_norm_eps, scale};
-            if ((st = launch_attention_group(s, at))) return st;
-        } else {
-            if ((st = launch_combine(s, nullptr, m->qkv_p, Gh, sQKV, (int)m->QKV, m->qkv))) return st;
-            QkRopeLaunch qr{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->qr, m->kc + l * layer_kv,
-                            m->vc + l * layer_kv, d_pos, pos_base, 1, (int)c.num_heads, (int)c.num_kv_heads,
-                            (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps};
-            if ((st = launch_qk_rope_kv(s, qr))) return st;
-            AttnLaunch at{m->qr, m->kc + l * layer_kv, m->vc + l * layer_kv, m->attn, d_pos, pos_base, 1,
-                          (int)c.num_heads, (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions, scale};
-            if ((st = launch_attention(s, at))) return st;
-        }
-        // o_proj -> partials
-        GemvLaunch g2{L.o->codes, L.o->scales, m->attn, nullptr, 0.0f, nullptr, nullptr, Hd, (int)m->QD};
-        g2.partials = m->o_p;
-        g2.partials_cap = (long long)(Gq * sH);
-        if ((st = launch_gemv(s, XS_PLAIN, g2))) return st;
-        // post_attention_layernorm(h + o) -> gate|up partials; h + o stored to other
-        GemvLaunch g3{L.gu->codes, L.gu->scales, cur, L.post_norm, c.rms_norm_eps, nullptr, nullptr, 2 * I, Hd};
-        g3.partials = m->gu_p;
-        g3.partials_cap = (long long)(Gh * sGU);
-        g3.xp = m->o_p;
-        g3.xg = Gq;
-        g3.xstride = sH;
-        g3.x_out = other;
-        if ((st = launch_gemv(s, XS_RMSNORM, g3))) return st;
-        std::swap(cur, other);
-        // down_proj(silu(gate) * up) -> partials, added by the next consumer
-        GemvLaunch g4{L.down->codes, L.down->scales, nullptr, nullptr, 0.0f, nullptr, nullptr, Hd, I};
-        g4.partials = m->dn_p;
-        g4.partials_cap = (long long)(Gi * sH);
-        g4.xp = m->gu_p;
-        g4.xg = Gh;
-        g4.xstride = sGU;
-        if ((st = launch_gemv(s, XS_SILU, g4))) return st;
-        pend = m->dn_p;
-        pend_g = Gi;
-        if (trace) {
-            if ((st = launch_combine(s, cur, pend, pend_g, sH, Hd, m->tr))) return st;
-            if ((st = trace_copy(m, trace + (l + 1) * Hd, m->tr, Hd))) return st;
-        }
+        // input_layernorm + q|k|v projection (src/transformer.rs:190; src/attention.rs:330-332)
+        GemvArgs g1 = gemv_args(L.qkv, m->h, m->qkv);
+        g1.norm_w = L.in_norm;
+        g1.eps = c.rms_norm_eps;
+        if ((st = launch_gemv(s, XS_RMSNORM, EPI_STORE, g1))) return st;
+        // q/k norm, RoPE, KV append, attention per segment (src/attention.rs:336-399)
+        AttnSegLaunch at{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->kc + l * layer_kv, m->vc + l * layer_kv,
+                         m->apart, d_pos, pos_base, (int)c.num_heads, (int)c.num_kv_heads, (int)c.max_positions,
+                         c.rms_norm_eps, scale};
+        if ((st = launch_attention_seg(s, at))) return st;
+        // o_proj on the combined attention output, + residual (src/transformer.rs:194)
+        GemvArgs g2 = gemv_args(L.o, m->apart, m->h2);
+        g2.resid = m->h;
+        g2.d_pos = d_pos;
+        g2.pos_base = pos_base;
+        g2.attn_heads = (int)c.num_heads;
+        g2.attn_cmax = m->cmax;
+        if ((st = launch_gemv(s, XS_ATTN, EPI_RESID, g2))) return st;
+        // post_attention_layernorm + gate|up (src/transformer.rs:197; src/mlp.rs:153,157)
+        GemvArgs g3 = gemv_args(L.gu, m->h2, m->gu);
+        g3.norm_w = L.post_norm;
+        g3.eps = c.rms_norm_eps;
+        if ((st = launch_gemv(s, XS_RMSNORM, EPI_STORE, g3))) return st;
+        // down(silu(gate) * up) + residual (src/mlp.rs:163; src/transformer.rs:203)
+        GemvArgs g4 = gemv_args(L.down, m->gu, m->h);
+        g4.resid = m->h2;
+        if ((st = launch_gemv(s, XS_SILU, EPI_RESID, g4))) return st;
+        if ((st = trace_copy(m, trace ? trace + (l + 1) * Hd : nullptr, m->h, Hd))) return st;
     }
-    if (final_hidden && (st = launch_combine(s, cur, pend, pend_g, sH, Hd, final_hidden))) return st;
-    // norm(h) -> lm_head logits
-    GemvLaunch g5{m->embed->codes, m->embed->scales, cur, m->final_norm, c.rms_norm_eps, m->logits, nullptr,
-                  (int)c.vocab_size, Hd};
-    g5.xp = pend;
-    g5.xg = pend_g;
-    g5.xstride = sH;
-    return launch_gemv(s, XS_RMSNORM, g5);
+    if (final_hidden)
+        LQ8_HIP(hipMemcpyAsync(final_hidden, m->h, Hd * sizeof(float), hipMemcpyDeviceToDevice, s));
+    // final norm -> lm_head logits + per-tile argmax (src/model.rs:357-371)
+    GemvArgs g5 = gemv_args(m->embed, m->h, m->logits);
+    g5.norm_w = m->final_norm;
+    g5.eps = c.rms_norm_eps;
+    g5.arg_val = m->arg_val;
+    g5.arg_idx = m->arg_idx;
+    return launch_gemv(s, XS_RMSNORM, EPI_ARGMAX, g5);
 }
 
 lq8_status quant_gemm(lq8_model* m, const float* x, int n, const lq8_weight* w, float* y, const float* resid) {
     hipStream_t s = m->ctx->stream;
     lq8_status st = launch_quantize_act(s, x, n, (int)w->k_in, m->P_xq, m->P_xs);
     if (st) return st;
-    return launch_gemm(s, m->P_xq, m->P_xs, n, w, y, resid, (int)w->n_out, 0);
+    return launch_gemm(s, m->P_xq, m->P_xs, n, w, y, resid);
 }
 
 // n positions starting at pos_base (src/model.rs:170-195), then the last
-// position's logits.
+// position's logits and per-tile argmax partials.
 lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base, float* trace = nullptr) {
     hipStream_t s = m->ctx->stream;
     const lq8_qwen3_config& c = m->c;
     const int Hd = (int)c.hidden_size, I = (int)c.intermediate_size;
     const size_t layer_kv = (size_t)c.num_kv_heads * c.head_dim * c.max_positions;
+    const float scale = 1.0f / std::sqrt((float)c.head_dim);
     lq8_status st;
     if ((st = launch_dequant_rows(s, m->embed, m->d_ids, 0, n, m->P_h))) return st;
     if ((st = trace_copy(m, trace, m->P_h, (size_t)n * Hd))) return st;
@@ -359,18 +326,9 @@ lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base, float* trace = nul
                         m->vc + l * layer_kv, nullptr, pos_base, n, (int)c.num_heads, (int)c.num_kv_heads,
                         (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps};
         if ((st = launch_qk_rope_kv(s, qr))) return st;
-        if (m->grouped_attn) {
-            AttnGroupLaunch at{nullptr, 0, 0, m->P_qr, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->kc + l * layer_kv,
-                               m->vc + l * layer_kv, m->P_attn, nullptr, pos_base, n, (int)c.num_heads,
-                               (int)c.num_kv_heads, (int)c.max_positions, c.rms_norm_eps,
-                               1.0f / std::sqrt((float)c.head_dim)};
-            if ((st = launch_attention_group(s, at))) return st;
-        } else {
-            AttnLaunch at{m->P_qr, m->kc + l * layer_kv, m->vc + l * layer_kv, m->P_attn, nullptr, pos_base, n,
-                          (int)c.num_heads, (int)c.num_kv_heads, (int)c.head_dim, (int)c.max_positions,
-                          1.0f / std::sqrt((float)c.head_dim)};
-            if ((st = launch_attention(s, at))) return st;
-        }
+        AttnRowsLaunch at{m->P_qr, m->kc + l * layer_kv, m->vc + l * layer_kv, m->P_attn, pos_base, n,
+                          (int)c.num_heads, (int)c.num_kv_heads, (int)c.max_positions, scale};
+        if ((st = launch_attention_rows(s, at))) return st;
         if ((st = quant_gemm(m, m->P_attn, n, L.o, m->P_h, m->P_h))) return st;
         if ((st = launch_rms_norm_rows(s, m->P_h, L.post_norm, n, Hd, c.rms_norm_eps, m->P_x))) return st;
         if ((st = quant_gemm(m, m->P_x, n, L.gu, m->P_gu, nullptr))) return st;
@@ -379,9 +337,17 @@ lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base, float* trace = nul
         if (trace && (st = trace_copy(m, trace + (l + 1) * (size_t)n * Hd, m->P_h, (size_t)n * Hd))) return st;
     }
     // final norm + lm_head on the last position only (src/model.rs:357-371)
-    GemvLaunch g{m->embed->codes, m->embed->scales, m->P_h + (size_t)(n - 1) * Hd, m->final_norm, c.rms_norm_eps,
-                 m->logits, nullptr, (int)c.vocab_size, Hd};
-    return launch_gemv(s, XS_RMSNORM, g);
+    GemvArgs g = gemv_args(m->embed, m->P_h + (size_t)(n - 1) * Hd, m->logits);
+    g.norm_w = m->final_norm;
+    g.eps = c.rms_norm_eps;
+    g.arg_val = m->arg_val;
+    g.arg_idx = m->arg_idx;
+    return launch_gemv(s, XS_RMSNORM, EPI_ARGMAX, g);
+}
+
+lq8_status launch_pick(lq8_model* m) {
+    return launch_argmax_final(m->ctx->stream, m->arg_val, m->arg_idx, (int)m->embed->tiles, m->d_tok, m->d_tokens,
+                               m->d_pos, m->d_step);
 }
 
 lq8_status capture_decode_graph(lq8_model* m) {
@@ -390,7 +356,7 @@ lq8_status capture_decode_graph(lq8_model* m) {
     hipGraph_t g = nullptr;
     LQ8_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
     lq8_status st = enqueue_decode(m, m->d_tok, m->d_pos, 0);
-    if (!st) st = launch_argmax_step(s, m->logits, (int)m->c.vocab_size, m->d_tok, m->d_tokens, m->d_pos, m->d_step);
+    if (!st) st = launch_pick(m);
     hipError_t e = hipStreamEndCapture(s, &g);
     if (st) {
         if (g) (void)hipGraphDestroy(g);
@@ -462,7 +428,7 @@ lq8_status lq8_model_create(lq8_ctx* ctx, const lq8_qwen3_config* cfg, const voi
         }
         hipError_t e = hipMemcpy(tmp, tensors[i], bytes, hipMemcpyHostToDevice);
         if (e != hipSuccess) { st = hip_fail(e, "tensor upload"); break; }
-        st = launch_repack_aos(ctx->stream, (const uint8_t*)tmp, t.rows, t.w->nb, t.row0, t.w);
+        st = launch_repack_aos(ctx->stream, (const uint8_t*)tmp, t.rows, t.row0, t.w);
         if (!st) {
             e = hipStreamSynchronize(ctx->stream);
             if (e != hipSuccess) st = hip_fail(e, "tensor repack");
@@ -572,8 +538,8 @@ lq8_status lq8_model_forward_with_intermediates(lq8_model* m, const uint32_t* id
     LQ8_HIP(hipMemcpyAsync(m->d_ids, ids, n * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     const float* last;
     if (n == 1) {
-        st = enqueue_decode(m, m->d_ids, nullptr, (int)offset, hidden, m->tr);
-        last = m->tr;
+        st = enqueue_decode(m, m->d_ids, nullptr, (int)offset, hidden, m->P_h);
+        last = m->P_h;
     } else {
         st = enqueue_prefill(m, (int)n, (int)offset, hidden);
         last = m->P_h;
@@ -622,17 +588,14 @@ lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_pr
     st = n_prompt == 1 ? enqueue_decode(m, m->d_ids, nullptr, 0) : enqueue_prefill(m, (int)n_prompt, 0);
     if (st) return st;
     // first token from the prefill logits; d_pos becomes n_prompt
-    if ((st = launch_argmax_step(s, m->logits, (int)m->c.vocab_size, m->d_tok, m->d_tokens, m->d_pos, m->d_step)))
-        return st;
+    if ((st = launch_pick(m))) return st;
     LQ8_HIP(hipEventRecord(m->e1, s));
     for (size_t t = 1; t < max_new; t++) {
         if (use_graph) {
             LQ8_HIP(hipGraphLaunch(m->graph, s));
         } else {
             if ((st = enqueue_decode(m, m->d_tok, m->d_pos, 0))) return st;
-            if ((st = launch_argmax_step(s, m->logits, (int)m->c.vocab_size, m->d_tok, m->d_tokens, m->d_pos,
-                                         m->d_step)))
-                return st;
+            if ((st = launch_pick(m))) return st;
         }
     }
     LQ8_HIP(hipEventRecord(m->e2, s));

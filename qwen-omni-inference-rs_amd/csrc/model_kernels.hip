@@ -6,7 +6,11 @@
 //           RMSNorm sum of squares and the softmax denominator.
 //   scores  q.k sequential over head_dim (src/tensor.rs:2846-2915), then
 //           times 1/sqrt(head_dim).
-//   p.v     sequential over positions for each output dimension.
+//   ATTN    positions in segments of 64: per segment m_c = max s, e = exp(s - m_c),
+//           l_c = SUM64(e), o_c = sum_j e_j v_j (j in order); then the running
+//           (m, num, den) update m' = max(m, m_c), a = exp(m - m'),
+//           b = exp(m_c - m'), num = num a + b o_c, den = den a + b l_c; the
+//           output is num / den.
 #include "lq8_internal.h"
 #include "lq8_numerics.h"
 
@@ -14,261 +18,283 @@ namespace lq8 {
 
 namespace {
 
+constexpr int SEG = ATT_SEG;
+constexpr int KPAD = 129;  // LDS row stride of staged keys (bank-conflict free scores)
+
+// LDS float offsets of the staged K/V rows (16-byte aligned for float4 stores)
+__host__ __device__ inline int seg_ks_off(int G) { return (G * 128 + 256 + G * SEG + 2 * G + 3) & ~3; }
+__host__ __device__ inline int rows_ks_off(int G) { return (G * 128 + G * SEG + 6 * G + 3) & ~3; }
+
 __device__ __forceinline__ float wave_sum64(float a) {
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) a = a + __shfl_xor(a, d, 64);
     return a;
 }
 
-// q/k RmsNorm per head (src/attention.rs:350-358), RoPE (src/rope.rs:270-297),
-// KV-cache append (src/attention.rs:507-559, without the re-copy).
-// grid (n, num_heads + num_kv_heads), block 64.
-__global__ __launch_bounds__(64) void k_qk_rope_kv(QkRopeLaunch a) {
-    const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-    const int hd = a.head_dim, R = hd / 2, per = hd / 64;
-    const int QD = a.num_heads * hd, KD = a.num_kv_heads * hd, row = QD + 2 * KD;
-    const int pos = (a.d_pos ? *a.d_pos : a.pos_base) + i;
-    const bool isq = h < a.num_heads;
-    const float* src = a.qkv + (size_t)i * row + (isq ? h * hd : QD + (h - a.num_heads) * hd);
-    const float* w = isq ? a.q_norm : a.k_norm;
-    float xb[8], y[8];
-    float acc = 0.0f;
-    for (int t = 0; t < per; t++) {
-        float v = bf16_round(src[lane + 64 * t]);
-        xb[t] = v;
-        acc = acc + v * v;
-    }
-    acc = wave_sum64(acc);
-    const float mean = __fdiv_rn(acc, (float)hd);
-    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(mean + a.eps));
-    for (int t = 0; t < per; t++) y[t] = bf16_round((xb[t] * inv) * bf16_round(w[lane + 64 * t]));
-    const float* cs = a.cos_t + (size_t)pos * R;
-    const float* sn = a.sin_t + (size_t)pos * R;
-    const int kvh = h - a.num_heads;
-    for (int t = 0; t < per / 2; t++) {
-        const int d = lane + 64 * t;
-        const float c = cs[d & ~1], s = sn[d & ~1];
-        const float x1 = y[t], x2 = y[t + per / 2];
-        const float o1 = x1 * c - x2 * s;
-        const float o2 = x2 * c + x1 * s;
-        if (isq) {
-            float* q = a.q_out + (size_t)i * QD + h * hd;
-            q[d] = o1;
-            q[d + R] = o2;
-        } else {
-            float* kr = a.k_cache + ((size_t)kvh * a.max_pos + pos) * hd;
-            kr[d] = o1;
-            kr[d + R] = o2;
-        }
-    }
-    if (!isq) {
-        const float* v = a.qkv + (size_t)i * row + QD + KD + kvh * hd;
-        float* vc = a.v_cache + ((size_t)kvh * a.max_pos + pos) * hd;
-        for (int t = 0; t < per; t++) vc[lane + 64 * t] = v[lane + 64 * t];
-    }
-}
-
-// One (q head, query row) per workgroup: scores, softmax, p.v
-// (src/attention.rs:366-394).  GQA maps q head h to kv head h / groups
-// (repeat_kv order, src/attention.rs:442-452).  Query i sees positions
-// 0..pos_i (the causal mask of src/causal_mask.rs:128-148; masked terms are
-// exact zeros of the softmax and are skipped).
-__global__ __launch_bounds__(256) void k_attention(AttnLaunch a) {
-    extern __shared__ float sm[];
-    const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int hd = a.head_dim, P = a.max_pos;
-    const int QD = a.num_heads * hd;
-    const int kvh = h / (a.num_heads / a.num_kv_heads);
-    const int L = (a.d_pos ? *a.d_pos : a.pos_base) + i + 1;
-    float* q = sm;
-    float* red = sm + hd;
-    float* sc = red + 8;
-    for (int d = tid; d < hd; d += 256) q[d] = a.q[(size_t)i * QD + h * hd + d];
-    __syncthreads();
-    const float* K = a.k_cache + (size_t)kvh * P * hd;
-    float lmax = -__builtin_huge_valf();
-    for (int j = tid; j < L; j += 256) {
-        float s = 0.0f;
-        for (int d = 0; d < hd; d++) s = s + q[d] * K[(size_t)j * hd + d];
-        s = s * a.scale;
-        sc[j] = s;
-        lmax = s > lmax ? s : lmax;
-    }
+__device__ __forceinline__ float wave_max64(float a) {
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
-        float o = __shfl_xor(lmax, d, 64);
-        lmax = o > lmax ? o : lmax;
+        const float o = __shfl_xor(a, d, 64);
+        a = o > a ? o : a;
     }
-    if (lane == 0) red[wave] = lmax;
-    __syncthreads();
-    float mx = red[0];
-    for (int w = 1; w < 4; w++) mx = red[w] > mx ? red[w] : mx;
-    for (int j = tid; j < L; j += 256) sc[j] = expf_cr(sc[j] - mx);
-    __syncthreads();
-    if (wave == 0) {
-        float acc = 0.0f;
-        for (int j = lane; j < L; j += 64) acc = acc + sc[j];
-        acc = wave_sum64(acc);
-        if (lane == 0) red[4] = acc;
-    }
-    __syncthreads();
-    const float sum = red[4];
-    for (int j = tid; j < L; j += 256) sc[j] = __fdiv_rn(sc[j], sum);
-    __syncthreads();
-    const float* V = a.v_cache + (size_t)kvh * P * hd;
-    for (int d = tid; d < hd; d += 256) {
-        // PV4 order: chunk c of 64 positions belongs to set c % 4; sets sum
-        // their positions in order, then ((A0 + A1) + A2) + A3.
-        float s4[4];
-        for (int st = 0; st < 4; st++) {
-            float o = 0.0f;
-            for (int j0 = st * 64; j0 < L; j0 += 256) {
-                const int je = min(j0 + 64, L);
-                for (int j = j0; j < je; j++) o = o + sc[j] * V[(size_t)j * hd + d];
-            }
-            s4[st] = o;
-        }
-        a.out[(size_t)i * QD + h * hd + d] = ((s4[0] + s4[1]) + s4[2]) + s4[3];
-    }
+    return a;
 }
 
-
-// ---- attention, one workgroup per (kv group, query) -------------------------
-
-// RmsNorm per head then RoPE of one head vector held by one wave (lane l has
-// elements l and l + 64), exactly as k_qk_rope_kv; src holds the projection
-// as (base +) partials.
-__device__ __forceinline__ void head_norm_rope(const float* src_p, int g_count, size_t stride, const float* w,
-                                               const float* cs, const float* sn, float eps, float* dst) {
+// RmsNorm of one head vector (src/attention.rs:350-358 with src/rms_norm.rs:143-176)
+// then RoPE (src/rope.rs:270-297) at table row cs/sn; one wave, lane l has
+// elements l and l + 64 (head_dim 128).
+__device__ __forceinline__ void head_norm_rope(const float* src, const float* w, const float* cs, const float* sn,
+                                               float eps, float* dst) {
     const int lane = threadIdx.x & 63;
-    float xb[2];
+    // all loads first, then the arithmetic
+    const float s0 = src[lane], s1 = src[lane + 64];
+    const float w0 = w[lane], w1 = w[lane + 64];
+    const float c = cs[lane & ~1], s = sn[lane & ~1];
+    const float x0 = bf16_round(s0), x1 = bf16_round(s1);
     float acc = 0.0f;
-    for (int t = 0; t < 2; t++) {
-        float s = 0.0f;
-        for (int g = 0; g < g_count; g++) s = s + src_p[(size_t)g * stride + lane + 64 * t];
-        float v = bf16_round(s);
-        xb[t] = v;
-        acc = acc + v * v;
-    }
+    acc = acc + x0 * x0;
+    acc = acc + x1 * x1;
     acc = wave_sum64(acc);
     const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, 128.0f) + eps));
-    const float y0 = bf16_round((xb[0] * inv) * bf16_round(w[lane]));
-    const float y1 = bf16_round((xb[1] * inv) * bf16_round(w[lane + 64]));
-    const float c = cs[lane & ~1], s = sn[lane & ~1];
+    const float y0 = bf16_round((x0 * inv) * bf16_round(w0));
+    const float y1 = bf16_round((x1 * inv) * bf16_round(w1));
     dst[lane] = y0 * c - y1 * s;
     dst[lane + 64] = y1 * c + y0 * s;
 }
 
-// grid (num_kv_heads, n), block G * 512 (G = q-heads per kv head, head_dim 128).
-// Decode (qkv_p set): the query heads and the new key come from the qkv
-// projection partials; the new key and value are appended to the cache and
-// used from LDS.  Prefill (q_rows set): normalized, rotated queries and a
-// filled cache.  Then scores (q.k sequential over d, times scale), softmax
-// (max, exp, SUM64, divide) and p.v in the PV4 order: thread group st of four
-// accumulates the positions of chunks st, st + 4, ... in order, and the four
-// partial sums are added in order.
-__global__ __launch_bounds__(1024) void k_attn_group(AttnGroupLaunch a) {
+// q/k RmsNorm per head, RoPE and KV-cache append for n rows (prefill).
+// grid (n, num_heads + num_kv_heads), block 64.
+__global__ __launch_bounds__(64) void k_qk_rope_kv(QkRopeLaunch a) {
+    const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int QD = a.num_heads * 128, KD = a.num_kv_heads * 128, row = QD + 2 * KD;
+    const int pos = (a.d_pos ? *a.d_pos : a.pos_base) + i;
+    const bool isq = h < a.num_heads;
+    const float* src = a.qkv + (size_t)i * row + (isq ? h * 128 : QD + (h - a.num_heads) * 128);
+    const float* cs = a.cos_t + (size_t)pos * 64;
+    const float* sn = a.sin_t + (size_t)pos * 64;
+    if (isq) {
+        head_norm_rope(src, a.q_norm, cs, sn, a.eps, a.q_out + (size_t)i * QD + h * 128);
+    } else {
+        const int kvh = h - a.num_heads;
+        head_norm_rope(src, a.k_norm, cs, sn, a.eps, a.k_cache + ((size_t)kvh * a.max_pos + pos) * 128);
+        const float* v = a.qkv + (size_t)i * row + QD + KD + kvh * 128;
+        float* vc = a.v_cache + ((size_t)kvh * a.max_pos + pos) * 128;
+        vc[lane] = v[lane];
+        vc[lane + 64] = v[lane + 64];
+    }
+}
+
+// Shared per-segment work of the attention kernels (block ATT_THREADS).
+// Stages the keys of positions [js, js + nj) into ks (row `knew_row` of the
+// segment, if >= 0, from knew), computes the scores of the G query heads in
+// qs into sc[h][j], then per head m_c, e_j (into sc) and l_c (mlc[2h], mlc[2h+1]).
+// kreg/vreg: this thread's prefetched float4s of the segment's K and V rows.
+// The loads are unconditional (rows past the segment read row js instead) so
+// they are all in flight together; the values of those rows, and of the new
+// position's row (written by this kernel), are never used.
+__device__ __forceinline__ void seg_load(const float* __restrict__ Kc, const float* __restrict__ Vc, int js, int nj,
+                                         float4* kreg, float4* vreg) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < ATT_F4; u++) {
+        const int f = tid + u * ATT_THREADS;  // float4 index in the [64][32] segment
+        const int j = f >> 5, c4 = f & 31;
+        const size_t row = (size_t)js + (j < nj ? j : 0);
+        kreg[u] = *(const float4*)(Kc + row * 128 + c4 * 4);
+        vreg[u] = *(const float4*)(Vc + row * 128 + c4 * 4);
+    }
+}
+
+__device__ __forceinline__ void seg_scores(const float4* kreg, int nj, int knew_row, const float* knew, const float* qs,
+                                           int G, float scale, float* ks, float* sc, float* mlc) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+#pragma unroll
+    for (int u = 0; u < ATT_F4; u++) {
+        const int f = tid + u * ATT_THREADS;
+        const int j = f >> 5, c4 = f & 31;
+        if (j < nj) {
+            float4 v = kreg[u];
+            if (j == knew_row) v = *(const float4*)(knew + c4 * 4);
+            float* dst = ks + j * KPAD + c4 * 4;
+            dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+        }
+    }
+    __syncthreads();
+    for (int t = tid; t < G * SEG; t += ATT_THREADS) {
+        const int h = t / SEG, j = t % SEG;
+        if (j < nj) {
+            const float* q = qs + h * 128;
+            const float* kr = ks + j * KPAD;
+            float s = 0.0f;
+            for (int d = 0; d < 128; d++) s = s + q[d] * kr[d];
+            sc[h * SEG + j] = s * scale;
+        }
+    }
+    __syncthreads();
+    for (int h = wave; h < G; h += ATT_THREADS / 64) {
+        const float s = lane < nj ? sc[h * SEG + lane] : -__builtin_huge_valf();
+        const float mc = wave_max64(s);
+        const float e = lane < nj ? expf_cr(s - mc) : 0.0f;
+        const float lc = wave_sum64(e);
+        if (lane < nj) sc[h * SEG + lane] = e;
+        if (lane == 0) {
+            mlc[2 * h] = mc;
+            mlc[2 * h + 1] = lc;
+        }
+    }
+}
+
+// V rows of the segment into vs [64][128] (row vnew_row from vnew).
+__device__ __forceinline__ void seg_stage_v(const float4* vreg, int nj, int vnew_row, const float* vnew, float* vs) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < ATT_F4; u++) {
+        const int f = tid + u * ATT_THREADS;
+        const int j = f >> 5, c4 = f & 31;
+        if (j < nj) {
+            float4 v = vreg[u];
+            if (j == vnew_row) v = *(const float4*)(vnew + c4 * 4);
+            *(float4*)(vs + j * 128 + c4 * 4) = v;
+        }
+    }
+}
+
+// Decode attention, one workgroup per (kv head, segment of 64 positions).
+// Every workgroup normalizes and rotates its G query heads; the workgroup of
+// the last segment also normalizes and rotates the new key, appends key and
+// value at the position and uses them from LDS.  Output: per (segment, q
+// head) o_c[128], m_c, l_c at part[(c * H + h) * ATT_PART_STRIDE].
+__global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
+    extern __shared__ float sm[];
+    const int kvh = blockIdx.x, c = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.num_heads / a.num_kv_heads;
+    const int pos = a.d_pos ? *a.d_pos : a.pos_base;
+    const int L = pos + 1;
+    const int C = (L + SEG - 1) / SEG;
+    if (c >= C) return;  // before any barrier: the whole workgroup leaves
+    const int js = c * SEG, nj = min(SEG, L - js);
+    const bool last = c == C - 1;
+    const int newrow = last ? pos - js : -1;
+    const int QD = a.num_heads * 128, KD = a.num_kv_heads * 128;
+    const float* Kc = a.k_cache + (size_t)kvh * a.max_pos * 128;
+    const float* Vc = a.v_cache + (size_t)kvh * a.max_pos * 128;
+    float* qs = sm;                      // [G][128]
+    float* kn = qs + G * 128;            // [128]
+    float* vn = kn + 128;                // [128]
+    float* sc = vn + 128;                // [G][64]
+    float* mlc = sc + G * SEG;           // [G][2]
+    float* ks = sm + seg_ks_off(G);      // [64][KPAD], later vs [64][128]
+    float4 kreg[ATT_F4], vreg[ATT_F4];
+    seg_load(Kc, Vc, js, nj, kreg, vreg);
+    const float* cs = a.cos_t + (size_t)pos * 64;
+    const float* sn = a.sin_t + (size_t)pos * 64;
+    for (int t = wave; t < G + 2; t += ATT_THREADS / 64) {
+        if (t < G) {
+            head_norm_rope(a.qkv + (kvh * G + t) * 128, a.q_norm, cs, sn, a.eps, qs + t * 128);
+        } else if (t == G && last) {
+            head_norm_rope(a.qkv + QD + kvh * 128, a.k_norm, cs, sn, a.eps, kn);
+            const int lane = tid & 63;
+            float* kr = a.k_cache + ((size_t)kvh * a.max_pos + pos) * 128;
+            kr[lane] = kn[lane];
+            kr[lane + 64] = kn[lane + 64];
+        } else if (t == G + 1 && last) {
+            const int lane = tid & 63;
+            const float* v = a.qkv + QD + KD + kvh * 128;
+            float* vr = a.v_cache + ((size_t)kvh * a.max_pos + pos) * 128;
+            const float v0 = v[lane], v1 = v[lane + 64];
+            vn[lane] = v0;
+            vn[lane + 64] = v1;
+            vr[lane] = v0;
+            vr[lane + 64] = v1;
+        }
+    }
+    __syncthreads();
+    seg_scores(kreg, nj, newrow, kn, qs, G, a.scale, ks, sc, mlc);
+    __syncthreads();
+    seg_stage_v(vreg, nj, newrow, vn, ks);
+    __syncthreads();
+    for (int t = tid; t < G * 128; t += ATT_THREADS) {
+        const int h = t >> 7, d = t & 127;
+        const float* e = sc + h * SEG;
+        float o = 0.0f;
+        for (int j = 0; j < nj; j++) o = o + e[j] * ks[j * 128 + d];
+        float* p = a.part + ((size_t)c * a.num_heads + kvh * G + h) * ATT_PART_STRIDE;
+        p[d] = o;
+        if (d == 0) {
+            p[128] = mlc[2 * h];
+            p[129] = mlc[2 * h + 1];
+        }
+    }
+}
+
+// Attention over n query rows with a filled cache (prefill), one workgroup
+// per (kv head, row); the segments run in order with the running update.
+__global__ __launch_bounds__(ATT_THREADS) void k_attn_rows(AttnRowsLaunch a) {
     extern __shared__ float sm[];
     const int kvh = blockIdx.x, i = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int G = a.num_heads / a.num_kv_heads, T = G * 512, P = a.max_pos;
-    const int QD = a.num_heads * 128, KD = a.num_kv_heads * 128;
-    const int pos = (a.d_pos ? *a.d_pos : a.pos_base) + i;
+    const int tid = threadIdx.x;
+    const int G = a.num_heads / a.num_kv_heads;
+    const int QD = a.num_heads * 128;
+    const int pos = a.pos_base + i;
     const int L = pos + 1;
-    float* qs = sm;                  // [G][128]
-    float* kn = qs + G * 128;        // [128] new key
-    float* vn = kn + 128;            // [128] new value
-    float* pr = vn + 128;            // [G][P] scores, then probabilities
-    float* part = pr + G * P;        // [4][G * 128]
-    const bool fused = a.qkv_p != nullptr;
-    if (fused) {
-        const float* cs = a.cos_t + (size_t)pos * 64;
-        const float* sn = a.sin_t + (size_t)pos * 64;
-        if (wave < G) {
-            head_norm_rope(a.qkv_p + (kvh * G + wave) * 128, a.qkv_g, a.qkv_stride, a.q_norm, cs, sn, a.eps,
-                           qs + wave * 128);
-        } else if (wave == G) {
-            head_norm_rope(a.qkv_p + QD + kvh * 128, a.qkv_g, a.qkv_stride, a.k_norm, cs, sn, a.eps, kn);
-            float* krow = a.k_cache + ((size_t)kvh * P + pos) * 128;
-            krow[lane] = kn[lane];
-            krow[lane + 64] = kn[lane + 64];
-        } else if (wave == G + 1) {
-            float* vrow = a.v_cache + ((size_t)kvh * P + pos) * 128;
-            for (int t = 0; t < 2; t++) {
-                float s = 0.0f;
-                for (int g = 0; g < a.qkv_g; g++) s = s + a.qkv_p[(size_t)g * a.qkv_stride + QD + KD + kvh * 128 + lane + 64 * t];
-                vn[lane + 64 * t] = s;
-                vrow[lane + 64 * t] = s;
-            }
-        }
-    } else {
-        for (int e = tid; e < G * 128; e += T) qs[e] = a.q_rows[(size_t)i * QD + kvh * G * 128 + e];
+    const float* Kc = a.k_cache + (size_t)kvh * a.max_pos * 128;
+    const float* Vc = a.v_cache + (size_t)kvh * a.max_pos * 128;
+    float* qs = sm;                      // [G][128]
+    float* sc = qs + G * 128;            // [G][64]
+    float* mlc = sc + G * SEG;           // [G][2]
+    float* run = mlc + 2 * G;            // [G][4]: m, den, a, b
+    float* ks = sm + rows_ks_off(G);     // [64][KPAD], later vs [64][128]
+    for (int e = tid; e < G * 128; e += ATT_THREADS) qs[e] = a.q_rows[(size_t)i * QD + kvh * G * 128 + e];
+    for (int h = tid; h < G; h += ATT_THREADS) {
+        run[4 * h] = -__builtin_huge_valf();
+        run[4 * h + 1] = 0.0f;
     }
-    __syncthreads();
-    // scores
-    const float* K = a.k_cache + (size_t)kvh * P * 128;
-    for (int j = tid; j < L; j += T) {
-        float s[8];
-        for (int h = 0; h < G; h++) s[h] = 0.0f;
-        if (fused && j == pos) {
-            for (int d = 0; d < 128; d++)
-                for (int h = 0; h < G; h++) s[h] = s[h] + qs[h * 128 + d] * kn[d];
-        } else {
-            const float4* kr = (const float4*)(K + (size_t)j * 128);
-            for (int t = 0; t < 32; t++) {
-                const float4 k4 = kr[t];
-                for (int h = 0; h < G; h++) {
-                    const float* q = qs + h * 128 + 4 * t;
-                    s[h] = s[h] + q[0] * k4.x;
-                    s[h] = s[h] + q[1] * k4.y;
-                    s[h] = s[h] + q[2] * k4.z;
-                    s[h] = s[h] + q[3] * k4.w;
-                }
-            }
-        }
-        for (int h = 0; h < G; h++) pr[h * P + j] = s[h] * a.scale;
-    }
-    __syncthreads();
-    // softmax per q-head, one wave each
-    if (wave < G) {
-        float* p = pr + wave * P;
-        float mx = -__builtin_huge_valf();
-        for (int j = lane; j < L; j += 64) mx = p[j] > mx ? p[j] : mx;
+    // thread t < G * 128 (looping) keeps num for (h, d) = (t / 128, t % 128)
+    constexpr int MAXR = 16 * 128 / ATT_THREADS;
+    float num[MAXR];
 #pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) {
-            float o = __shfl_xor(mx, d, 64);
-            mx = o > mx ? o : mx;
+    for (int r = 0; r < MAXR; r++) num[r] = 0.0f;
+    float4 kreg[ATT_F4], vreg[ATT_F4];
+    for (int js = 0; js < L; js += SEG) {
+        const int nj = min(SEG, L - js);
+        seg_load(Kc, Vc, js, nj, kreg, vreg);
+        __syncthreads();
+        seg_scores(kreg, nj, -1, nullptr, qs, G, a.scale, ks, sc, mlc);
+        __syncthreads();
+        for (int h = tid; h < G; h += ATT_THREADS) {
+            const float m = run[4 * h], mc = mlc[2 * h];
+            const float mn = m > mc ? m : mc;
+            const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
+            run[4 * h] = mn;
+            run[4 * h + 1] = run[4 * h + 1] * ea + eb * mlc[2 * h + 1];
+            run[4 * h + 2] = ea;
+            run[4 * h + 3] = eb;
         }
-        float acc = 0.0f;
-        for (int j = lane; j < L; j += 64) {
-            float e = expf_cr(p[j] - mx);
-            p[j] = e;
-            acc = acc + e;
-        }
-        acc = wave_sum64(acc);
-        for (int j = lane; j < L; j += 64) p[j] = __fdiv_rn(p[j], acc);
-    }
-    __syncthreads();
-    // p.v, PV4 order
-    {
-        const int st = tid / (G * 128), r = tid % (G * 128), hq = r / 128, d = r % 128;
-        const float* V = a.v_cache + (size_t)kvh * P * 128;
-        const float* p = pr + hq * P;
-        float o = 0.0f;
-        for (int j0 = st * 64; j0 < L; j0 += 256) {
-            const int je = min(j0 + 64, L);
-            for (int j = j0; j < je; j++) {
-                const float v = (fused && j == pos) ? vn[d] : V[(size_t)j * 128 + d];
-                o = o + p[j] * v;
+        seg_stage_v(vreg, nj, -1, nullptr, ks);
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < MAXR; r++) {
+            const int t = tid + r * ATT_THREADS;
+            if (t < G * 128) {
+                const int h = t >> 7, d = t & 127;
+                const float* e = sc + h * SEG;
+                float o = 0.0f;
+                for (int j = 0; j < nj; j++) o = o + e[j] * ks[j * 128 + d];
+                num[r] = num[r] * run[4 * h + 2] + run[4 * h + 3] * o;
             }
         }
-        part[st * G * 128 + r] = o;
     }
     __syncthreads();
-    for (int r = tid; r < G * 128; r += T) {
-        const float o = ((part[r] + part[G * 128 + r]) + part[2 * G * 128 + r]) + part[3 * G * 128 + r];
-        a.out[(size_t)i * QD + kvh * G * 128 + r] = o;
+#pragma unroll
+    for (int r = 0; r < MAXR; r++) {
+        const int t = tid + r * ATT_THREADS;
+        if (t < G * 128) {
+            const int h = t >> 7, d = t & 127;
+            a.out[(size_t)i * QD + (kvh * G + h) * 128 + d] = __fdiv_rn(num[r], run[4 * h + 1]);
+        }
     }
 }
 
@@ -279,7 +305,7 @@ __global__ __launch_bounds__(64) void k_rms_norm_rows(const float* __restrict__ 
     const float* xr = x + (size_t)r * dim;
     float acc = 0.0f;
     for (int i = lane; i < dim; i += 64) {
-        float v = bf16_round(xr[i]);
+        const float v = bf16_round(xr[i]);
         acc = acc + v * v;
     }
     acc = wave_sum64(acc);
@@ -291,88 +317,59 @@ __global__ __launch_bounds__(64) void k_rms_norm_rows(const float* __restrict__ 
 
 // act = silu(gate) * up (src/mlp.rs:151-164; silu src/tensor.rs:1978).
 __global__ void k_silu_mul(const float* __restrict__ gu, int rows, int inter, float* __restrict__ act) {
-    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (size_t)rows * inter) return;
-    size_t r = idx / inter, j = idx % inter;
-    float g = gu[r * 2 * inter + j], u = gu[r * 2 * inter + inter + j];
-    float s = __fdiv_rn(g, 1.0f + expf_cr(-g));
+    const size_t r = idx / inter, j = idx % inter;
+    const float g = gu[r * 2 * inter + j], u = gu[r * 2 * inter + inter + j];
+    const float s = __fdiv_rn(g, 1.0f + expf_cr(-g));
     act[idx] = s * u;
 }
 
 // Tensor::silu f32 branch (src/tensor.rs:1978): x / (1 + exp(-x)).
 __global__ void k_silu(const float* __restrict__ x, size_t n, float* __restrict__ y) {
-    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= n) return;
-    float v = x[idx];
+    const float v = x[idx];
     y[idx] = __fdiv_rn(v, 1.0f + expf_cr(-v));
-}
-
-// Greedy pick (src/generate.rs:153-174): maximum, last index on ties.
-__global__ __launch_bounds__(1024) void k_argmax_step(const float* __restrict__ logits, int n, uint32_t* d_tok,
-                                                      uint32_t* tokens_out, int* d_pos, int* d_step) {
-    __shared__ float sv[16];
-    __shared__ int si[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float bv = -__builtin_huge_valf();
-    int bi = -1;
-    for (int i = tid; i < n; i += 1024) {
-        float v = logits[i];
-        if (v > bv || v == bv) { bv = v; bi = i; }
-    }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        float ov = __shfl_xor(bv, d, 64);
-        int oi = __shfl_xor(bi, d, 64);
-        if (ov > bv || (ov == bv && oi > bi)) { bv = ov; bi = oi; }
-    }
-    if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
-    __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < 16; w++)
-            if (sv[w] > bv || (sv[w] == bv && si[w] > bi)) { bv = sv[w]; bi = si[w]; }
-        uint32_t tok = (uint32_t)(bi < 0 ? 0 : bi);
-        *d_tok = tok;
-        tokens_out[*d_step] = tok;
-        *d_step = *d_step + 1;
-        *d_pos = *d_pos + 1;
-    }
 }
 
 inline unsigned grid1(size_t n, unsigned block) { return (unsigned)((n + block - 1) / block); }
 
+size_t seg_smem(int G) { return ((size_t)seg_ks_off(G) + (size_t)SEG * KPAD) * sizeof(float); }
+size_t rows_smem(int G) { return ((size_t)rows_ks_off(G) + (size_t)SEG * KPAD) * sizeof(float); }
+
 }  // namespace
 
+bool attention_supported(int num_heads, int num_kv_heads, int head_dim) {
+    return head_dim == 128 && num_kv_heads > 0 && num_heads % num_kv_heads == 0 &&
+           num_heads / num_kv_heads <= ATT_MAX_GROUP;
+}
+
 lq8_status launch_qk_rope_kv(hipStream_t s, const QkRopeLaunch& a) {
-    if (a.head_dim % 128 || a.head_dim > 512)
-        return fail(LQ8_ERR_SHAPE_MISMATCH, "head_dim must be a multiple of 128 and at most 512");
-    dim3 grid((unsigned)a.n, (unsigned)(a.num_heads + a.num_kv_heads));
+    if (a.head_dim != 128) return fail(LQ8_ERR_SHAPE_MISMATCH, "head_dim must be 128");
+    const dim3 grid((unsigned)a.n, (unsigned)(a.num_heads + a.num_kv_heads));
     hipLaunchKernelGGL(k_qk_rope_kv, grid, dim3(64), 0, s, a);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
 
-lq8_status launch_attention(hipStream_t s, const AttnLaunch& a) {
-    size_t smem = ((size_t)a.head_dim + 8 + (size_t)a.max_pos) * sizeof(float);
-    dim3 grid((unsigned)a.num_heads, (unsigned)a.n);
-    hipLaunchKernelGGL(k_attention, grid, dim3(256), smem, s, a);
+lq8_status launch_attention_seg(hipStream_t s, const AttnSegLaunch& a) {
+    if (!attention_supported(a.num_heads, a.num_kv_heads, 128))
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "attention: unsupported head layout");
+    const int G = a.num_heads / a.num_kv_heads;
+    const int cmax = (a.max_pos + SEG - 1) / SEG;
+    hipLaunchKernelGGL(k_attn_seg, dim3((unsigned)a.num_kv_heads, (unsigned)cmax), dim3(ATT_THREADS), seg_smem(G), s,
+                       a);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
 
-
-bool attention_group_supported(int num_heads, int num_kv_heads, int head_dim, int max_pos) {
-    if (head_dim != 128 || num_heads % num_kv_heads) return false;
-    const long long G = num_heads / num_kv_heads;
-    const long long lds = (G * 128 + 256 + G * max_pos + 4 * G * 128) * 4;
-    return G >= 1 && G <= 2 && lds <= 64 * 1024;
-}
-
-lq8_status launch_attention_group(hipStream_t s, const AttnGroupLaunch& a) {
-    if (!attention_group_supported(a.num_heads, a.num_kv_heads, 128, a.max_pos))
-        return fail(LQ8_ERR_SHAPE_MISMATCH, "grouped attention: unsupported head layout");
+lq8_status launch_attention_rows(hipStream_t s, const AttnRowsLaunch& a) {
+    if (!attention_supported(a.num_heads, a.num_kv_heads, 128))
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "attention: unsupported head layout");
     const int G = a.num_heads / a.num_kv_heads;
-    size_t smem = ((size_t)G * 128 + 256 + (size_t)G * a.max_pos + 4 * (size_t)G * 128) * sizeof(float);
-    hipLaunchKernelGGL(k_attn_group, dim3((unsigned)a.num_kv_heads, (unsigned)a.n), dim3(G * 512), smem, s, a);
+    hipLaunchKernelGGL(k_attn_rows, dim3((unsigned)a.num_kv_heads, (unsigned)a.n), dim3(ATT_THREADS), rows_smem(G), s,
+                       a);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
@@ -384,7 +381,8 @@ lq8_status launch_rms_norm_rows(hipStream_t s, const float* x, const float* w, i
 }
 
 lq8_status launch_silu_mul(hipStream_t s, const float* gu, int rows, int inter, float* act) {
-    size_t n = (size_t)rows * inter;
+    const size_t n = (size_t)rows * inter;
+    if (!n) return LQ8_OK;
     hipLaunchKernelGGL(k_silu_mul, dim3(grid1(n, 256)), dim3(256), 0, s, gu, rows, inter, act);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
@@ -393,13 +391,6 @@ lq8_status launch_silu_mul(hipStream_t s, const float* gu, int rows, int inter, 
 lq8_status launch_silu(hipStream_t s, const float* x, size_t n, float* y) {
     if (!n) return LQ8_OK;
     hipLaunchKernelGGL(k_silu, dim3(grid1(n, 256)), dim3(256), 0, s, x, n, y);
-    LQ8_HIP(hipGetLastError());
-    return LQ8_OK;
-}
-
-lq8_status launch_argmax_step(hipStream_t s, const float* logits, int n, uint32_t* d_tok, uint32_t* tokens_out,
-                              int* d_pos, int* d_step) {
-    hipLaunchKernelGGL(k_argmax_step, dim3(1), dim3(1024), 0, s, logits, n, d_tok, tokens_out, d_pos, d_step);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

@@ -70,11 +70,15 @@ lq8_status weight_alloc(lq8_ctx* ctx, size_t n_out, size_t k_in, lq8_weight** ou
     w->n_out = n_out;
     w->k_in = k_in;
     w->nb = k_in / QK;
+    w->np = (w->nb + 1) / 2;
     w->tiles = (n_out + TILE_ROWS - 1) / TILE_ROWS;
-    size_t code_bytes = w->tiles * w->nb * 2048, scale_bytes = w->tiles * w->nb * 64 * sizeof(uint16_t);
+    // storage rounds the rows up to 32 (two tiles): a 32-row MFMA operand never reads past it
+    const size_t alloc_tiles = (n_out + 31) / 32 * 2;
+    const size_t code_bytes = alloc_tiles * w->np * CHUNK_BYTES;
+    const size_t scale_bytes = alloc_tiles * 2 * w->np * TILE_ROWS * sizeof(uint16_t);
     hipError_t e = hipMalloc(&w->codes, code_bytes);
     if (e == hipSuccess) e = hipMalloc(&w->scales, scale_bytes);
-    // padded rows are zero so every kernel can read whole tiles
+    // padding rows and the padding block of an odd nb are zero
     if (e == hipSuccess) e = hipMemsetAsync(w->codes, 0, code_bytes, ctx->stream);
     if (e == hipSuccess) e = hipMemsetAsync(w->scales, 0, scale_bytes, ctx->stream);
     if (e != hipSuccess) {
@@ -305,7 +309,7 @@ lq8_status lq8_weight_upload(lq8_ctx* ctx, const void* blocks, size_t n_out, siz
         weight_release(w);
         return hip_fail(e, "weight upload");
     }
-    st = launch_repack_aos(ctx->stream, (const uint8_t*)tmp, n_out, w->nb, 0, w);
+    st = launch_repack_aos(ctx->stream, (const uint8_t*)tmp, n_out, 0, w);
     e = hipStreamSynchronize(ctx->stream);
     (void)hipFree(tmp);
     if (st || e != hipSuccess) {
@@ -431,8 +435,8 @@ lq8_status lq8_gemv_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* 
     CHECK_W(w);
     if (!d_x || !d_y) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
     if (((uintptr_t)d_x & 15) != 0) return fail(LQ8_ERR_INVALID_ARG, "x must be 16-byte aligned");
-    GemvLaunch a{w->codes, w->scales, d_x, nullptr, 0.0f, d_y, nullptr, (int)w->n_out, (int)w->k_in};
-    return launch_gemv(ctx->stream, XS_PLAIN, a);
+    GemvArgs a{w->codes, w->scales, d_x, nullptr, d_y, nullptr, nullptr, nullptr, (int)w->n_out, (int)w->k_in, 0.0f};
+    return launch_gemv(ctx->stream, XS_PLAIN, EPI_STORE, a);
 }
 
 lq8_status lq8_gemm_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m, float* d_y) {
@@ -442,8 +446,7 @@ lq8_status lq8_gemm_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* 
     if (m == 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemm: m must be positive");
     if (m > (size_t)INT32_MAX / 2) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemm: m too large");
     if (((uintptr_t)d_x & 15) != 0) return fail(LQ8_ERR_INVALID_ARG, "x must be 16-byte aligned");
-    size_t mt = (m + 63) / 64;
-    size_t code_bytes = mt * w->nb * 2048, scale_bytes = mt * w->nb * 64 * sizeof(float);
+    const size_t code_bytes = act_code_bytes((int)m, (int)w->k_in), scale_bytes = act_scale_bytes((int)m, (int)w->k_in);
     void* sc = nullptr;
     lq8_status st = ctx_scratch(ctx, code_bytes + scale_bytes, &sc);
     if (st) return st;
@@ -451,7 +454,7 @@ lq8_status lq8_gemm_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* 
     float* xs = (float*)((char*)sc + code_bytes);
     st = launch_quantize_act(ctx->stream, d_x, (int)m, (int)w->k_in, xq, xs);
     if (st) return st;
-    return launch_gemm(ctx->stream, xq, xs, (int)m, w, d_y, nullptr, (int)w->n_out, 0);
+    return launch_gemm(ctx->stream, xq, xs, (int)m, w, d_y, nullptr);
 }
 
 lq8_status lq8_linear_forward_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m, float* d_y) {
@@ -494,7 +497,7 @@ lq8_status lq8_gemv_grouped_device(lq8_ctx* ctx, const lq8_gemv_problem* problem
         if (!registry_has(p.w)) return fail(LQ8_ERR_INVALID_ARG, "invalid weight handle in problem list");
         if (!p.x || !p.y) return fail(LQ8_ERR_INVALID_ARG, "null pointer in problem list");
         if (((uintptr_t)p.x & 15) != 0) return fail(LQ8_ERR_INVALID_ARG, "x must be 16-byte aligned");
-        if (p.w->k_in > 16384) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k > 16384 not supported");
+        if (p.w->k_in > (size_t)GEMV_MAX_K) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k above 12288 is not supported");
         host[i] = GemvProblemDev{p.w->codes, p.w->scales, p.x, p.y, (int)p.w->n_out, (int)p.w->k_in, (int)tiles, 0};
         tiles += p.w->tiles;
         if ((int)p.w->k_in > max_k) max_k = (int)p.w->k_in;
@@ -518,12 +521,14 @@ lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t
                           float* ms) {
     CHECK_CTX(ctx);
     if (!problems || !count || reps <= 0 || !ms) return fail(LQ8_ERR_INVALID_ARG, "bad benchmark arguments");
-    std::vector<GemvLaunch> L(count);
+    std::vector<GemvArgs> L(count);
     for (size_t i = 0; i < count; i++) {
         const lq8_gemv_problem& p = problems[i];
         if (!registry_has(p.w)) return fail(LQ8_ERR_INVALID_ARG, "invalid weight handle in problem list");
         if (!p.x || !p.y || ((uintptr_t)p.x & 15)) return fail(LQ8_ERR_INVALID_ARG, "bad x / y pointer");
-        L[i] = GemvLaunch{p.w->codes, p.w->scales, p.x, nullptr, 0.0f, p.y, nullptr, (int)p.w->n_out, (int)p.w->k_in};
+        if (p.w->k_in > (size_t)GEMV_MAX_K) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k above 12288 is not supported");
+        L[i] = GemvArgs{p.w->codes, p.w->scales, p.x, nullptr, p.y, nullptr, nullptr, nullptr, (int)p.w->n_out,
+                        (int)p.w->k_in, 0.0f};
     }
     hipStream_t s = ctx->stream;
     lq8_status st = LQ8_OK;
@@ -532,7 +537,7 @@ lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t
         if (mode == 2) {
             hipGraph_t g = nullptr;
             LQ8_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
-            for (size_t i = 0; i < count && !st; i++) st = launch_gemv(s, XS_PLAIN, L[i]);
+            for (size_t i = 0; i < count && !st; i++) st = launch_gemv(s, XS_PLAIN, EPI_STORE, L[i]);
             hipError_t e = hipStreamEndCapture(s, &g);
             if (st) { if (g) (void)hipGraphDestroy(g); return st; }
             if (e != hipSuccess) return hip_fail(e, "capture");
@@ -546,7 +551,7 @@ lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t
                 hipError_t e = hipGraphLaunch(exec, s);
                 if (e != hipSuccess) st = hip_fail(e, "graph launch");
             } else {
-                for (size_t i = 0; i < count && !st; i++) st = launch_gemv(s, XS_PLAIN, L[i]);
+                for (size_t i = 0; i < count && !st; i++) st = launch_gemv(s, XS_PLAIN, EPI_STORE, L[i]);
             }
         }
         LQ8_HIP(hipEventRecord(ctx->t1, s));
@@ -588,7 +593,7 @@ lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t
         for (int r = 0; r < reps && !st; r++) {
             for (size_t i = 0; i < count && !st; i++) {
                 (void)hipEventRecord(ev[2 * i], s);
-                st = launch_gemv(s, XS_PLAIN, L[i]);
+                st = launch_gemv(s, XS_PLAIN, EPI_STORE, L[i]);
                 (void)hipEventRecord(ev[2 * i + 1], s);
             }
             if (st) break;

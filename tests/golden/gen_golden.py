@@ -45,6 +45,8 @@ def main():
     y = oracle.gemv_q8_0(wb, n, k, x)
     ref = numpy_q8.gemv_f64(wb, n, k, x)
     assert np.max(np.abs(y - ref)) <= 1e-5 * np.max(np.abs(ref))
+    exact = numpy_q8.gemv_tree_rows(wb, n, k, x, range(n))
+    assert np.array_equal(y.view(np.uint32), exact.view(np.uint32)), "oracle GEMV disagrees with its exact restatement"
 
     m = 5
     xm = rng.standard_normal((m, k)).astype(np.float32)

@@ -43,3 +43,58 @@ def bf16_round(x):
     b = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
     r = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFFFFFF
     return ((r >> 16) << 16).astype(np.uint32).view(np.float32)
+
+
+# ---- exact restatement of the GEMV canonical order (small shapes only) ----
+from fractions import Fraction  # noqa: E402
+
+
+def round_f32(q):
+    """Rational -> float32, round to nearest, ties to even (finite results)."""
+    if q == 0:
+        return np.float32(0.0)
+    f = np.float32(float(q))
+    best = None
+    for c in (np.nextafter(f, np.float32(-np.inf), dtype=np.float32), f,
+              np.nextafter(f, np.float32(np.inf), dtype=np.float32)):
+        if not np.isfinite(c):
+            continue
+        key = (abs(Fraction(float(c)) - q), int(np.array(c, np.float32).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, c)
+    return np.float32(best[1])
+
+
+def fmaf_exact(a, b, c):
+    """fmaf(a, b, c) for finite float32 operands: one rounding of the exact value.
+    An exact zero result is +0 (round to nearest; never both addends -0 here)."""
+    return round_f32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def gemv_tree_rows(blocks, n_out, k_in, x, rows):
+    """GEMV canonical order for the given rows: per block, h0 = fmaf chain over
+    codes 0..15, h1 over codes 16..31 (from +0), v_b = (h0 + h1) * d_b (float32
+    ops); then the pairwise tree v[i] += v[i + s], s = 1, 2, 4, ..., i + s < nb."""
+    nb = k_in // 32
+    b = np.asarray(blocks, np.uint8).reshape(n_out, nb, 34)
+    x = np.asarray(x, np.float32)
+    out = []
+    for r in rows:
+        v = []
+        for j in range(nb):
+            d = b[r, j, :2].copy().view(np.float16).astype(np.float32)[0]
+            q = b[r, j, 2:].view(np.int8)
+            h0 = np.float32(0.0)
+            for t in range(16):
+                h0 = fmaf_exact(np.float32(q[t]), x[32 * j + t], h0)
+            h1 = np.float32(0.0)
+            for t in range(16, 32):
+                h1 = fmaf_exact(np.float32(q[t]), x[32 * j + t], h1)
+            v.append(np.float32(np.float32(h0 + h1) * d))
+        s = 1
+        while s < nb:
+            for i in range(0, nb - s, 2 * s):
+                v[i] = np.float32(v[i] + v[i + s])
+            s *= 2
+        out.append(v[0])
+    return np.array(out, np.float32)

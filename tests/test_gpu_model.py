@@ -97,16 +97,39 @@ def test_graph_replays_repeatable(small_pair):
     assert a.tolist() == b.tolist()
 
 
-def test_long_context_config_uses_unfused_attention(ctx):
-    """max_positions 8192 exceeds the fused decode attention's LDS budget, so
-    decode runs the per-head kernels; results still match the oracle."""
+def test_long_context_many_segments(ctx):
+    """max_positions 8192 (128 attention segments launched, most idle) and a
+    200-token prompt: decode attention combines 4-5 segments; tokens match."""
     cfg = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
                           num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=8192)
     model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=9)
     ref = oracle.Model(cfg, model.export_all())
-    prompt = np.random.default_rng(9).integers(0, cfg.vocab_size, 70).astype(np.uint32)
-    toks, _ = model.generate_greedy(prompt, 10)
-    ref_toks, _ = ref.generate_greedy(prompt, 10)
+    prompt = np.random.default_rng(9).integers(0, cfg.vocab_size, 200).astype(np.uint32)
+    toks, _ = model.generate_greedy(prompt, 70)
+    ref_toks, _ = ref.generate_greedy(prompt, 70)
+    assert toks.tolist() == ref_toks.tolist()
+    model.clear_kv_cache()
+    ref.clear_kv_cache()
+    assert same_bits(model.forward(prompt[:129], 0), ref.forward(prompt[:129], 0))
+    for t in range(3):
+        assert same_bits(model.forward([int(prompt[129 + t])], 129 + t), ref.forward([int(prompt[129 + t])], 129 + t))
+    model.free()
+    ref.close()
+
+
+def test_wide_gqa_and_odd_block_counts(ctx):
+    """8 query heads per kv head (the MoE layer's grouping) and hidden /
+    intermediate sizes with an odd number of Q8_0 blocks (224 = 7 blocks,
+    352 = 11 blocks): logits bit-exact, tokens identical."""
+    cfg = lq8.Qwen3Config(vocab_size=1000, hidden_size=224, intermediate_size=352, num_hidden_layers=2,
+                          num_attention_heads=8, num_key_value_heads=1, head_dim=128, max_position_embeddings=160)
+    model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=21)
+    ref = oracle.Model(cfg, model.export_all())
+    prompt = np.random.default_rng(21).integers(0, cfg.vocab_size, 66).astype(np.uint32)
+    assert same_bits(model.forward(prompt, 0), ref.forward(prompt, 0))
+    assert same_bits(model.forward([7], 66), ref.forward([7], 66))
+    toks, _ = model.generate_greedy(prompt, 20)
+    ref_toks, _ = ref.generate_greedy(prompt, 20)
     assert toks.tolist() == ref_toks.tolist()
     model.free()
     ref.close()

@@ -227,10 +227,9 @@ def test_errors_no_fallback(ctx):
         lq8._check(lq8.lib().lq8_gemv_q8_0_device(ctx.handle, stale, None, None))
 
 
-def test_gemv_split_repeated_calls(ctx):
-    """Small-N GEMVs combine group partials across workgroups through device
-    counters; repeated calls (counters reset by the last workgroup) and
-    interleaved shapes give the oracle's bits every time."""
+def test_gemv_repeated_and_graph_calls(ctx):
+    """Repeated calls, interleaved shapes and graph replays give the oracle's
+    bits every time."""
     cases = []
     for i, (n, k) in enumerate([(1024, 3072), (64, 2048), (1024, 1024), (200, 768)]):
         blocks = oracle.quantize_q8_0(normal((n, k), 0.02, 500 + i))

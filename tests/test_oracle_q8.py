@@ -145,3 +145,44 @@ def test_golden_fixtures():
     n, k = g["gemv_y"].size, g["gemv_x"].size
     assert np.array_equal(oracle.gemv_q8_0(g["gemv_w"], n, k, g["gemv_x"]).view(np.uint32), g["gemv_y"].view(np.uint32))
     assert np.array_equal(oracle.gemm_q8_0(g["gemv_w"], n, k, g["gemm_x"]).view(np.uint32), g["gemm_y"].view(np.uint32))
+
+
+@pytest.mark.parametrize("n,k", [(5, 1024), (3, 96), (4, 3072), (2, 32)])
+def test_gemv_tree_order_exact(n, k):
+    """The oracle's GEMV equals an exact rational restatement of its documented
+    summation order (fmaf rounded once from the exact value), bit for bit."""
+    b = oracle.quantize_q8_0(normal((n, k), 0.02, 40 + k))
+    x = normal(k, 1.0, 41 + k)
+    y = oracle.gemv_q8_0(b, n, k, x)
+    ref = numpy_q8.gemv_tree_rows(b, n, k, x, range(n))
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+
+
+def test_gemv_tree_order_is_not_sequential():
+    """The exact restatement separates the tree from a plain chain over blocks
+    (a plausible mistake): on a row where the two differ, the oracle gives the
+    tree's bits."""
+    k = 256
+    for seed in range(200):
+        b = oracle.quantize_q8_0(normal((1, k), 0.02, 1000 + seed))
+        x = normal(k, 1.0, 2000 + seed)
+        bb = b.reshape(8, 34)
+        vals = []
+        for j in range(8):
+            d = bb[j, :2].copy().view(np.float16).astype(np.float32)[0]
+            q = bb[j, 2:].view(np.int8).astype(np.float32)
+            h0 = np.float32(0)
+            for t in range(16):
+                h0 = numpy_q8.fmaf_exact(q[t], x[32 * j + t], h0)
+            h1 = np.float32(0)
+            for t in range(16, 32):
+                h1 = numpy_q8.fmaf_exact(q[t], x[32 * j + t], h1)
+            vals.append(np.float32(np.float32(h0 + h1) * d))
+        chain = np.float32(0)
+        for v in vals:
+            chain = np.float32(chain + v)
+        tree = numpy_q8.gemv_tree_rows(b, 1, k, x, [0])[0]
+        if chain != tree:
+            assert oracle.gemv_q8_0(b, 1, k, x)[0] == tree
+            return
+    pytest.fail("no row separating the two orders found")
