@@ -3,19 +3,25 @@
 Workload (one "step"): every linear layer of one Qwen3-0.6B decode token at
 batch 1 as a Q8_0 GEMV -- 28 layers x {q 2048x1024, k 1024x1024, v 1024x1024,
 o 1024x2048, gate 3072x1024, up 3072x1024, down 1024x3072} plus the lm_head
-151936x1024 -- over distinct resident weights (633 MB, more than twice the
-256 MB Infinity Cache, so every step streams from HBM).  Weights N(0, 0.02)
-and activations N(0, 1) from seeded device generators.
+151936x1024 -- 197 GEMVs over distinct resident weights (633 MB, more than
+twice the 256 MB Infinity Cache, so every step streams from HBM), each with
+its own seeded N(0, 1) input.  Weights N(0, 0.02) from a seeded device
+generator, quantized to Q8_0 on the device.
 
-Prints one JSON line: the step's whole-job HBM throughput (GB/s of
-algorithmic bytes), the roofline of the dominant kernel (the GEMV), and the
-CPU oracle timed on a bounded sample of the same workload.  Side results:
-batch-1 greedy decode tokens/s of the random-init Q8_0 Qwen3-0.6B (128-token
-prompt, 128 new tokens) and the M=512 W8A8 MFMA GEMM.
+The headline value runs the step as one grouped launch (the 197 GEMVs are
+independent, so one kernel streams them back to back); the same step with one
+launch per GEMV replayed from a HIP graph, the lm_head alone, the single
+3072x1024 GEMV, the M = 512 W8A8 MFMA GEMM, and batch-1 greedy decode of the
+random-init Q8_0 Qwen3-0.6B (128-token prompt, 128 new tokens) are reported
+beside it.  The CPU oracle's GEMV, single-threaded over a bounded sample of the
+same workload, is the CPU baseline.
+
+Prints one JSON line on stdout; progress goes to stderr.
 """
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -32,10 +38,12 @@ LAYER_SHAPES = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1
                 ("gate", 3072, 1024), ("up", 3072, 1024), ("down", 1024, 3072)]
 LM_HEAD = ("lm_head", 151936, 1024)
 LAYERS = 28
+CALIB_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_grouped_qwen3_decode_step_traffic.md")
 
 
 def gemv_bytes(n, k):
-    """Algorithmic bytes of one GEMV: Q8_0 weight + f32 x + f32 y."""
+    """Algorithmic bytes of one GEMV: Q8_0 weight (34 B per 32) + f32 x + f32 y."""
     return n * k * 34 // 32 + 4 * k + 4 * n
 
 
@@ -54,6 +62,18 @@ def make_problems(ctx, seed):
         probs.append((w, x, y))
         bufs += [x, y]
     return shapes, probs, bufs
+
+
+def measured_traffic():
+    """HBM bytes per grouped launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by the same counters on a copy of known
+    size), or None when the summary is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 def cpu_baseline(seconds_target=12.0):
@@ -79,7 +99,23 @@ def cpu_baseline(seconds_target=12.0):
     oracle.set_threads(0)
     return {"value": round(passes * layer_bytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{passes} passes over one Qwen3-0.6B decode layer's 7 Q8_0 GEMVs "
-                      f"({layer_bytes} B each), {el:.1f} s single-threaded"}
+                      f"({layer_bytes} B each), {el:.1f} s on one host core"}
+
+
+def rotating_gemv_us(ctx, n, k, copies):
+    """Per-launch time of an n x k GEMV, graph-replayed over `copies` distinct
+    weights (cold: the copies together exceed the Infinity Cache)."""
+    ws = [lq8.Q8Weight.random(ctx, n, k, seed=11, stream=i) for i in range(copies)]
+    x = lq8.DeviceBuffer.from_array(ctx, np.random.default_rng(1).standard_normal(k).astype(np.float32))
+    y = lq8.DeviceBuffer(ctx, 4 * n)
+    probs = [(w, x, y) for w in ws]
+    lq8.bench_gemv(ctx, probs, mode=2, reps=2)
+    us = lq8.bench_gemv(ctx, probs, mode=2, reps=10) * 1e3 / (10 * copies)
+    for w in ws:
+        w.free()
+    x.free()
+    y.free()
+    return us
 
 
 def main():
@@ -89,62 +125,68 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-step", action="store_true",
+                    help="only the headline step and the calibration copy (for hardware-counter runs)")
     args = ap.parse_args()
+    if args.only_step:
+        args.no_decode = args.no_cpu = True
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (multi-GPU sharding is a "
-                                   "design note, not built)"}))
+        print(json.dumps({"error": "this build runs on one GPU only (--gpus 1); multi-GPU sharding is a design "
+                                   "note, not built"}))
         sys.exit(2)
 
     ctx = lq8.Context(0)
     shapes, probs, bufs = make_problems(ctx, seed=1234)
     step_bytes = sum(gemv_bytes(n, k) for _, n, k in shapes)
     nlaunch = len(probs)
-    log(f"config-2 step: {nlaunch} GEMVs, {step_bytes} algorithmic bytes")
+    log(f"step: {nlaunch} GEMVs, {step_bytes} algorithmic bytes")
 
-    # warmup, then the timed steps: one launch per Linear::forward, replayed as a HIP graph
-    lq8.bench_gemv(ctx, probs, mode=2, reps=max(args.warmup, 1))
+    # headline: the step as one grouped launch; W warmup steps, then exactly K
+    # steps between HIP events on the context stream (synchronized both sides)
+    lq8.bench_gemv(ctx, probs, mode=1, reps=max(args.warmup, 1))
     ctx.synchronize()
-    ms_graph = lq8.bench_gemv(ctx, probs, mode=2, reps=args.steps)
+    ms = lq8.bench_gemv(ctx, probs, mode=1, reps=args.steps)
     ctx.synchronize()
-    ms_step = ms_graph / args.steps
+    ms_step = ms / args.steps
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"graph of per-layer launches: {ms_step * 1e3:.1f} us/step, {value:.1f} GB/s")
+    log(f"grouped launch: {ms_step * 1e3:.1f} us/step, {value:.1f} GB/s ({value / HBM_PEAK_GBS:.1%} of HBM peak)")
 
-    # kernel-only time of the same launches: per-launch HIP-event intervals
-    reps_ev = max(2, min(10, args.steps))
-    ms_ev = lq8.bench_gemv(ctx, probs, mode=3, reps=reps_ev) / reps_ev
-    avg_launch_us = ms_ev * 1e3 / nlaunch
-    achieved = step_bytes / (ms_ev * 1e-3) / 1e9
-    log(f"per-launch event intervals: {avg_launch_us:.2f} us/launch avg, {achieved:.1f} GB/s")
-
-    # whole step as one grouped launch (independent GEMVs streamed back to back)
-    lq8.bench_gemv(ctx, probs, mode=1, reps=2)
-    ms_grp = lq8.bench_gemv(ctx, probs, mode=1, reps=args.steps) / args.steps
-    grouped = step_bytes / (ms_grp * 1e-3) / 1e9
-    log(f"grouped single launch: {ms_grp * 1e3:.1f} us/step, {grouped:.1f} GB/s")
-
-    # lm_head alone (165 MB: the largest single GEMV)
-    lm = [probs[-1]]
-    lq8.bench_gemv(ctx, lm, mode=0, reps=3)
-    ms_lm = lq8.bench_gemv(ctx, lm, mode=0, reps=20) / 20
+    ms_chain = ms_lm = float("nan")
+    if not args.only_step:
+        # the same step, one launch per GEMV (a Linear::forward each), replayed as a HIP graph
+        lq8.bench_gemv(ctx, probs, mode=2, reps=2)
+        ms_chain = lq8.bench_gemv(ctx, probs, mode=2, reps=max(5, args.steps // 5)) / max(5, args.steps // 5)
+        log(f"one launch per GEMV (graph): {ms_chain * 1e3:.1f} us/step, "
+            f"{step_bytes / (ms_chain * 1e-3) / 1e9:.1f} GB/s")
+        # lm_head alone (165 MB: the largest single GEMV)
+        lm = [probs[-1]]
+        lq8.bench_gemv(ctx, lm, mode=0, reps=3)
+        ms_lm = lq8.bench_gemv(ctx, lm, mode=0, reps=20) / 20
+        log(f"lm_head: {ms_lm * 1e3:.1f} us, {gemv_bytes(*LM_HEAD[1:]) / (ms_lm * 1e-3) / 1e9:.1f} GB/s")
+    chain_gbs = step_bytes / (ms_chain * 1e-3) / 1e9
     lm_gbs = gemv_bytes(*LM_HEAD[1:]) / (ms_lm * 1e-3) / 1e9
-    log(f"lm_head: {ms_lm * 1e3:.1f} us, {lm_gbs:.1f} GB/s")
-
-    # config 1: the single 3072x1024 GEMV (hot in cache when repeated; reported as is)
-    c1 = lq8.Q8Weight.random(ctx, 3072, 1024, seed=1, stream=0)
-    c1x = lq8.DeviceBuffer.from_array(ctx, np.random.default_rng(1).standard_normal(1024).astype(np.float32))
-    c1y = lq8.DeviceBuffer(ctx, 3072 * 4)
-    ms_c1 = lq8.bench_gemv(ctx, [(c1, c1x, c1y)], mode=3, reps=50) / 50
-    log(f"config-1 GEMV 3072x1024: {ms_c1 * 1e3:.2f} us")
-
     for w, _, _ in probs:
         w.free()
     for b in bufs:
         b.free()
 
-    # config 3: prefill-shaped W8A8 GEMM, M = 512
+    # known-size copy: calibrates FETCH_SIZE / WRITE_SIZE when profiled
+    src, dst = lq8.DeviceBuffer(ctx, CALIB_BYTES), lq8.DeviceBuffer(ctx, CALIB_BYTES)
+    for _ in range(3):
+        lq8._check(lq8.lib().lq8_copy_device(ctx.handle, dst.ptr, src.ptr, CALIB_BYTES))
+    ctx.synchronize()
+    src.free()
+    dst.free()
+
+    # the single 3072 x 1024 GEMV (cold: 64 rotating copies)
+    c1_us = float("nan")
+    if not args.only_step:
+        c1_us = rotating_gemv_us(ctx, 3072, 1024, 64)
+        log(f"GEMV 3072x1024: {c1_us:.2f} us, {gemv_bytes(3072, 1024) / c1_us / 1e3:.1f} GB/s")
+
+    # prefill-shaped W8A8 GEMM, M = 512 (activation quantize + int8 MFMA)
     gemm = {}
-    for name, n, k in [("gate", 3072, 1024), ("down", 1024, 3072)]:
+    for name, n, k in ([] if args.only_step else [("gate_up", 3072, 1024), ("down", 1024, 3072)]):
         w = lq8.Q8Weight.random(ctx, n, k, seed=3, stream=n)
         x = lq8.DeviceBuffer.from_array(ctx, np.random.default_rng(3).standard_normal((512, k)).astype(np.float32))
         y = lq8.DeviceBuffer(ctx, 512 * n * 4)
@@ -157,9 +199,8 @@ def main():
             lin.forward_device(x, 512, y)
         ms = ctx.timer_stop() / 20
         tops = 2 * 512 * n * k / (ms * 1e-3) / 1e12
-        gemm[name] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1),
-                      "mfma_util": round(tops / INT8_PEAK_TOPS, 4)}
-        log(f"config-3 GEMM {name} M=512: {ms * 1e3:.1f} us, {tops:.1f} TOPS (incl. activation quantize)")
+        gemm[name] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4)}
+        log(f"GEMM {name} M=512: {ms * 1e3:.1f} us, {tops:.1f} TOPS (includes the activation quantize)")
         w.free(); x.free(); y.free()
 
     decode = None
@@ -172,7 +213,7 @@ def main():
         tps = sorted(r["decode_tokens_per_s"] for r in runs)[1]
         decode = {"tokens_per_s": round(tps, 1), "prefill_ms": round(runs[0]["prefill_ms"], 2),
                   "graph": runs[0]["used_graph"], "prompt": 128, "new_tokens": 128}
-        log(f"config-4 decode: {tps:.1f} tok/s (median of 3), prefill {runs[0]['prefill_ms']:.1f} ms")
+        log(f"decode: {tps:.1f} tok/s (median of 3), prefill {runs[0]['prefill_ms']:.2f} ms")
         model.free()
     ctx.close()
 
@@ -180,6 +221,7 @@ def main():
     if cpu:
         log(f"cpu baseline: {cpu['value']} GB/s ({cpu['sample']})")
 
+    traffic = measured_traffic()
     out = {
         "metric": "Q8_0 GEMV HBM GB/s (% peak) + batch-1 decode tokens/s, Qwen3-0.6B shapes",
         "value": round(value, 2),
@@ -192,17 +234,20 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 codes x f32 (W8A32), f32 accumulate",
-        "data": "synthetic: seeded N(0,0.02) Q8_0 weights, N(0,1) activations",
-        "config": {"workload": "Qwen3-0.6B decode-token linear set at batch 1: 28 x {q,k,v,o,gate,up,down} "
-                               "+ lm_head as Q8_0 GEMVs, one launch each, replayed as a HIP graph",
-                   "gemvs_per_step": nlaunch, "bytes_per_step": step_bytes, "pct_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemv<XS_PLAIN>", "avg_launch_us": round(avg_launch_us, 3),
-                     "bytes_per_launch_avg": step_bytes // nlaunch},
-        "grouped_launch_gbs": round(grouped, 1),
-        "lm_head_gbs": round(lm_gbs, 1),
-        "config1_gemv_us": round(ms_c1 * 1e3, 3),
+        "data": "synthetic: seeded N(0,0.02) Q8_0 weights, N(0,1) inputs",
+        "config": {"workload": "Qwen3-0.6B decode-token linear set, batch 1: 28 x {q 2048x1024, k 1024x1024, "
+                               "v 1024x1024, o 1024x2048, gate 3072x1024, up 3072x1024, down 1024x3072} + lm_head "
+                               "151936x1024, 197 independent Q8_0 GEMVs streamed by one grouped launch",
+                   "gemvs_per_step": nlaunch, "bytes_per_step": step_bytes,
+                   "pct_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "k_gemv_grouped", "launch_us": round(ms_step * 1e3, 2),
+                     "bytes_per_launch": step_bytes},
+        "one_launch_per_gemv_gbs": None if args.only_step else round(chain_gbs, 1),
+        "one_launch_per_gemv_us_per_step": None if args.only_step else round(ms_chain * 1e3, 1),
+        "lm_head_gbs": None if args.only_step else round(lm_gbs, 1),
+        "gemv_3072x1024_us": None if args.only_step else round(c1_us, 3),
         "gemm_m512": gemm,
         "decode": decode,
         "cpu_baseline": cpu,

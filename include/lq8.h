@@ -71,6 +71,10 @@ lq8_status lq8_device_alloc(lq8_ctx* ctx, size_t bytes, void** dptr);
 lq8_status lq8_device_free(lq8_ctx* ctx, void* dptr);
 lq8_status lq8_copy_to_device(lq8_ctx* ctx, void* dst, const void* src, size_t bytes);
 lq8_status lq8_copy_to_host(lq8_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Device-to-device copy enqueued on the context stream (no synchronization).
+ * No reference counterpart: used as the known-size copy that calibrates HBM
+ * traffic counters, and for device-side staging. */
+lq8_status lq8_copy_device(lq8_ctx* ctx, void* dst, const void* src, size_t bytes);
 /* HIP-event timer on the context stream (the reference's PROFILE timings,
  * src/tensor.rs:824-885, measured on the device instead of wall clock). */
 lq8_status lq8_timer_start(lq8_ctx* ctx);

@@ -276,6 +276,14 @@ lq8_status lq8_copy_to_host(lq8_ctx* ctx, void* dst, const void* src, size_t byt
     return LQ8_OK;
 }
 
+lq8_status lq8_copy_device(lq8_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    CHECK_CTX(ctx);
+    if ((!dst || !src) && bytes) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (!bytes) return LQ8_OK;
+    LQ8_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return LQ8_OK;
+}
+
 lq8_status lq8_timer_start(lq8_ctx* ctx) {
     CHECK_CTX(ctx);
     LQ8_HIP(hipEventRecord(ctx->t0, ctx->stream));

@@ -107,6 +107,7 @@ _SIGS = [
     ("lq8_device_free", C.c_int, [C.c_void_p, C.c_void_p]),
     ("lq8_copy_to_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
     ("lq8_copy_to_host", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    ("lq8_copy_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
     ("lq8_timer_start", C.c_int, [C.c_void_p]),
     ("lq8_timer_stop", C.c_int, [C.c_void_p, C.POINTER(C.c_float)]),
     ("lq8_weight_upload", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_void_p)]),
