@@ -122,14 +122,15 @@ lq8_status launch_argmax_final(hipStream_t s, const float* arg_val, const int* a
                                uint32_t* tokens_out, int* d_pos, int* d_step);
 
 // ---- Q8_0 format, activation quantization, GEMM (q8_kernels.hip) -------------
-// Activation rows x[m, k] -> tiled codes (as a weight) + f32 scales [mtiles][2*np][16].
-lq8_status launch_quantize_act(hipStream_t s, const float* x, int m, int k, int8_t* codes, float* scales32);
+// Activation rows x[m, k] -> tiled codes (as a weight, 2 * ceil(m/32) tiles) + f16
+// scales in the GEMM's operand layout (act_scale_bytes).
+lq8_status launch_quantize_act(hipStream_t s, const float* x, int m, int k, int8_t* codes, uint32_t* scales);
 size_t act_code_bytes(int m, int k);
 size_t act_scale_bytes(int m, int k);
 // AoS quantization (public device quantizer).
 lq8_status launch_quantize_aos(hipStream_t s, const float* x, size_t nblocks, uint8_t* blocks);
 // W8A8 GEMM: y[m, n] (+ resid) from tiled activations and a tiled weight.
-lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const float* xs, int m, const lq8_weight* w, float* y,
+lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const uint32_t* xs, int m, const lq8_weight* w, float* y,
                        const float* resid);
 
 lq8_status launch_repack_aos(hipStream_t s, const uint8_t* aos, size_t n_rows, size_t row0, const lq8_weight* w);

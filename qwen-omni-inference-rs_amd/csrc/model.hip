@@ -302,9 +302,10 @@ lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, 
 
 lq8_status quant_gemm(lq8_model* m, const float* x, int n, const lq8_weight* w, float* y, const float* resid) {
     hipStream_t s = m->ctx->stream;
-    lq8_status st = launch_quantize_act(s, x, n, (int)w->k_in, m->P_xq, m->P_xs);
+    uint32_t* xs = reinterpret_cast<uint32_t*>(m->P_xs);
+    lq8_status st = launch_quantize_act(s, x, n, (int)w->k_in, m->P_xq, xs);
     if (st) return st;
-    return launch_gemm(s, m->P_xq, m->P_xs, n, w, y, resid);
+    return launch_gemm(s, m->P_xq, xs, n, w, y, resid);
 }
 
 // n positions starting at pos_base (src/model.rs:170-195), then the last

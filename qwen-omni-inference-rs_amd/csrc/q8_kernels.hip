@@ -161,90 +161,223 @@ __global__ void k_dequant_rows(const int8_t* __restrict__ codes, const uint16_t*
 
 // ---- activation quantization (tiled A operand of the GEMM) ----------------
 
-__global__ void k_quantize_act(const float* __restrict__ x, int m, int k, int8_t* __restrict__ codes,
-                               float* __restrict__ scales32) {
-    const size_t nb = (size_t)k / 32, np = (nb + 1) / 2;
-    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (size_t)m * nb) return;
-    const size_t r = idx / nb, b = idx % nb;
-    float v[32];
-    const float4* s4 = (const float4*)(x + r * (size_t)k + b * 32);
+// One wave per (16-row tile, block pair): its 64 lanes write the pair's 1 KiB
+// code chunk with one 16-byte store each.  Lane l covers row l % 16 of the
+// tile and part l / 16 of the chunk, i.e. half (l / 16) % 2 of block
+// 2p + l / 32; the two halves of a block (lanes l and l ^ 16) share amax
+// through one shuffle (max is exact in any order).  Rows past m repeat row
+// m - 1 (finite data for the padding rows of the last 32-row tile); blocks
+// past nb get zero codes and a zero scale.  Scales go to the GEMM's f16
+// operand layout: u32 words (f16 bits, high half zero) in
+// [m/32][nbp/4][64 lanes][4 blocks], lanes 0..31 = rows, lanes 32..63 = 0.
+__global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ x, int m, int k, int waves, int np8,
+                                                      int8_t* __restrict__ codes, uint32_t* __restrict__ xs) {
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= waves) return;
+    const int lane = threadIdx.x & 63;
+    const int tile = gw / np8, p = gw - tile * np8;
+    const int nb = k >> 5, np = (nb + 1) >> 1;
+    const int r = lane & 15, part = lane >> 4, b = 2 * p + (part >> 1), hf = part & 1;
+    uint32_t d16 = 0;
+    if (p < np) {
+        const int row = min(tile * TILE_ROWS + r, m - 1);
+        const float4* src = (const float4*)(x + (size_t)row * k + min(b, nb - 1) * 32 + hf * 16);
+        const float4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
+        const float v[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
+                             v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+        // amax from 0, NaN ignored (as `if (v > amax) amax = v`): fmaxf returns the non-NaN operand
+        float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float4 t = s4[i];
-        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+        for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        const QBlock qb = block_scale(amax);
+        const float id = block_inv(qb.d);
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            w[i] = (uint32_t)(quant_code(v[4 * i], id) & 0xFF) | ((uint32_t)(quant_code(v[4 * i + 1], id) & 0xFF) << 8) |
+                   ((uint32_t)(quant_code(v[4 * i + 2], id) & 0xFF) << 16) |
+                   ((uint32_t)(quant_code(v[4 * i + 3], id) & 0xFF) << 24);
+        const bool real = b < nb;
+        *(uint4*)(codes + ((size_t)(tile * np + p) * 64 + lane) * 16) =
+            real ? make_uint4(w[0], w[1], w[2], w[3]) : make_uint4(0, 0, 0, 0);
+        d16 = real ? qb.d16 : 0u;
     }
-    int q[32];
-    QBlock qb;
-    quantize32(v, q, &qb);
-    store_tiled(codes, np, r, b, q);
-    scales32[scale_off(r / TILE_ROWS, np, b, (int)(r % TILE_ROWS))] = f16_bits_to_f32(qb.d16);
+    const int slot = hf * 32 + (tile & 1) * TILE_ROWS + r;
+    xs[((size_t)((tile >> 1) * (np8 >> 1) + (b >> 2)) * 64 + slot) * 4 + (b & 3)] = hf ? 0u : d16;
 }
 
 // ---- GEMM (W8A8, v_mfma_i32_32x32x32_i8) -------------------------------------
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
-// Workgroup tile 64 (m) x 64 (n); wave w owns the 32 x 32 sub-tile (w >> 1, w & 1).
-// Operand lane l of a 32-row MFMA tile at row R0: row R0 + l % 32 (16-row tile
-// R0 / 16 + (l % 32) / 16), codes of half l / 32 of the block; the two operands
-// use the same split of the 32 k-values, so the int32 block dot is exact.
-// Accumulator layout: lane l holds column l % 32, register i holds row
-// 8 * (i / 4) + 4 * (l / 32) + i % 4.
-__global__ __launch_bounds__(WG) void k_gemm(const int8_t* __restrict__ xq, const float* __restrict__ xs32, int m,
-                                             const int8_t* __restrict__ wc, const uint16_t* __restrict__ ws, int n,
-                                             int nb, float* __restrict__ y, const float* __restrict__ resid) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int mt32 = blockIdx.y * 2 + (wave >> 1), nt32 = blockIdx.x * 2 + (wave & 1);
-    if (mt32 * 32 >= m || nt32 * 32 >= n) return;  // no barriers below
-    const int np = (nb + 1) >> 1;
-    const int half = lane >> 5, r32 = lane & 31;
-    const int atile = mt32 * 2 + (r32 >> 4), btile = nt32 * 2 + (r32 >> 4);
-    const int8_t* ab = xq + ((size_t)atile * np * 64 + half * 16 + (r32 & 15)) * 16;
-    const int8_t* bb = wc + ((size_t)btile * np * 64 + half * 16 + (r32 & 15)) * 16;
-    // scale pointers: dw for column r32 (tile btile, row r32 % 16); dx rows 4*half + 0..3 (+8) in tiles 2*mt32, 2*mt32+1
-    const uint16_t* dwp = ws + (size_t)btile * 2 * np * 16 + (r32 & 15);
-    const float* dxp0 = xs32 + (size_t)(mt32 * 2) * 2 * np * 16 + 4 * half;
-    const float* dxp1 = xs32 + (size_t)(mt32 * 2 + 1) * 2 * np * 16 + 4 * half;
-    auto boff = [&](int b) { return (size_t)((b >> 1) * 64 + (b & 1) * 32) * 16; };
-    float yacc[16], acc[16];
+constexpr int RSRC_CFG = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
+struct GemmArgs {
+    const int8_t* xq;   // activation codes, tiled like a weight (2 * ntm 16-row tiles)
+    const uint32_t* xs; // activation scales, f16 operand layout written by k_quantize_act
+    const int8_t* wc;   // weight codes
+    const uint16_t* ws; // weight scales (f16 bits)
+    float* y;
+    const float* resid;
+    int m, n, nb, np, groups, ntm, ntiles;
+    int xq_bytes, xs_bytes, wc_bytes, ws_bytes;
+};
+
+// Buffer resources and per-lane byte offsets of one wave's operands.
+struct GemmSrc {
+    __amdgpu_buffer_rsrc_t ra, rb, rx, rw;
+    int oa, ob, ox, ow;
+};
+
+// Operands of 4 consecutive blocks b0 .. b0 + 3 (b0 % 4 == 0).  Codes and
+// weight scales of blocks past nb are read from block nb - 1 (in bounds);
+// their products are cancelled by zero scales in the compute step.
+struct Quad {
+    v4i dx;       // activation scales of the 4 blocks (lanes 32..63: 0)
+    v4i a[4], w[4];
+    uint32_t dw[4];
+};
+
+__device__ __forceinline__ void gemm_load(const GemmSrc& o, int b0, int nb, Quad& q) {
+    q.dx = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(o.rx, o.ox, (b0 >> 2) * 1024, 0));
 #pragma unroll
-    for (int i = 0; i < 16; i++) { yacc[i] = 0.0f; acc[i] = 0.0f; }
-    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    v4i av = *(const v4i*)(ab + boff(0));
-    v4i bv = *(const v4i*)(bb + boff(0));
-    for (int b = 0; b < nb; b++) {
-        const v4i a_cur = av, b_cur = bv;
-        if (b + 1 < nb) {
-            av = *(const v4i*)(ab + boff(b + 1));
-            bv = *(const v4i*)(bb + boff(b + 1));
-        }
-        const float dw = f16_bits_to_f32(dwp[b * 16]);
-        const float4 d0 = *(const float4*)(dxp0 + b * 16);
-        const float4 d1 = *(const float4*)(dxp0 + b * 16 + 8);
-        const float4 d2 = *(const float4*)(dxp1 + b * 16);
-        const float4 d3 = *(const float4*)(dxp1 + b * 16 + 8);
-        const float dx[16] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w,
-                              d2.x, d2.y, d2.z, d2.w, d3.x, d3.y, d3.z, d3.w};
-        const v16i isum = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_cur, b_cur, zero, 0, 0, 0);
+    for (int i = 0; i < 4; i++) {
+        const int bc = min(b0 + i, nb - 1);
+        const int cs = (bc >> 1) * 1024 + (bc & 1) * 512;
+        q.a[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(o.ra, o.oa, cs, 0));
+        q.w[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(o.rb, o.ob, cs, 0));
+        q.dw[i] = __builtin_amdgcn_raw_buffer_load_b16(o.rw, o.ow, bc * 32, 0);
+    }
+}
+
+// acc[r] = fmaf((float)I_b[r], dw_b * dx_b[r], acc[r]) for the 4 blocks in
+// order.  The scale products come from one v_mfma_f32_32x32x8f16 per block:
+// A = (dx[row], 0, 0, 0) in lanes 0..31 and 0 in lanes 32..63, B = (dw[col],
+// 0, 0, 0) in lanes 0..31 of a real block and 0 elsewhere, so D[row][col] =
+// dx * dw exactly (a product of two f16 values fits f32) -- the same value
+// the VALU product gives -- and exactly 0 for a block past nb.
+__device__ __forceinline__ void gemm_quad(const Quad& q, int b0, int nb, bool lo, float* acc) {
+    const v16i zi = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc[i] = fmaf((float)isum[i], dw * dx[i], acc[i]);
-        if ((b % GEMM_GROUP) == GEMM_GROUP - 1 || b == nb - 1) {
+    for (int i = 0; i < 4; i++) {
+        const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.a[i], q.w[i], zi, 0, 0, 0);
+        const uint2 au = {(uint32_t)q.dx[i], 0u};
+        const uint2 bu = {(lo && b0 + i < nb) ? q.dw[i] : 0u, 0u};
+        const v16f P = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, au), __builtin_bit_cast(v4h, bu),
+                                                            zf, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 16; i++) { yacc[i] = yacc[i] + acc[i]; acc[i] = 0.0f; }
+        for (int r = 0; r < 16; r++) acc[r] = fmaf((float)I[r], P[r], acc[r]);
+    }
+}
+
+// One round: the wave's group g (8 blocks in two quads q0, q1), with the
+// loads of the next round's group gn issued behind each quad's compute.
+template <bool NEXT>
+__device__ __forceinline__ void gemm_group(const GemmSrc& o, int g, int gn, int nb, bool lo, Quad& q0, Quad& q1,
+                                           float* acc) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    gemm_quad(q0, g * GEMM_GROUP, nb, lo, acc);
+    if (NEXT) gemm_load(o, gn * GEMM_GROUP, nb, q0);
+    gemm_quad(q1, g * GEMM_GROUP + 4, nb, lo, acc);
+    if (NEXT) gemm_load(o, gn * GEMM_GROUP + 4, nb, q1);
+}
+
+// Round combine: wave 0 adds its own group, then the other waves' groups
+// from LDS, in group order (y = y + a_g).  part is double-buffered by round
+// parity, so one barrier per round suffices.
+template <int S>
+__device__ __forceinline__ void gemm_combine(float4 (*part)[S > 1 ? S - 1 : 1][4][64], int j, int s, int lane,
+                                             int G, const float* acc, float* y) {
+    if (S == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) y[r] = y[r] + acc[r];
+        return;
+    }
+    if (s > 0 && j * S + s < G) {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            part[j & 1][s - 1][q][lane] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+    }
+    __syncthreads();
+    if (s == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) y[r] = y[r] + acc[r];
+        for (int t = 1; t < S && j * S + t < G; t++) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 v = part[j & 1][t - 1][q][lane];
+                y[4 * q] = y[4 * q] + v.x;
+                y[4 * q + 1] = y[4 * q + 1] + v.y;
+                y[4 * q + 2] = y[4 * q + 2] + v.z;
+                y[4 * q + 3] = y[4 * q + 3] + v.w;
+            }
         }
     }
-    const int col = nt32 * 32 + r32;
-    if (col >= n) return;
+}
+
+// One 32 (m) x 32 (n) output tile per workgroup of S waves; wave s takes the
+// groups g = s, s + S, s + 2S, ... (one per round).  Tiles are numbered so
+// that the workgroups one XCD receives (workgroup ids congruent mod 8) cover
+// a contiguous run of n-tiles over all m-tiles: each XCD's L2 holds its own
+// slice of the weight.  Operand lane l: row l % 32 of the 32-row tile, codes
+// of half l / 32 of the block (A and B split the block's 32 k-values alike,
+// so the int32 dot is exact).  Accumulator layout: lane l holds column
+// l % 32, register i holds row 8 * (i / 4) + 4 * (l / 32) + i % 4.
+template <int S>
+__global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(3))) void k_gemm(GemmArgs g) {
+    __shared__ float4 part[2][S > 1 ? S - 1 : 1][4][64];
+    const int lane = threadIdx.x & 63;
+    const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wgi = blockIdx.x, per = g.ntiles >> 3, rem = g.ntiles & 7, xcd = wgi & 7, j8 = wgi >> 3;
+    const int tl = xcd < rem ? xcd * (per + 1) + j8 : rem * (per + 1) + (xcd - rem) * per + j8;
+    const int nt = tl / g.ntm, mt = tl - nt * g.ntm;
+    const int half = lane >> 5, r32 = lane & 31;
+    const bool lo = lane < 32;
+    const int nb = g.nb, G = g.groups;
+    GemmSrc o;
+    o.ra = __builtin_amdgcn_make_buffer_rsrc((void*)g.xq, (short)0, g.xq_bytes, RSRC_CFG);
+    o.rb = __builtin_amdgcn_make_buffer_rsrc((void*)g.wc, (short)0, g.wc_bytes, RSRC_CFG);
+    o.rx = __builtin_amdgcn_make_buffer_rsrc((void*)g.xs, (short)0, g.xs_bytes, RSRC_CFG);
+    o.rw = __builtin_amdgcn_make_buffer_rsrc((void*)g.ws, (short)0, g.ws_bytes, RSRC_CFG);
+    o.oa = ((mt * 2 + (r32 >> 4)) * g.np * 64 + half * 16 + (r32 & 15)) * 16;
+    o.ob = ((nt * 2 + (r32 >> 4)) * g.np * 64 + half * 16 + (r32 & 15)) * 16;
+    o.ox = (mt * 2 * G * 64 + lane) * 16;
+    o.ow = ((nt * 2 + (r32 >> 4)) * 2 * g.np * 16 + (r32 & 15)) * 2;
+
+    float y[16], acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) y[r] = 0.0f;
+    Quad q0, q1;
+    const int R = (G + S - 1) / S;
+    {
+        const int g0 = min(s, G - 1);
+        gemm_load(o, g0 * GEMM_GROUP, nb, q0);
+        gemm_load(o, g0 * GEMM_GROUP + 4, nb, q1);
+    }
+    for (int j = 0; j + 1 < R; j++) {
+        gemm_group<true>(o, j * S + s, min((j + 1) * S + s, G - 1), nb, lo, q0, q1, acc);
+        gemm_combine<S>(part, j, s, lane, G, acc, y);
+    }
+    if (s == 0 || (R - 1) * S + s < G) gemm_group<false>(o, (R - 1) * S + s, 0, nb, lo, q0, q1, acc);
+    gemm_combine<S>(part, R - 1, s, lane, G, acc, y);
+
+    if (s != 0) return;
+    const int col = nt * 32 + r32;
+    if (col >= g.n) return;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-        const int row = mt32 * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
-        if (row < m) {
-            const size_t o = (size_t)row * n + col;
-            float v = yacc[i];
-            if (resid) v = resid[o] + v;
-            y[o] = v;
+        const int row = mt * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
+        if (row < g.m) {
+            const size_t off = (size_t)row * g.n + col;
+            float v = y[i];
+            if (g.resid) v = g.resid[off] + v;
+            g.y[off] = v;
         }
     }
 }
@@ -259,15 +392,18 @@ size_t act_code_bytes(int m, int k) {
     const size_t np = ((size_t)k / 32 + 1) / 2;
     return (size_t)((m + 31) / 32) * 2 * np * CHUNK_BYTES;
 }
+// [m/32][nbp/4][64][4] u32 with nbp = 8 * groups: 1 KiB per 32 rows and 4 blocks.
 size_t act_scale_bytes(int m, int k) {
-    const size_t np = ((size_t)k / 32 + 1) / 2;
-    return (size_t)((m + 31) / 32) * 2 * 2 * np * 16 * sizeof(float);
+    const size_t groups = ((size_t)k / 32 + GEMM_GROUP - 1) / GEMM_GROUP;
+    return (size_t)((m + 31) / 32) * 2 * groups * 1024;
 }
 
-lq8_status launch_quantize_act(hipStream_t s, const float* x, int m, int k, int8_t* codes, float* scales32) {
-    const size_t n = (size_t)m * (k / 32);
-    if (!n) return LQ8_OK;
-    hipLaunchKernelGGL(k_quantize_act, dim3(grid1(n, WG)), dim3(WG), 0, s, x, m, k, codes, scales32);
+lq8_status launch_quantize_act(hipStream_t s, const float* x, int m, int k, int8_t* codes, uint32_t* scales) {
+    const int groups = (k / 32 + GEMM_GROUP - 1) / GEMM_GROUP;
+    const size_t waves = (size_t)((m + 31) / 32) * 2 * (4 * groups);
+    if (!waves) return LQ8_OK;
+    hipLaunchKernelGGL(k_quantize_act, dim3(grid1(waves, 4)), dim3(256), 0, s, x, m, k, (int)waves, 4 * groups,
+                       codes, scales);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
@@ -279,11 +415,48 @@ lq8_status launch_quantize_aos(hipStream_t s, const float* x, size_t nblocks, ui
     return LQ8_OK;
 }
 
-lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const float* xs, int m, const lq8_weight* w, float* y,
+lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const uint32_t* xs, int m, const lq8_weight* w, float* y,
                        const float* resid) {
-    const dim3 grid((unsigned)((w->n_out + 63) / 64), (unsigned)((m + 63) / 64));
-    hipLaunchKernelGGL(k_gemm, grid, dim3(WG), 0, s, xq, xs, m, w->codes, w->scales, (int)w->n_out, (int)w->nb, y,
-                       resid);
+    const size_t k = w->k_in;
+    const size_t xq_bytes = act_code_bytes(m, (int)k), xs_bytes = act_scale_bytes(m, (int)k);
+    const size_t wc_bytes = w->tiles * w->np * CHUNK_BYTES, ws_bytes = w->tiles * 2 * w->np * TILE_ROWS * 2;
+    const size_t lim = (size_t)INT32_MAX;
+    if (xq_bytes > lim || xs_bytes > lim || wc_bytes > lim || ws_bytes > lim)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "gemm: operand larger than 2 GiB");
+    GemmArgs g;
+    g.xq = xq;
+    g.xs = xs;
+    g.wc = w->codes;
+    g.ws = w->scales;
+    g.y = y;
+    g.resid = resid;
+    g.m = m;
+    g.n = (int)w->n_out;
+    g.nb = (int)w->nb;
+    g.np = (int)w->np;
+    g.groups = (g.nb + GEMM_GROUP - 1) / GEMM_GROUP;
+    g.ntm = (m + 31) / 32;
+    const int ntn = (g.n + 31) / 32;
+    if ((size_t)g.ntm * ntn > lim) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemm: too many tiles");
+    g.ntiles = g.ntm * ntn;
+    g.xq_bytes = (int)xq_bytes;
+    g.xs_bytes = (int)xs_bytes;
+    g.wc_bytes = (int)wc_bytes;
+    g.ws_bytes = (int)ws_bytes;
+    // K-split: the fewest waves per tile (at least 2 when K spans more than one
+    // group: the single-wave variant runs short of registers in its round loop)
+    // that give >= 2 waves per SIMD (1024 SIMDs).
+    int S = g.groups > 1 ? 2 : 1;
+    while (S < 8 && S < g.groups && (size_t)g.ntiles * S < 2048) S = S == 4 ? 6 : S == 6 ? 8 : S + 1;
+    const dim3 grid((unsigned)g.ntiles);
+    switch (S) {
+        case 1: hipLaunchKernelGGL(k_gemm<1>, grid, dim3(64), 0, s, g); break;
+        case 2: hipLaunchKernelGGL(k_gemm<2>, grid, dim3(128), 0, s, g); break;
+        case 3: hipLaunchKernelGGL(k_gemm<3>, grid, dim3(192), 0, s, g); break;
+        case 4: hipLaunchKernelGGL(k_gemm<4>, grid, dim3(256), 0, s, g); break;
+        case 6: hipLaunchKernelGGL(k_gemm<6>, grid, dim3(384), 0, s, g); break;
+        default: hipLaunchKernelGGL(k_gemm<8>, grid, dim3(512), 0, s, g); break;
+    }
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

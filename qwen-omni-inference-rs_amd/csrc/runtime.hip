@@ -459,7 +459,7 @@ lq8_status lq8_gemm_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* 
     lq8_status st = ctx_scratch(ctx, code_bytes + scale_bytes, &sc);
     if (st) return st;
     int8_t* xq = (int8_t*)sc;
-    float* xs = (float*)((char*)sc + code_bytes);
+    uint32_t* xs = (uint32_t*)((char*)sc + code_bytes);
     st = launch_quantize_act(ctx->stream, d_x, (int)m, (int)w->k_in, xq, xs);
     if (st) return st;
     return launch_gemm(ctx->stream, xq, xs, (int)m, w, d_y, nullptr);

@@ -163,6 +163,30 @@ def test_gemm_ragged(ctx, m, n, k):
     assert_parity(y, ref)
 
 
+def test_gemm_scale_edge_cases(ctx):
+    """Activation and weight blocks whose f16 scales are subnormal (amax
+    below 127 * 2^-14) or zero, NaN entries (ignored by amax), and a block
+    count that is neither even nor a multiple of the 8-block group."""
+    m, n, k = 45, 70, 32 * 11
+    wf = normal((n, k), 0.02, 40)
+    wf[::3] *= np.float32(1e-3)          # weight scales ~5e-7: f16 subnormal
+    wf[5, :64] = 0.0                    # two all-zero weight blocks
+    x = normal((m, k), 1.0, 41)
+    x *= np.float32(10.0) ** -(np.arange(m) % 7).astype(np.float32)[:, None]   # down to 1e-6
+    x[3, 32:64] = 0.0                   # zero activation block
+    x[4, 7] = np.nan                    # NaN is ignored by amax; its code follows the quantizer
+    blocks = oracle.quantize_q8_0(wf)
+    w = lq8.Q8Weight.from_blocks(ctx, blocks, n, k)
+    dx = lq8.DeviceBuffer.from_array(ctx, x)
+    dy = lq8.DeviceBuffer(ctx, m * n * 4)
+    lq8._check(lq8.lib().lq8_gemm_q8_0_device(ctx.handle, w.handle, dx.ptr, m, dy.ptr))
+    y = dy.download(np.float32, m * n).reshape(m, n)
+    dx.free(); dy.free(); w.free()
+    ref = oracle.gemm_q8_0(blocks, n, k, x)
+    bad = np.flatnonzero(y.view(np.uint32) != ref.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} elements differ, first at {bad[:5]}: {y.ravel()[bad[:5]]} vs {ref.ravel()[bad[:5]]}"
+
+
 def test_gemm_int_blocks_exact(ctx):
     """Per-block int32 sums are exact: with d_w = d_x = 1 (a 127 in every
     block) the f32 result is the integer dot product itself."""
