@@ -189,6 +189,57 @@ lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_pr
                                uint32_t* out_tokens, lq8_gen_stats* stats);
 lq8_status lq8_model_free(lq8_model* m);
 
+/* ---- Qwen3-MoE decoder layers (Qwen3-30B-A3B style), decode steps --------
+ * No reference counterpart: the reference has no MoE code.  The layer is
+ * assembled from the reference's decoder numerics (src/transformer.rs:180-204,
+ * src/attention.rs:318-403, src/mlp.rs:151-164) with a routed expert MLP.
+ * A forward call decodes one token for each of T independent sequences
+ * (sequence t owns KV cache slot t and writes position pos[t]); every
+ * projection is applied per token (the W8A32 GEMV order), so a token's
+ * result does not depend on the rest of the batch.
+ * Router, from given scores s [T][num_experts] per layer: p = softmax(s)
+ * (max, exp(s - max), SUM64 denominator, divide); top_k by p descending,
+ * ties to the lower expert index; weights renormalised over the top_k in
+ * rank order.  Experts combine in ascending expert index:
+ * out = h2 + ((0 + w_a * y_a) + w_b * y_b) + ...  */
+typedef struct lq8_moe lq8_moe;
+typedef struct {
+    uint32_t hidden_size, num_heads, num_kv_heads, head_dim;
+    uint32_t num_experts, top_k, expert_intermediate_size;
+    uint32_t max_positions; /* KV capacity per sequence */
+    uint32_t max_batch;     /* sequences per forward call */
+    uint32_t num_layers;
+    float rms_norm_eps;
+    double rope_theta;
+} lq8_moe_config;
+
+/* Tensor table (host pointers), layer l at base (8 + 3 * num_experts) * l:
+ *   +0 input_layernorm f32 [hidden]  +1 post_attention_layernorm f32 [hidden]
+ *   +2 q_norm f32 [head_dim]          +3 k_norm f32 [head_dim]
+ *   +4 q_proj +5 k_proj +6 v_proj +7 o_proj (Q8_0)
+ *   +8 + e  expert e gate_proj Q8_0 [expert_intermediate, hidden]
+ *   +8 + E + e  up_proj (same shape), +8 + 2E + e  down_proj [hidden, expert_intermediate] */
+size_t lq8_moe_tensor_count(const lq8_moe_config* cfg);
+lq8_status lq8_moe_tensor_bytes(const lq8_moe_config* cfg, size_t index, size_t* bytes);
+lq8_status lq8_moe_create(lq8_ctx* ctx, const lq8_moe_config* cfg, const void* const* tensors, lq8_moe** out);
+/* Q8_0 weights N(0, std) from a seeded counter generator, norms 1. */
+lq8_status lq8_moe_create_random(lq8_ctx* ctx, const lq8_moe_config* cfg, uint64_t seed, float std, lq8_moe** out);
+lq8_status lq8_moe_export_tensor(lq8_moe* m, size_t index, void* host_out);
+/* Q8_0 bytes of all layers' weights (attention + every expert). */
+lq8_status lq8_moe_weight_bytes(lq8_moe* m, size_t* bytes);
+/* Device pointers: hidden [T][hidden] (input, overwritten by the last layer's
+ * output), scores [num_layers][T][num_experts], pos [T] (each < max_positions).
+ * Enqueued on the context stream; no host synchronisation. */
+lq8_status lq8_moe_forward_device(lq8_moe* m, float* d_hidden, const float* d_scores, const int32_t* d_pos, size_t T);
+/* Host arrays; synchronous. */
+lq8_status lq8_moe_forward(lq8_moe* m, float* hidden, const float* scores, const int32_t* pos, size_t T);
+/* Routing of the last forward: experts [num_layers][T][top_k] in rank order and
+ * their renormalised weights (host arrays). */
+lq8_status lq8_moe_routing(lq8_moe* m, uint32_t* experts, float* weights);
+/* Zero every KV cache slot. */
+lq8_status lq8_moe_clear_kv_cache(lq8_moe* m);
+lq8_status lq8_moe_free(lq8_moe* m);
+
 #ifdef __cplusplus
 }
 #endif

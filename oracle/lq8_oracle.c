@@ -477,11 +477,7 @@ void orc_model_clear_kv_cache(orc_model* m) { m->kv_len = 0; }
  *   out[d] = num[d] / den.
  * With the plain sequential sums switch on, the reference's order is used. */
 #define ORC_ATT_SEG 64
-static void attend(const orc_model* m, size_t layer, size_t kvh, const float* q, size_t L, float* out, float* sc) {
-    const orc_qwen3_config* c = &m->c;
-    size_t hd = c->head_dim, P = c->max_positions;
-    const float* K = m->kc + ((layer * c->num_kv_heads + kvh) * P) * hd;
-    const float* V = m->vc + ((layer * c->num_kv_heads + kvh) * P) * hd;
+static void attend_kv(const float* K, const float* V, size_t hd, const float* q, size_t L, float* out, float* sc) {
     float scale = 1.0f / sqrtf((float)hd);
     if (g_seq_sums) {
         float mx = -INFINITY;
@@ -528,6 +524,13 @@ static void attend(const orc_model* m, size_t layer, size_t kvh, const float* q,
         run_m = mn;
     }
     for (size_t d = 0; d < hd; d++) out[d] = out[d] / den;
+}
+
+static void attend(const orc_model* m, size_t layer, size_t kvh, const float* q, size_t L, float* out, float* sc) {
+    const orc_qwen3_config* c = &m->c;
+    size_t hd = c->head_dim, P = c->max_positions;
+    attend_kv(m->kc + ((layer * c->num_kv_heads + kvh) * P) * hd, m->vc + ((layer * c->num_kv_heads + kvh) * P) * hd,
+              hd, q, L, out, sc);
 }
 
 static int model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t offset, float* logits, float* hidden,
@@ -659,5 +662,159 @@ int orc_generate_greedy(orc_model* m, const uint32_t* prompt, size_t n_prompt, s
         }
     }
     free(logits);
+    return rc;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Qwen3-MoE decoder layer, decode step of T independent sequences           */
+/* ------------------------------------------------------------------------ */
+/* No MoE code exists in the reference; the layer is the Qwen3-MoE block
+ * (Qwen3-30B-A3B style) assembled from the reference's decoder numerics above
+ * (src/transformer.rs:180-204 residual structure, src/attention.rs:318-403
+ * attention, src/mlp.rs:151-164 SwiGLU) with these choices, which the GPU
+ * path follows bit for bit:
+ *   - every projection is applied per token (M = 1, the W8A32 GEMV order), so
+ *     a token's result does not depend on the other tokens of the batch;
+ *   - router: m = max s, e_i = exp(s_i - m), S = SUM64(e), p_i = e_i / S;
+ *     top-k by p, descending, ties to the lower expert index; the k weights
+ *     are renormalised: w_r = p_r / (((p_0 + p_1) + p_2) + ...) in rank order;
+ *   - expert e: y_e = down(silu(gate x) * up x), x = post-attention RmsNorm;
+ *   - combine in ascending expert index: acc = 0; acc = acc + w_e * y_e;
+ *     out = h2 + acc (h2 = input + attention output). */
+
+struct orc_moe {
+    orc_moe_config c;
+    const void* const* t; /* per layer: 8 + 3E pointers */
+    float *cos_t, *sin_t;
+    float *kc, *vc; /* [layer][seq][kv_head][max_pos][head_dim] */
+};
+
+orc_moe* orc_moe_new(const orc_moe_config* cfg, const void* const* tensors) {
+    orc_moe* m = (orc_moe*)calloc(1, sizeof(orc_moe));
+    if (!m) return NULL;
+    m->c = *cfg;
+    m->t = tensors;
+    size_t hd = cfg->head_dim, R = hd / 2;
+    m->cos_t = (float*)malloc((size_t)cfg->max_positions * R * sizeof(float));
+    m->sin_t = (float*)malloc((size_t)cfg->max_positions * R * sizeof(float));
+    size_t kvsz = (size_t)cfg->num_layers * cfg->max_batch * cfg->num_kv_heads * cfg->max_positions * hd;
+    m->kc = (float*)calloc(kvsz, sizeof(float));
+    m->vc = (float*)calloc(kvsz, sizeof(float));
+    if (!m->cos_t || !m->sin_t || !m->kc || !m->vc) { orc_moe_free(m); return NULL; }
+    orc_rope_tables(hd, cfg->max_positions, cfg->rope_theta, m->cos_t, m->sin_t);
+    return m;
+}
+
+void orc_moe_free(orc_moe* m) {
+    if (!m) return;
+    free(m->cos_t); free(m->sin_t); free(m->kc); free(m->vc);
+    free(m);
+}
+
+int orc_moe_route(const float* scores, size_t T, size_t E, size_t k, uint32_t* ids, float* weights) {
+    if (E == 0 || k == 0 || k > E) return 1;
+    float* e = (float*)malloc(E * sizeof(float));
+    unsigned char* used = (unsigned char*)malloc(E);
+    if (!e || !used) { free(e); free(used); return 2; }
+    for (size_t t = 0; t < T; t++) {
+        const float* s = scores + t * E;
+        float mx = -INFINITY;
+        for (size_t i = 0; i < E; i++) if (s[i] > mx) mx = s[i];
+        for (size_t i = 0; i < E; i++) e[i] = orc_expf(s[i] - mx);
+        float S = sum64(e, E);
+        for (size_t i = 0; i < E; i++) { e[i] = e[i] / S; used[i] = 0; }
+        float tot = 0.0f;
+        for (size_t r = 0; r < k; r++) {
+            size_t best = E;
+            for (size_t i = 0; i < E; i++)
+                if (!used[i] && (best == E || e[i] > e[best])) best = i;
+            used[best] = 1;
+            ids[t * k + r] = (uint32_t)best;
+            weights[t * k + r] = e[best];
+            tot = tot + e[best];
+        }
+        for (size_t r = 0; r < k; r++) weights[t * k + r] = weights[t * k + r] / tot;
+    }
+    free(e); free(used);
+    return 0;
+}
+
+int orc_moe_forward(orc_moe* m, float* hidden, const float* scores, const uint32_t* pos, size_t T) {
+    const orc_moe_config* c = &m->c;
+    size_t H = c->hidden_size, hd = c->head_dim, NH = c->num_heads, NKV = c->num_kv_heads;
+    size_t E = c->num_experts, K = c->top_k, I = c->expert_intermediate_size, P = c->max_positions;
+    size_t QD = NH * hd, KD = NKV * hd, R = hd / 2, groups = NH / NKV;
+    if (T == 0 || T > c->max_batch) return 1;
+    for (size_t t = 0; t < T; t++) if (pos[t] >= P) return 3;
+    float* X = (float*)malloc(H * sizeof(float));
+    float* Q = (float*)malloc(QD * sizeof(float));
+    float* Kx = (float*)malloc(KD * sizeof(float));
+    float* Vx = (float*)malloc(KD * sizeof(float));
+    float* A = (float*)malloc(QD * sizeof(float));
+    float* O = (float*)malloc(H * sizeof(float));
+    float* G = (float*)malloc(I * sizeof(float));
+    float* U = (float*)malloc(I * sizeof(float));
+    float* Y = (float*)malloc(H * sizeof(float));
+    float* acc = (float*)malloc(H * sizeof(float));
+    float* sc = (float*)malloc((P > H ? P : H) * 2 * sizeof(float));
+    float* tmp = (float*)malloc(hd * sizeof(float));
+    uint32_t* ids = (uint32_t*)malloc(T * K * sizeof(uint32_t));
+    float* wts = (float*)malloc(T * K * sizeof(float));
+    int rc = 0;
+    if (!X || !Q || !Kx || !Vx || !A || !O || !G || !U || !Y || !acc || !sc || !tmp || !ids || !wts) { rc = 2; goto done; }
+    for (size_t l = 0; l < c->num_layers; l++) {
+        const void* const* b = m->t + (8 + 3 * E) * l;
+        const float *in_norm = (const float*)b[0], *post_norm = (const float*)b[1];
+        const float *q_norm = (const float*)b[2], *k_norm = (const float*)b[3];
+        orc_moe_route(scores + l * T * E, T, E, K, ids, wts);
+        for (size_t t = 0; t < T; t++) {
+            float* h = hidden + t * H;
+            size_t p = pos[t];
+            float* kc = m->kc + ((l * c->max_batch + t) * NKV) * P * hd;
+            float* vc = m->vc + ((l * c->max_batch + t) * NKV) * P * hd;
+            orc_rms_norm(h, in_norm, 1, H, c->rms_norm_eps, X);
+            orc_gemv_q8_0((const uint8_t*)b[4], QD, H, X, Q);
+            orc_gemv_q8_0((const uint8_t*)b[5], KD, H, X, Kx);
+            orc_gemv_q8_0((const uint8_t*)b[6], KD, H, X, Vx);
+            const float* cs = m->cos_t + p * R;
+            const float* sn = m->sin_t + p * R;
+            for (size_t hh = 0; hh < NH + NKV; hh++) {
+                int isq = hh < NH;
+                float* src = isq ? Q + hh * hd : Kx + (hh - NH) * hd;
+                rms_norm_row(src, isq ? q_norm : k_norm, hd, c->rms_norm_eps, tmp, sc);
+                float* dst = isq ? src : kc + ((hh - NH) * P + p) * hd;
+                for (size_t d = 0; d < R; d++) {
+                    float cv = cs[d & ~(size_t)1], sv = sn[d & ~(size_t)1];
+                    float x1 = tmp[d], x2 = tmp[d + R];
+                    dst[d] = x1 * cv - x2 * sv;
+                    dst[d + R] = x2 * cv + x1 * sv;
+                }
+            }
+            for (size_t hh = 0; hh < NKV; hh++) memcpy(vc + (hh * P + p) * hd, Vx + hh * hd, hd * sizeof(float));
+            for (size_t hh = 0; hh < NH; hh++) {
+                size_t kvh = hh / groups;
+                attend_kv(kc + kvh * P * hd, vc + kvh * P * hd, hd, Q + hh * hd, p + 1, A + hh * hd, sc);
+            }
+            orc_gemv_q8_0((const uint8_t*)b[7], H, QD, A, O);
+            for (size_t i = 0; i < H; i++) h[i] = h[i] + O[i];   /* h2 */
+            orc_rms_norm(h, post_norm, 1, H, c->rms_norm_eps, X);
+            for (size_t i = 0; i < H; i++) acc[i] = 0.0f;
+            for (size_t e = 0; e < E; e++) {
+                float w = 0.0f;
+                int hit = 0;
+                for (size_t r = 0; r < K; r++) if (ids[t * K + r] == e) { w = wts[t * K + r]; hit = 1; }
+                if (!hit) continue;
+                orc_gemv_q8_0((const uint8_t*)b[8 + e], I, H, X, G);
+                orc_gemv_q8_0((const uint8_t*)b[8 + E + e], I, H, X, U);
+                for (size_t i = 0; i < I; i++) G[i] = orc_silu(G[i]) * U[i];
+                orc_gemv_q8_0((const uint8_t*)b[8 + 2 * E + e], H, I, G, Y);
+                for (size_t i = 0; i < H; i++) acc[i] = acc[i] + w * Y[i];
+            }
+            for (size_t i = 0; i < H; i++) h[i] = h[i] + acc[i];
+        }
+    }
+done:
+    free(X); free(Q); free(Kx); free(Vx); free(A); free(O); free(G); free(U); free(Y); free(acc); free(sc); free(tmp);
+    free(ids); free(wts);
     return rc;
 }

@@ -81,6 +81,25 @@ int orc_model_forward_with_intermediates(orc_model* m, const uint32_t* ids, size
 int orc_generate_greedy(orc_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
                         uint32_t* out_tokens, float* out_margins);
 
+/* ---- Qwen3-MoE decoder layers (decode step of T independent sequences) ----
+ * Tensor table, per layer l, base = (8 + 3 * num_experts) * l:
+ *   +0 input_layernorm f32 [hidden]  +1 post_attention_layernorm f32 [hidden]
+ *   +2 q_norm f32 [head_dim]          +3 k_norm f32 [head_dim]
+ *   +4 q_proj  +5 k_proj  +6 v_proj  +7 o_proj  (Q8_0)
+ *   +8 + e gate_proj of expert e, +8 + E + e up_proj, +8 + 2E + e down_proj
+ * Sequence t of a batch owns KV cache slot t; it is written at pos[t]. */
+typedef struct {
+    uint32_t hidden_size, num_heads, num_kv_heads, head_dim;
+    uint32_t num_experts, top_k, expert_intermediate_size, max_positions, max_batch, num_layers;
+    float rms_norm_eps;
+    double rope_theta;
+} orc_moe_config;
+typedef struct orc_moe orc_moe;
+orc_moe* orc_moe_new(const orc_moe_config* cfg, const void* const* tensors);
+void orc_moe_free(orc_moe* m);
+int orc_moe_route(const float* scores, size_t T, size_t E, size_t k, uint32_t* ids, float* weights);
+int orc_moe_forward(orc_moe* m, float* hidden, const float* scores, const uint32_t* pos, size_t T);
+
 #ifdef __cplusplus
 }
 #endif

@@ -28,6 +28,15 @@ class OrcConfig(C.Structure):
     ]
 
 
+class OrcMoeConfig(C.Structure):
+    _fields_ = [
+        ("hidden_size", C.c_uint32), ("num_heads", C.c_uint32), ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32), ("num_experts", C.c_uint32), ("top_k", C.c_uint32),
+        ("expert_intermediate_size", C.c_uint32), ("max_positions", C.c_uint32), ("max_batch", C.c_uint32),
+        ("num_layers", C.c_uint32), ("rms_norm_eps", C.c_float), ("rope_theta", C.c_double),
+    ]
+
+
 _lib = None
 
 
@@ -65,6 +74,10 @@ def lib():
             "orc_model_forward": (C.c_int, [vp, vp, sz, sz, vp]),
             "orc_model_forward_with_intermediates": (C.c_int, [vp, vp, sz, sz, vp, vp, vp]),
             "orc_generate_greedy": (C.c_int, [vp, vp, sz, sz, vp, vp]),
+            "orc_moe_new": (vp, [C.POINTER(OrcMoeConfig), vp]),
+            "orc_moe_free": (None, [vp]),
+            "orc_moe_route": (C.c_int, [vp, sz, sz, sz, vp, vp]),
+            "orc_moe_forward": (C.c_int, [vp, vp, vp, vp, sz]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(L, name)
@@ -262,3 +275,50 @@ def random_q8_tensors(cfg, seed: int, std: float = 0.02):
             w = (rng.standard_normal(shape) * std).astype(np.float32)
             out.append(quantize_q8_0(w))
     return out
+
+
+def moe_route(scores, top_k: int):
+    """Router of the MoE layer: scores [T, E] -> (expert ids [T, k] in rank
+    order, renormalised weights [T, k])."""
+    scores = np.ascontiguousarray(scores, dtype=np.float32)
+    T, E = scores.shape
+    ids = np.empty((T, top_k), dtype=np.uint32)
+    w = np.empty((T, top_k), dtype=np.float32)
+    if lib().orc_moe_route(_p(scores), T, E, top_k, _p(ids), _p(w)):
+        raise ValueError("bad router shape")
+    return ids, w
+
+
+class MoeStack:
+    """Oracle Qwen3-MoE decoder layers over host tensors (table order of
+    orc_moe_new: per layer 4 f32 norms, q/k/v/o, then gate[E], up[E], down[E]
+    as Q8_0 blocks); one KV cache slot per sequence of the batch."""
+
+    def __init__(self, cfg, tensors: Sequence[np.ndarray]):
+        self.cfg = cfg
+        self._keep = [np.ascontiguousarray(t) for t in tensors]
+        self._arr = (C.c_void_p * len(self._keep))(*[t.ctypes.data for t in self._keep])
+        self._c = OrcMoeConfig(cfg.hidden_size, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.num_experts,
+                               cfg.top_k, cfg.expert_intermediate_size, cfg.max_positions, cfg.max_batch,
+                               cfg.num_layers, cfg.rms_norm_eps, cfg.rope_theta)
+        self.h = lib().orc_moe_new(C.byref(self._c), self._arr)
+        if not self.h:
+            raise MemoryError("oracle MoE allocation failed")
+
+    def close(self):
+        if self.h:
+            lib().orc_moe_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def forward(self, hidden, scores, pos):
+        """hidden [T, H] (returned updated), scores [layers, T, E], pos [T]."""
+        h = np.array(hidden, dtype=np.float32, copy=True, order="C")
+        sc = np.ascontiguousarray(scores, dtype=np.float32)
+        p = np.ascontiguousarray(pos, dtype=np.uint32)
+        rc = lib().orc_moe_forward(self.h, _p(h), _p(sc), _p(p), p.size)
+        if rc:
+            raise ValueError(f"oracle MoE forward failed ({rc})")
+        return h

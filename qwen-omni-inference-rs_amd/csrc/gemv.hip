@@ -88,7 +88,7 @@ struct Stage {
             }
         } else {
             const int H = a.attn_heads;
-            const int C = (a.d_pos ? *a.d_pos : a.pos_base) / ATT_SEG + 1;
+            const int C = min(max(a.d_pos ? *a.d_pos : a.pos_base, 0) / ATT_SEG + 1, a.attn_cmax);
             const int h = min(tid, H - 1);
             if (wave * 64 < H) {
 #pragma unroll
@@ -176,7 +176,7 @@ struct Stage {
             // m' = max(m, m_c), a = exp(m - m'), b = exp(m_c - m'),
             // num = num * a + b * o_c, den = den * a + b * l_c; x = num / den.
             const int H = a.attn_heads;
-            const int C = (a.d_pos ? *a.d_pos : a.pos_base) / ATT_SEG + 1;
+            const int C = min(max(a.d_pos ? *a.d_pos : a.pos_base, 0) / ATT_SEG + 1, a.attn_cmax);
             float* coef = red + 4;                     // [C][H][2]
             float* dens = coef + a.attn_cmax * H * 2;  // [H]
             for (int h = tid; h < H; h += nt) {
@@ -384,6 +384,157 @@ __global__ __launch_bounds__(256) void k_gemv_grouped(const GemvProblemDev* __re
     gemv_tiles<XS_PLAIN, EPI_STORE, MAX_CH>(a, t - p.tile_begin, 1, smem);
 }
 
+// ---- multi-vector GEMV ------------------------------------------------------
+//
+// One workgroup (4 waves) per (problem, 16-row tile, vector split).  Up to VB
+// input vectors are staged in LDS at a time; a wave takes (group of CH pairs)
+// items, unpacks each 16-byte code chunk to floats once and runs the GEMV
+// order of gemv_tiles for every staged vector; the group sums go to LDS and
+// one thread per (vector, row) runs the tree over the groups.
+template <int XS, int EPI, int CH, int VB>
+__global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
+    extern __shared__ float smem[];
+    const int tiles_p = (a.rows + TILE_ROWS - 1) / TILE_ROWS;
+    const int j = blockIdx.x / tiles_p, tile = blockIdx.x - j * tiles_p;
+    if (j >= (a.n_prob ? *a.n_prob : 1)) return;
+    const int e = a.prob_id ? a.prob_id[j] : j;
+    const int vbeg = a.vec_begin ? a.vec_begin[j] : 0;
+    const int vcnt = a.vec_count ? a.vec_count[j] : a.nvec;
+    if ((int)blockIdx.y * VB >= vcnt) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int k = a.k, k4 = k >> 2, nb = k >> 5, np = (nb + 1) >> 1;
+    const int G = (np + CH - 1) / CH;
+    float* xs = smem;                    // [VB][np * 64]
+    float* gs = xs + VB * np * 64;       // [VB][G][16]
+    float* red = gs + VB * G * 16;       // [VB]
+    const int r = lane & 15, part = lane >> 4, bsel = part >> 1, half = part & 1;
+    const size_t gt = (size_t)e * a.prob_tiles + tile;
+    const int8_t* cbase = a.codes + gt * np * CHUNK_BYTES + lane * 16;
+    const uint16_t* sbase = a.scales + gt * 2 * np * 16 + bsel * 16 + r;
+    for (int v0 = blockIdx.y * VB; v0 < vcnt; v0 += gridDim.y * VB) {
+        const int nv = min(VB, vcnt - v0);
+        // ---- stage nv vectors (transform per XS) ----
+        for (int v = 0; v < nv; v++) {
+            const int ent = vbeg + v0 + v;
+            const int slot = a.slots ? a.slots[ent] : ent;
+            const float* x = a.x + (size_t)(slot / a.x_div) * a.x_stride;
+            float* xv = xs + v * np * 64;
+            for (int i4 = tid; i4 < k4; i4 += 256) {
+                const float4 g = *(const float4*)(x + 4 * i4);
+                float4 o;
+                if (XS == XS_SILU) {
+                    const float4 u = *(const float4*)(x + k + 4 * i4);
+                    o = make_float4(silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w));
+                } else if (XS == XS_RMSNORM) {
+                    o = bf16_round4(g);
+                } else {
+                    o = g;
+                }
+                *(float4*)(xv + 4 * i4) = o;
+            }
+            if ((nb & 1) && tid < 32) xv[k + tid] = 0.0f;
+        }
+        __syncthreads();
+        if (XS == XS_RMSNORM) {
+            // SUM64 order per vector (wave v), as the single-vector staging
+            if (wave < nv) {
+                const float* xv = xs + wave * np * 64;
+                float acc = 0.0f;
+                for (int i = lane; i < k; i += 64) {
+                    const float v = xv[i];
+                    acc = acc + v * v;
+                }
+#pragma unroll
+                for (int d = 32; d >= 1; d >>= 1) acc = acc + __shfl_xor(acc, d, 64);
+                if (lane == 0) red[wave] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)k) + a.eps));
+            }
+            __syncthreads();
+            for (int v = 0; v < nv; v++) {
+                const float inv = red[v];
+                float* xv = xs + v * np * 64;
+                for (int i4 = tid; i4 < k4; i4 += 256) {
+                    float4* p = (float4*)(xv + 4 * i4);
+                    *p = norm4(*p, *(const float4*)(a.norm_w + 4 * i4), inv);
+                }
+            }
+            __syncthreads();
+        }
+        // ---- items: (group of CH pairs) ----
+        for (int g = wave; g < G; g += 4) {
+            u32x4 cv[CH];
+            uint16_t ds[CH];
+#pragma unroll
+            for (int i = 0; i < CH; i++) {
+                const int c = min(g * CH + i, np - 1);
+                cv[i] = __builtin_nontemporal_load((const u32x4*)(cbase + (size_t)c * CHUNK_BYTES));
+                ds[i] = sbase[(size_t)c * 32];
+            }
+            float wf[CH][16];
+#pragma unroll
+            for (int i = 0; i < CH; i++) {
+                const uint32_t w4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    wf[i][4 * q] = (float)(int8_t)(w4[q] & 0xFF);
+                    wf[i][4 * q + 1] = (float)(int8_t)((w4[q] >> 8) & 0xFF);
+                    wf[i][4 * q + 2] = (float)(int8_t)((w4[q] >> 16) & 0xFF);
+                    wf[i][4 * q + 3] = (float)(int8_t)(w4[q] >> 24);
+                }
+            }
+            const int cnt = min(CH, np - g * CH);
+            for (int v = 0; v < nv; v++) {
+                const float* xv = xs + v * np * 64;
+                float t[CH];
+#pragma unroll
+                for (int i = 0; i < CH; i++) {
+                    const int p = min(g * CH + i, np - 1);
+                    const float* xp = xv + (2 * p + bsel) * 32 + half * 16;
+                    float h = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 xq = *(const float4*)(xp + 4 * q);
+                        h = fmaf(wf[i][4 * q], xq.x, h);
+                        h = fmaf(wf[i][4 * q + 1], xq.y, h);
+                        h = fmaf(wf[i][4 * q + 2], xq.z, h);
+                        h = fmaf(wf[i][4 * q + 3], xq.w, h);
+                    }
+                    const float o = __shfl_xor(h, 16, 64);
+                    const float h0 = half ? o : h, h1 = half ? h : o;
+                    const float vb = (h0 + h1) * f16_bits_to_f32(ds[i]);
+                    const float ov = __shfl_xor(vb, 32, 64);
+                    if (2 * p + 1 >= nb) t[i] = bsel ? ov : vb;
+                    else t[i] = bsel ? ov + vb : vb + ov;
+                }
+#pragma unroll
+                for (int s = 1; s < CH; s *= 2)
+#pragma unroll
+                    for (int i = 0; i + s < CH; i += 2 * s)
+                        if (i + s < cnt) t[i] = t[i] + t[i + s];
+                if (lane < 16) gs[(v * G + g) * 16 + lane] = t[0];
+            }
+        }
+        __syncthreads();
+        // ---- tree over the group sums, one thread per (vector, row) ----
+        if (tid < nv * 16) {
+            const int v = tid >> 4, rr = tid & 15;
+            float* col = gs + v * G * 16 + rr;
+            for (int s = 1; s < G; s *= 2)
+                for (int i = 0; i + s < G; i += 2 * s) col[i * 16] = col[i * 16] + col[(i + s) * 16];
+            const float acc = col[0];
+            const int row = tile * TILE_ROWS + rr;
+            if (row < a.rows) {
+                const int ent = vbeg + v0 + v;
+                const int slot = a.slots ? a.slots[ent] : ent;
+                float* yp = a.y + (size_t)slot * a.y_stride + row;
+                if (EPI == EPI_RESID) *yp = a.resid[(size_t)slot * a.resid_stride + row] + acc;
+                else *yp = acc;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // Greedy pick (src/generate.rs:153-174 via src/tensor.rs:2451-2480):
 // maximum over the tiles' partials, last index on ties.
 __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__ val, const int* __restrict__ idx,
@@ -493,6 +644,55 @@ lq8_status launch_gemv_grouped(hipStream_t s, const GemvProblemDev* d_probs, int
     hipLaunchKernelGGL(k_gemv_grouped, dim3((unsigned)total_tiles), dim3(256), smem, s, d_probs, count);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
+}
+
+namespace {
+
+template <int XS, int EPI, int CH>
+lq8_status mv_vb(hipStream_t s, const MvArgs& a, dim3 grid, int vb, size_t xs_floats_per_vec, int G) {
+    const size_t smem = ((size_t)vb * xs_floats_per_vec + (size_t)vb * G * 16 + 4) * sizeof(float);
+    if (smem > 64 * 1024) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: input staging exceeds 64 KiB of LDS");
+    if (vb == 4) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 4>), grid, dim3(256), smem, s, a);
+    else if (vb == 2) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 2>), grid, dim3(256), smem, s, a);
+    else hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 1>), grid, dim3(256), smem, s, a);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
+template <int XS, int EPI>
+lq8_status mv_ch(hipStream_t s, const MvArgs& a, int max_probs, int vsplit) {
+    const int nb = a.k >> 5, np = (nb + 1) >> 1;
+    const int ch = pick_ch(np, 4);
+    const int G = (np + ch - 1) / ch;
+    const size_t per_vec = (size_t)np * 64;
+    // vectors staged per pass: as many as fit in 40 KiB
+    const int vb = per_vec * 4 * sizeof(float) <= 40 * 1024 ? 4 : per_vec * 2 * sizeof(float) <= 40 * 1024 ? 2 : 1;
+    const int tiles_p = (a.rows + TILE_ROWS - 1) / TILE_ROWS;
+    const dim3 grid((unsigned)(tiles_p * max_probs), (unsigned)vsplit);
+    if (ch == 1) return mv_vb<XS, EPI, 1>(s, a, grid, vb, per_vec, G);
+    if (ch == 2) return mv_vb<XS, EPI, 2>(s, a, grid, vb, per_vec, G);
+    return mv_vb<XS, EPI, 4>(s, a, grid, vb, per_vec, G);
+}
+
+}  // namespace
+
+lq8_status launch_gemv_mv(hipStream_t s, XSource xs, Epilogue epi, const MvArgs& a, int max_probs, int vsplit) {
+    if (a.k <= 0 || a.k % 32 || a.rows <= 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k must be a positive multiple of 32");
+    if (a.k > GEMV_MAX_K) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k above 12288 is not supported");
+    if (max_probs <= 0 || vsplit <= 0) return LQ8_OK;
+    if (epi == EPI_RESID && !a.resid) return fail(LQ8_ERR_INVALID_ARG, "gemv: residual is null");
+    if (xs == XS_RMSNORM && !a.norm_w) return fail(LQ8_ERR_INVALID_ARG, "gemv: norm weight is null");
+    if (epi == EPI_ARGMAX || xs == XS_ATTN) return fail(LQ8_ERR_INVALID_ARG, "gemv: unsupported multi-vector mode");
+    if (a.x_div <= 0) return fail(LQ8_ERR_INVALID_ARG, "gemv: x_div must be positive");
+    const bool resid = epi == EPI_RESID;
+    switch (xs) {
+        case XS_PLAIN: return resid ? mv_ch<XS_PLAIN, EPI_RESID>(s, a, max_probs, vsplit)
+                                    : mv_ch<XS_PLAIN, EPI_STORE>(s, a, max_probs, vsplit);
+        case XS_RMSNORM: return resid ? mv_ch<XS_RMSNORM, EPI_RESID>(s, a, max_probs, vsplit)
+                                      : mv_ch<XS_RMSNORM, EPI_STORE>(s, a, max_probs, vsplit);
+        default: return resid ? mv_ch<XS_SILU, EPI_RESID>(s, a, max_probs, vsplit)
+                              : mv_ch<XS_SILU, EPI_STORE>(s, a, max_probs, vsplit);
+    }
 }
 
 lq8_status launch_argmax_final(hipStream_t s, const float* arg_val, const int* arg_idx, int count, uint32_t* d_tok,

@@ -116,6 +116,35 @@ struct GemvProblemDev {
 };
 lq8_status launch_gemv_grouped(hipStream_t s, const GemvProblemDev* d_probs, int count, int total_tiles,
                                int max_k);
+// Multi-vector GEMV: each workgroup owns one 16-row tile of one problem and
+// applies it to that problem's vectors, each in the single-vector GEMV order
+// (so every output equals launch_gemv on that vector).  Problems are the
+// routed experts of a MoE layer (lists written on the device) or one dense
+// weight applied to a batch of vectors.
+struct MvArgs {
+    const int8_t* codes;    // problem e's tiles start at tile e * prob_tiles
+    const uint16_t* scales;
+    int rows, k;            // output rows per problem, input length
+    int prob_tiles;
+    const int* n_prob;      // device: problem count (null: 1)
+    const int* prob_id;     // device: weight index of problem j (null: j)
+    const int* vec_begin;   // device: first slots entry of problem j (null: 0)
+    const int* vec_count;   // device: vectors of problem j (null: nvec)
+    const int* slots;       // device: slot ids (null: slot = entry index)
+    int nvec;
+    const float* x;         // vector of slot s: x + (s / x_div) * x_stride
+    int x_stride, x_div;
+    float* y;               // output of slot s: y + s * y_stride
+    int y_stride;
+    const float* resid;     // EPI_RESID: y = resid[s] + acc, resid + s * resid_stride
+    int resid_stride;
+    const float* norm_w;    // XS_RMSNORM
+    float eps;
+};
+// max_probs: grid rows of problems (n_prob on the device may be smaller);
+// vsplit: workgroups per tile sharing the vectors of a problem.
+lq8_status launch_gemv_mv(hipStream_t s, XSource xs, Epilogue epi, const MvArgs& a, int max_probs, int vsplit);
+
 // Final greedy pick over the per-tile argmax partials: token -> *d_tok and
 // tokens_out[*d_step], then *d_pos and *d_step advance (device scalars).
 lq8_status launch_argmax_final(hipStream_t s, const float* arg_val, const int* arg_idx, int count, uint32_t* d_tok,
@@ -181,11 +210,20 @@ struct AttnSegLaunch {
     float* k_cache;        // [kv_heads][max_pos][128] (this layer)
     float* v_cache;
     float* part;           // [ceil(max_pos / ATT_SEG)][num_heads][ATT_PART_STRIDE]
-    const int* d_pos;
+    const int* d_pos;      // [batch] (null: every sequence at pos_base)
     int pos_base, num_heads, num_kv_heads, max_pos;
     float eps, scale;
+    // independent sequences (grid z): sequence b reads qkv + b * qkv_stride,
+    // owns k/v_cache + b * kv_stride and writes part + b * part_stride
+    int batch = 1;
+    size_t qkv_stride = 0, kv_stride = 0, part_stride = 0;
 };
 lq8_status launch_attention_seg(hipStream_t s, const AttnSegLaunch& a);
+// Attention outputs from the per-segment partials of launch_attention_seg,
+// for each sequence: out[b][h * 128 + d], combined in segment order with the
+// running update of the o-projection's XS_ATTN staging.
+lq8_status launch_attention_combine(hipStream_t s, const float* part, size_t part_stride, const int* d_pos,
+                                    int batch, int num_heads, int cmax, float* out);
 
 // Prefill: one workgroup per (kv head, query row) over a filled cache.
 struct AttnRowsLaunch {

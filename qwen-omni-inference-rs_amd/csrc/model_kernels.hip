@@ -167,14 +167,20 @@ __device__ __forceinline__ void seg_stage_v(const float4* vreg, int nj, int vnew
 // head) o_c[128], m_c, l_c at part[(c * H + h) * ATT_PART_STRIDE].
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     extern __shared__ float sm[];
-    const int kvh = blockIdx.x, c = blockIdx.y;
+    const int kvh = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.num_heads / a.num_kv_heads;
-    const int pos = a.d_pos ? *a.d_pos : a.pos_base;
+    const int pos = a.d_pos ? a.d_pos[b] : a.pos_base;
+    a.qkv += b * a.qkv_stride;
+    a.k_cache += b * a.kv_stride;
+    a.v_cache += b * a.kv_stride;
+    a.part += b * a.part_stride;
     const int L = pos + 1;
     const int C = (L + SEG - 1) / SEG;
-    if (c >= C) return;  // before any barrier: the whole workgroup leaves
+    // before any barrier: the whole workgroup leaves (a position outside the
+    // cache writes nothing)
+    if (c >= C || pos < 0 || pos >= a.max_pos) return;
     const int js = c * SEG, nj = min(SEG, L - js);
     const bool last = c == C - 1;
     const int newrow = last ? pos - js : -1;
@@ -228,6 +234,30 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
             p[129] = mlc[2 * h + 1];
         }
     }
+}
+
+// Attention output of one sequence's head from its per-segment partials,
+// one thread per head dimension d: the running update over the segments in
+// order, m' = max(m, m_c), a = exp(m - m'), b = exp(m_c - m'),
+// num = num * a + b * o_c, den = den * a + b * l_c; out = num / den (the
+// arithmetic of the o-projection's XS_ATTN staging, thread by thread).
+__global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ part, size_t part_stride,
+                                                      const int* __restrict__ d_pos, int H, int cmax,
+                                                      float* __restrict__ out) {
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const int C = min(max(d_pos[b], 0) / SEG + 1, cmax);
+    const float* pb = part + b * part_stride;
+    float m = -__builtin_huge_valf(), den = 0.0f, num = 0.0f;
+    for (int c = 0; c < C; c++) {
+        const float* p = pb + ((size_t)c * H + h) * ATT_PART_STRIDE;
+        const float mc = p[128], lc = p[129];
+        const float mn = m > mc ? m : mc;
+        const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
+        den = den * ea + eb * lc;
+        num = num * ea + eb * p[d];
+        m = mn;
+    }
+    out[(size_t)b * H * 128 + h * 128 + d] = __fdiv_rn(num, den);
 }
 
 // Attention over n query rows with a filled cache (prefill), one workgroup
@@ -358,8 +388,18 @@ lq8_status launch_attention_seg(hipStream_t s, const AttnSegLaunch& a) {
         return fail(LQ8_ERR_SHAPE_MISMATCH, "attention: unsupported head layout");
     const int G = a.num_heads / a.num_kv_heads;
     const int cmax = (a.max_pos + SEG - 1) / SEG;
-    hipLaunchKernelGGL(k_attn_seg, dim3((unsigned)a.num_kv_heads, (unsigned)cmax), dim3(ATT_THREADS), seg_smem(G), s,
-                       a);
+    if (a.batch <= 0) return fail(LQ8_ERR_INVALID_ARG, "attention: batch must be positive");
+    hipLaunchKernelGGL(k_attn_seg, dim3((unsigned)a.num_kv_heads, (unsigned)cmax, (unsigned)a.batch), dim3(ATT_THREADS),
+                       seg_smem(G), s, a);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
+lq8_status launch_attention_combine(hipStream_t s, const float* part, size_t part_stride, const int* d_pos,
+                                    int batch, int num_heads, int cmax, float* out) {
+    if (batch <= 0 || num_heads <= 0 || cmax <= 0) return LQ8_OK;
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)num_heads, (unsigned)batch), dim3(128), 0, s, part, part_stride,
+                       d_pos, num_heads, cmax, out);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

@@ -1,0 +1,603 @@
+// moe.hip -- Qwen3-MoE decoder layers (Qwen3-30B-A3B style) for decode steps
+// of a batch of independent sequences: router, grouped expert GEMVs,
+// expert combine, and the layer runtime behind the lq8_moe_* C ABI.
+//
+// Per layer (T sequences, one token each):
+//   qkv   = [q|k|v](RmsNorm(h))               GEMV (T = 1) / multi-vector GEMV
+//   part  = attention segments per sequence    (q/k norm, RoPE, KV append)
+//   h2    = h + o(attention(part))             GEMV with the combine fused (T = 1),
+//                                              combine kernel + multi-vector GEMV (T > 1)
+//   route = top_k of softmax(scores)           one workgroup, expert lists on the device
+//   gu    = [gate|up]_e(RmsNorm(h2))           grouped multi-vector GEMV over the routed experts
+//   eo    = down_e(silu(gate) * up)            grouped multi-vector GEMV
+//   h     = h2 + sum_e w_e * eo_e              ascending expert index
+// Every projection is the single-vector GEMV order per token, so each
+// token's result is independent of the batch it runs in.
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "lq8_internal.h"
+#include "lq8_numerics.h"
+
+using namespace lq8;
+
+namespace {
+
+constexpr int MOE_MAX_EXPERTS = 256;
+constexpr int MOE_MAX_TOPK = 16;
+constexpr int MOE_MAX_BATCH = 64;
+
+struct MoeLayer {
+    lq8_weight *qkv = nullptr, *o = nullptr;
+    lq8_weight *gu = nullptr;    // [E * 2I, H]: expert e rows e*2I .. (gate I rows, then up I rows)
+    lq8_weight *down = nullptr;  // [E * H, I]: expert e rows e*H ..
+    float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+};
+
+}  // namespace
+
+struct lq8_moe {
+    lq8_ctx* ctx = nullptr;
+    lq8_moe_config c{};
+    size_t QD = 0, KD = 0, QKV = 0;
+    int cmax = 0;
+    std::vector<MoeLayer> layers;
+    float *cos_t = nullptr, *sin_t = nullptr;
+    float *kc = nullptr, *vc = nullptr;  // [layer][seq][kv_head][max_pos][128]
+    float *h2 = nullptr, *qkv = nullptr, *apart = nullptr, *aout = nullptr, *gu = nullptr, *eo = nullptr;
+    uint32_t* rids = nullptr;  // [layer][max_batch][top_k]
+    float* rw = nullptr;
+    int *n_act = nullptr, *act_e = nullptr, *vbeg = nullptr, *vcnt = nullptr, *slots = nullptr;
+    float *hid_tmp = nullptr, *scores_tmp = nullptr;
+    int* pos_tmp = nullptr;
+    size_t last_T = 0;
+};
+
+namespace {
+
+// ---- router ------------------------------------------------------------------
+// One workgroup for the batch.  Wave w routes tokens w, w + 4, ...: lane l
+// holds scores l, l + 64, ...; m = max (exact in any order), e = exp(s - m),
+// S = SUM64(e) (lane l adds its entries in order, then the xor fold), p = e / S;
+// top_k rounds of a wave arg-max (higher p, then lower index); weights
+// p_r / (((p_0 + p_1) + p_2) + ...).  Then thread e lists the slots
+// (t * top_k + r) routed to expert e in token order, and the active experts
+// are numbered in ascending order (n_act, act_e, vbeg, vcnt, slots).
+__global__ __launch_bounds__(256) void k_moe_route(const float* __restrict__ scores, int T, int E, int K,
+                                                   uint32_t* __restrict__ rids, float* __restrict__ rw,
+                                                   int* __restrict__ n_act, int* __restrict__ act_e,
+                                                   int* __restrict__ vbeg, int* __restrict__ vcnt,
+                                                   int* __restrict__ slots) {
+    __shared__ int sid[MOE_MAX_BATCH * MOE_MAX_TOPK];
+    __shared__ int cnt[MOE_MAX_EXPERTS], beg[MOE_MAX_EXPERTS];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const float NEG = -__builtin_huge_valf();
+    for (int t = wave; t < T; t += 4) {
+        float p[4];
+        float m = NEG;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = lane + 64 * j;
+            p[j] = i < E ? scores[(size_t)t * E + i] : NEG;
+            m = fmaxf(m, p[j]);
+        }
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (lane + 64 * j < E) {
+                p[j] = expf_cr(p[j] - m);
+                acc = acc + p[j];
+            }
+        }
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) acc = acc + __shfl_xor(acc, d, 64);
+#pragma unroll
+        for (int j = 0; j < 4; j++) p[j] = lane + 64 * j < E ? __fdiv_rn(p[j], acc) : NEG;
+        float tot = 0.0f;
+        float pr[MOE_MAX_TOPK];
+        int ir[MOE_MAX_TOPK];
+        for (int r = 0; r < K; r++) {
+            float bv = NEG;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = lane + 64 * j;
+                if (p[j] > bv || (p[j] == bv && i < bi)) { bv = p[j]; bi = i; }
+            }
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) {
+                const float ov = __shfl_xor(bv, d, 64);
+                const int oi = __shfl_xor(bi, d, 64);
+                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (lane + 64 * j == bi) p[j] = NEG;  // taken
+            pr[r < MOE_MAX_TOPK ? r : 0] = bv;
+            ir[r < MOE_MAX_TOPK ? r : 0] = bi;
+            tot = tot + bv;
+        }
+        if (lane < K) {
+            float w = 0.0f;
+            int id = 0;
+            for (int r = 0; r < K; r++)
+                if (r == lane) { w = pr[r]; id = ir[r]; }
+            rids[t * K + lane] = (uint32_t)id;
+            rw[t * K + lane] = __fdiv_rn(w, tot);
+            sid[t * K + lane] = id;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 256) {
+        int c = 0;
+        for (int s = 0; s < T * K; s++) c += sid[s] == e;
+        cnt[e] = c;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int na = 0, off = 0;
+        for (int e = 0; e < E; e++) {
+            beg[e] = off;
+            if (cnt[e]) {
+                act_e[na] = e;
+                vbeg[na] = off;
+                vcnt[na] = cnt[e];
+                na++;
+                off += cnt[e];
+            }
+        }
+        *n_act = na;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 256) {
+        int o = beg[e];
+        for (int s = 0; s < T * K; s++)
+            if (sid[s] == e) slots[o++] = s;
+    }
+}
+
+// ---- expert combine -----------------------------------------------------------
+// out[t][i] = h2[t][i] + acc, acc = ((0 + w_a * eo_a) + w_b * eo_b) + ... over
+// the token's experts in ascending expert index (products rounded, then added).
+__global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ h2, const float* __restrict__ eo,
+                                                     const uint32_t* __restrict__ rids, const float* __restrict__ rw,
+                                                     int K, int H, float* __restrict__ out) {
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= H) return;
+    uint32_t id[MOE_MAX_TOPK];
+    int rk[MOE_MAX_TOPK];
+    for (int r = 0; r < K; r++) {
+        id[r] = rids[t * K + r];
+        rk[r] = r;
+    }
+    for (int a = 1; a < K; a++)  // insertion sort by expert index (distinct ids)
+        for (int b = a; b > 0 && id[b - 1] > id[b]; b--) {
+            const uint32_t ti = id[b]; id[b] = id[b - 1]; id[b - 1] = ti;
+            const int tr = rk[b]; rk[b] = rk[b - 1]; rk[b - 1] = tr;
+        }
+    float acc = 0.0f;
+    for (int r = 0; r < K; r++) {
+        const int slot = t * K + rk[r];
+        acc = acc + rw[slot] * eo[(size_t)slot * H + i];
+    }
+    out[(size_t)t * H + i] = h2[(size_t)t * H + i] + acc;
+}
+
+template <typename T>
+lq8_status dalloc(T** p, size_t count) {
+    *p = nullptr;
+    if (!count) return LQ8_OK;
+    hipError_t e = hipMalloc((void**)p, count * sizeof(T));
+    if (e != hipSuccess) {
+        *p = nullptr;
+        return e == hipErrorOutOfMemory ? fail(LQ8_ERR_OUT_OF_MEMORY, "device allocation failed")
+                                        : hip_fail(e, "hipMalloc");
+    }
+    return LQ8_OK;
+}
+
+lq8_status validate(const lq8_moe_config* c) {
+    if (!c) return fail(LQ8_ERR_INVALID_ARG, "null config");
+    if (c->head_dim != 128 || !attention_supported((int)c->num_heads, (int)c->num_kv_heads, (int)c->head_dim))
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: head_dim 128 and num_heads / num_kv_heads <= 16 required");
+    if (c->hidden_size == 0 || c->hidden_size % 32 || c->hidden_size > GEMV_MAX_K)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: hidden_size must be a multiple of 32 up to 12288");
+    if ((size_t)c->num_heads * c->head_dim > GEMV_MAX_K)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: num_heads * head_dim above 12288");
+    if (c->expert_intermediate_size == 0 || c->expert_intermediate_size % 32 || c->expert_intermediate_size > GEMV_MAX_K)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: expert_intermediate_size must be a multiple of 32 up to 12288");
+    if (c->num_experts == 0 || c->num_experts > MOE_MAX_EXPERTS)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: num_experts must be 1..256");
+    if (c->top_k == 0 || c->top_k > c->num_experts || c->top_k > MOE_MAX_TOPK)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: top_k must be 1..min(num_experts, 16)");
+    if (c->max_batch == 0 || c->max_batch > MOE_MAX_BATCH)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: max_batch must be 1..64");
+    if (c->max_positions == 0 || c->max_positions > 8192)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: max_positions must be 1..8192");
+    if (c->num_layers == 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: num_layers must be positive");
+    return LQ8_OK;
+}
+
+void release(lq8_moe* m) {
+    if (!m) return;
+    registry_remove(m);
+    auto F = [](void* p) { if (p) (void)hipFree(p); };
+    for (auto& L : m->layers) {
+        weight_release(L.qkv); weight_release(L.o); weight_release(L.gu); weight_release(L.down);
+        F(L.in_norm); F(L.post_norm); F(L.q_norm); F(L.k_norm);
+    }
+    F(m->cos_t); F(m->sin_t); F(m->kc); F(m->vc);
+    F(m->h2); F(m->qkv); F(m->apart); F(m->aout); F(m->gu); F(m->eo);
+    F(m->rids); F(m->rw); F(m->n_act); F(m->act_e); F(m->vbeg); F(m->vcnt); F(m->slots);
+    F(m->hid_tmp); F(m->scores_tmp); F(m->pos_tmp);
+    delete m;
+}
+
+lq8_status build_skeleton(lq8_ctx* ctx, const lq8_moe_config* c, lq8_moe* m) {
+    m->ctx = ctx;
+    m->c = *c;
+    const size_t H = c->hidden_size, I = c->expert_intermediate_size, hd = c->head_dim, P = c->max_positions;
+    const size_t E = c->num_experts, B = c->max_batch, K = c->top_k, NL = c->num_layers;
+    m->QD = (size_t)c->num_heads * hd;
+    m->KD = (size_t)c->num_kv_heads * hd;
+    m->QKV = m->QD + 2 * m->KD;
+    m->cmax = (int)((P + ATT_SEG - 1) / ATT_SEG);
+    lq8_status st;
+    m->layers.resize(NL);
+    for (auto& L : m->layers) {
+        if ((st = weight_alloc(ctx, m->QKV, H, &L.qkv)) || (st = weight_alloc(ctx, H, m->QD, &L.o)) ||
+            (st = weight_alloc(ctx, E * 2 * I, H, &L.gu)) || (st = weight_alloc(ctx, E * H, I, &L.down)))
+            return st;
+        if ((st = dalloc(&L.in_norm, H)) || (st = dalloc(&L.post_norm, H)) || (st = dalloc(&L.q_norm, hd)) ||
+            (st = dalloc(&L.k_norm, hd)))
+            return st;
+    }
+    // RoPE tables (src/rope.rs:77-128): f64 math, cast to f32, each frequency twice.
+    const size_t R = hd / 2, half = R / 2;
+    std::vector<float> ct(P * R), stbl(P * R);
+    std::vector<double> inv(half);
+    for (size_t i = 0; i < half; i++) inv[i] = 1.0 / std::pow(c->rope_theta, (double)(2 * i) / (double)R);
+    for (size_t p = 0; p < P; p++)
+        for (size_t i = 0; i < half; i++) {
+            const double f = (double)p * inv[i];
+            const float cv = (float)std::cos(f), sv = (float)std::sin(f);
+            ct[p * R + 2 * i] = ct[p * R + 2 * i + 1] = cv;
+            stbl[p * R + 2 * i] = stbl[p * R + 2 * i + 1] = sv;
+        }
+    if ((st = dalloc(&m->cos_t, P * R)) || (st = dalloc(&m->sin_t, P * R))) return st;
+    LQ8_HIP(hipMemcpy(m->cos_t, ct.data(), P * R * sizeof(float), hipMemcpyHostToDevice));
+    LQ8_HIP(hipMemcpy(m->sin_t, stbl.data(), P * R * sizeof(float), hipMemcpyHostToDevice));
+    const size_t kv = NL * B * c->num_kv_heads * P * hd;
+    if ((st = dalloc(&m->kc, kv)) || (st = dalloc(&m->vc, kv))) return st;
+    LQ8_HIP(hipMemset(m->kc, 0, kv * sizeof(float)));
+    LQ8_HIP(hipMemset(m->vc, 0, kv * sizeof(float)));
+    if ((st = dalloc(&m->h2, B * H)) || (st = dalloc(&m->qkv, B * m->QKV)) ||
+        (st = dalloc(&m->apart, B * m->cmax * c->num_heads * ATT_PART_STRIDE)) || (st = dalloc(&m->aout, B * m->QD)) ||
+        (st = dalloc(&m->gu, B * K * 2 * I)) || (st = dalloc(&m->eo, B * K * H)) ||
+        (st = dalloc(&m->rids, NL * B * K)) || (st = dalloc(&m->rw, NL * B * K)) || (st = dalloc(&m->n_act, 1)) ||
+        (st = dalloc(&m->act_e, E)) || (st = dalloc(&m->vbeg, E)) || (st = dalloc(&m->vcnt, E)) ||
+        (st = dalloc(&m->slots, B * K)) || (st = dalloc(&m->hid_tmp, B * H)) ||
+        (st = dalloc(&m->scores_tmp, NL * B * E)) || (st = dalloc(&m->pos_tmp, B)))
+        return st;
+    return LQ8_OK;
+}
+
+lq8_status fill_norm(float* d, size_t n, const float* host) {
+    if (host) {
+        LQ8_HIP(hipMemcpy(d, host, n * sizeof(float), hipMemcpyHostToDevice));
+    } else {
+        std::vector<float> ones(n, 1.0f);
+        LQ8_HIP(hipMemcpy(d, ones.data(), n * sizeof(float), hipMemcpyHostToDevice));
+    }
+    return LQ8_OK;
+}
+
+size_t per_layer(const lq8_moe_config* c) { return 8 + 3 * (size_t)c->num_experts; }
+
+struct TensorRef {
+    lq8_weight* w = nullptr;
+    size_t row0 = 0, rows = 0;
+    float* norm = nullptr;
+    size_t norm_len = 0;
+};
+
+TensorRef tensor_ref(lq8_moe* m, size_t idx) {
+    TensorRef t;
+    const size_t H = m->c.hidden_size, I = m->c.expert_intermediate_size, E = m->c.num_experts;
+    const size_t l = idx / per_layer(&m->c), k = idx % per_layer(&m->c);
+    MoeLayer& L = m->layers[l];
+    switch (k) {
+        case 0: t.norm = L.in_norm; t.norm_len = H; return t;
+        case 1: t.norm = L.post_norm; t.norm_len = H; return t;
+        case 2: t.norm = L.q_norm; t.norm_len = m->c.head_dim; return t;
+        case 3: t.norm = L.k_norm; t.norm_len = m->c.head_dim; return t;
+        case 4: t.w = L.qkv; t.row0 = 0; t.rows = m->QD; return t;
+        case 5: t.w = L.qkv; t.row0 = m->QD; t.rows = m->KD; return t;
+        case 6: t.w = L.qkv; t.row0 = m->QD + m->KD; t.rows = m->KD; return t;
+        case 7: t.w = L.o; t.rows = H; return t;
+        default: break;
+    }
+    const size_t x = k - 8, e = x % E;
+    if (x < E) { t.w = L.gu; t.row0 = e * 2 * I; t.rows = I; }
+    else if (x < 2 * E) { t.w = L.gu; t.row0 = e * 2 * I + I; t.rows = I; }
+    else { t.w = L.down; t.row0 = e * H; t.rows = H; }
+    return t;
+}
+
+lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, const int* d_pos, int T) {
+    hipStream_t s = m->ctx->stream;
+    const lq8_moe_config& c = m->c;
+    const int H = (int)c.hidden_size, I = (int)c.expert_intermediate_size, E = (int)c.num_experts, K = (int)c.top_k;
+    const int NH = (int)c.num_heads, B = (int)c.max_batch;
+    const size_t P = c.max_positions;
+    const size_t seq_kv = (size_t)c.num_kv_heads * P * 128, layer_kv = (size_t)B * seq_kv;
+    const size_t part_stride = (size_t)m->cmax * NH * ATT_PART_STRIDE;
+    const float scale = 1.0f / std::sqrt((float)c.head_dim);
+    const int vsplit = (T + 3) / 4;
+    const int max_probs = std::min(E, T * K);
+    lq8_status st;
+    for (size_t l = 0; l < m->layers.size(); l++) {
+        MoeLayer& L = m->layers[l];
+        // input_layernorm + q|k|v
+        if (T == 1) {
+            GemvArgs g{L.qkv->codes, L.qkv->scales, d_hidden, L.in_norm, m->qkv, nullptr, nullptr, nullptr,
+                       (int)m->QKV, H, c.rms_norm_eps};
+            if ((st = launch_gemv(s, XS_RMSNORM, EPI_STORE, g))) return st;
+        } else {
+            MvArgs a{};
+            a.codes = L.qkv->codes; a.scales = L.qkv->scales; a.rows = (int)m->QKV; a.k = H;
+            a.nvec = T; a.x = d_hidden; a.x_stride = H; a.x_div = 1; a.y = m->qkv; a.y_stride = (int)m->QKV;
+            a.norm_w = L.in_norm; a.eps = c.rms_norm_eps;
+            if ((st = launch_gemv_mv(s, XS_RMSNORM, EPI_STORE, a, 1, vsplit))) return st;
+        }
+        // q/k norm, RoPE, KV append, attention per segment, per sequence
+        AttnSegLaunch at{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->kc + l * layer_kv, m->vc + l * layer_kv,
+                         m->apart, d_pos, 0, NH, (int)c.num_kv_heads, (int)P, c.rms_norm_eps, scale};
+        at.batch = T;
+        at.qkv_stride = m->QKV;
+        at.kv_stride = seq_kv;
+        at.part_stride = part_stride;
+        if ((st = launch_attention_seg(s, at))) return st;
+        // o_proj on the attention output, + residual -> h2
+        if (T == 1) {
+            GemvArgs g{L.o->codes, L.o->scales, m->apart, nullptr, m->h2, d_hidden, nullptr, nullptr, H, (int)m->QD,
+                       0.0f};
+            g.d_pos = d_pos;
+            g.attn_heads = NH;
+            g.attn_cmax = m->cmax;
+            if ((st = launch_gemv(s, XS_ATTN, EPI_RESID, g))) return st;
+        } else {
+            if ((st = launch_attention_combine(s, m->apart, part_stride, d_pos, T, NH, m->cmax, m->aout))) return st;
+            MvArgs a{};
+            a.codes = L.o->codes; a.scales = L.o->scales; a.rows = H; a.k = (int)m->QD;
+            a.nvec = T; a.x = m->aout; a.x_stride = (int)m->QD; a.x_div = 1; a.y = m->h2; a.y_stride = H;
+            a.resid = d_hidden; a.resid_stride = H;
+            if ((st = launch_gemv_mv(s, XS_PLAIN, EPI_RESID, a, 1, vsplit))) return st;
+        }
+        // router -> expert lists
+        uint32_t* rids = m->rids + l * B * K;
+        float* rw = m->rw + l * B * K;
+        hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, s, d_scores + l * (size_t)T * E, T, E, K, rids, rw,
+                           m->n_act, m->act_e, m->vbeg, m->vcnt, m->slots);
+        LQ8_HIP(hipGetLastError());
+        // post_attention_layernorm + [gate|up] of each routed expert
+        MvArgs g{};
+        g.codes = L.gu->codes; g.scales = L.gu->scales; g.rows = 2 * I; g.k = H; g.prob_tiles = 2 * I / TILE_ROWS;
+        g.n_prob = m->n_act; g.prob_id = m->act_e; g.vec_begin = m->vbeg; g.vec_count = m->vcnt; g.slots = m->slots;
+        g.x = m->h2; g.x_stride = H; g.x_div = K; g.y = m->gu; g.y_stride = 2 * I;
+        g.norm_w = L.post_norm; g.eps = c.rms_norm_eps;
+        if ((st = launch_gemv_mv(s, XS_RMSNORM, EPI_STORE, g, max_probs, 1))) return st;
+        // down(silu(gate) * up) of each routed expert
+        MvArgs d{};
+        d.codes = L.down->codes; d.scales = L.down->scales; d.rows = H; d.k = I; d.prob_tiles = H / TILE_ROWS;
+        d.n_prob = m->n_act; d.prob_id = m->act_e; d.vec_begin = m->vbeg; d.vec_count = m->vcnt; d.slots = m->slots;
+        d.x = m->gu; d.x_stride = 2 * I; d.x_div = 1; d.y = m->eo; d.y_stride = H;
+        if ((st = launch_gemv_mv(s, XS_SILU, EPI_STORE, d, max_probs, 1))) return st;
+        // h = h2 + experts (ascending expert index)
+        hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s, m->h2, m->eo,
+                           rids, rw, K, H, d_hidden);
+        LQ8_HIP(hipGetLastError());
+    }
+    return LQ8_OK;
+}
+
+lq8_status upload_table(lq8_moe* m, const void* const* tensors) {
+    const size_t count = m->layers.size() * per_layer(&m->c);
+    void* tmp = nullptr;
+    size_t tmp_cap = 0;
+    lq8_status st = LQ8_OK;
+    for (size_t i = 0; i < count && !st; i++) {
+        TensorRef t = tensor_ref(m, i);
+        if (t.norm) { st = fill_norm(t.norm, t.norm_len, (const float*)tensors[i]); continue; }
+        const size_t bytes = t.rows * t.w->nb * BLOCK_BYTES;
+        if (bytes > tmp_cap) {
+            if (tmp) (void)hipFree(tmp);
+            tmp = nullptr;
+            hipError_t e = hipMalloc(&tmp, bytes);
+            if (e != hipSuccess) { st = hip_fail(e, "staging"); break; }
+            tmp_cap = bytes;
+        }
+        hipError_t e = hipMemcpy(tmp, tensors[i], bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) { st = hip_fail(e, "tensor upload"); break; }
+        st = launch_repack_aos(m->ctx->stream, (const uint8_t*)tmp, t.rows, t.row0, t.w);
+        if (!st) {
+            e = hipStreamSynchronize(m->ctx->stream);
+            if (e != hipSuccess) st = hip_fail(e, "tensor repack");
+        }
+    }
+    if (tmp) (void)hipFree(tmp);
+    return st;
+}
+
+}  // namespace
+
+#define CHECK_MOE(m) \
+    if (!registry_has(m)) return fail(LQ8_ERR_INVALID_ARG, "invalid or released MoE handle")
+
+extern "C" {
+
+size_t lq8_moe_tensor_count(const lq8_moe_config* cfg) { return cfg ? per_layer(cfg) * cfg->num_layers : 0; }
+
+lq8_status lq8_moe_tensor_bytes(const lq8_moe_config* c, size_t idx, size_t* bytes) {
+    if (!c || !bytes) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (idx >= lq8_moe_tensor_count(c)) return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "tensor index out of range");
+    const size_t H = c->hidden_size, I = c->expert_intermediate_size, hd = c->head_dim, E = c->num_experts;
+    const size_t QD = (size_t)c->num_heads * hd, KD = (size_t)c->num_kv_heads * hd;
+    auto q8 = [](size_t r, size_t k) { return r * (k / 32) * 34; };
+    const size_t k = idx % per_layer(c);
+    switch (k) {
+        case 0: case 1: *bytes = H * 4; return LQ8_OK;
+        case 2: case 3: *bytes = hd * 4; return LQ8_OK;
+        case 4: *bytes = q8(QD, H); return LQ8_OK;
+        case 5: case 6: *bytes = q8(KD, H); return LQ8_OK;
+        case 7: *bytes = q8(H, QD); return LQ8_OK;
+        default: break;
+    }
+    *bytes = k - 8 < 2 * E ? q8(I, H) : q8(H, I);
+    return LQ8_OK;
+}
+
+lq8_status lq8_moe_create(lq8_ctx* ctx, const lq8_moe_config* cfg, const void* const* tensors, lq8_moe** out) {
+    if (!registry_has(ctx)) return fail(LQ8_ERR_INVALID_ARG, "invalid context handle");
+    if (!tensors || !out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    lq8_status st = validate(cfg);
+    if (st) return st;
+    const size_t count = lq8_moe_tensor_count(cfg);
+    for (size_t i = 0; i < count; i++)
+        if (!tensors[i]) return fail(LQ8_ERR_INVALID_ARG, "null tensor in table");
+    LQ8_HIP(hipSetDevice(ctx->device));
+    lq8_moe* m = new lq8_moe();
+    registry_add(m);
+    if ((st = build_skeleton(ctx, cfg, m)) || (st = upload_table(m, tensors))) { release(m); return st; }
+    *out = m;
+    return LQ8_OK;
+}
+
+lq8_status lq8_moe_create_random(lq8_ctx* ctx, const lq8_moe_config* cfg, uint64_t seed, float stddev,
+                                 lq8_moe** out) {
+    if (!registry_has(ctx)) return fail(LQ8_ERR_INVALID_ARG, "invalid context handle");
+    if (!out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    lq8_status st = validate(cfg);
+    if (st) return st;
+    LQ8_HIP(hipSetDevice(ctx->device));
+    lq8_moe* m = new lq8_moe();
+    registry_add(m);
+    if ((st = build_skeleton(ctx, cfg, m))) { release(m); return st; }
+    const size_t count = lq8_moe_tensor_count(cfg);
+    for (size_t i = 0; i < count && !st; i++) {
+        TensorRef t = tensor_ref(m, i);
+        if (t.norm) st = fill_norm(t.norm, t.norm_len, nullptr);
+        else st = launch_random_weight(ctx->stream, t.w, t.row0, t.rows, seed, i, stddev);
+    }
+    if (!st) {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) st = hip_fail(e, "random init");
+    }
+    if (st) { release(m); return st; }
+    *out = m;
+    return LQ8_OK;
+}
+
+lq8_status lq8_moe_export_tensor(lq8_moe* m, size_t idx, void* host_out) {
+    CHECK_MOE(m);
+    if (!host_out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (idx >= lq8_moe_tensor_count(&m->c)) return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "tensor index out of range");
+    TensorRef t = tensor_ref(m, idx);
+    hipStream_t s = m->ctx->stream;
+    if (t.norm) {
+        LQ8_HIP(hipMemcpyAsync(host_out, t.norm, t.norm_len * sizeof(float), hipMemcpyDeviceToHost, s));
+        LQ8_HIP(hipStreamSynchronize(s));
+        return LQ8_OK;
+    }
+    const size_t bytes = t.rows * t.w->nb * BLOCK_BYTES;
+    void* tmp = nullptr;
+    LQ8_HIP(hipMalloc(&tmp, bytes));
+    lq8_status st = launch_unpack_aos(s, t.w, t.row0, t.rows, (uint8_t*)tmp);
+    hipError_t e = hipSuccess;
+    if (!st) e = hipMemcpyAsync(host_out, tmp, bytes, hipMemcpyDeviceToHost, s);
+    if (!st && e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(tmp);
+    if (st) return st;
+    if (e != hipSuccess) return hip_fail(e, "export tensor");
+    return LQ8_OK;
+}
+
+lq8_status lq8_moe_weight_bytes(lq8_moe* m, size_t* bytes) {
+    CHECK_MOE(m);
+    if (!bytes) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    size_t total = 0;
+    const size_t count = lq8_moe_tensor_count(&m->c);
+    for (size_t i = 0; i < count; i++) {
+        TensorRef t = tensor_ref(m, i);
+        if (t.w) total += t.rows * t.w->nb * BLOCK_BYTES;
+    }
+    *bytes = total;
+    return LQ8_OK;
+}
+
+lq8_status lq8_moe_forward_device(lq8_moe* m, float* d_hidden, const float* d_scores, const int32_t* d_pos, size_t T) {
+    CHECK_MOE(m);
+    if (!d_hidden || !d_scores || !d_pos) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (T == 0 || T > m->c.max_batch) return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: T must be 1..max_batch");
+    if (((uintptr_t)d_hidden & 15) != 0) return fail(LQ8_ERR_INVALID_ARG, "hidden must be 16-byte aligned");
+    lq8_status st = enqueue_forward(m, d_hidden, d_scores, d_pos, (int)T);
+    if (st) return st;
+    m->last_T = T;
+    return LQ8_OK;
+}
+
+lq8_status lq8_moe_forward(lq8_moe* m, float* hidden, const float* scores, const int32_t* pos, size_t T) {
+    CHECK_MOE(m);
+    if (!hidden || !scores || !pos) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (T == 0 || T > m->c.max_batch) return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: T must be 1..max_batch");
+    for (size_t t = 0; t < T; t++)
+        if (pos[t] < 0 || (uint32_t)pos[t] >= m->c.max_positions)
+            return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "moe: position outside the KV cache");
+    hipStream_t s = m->ctx->stream;
+    const size_t H = m->c.hidden_size, E = m->c.num_experts, NL = m->c.num_layers;
+    LQ8_HIP(hipMemcpyAsync(m->hid_tmp, hidden, T * H * sizeof(float), hipMemcpyHostToDevice, s));
+    LQ8_HIP(hipMemcpyAsync(m->scores_tmp, scores, NL * T * E * sizeof(float), hipMemcpyHostToDevice, s));
+    LQ8_HIP(hipMemcpyAsync(m->pos_tmp, pos, T * sizeof(int32_t), hipMemcpyHostToDevice, s));
+    lq8_status st = enqueue_forward(m, m->hid_tmp, m->scores_tmp, m->pos_tmp, (int)T);
+    if (st) return st;
+    m->last_T = T;
+    LQ8_HIP(hipMemcpyAsync(hidden, m->hid_tmp, T * H * sizeof(float), hipMemcpyDeviceToHost, s));
+    LQ8_HIP(hipStreamSynchronize(s));
+    return LQ8_OK;
+}
+
+lq8_status lq8_moe_routing(lq8_moe* m, uint32_t* experts, float* weights) {
+    CHECK_MOE(m);
+    if (!experts || !weights) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    const size_t B = m->c.max_batch, K = m->c.top_k, T = m->last_T;
+    hipStream_t s = m->ctx->stream;
+    for (size_t l = 0; l < m->layers.size(); l++) {
+        LQ8_HIP(hipMemcpyAsync(experts + l * T * K, m->rids + l * B * K, T * K * sizeof(uint32_t),
+                               hipMemcpyDeviceToHost, s));
+        LQ8_HIP(hipMemcpyAsync(weights + l * T * K, m->rw + l * B * K, T * K * sizeof(float), hipMemcpyDeviceToHost, s));
+    }
+    LQ8_HIP(hipStreamSynchronize(s));
+    return LQ8_OK;
+}
+
+lq8_status lq8_moe_clear_kv_cache(lq8_moe* m) {
+    CHECK_MOE(m);
+    const size_t kv = (size_t)m->c.num_layers * m->c.max_batch * m->c.num_kv_heads * m->c.max_positions * 128;
+    LQ8_HIP(hipMemsetAsync(m->kc, 0, kv * sizeof(float), m->ctx->stream));
+    LQ8_HIP(hipMemsetAsync(m->vc, 0, kv * sizeof(float), m->ctx->stream));
+    LQ8_HIP(hipStreamSynchronize(m->ctx->stream));
+    return LQ8_OK;
+}
+
+lq8_status lq8_moe_free(lq8_moe* m) {
+    CHECK_MOE(m);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    release(m);
+    return LQ8_OK;
+}
+
+}  // extern "C"

@@ -85,6 +85,15 @@ class GemvProblemC(C.Structure):
     _fields_ = [("w", C.c_void_p), ("x", C.c_void_p), ("y", C.c_void_p)]
 
 
+class MoeConfigC(C.Structure):
+    _fields_ = [
+        ("hidden_size", C.c_uint32), ("num_heads", C.c_uint32), ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32), ("num_experts", C.c_uint32), ("top_k", C.c_uint32),
+        ("expert_intermediate_size", C.c_uint32), ("max_positions", C.c_uint32), ("max_batch", C.c_uint32),
+        ("num_layers", C.c_uint32), ("rms_norm_eps", C.c_float), ("rope_theta", C.c_double),
+    ]
+
+
 class GenStatsC(C.Structure):
     _fields_ = [("prefill_ms", C.c_double), ("decode_ms", C.c_double), ("decode_tokens_per_s", C.c_double),
                 ("used_graph", C.c_uint32)]
@@ -142,6 +151,18 @@ _SIGS = [
     ("lq8_generate_greedy", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.POINTER(GenStatsC)]),
     ("lq8_model_free", C.c_int, [C.c_void_p]),
+    ("lq8_moe_tensor_count", C.c_size_t, [C.POINTER(MoeConfigC)]),
+    ("lq8_moe_tensor_bytes", C.c_int, [C.POINTER(MoeConfigC), C.c_size_t, C.POINTER(C.c_size_t)]),
+    ("lq8_moe_create", C.c_int, [C.c_void_p, C.POINTER(MoeConfigC), C.c_void_p, C.POINTER(C.c_void_p)]),
+    ("lq8_moe_create_random", C.c_int,
+     [C.c_void_p, C.POINTER(MoeConfigC), C.c_uint64, C.c_float, C.POINTER(C.c_void_p)]),
+    ("lq8_moe_export_tensor", C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("lq8_moe_weight_bytes", C.c_int, [C.c_void_p, C.POINTER(C.c_size_t)]),
+    ("lq8_moe_forward_device", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    ("lq8_moe_forward", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    ("lq8_moe_routing", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    ("lq8_moe_clear_kv_cache", C.c_int, [C.c_void_p]),
+    ("lq8_moe_free", C.c_int, [C.c_void_p]),
 ]
 
 EXPORTED = [s[0] for s in _SIGS]
@@ -469,6 +490,121 @@ class Qwen3ForCausalLM:
     def free(self) -> None:
         if self.handle:
             _check(lib().lq8_model_free(self.handle))
+            self.handle = None
+
+
+# ---- Qwen3-MoE decoder layers --------------------------------------------------
+
+@dataclass
+class MoeConfig:
+    """Qwen3-MoE decoder layer dimensions (Qwen3-30B-A3B defaults)."""
+
+    hidden_size: int = 2048
+    num_heads: int = 32
+    num_kv_heads: int = 4
+    head_dim: int = 128
+    num_experts: int = 128
+    top_k: int = 8
+    expert_intermediate_size: int = 768
+    max_positions: int = 256
+    max_batch: int = 32
+    num_layers: int = 1
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+
+    def c(self) -> MoeConfigC:
+        return MoeConfigC(self.hidden_size, self.num_heads, self.num_kv_heads, self.head_dim, self.num_experts,
+                          self.top_k, self.expert_intermediate_size, self.max_positions, self.max_batch,
+                          self.num_layers, self.rms_norm_eps, self.rope_theta)
+
+    def per_layer(self) -> int:
+        return 8 + 3 * self.num_experts
+
+    def tensor_count(self) -> int:
+        return self.per_layer() * self.num_layers
+
+    def tensor_shape(self, idx: int):
+        """(kind, shape) of tensor ``idx`` in the table order of include/lq8.h."""
+        H, I, hd, E = self.hidden_size, self.expert_intermediate_size, self.head_dim, self.num_experts
+        QD, KD = self.num_heads * hd, self.num_kv_heads * hd
+        k = idx % self.per_layer()
+        if k < 8:
+            return [("f32", (H,)), ("f32", (H,)), ("f32", (hd,)), ("f32", (hd,)), ("q8", (QD, H)), ("q8", (KD, H)),
+                    ("q8", (KD, H)), ("q8", (H, QD))][k]
+        return ("q8", (I, H)) if k - 8 < 2 * E else ("q8", (H, I))
+
+
+def qwen3_30b_a3b_layers(num_layers: int = 1, max_positions: int = 256, max_batch: int = 32) -> MoeConfig:
+    return MoeConfig(num_layers=num_layers, max_positions=max_positions, max_batch=max_batch)
+
+
+class Qwen3MoeLayers:
+    """A stack of Qwen3-MoE decoder layers decoding T independent sequences
+    per call (sequence t owns KV cache slot t and writes position pos[t])."""
+
+    def __init__(self, ctx: Context, cfg: MoeConfig, handle: C.c_void_p):
+        self.ctx, self.cfg, self.handle = ctx, cfg, handle
+        self._c = cfg.c()
+
+    @classmethod
+    def load(cls, ctx: Context, cfg: MoeConfig, tensors: Sequence[np.ndarray]) -> "Qwen3MoeLayers":
+        if len(tensors) != cfg.tensor_count():
+            raise ModelError(f"expected {cfg.tensor_count()} tensors, got {len(tensors)}")
+        keep = [np.ascontiguousarray(t) for t in tensors]
+        arr = (C.c_void_p * len(keep))(*[t.ctypes.data for t in keep])
+        h = C.c_void_p()
+        c = cfg.c()
+        _check(lib().lq8_moe_create(ctx.handle, C.byref(c), arr, C.byref(h)))
+        return cls(ctx, cfg, h)
+
+    @classmethod
+    def random(cls, ctx: Context, cfg: MoeConfig, seed: int, std: float = 0.02) -> "Qwen3MoeLayers":
+        h = C.c_void_p()
+        c = cfg.c()
+        _check(lib().lq8_moe_create_random(ctx.handle, C.byref(c), seed, std, C.byref(h)))
+        return cls(ctx, cfg, h)
+
+    def export_tensor(self, idx: int) -> np.ndarray:
+        nb = C.c_size_t()
+        _check(lib().lq8_moe_tensor_bytes(C.byref(self._c), idx, C.byref(nb)))
+        kind, _ = self.cfg.tensor_shape(idx)
+        out = np.empty(nb.value // 4 if kind == "f32" else nb.value, dtype=np.float32 if kind == "f32" else np.uint8)
+        _check(lib().lq8_moe_export_tensor(self.handle, idx, _ptr(out)))
+        return out
+
+    def export_all(self):
+        return [self.export_tensor(i) for i in range(self.cfg.tensor_count())]
+
+    def weight_bytes(self) -> int:
+        nb = C.c_size_t()
+        _check(lib().lq8_moe_weight_bytes(self.handle, C.byref(nb)))
+        return nb.value
+
+    def forward(self, hidden: np.ndarray, scores: np.ndarray, pos: Sequence[int]) -> np.ndarray:
+        """hidden [T, H], scores [num_layers, T, E], pos [T] -> hidden after the last layer."""
+        h = np.array(hidden, dtype=np.float32, copy=True, order="C")
+        sc = np.ascontiguousarray(scores, dtype=np.float32)
+        p = np.ascontiguousarray(pos, dtype=np.int32)
+        _check(lib().lq8_moe_forward(self.handle, _ptr(h), _ptr(sc), _ptr(p), p.size))
+        return h
+
+    def forward_device(self, hidden: DeviceBuffer, scores: DeviceBuffer, pos: DeviceBuffer, T: int) -> None:
+        _check(lib().lq8_moe_forward_device(self.handle, hidden.ptr, scores.ptr, pos.ptr, T))
+
+    def routing(self, T: int):
+        """(experts [layers, T, k], weights [layers, T, k]) of the last forward."""
+        L, K = self.cfg.num_layers, self.cfg.top_k
+        ids = np.empty((L, T, K), dtype=np.uint32)
+        w = np.empty((L, T, K), dtype=np.float32)
+        _check(lib().lq8_moe_routing(self.handle, _ptr(ids), _ptr(w)))
+        return ids, w
+
+    def clear_kv_cache(self) -> None:
+        _check(lib().lq8_moe_clear_kv_cache(self.handle))
+
+    def free(self) -> None:
+        if self.handle:
+            _check(lib().lq8_moe_free(self.handle))
             self.handle = None
 
 
