@@ -118,6 +118,45 @@ def rotating_gemv_us(ctx, n, k, copies):
     return us
 
 
+def moe_stack(ctx, layers=48, reps=10):
+    """Qwen3-30B-A3B-style MoE decoder stack (48 layers, ~31.8 GB of Q8_0
+    weights resident), one decode step for T = 1 and T = 32 sequences at
+    position 128, router scores N(0, 1).  Bytes per step = attention weights +
+    the weights of every distinct routed expert of every layer."""
+    cfg = lq8.MoeConfig(num_layers=layers, max_positions=256, max_batch=32)
+    m = lq8.Qwen3MoeLayers.random(ctx, cfg, seed=5)
+    H, E = cfg.hidden_size, cfg.num_experts
+    q8 = lambda r, k: r * (k // 32) * 34
+    attn_b = q8(cfg.num_heads * 128 + 2 * cfg.num_kv_heads * 128, H) + q8(H, cfg.num_heads * 128)
+    exp_b = 2 * q8(cfg.expert_intermediate_size, H) + q8(H, cfg.expert_intermediate_size)
+    out = {"weights_gb": round(m.weight_bytes() / 1e9, 2), "position": 128}
+    for T in (1, 32):
+        rng = np.random.default_rng(T)
+        x = lq8.DeviceBuffer.from_array(ctx, rng.standard_normal((T, H)).astype(np.float32))
+        sc = lq8.DeviceBuffer.from_array(ctx, rng.standard_normal((layers, T, E)).astype(np.float32))
+        pos = lq8.DeviceBuffer.from_array(ctx, np.full(T, 128, np.int32))
+        for _ in range(3):
+            m.forward_device(x, sc, pos, T)
+        ctx.synchronize()
+        ids, _ = m.routing(T)
+        nact = [len(set(ids[l].ravel().tolist())) for l in range(layers)]
+        step_b = sum(attn_b + n * exp_b for n in nact)
+        ctx.timer_start()
+        for _ in range(reps):
+            m.forward_device(x, sc, pos, T)
+        ms = ctx.timer_stop() / reps
+        gbs = step_b / (ms * 1e-3) / 1e9
+        out[f"batch{T}"] = {"us_per_step": round(ms * 1e3, 1), "us_per_layer": round(ms * 1e3 / layers, 2),
+                            "tokens_per_s": round(T / (ms * 1e-3), 1), "bytes_per_step": step_b,
+                            "experts_per_layer": round(float(np.mean(nact)), 1), "gbs": round(gbs, 1),
+                            "pct_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"MoE {layers} layers, T={T}: {ms * 1e3:.0f} us/step ({ms * 1e3 / layers:.1f} us/layer), "
+            f"{gbs:.0f} GB/s, {T / (ms * 1e-3):.0f} tok/s")
+        x.free(); sc.free(); pos.free()
+    m.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -125,11 +164,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--only-step", action="store_true",
                     help="only the headline step and the calibration copy (for hardware-counter runs)")
     args = ap.parse_args()
     if args.only_step:
-        args.no_decode = args.no_cpu = True
+        args.no_decode = args.no_cpu = args.no_moe = True
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only (--gpus 1); multi-GPU sharding is a design "
                                    "note, not built"}))
@@ -220,6 +260,8 @@ def main():
                   "graph": runs[0]["used_graph"], "prompt": 128, "new_tokens": 128}
         log(f"decode: {tps:.1f} tok/s (median of 3), prefill {runs[0]['prefill_ms']:.2f} ms")
         model.free()
+
+    moe = None if args.no_moe else moe_stack(ctx)
     ctx.close()
 
     cpu = None if args.no_cpu else cpu_baseline()
@@ -255,6 +297,7 @@ def main():
         "gemv_3072x1024_us": None if args.only_step else round(c1_us, 3),
         "gemm_m512": gemm,
         "decode": decode,
+        "moe_qwen3_30b_a3b_48_layers": moe,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -386,15 +386,19 @@ __global__ __launch_bounds__(256) void k_gemv_grouped(const GemvProblemDev* __re
 
 // ---- multi-vector GEMV ------------------------------------------------------
 //
-// One workgroup (4 waves) per (problem, 16-row tile, vector split).  Up to VB
-// input vectors are staged in LDS at a time; a wave takes (group of CH pairs)
-// items, unpacks each 16-byte code chunk to floats once and runs the GEMV
-// order of gemv_tiles for every staged vector; the group sums go to LDS and
-// one thread per (vector, row) runs the tree over the groups.
+// One workgroup (4 waves) per (problem, 16-row tile, vector split); with
+// EPI_SWIGLU per (problem, gate tile i) and it also runs up tile i + rows/32.
+// Up to VB input vectors are staged in LDS at a time; a wave takes (tile,
+// group of CH pairs) items, unpacks each 16-byte code chunk to floats once
+// and runs the GEMV order of gemv_tiles for every staged vector; the group
+// sums go to LDS and one thread per (vector, row) runs the tree over the
+// groups.
 template <int XS, int EPI, int CH, int VB>
 __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
     extern __shared__ float smem[];
-    const int tiles_p = (a.rows + TILE_ROWS - 1) / TILE_ROWS;
+    constexpr int NT = EPI == EPI_SWIGLU ? 2 : 1;  // tiles per workgroup
+    const int tiles_all = (a.rows + TILE_ROWS - 1) / TILE_ROWS;
+    const int tiles_p = tiles_all / NT, tstride = tiles_all / NT;
     const int j = blockIdx.x / tiles_p, tile = blockIdx.x - j * tiles_p;
     if (j >= (a.n_prob ? *a.n_prob : 1)) return;
     const int e = a.prob_id ? a.prob_id[j] : j;
@@ -406,12 +410,13 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
     const int k = a.k, k4 = k >> 2, nb = k >> 5, np = (nb + 1) >> 1;
     const int G = (np + CH - 1) / CH;
     float* xs = smem;                    // [VB][np * 64]
-    float* gs = xs + VB * np * 64;       // [VB][G][16]
-    float* red = gs + VB * G * 16;       // [VB]
+    float* gs = xs + VB * np * 64;       // [VB][NT][G][16]
+    float* red = gs + VB * NT * G * 16;  // [VB]
     const int r = lane & 15, part = lane >> 4, bsel = part >> 1, half = part & 1;
     const size_t gt = (size_t)e * a.prob_tiles + tile;
     const int8_t* cbase = a.codes + gt * np * CHUNK_BYTES + lane * 16;
     const uint16_t* sbase = a.scales + gt * 2 * np * 16 + bsel * 16 + r;
+    const size_t cstep = (size_t)tstride * np * CHUNK_BYTES, sstep = (size_t)tstride * 2 * np * 16;
     for (int v0 = blockIdx.y * VB; v0 < vcnt; v0 += gridDim.y * VB) {
         const int nv = min(VB, vcnt - v0);
         // ---- stage nv vectors (transform per XS) ----
@@ -460,15 +465,16 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
             }
             __syncthreads();
         }
-        // ---- items: (group of CH pairs) ----
-        for (int g = wave; g < G; g += 4) {
+        // ---- items: (tile, group of CH pairs) ----
+        for (int it = wave; it < NT * G; it += 4) {
+            const int tt = it / G, g = it - tt * G;
             u32x4 cv[CH];
             uint16_t ds[CH];
 #pragma unroll
             for (int i = 0; i < CH; i++) {
                 const int c = min(g * CH + i, np - 1);
-                cv[i] = __builtin_nontemporal_load((const u32x4*)(cbase + (size_t)c * CHUNK_BYTES));
-                ds[i] = sbase[(size_t)c * 32];
+                cv[i] = __builtin_nontemporal_load((const u32x4*)(cbase + tt * cstep + (size_t)c * CHUNK_BYTES));
+                ds[i] = sbase[tt * sstep + (size_t)c * 32];
             }
             float wf[CH][16];
 #pragma unroll
@@ -511,24 +517,37 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
 #pragma unroll
                     for (int i = 0; i + s < CH; i += 2 * s)
                         if (i + s < cnt) t[i] = t[i] + t[i + s];
-                if (lane < 16) gs[(v * G + g) * 16 + lane] = t[0];
+                if (lane < 16) gs[((v * NT + tt) * G + g) * 16 + lane] = t[0];
             }
         }
         __syncthreads();
-        // ---- tree over the group sums, one thread per (vector, row) ----
-        if (tid < nv * 16) {
-            const int v = tid >> 4, rr = tid & 15;
-            float* col = gs + v * G * 16 + rr;
+        // ---- tree over the group sums, one thread per (vector, tile, row) ----
+        if (tid < nv * NT * 16) {
+            const int v = tid / (NT * 16), tt = (tid >> 4) % NT, rr = tid & 15;
+            float* col = gs + (v * NT + tt) * G * 16 + rr;
             for (int s = 1; s < G; s *= 2)
                 for (int i = 0; i + s < G; i += 2 * s) col[i * 16] = col[i * 16] + col[(i + s) * 16];
-            const float acc = col[0];
-            const int row = tile * TILE_ROWS + rr;
-            if (row < a.rows) {
+            if (EPI != EPI_SWIGLU) {
+                const float acc = col[0];
+                const int row = tile * TILE_ROWS + rr;
+                if (row < a.rows) {
+                    const int ent = vbeg + v0 + v;
+                    const int slot = a.slots ? a.slots[ent] : ent;
+                    float* yp = a.y + (size_t)slot * a.y_stride + row;
+                    if (EPI == EPI_RESID) *yp = a.resid[(size_t)slot * a.resid_stride + row] + acc;
+                    else *yp = acc;
+                }
+            }
+        }
+        if (EPI == EPI_SWIGLU) {
+            __syncthreads();
+            if (tid < nv * 16) {
+                const int v = tid >> 4, rr = tid & 15;
+                const float gate = gs[(v * NT) * G * 16 + rr], up = gs[(v * NT + 1) * G * 16 + rr];
+                const int row = tile * TILE_ROWS + rr;  // < rows / 2 (a multiple of 16)
                 const int ent = vbeg + v0 + v;
                 const int slot = a.slots ? a.slots[ent] : ent;
-                float* yp = a.y + (size_t)slot * a.y_stride + row;
-                if (EPI == EPI_RESID) *yp = a.resid[(size_t)slot * a.resid_stride + row] + acc;
-                else *yp = acc;
+                a.y[(size_t)slot * a.y_stride + row] = silu_mul(gate, up);
             }
         }
         __syncthreads();
@@ -650,7 +669,8 @@ namespace {
 
 template <int XS, int EPI, int CH>
 lq8_status mv_vb(hipStream_t s, const MvArgs& a, dim3 grid, int vb, size_t xs_floats_per_vec, int G) {
-    const size_t smem = ((size_t)vb * xs_floats_per_vec + (size_t)vb * G * 16 + 4) * sizeof(float);
+    const size_t NT = EPI == EPI_SWIGLU ? 2 : 1;
+    const size_t smem = ((size_t)vb * xs_floats_per_vec + (size_t)vb * NT * G * 16 + 4) * sizeof(float);
     if (smem > 64 * 1024) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: input staging exceeds 64 KiB of LDS");
     if (vb == 4) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 4>), grid, dim3(256), smem, s, a);
     else if (vb == 2) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 2>), grid, dim3(256), smem, s, a);
@@ -667,7 +687,7 @@ lq8_status mv_ch(hipStream_t s, const MvArgs& a, int max_probs, int vsplit) {
     const size_t per_vec = (size_t)np * 64;
     // vectors staged per pass: as many as fit in 40 KiB
     const int vb = per_vec * 4 * sizeof(float) <= 40 * 1024 ? 4 : per_vec * 2 * sizeof(float) <= 40 * 1024 ? 2 : 1;
-    const int tiles_p = (a.rows + TILE_ROWS - 1) / TILE_ROWS;
+    const int tiles_p = (a.rows + TILE_ROWS - 1) / TILE_ROWS / (EPI == EPI_SWIGLU ? 2 : 1);
     const dim3 grid((unsigned)(tiles_p * max_probs), (unsigned)vsplit);
     if (ch == 1) return mv_vb<XS, EPI, 1>(s, a, grid, vb, per_vec, G);
     if (ch == 2) return mv_vb<XS, EPI, 2>(s, a, grid, vb, per_vec, G);
@@ -684,6 +704,11 @@ lq8_status launch_gemv_mv(hipStream_t s, XSource xs, Epilogue epi, const MvArgs&
     if (xs == XS_RMSNORM && !a.norm_w) return fail(LQ8_ERR_INVALID_ARG, "gemv: norm weight is null");
     if (epi == EPI_ARGMAX || xs == XS_ATTN) return fail(LQ8_ERR_INVALID_ARG, "gemv: unsupported multi-vector mode");
     if (a.x_div <= 0) return fail(LQ8_ERR_INVALID_ARG, "gemv: x_div must be positive");
+    if (epi == EPI_SWIGLU) {
+        if (a.rows % (2 * TILE_ROWS) || xs != XS_RMSNORM)
+            return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: swiglu needs rows a multiple of 32 and a normed input");
+        return mv_ch<XS_RMSNORM, EPI_SWIGLU>(s, a, max_probs, vsplit);
+    }
     const bool resid = epi == EPI_RESID;
     switch (xs) {
         case XS_PLAIN: return resid ? mv_ch<XS_PLAIN, EPI_RESID>(s, a, max_probs, vsplit)

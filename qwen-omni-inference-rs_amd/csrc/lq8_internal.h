@@ -87,7 +87,10 @@ lq8_status ctx_scratch(lq8_ctx* ctx, size_t bytes, void** out);
 enum XSource : int { XS_PLAIN = 0, XS_RMSNORM = 1, XS_SILU = 2, XS_ATTN = 3 };
 // Output: y = W x, y = resid + W x, or y = W x plus the per-tile argmax
 // (value, index; last index on ties) of the logits.
-enum Epilogue : int { EPI_STORE = 0, EPI_RESID = 1, EPI_ARGMAX = 2 };
+// EPI_SWIGLU (multi-vector GEMV only): rows = [gate | up] halves; the
+// workgroup of gate tile i also runs up tile i and stores silu(gate) * up
+// (rows / 2 outputs per vector).
+enum Epilogue : int { EPI_STORE = 0, EPI_RESID = 1, EPI_ARGMAX = 2, EPI_SWIGLU = 3 };
 
 struct GemvArgs {
     const int8_t* codes;

@@ -7,9 +7,11 @@
 //   part  = attention segments per sequence    (q/k norm, RoPE, KV append)
 //   h2    = h + o(attention(part))             GEMV with the combine fused (T = 1),
 //                                              combine kernel + multi-vector GEMV (T > 1)
-//   route = top_k of softmax(scores)           one workgroup, expert lists on the device
-//   gu    = [gate|up]_e(RmsNorm(h2))           grouped multi-vector GEMV over the routed experts
-//   eo    = down_e(silu(gate) * up)            grouped multi-vector GEMV
+//   route = top_k of softmax(scores)           all layers in one launch before the first
+//                                              layer (scores are inputs); expert lists on the device
+//   act   = silu(gate_e x) * up_e x, x = RmsNorm(h2)   grouped multi-vector GEMV over the
+//                                              routed experts (gate and up tiles in one workgroup)
+//   eo    = down_e(act)                        grouped multi-vector GEMV
 //   h     = h2 + sum_e w_e * eo_e              ascending expert index
 // Every projection is the single-vector GEMV order per token, so each
 // token's result is independent of the batch it runs in.
@@ -45,10 +47,13 @@ struct lq8_moe {
     std::vector<MoeLayer> layers;
     float *cos_t = nullptr, *sin_t = nullptr;
     float *kc = nullptr, *vc = nullptr;  // [layer][seq][kv_head][max_pos][128]
-    float *h2 = nullptr, *qkv = nullptr, *apart = nullptr, *aout = nullptr, *gu = nullptr, *eo = nullptr;
+    float *h2 = nullptr, *qkv = nullptr, *apart = nullptr, *aout = nullptr;
+    float *gu = nullptr;  // [max_batch * top_k][expert_intermediate]: silu(gate) * up per slot
+    float *eo = nullptr;  // [max_batch * top_k][hidden]: expert outputs per slot
     uint32_t* rids = nullptr;  // [layer][max_batch][top_k]
     float* rw = nullptr;
-    int *n_act = nullptr, *act_e = nullptr, *vbeg = nullptr, *vcnt = nullptr, *slots = nullptr;
+    int *n_act = nullptr, *act_e = nullptr, *vbeg = nullptr, *vcnt = nullptr;  // per layer: [layer], [layer][E]
+    int* slots = nullptr;                                                      // [layer][max_batch * top_k]
     float *hid_tmp = nullptr, *scores_tmp = nullptr;
     int* pos_tmp = nullptr;
     size_t last_T = 0;
@@ -57,24 +62,52 @@ struct lq8_moe {
 namespace {
 
 // ---- router ------------------------------------------------------------------
-// One workgroup for the batch.  Wave w routes tokens w, w + 4, ...: lane l
-// holds scores l, l + 64, ...; m = max (exact in any order), e = exp(s - m),
-// S = SUM64(e) (lane l adds its entries in order, then the xor fold), p = e / S;
-// top_k rounds of a wave arg-max (higher p, then lower index); weights
-// p_r / (((p_0 + p_1) + p_2) + ...).  Then thread e lists the slots
-// (t * top_k + r) routed to expert e in token order, and the active experts
-// are numbered in ascending order (n_act, act_e, vbeg, vcnt, slots).
-__global__ __launch_bounds__(256) void k_moe_route(const float* __restrict__ scores, int T, int E, int K,
-                                                   uint32_t* __restrict__ rids, float* __restrict__ rw,
-                                                   int* __restrict__ n_act, int* __restrict__ act_e,
-                                                   int* __restrict__ vbeg, int* __restrict__ vcnt,
-                                                   int* __restrict__ slots) {
+// One workgroup of 16 waves for the batch.  Wave w routes tokens w, w + 16,
+// ...: lane l holds scores l, l + 64, ...; m = max (exact in any order),
+// e = exp(s - m), S = SUM64(e) (lane l adds its entries in order, then the
+// xor fold), p = e / S.  An entry's rank is the number of entries with a
+// larger p or an equal p and a lower index; ranks below top_k are chosen, in
+// rank order; weights p_r / (((p_0 + p_1) + p_2) + ...).  Then the routed
+// (token, rank) slots t * top_k + r are counted per expert, the active
+// experts numbered in ascending order (n_act, act_e, vbeg, vcnt) and each
+// slot placed in its expert's list (slots).  The order inside one expert's
+// list is whatever the atomics give: every slot is computed on its own, so
+// results do not depend on it.
+constexpr int ROUTE_WAVES = 16;
+struct RouteArgs {
+    const float* scores;  // [layers][T][E]
+    int T, E, K, B;       // B: per-layer stride of the slot tables (max_batch)
+    uint32_t* rids;       // [layers][B][K]
+    float* rw;            // [layers][B][K]
+    int* n_act;           // [layers]
+    int* act_e;           // [layers][E]
+    int* vbeg;            // [layers][E]
+    int* vcnt;            // [layers][E]
+    int* slots;           // [layers][B * K]
+};
+__global__ __launch_bounds__(64 * ROUTE_WAVES) void k_moe_route(RouteArgs ra) {
+    __shared__ float4 sp4[ROUTE_WAVES][MOE_MAX_EXPERTS / 4];
+    __shared__ float selp[ROUTE_WAVES][MOE_MAX_TOPK];
     __shared__ int sid[MOE_MAX_BATCH * MOE_MAX_TOPK];
-    __shared__ int cnt[MOE_MAX_EXPERTS], beg[MOE_MAX_EXPERTS];
+    __shared__ int cnt[MOE_MAX_EXPERTS], beg[MOE_MAX_EXPERTS], fill[MOE_MAX_EXPERTS];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const float NEG = -__builtin_huge_valf();
-    for (int t = wave; t < T; t += 4) {
+    const int l = blockIdx.x, T = ra.T, E = ra.E, K = ra.K;
+    const float* __restrict__ scores = ra.scores + (size_t)l * T * E;
+    uint32_t* __restrict__ rids = ra.rids + (size_t)l * ra.B * K;
+    float* __restrict__ rw = ra.rw + (size_t)l * ra.B * K;
+    int* __restrict__ act_e = ra.act_e + (size_t)l * E;
+    int* __restrict__ vbeg = ra.vbeg + (size_t)l * E;
+    int* __restrict__ vcnt = ra.vcnt + (size_t)l * E;
+    int* __restrict__ slots = ra.slots + (size_t)l * ra.B * K;
+    float* sp = (float*)sp4[wave];
+    const int E16 = (E + 15) & ~15;  // the rank loop reads 16 entries at a time; padding is -inf
+    for (int e = tid; e < E; e += 64 * ROUTE_WAVES) {
+        cnt[e] = 0;
+        fill[e] = 0;
+    }
+    for (int t = wave; t < T; t += ROUTE_WAVES) {
         float p[4];
         float m = NEG;
 #pragma unroll
@@ -96,67 +129,94 @@ __global__ __launch_bounds__(256) void k_moe_route(const float* __restrict__ sco
 #pragma unroll
         for (int d = 32; d >= 1; d >>= 1) acc = acc + __shfl_xor(acc, d, 64);
 #pragma unroll
-        for (int j = 0; j < 4; j++) p[j] = lane + 64 * j < E ? __fdiv_rn(p[j], acc) : NEG;
+        for (int j = 0; j < 4; j++) {
+            const int i = lane + 64 * j;
+            if (i < E) p[j] = __fdiv_rn(p[j], acc);
+            if (i < E16) sp[i] = p[j];  // NEG past E
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+        // rank = entries with a larger p, or an equal p and a lower index
+        int rank[4] = {0, 0, 0, 0};
+        for (int i0 = 0; i0 < E16; i0 += 16) {
+            float4 q4[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) q4[u] = sp4[wave][(i0 >> 2) + u];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float q[4] = {q4[u].x, q4[u].y, q4[u].z, q4[u].w};
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int i2 = i0 + 4 * u + c;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int i = lane + 64 * j;
+                        rank[j] += (q[c] > p[j] || (q[c] == p[j] && i2 < i)) ? 1 : 0;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = lane + 64 * j;
+            if (i < E && rank[j] < K) {
+                selp[wave][rank[j]] = p[j];
+                rids[t * K + rank[j]] = (uint32_t)i;
+                sid[t * K + rank[j]] = i;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+        float pk[MOE_MAX_TOPK];
+#pragma unroll
+        for (int r = 0; r < MOE_MAX_TOPK; r++) pk[r] = r < K ? selp[wave][r] : 0.0f;
         float tot = 0.0f;
-        float pr[MOE_MAX_TOPK];
-        int ir[MOE_MAX_TOPK];
-        for (int r = 0; r < K; r++) {
-            float bv = NEG;
-            int bi = 0x7fffffff;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int i = lane + 64 * j;
-                if (p[j] > bv || (p[j] == bv && i < bi)) { bv = p[j]; bi = i; }
-            }
-#pragma unroll
-            for (int d = 32; d >= 1; d >>= 1) {
-                const float ov = __shfl_xor(bv, d, 64);
-                const int oi = __shfl_xor(bi, d, 64);
-                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (lane + 64 * j == bi) p[j] = NEG;  // taken
-            pr[r < MOE_MAX_TOPK ? r : 0] = bv;
-            ir[r < MOE_MAX_TOPK ? r : 0] = bi;
-            tot = tot + bv;
-        }
-        if (lane < K) {
-            float w = 0.0f;
-            int id = 0;
-            for (int r = 0; r < K; r++)
-                if (r == lane) { w = pr[r]; id = ir[r]; }
-            rids[t * K + lane] = (uint32_t)id;
-            rw[t * K + lane] = __fdiv_rn(w, tot);
-            sid[t * K + lane] = id;
-        }
+        for (int r = 0; r < MOE_MAX_TOPK; r++)
+            if (r < K) tot = tot + pk[r];
+        if (lane < K) rw[t * K + lane] = __fdiv_rn(selp[wave][lane], tot);
+        __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
-    for (int e = tid; e < E; e += 256) {
-        int c = 0;
-        for (int s = 0; s < T * K; s++) c += sid[s] == e;
-        cnt[e] = c;
-    }
+    for (int s = tid; s < T * K; s += 64 * ROUTE_WAVES) atomicAdd(&cnt[sid[s]], 1);
     __syncthreads();
-    if (tid == 0) {
-        int na = 0, off = 0;
-        for (int e = 0; e < E; e++) {
-            beg[e] = off;
-            if (cnt[e]) {
-                act_e[na] = e;
-                vbeg[na] = off;
-                vcnt[na] = cnt[e];
-                na++;
-                off += cnt[e];
+    if (wave == 0) {
+        // ascending scan over the experts: lane l owns experts 4l .. 4l + 3
+        int c[4], nz = 0, tot = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int e = 4 * lane + q;
+            c[q] = e < E ? cnt[e] : 0;
+            tot += c[q];
+            nz += c[q] > 0;
+        }
+        int ptot = tot, pnz = nz;  // inclusive prefix over lanes
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int a1 = __shfl_up(ptot, d, 64), a2 = __shfl_up(pnz, d, 64);
+            if (lane >= d) { ptot += a1; pnz += a2; }
+        }
+        int off = ptot - tot, j = pnz - nz;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int e = 4 * lane + q;
+            if (e < E) {
+                beg[e] = off;
+                if (c[q]) {
+                    act_e[j] = e;
+                    vbeg[j] = off;
+                    vcnt[j] = c[q];
+                    j++;
+                }
+                off += c[q];
             }
         }
-        *n_act = na;
+        if (lane == 63) ra.n_act[l] = pnz;
     }
     __syncthreads();
-    for (int e = tid; e < E; e += 256) {
-        int o = beg[e];
-        for (int s = 0; s < T * K; s++)
-            if (sid[s] == e) slots[o++] = s;
+    for (int s = tid; s < T * K; s += 64 * ROUTE_WAVES) {
+        const int e = sid[s];
+        slots[beg[e] + atomicAdd(&fill[e], 1)] = s;
     }
 }
 
@@ -166,24 +226,27 @@ __global__ __launch_bounds__(256) void k_moe_route(const float* __restrict__ sco
 __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ h2, const float* __restrict__ eo,
                                                      const uint32_t* __restrict__ rids, const float* __restrict__ rw,
                                                      int K, int H, float* __restrict__ out) {
+    __shared__ int order[MOE_MAX_TOPK];  // ranks in ascending expert index
     const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (threadIdx.x < K) {
+        const uint32_t me = rids[t * K + threadIdx.x];
+        int below = 0;
+        for (int r = 0; r < K; r++) below += rids[t * K + r] < me;
+        order[below] = threadIdx.x;  // expert ids of a token are distinct
+    }
+    __syncthreads();
     if (i >= H) return;
-    uint32_t id[MOE_MAX_TOPK];
-    int rk[MOE_MAX_TOPK];
-    for (int r = 0; r < K; r++) {
-        id[r] = rids[t * K + r];
-        rk[r] = r;
+    float wv[MOE_MAX_TOPK], ev[MOE_MAX_TOPK];
+#pragma unroll
+    for (int q = 0; q < MOE_MAX_TOPK; q++) {
+        const int slot = t * K + order[q < K ? q : 0];
+        wv[q] = rw[slot];
+        ev[q] = eo[(size_t)slot * H + i];
     }
-    for (int a = 1; a < K; a++)  // insertion sort by expert index (distinct ids)
-        for (int b = a; b > 0 && id[b - 1] > id[b]; b--) {
-            const uint32_t ti = id[b]; id[b] = id[b - 1]; id[b - 1] = ti;
-            const int tr = rk[b]; rk[b] = rk[b - 1]; rk[b - 1] = tr;
-        }
     float acc = 0.0f;
-    for (int r = 0; r < K; r++) {
-        const int slot = t * K + rk[r];
-        acc = acc + rw[slot] * eo[(size_t)slot * H + i];
-    }
+#pragma unroll
+    for (int q = 0; q < MOE_MAX_TOPK; q++)
+        if (q < K) acc = acc + wv[q] * ev[q];
     out[(size_t)t * H + i] = h2[(size_t)t * H + i] + acc;
 }
 
@@ -277,10 +340,10 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_moe_config* c, lq8_moe* m) {
     LQ8_HIP(hipMemset(m->vc, 0, kv * sizeof(float)));
     if ((st = dalloc(&m->h2, B * H)) || (st = dalloc(&m->qkv, B * m->QKV)) ||
         (st = dalloc(&m->apart, B * m->cmax * c->num_heads * ATT_PART_STRIDE)) || (st = dalloc(&m->aout, B * m->QD)) ||
-        (st = dalloc(&m->gu, B * K * 2 * I)) || (st = dalloc(&m->eo, B * K * H)) ||
-        (st = dalloc(&m->rids, NL * B * K)) || (st = dalloc(&m->rw, NL * B * K)) || (st = dalloc(&m->n_act, 1)) ||
-        (st = dalloc(&m->act_e, E)) || (st = dalloc(&m->vbeg, E)) || (st = dalloc(&m->vcnt, E)) ||
-        (st = dalloc(&m->slots, B * K)) || (st = dalloc(&m->hid_tmp, B * H)) ||
+        (st = dalloc(&m->gu, B * K * I)) || (st = dalloc(&m->eo, B * K * H)) ||
+        (st = dalloc(&m->rids, NL * B * K)) || (st = dalloc(&m->rw, NL * B * K)) || (st = dalloc(&m->n_act, NL)) ||
+        (st = dalloc(&m->act_e, NL * E)) || (st = dalloc(&m->vbeg, NL * E)) || (st = dalloc(&m->vcnt, NL * E)) ||
+        (st = dalloc(&m->slots, NL * B * K)) || (st = dalloc(&m->hid_tmp, B * H)) ||
         (st = dalloc(&m->scores_tmp, NL * B * E)) || (st = dalloc(&m->pos_tmp, B)))
         return st;
     return LQ8_OK;
@@ -340,8 +403,17 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
     const int vsplit = (T + 3) / 4;
     const int max_probs = std::min(E, T * K);
     lq8_status st;
+    // the router reads only the given scores: every layer's routing in one launch
+    RouteArgs ra{d_scores, T, E, K, B, m->rids, m->rw, m->n_act, m->act_e, m->vbeg, m->vcnt, m->slots};
+    hipLaunchKernelGGL(k_moe_route, dim3((unsigned)m->layers.size()), dim3(64 * ROUTE_WAVES), 0, s, ra);
+    LQ8_HIP(hipGetLastError());
     for (size_t l = 0; l < m->layers.size(); l++) {
         MoeLayer& L = m->layers[l];
+        int* n_act = m->n_act + l;
+        int* act_e = m->act_e + l * E;
+        int* vbeg = m->vbeg + l * E;
+        int* vcnt = m->vcnt + l * E;
+        int* slots = m->slots + l * (size_t)B * K;
         // input_layernorm + q|k|v
         if (T == 1) {
             GemvArgs g{L.qkv->codes, L.qkv->scales, d_hidden, L.in_norm, m->qkv, nullptr, nullptr, nullptr,
@@ -378,25 +450,21 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
             a.resid = d_hidden; a.resid_stride = H;
             if ((st = launch_gemv_mv(s, XS_PLAIN, EPI_RESID, a, 1, vsplit))) return st;
         }
-        // router -> expert lists
         uint32_t* rids = m->rids + l * B * K;
         float* rw = m->rw + l * B * K;
-        hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, s, d_scores + l * (size_t)T * E, T, E, K, rids, rw,
-                           m->n_act, m->act_e, m->vbeg, m->vcnt, m->slots);
-        LQ8_HIP(hipGetLastError());
-        // post_attention_layernorm + [gate|up] of each routed expert
+        // post_attention_layernorm + gate and up of each routed expert -> silu(gate) * up
         MvArgs g{};
         g.codes = L.gu->codes; g.scales = L.gu->scales; g.rows = 2 * I; g.k = H; g.prob_tiles = 2 * I / TILE_ROWS;
-        g.n_prob = m->n_act; g.prob_id = m->act_e; g.vec_begin = m->vbeg; g.vec_count = m->vcnt; g.slots = m->slots;
-        g.x = m->h2; g.x_stride = H; g.x_div = K; g.y = m->gu; g.y_stride = 2 * I;
+        g.n_prob = n_act; g.prob_id = act_e; g.vec_begin = vbeg; g.vec_count = vcnt; g.slots = slots;
+        g.x = m->h2; g.x_stride = H; g.x_div = K; g.y = m->gu; g.y_stride = I;
         g.norm_w = L.post_norm; g.eps = c.rms_norm_eps;
-        if ((st = launch_gemv_mv(s, XS_RMSNORM, EPI_STORE, g, max_probs, 1))) return st;
-        // down(silu(gate) * up) of each routed expert
+        if ((st = launch_gemv_mv(s, XS_RMSNORM, EPI_SWIGLU, g, max_probs, 1))) return st;
+        // down of each routed expert
         MvArgs d{};
         d.codes = L.down->codes; d.scales = L.down->scales; d.rows = H; d.k = I; d.prob_tiles = H / TILE_ROWS;
-        d.n_prob = m->n_act; d.prob_id = m->act_e; d.vec_begin = m->vbeg; d.vec_count = m->vcnt; d.slots = m->slots;
-        d.x = m->gu; d.x_stride = 2 * I; d.x_div = 1; d.y = m->eo; d.y_stride = H;
-        if ((st = launch_gemv_mv(s, XS_SILU, EPI_STORE, d, max_probs, 1))) return st;
+        d.n_prob = n_act; d.prob_id = act_e; d.vec_begin = vbeg; d.vec_count = vcnt; d.slots = slots;
+        d.x = m->gu; d.x_stride = I; d.x_div = 1; d.y = m->eo; d.y_stride = H;
+        if ((st = launch_gemv_mv(s, XS_PLAIN, EPI_STORE, d, max_probs, 1))) return st;
         // h = h2 + experts (ascending expert index)
         hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s, m->h2, m->eo,
                            rids, rw, K, H, d_hidden);
