@@ -489,6 +489,9 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
                 }
             }
             const int cnt = min(CH, np - g * CH);
+            float dsf[CH];
+#pragma unroll
+            for (int i = 0; i < CH; i++) dsf[i] = f16_bits_to_f32(ds[i]);
             for (int v = 0; v < nv; v++) {
                 const float* xv = xs + v * np * 64;
                 float t[CH];
@@ -505,12 +508,12 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
                         h = fmaf(wf[i][4 * q + 2], xq.z, h);
                         h = fmaf(wf[i][4 * q + 3], xq.w, h);
                     }
-                    const float o = __shfl_xor(h, 16, 64);
-                    const float h0 = half ? o : h, h1 = half ? h : o;
-                    const float vb = (h0 + h1) * f16_bits_to_f32(ds[i]);
+                    // h0 + h1 and v_2p + v_2p+1: IEEE addition is commutative, so
+                    // either lane of a pair computes the same bits without a select
+                    const float vb = (h + __shfl_xor(h, 16, 64)) * dsf[i];
                     const float ov = __shfl_xor(vb, 32, 64);
                     if (2 * p + 1 >= nb) t[i] = bsel ? ov : vb;
-                    else t[i] = bsel ? ov + vb : vb + ov;
+                    else t[i] = vb + ov;
                 }
 #pragma unroll
                 for (int s = 1; s < CH; s *= 2)
