@@ -149,9 +149,13 @@ struct Stage {
             __syncthreads();
             if (tid < 64) {
                 float acc = 0.0f;
-                for (int i = tid; i < k; i += 64) {
-                    const float v = xs[i];
-                    acc = acc + v * v;
+                for (int i0 = tid; i0 < k; i0 += 64 * 8) {  // 8 LDS reads in flight, then the adds in order
+                    float v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) v[u] = xs[min(i0 + 64 * u, k - 1)];
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+                        if (i0 + 64 * u < k) acc = acc + v[u] * v[u];
                 }
 #pragma unroll
                 for (int d = 32; d >= 1; d >>= 1) acc = acc + __shfl_xor(acc, d, 64);
@@ -446,9 +450,13 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
             if (wave < nv) {
                 const float* xv = xs + wave * np * 64;
                 float acc = 0.0f;
-                for (int i = lane; i < k; i += 64) {
-                    const float v = xv[i];
-                    acc = acc + v * v;
+                for (int i0 = lane; i0 < k; i0 += 64 * 8) {
+                    float v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) v[u] = xv[min(i0 + 64 * u, k - 1)];
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+                        if (i0 + 64 * u < k) acc = acc + v[u] * v[u];
                 }
 #pragma unroll
                 for (int d = 32; d >= 1; d >>= 1) acc = acc + __shfl_xor(acc, d, 64);
