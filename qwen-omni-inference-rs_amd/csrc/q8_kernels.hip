@@ -330,7 +330,7 @@ __device__ __forceinline__ void gemm_combine(float4 (*part)[S > 1 ? S - 1 : 1][4
 // so the int32 dot is exact).  Accumulator layout: lane l holds column
 // l % 32, register i holds row 8 * (i / 4) + 4 * (l / 32) + i % 4.
 template <int S>
-__global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(3))) void k_gemm(GemmArgs g) {
+__global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(S == 1 ? 2 : 3))) void k_gemm(GemmArgs g) {
     __shared__ float4 part[2][S > 1 ? S - 1 : 1][4][64];
     const int lane = threadIdx.x & 63;
     const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
