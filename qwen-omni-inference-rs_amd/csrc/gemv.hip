@@ -716,9 +716,10 @@ lq8_status launch_gemv_mv(hipStream_t s, XSource xs, Epilogue epi, const MvArgs&
     if (epi == EPI_ARGMAX || xs == XS_ATTN) return fail(LQ8_ERR_INVALID_ARG, "gemv: unsupported multi-vector mode");
     if (a.x_div <= 0) return fail(LQ8_ERR_INVALID_ARG, "gemv: x_div must be positive");
     if (epi == EPI_SWIGLU) {
-        if (a.rows % (2 * TILE_ROWS) || xs != XS_RMSNORM)
-            return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: swiglu needs rows a multiple of 32 and a normed input");
-        return mv_ch<XS_RMSNORM, EPI_SWIGLU>(s, a, max_probs, vsplit);
+        if (a.rows % (2 * TILE_ROWS) || (xs != XS_RMSNORM && xs != XS_PLAIN))
+            return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: swiglu needs rows a multiple of 32 and a plain or normed input");
+        return xs == XS_PLAIN ? mv_ch<XS_PLAIN, EPI_SWIGLU>(s, a, max_probs, vsplit)
+                              : mv_ch<XS_RMSNORM, EPI_SWIGLU>(s, a, max_probs, vsplit);
     }
     const bool resid = epi == EPI_RESID;
     switch (xs) {

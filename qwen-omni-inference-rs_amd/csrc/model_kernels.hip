@@ -331,18 +331,37 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_rows(AttnRowsLaunch a) {
 // RmsNorm of each row (src/rms_norm.rs:143-176), one wave per row.
 __global__ __launch_bounds__(64) void k_rms_norm_rows(const float* __restrict__ x, const float* __restrict__ w, int dim,
                                                       float eps, float* __restrict__ y) {
+    constexpr int U = 16;  // loads in flight per lane
     const int r = blockIdx.x, lane = threadIdx.x;
     const float* xr = x + (size_t)r * dim;
     float acc = 0.0f;
-    for (int i = lane; i < dim; i += 64) {
-        const float v = bf16_round(xr[i]);
-        acc = acc + v * v;
+    for (int i0 = lane; i0 < dim; i0 += 64 * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = xr[min(i0 + 64 * u, dim - 1)];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (i0 + 64 * u < dim) {
+                const float b = bf16_round(v[u]);
+                acc = acc + b * b;
+            }
     }
     acc = wave_sum64(acc);
     const float mean = __fdiv_rn(acc, (float)dim);
     const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(mean + eps));
     float* yr = y + (size_t)r * dim;
-    for (int i = lane; i < dim; i += 64) yr[i] = bf16_round((bf16_round(xr[i]) * inv) * bf16_round(w[i]));
+    for (int i0 = lane; i0 < dim; i0 += 64 * U) {
+        float v[U], wv[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = min(i0 + 64 * u, dim - 1);
+            v[u] = xr[i];
+            wv[u] = w[i];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (i0 + 64 * u < dim) yr[i0 + 64 * u] = bf16_round((bf16_round(v[u]) * inv) * bf16_round(wv[u]));
+    }
 }
 
 // act = silu(gate) * up (src/mlp.rs:151-164; silu src/tensor.rs:1978).

@@ -48,6 +48,7 @@ struct lq8_moe {
     float *cos_t = nullptr, *sin_t = nullptr;
     float *kc = nullptr, *vc = nullptr;  // [layer][seq][kv_head][max_pos][128]
     float *h2 = nullptr, *qkv = nullptr, *apart = nullptr, *aout = nullptr;
+    float* xn = nullptr;  // [max_batch][hidden]: RmsNorm rows (batched decode)
     float *gu = nullptr;  // [max_batch * top_k][expert_intermediate]: silu(gate) * up per slot
     float *eo = nullptr;  // [max_batch * top_k][hidden]: expert outputs per slot
     uint32_t* rids = nullptr;  // [layer][max_batch][top_k]
@@ -294,7 +295,7 @@ void release(lq8_moe* m) {
         F(L.in_norm); F(L.post_norm); F(L.q_norm); F(L.k_norm);
     }
     F(m->cos_t); F(m->sin_t); F(m->kc); F(m->vc);
-    F(m->h2); F(m->qkv); F(m->apart); F(m->aout); F(m->gu); F(m->eo);
+    F(m->h2); F(m->xn); F(m->qkv); F(m->apart); F(m->aout); F(m->gu); F(m->eo);
     F(m->rids); F(m->rw); F(m->n_act); F(m->act_e); F(m->vbeg); F(m->vcnt); F(m->slots);
     F(m->hid_tmp); F(m->scores_tmp); F(m->pos_tmp);
     delete m;
@@ -338,7 +339,7 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_moe_config* c, lq8_moe* m) {
     if ((st = dalloc(&m->kc, kv)) || (st = dalloc(&m->vc, kv))) return st;
     LQ8_HIP(hipMemset(m->kc, 0, kv * sizeof(float)));
     LQ8_HIP(hipMemset(m->vc, 0, kv * sizeof(float)));
-    if ((st = dalloc(&m->h2, B * H)) || (st = dalloc(&m->qkv, B * m->QKV)) ||
+    if ((st = dalloc(&m->h2, B * H)) || (st = dalloc(&m->xn, B * H)) || (st = dalloc(&m->qkv, B * m->QKV)) ||
         (st = dalloc(&m->apart, B * m->cmax * c->num_heads * ATT_PART_STRIDE)) || (st = dalloc(&m->aout, B * m->QD)) ||
         (st = dalloc(&m->gu, B * K * I)) || (st = dalloc(&m->eo, B * K * H)) ||
         (st = dalloc(&m->rids, NL * B * K)) || (st = dalloc(&m->rw, NL * B * K)) || (st = dalloc(&m->n_act, NL)) ||
@@ -414,17 +415,19 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
         int* vbeg = m->vbeg + l * E;
         int* vcnt = m->vcnt + l * E;
         int* slots = m->slots + l * (size_t)B * K;
-        // input_layernorm + q|k|v
+        // input_layernorm + q|k|v.  T = 1: the norm is fused into the GEMV's
+        // input staging; T > 1: the rows are normed once (the same arithmetic)
+        // instead of once per output tile.
         if (T == 1) {
             GemvArgs g{L.qkv->codes, L.qkv->scales, d_hidden, L.in_norm, m->qkv, nullptr, nullptr, nullptr,
                        (int)m->QKV, H, c.rms_norm_eps};
             if ((st = launch_gemv(s, XS_RMSNORM, EPI_STORE, g))) return st;
         } else {
+            if ((st = launch_rms_norm_rows(s, d_hidden, L.in_norm, T, H, c.rms_norm_eps, m->xn))) return st;
             MvArgs a{};
             a.codes = L.qkv->codes; a.scales = L.qkv->scales; a.rows = (int)m->QKV; a.k = H;
-            a.nvec = T; a.x = d_hidden; a.x_stride = H; a.x_div = 1; a.y = m->qkv; a.y_stride = (int)m->QKV;
-            a.norm_w = L.in_norm; a.eps = c.rms_norm_eps;
-            if ((st = launch_gemv_mv(s, XS_RMSNORM, EPI_STORE, a, 1, vsplit))) return st;
+            a.nvec = T; a.x = m->xn; a.x_stride = H; a.x_div = 1; a.y = m->qkv; a.y_stride = (int)m->QKV;
+            if ((st = launch_gemv_mv(s, XS_PLAIN, EPI_STORE, a, 1, vsplit))) return st;
         }
         // q/k norm, RoPE, KV append, attention per segment, per sequence
         AttnSegLaunch at{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->kc + l * layer_kv, m->vc + l * layer_kv,
@@ -453,12 +456,21 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
         uint32_t* rids = m->rids + l * B * K;
         float* rw = m->rw + l * B * K;
         // post_attention_layernorm + gate and up of each routed expert -> silu(gate) * up
+        // (the norm fused at T = 1, once per row at T > 1, as above)
         MvArgs g{};
         g.codes = L.gu->codes; g.scales = L.gu->scales; g.rows = 2 * I; g.k = H; g.prob_tiles = 2 * I / TILE_ROWS;
         g.n_prob = n_act; g.prob_id = act_e; g.vec_begin = vbeg; g.vec_count = vcnt; g.slots = slots;
-        g.x = m->h2; g.x_stride = H; g.x_div = K; g.y = m->gu; g.y_stride = I;
-        g.norm_w = L.post_norm; g.eps = c.rms_norm_eps;
-        if ((st = launch_gemv_mv(s, XS_RMSNORM, EPI_SWIGLU, g, max_probs, 1))) return st;
+        g.x_stride = H; g.x_div = K; g.y = m->gu; g.y_stride = I;
+        if (T == 1) {
+            g.x = m->h2;
+            g.norm_w = L.post_norm;
+            g.eps = c.rms_norm_eps;
+            if ((st = launch_gemv_mv(s, XS_RMSNORM, EPI_SWIGLU, g, max_probs, 1))) return st;
+        } else {
+            if ((st = launch_rms_norm_rows(s, m->h2, L.post_norm, T, H, c.rms_norm_eps, m->xn))) return st;
+            g.x = m->xn;
+            if ((st = launch_gemv_mv(s, XS_PLAIN, EPI_SWIGLU, g, max_probs, 1))) return st;
+        }
         // down of each routed expert
         MvArgs d{};
         d.codes = L.down->codes; d.scales = L.down->scales; d.rows = H; d.k = I; d.prob_tiles = H / TILE_ROWS;
