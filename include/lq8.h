@@ -42,6 +42,13 @@ typedef enum {
     LQ8_ERR_MODEL = 8             /* LludaError::Model */
 } lq8_status;
 
+/* Element type of a host tensor handed to a loader. */
+typedef enum {
+    LQ8_DTYPE_Q8_0 = 0, /* GGUF block_q8_0 rows (34 bytes per 32 values) */
+    LQ8_DTYPE_F32 = 1,
+    LQ8_DTYPE_BF16 = 2  /* little-endian bf16, as safetensors stores it */
+} lq8_dtype;
+
 typedef struct lq8_ctx lq8_ctx;
 typedef struct lq8_weight lq8_weight;
 typedef struct lq8_model lq8_model;
@@ -87,6 +94,11 @@ lq8_status lq8_timer_stop(lq8_ctx* ctx, float* elapsed_ms);
 lq8_status lq8_weight_upload(lq8_ctx* ctx, const void* blocks, size_t n_out, size_t k_in, lq8_weight** out);
 /* Quantizes f32 [n_out, k_in] on the device (bit-exact with lq8_quantize_q8_0). */
 lq8_status lq8_weight_quantize_upload(lq8_ctx* ctx, const float* w, size_t n_out, size_t k_in, lq8_weight** out);
+/* The same from bf16 rows (checkpoint weights, ModelWeights::from_safetensors,
+ * src/loader.rs:68-188): a bf16 value widens exactly to f32, then the Q8_0
+ * quantizer runs on the device. */
+lq8_status lq8_weight_quantize_upload_bf16(lq8_ctx* ctx, const uint16_t* w, size_t n_out, size_t k_in,
+                                           lq8_weight** out);
 /* Device N(0, std) weights from a counter-based generator, quantized on the device. */
 lq8_status lq8_weight_random(lq8_ctx* ctx, size_t n_out, size_t k_in, uint64_t seed, uint64_t stream, float std,
                              lq8_weight** out);
@@ -163,6 +175,11 @@ size_t lq8_model_tensor_count(const lq8_qwen3_config* cfg);
 lq8_status lq8_model_tensor_bytes(const lq8_qwen3_config* cfg, size_t index, size_t* bytes);
 lq8_status lq8_model_create(lq8_ctx* ctx, const lq8_qwen3_config* cfg, const void* const* tensors,
                             lq8_model** out);
+/* The same table with a type per tensor (quantize-on-load): matrices may be
+ * LQ8_DTYPE_Q8_0 blocks (a GGUF file), or BF16 / F32 rows (a safetensors
+ * checkpoint) quantized on the device; norms may be F32 or BF16. */
+lq8_status lq8_model_create_typed(lq8_ctx* ctx, const lq8_qwen3_config* cfg, const void* const* tensors,
+                                  const int32_t* dtypes, lq8_model** out);
 /* Random init as HF does: Linear/Embedding N(0, std) from a seeded counter
  * generator (quantized on the device), RMSNorm weights 1. */
 lq8_status lq8_model_create_random(lq8_ctx* ctx, const lq8_qwen3_config* cfg, uint64_t seed, float std,

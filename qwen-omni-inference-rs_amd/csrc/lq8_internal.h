@@ -169,6 +169,8 @@ lq8_status launch_repack_aos(hipStream_t s, const uint8_t* aos, size_t n_rows, s
 lq8_status launch_unpack_aos(hipStream_t s, const lq8_weight* w, size_t row0, size_t n_rows, uint8_t* aos);
 lq8_status launch_quantize_weight_f32(hipStream_t s, const float* src, size_t n_rows, size_t row0,
                                       const lq8_weight* w);
+lq8_status launch_quantize_weight_bf16(hipStream_t s, const uint16_t* src, size_t n_rows, size_t row0,
+                                       const lq8_weight* w);
 lq8_status launch_random_weight(hipStream_t s, const lq8_weight* w, size_t row0, size_t n_rows, uint64_t seed,
                                 uint64_t stream, float stddev);
 lq8_status launch_dequant_rows(hipStream_t s, const lq8_weight* w, const uint32_t* d_ids, size_t row0,

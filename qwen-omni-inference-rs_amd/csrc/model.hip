@@ -402,24 +402,47 @@ lq8_status lq8_model_tensor_bytes(const lq8_qwen3_config* c, size_t idx, size_t*
     return LQ8_OK;
 }
 
-lq8_status lq8_model_create(lq8_ctx* ctx, const lq8_qwen3_config* cfg, const void* const* tensors, lq8_model** out) {
+lq8_status lq8_model_create_typed(lq8_ctx* ctx, const lq8_qwen3_config* cfg, const void* const* tensors,
+                                  const int32_t* dtypes, lq8_model** out) {
     if (!registry_has(ctx)) return fail(LQ8_ERR_INVALID_ARG, "invalid context handle");
     if (!tensors || !out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
     lq8_status st = validate(cfg);
     if (st) return st;
-    size_t count = lq8_model_tensor_count(cfg);
-    for (size_t i = 0; i < count; i++)
+    const size_t count = lq8_model_tensor_count(cfg);
+    for (size_t i = 0; i < count; i++) {
         if (!tensors[i]) return fail(LQ8_ERR_INVALID_ARG, "null tensor in table");
+        if (dtypes && dtypes[i] != LQ8_DTYPE_Q8_0 && dtypes[i] != LQ8_DTYPE_F32 && dtypes[i] != LQ8_DTYPE_BF16)
+            return fail(LQ8_ERR_DTYPE_MISMATCH, "unknown tensor dtype");
+    }
     LQ8_HIP(hipSetDevice(ctx->device));
     lq8_model* m = new lq8_model();
     registry_add(m);
     if ((st = build_skeleton(ctx, cfg, m))) { release(m); return st; }
     void* tmp = nullptr;
     size_t tmp_cap = 0;
+    std::vector<float> widened;
     for (size_t i = 0; i < count && !st; i++) {
         TensorRef t = tensor_ref(m, i);
-        if (t.norm) { st = fill_norm(t.norm, t.norm_len, (const float*)tensors[i]); continue; }
-        size_t bytes = t.rows * t.w->nb * BLOCK_BYTES;
+        const int dt = dtypes ? dtypes[i] : (t.norm ? LQ8_DTYPE_F32 : LQ8_DTYPE_Q8_0);
+        if (t.norm) {
+            if (dt == LQ8_DTYPE_Q8_0) { st = fail(LQ8_ERR_DTYPE_MISMATCH, "norm weights must be F32 or BF16"); break; }
+            const float* host = (const float*)tensors[i];
+            if (dt == LQ8_DTYPE_BF16) {  // widen on the host (exact)
+                const uint16_t* b = (const uint16_t*)tensors[i];
+                widened.resize(t.norm_len);
+                for (size_t j = 0; j < t.norm_len; j++) {
+                    const uint32_t u = (uint32_t)b[j] << 16;
+                    std::memcpy(&widened[j], &u, 4);
+                }
+                host = widened.data();
+            }
+            st = fill_norm(t.norm, t.norm_len, host);
+            continue;
+        }
+        const size_t k = t.w->nb * 32;
+        const size_t bytes = dt == LQ8_DTYPE_Q8_0 ? t.rows * t.w->nb * BLOCK_BYTES
+                             : dt == LQ8_DTYPE_F32 ? t.rows * k * sizeof(float)
+                                                   : t.rows * k * sizeof(uint16_t);
         if (bytes > tmp_cap) {
             if (tmp) (void)hipFree(tmp);
             tmp = nullptr;
@@ -429,7 +452,9 @@ lq8_status lq8_model_create(lq8_ctx* ctx, const lq8_qwen3_config* cfg, const voi
         }
         hipError_t e = hipMemcpy(tmp, tensors[i], bytes, hipMemcpyHostToDevice);
         if (e != hipSuccess) { st = hip_fail(e, "tensor upload"); break; }
-        st = launch_repack_aos(ctx->stream, (const uint8_t*)tmp, t.rows, t.row0, t.w);
+        if (dt == LQ8_DTYPE_Q8_0) st = launch_repack_aos(ctx->stream, (const uint8_t*)tmp, t.rows, t.row0, t.w);
+        else if (dt == LQ8_DTYPE_F32) st = launch_quantize_weight_f32(ctx->stream, (const float*)tmp, t.rows, t.row0, t.w);
+        else st = launch_quantize_weight_bf16(ctx->stream, (const uint16_t*)tmp, t.rows, t.row0, t.w);
         if (!st) {
             e = hipStreamSynchronize(ctx->stream);
             if (e != hipSuccess) st = hip_fail(e, "tensor repack");
@@ -439,6 +464,10 @@ lq8_status lq8_model_create(lq8_ctx* ctx, const lq8_qwen3_config* cfg, const voi
     if (st) { release(m); return st; }
     *out = m;
     return LQ8_OK;
+}
+
+lq8_status lq8_model_create(lq8_ctx* ctx, const lq8_qwen3_config* cfg, const void* const* tensors, lq8_model** out) {
+    return lq8_model_create_typed(ctx, cfg, tensors, nullptr, out);
 }
 
 lq8_status lq8_model_create_random(lq8_ctx* ctx, const lq8_qwen3_config* cfg, uint64_t seed, float stddev,

@@ -159,6 +159,34 @@ __global__ void k_dequant_rows(const int8_t* __restrict__ codes, const uint16_t*
     y[idx] = d * (float)q;
 }
 
+// bf16 rows (checkpoint weights) -> the tiled Q8_0 layout; a bf16 value is
+// exactly the f32 with those 16 high bits, so this is the f32 quantizer on
+// the widened values.
+__global__ void k_quantize_weight_bf16(const uint16_t* __restrict__ src, size_t n_rows, size_t row0, size_t nb,
+                                       size_t np, int8_t* __restrict__ codes, uint16_t* __restrict__ scales) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_rows * nb) return;
+    const size_t r = idx / nb, b = idx % nb;
+    float x[32];
+    const uint4* s4 = (const uint4*)(src + r * nb * 32 + b * 32);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 v = s4[i];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
+            x[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+        }
+    }
+    int q[32];
+    QBlock qb;
+    quantize32(x, q, &qb);
+    const size_t row = row0 + r;
+    store_tiled(codes, np, row, b, q);
+    scales[scale_off(row / TILE_ROWS, np, b, (int)(row % TILE_ROWS))] = qb.d16;
+}
+
 // ---- activation quantization (tiled A operand of the GEMM) ----------------
 
 // One wave per (16-row tile, block pair): its 64 lanes write the pair's 1 KiB
@@ -484,6 +512,16 @@ lq8_status launch_quantize_weight_f32(hipStream_t s, const float* src, size_t n_
     const size_t n = n_rows * w->nb;
     if (!n) return LQ8_OK;
     hipLaunchKernelGGL(k_quantize_weight_f32, dim3(grid1(n, WG)), dim3(WG), 0, s, src, n_rows, row0, w->nb, w->np,
+                       w->codes, w->scales);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
+lq8_status launch_quantize_weight_bf16(hipStream_t s, const uint16_t* src, size_t n_rows, size_t row0,
+                                       const lq8_weight* w) {
+    const size_t n = n_rows * w->nb;
+    if (!n) return LQ8_OK;
+    hipLaunchKernelGGL(k_quantize_weight_bf16, dim3(grid1(n, WG)), dim3(WG), 0, s, src, n_rows, row0, w->nb, w->np,
                        w->codes, w->scales);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;

@@ -355,6 +355,34 @@ lq8_status lq8_weight_quantize_upload(lq8_ctx* ctx, const float* src, size_t n_o
     return LQ8_OK;
 }
 
+lq8_status lq8_weight_quantize_upload_bf16(lq8_ctx* ctx, const uint16_t* src, size_t n_out, size_t k_in,
+                                           lq8_weight** out) {
+    CHECK_CTX(ctx);
+    if (!src || !out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (set_device(ctx)) return LQ8_ERR_DEVICE;
+    lq8_weight* w = nullptr;
+    lq8_status st = weight_alloc(ctx, n_out, k_in, &w);
+    if (st) return st;
+    const size_t bytes = n_out * k_in * sizeof(uint16_t);
+    void* tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, bytes);
+    if (e == hipSuccess) e = hipMemcpyAsync(tmp, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) {
+        if (tmp) (void)hipFree(tmp);
+        weight_release(w);
+        return hip_fail(e, "weight upload");
+    }
+    st = launch_quantize_weight_bf16(ctx->stream, (const uint16_t*)tmp, n_out, 0, w);
+    e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(tmp);
+    if (st || e != hipSuccess) {
+        weight_release(w);
+        return st ? st : hip_fail(e, "weight quantize");
+    }
+    *out = w;
+    return LQ8_OK;
+}
+
 lq8_status lq8_weight_random(lq8_ctx* ctx, size_t n_out, size_t k_in, uint64_t seed, uint64_t stream, float stddev,
                              lq8_weight** out) {
     CHECK_CTX(ctx);

@@ -68,6 +68,8 @@ class ModelError(LludaError):
     status = 8
 
 
+DTYPE_Q8_0, DTYPE_F32, DTYPE_BF16 = 0, 1, 2  # lq8_dtype
+
 _ERRORS = {c.status: c for c in (ShapeMismatch, DTypeMismatch, DimOutOfRange, InvalidArgument, NoDevice,
                                   DeviceError, OutOfMemory, ModelError)}
 
@@ -122,6 +124,8 @@ _SIGS = [
     ("lq8_weight_upload", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_void_p)]),
     ("lq8_weight_quantize_upload", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_void_p)]),
+    ("lq8_weight_quantize_upload_bf16", C.c_int,
+     [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_void_p)]),
     ("lq8_weight_random", C.c_int,
      [C.c_void_p, C.c_size_t, C.c_size_t, C.c_uint64, C.c_uint64, C.c_float, C.POINTER(C.c_void_p)]),
     ("lq8_weight_download", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
@@ -141,6 +145,8 @@ _SIGS = [
     ("lq8_model_tensor_count", C.c_size_t, [C.POINTER(Qwen3ConfigC)]),
     ("lq8_model_tensor_bytes", C.c_int, [C.POINTER(Qwen3ConfigC), C.c_size_t, C.POINTER(C.c_size_t)]),
     ("lq8_model_create", C.c_int, [C.c_void_p, C.POINTER(Qwen3ConfigC), C.c_void_p, C.POINTER(C.c_void_p)]),
+    ("lq8_model_create_typed", C.c_int,
+     [C.c_void_p, C.POINTER(Qwen3ConfigC), C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]),
     ("lq8_model_create_random", C.c_int,
      [C.c_void_p, C.POINTER(Qwen3ConfigC), C.c_uint64, C.c_float, C.POINTER(C.c_void_p)]),
     ("lq8_model_export_tensor", C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
@@ -447,6 +453,92 @@ class Qwen3ForCausalLM:
         c = cfg.c()
         _check(lib().lq8_model_create_random(ctx.handle, C.byref(c), seed, std, C.byref(h)))
         return cls(ctx, cfg, h)
+
+    @classmethod
+    def load_typed(cls, ctx: Context, cfg: Qwen3Config, tensors: Sequence[np.ndarray],
+                   dtypes: Sequence[int]) -> "Qwen3ForCausalLM":
+        """Table-order tensors with a dtype each (DTYPE_Q8_0 blocks, DTYPE_F32 or
+        DTYPE_BF16 rows); BF16/F32 matrices are quantized on the device."""
+        if len(tensors) != cfg.tensor_count() or len(dtypes) != cfg.tensor_count():
+            raise ModelError(f"expected {cfg.tensor_count()} tensors and dtypes")
+        keep = [np.ascontiguousarray(t) for t in tensors]
+        arr = (C.c_void_p * len(keep))(*[t.ctypes.data for t in keep])
+        dt = np.ascontiguousarray(dtypes, dtype=np.int32)
+        h = C.c_void_p()
+        c = cfg.c()
+        _check(lib().lq8_model_create_typed(ctx.handle, C.byref(c), arr, _ptr(dt), C.byref(h)))
+        return cls(ctx, cfg, h)
+
+    @classmethod
+    def from_safetensors(cls, ctx: Context, path: str, cfg: Optional[Qwen3Config] = None,
+                         max_positions: Optional[int] = None) -> "Qwen3ForCausalLM":
+        """A HF Qwen3 checkpoint (a directory with config.json and
+        model.safetensors, or the .safetensors file plus cfg): BF16/F32
+        weights quantized to Q8_0 on the device (ModelWeights::from_safetensors,
+        src/loader.rs:68-188, then Qwen3ForCausalLM::load, src/model.rs:273-302)."""
+        from . import checkpoint as ck
+        st_path = path
+        if os.path.isdir(path):
+            st_path = os.path.join(path, "model.safetensors")
+            if cfg is None:
+                cfg = ck.qwen3_config_from_json(os.path.join(path, "config.json"), max_positions)
+        if cfg is None:
+            raise ModelError("a config is needed with a bare .safetensors file")
+        f = ck.SafeTensorsFile(st_path)
+        try:
+            names = ck.hf_tensor_names(cfg)
+            tens, dts, shapes = [], [], []
+            for n in names:
+                t = f.get(n)
+                if t is None:
+                    raise ModelError(f"Missing {n}")
+                tens.append(t.data)
+                dts.append(DTYPE_BF16 if t.dtype == "BF16" else DTYPE_F32)
+                shapes.append(t.shape)
+            ck.check_shapes(cfg, shapes, names)
+            return cls.load_typed(ctx, cfg, tens, dts)
+        finally:
+            f.close()
+
+    @classmethod
+    def from_gguf(cls, ctx: Context, path: str, max_positions: Optional[int] = None) -> "Qwen3ForCausalLM":
+        """A GGUF Q8_0 Qwen3 file (llama.cpp tensor names; F32/BF16 norms,
+        Q8_0 or BF16/F32 matrices)."""
+        from . import checkpoint as ck
+        g = ck.GgufFile(path)
+        try:
+            cfg = ck.qwen3_config_from_gguf(g, max_positions)
+            names = ck.gguf_tensor_names(cfg)
+            tens, dts, shapes = [], [], []
+            for n in names:
+                t = g.tensors.get(n)
+                if t is None:
+                    raise ModelError(f"Missing {n}")
+                if t.ggml_type == ck.GGML_Q8_0:
+                    dts.append(DTYPE_Q8_0)
+                elif t.ggml_type == ck.GGML_F32:
+                    dts.append(DTYPE_F32)
+                elif t.ggml_type == ck.GGML_BF16:
+                    dts.append(DTYPE_BF16)
+                else:
+                    raise DTypeMismatch(f"{n}: ggml type {t.ggml_type} (expected Q8_0, F32 or BF16)")
+                tens.append(t.data)
+                shapes.append(t.shape)
+            ck.check_shapes(cfg, shapes, names)
+            return cls.load_typed(ctx, cfg, tens, dts)
+        finally:
+            g.close()
+
+    def save_gguf(self, path: str) -> None:
+        """The model's weights as a GGUF v3 file (Q8_0 matrices, F32 norms)."""
+        from . import checkpoint as ck
+        names = ck.gguf_tensor_names(self.cfg)
+        tens = []
+        for i, n in enumerate(names):
+            kind, shape = self.cfg.tensor_shape(i)
+            data = self.export_tensor(i)
+            tens.append(ck.GgufTensor(n, ck.GGML_Q8_0 if kind == "q8" else ck.GGML_F32, tuple(shape), data))
+        ck.write_gguf(path, ck.qwen3_gguf_metadata(self.cfg), tens)
 
     def export_tensor(self, idx: int) -> np.ndarray:
         nb = C.c_size_t()
