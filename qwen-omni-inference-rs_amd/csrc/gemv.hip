@@ -396,8 +396,9 @@ __global__ __launch_bounds__(256) void k_gemv_grouped(const GemvProblemDev* __re
 // group of CH pairs) items, unpacks each 16-byte code chunk to floats once
 // and runs the GEMV order of gemv_tiles for every staged vector; the group
 // sums go to LDS and one thread per (vector, row) runs the tree over the
-// groups.
-template <int XS, int EPI, int CH, int VB>
+// groups.  PF (one vector per problem): the wave's first item's weights are
+// issued before the input staging and every item prefetches the next one.
+template <int XS, int EPI, int CH, int VB, bool PF>
 __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
     extern __shared__ float smem[];
     constexpr int NT = EPI == EPI_SWIGLU ? 2 : 1;  // tiles per workgroup
@@ -421,6 +422,26 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
     const int8_t* cbase = a.codes + gt * np * CHUNK_BYTES + lane * 16;
     const uint16_t* sbase = a.scales + gt * 2 * np * 16 + bsel * 16 + r;
     const size_t cstep = (size_t)tstride * np * CHUNK_BYTES, sstep = (size_t)tstride * 2 * np * 16;
+    const int items = NT * G;
+    // weights of item `it` (clamped: every load in bounds and unconditional)
+    u32x4 pv[CH];
+    uint16_t ps[CH];
+#define MV_LOAD_ITEM(it_)                                                                                   \
+    {                                                                                                       \
+        const int itc = min((it_), items - 1), ttc = itc / G, gc = itc - ttc * G;                           \
+        _Pragma("unroll") for (int i = 0; i < CH; i++) {                                                    \
+            const int c = min(gc * CH + i, np - 1);                                                         \
+            pv[i] = __builtin_nontemporal_load((const u32x4*)(cbase + ttc * cstep + (size_t)c * CHUNK_BYTES)); \
+            ps[i] = sbase[ttc * sstep + (size_t)c * 32];                                                    \
+        }                                                                                                   \
+    }
+    if (PF) MV_LOAD_ITEM(wave);
+    // norm weights with the inputs (4 float4 per thread cover k <= 4096)
+    float4 nw[4];
+    if (XS == XS_RMSNORM) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) nw[j] = *(const float4*)(a.norm_w + 4 * min(tid + 256 * j, k4 - 1));
+    }
     for (int v0 = blockIdx.y * VB; v0 < vcnt; v0 += gridDim.y * VB) {
         const int nv = min(VB, vcnt - v0);
         // ---- stage nv vectors (transform per XS) ----
@@ -466,7 +487,13 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
             for (int v = 0; v < nv; v++) {
                 const float inv = red[v];
                 float* xv = xs + v * np * 64;
-                for (int i4 = tid; i4 < k4; i4 += 256) {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (tid + 256 * j < k4) {
+                        float4* p = (float4*)(xv + 4 * (tid + 256 * j));
+                        *p = norm4(*p, nw[j], inv);
+                    }
+                for (int i4 = tid + 1024; i4 < k4; i4 += 256) {
                     float4* p = (float4*)(xv + 4 * i4);
                     *p = norm4(*p, *(const float4*)(a.norm_w + 4 * i4), inv);
                 }
@@ -474,16 +501,17 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
             __syncthreads();
         }
         // ---- items: (tile, group of CH pairs) ----
-        for (int it = wave; it < NT * G; it += 4) {
+        for (int it = wave; it < items; it += 4) {
             const int tt = it / G, g = it - tt * G;
             u32x4 cv[CH];
             uint16_t ds[CH];
+            if (!PF) MV_LOAD_ITEM(it);
 #pragma unroll
             for (int i = 0; i < CH; i++) {
-                const int c = min(g * CH + i, np - 1);
-                cv[i] = __builtin_nontemporal_load((const u32x4*)(cbase + tt * cstep + (size_t)c * CHUNK_BYTES));
-                ds[i] = sbase[tt * sstep + (size_t)c * 32];
+                cv[i] = pv[i];
+                ds[i] = ps[i];
             }
+            if (PF) MV_LOAD_ITEM(it + 4);  // the next item's weights while this one computes
             float wf[CH][16];
 #pragma unroll
             for (int i = 0; i < CH; i++) {
@@ -563,6 +591,7 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
         }
         __syncthreads();
     }
+#undef MV_LOAD_ITEM
 }
 
 // Greedy pick (src/generate.rs:153-174 via src/tensor.rs:2451-2480):
@@ -683,9 +712,11 @@ lq8_status mv_vb(hipStream_t s, const MvArgs& a, dim3 grid, int vb, size_t xs_fl
     const size_t NT = EPI == EPI_SWIGLU ? 2 : 1;
     const size_t smem = ((size_t)vb * xs_floats_per_vec + (size_t)vb * NT * G * 16 + 4) * sizeof(float);
     if (smem > 64 * 1024) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: input staging exceeds 64 KiB of LDS");
-    if (vb == 4) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 4>), grid, dim3(256), smem, s, a);
-    else if (vb == 2) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 2>), grid, dim3(256), smem, s, a);
-    else hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 1>), grid, dim3(256), smem, s, a);
+    // single vector and more items than waves: the pipelined variant
+    if (a.max_vec == 1 && NT * G > 4) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 1, true>), grid, dim3(256), smem, s, a);
+    else if (vb == 4) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 4, false>), grid, dim3(256), smem, s, a);
+    else if (vb == 2) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 2, false>), grid, dim3(256), smem, s, a);
+    else hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 1, false>), grid, dim3(256), smem, s, a);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
@@ -697,7 +728,8 @@ lq8_status mv_ch(hipStream_t s, const MvArgs& a, int max_probs, int vsplit) {
     const int G = (np + ch - 1) / ch;
     const size_t per_vec = (size_t)np * 64;
     // vectors staged per pass: as many as fit in 40 KiB
-    const int vb = per_vec * 4 * sizeof(float) <= 40 * 1024 ? 4 : per_vec * 2 * sizeof(float) <= 40 * 1024 ? 2 : 1;
+    int vb = per_vec * 4 * sizeof(float) <= 40 * 1024 ? 4 : per_vec * 2 * sizeof(float) <= 40 * 1024 ? 2 : 1;
+    if (a.max_vec == 1 && (EPI == EPI_SWIGLU ? 2 : 1) * G > 4) vb = 1;  // the pipelined variant stages one vector
     const int tiles_p = (a.rows + TILE_ROWS - 1) / TILE_ROWS / (EPI == EPI_SWIGLU ? 2 : 1);
     const dim3 grid((unsigned)(tiles_p * max_probs), (unsigned)vsplit);
     if (ch == 1) return mv_vb<XS, EPI, 1>(s, a, grid, vb, per_vec, G);

@@ -143,6 +143,7 @@ struct MvArgs {
     int resid_stride;
     const float* norm_w;    // XS_RMSNORM
     float eps;
+    int max_vec = 0;        // upper bound of vectors per problem (1: single-vector pipelined variant)
 };
 // max_probs: grid rows of problems (n_prob on the device may be smaller);
 // vsplit: workgroups per tile sharing the vectors of a problem.

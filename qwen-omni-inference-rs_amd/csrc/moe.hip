@@ -460,7 +460,7 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
         MvArgs g{};
         g.codes = L.gu->codes; g.scales = L.gu->scales; g.rows = 2 * I; g.k = H; g.prob_tiles = 2 * I / TILE_ROWS;
         g.n_prob = n_act; g.prob_id = act_e; g.vec_begin = vbeg; g.vec_count = vcnt; g.slots = slots;
-        g.x_stride = H; g.x_div = K; g.y = m->gu; g.y_stride = I;
+        g.x_stride = H; g.x_div = K; g.y = m->gu; g.y_stride = I; g.max_vec = T;
         if (T == 1) {
             g.x = m->h2;
             g.norm_w = L.post_norm;
@@ -475,7 +475,7 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
         MvArgs d{};
         d.codes = L.down->codes; d.scales = L.down->scales; d.rows = H; d.k = I; d.prob_tiles = H / TILE_ROWS;
         d.n_prob = n_act; d.prob_id = act_e; d.vec_begin = vbeg; d.vec_count = vcnt; d.slots = slots;
-        d.x = m->gu; d.x_stride = I; d.x_div = 1; d.y = m->eo; d.y_stride = H;
+        d.x = m->gu; d.x_stride = I; d.x_div = 1; d.y = m->eo; d.y_stride = H; d.max_vec = T;
         if ((st = launch_gemv_mv(s, XS_PLAIN, EPI_STORE, d, max_probs, 1))) return st;
         // h = h2 + experts (ascending expert index)
         hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s, m->h2, m->eo,
