@@ -216,10 +216,19 @@ def main():
         b.free()
 
     # known-size copy: calibrates FETCH_SIZE / WRITE_SIZE when profiled
+    # (also the measured stream-copy peak: read + write bytes per second)
     src, dst = lq8.DeviceBuffer(ctx, CALIB_BYTES), lq8.DeviceBuffer(ctx, CALIB_BYTES)
     for _ in range(3):
         lq8._check(lq8.lib().lq8_copy_device(ctx.handle, dst.ptr, src.ptr, CALIB_BYTES))
     ctx.synchronize()
+    copy_gbs = None
+    if not args.only_step:
+        ctx.timer_start()
+        for _ in range(10):
+            lq8._check(lq8.lib().lq8_copy_device(ctx.handle, dst.ptr, src.ptr, CALIB_BYTES))
+        copy_ms = ctx.timer_stop() / 10
+        copy_gbs = 2 * CALIB_BYTES / (copy_ms * 1e-3) / 1e9
+        log(f"device copy 256 MiB: {copy_ms * 1e3:.1f} us, {copy_gbs:.0f} GB/s read+write")
     src.free()
     dst.free()
 
@@ -291,6 +300,7 @@ def main():
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_gemv_grouped", "launch_us": round(ms_step * 1e3, 2),
                      "bytes_per_launch": step_bytes},
+        "copy_peak_gbs": None if copy_gbs is None else round(copy_gbs, 1),
         "one_launch_per_gemv_gbs": None if args.only_step else round(chain_gbs, 1),
         "one_launch_per_gemv_us_per_step": None if args.only_step else round(ms_chain * 1e3, 1),
         "lm_head_gbs": None if args.only_step else round(lm_gbs, 1),

@@ -9,6 +9,7 @@ import pytest
 
 import lq8
 import oracle
+from test_oracle_q8 import MATMUL_KNOWN, exact_operands
 
 pytestmark = pytest.mark.gpu
 
@@ -270,3 +271,18 @@ def test_gemv_repeated_and_graph_calls(ctx):
     for w, dx, dy, ref in cases:
         assert_parity(dy.download(np.float32, w.n_out), ref)
         dx.free(); dy.free(); w.free()
+
+
+@pytest.mark.parametrize("case", MATMUL_KNOWN, ids=[c[0].split()[1] for c in MATMUL_KNOWN])
+def test_matmul_known_answers_gpu(ctx, case):
+    """The reference's matmul known answers through Linear::forward: the
+    W8A8 GEMM for m > 1 rows and the W8A32 GEMV for each row."""
+    _, a, b, want = case
+    x, w = exact_operands(a, b)
+    q = lq8.Q8Weight.quantize(ctx, w)
+    lin = lq8.Linear.new(q)
+    want = np.asarray(want, np.float32)
+    assert np.array_equal(lin.forward(x), want)
+    for r in range(x.shape[0]):
+        assert np.array_equal(lin.forward(x[r:r + 1]), want[r:r + 1])
+    q.free()

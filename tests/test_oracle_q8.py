@@ -186,3 +186,45 @@ def test_gemv_tree_order_is_not_sequential():
             assert oracle.gemv_q8_0(b, 1, k, x)[0] == tree
             return
     pytest.fail("no row separating the two orders found")
+
+
+# Known answers of the reference's matmul tests, made Q8_0-exact: the operands
+# are padded to one 32-value block with a 127 in a column where the other
+# operand is 0, so both block scales are exactly 1 and the codes are the
+# integers themselves.
+MATMUL_KNOWN = [
+    ("src/tensor.rs:3360 test_matmul_2d_basic", [[1, 2], [3, 4]], [[5, 6], [7, 8]], [[19, 22], [43, 50]]),
+    ("src/tensor.rs:3377 test_matmul_2d_non_square", [[1, 2], [3, 4], [5, 6]], [[1, 2, 3, 4], [5, 6, 7, 8]],
+     [[11, 14, 17, 20], [23, 30, 37, 44], [35, 46, 57, 68]]),
+    ("src/tensor.rs:3408 test_matmul_2d_identity", [[1, 2], [3, 4]], [[1, 0], [0, 1]], [[1, 2], [3, 4]]),
+    ("src/tensor.rs:3420 test_matmul_2d_zero_matrix", [[1, 2], [3, 4]], [[0, 0], [0, 0]], [[0, 0], [0, 0]]),
+    ("src/gpu/gemm.rs:530 test_gemm_small", [[1, 2, 3], [4, 5, 6], [7, 8, 9], [10, 11, 12]],
+     [[1, 0, 0, 0, 1], [0, 1, 0, 1, 0], [0, 0, 1, 0, 0]],
+     [[1, 2, 3, 2, 1], [4, 5, 6, 5, 4], [7, 8, 9, 8, 7], [10, 11, 12, 11, 10]]),
+]
+
+
+def exact_operands(a, b):
+    """x [m, 32] and W [n, 32] (W = b^T) for x W^T = a b, Q8_0-exact."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    m, k = a.shape
+    n = b.shape[1]
+    x = np.zeros((m, 32), np.float32)
+    x[:, :k] = a
+    x[:, 31] = 127.0
+    w = np.zeros((n, 32), np.float32)
+    w[:, :k] = b.T
+    w[:, 30] = 127.0
+    return x, w
+
+
+@pytest.mark.parametrize("case", MATMUL_KNOWN, ids=[c[0].split()[1] for c in MATMUL_KNOWN])
+def test_matmul_known_answers(case):
+    _, a, b, want = case
+    x, w = exact_operands(a, b)
+    blocks = oracle.quantize_q8_0(w)
+    n = w.shape[0]
+    want = np.asarray(want, np.float32)
+    assert np.array_equal(oracle.gemm_q8_0(blocks, n, 32, x), want)
+    for r in range(x.shape[0]):
+        assert np.array_equal(oracle.gemv_q8_0(blocks, n, 32, x[r]), want[r])
