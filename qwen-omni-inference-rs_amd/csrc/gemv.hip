@@ -87,13 +87,16 @@ struct Stage {
                 }
             }
         } else {
+            // segment indices clamped to the buffer's capacity, not to the
+            // position's segment count: these loads do not wait for the
+            // position (entries past it are loaded and never used)
             const int H = a.attn_heads;
-            const int C = min(max(a.d_pos ? *a.d_pos : a.pos_base, 0) / ATT_SEG + 1, a.attn_cmax);
+            const int cl = a.attn_cmax - 1;
             const int h = min(tid, H - 1);
             if (wave * 64 < H) {
 #pragma unroll
                 for (int c = 0; c < CU; c++) {
-                    const float* p = x + ((size_t)min(c, C - 1) * H + h) * ATT_PART_STRIDE;
+                    const float* p = x + ((size_t)min(c, cl) * H + h) * ATT_PART_STRIDE;
                     mcs[c] = p[128];
                     lcs[c] = p[129];
                 }
@@ -104,7 +107,7 @@ struct Stage {
                     const int i = min(tid + e * nt, a.k - 1);
 #pragma unroll
                     for (int c = 0; c < CU; c++)
-                        ov[e][c] = x[((size_t)min(c, C - 1) * H + (i >> 7)) * ATT_PART_STRIDE + (i & 127)];
+                        ov[e][c] = x[((size_t)min(c, cl) * H + (i >> 7)) * ATT_PART_STRIDE + (i & 127)];
                 }
             }
         }
@@ -198,15 +201,26 @@ struct Stage {
                             lc[c] = p[129];
                         }
                     }
+                    // the running maxima first, then the exps of every segment
+                    // (independent of each other), then the denominator chain
+                    float mp[CU], mn[CU], ea[CU], eb[CU];
+#pragma unroll
+                    for (int c = 0; c < CU; c++) {
+                        mp[c] = m;
+                        if (c0 + c < C) m = m > mc[c] ? m : mc[c];
+                        mn[c] = m;
+                    }
+#pragma unroll
+                    for (int c = 0; c < CU; c++) {
+                        ea[c] = expf_cr(mp[c] - mn[c]);
+                        eb[c] = expf_cr(mc[c] - mn[c]);
+                    }
 #pragma unroll
                     for (int c = 0; c < CU; c++) {
                         if (c0 + c < C) {
-                            const float mn = m > mc[c] ? m : mc[c];
-                            const float ea = expf_cr(m - mn), eb = expf_cr(mc[c] - mn);
-                            coef[((c0 + c) * H + h) * 2] = ea;
-                            coef[((c0 + c) * H + h) * 2 + 1] = eb;
-                            den = den * ea + eb * lc[c];
-                            m = mn;
+                            coef[((c0 + c) * H + h) * 2] = ea[c];
+                            coef[((c0 + c) * H + h) * 2 + 1] = eb[c];
+                            den = den * ea[c] + eb[c] * lc[c];
                         }
                     }
                 }
@@ -221,15 +235,17 @@ struct Stage {
                         const int h = i >> 7, d = i & 127;
                         float num = 0.0f;
                         for (int c0 = 0; c0 < C; c0 += CU) {
-                            float o[CU];
+                            float o[CU], ca[CU], cb[CU];
+#pragma unroll
+                            for (int c = 0; c < CU; c++) {
+                                const int cc = min(c0 + c, C - 1);
+                                o[c] = (c0 == 0 && e0 == 0) ? ov[e][c] : x[((size_t)cc * H + h) * ATT_PART_STRIDE + d];
+                                ca[c] = coef[(cc * H + h) * 2];  // coefficients read before the chain
+                                cb[c] = coef[(cc * H + h) * 2 + 1];
+                            }
 #pragma unroll
                             for (int c = 0; c < CU; c++)
-                                o[c] = (c0 == 0 && e0 == 0) ? ov[e][c]
-                                                            : x[((size_t)min(c0 + c, C - 1) * H + h) * ATT_PART_STRIDE + d];
-#pragma unroll
-                            for (int c = 0; c < CU; c++)
-                                if (c0 + c < C)
-                                    num = num * coef[((c0 + c) * H + h) * 2] + coef[((c0 + c) * H + h) * 2 + 1] * o[c];
+                                if (c0 + c < C) num = num * ca[c] + cb[c] * o[c];
                         }
                         xs[i] = __fdiv_rn(num, dens[h]);
                     }
