@@ -158,6 +158,13 @@ lq8_status launch_argmax_final(hipStream_t s, const float* arg_val, const int* a
 // Activation rows x[m, k] -> tiled codes (as a weight, 2 * ceil(m/32) tiles) + f16
 // scales in the GEMM's operand layout (act_scale_bytes).
 lq8_status launch_quantize_act(hipStream_t s, const float* x, int m, int k, int8_t* codes, uint32_t* scales);
+// The same operand from RmsNorm(x) rows (the values launch_rms_norm_rows gives)
+// and from silu(gate) * up of [gate | up] rows (the values launch_silu_mul gives).
+bool rms_quantize_supported(int dim);
+lq8_status launch_rms_quantize_act(hipStream_t s, const float* x, const float* w, int m, int dim, float eps,
+                                   int8_t* codes, uint32_t* scales);
+lq8_status launch_silu_quantize_act(hipStream_t s, const float* gu, int m, int inter, int8_t* codes,
+                                    uint32_t* scales);
 size_t act_code_bytes(int m, int k);
 size_t act_scale_bytes(int m, int k);
 // AoS quantization (public device quantizer).

@@ -63,6 +63,13 @@ __device__ __forceinline__ int sat_i8(float v) {
     return (int)v;
 }
 
+// SUM64 fold of one 64-lane wave's partials: distances 32, 16, 8, 4, 2, 1.
+__device__ __forceinline__ float wave_sum64(float a) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) a = a + __shfl_xor(a, d, 64);
+    return a;
+}
+
 // Q8_0 block quantizer (GGML quantize_row_q8_0 / candle BlockQ8_0::from_float):
 // amax ignores NaN, d = amax/127, id = d ? 1/d : 0, q = round_half_away(x*id).
 struct QBlock {

@@ -11,7 +11,8 @@
 //   RmsNorm + gate|up GEMV
 //   silu(gate) * up staged into the down GEMV, + residual
 // then RmsNorm + lm_head GEMV with per-tile argmax and one argmax kernel.
-// Prefill (n > 1 positions) quantizes activations and uses the MFMA GEMM.
+// Prefill (n > 1 positions) runs the MFMA GEMM on quantized activations; the
+// RmsNorms and silu(gate) * up are fused into the activation quantizer.
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -54,7 +55,7 @@ struct lq8_model {
     // prefill buffers, capacity in rows
     size_t pf_cap = 0;
     float *P_h = nullptr, *P_x = nullptr, *P_qkv = nullptr, *P_qr = nullptr, *P_attn = nullptr, *P_gu = nullptr,
-          *P_act = nullptr, *P_xs = nullptr;
+          *P_xs = nullptr;
     int8_t* P_xq = nullptr;
     hipGraphExec_t graph = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
@@ -102,7 +103,7 @@ void release(lq8_model* m) {
     F(m->cos_t); F(m->sin_t); F(m->kc); F(m->vc);
     F(m->h); F(m->h2); F(m->qkv); F(m->gu); F(m->apart); F(m->logits); F(m->arg_val); F(m->arg_idx);
     F(m->d_ids); F(m->d_pos); F(m->d_step); F(m->d_tok); F(m->d_tokens);
-    F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_act); F(m->P_xs); F(m->P_xq);
+    F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_xs); F(m->P_xq);
     delete m;
 }
 
@@ -216,7 +217,7 @@ lq8_status ensure_prefill(lq8_model* m, size_t n) {
     if (n <= m->pf_cap) return LQ8_OK;
     LQ8_HIP(hipStreamSynchronize(m->ctx->stream));
     auto F = [](float*& p) { if (p) (void)hipFree(p); p = nullptr; };
-    F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_act); F(m->P_xs);
+    F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_xs);
     if (m->P_xq) (void)hipFree(m->P_xq);
     m->P_xq = nullptr;
     m->pf_cap = 0;
@@ -225,7 +226,7 @@ lq8_status ensure_prefill(lq8_model* m, size_t n) {
     lq8_status st;
     if ((st = dalloc(&m->P_h, n * Hd)) || (st = dalloc(&m->P_x, n * Hd)) || (st = dalloc(&m->P_qkv, n * m->QKV)) ||
         (st = dalloc(&m->P_qr, n * m->QD)) || (st = dalloc(&m->P_attn, n * m->QD)) ||
-        (st = dalloc(&m->P_gu, n * 2 * I)) || (st = dalloc(&m->P_act, n * I)) ||
+        (st = dalloc(&m->P_gu, n * 2 * I)) ||
         (st = dalloc(&m->P_xs, act_scale_bytes((int)n, kmax) / sizeof(float))) ||
         (st = dalloc(&m->P_xq, act_code_bytes((int)n, kmax))))
         return st;
@@ -308,6 +309,21 @@ lq8_status quant_gemm(lq8_model* m, const float* x, int n, const lq8_weight* w, 
     return launch_gemm(s, m->P_xq, xs, n, w, y, resid);
 }
 
+// GEMM input RmsNorm(h) rows: the norm is fused into the activation quantizer
+// (the same operand as rms_norm_rows followed by quantize_act) where the
+// hidden size allows it.
+lq8_status norm_quant_gemm(lq8_model* m, const float* h, const float* norm_w, int n, const lq8_weight* w, float* y) {
+    hipStream_t s = m->ctx->stream;
+    const int Hd = (int)m->c.hidden_size;
+    if (!rms_quantize_supported(Hd)) {
+        lq8_status st = launch_rms_norm_rows(s, h, norm_w, n, Hd, m->c.rms_norm_eps, m->P_x);
+        return st ? st : quant_gemm(m, m->P_x, n, w, y, nullptr);
+    }
+    uint32_t* xs = reinterpret_cast<uint32_t*>(m->P_xs);
+    lq8_status st = launch_rms_quantize_act(s, h, norm_w, n, Hd, m->c.rms_norm_eps, m->P_xq, xs);
+    return st ? st : launch_gemm(s, m->P_xq, xs, n, w, y, nullptr);
+}
+
 // n positions starting at pos_base (src/model.rs:170-195), then the last
 // position's logits and per-tile argmax partials.
 lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base, float* trace = nullptr) {
@@ -321,8 +337,7 @@ lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base, float* trace = nul
     if ((st = trace_copy(m, trace, m->P_h, (size_t)n * Hd))) return st;
     for (size_t l = 0; l < m->layers.size(); l++) {
         Layer& L = m->layers[l];
-        if ((st = launch_rms_norm_rows(s, m->P_h, L.in_norm, n, Hd, c.rms_norm_eps, m->P_x))) return st;
-        if ((st = quant_gemm(m, m->P_x, n, L.qkv, m->P_qkv, nullptr))) return st;
+        if ((st = norm_quant_gemm(m, m->P_h, L.in_norm, n, L.qkv, m->P_qkv))) return st;
         QkRopeLaunch qr{m->P_qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->P_qr, m->kc + l * layer_kv,
                         m->vc + l * layer_kv, nullptr, pos_base, n, (int)c.num_heads, (int)c.num_kv_heads,
                         (int)c.head_dim, (int)c.max_positions, c.rms_norm_eps};
@@ -331,10 +346,11 @@ lq8_status enqueue_prefill(lq8_model* m, int n, int pos_base, float* trace = nul
                           (int)c.num_heads, (int)c.num_kv_heads, (int)c.max_positions, scale};
         if ((st = launch_attention_rows(s, at))) return st;
         if ((st = quant_gemm(m, m->P_attn, n, L.o, m->P_h, m->P_h))) return st;
-        if ((st = launch_rms_norm_rows(s, m->P_h, L.post_norm, n, Hd, c.rms_norm_eps, m->P_x))) return st;
-        if ((st = quant_gemm(m, m->P_x, n, L.gu, m->P_gu, nullptr))) return st;
-        if ((st = launch_silu_mul(s, m->P_gu, n, I, m->P_act))) return st;
-        if ((st = quant_gemm(m, m->P_act, n, L.down, m->P_h, m->P_h))) return st;
+        if ((st = norm_quant_gemm(m, m->P_h, L.post_norm, n, L.gu, m->P_gu))) return st;
+        if ((st = launch_silu_quantize_act(s, m->P_gu, n, I, m->P_xq, reinterpret_cast<uint32_t*>(m->P_xs))))
+            return st;
+        if ((st = launch_gemm(s, m->P_xq, reinterpret_cast<const uint32_t*>(m->P_xs), n, L.down, m->P_h, m->P_h)))
+            return st;
         if (trace && (st = trace_copy(m, trace + (l + 1) * (size_t)n * Hd, m->P_h, (size_t)n * Hd))) return st;
     }
     // final norm + lm_head on the last position only (src/model.rs:357-371)

@@ -25,12 +25,6 @@ constexpr int KPAD = 129;  // LDS row stride of staged keys (bank-conflict free 
 __host__ __device__ inline int seg_ks_off(int G) { return (G * 128 + 256 + G * SEG + 2 * G + 3) & ~3; }
 __host__ __device__ inline int rows_ks_off(int G) { return (G * 128 + G * SEG + 6 * G + 3) & ~3; }
 
-__device__ __forceinline__ float wave_sum64(float a) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) a = a + __shfl_xor(a, d, 64);
-    return a;
-}
-
 __device__ __forceinline__ float wave_max64(float a) {
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
@@ -329,18 +323,44 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_rows(AttnRowsLaunch a) {
 }
 
 // RmsNorm of each row (src/rms_norm.rs:143-176), one wave per row.
+template <int U>
 __global__ __launch_bounds__(64) void k_rms_norm_rows(const float* __restrict__ x, const float* __restrict__ w, int dim,
                                                       float eps, float* __restrict__ y) {
-    constexpr int U = 16;  // loads in flight per lane
+    // U <= 32: the row and the norm weights stay in registers (loaded together);
+    // U == 0: longer rows, two passes of 16 loads in flight per lane.
     const int r = blockIdx.x, lane = threadIdx.x;
     const float* xr = x + (size_t)r * dim;
+    float* yr = y + (size_t)r * dim;
+    if (U > 0) {
+        constexpr int UU = U > 0 ? U : 1;
+        float v[UU], wn[UU];
+#pragma unroll
+        for (int u = 0; u < UU; u++) {
+            v[u] = xr[min(lane + 64 * u, dim - 1)];
+            wn[u] = w[min(lane + 64 * u, dim - 1)];
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < UU; u++)
+            if (lane + 64 * u < dim) {
+                const float b = bf16_round(v[u]);
+                acc = acc + b * b;
+            }
+        acc = wave_sum64(acc);
+        const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)dim) + eps));
+#pragma unroll
+        for (int u = 0; u < UU; u++)
+            if (lane + 64 * u < dim) yr[lane + 64 * u] = bf16_round((bf16_round(v[u]) * inv) * bf16_round(wn[u]));
+        return;
+    }
+    constexpr int L = 16;  // loads in flight per lane
     float acc = 0.0f;
-    for (int i0 = lane; i0 < dim; i0 += 64 * U) {
-        float v[U];
+    for (int i0 = lane; i0 < dim; i0 += 64 * L) {
+        float v[L];
 #pragma unroll
-        for (int u = 0; u < U; u++) v[u] = xr[min(i0 + 64 * u, dim - 1)];
+        for (int u = 0; u < L; u++) v[u] = xr[min(i0 + 64 * u, dim - 1)];
 #pragma unroll
-        for (int u = 0; u < U; u++)
+        for (int u = 0; u < L; u++)
             if (i0 + 64 * u < dim) {
                 const float b = bf16_round(v[u]);
                 acc = acc + b * b;
@@ -349,17 +369,16 @@ __global__ __launch_bounds__(64) void k_rms_norm_rows(const float* __restrict__ 
     acc = wave_sum64(acc);
     const float mean = __fdiv_rn(acc, (float)dim);
     const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(mean + eps));
-    float* yr = y + (size_t)r * dim;
-    for (int i0 = lane; i0 < dim; i0 += 64 * U) {
-        float v[U], wv[U];
+    for (int i0 = lane; i0 < dim; i0 += 64 * L) {
+        float v[L], wv[L];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
+        for (int u = 0; u < L; u++) {
             const int i = min(i0 + 64 * u, dim - 1);
             v[u] = xr[i];
             wv[u] = w[i];
         }
 #pragma unroll
-        for (int u = 0; u < U; u++)
+        for (int u = 0; u < L; u++)
             if (i0 + 64 * u < dim) yr[i0 + 64 * u] = bf16_round((bf16_round(v[u]) * inv) * bf16_round(wv[u]));
     }
 }
@@ -434,7 +453,13 @@ lq8_status launch_attention_rows(hipStream_t s, const AttnRowsLaunch& a) {
 }
 
 lq8_status launch_rms_norm_rows(hipStream_t s, const float* x, const float* w, int rows, int dim, float eps, float* y) {
-    hipLaunchKernelGGL(k_rms_norm_rows, dim3((unsigned)rows), dim3(64), 0, s, x, w, dim, eps, y);
+    const dim3 grid((unsigned)rows);
+    const int u = (dim + 63) / 64;
+    if (u <= 4) hipLaunchKernelGGL(k_rms_norm_rows<4>, grid, dim3(64), 0, s, x, w, dim, eps, y);
+    else if (u <= 8) hipLaunchKernelGGL(k_rms_norm_rows<8>, grid, dim3(64), 0, s, x, w, dim, eps, y);
+    else if (u <= 16) hipLaunchKernelGGL(k_rms_norm_rows<16>, grid, dim3(64), 0, s, x, w, dim, eps, y);
+    else if (u <= 32) hipLaunchKernelGGL(k_rms_norm_rows<32>, grid, dim3(64), 0, s, x, w, dim, eps, y);
+    else hipLaunchKernelGGL(k_rms_norm_rows<0>, grid, dim3(64), 0, s, x, w, dim, eps, y);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

@@ -198,6 +198,43 @@ __global__ void k_quantize_weight_bf16(const uint16_t* __restrict__ src, size_t 
 // past nb get zero codes and a zero scale.  Scales go to the GEMM's f16
 // operand layout: u32 words (f16 bits, high half zero) in
 // [m/32][nbp/4][64 lanes][4 blocks], lanes 0..31 = rows, lanes 32..63 = 0.
+// amax of 16 values from 0, NaN ignored (as `if (v > amax) amax = v`):
+// fmaxf returns the non-NaN operand.
+__device__ __forceinline__ float half_amax(const float* v) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
+    return amax;
+}
+
+// Store half hf of block b of activation row `row`: the 16 codes of v under the
+// block's amax (both halves combined) into the tiled code layout (only where a
+// code slot exists, b < 2 np; zero codes past nb), and into the scale layout
+// [m/32][nbp/4][64 lanes][4 blocks] the f16 scale (half 0; 0 past nb) or the
+// zero of the upper 32 lanes (half 1).
+__device__ __forceinline__ void put_act_half(int8_t* __restrict__ codes, uint32_t* __restrict__ xs, int np, int nbp4,
+                                             int nb, int row, int b, int hf, const float* v, float amax) {
+    uint32_t d16 = 0;
+    if (b < 2 * np) {
+        uint4 c = make_uint4(0, 0, 0, 0);
+        if (b < nb) {
+            const QBlock qb = block_scale(amax);
+            const float id = block_inv(qb.d);
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                w[i] = (uint32_t)(quant_code(v[4 * i], id) & 0xFF) |
+                       ((uint32_t)(quant_code(v[4 * i + 1], id) & 0xFF) << 8) |
+                       ((uint32_t)(quant_code(v[4 * i + 2], id) & 0xFF) << 16) |
+                       ((uint32_t)(quant_code(v[4 * i + 3], id) & 0xFF) << 24);
+            c = make_uint4(w[0], w[1], w[2], w[3]);
+            d16 = qb.d16;
+        }
+        *(uint4*)(codes + code_off(row / TILE_ROWS, np, b, hf, row % TILE_ROWS)) = c;
+    }
+    xs[((size_t)((row >> 5) * nbp4 + (b >> 2)) * 64 + hf * 32 + (row & 31)) * 4 + (b & 3)] = hf ? 0u : d16;
+}
+
 __global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ x, int m, int k, int waves, int np8,
                                                       int8_t* __restrict__ codes, uint32_t* __restrict__ xs) {
     const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -206,33 +243,125 @@ __global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ 
     const int tile = gw / np8, p = gw - tile * np8;
     const int nb = k >> 5, np = (nb + 1) >> 1;
     const int r = lane & 15, part = lane >> 4, b = 2 * p + (part >> 1), hf = part & 1;
-    uint32_t d16 = 0;
+    float v[16] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    float amax = 0.0f;
     if (p < np) {
         const int row = min(tile * TILE_ROWS + r, m - 1);
         const float4* src = (const float4*)(x + (size_t)row * k + min(b, nb - 1) * 32 + hf * 16);
-        const float4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
-        const float v[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
-                             v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
-        // amax from 0, NaN ignored (as `if (v > amax) amax = v`): fmaxf returns the non-NaN operand
-        float amax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
+        for (int i = 0; i < 4; i++) {
+            const float4 t = src[i];
+            v[4 * i] = t.x;
+            v[4 * i + 1] = t.y;
+            v[4 * i + 2] = t.z;
+            v[4 * i + 3] = t.w;
+        }
+        amax = half_amax(v);
         amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-        const QBlock qb = block_scale(amax);
-        const float id = block_inv(qb.d);
-        uint32_t w[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            w[i] = (uint32_t)(quant_code(v[4 * i], id) & 0xFF) | ((uint32_t)(quant_code(v[4 * i + 1], id) & 0xFF) << 8) |
-                   ((uint32_t)(quant_code(v[4 * i + 2], id) & 0xFF) << 16) |
-                   ((uint32_t)(quant_code(v[4 * i + 3], id) & 0xFF) << 24);
-        const bool real = b < nb;
-        *(uint4*)(codes + ((size_t)(tile * np + p) * 64 + lane) * 16) =
-            real ? make_uint4(w[0], w[1], w[2], w[3]) : make_uint4(0, 0, 0, 0);
-        d16 = real ? qb.d16 : 0u;
     }
-    const int slot = hf * 32 + (tile & 1) * TILE_ROWS + r;
-    xs[((size_t)((tile >> 1) * (np8 >> 1) + (b >> 2)) * 64 + slot) * 4 + (b & 3)] = hf ? 0u : d16;
+    put_act_half(codes, xs, np, np8 >> 1, nb, tile * TILE_ROWS + r, b, hf, v, amax);
+}
+
+// RMSNorm of rows x[m, dim] quantized straight into the GEMM operand layout:
+// the same values as k_quantize_act applied to the output of
+// k_rms_norm_rows (SUM64 of bf16(x)^2, mean = sum / dim,
+// inv = 1 / sqrt(mean + eps), out = bf16((bf16(x) * inv) * bf16(w)),
+// src/rms_norm.rs:143-176).  One wave per padded row (rows past m repeat row
+// m - 1); lane l holds elements l, l + 64, ... in registers for the sum,
+// the normed row is staged in LDS, then lane l quantizes half-blocks l,
+// l + 64, ... (16 consecutive values each; the two halves of a block are
+// neighbouring lanes).  dim <= 64 U.
+template <int U>
+__global__ __launch_bounds__(256) void k_rms_quantize_act(const float* __restrict__ x, const float* __restrict__ w, int m,
+                                                          int dim, float eps, int np, int nbp,
+                                                          int8_t* __restrict__ codes, uint32_t* __restrict__ xs) {
+    __shared__ __attribute__((aligned(16))) float rowbuf[4][64 * U];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + wv;  // the grid covers the padded rows exactly
+    const float* xr = x + (size_t)min(row, m - 1) * dim;
+    float v[U], wn[U];  // the norm weights are loaded with the row, off the sum's critical path
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        v[u] = xr[min(lane + 64 * u, dim - 1)];
+        wn[u] = w[min(lane + 64 * u, dim - 1)];
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        if (lane + 64 * u < dim) {
+            const float b = bf16_round(v[u]);
+            acc = acc + b * b;
+        }
+    acc = wave_sum64(acc);
+    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)dim) + eps));
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int i = lane + 64 * u;
+        if (i < dim) rowbuf[wv][i] = bf16_round((bf16_round(v[u]) * inv) * bf16_round(wn[u]));
+    }
+    __syncthreads();
+    const int nb = dim >> 5, nhb = 2 * nbp;
+    for (int hb0 = 0; hb0 < nhb; hb0 += 64) {
+        const int hb = hb0 + lane, b = hb >> 1, hf = hb & 1;
+        float q[16] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        if (b < nb) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 t = *(const float4*)&rowbuf[wv][b * 32 + hf * 16 + 4 * i];
+                q[4 * i] = t.x;
+                q[4 * i + 1] = t.y;
+                q[4 * i + 2] = t.z;
+                q[4 * i + 3] = t.w;
+            }
+        }
+        float amax = half_amax(q);
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        if (hb < nhb) put_act_half(codes, xs, np, nbp >> 2, nb, row, b, hf, q, amax);
+    }
+}
+
+// act = silu(gate) * up of rows gu[m, 2 inter] (as k_silu_mul: silu(g) =
+// g / (1 + exp(-g)), src/tensor.rs:1978, mlp.rs:151-164) quantized straight
+// into the GEMM operand layout.  One wave per (padded row, group of 8
+// blocks): lanes 8j .. 8j + 7 hold block j of the group, 4 consecutive values
+// each (lanes 8j .. 8j + 3 half 0, 8j + 4 .. 8j + 7 half 1); the block amax
+// folds over those 8 lanes (max is exact in any order).  Rows past m repeat
+// row m - 1.
+__global__ __launch_bounds__(256) void k_silu_quantize_act(const float* __restrict__ gu, int m, int inter, int waves,
+                                                           int groups, int np, int8_t* __restrict__ codes,
+                                                           uint32_t* __restrict__ xs) {
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= waves) return;
+    const int lane = threadIdx.x & 63;
+    const int row = gw / groups, g = gw - row * groups;
+    const int b = g * GEMM_GROUP + (lane >> 3), hf = (lane >> 2) & 1, sub = lane & 3, nb = inter >> 5;
+    float q[4] = {0, 0, 0, 0};
+    if (b < nb) {
+        const float* gp = gu + (size_t)min(row, m - 1) * 2 * inter + b * 32 + hf * 16 + sub * 4;
+        const float4 gv = *(const float4*)gp, uv = *(const float4*)(gp + inter);
+        q[0] = __fdiv_rn(gv.x, 1.0f + expf_cr(-gv.x)) * uv.x;
+        q[1] = __fdiv_rn(gv.y, 1.0f + expf_cr(-gv.y)) * uv.y;
+        q[2] = __fdiv_rn(gv.z, 1.0f + expf_cr(-gv.z)) * uv.z;
+        q[3] = __fdiv_rn(gv.w, 1.0f + expf_cr(-gv.w)) * uv.w;
+    }
+    float amax = fmaxf(fmaxf(fmaxf(0.0f, fabsf(q[0])), fabsf(q[1])), fmaxf(fabsf(q[2]), fabsf(q[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    uint32_t d16 = 0;
+    if (b < 2 * np) {
+        uint32_t c = 0;
+        if (b < nb) {
+            const QBlock qb = block_scale(amax);
+            const float id = block_inv(qb.d);
+            c = (uint32_t)(quant_code(q[0], id) & 0xFF) | ((uint32_t)(quant_code(q[1], id) & 0xFF) << 8) |
+                ((uint32_t)(quant_code(q[2], id) & 0xFF) << 16) | ((uint32_t)(quant_code(q[3], id) & 0xFF) << 24);
+            d16 = qb.d16;
+        }
+        *(uint32_t*)(codes + code_off(row / TILE_ROWS, np, b, hf, row % TILE_ROWS) + 4 * sub) = c;
+    }
+    if (sub == 0)
+        xs[((size_t)((row >> 5) * 2 * groups + (b >> 2)) * 64 + hf * 32 + (row & 31)) * 4 + (b & 3)] = hf ? 0u : d16;
 }
 
 // ---- GEMM (W8A8, v_mfma_i32_32x32x32_i8) -------------------------------------
@@ -432,6 +561,42 @@ lq8_status launch_quantize_act(hipStream_t s, const float* x, int m, int k, int8
     if (!waves) return LQ8_OK;
     hipLaunchKernelGGL(k_quantize_act, dim3(grid1(waves, 4)), dim3(256), 0, s, x, m, k, (int)waves, 4 * groups,
                        codes, scales);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
+bool rms_quantize_supported(int dim) { return dim > 0 && dim % 32 == 0 && dim <= 64 * 32; }
+
+lq8_status launch_rms_quantize_act(hipStream_t s, const float* x, const float* w, int m, int dim, float eps,
+                                   int8_t* codes, uint32_t* scales) {
+    if (!rms_quantize_supported(dim)) return fail(LQ8_ERR_SHAPE_MISMATCH, "rms_quantize_act: unsupported dim");
+    if (m <= 0) return LQ8_OK;
+    const int nb = dim / 32, np = (nb + 1) / 2, nbp = GEMM_GROUP * ((nb + GEMM_GROUP - 1) / GEMM_GROUP);
+    const unsigned grid = (unsigned)((m + 31) / 32 * 8);  // 4 padded rows per workgroup
+    const int u = (dim + 63) / 64;
+    if (u <= 4)
+        hipLaunchKernelGGL(k_rms_quantize_act<4>, dim3(grid), dim3(256), 0, s, x, w, m, dim, eps, np, nbp, codes, scales);
+    else if (u <= 8)
+        hipLaunchKernelGGL(k_rms_quantize_act<8>, dim3(grid), dim3(256), 0, s, x, w, m, dim, eps, np, nbp, codes, scales);
+    else if (u <= 16)
+        hipLaunchKernelGGL(k_rms_quantize_act<16>, dim3(grid), dim3(256), 0, s, x, w, m, dim, eps, np, nbp, codes,
+                           scales);
+    else
+        hipLaunchKernelGGL(k_rms_quantize_act<32>, dim3(grid), dim3(256), 0, s, x, w, m, dim, eps, np, nbp, codes,
+                           scales);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
+lq8_status launch_silu_quantize_act(hipStream_t s, const float* gu, int m, int inter, int8_t* codes,
+                                    uint32_t* scales) {
+    if (inter <= 0 || inter % 32) return fail(LQ8_ERR_SHAPE_MISMATCH, "silu_quantize_act: unsupported width");
+    if (m <= 0) return LQ8_OK;
+    const int nb = inter / 32, np = (nb + 1) / 2, groups = (nb + GEMM_GROUP - 1) / GEMM_GROUP;
+    const size_t waves = (size_t)((m + 31) / 32 * 32) * groups;
+    if (waves > (size_t)INT32_MAX) return fail(LQ8_ERR_SHAPE_MISMATCH, "silu_quantize_act: too many rows");
+    hipLaunchKernelGGL(k_silu_quantize_act, dim3(grid1(waves, 4)), dim3(256), 0, s, gu, m, inter, (int)waves, groups,
+                       np, codes, scales);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
