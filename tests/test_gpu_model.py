@@ -135,6 +135,24 @@ def test_wide_gqa_and_odd_block_counts(ctx):
     ref.close()
 
 
+@pytest.mark.parametrize("hidden", [1568, 2112])
+def test_wide_hidden_prefill_paths(ctx, hidden):
+    """Prefill normalizes and quantizes GEMM inputs in one kernel for hidden
+    sizes up to 2048 (1568: 49 blocks, odd, the widest register variant) and
+    falls back to RmsNorm rows + quantize above it (2112); intermediate 800
+    (25 blocks) takes silu(gate) * up straight into the quantizer.  Prefill
+    and decode logits bit-exact either way."""
+    cfg = lq8.Qwen3Config(vocab_size=640, hidden_size=hidden, intermediate_size=800, num_hidden_layers=2,
+                          num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=96)
+    model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=hidden)
+    ref = oracle.Model(cfg, model.export_all())
+    prompt = np.random.default_rng(hidden).integers(0, cfg.vocab_size, 37).astype(np.uint32)
+    assert same_bits(model.forward(prompt, 0), ref.forward(prompt, 0))
+    assert same_bits(model.forward([5], 37), ref.forward([5], 37))
+    model.free()
+    ref.close()
+
+
 def test_qwen3_0_6b_greedy_128_plus_128(ctx):
     """Qwen3-0.6B random-init Q8_0, 128 uniform-random prompt ids, 128 greedy
     tokens: identical to the oracle; the prefill logits are bit-identical."""
