@@ -254,60 +254,113 @@ __global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ 
     out[(size_t)b * H * 128 + h * 128 + d] = __fdiv_rn(num, den);
 }
 
-// Attention over n query rows with a filled cache (prefill), one workgroup
-// per (kv head, row); the segments run in order with the running update.
+// Attention over n query rows with a filled cache (prefill): one workgroup
+// per (kv head, R consecutive rows), R * G <= 16.  The segments run in order
+// with the running update; each K/V segment is staged once for the R rows,
+// and a row whose positions end before a segment skips it (its arithmetic is
+// the single-row sequence exactly).
+template <int R>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_rows(AttnRowsLaunch a) {
     extern __shared__ float sm[];
-    const int kvh = blockIdx.x, i = blockIdx.y;
-    const int tid = threadIdx.x;
-    const int G = a.num_heads / a.num_kv_heads;
+    const int kvh = blockIdx.x, i0 = blockIdx.y * R;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = a.num_heads / a.num_kv_heads, RG = R * G;
     const int QD = a.num_heads * 128;
-    const int pos = a.pos_base + i;
-    const int L = pos + 1;
+    const int nr = min(R, a.n - i0);
+    const int Lmax = a.pos_base + i0 + nr;  // positions of the workgroup's last row
     const float* Kc = a.k_cache + (size_t)kvh * a.max_pos * 128;
     const float* Vc = a.v_cache + (size_t)kvh * a.max_pos * 128;
-    float* qs = sm;                      // [G][128]
-    float* sc = qs + G * 128;            // [G][64]
-    float* mlc = sc + G * SEG;           // [G][2]
-    float* run = mlc + 2 * G;            // [G][4]: m, den, a, b
-    float* ks = sm + rows_ks_off(G);     // [64][KPAD], later vs [64][128]
-    for (int e = tid; e < G * 128; e += ATT_THREADS) qs[e] = a.q_rows[(size_t)i * QD + kvh * G * 128 + e];
-    for (int h = tid; h < G; h += ATT_THREADS) {
+    float* qs = sm;                      // [R][G][128]
+    float* sc = qs + RG * 128;           // [R][G][64]
+    float* mlc = sc + RG * SEG;          // [R][G][2]
+    float* run = mlc + 2 * RG;           // [R][G][4]: m, den, a, b
+    float* ks = sm + rows_ks_off(RG);    // [64][KPAD], later vs [64][128]
+    for (int e = tid; e < RG * 128; e += ATT_THREADS) {
+        const int rr = e / (G * 128), w = e - rr * G * 128;
+        qs[e] = a.q_rows[(size_t)(i0 + min(rr, nr - 1)) * QD + kvh * G * 128 + w];
+    }
+    for (int h = tid; h < RG; h += ATT_THREADS) {
         run[4 * h] = -__builtin_huge_valf();
         run[4 * h + 1] = 0.0f;
     }
-    // thread t < G * 128 (looping) keeps num for (h, d) = (t / 128, t % 128)
+    // thread t < R * G * 128 (looping) keeps num for (row, head, d) = (t / (G * 128), (t / 128) % G, t % 128)
     constexpr int MAXR = 16 * 128 / ATT_THREADS;
     float num[MAXR];
 #pragma unroll
     for (int r = 0; r < MAXR; r++) num[r] = 0.0f;
     float4 kreg[ATT_F4], vreg[ATT_F4];
-    for (int js = 0; js < L; js += SEG) {
-        const int nj = min(SEG, L - js);
-        seg_load(Kc, Vc, js, nj, kreg, vreg);
+    for (int js = 0; js < Lmax; js += SEG) {
+        const int njmax = min(SEG, Lmax - js);
+        seg_load(Kc, Vc, js, njmax, kreg, vreg);
         __syncthreads();
-        seg_scores(kreg, nj, -1, nullptr, qs, G, a.scale, ks, sc, mlc);
-        __syncthreads();
-        for (int h = tid; h < G; h += ATT_THREADS) {
-            const float m = run[4 * h], mc = mlc[2 * h];
-            const float mn = m > mc ? m : mc;
-            const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
-            run[4 * h] = mn;
-            run[4 * h + 1] = run[4 * h + 1] * ea + eb * mlc[2 * h + 1];
-            run[4 * h + 2] = ea;
-            run[4 * h + 3] = eb;
+#pragma unroll
+        for (int u = 0; u < ATT_F4; u++) {
+            const int f = tid + u * ATT_THREADS;
+            const int j = f >> 5, c4 = f & 31;
+            if (j < njmax) {
+                const float4 v = kreg[u];
+                float* dst = ks + j * KPAD + c4 * 4;
+                dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+            }
         }
-        seg_stage_v(vreg, nj, -1, nullptr, ks);
+        __syncthreads();
+        // scores q.k, sequential over d, then times the scale (one thread per (row, head, position))
+        for (int t = tid; t < RG * SEG; t += ATT_THREADS) {
+            const int rh = t / SEG, j = t - rh * SEG, rr = rh / G;
+            const int nj = min(SEG, a.pos_base + i0 + rr + 1 - js);
+            if (rr < nr && j < nj) {
+                const float* q = qs + rh * 128;
+                const float* kr = ks + j * KPAD;
+                float sv = 0.0f;
+                for (int d = 0; d < 128; d++) sv = sv + q[d] * kr[d];
+                sc[rh * SEG + j] = sv * a.scale;
+            }
+        }
+        __syncthreads();
+        // segment softmax per (row, head): max, exp, SUM64 denominator
+        for (int rh = wave; rh < RG; rh += ATT_THREADS / 64) {
+            const int rr = rh / G;
+            const int nj = min(SEG, a.pos_base + i0 + rr + 1 - js);
+            if (rr < nr && nj > 0) {
+                const float sv = lane < nj ? sc[rh * SEG + lane] : -__builtin_huge_valf();
+                const float mc = wave_max64(sv);
+                const float e = lane < nj ? expf_cr(sv - mc) : 0.0f;
+                const float lc = wave_sum64(e);
+                if (lane < nj) sc[rh * SEG + lane] = e;
+                if (lane == 0) {
+                    mlc[2 * rh] = mc;
+                    mlc[2 * rh + 1] = lc;
+                }
+            }
+        }
+        __syncthreads();
+        for (int rh = tid; rh < RG; rh += ATT_THREADS) {
+            const int rr = rh / G;
+            if (rr < nr && a.pos_base + i0 + rr + 1 - js > 0) {
+                const float m = run[4 * rh], mc = mlc[2 * rh];
+                const float mn = m > mc ? m : mc;
+                const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
+                run[4 * rh] = mn;
+                run[4 * rh + 1] = run[4 * rh + 1] * ea + eb * mlc[2 * rh + 1];
+                run[4 * rh + 2] = ea;
+                run[4 * rh + 3] = eb;
+            }
+        }
+        seg_stage_v(vreg, njmax, -1, nullptr, ks);
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < MAXR; r++) {
             const int t = tid + r * ATT_THREADS;
-            if (t < G * 128) {
-                const int h = t >> 7, d = t & 127;
-                const float* e = sc + h * SEG;
-                float o = 0.0f;
-                for (int j = 0; j < nj; j++) o = o + e[j] * ks[j * 128 + d];
-                num[r] = num[r] * run[4 * h + 2] + run[4 * h + 3] * o;
+            if (t < RG * 128) {
+                const int rh = t >> 7, d = t & 127, rr = rh / G;
+                const int nj = min(SEG, a.pos_base + i0 + rr + 1 - js);
+                if (rr < nr && nj > 0) {
+                    const float* e = sc + rh * SEG;
+                    float o = 0.0f;
+                    for (int j = 0; j < nj; j++) o = o + e[j] * ks[j * 128 + d];
+                    num[r] = num[r] * run[4 * rh + 2] + run[4 * rh + 3] * o;
+                }
             }
         }
     }
@@ -315,9 +368,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_rows(AttnRowsLaunch a) {
 #pragma unroll
     for (int r = 0; r < MAXR; r++) {
         const int t = tid + r * ATT_THREADS;
-        if (t < G * 128) {
-            const int h = t >> 7, d = t & 127;
-            a.out[(size_t)i * QD + (kvh * G + h) * 128 + d] = __fdiv_rn(num[r], run[4 * h + 1]);
+        if (t < RG * 128) {
+            const int rh = t >> 7, d = t & 127, rr = rh / G, h = rh - rr * G;
+            if (rr < nr)
+                a.out[(size_t)(i0 + rr) * QD + (kvh * G + h) * 128 + d] = __fdiv_rn(num[r], run[4 * rh + 1]);
         }
     }
 }
@@ -446,8 +500,12 @@ lq8_status launch_attention_rows(hipStream_t s, const AttnRowsLaunch& a) {
     if (!attention_supported(a.num_heads, a.num_kv_heads, 128))
         return fail(LQ8_ERR_SHAPE_MISMATCH, "attention: unsupported head layout");
     const int G = a.num_heads / a.num_kv_heads;
-    hipLaunchKernelGGL(k_attn_rows, dim3((unsigned)a.num_kv_heads, (unsigned)a.n), dim3(ATT_THREADS), rows_smem(G), s,
-                       a);
+    // rows per workgroup: R * G <= 16 (the per-thread output registers)
+    const int R = G <= 4 ? 4 : G <= 8 ? 2 : 1;
+    const dim3 grid((unsigned)a.num_kv_heads, (unsigned)((a.n + R - 1) / R));
+    if (R == 4) hipLaunchKernelGGL(k_attn_rows<4>, grid, dim3(ATT_THREADS), rows_smem(R * G), s, a);
+    else if (R == 2) hipLaunchKernelGGL(k_attn_rows<2>, grid, dim3(ATT_THREADS), rows_smem(R * G), s, a);
+    else hipLaunchKernelGGL(k_attn_rows<1>, grid, dim3(ATT_THREADS), rows_smem(R * G), s, a);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

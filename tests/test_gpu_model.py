@@ -135,6 +135,25 @@ def test_wide_gqa_and_odd_block_counts(ctx):
     ref.close()
 
 
+@pytest.mark.parametrize("heads,kv", [(4, 2), (8, 1)])
+def test_chunked_prefill_across_segments(ctx, heads, kv):
+    """Prefill in chunks at offsets 0, 30 and 61: the later chunks' rows
+    straddle 64-position segment boundaries, so rows of one attention
+    workgroup end in different segments.  Logits bit-exact after every chunk
+    and for a decode step."""
+    cfg = lq8.Qwen3Config(vocab_size=700, hidden_size=256, intermediate_size=352, num_hidden_layers=2,
+                          num_attention_heads=heads, num_key_value_heads=kv, head_dim=128,
+                          max_position_embeddings=192)
+    model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=40 + heads)
+    ref = oracle.Model(cfg, model.export_all())
+    ids = np.random.default_rng(heads).integers(0, cfg.vocab_size, 140).astype(np.uint32)
+    for a, b in [(0, 30), (30, 61), (61, 139)]:
+        assert same_bits(model.forward(ids[a:b], a), ref.forward(ids[a:b], a)), (a, b)
+    assert same_bits(model.forward([int(ids[139])], 139), ref.forward([int(ids[139])], 139))
+    model.free()
+    ref.close()
+
+
 @pytest.mark.parametrize("hidden", [1568, 2112])
 def test_wide_hidden_prefill_paths(ctx, hidden):
     """Prefill normalizes and quantizes GEMM inputs in one kernel for hidden
