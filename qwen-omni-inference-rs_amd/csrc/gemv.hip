@@ -160,8 +160,7 @@ struct Stage {
                     for (int u = 0; u < 8; u++)
                         if (i0 + 64 * u < k) acc = acc + v[u] * v[u];
                 }
-#pragma unroll
-                for (int d = 32; d >= 1; d >>= 1) acc = acc + __shfl_xor(acc, d, 64);
+                acc = wave_sum64(acc);
                 if (tid == 0) red[0] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)k) + a.eps));
             }
             __syncthreads();
@@ -319,13 +318,13 @@ __device__ __forceinline__ void gemv_tiles(const GemvArgs& a, int tile0, int nti
         for (int i = 0; i < CH; i++) {
             const int p = min(g * CH + i, np - 1);
             const float h = dot16(cv[i], xs + (2 * p + bsel) * 32 + half * 16);
-            const float o = __shfl_xor(h, 16, 64);
-            const float h0 = half ? o : h, h1 = half ? h : o;
-            const float vb = (h0 + h1) * f16_bits_to_f32(ds[i]);
-            const float ov = __shfl_xor(vb, 32, 64);
-            // level s = 1 of the tree: blocks 2p and 2p + 1 (absent when nb is odd)
-            if (2 * p + 1 >= nb) v[i] = bsel ? ov : vb;
-            else v[i] = bsel ? ov + vb : vb + ov;
+            // h0 + h1: the half-0 lane's sum (even 16-lane row) plus the half-1 lane's
+            const LanePair hh = lanes16(h);
+            const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(ds[i]);
+            // level s = 1 of the tree: v_2p (lanes 0..31) + v_2p+1 (lanes 32..63),
+            // v_2p alone when block 2p + 1 is the padding of an odd nb
+            const LanePair vv = lanes32(vb);
+            v[i] = 2 * p + 1 >= nb ? vv.lo : vv.lo + vv.hi;
         }
 #pragma unroll
         for (int s = 1; s < CH; s *= 2)
@@ -495,8 +494,7 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
                     for (int u = 0; u < 8; u++)
                         if (i0 + 64 * u < k) acc = acc + v[u] * v[u];
                 }
-#pragma unroll
-                for (int d = 32; d >= 1; d >>= 1) acc = acc + __shfl_xor(acc, d, 64);
+                acc = wave_sum64(acc);
                 if (lane == 0) red[wave] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)k) + a.eps));
             }
             __syncthreads();
@@ -560,12 +558,12 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
                         h = fmaf(wf[i][4 * q + 2], xq.z, h);
                         h = fmaf(wf[i][4 * q + 3], xq.w, h);
                     }
-                    // h0 + h1 and v_2p + v_2p+1: IEEE addition is commutative, so
-                    // either lane of a pair computes the same bits without a select
-                    const float vb = (h + __shfl_xor(h, 16, 64)) * dsf[i];
-                    const float ov = __shfl_xor(vb, 32, 64);
-                    if (2 * p + 1 >= nb) t[i] = bsel ? ov : vb;
-                    else t[i] = vb + ov;
+                    // h0 + h1 (half-0 lane's sum first) and v_2p + v_2p+1, v_2p alone
+                    // when block 2p + 1 is the padding of an odd nb
+                    const LanePair hh = lanes16(h);
+                    const float vb = (hh.lo + hh.hi) * dsf[i];
+                    const LanePair vv = lanes32(vb);
+                    t[i] = 2 * p + 1 >= nb ? vv.lo : vv.lo + vv.hi;
                 }
 #pragma unroll
                 for (int s = 1; s < CH; s *= 2)

@@ -63,10 +63,63 @@ __device__ __forceinline__ int sat_i8(float v) {
     return (int)v;
 }
 
-// SUM64 fold of one 64-lane wave's partials: distances 32, 16, 8, 4, 2, 1.
+// ---- cross-lane exchange without the LDS path (gfx950) ----------------------
+// lane_xor<D>(v): the value v of lane l ^ D (exactly the __shfl_xor partner)
+// from VALU lane moves: v_permlane32_swap / v_permlane16_swap (the same
+// register as both operands returns, in every lane, the values of the lower
+// and the upper lane of the pair), DPP row_ror:8 (lane i of a 16-lane row
+// reads lane (i - 8) mod 16 = i ^ 8), row_shl:4 / row_shr:4 (lanes i + 4 and
+// i - 4; the one inside the row is i ^ 4) and quad_perm (i ^ 2, i ^ 1).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+struct LanePair {
+    float lo, hi;  // values of lanes l & ~D and l | D
+};
+
+__device__ __forceinline__ LanePair lanes32(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return {__uint_as_float(p[0]), __uint_as_float(p[1])};
+}
+
+__device__ __forceinline__ LanePair lanes16(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return {__uint_as_float(p[0]), __uint_as_float(p[1])};
+}
+
+template <int D>
+__device__ __forceinline__ float lane_xor(float v) {
+    static_assert(D == 1 || D == 2 || D == 4 || D == 8 || D == 16 || D == 32, "xor distance");
+    const int lane = __lane_id();
+    if constexpr (D == 32) {
+        const LanePair p = lanes32(v);
+        return (lane & 32) ? p.lo : p.hi;
+    } else if constexpr (D == 16) {
+        const LanePair p = lanes16(v);
+        return (lane & 16) ? p.lo : p.hi;
+    } else if constexpr (D == 8) {
+        return dpp_move<0x128>(v);  // row_ror:8
+    } else if constexpr (D == 4) {
+        const float up = dpp_move<0x104>(v), down = dpp_move<0x114>(v);  // row_shl:4, row_shr:4
+        return (lane & 4) ? down : up;
+    } else if constexpr (D == 2) {
+        return dpp_move<0x4E>(v);  // quad_perm [2, 3, 0, 1]
+    } else {
+        return dpp_move<0xB1>(v);  // quad_perm [1, 0, 3, 2]
+    }
+}
+
+// SUM64 fold of one 64-lane wave's partials: a = a + (lane l ^ d's a) for
+// d = 32, 16, 8, 4, 2, 1.
 __device__ __forceinline__ float wave_sum64(float a) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) a = a + __shfl_xor(a, d, 64);
+    a = a + lane_xor<32>(a);
+    a = a + lane_xor<16>(a);
+    a = a + lane_xor<8>(a);
+    a = a + lane_xor<4>(a);
+    a = a + lane_xor<2>(a);
+    a = a + lane_xor<1>(a);
     return a;
 }
 

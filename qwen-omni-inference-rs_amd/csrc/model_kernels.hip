@@ -25,12 +25,20 @@ constexpr int KPAD = 129;  // LDS row stride of staged keys (bank-conflict free 
 __host__ __device__ inline int seg_ks_off(int G) { return (G * 128 + 256 + G * SEG + 2 * G + 3) & ~3; }
 __host__ __device__ inline int rows_ks_off(int G) { return (G * 128 + G * SEG + 6 * G + 3) & ~3; }
 
+// max fold in the SUM64 pattern: a = (o > a ? o : a) with o the value of lane
+// l ^ d, d = 32, 16, 8, 4, 2, 1.
+template <int D>
+__device__ __forceinline__ float max_step(float a) {
+    const float o = lane_xor<D>(a);
+    return o > a ? o : a;
+}
 __device__ __forceinline__ float wave_max64(float a) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        const float o = __shfl_xor(a, d, 64);
-        a = o > a ? o : a;
-    }
+    a = max_step<32>(a);
+    a = max_step<16>(a);
+    a = max_step<8>(a);
+    a = max_step<4>(a);
+    a = max_step<2>(a);
+    a = max_step<1>(a);
     return a;
 }
 

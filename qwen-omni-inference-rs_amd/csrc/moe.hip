@@ -117,8 +117,12 @@ __global__ __launch_bounds__(64 * ROUTE_WAVES) void k_moe_route(RouteArgs ra) {
             p[j] = i < E ? scores[(size_t)t * E + i] : NEG;
             m = fmaxf(m, p[j]);
         }
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+        m = fmaxf(m, lane_xor<32>(m));
+        m = fmaxf(m, lane_xor<16>(m));
+        m = fmaxf(m, lane_xor<8>(m));
+        m = fmaxf(m, lane_xor<4>(m));
+        m = fmaxf(m, lane_xor<2>(m));
+        m = fmaxf(m, lane_xor<1>(m));
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -127,8 +131,7 @@ __global__ __launch_bounds__(64 * ROUTE_WAVES) void k_moe_route(RouteArgs ra) {
                 acc = acc + p[j];
             }
         }
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) acc = acc + __shfl_xor(acc, d, 64);
+        acc = wave_sum64(acc);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int i = lane + 64 * j;

@@ -257,7 +257,7 @@ __global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ 
             v[4 * i + 3] = t.w;
         }
         amax = half_amax(v);
-        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        amax = fmaxf(amax, lane_xor<16>(amax));
     }
     put_act_half(codes, xs, np, np8 >> 1, nb, tile * TILE_ROWS + r, b, hf, v, amax);
 }
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(256) void k_rms_quantize_act(const float* __restric
             }
         }
         float amax = half_amax(q);
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, lane_xor<1>(amax));
         if (hb < nhb) put_act_half(codes, xs, np, nbp >> 2, nb, row, b, hf, q, amax);
     }
 }
@@ -345,9 +345,9 @@ __global__ __launch_bounds__(256) void k_silu_quantize_act(const float* __restri
         q[3] = __fdiv_rn(gv.w, 1.0f + expf_cr(-gv.w)) * uv.w;
     }
     float amax = fmaxf(fmaxf(fmaxf(0.0f, fabsf(q[0])), fabsf(q[1])), fmaxf(fabsf(q[2]), fabsf(q[3])));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    amax = fmaxf(amax, lane_xor<1>(amax));
+    amax = fmaxf(amax, lane_xor<2>(amax));
+    amax = fmaxf(amax, lane_xor<4>(amax));
     uint32_t d16 = 0;
     if (b < 2 * np) {
         uint32_t c = 0;
