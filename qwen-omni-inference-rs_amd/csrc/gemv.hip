@@ -53,6 +53,18 @@ __device__ __forceinline__ float dot16(u32x4 v, const float* __restrict__ x) {
     return p;
 }
 
+// One level of the greedy pick between lane l and lane l ^ D: maximum, last
+// index on ties.
+template <int D>
+__device__ __forceinline__ void argmax_step(float& bv, int& bi) {
+    const float ov = lane_xor<D>(bv);
+    const int oi = lane_xor_int<D>(bi);
+    if (ov > bv || (ov == bv && oi > bi)) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
 __device__ __forceinline__ float4 bf16_round4(float4 v) {
     return make_float4(bf16_round(v.x), bf16_round(v.y), bf16_round(v.z), bf16_round(v.w));
 }
@@ -366,12 +378,10 @@ __device__ __forceinline__ void gemv_tiles(const GemvArgs& a, int tile0, int nti
             // greedy pick within the tile: maximum, last index on ties
             float bv = valid ? acc : -__builtin_huge_valf();
             int bi = valid ? row : -1;
-#pragma unroll
-            for (int d = 8; d >= 1; d >>= 1) {
-                const float ov = __shfl_xor(bv, d, 64);
-                const int oi = __shfl_xor(bi, d, 64);
-                if (ov > bv || (ov == bv && oi > bi)) { bv = ov; bi = oi; }
-            }
+            argmax_step<8>(bv, bi);
+            argmax_step<4>(bv, bi);
+            argmax_step<2>(bv, bi);
+            argmax_step<1>(bv, bi);
             if (lane == 0) {
                 a.arg_val[tile] = bv;
                 a.arg_idx[tile] = bi;
@@ -632,12 +642,12 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__
         for (int e = 0; e < AU; e++)
             if (i0 + e * 1024 < count && (v[e] > bv || (v[e] == bv && j[e] > bi))) { bv = v[e]; bi = j[e]; }
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        const float ov = __shfl_xor(bv, d, 64);
-        const int oi = __shfl_xor(bi, d, 64);
-        if (ov > bv || (ov == bv && oi > bi)) { bv = ov; bi = oi; }
-    }
+    argmax_step<32>(bv, bi);
+    argmax_step<16>(bv, bi);
+    argmax_step<8>(bv, bi);
+    argmax_step<4>(bv, bi);
+    argmax_step<2>(bv, bi);
+    argmax_step<1>(bv, bi);
     if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
     __syncthreads();
     if (tid == 0) {

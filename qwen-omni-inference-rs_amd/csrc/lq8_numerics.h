@@ -111,6 +111,11 @@ __device__ __forceinline__ float lane_xor(float v) {
     }
 }
 
+template <int D>
+__device__ __forceinline__ int lane_xor_int(int v) {
+    return __builtin_bit_cast(int, lane_xor<D>(__builtin_bit_cast(float, v)));
+}
+
 // SUM64 fold of one 64-lane wave's partials: a = a + (lane l ^ d's a) for
 // d = 32, 16, 8, 4, 2, 1.
 __device__ __forceinline__ float wave_sum64(float a) {
