@@ -204,6 +204,48 @@ typedef struct {
 /* Greedy generation; the token loop stays on the device.  out_tokens: max_new. */
 lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
                                uint32_t* out_tokens, lq8_gen_stats* stats);
+
+/* ---- sampling ----------------------------------------------------------------
+ * The fields of GenerationConfig (src/generate.rs:40-128) besides
+ * max_new_tokens, plus the RNG seed; GenerationConfig::new's ranges are
+ * enforced (temperature >= 0, top_p in [0, 1], repetition_penalty >= 1;
+ * LQ8_ERR_INVALID_ARG otherwise).
+ * The reference's samplers are argmax stubs (src/generate.rs:191-329); this
+ * library samples for real, by this rule:
+ *   x = logits with the repetition penalty applied once per earlier
+ *       occurrence of each token (src/generate.rs:353-380; off at 1.0);
+ *   temperature 0: greedy, the largest x, the last index on ties;
+ *   otherwise z = x / temperature; tokens ordered by z descending (ties: the
+ *   lower index first); the first top_k kept (all for 0); e = exp(z - z_max);
+ *   prefix sums C of e in that order, in chunks of 64 (chunk totals
+ *   sequential, then sequential over the chunks); the nucleus ends at the
+ *   first C >= top_p * C_last (the whole kept set for top_p = 1);
+ *   u = (SplitMix64(seed + step * 0x9E3779B97F4A7C15) >> 40) * 2^-24, where
+ *   step is the index of the generated token (0 for the token after the
+ *   prompt); the token is the first one of the nucleus with C > u * C_end.
+ * Unlike the reference's dispatch (src/generate.rs:670-693), temperature 1
+ * with no top-k / top-p samples (the stub returns the argmax there). */
+typedef struct {
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    float repetition_penalty;
+    uint64_t seed;
+} lq8_sampling;
+
+/* sample_with_config (src/generate.rs:670-693) on device logits [vocab]:
+ * the token goes to *d_token (device).  d_counts: device [vocab] counts of
+ * each token generated so far (the repetition penalty; NULL for none); step:
+ * the RNG counter.  Blocks until the token is written. */
+lq8_status lq8_sample_device(lq8_ctx* ctx, const float* d_logits, size_t vocab, const uint32_t* d_counts,
+                             const lq8_sampling* cfg, uint32_t step, uint32_t* d_token);
+
+/* generate (src/generate.rs:611-664) with a sampling configuration: prefill,
+ * the first token from the prefill logits, then max_new - 1 decode steps,
+ * each sampled on the device (the repetition penalty counts the generated
+ * tokens, as the reference's generated_tokens).  out_tokens: max_new. */
+lq8_status lq8_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                        const lq8_sampling* cfg, uint32_t* out_tokens, lq8_gen_stats* stats);
 lq8_status lq8_model_free(lq8_model* m);
 
 /* ---- Qwen3-MoE decoder layers (Qwen3-30B-A3B style), decode steps --------

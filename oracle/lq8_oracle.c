@@ -818,3 +818,118 @@ done:
     free(ids); free(wts);
     return rc;
 }
+
+/* ---- sampling (the library's rule; the reference's samplers are argmax
+ * stubs, src/generate.rs:191-329) ------------------------------------------
+ * penalty per earlier occurrence (src/generate.rs:353-380), T = 0 greedy
+ * (last index on ties), else z = x / T, order by z descending (lower index
+ * first on ties), top_k, e = exp(z - z0), chunked prefix sums (chunks of 64:
+ * totals sequential, then sequential over the chunks), nucleus end = first
+ * C >= top_p * S, u from SplitMix64(seed + step * golden), first C > u * C_end. */
+static uint32_t orc_order_bits(float z) {
+    uint32_t b;
+    memcpy(&b, &z, 4);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+static float orc_from_order(uint32_t k) {
+    uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+static int orc_cmp_desc_u64(const void* a, const void* b) {
+    const uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
+    return x < y ? 1 : (x > y ? -1 : 0);
+}
+static uint64_t orc_splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+int64_t orc_sample(const float* logits, size_t V, const uint32_t* counts, float T, uint32_t top_k, float top_p,
+                   float penalty, uint64_t seed, uint32_t step) {
+    if (V == 0) return -1;
+    uint64_t* keys = (uint64_t*)malloc(V * sizeof(uint64_t));
+    if (!keys) return -1;
+    for (size_t i = 0; i < V; i++) {
+        float x = logits[i];
+        if (fabsf(penalty - 1.0f) >= 1e-6f && counts)
+            for (uint32_t c = 0; c < counts[i]; c++) {
+                if (x > 0.0f) x = x / penalty;
+                else if (x < 0.0f) x = x * penalty;
+            }
+        const float z = T > 0.0f ? x / T : x;
+        const uint32_t lo = T > 0.0f ? ~(uint32_t)i : (uint32_t)i;
+        keys[i] = ((uint64_t)orc_order_bits(z) << 32) | lo;
+    }
+    qsort(keys, V, sizeof(uint64_t), orc_cmp_desc_u64);
+    int64_t token;
+    if (!(T > 0.0f)) {
+        token = (uint32_t)keys[0];
+        free(keys);
+        return token;
+    }
+    const size_t K = top_k > 0 && top_k < V ? top_k : V, nch = (K + 63) / 64;
+    const float z0 = orc_from_order((uint32_t)(keys[0] >> 32));
+    float* tot = (float*)malloc(nch * sizeof(float));
+    if (!tot) {
+        free(keys);
+        return -1;
+    }
+    for (size_t c = 0; c < nch; c++) {
+        float t = 0.0f;
+        for (size_t j = c * 64; j < c * 64 + 64 && j < K; j++) t = t + orc_expf(orc_from_order((uint32_t)(keys[j] >> 32)) - z0);
+        tot[c] = t;
+    }
+    float S = 0.0f;
+    for (size_t c = 0; c < nch; c++) S = S + tot[c];
+    size_t end = K - 1;
+    float Cend = S;
+    if (top_p < 1.0f) {
+        const float thr = top_p * S;
+        float P = 0.0f;
+        size_t c = 0;
+        while (c + 1 < nch && !(P + tot[c] >= thr)) {
+            P = P + tot[c];
+            c++;
+        }
+        const size_t jl = (c * 64 + 64 < K ? c * 64 + 64 : K) - 1;
+        float I = 0.0f;
+        int64_t found = -1;
+        for (size_t j = c * 64; j <= jl; j++) {
+            I = I + orc_expf(orc_from_order((uint32_t)(keys[j] >> 32)) - z0);
+            Cend = P + I;
+            if (Cend >= thr) {
+                found = (int64_t)j;
+                break;
+            }
+        }
+        end = found >= 0 ? (size_t)found : jl;
+    }
+    const uint64_t h = orc_splitmix64(seed + (uint64_t)step * 0x9E3779B97F4A7C15ull);
+    const float u = (float)(uint32_t)(h >> 40) * 5.9604644775390625e-8f;
+    const float r = u * Cend;
+    const size_t ce = end / 64;
+    float P = 0.0f;
+    size_t c = 0;
+    while (c < ce && !(P + tot[c] > r)) {
+        P = P + tot[c];
+        c++;
+    }
+    const size_t jl = c < ce ? c * 64 + 63 : end;
+    float I = 0.0f;
+    int64_t found = -1;
+    for (size_t j = c * 64; j <= jl; j++) {
+        I = I + orc_expf(orc_from_order((uint32_t)(keys[j] >> 32)) - z0);
+        if (P + I > r) {
+            found = (int64_t)j;
+            break;
+        }
+    }
+    token = ~(uint32_t)keys[found >= 0 ? (size_t)found : end];
+    free(tot);
+    free(keys);
+    return token;
+}

@@ -54,6 +54,9 @@ int orc_rope_apply(const float* x, size_t heads, size_t seq, size_t head_dim, co
                    const float* sin_t, size_t offset, float* y);
 float orc_silu(float x);
 uint32_t orc_argmax_last(const float* x, size_t n);
+/* the library's sampling rule (see lq8_sample_device); -1 on bad input */
+int64_t orc_sample(const float* logits, size_t V, const uint32_t* counts, float T, uint32_t top_k, float top_p,
+                   float penalty, uint64_t seed, uint32_t step);
 
 /* ---- Qwen3 model ---- */
 typedef struct {

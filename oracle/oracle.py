@@ -68,6 +68,8 @@ def lib():
             "orc_rope_apply": (C.c_int, [vp, sz, sz, sz, vp, vp, sz, vp]),
             "orc_silu": (C.c_float, [C.c_float]),
             "orc_argmax_last": (C.c_uint32, [vp, sz]),
+            "orc_sample": (C.c_int64, [vp, sz, vp, C.c_float, C.c_uint32, C.c_float, C.c_float, C.c_uint64,
+                                       C.c_uint32]),
             "orc_model_new": (vp, [C.POINTER(OrcConfig), vp]),
             "orc_model_free": (None, [vp]),
             "orc_model_clear_kv_cache": (None, [vp]),
@@ -209,6 +211,18 @@ def argmax_last(x) -> int:
     return int(lib().orc_argmax_last(_p(x), x.size))
 
 
+def sample(logits, counts, temperature: float, top_k: int, top_p: float, repetition_penalty: float, seed: int,
+           step: int) -> int:
+    """The library's sampling rule (lq8_sample_device), restated on the CPU."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    cnt = None if counts is None else np.ascontiguousarray(counts, dtype=np.uint32)
+    t = lib().orc_sample(_p(x), x.size, _p(cnt) if cnt is not None else None, temperature, top_k, top_p,
+                         repetition_penalty, seed & (2**64 - 1), step)
+    if t < 0:
+        raise ValueError("oracle sample failed")
+    return int(t)
+
+
 class Model:
     """Oracle Qwen3ForCausalLM over host tensors in the include/lq8.h table order."""
 
@@ -261,6 +275,24 @@ class Model:
         if rc:
             raise ValueError(f"oracle generate failed ({rc})")
         return toks, margins
+
+    def generate_sampled(self, prompt, max_new: int, temperature: float, top_k: int, top_p: float,
+                         repetition_penalty: float, seed: int) -> np.ndarray:
+        """generate() with the sampling rule: prefill, then one sampled token
+        per step (step t draws with counter t; the penalty counts the tokens
+        generated before it)."""
+        ids = np.ascontiguousarray(prompt, dtype=np.uint32)
+        self.clear_kv_cache()
+        logits = self.forward(ids, 0)
+        counts = np.zeros(self.cfg.vocab_size, dtype=np.uint32)
+        toks = np.empty(max_new, dtype=np.uint32)
+        for t in range(max_new):
+            tok = sample(logits, counts, temperature, top_k, top_p, repetition_penalty, seed, t)
+            toks[t] = tok
+            counts[tok] += 1
+            if t + 1 < max_new:
+                logits = self.forward([tok], ids.size + t)
+        return toks
 
 
 def random_q8_tensors(cfg, seed: int, std: float = 0.02):

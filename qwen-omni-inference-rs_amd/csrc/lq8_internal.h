@@ -173,6 +173,31 @@ lq8_status launch_quantize_aos(hipStream_t s, const float* x, size_t nblocks, ui
 lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const uint32_t* xs, int m, const lq8_weight* w, float* y,
                        const float* resid);
 
+// ---- sampling (sample.hip) -----------------------------------------------------
+struct SampleCfg {
+    float temperature;  // 0: greedy
+    int top_k;          // 0: all
+    float top_p;        // >= 1: off
+    float penalty;      // repetition penalty (1: off)
+    unsigned long long seed;
+};
+struct SampleLaunch {
+    const float* logits;
+    int vocab;
+    const uint32_t* counts;   // occurrences of each token so far (penalty; null: none)
+    uint32_t* counts_out;     // incremented at the chosen token (null: not kept)
+    const SampleCfg* cfg;     // device
+    int* d_step;              // device: the RNG counter and output index (advances)
+    uint32_t* d_tok;          // device: the token
+    uint32_t* tokens_out;     // device [steps] (null: not kept)
+    int* d_pos;               // device position, advanced (null: none)
+    void* work;               // device, sample_work_bytes(vocab): sort buffers, histograms, chunk sums
+};
+// GenerationConfig ranges (src/generate.rs:96-128) -> the device config.
+lq8_status check_sampling(const lq8_sampling* c, SampleCfg* out);
+size_t sample_work_bytes(int vocab);
+lq8_status launch_sample(hipStream_t s, const SampleLaunch& a);
+
 lq8_status launch_repack_aos(hipStream_t s, const uint8_t* aos, size_t n_rows, size_t row0, const lq8_weight* w);
 lq8_status launch_unpack_aos(hipStream_t s, const lq8_weight* w, size_t row0, size_t n_rows, uint8_t* aos);
 lq8_status launch_quantize_weight_f32(hipStream_t s, const float* src, size_t n_rows, size_t row0,

@@ -58,6 +58,11 @@ struct lq8_model {
           *P_xs = nullptr;
     int8_t* P_xq = nullptr;
     hipGraphExec_t graph = nullptr;
+    // sampling: device config, token counts, sort buffers, the sampled decode graph
+    SampleCfg* d_scfg = nullptr;
+    uint32_t* d_counts = nullptr;
+    uint8_t* s_work = nullptr;  // sampler workspace (sample_work_bytes(vocab))
+    hipGraphExec_t sgraph = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
 };
 
@@ -91,6 +96,7 @@ void release(lq8_model* m) {
     registry_remove(m);
     auto F = [](void* p) { if (p) (void)hipFree(p); };
     if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    if (m->sgraph) (void)hipGraphExecDestroy(m->sgraph);
     if (m->e0) (void)hipEventDestroy(m->e0);
     if (m->e1) (void)hipEventDestroy(m->e1);
     if (m->e2) (void)hipEventDestroy(m->e2);
@@ -104,6 +110,7 @@ void release(lq8_model* m) {
     F(m->h); F(m->h2); F(m->qkv); F(m->gu); F(m->apart); F(m->logits); F(m->arg_val); F(m->arg_idx);
     F(m->d_ids); F(m->d_pos); F(m->d_step); F(m->d_tok); F(m->d_tokens);
     F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_xs); F(m->P_xq);
+    F(m->d_scfg); F(m->d_counts); F(m->s_work);
     delete m;
 }
 
@@ -367,6 +374,56 @@ lq8_status launch_pick(lq8_model* m) {
                                m->d_pos, m->d_step);
 }
 
+// Sampling buffers (allocated on first use, vocabulary-sized).
+lq8_status ensure_sampler(lq8_model* m) {
+    if (m->d_scfg) return LQ8_OK;
+    const int V = (int)m->c.vocab_size;
+    lq8_status st;
+    if ((st = dalloc(&m->d_scfg, 1)) || (st = dalloc(&m->d_counts, (size_t)V)) ||
+        (st = dalloc(&m->s_work, sample_work_bytes(V))))
+        return st;
+    return LQ8_OK;
+}
+
+// sample_with_config on the model's logits: the token -> d_tok and
+// d_tokens[*d_step]; d_step, d_pos and the token's count advance.
+lq8_status launch_sample_pick(lq8_model* m) {
+    SampleLaunch a{};
+    a.logits = m->logits;
+    a.vocab = (int)m->c.vocab_size;
+    a.counts = m->d_counts;
+    a.counts_out = m->d_counts;
+    a.cfg = m->d_scfg;
+    a.d_step = m->d_step;
+    a.d_tok = m->d_tok;
+    a.tokens_out = m->d_tokens;
+    a.d_pos = m->d_pos;
+    a.work = m->s_work;
+    return launch_sample(m->ctx->stream, a);
+}
+
+lq8_status capture_sample_graph(lq8_model* m) {
+    if (m->sgraph) return LQ8_OK;
+    hipStream_t s = m->ctx->stream;
+    hipGraph_t g = nullptr;
+    LQ8_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
+    lq8_status st = enqueue_decode(m, m->d_tok, m->d_pos, 0);
+    if (!st) st = launch_sample_pick(m);
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (st) {
+        if (g) (void)hipGraphDestroy(g);
+        return st;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    e = hipGraphInstantiate(&m->sgraph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        m->sgraph = nullptr;
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    return LQ8_OK;
+}
+
 lq8_status capture_decode_graph(lq8_model* m) {
     if (m->graph) return LQ8_OK;
     hipStream_t s = m->ctx->stream;
@@ -385,6 +442,76 @@ lq8_status capture_decode_graph(lq8_model* m) {
     if (e != hipSuccess) {
         m->graph = nullptr;
         return hip_fail(e, "hipGraphInstantiate");
+    }
+    return LQ8_OK;
+}
+
+}  // namespace
+
+namespace {
+
+// generate (src/generate.rs:611-664): greedy picks (sc null) or sampled ones.
+lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new, const SampleCfg* sc,
+                        uint32_t* out_tokens, lq8_gen_stats* stats) {
+    if (!prompt || n_prompt == 0) return fail(LQ8_ERR_INVALID_ARG, "empty prompt");
+    if (max_new == 0 || !out_tokens) return fail(LQ8_ERR_INVALID_ARG, "max_new must be positive");
+    if (n_prompt + max_new - 1 > m->c.max_positions)
+        return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "prompt + generated tokens exceed max_positions");
+    for (size_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= m->c.vocab_size) return fail(LQ8_ERR_INVALID_ARG, "token id out of range for vocab_size");
+    LQ8_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    lq8_status st;
+    if ((st = ensure_ids(m, n_prompt))) return st;
+    if (max_new > m->tokens_cap) {
+        if (m->d_tokens) LQ8_HIP(hipFree(m->d_tokens));
+        m->d_tokens = nullptr;
+        if ((st = dalloc(&m->d_tokens, max_new))) return st;
+        m->tokens_cap = max_new;
+        if (m->graph) { (void)hipGraphExecDestroy(m->graph); m->graph = nullptr; }
+        if (m->sgraph) { (void)hipGraphExecDestroy(m->sgraph); m->sgraph = nullptr; }
+    }
+    if (n_prompt > 1 && (st = ensure_prefill(m, n_prompt))) return st;
+    const bool use_graph = std::getenv("LQ8_NO_GRAPH") == nullptr;
+    if (sc && (st = ensure_sampler(m))) return st;
+    if (use_graph && max_new > 1 && (st = sc ? capture_sample_graph(m) : capture_decode_graph(m))) return st;
+    // clear_kv_cache (src/generate.rs:618), then prefill at offset 0
+    m->kv_len = 0;
+    const int zero = 0, pos0 = (int)n_prompt - 1;
+    LQ8_HIP(hipMemcpyAsync(m->d_ids, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    LQ8_HIP(hipMemcpyAsync(m->d_step, &zero, sizeof(int), hipMemcpyHostToDevice, s));
+    LQ8_HIP(hipMemcpyAsync(m->d_pos, &pos0, sizeof(int), hipMemcpyHostToDevice, s));
+    if (sc) {
+        // the penalty counts the generated tokens only (generated_tokens, src/generate.rs:627-660)
+        LQ8_HIP(hipMemcpyAsync(m->d_scfg, sc, sizeof(SampleCfg), hipMemcpyHostToDevice, s));
+        LQ8_HIP(hipMemsetAsync(m->d_counts, 0, m->c.vocab_size * sizeof(uint32_t), s));
+    }
+    LQ8_HIP(hipEventRecord(m->e0, s));
+    st = n_prompt == 1 ? enqueue_decode(m, m->d_ids, nullptr, 0) : enqueue_prefill(m, (int)n_prompt, 0);
+    if (st) return st;
+    // first token from the prefill logits; d_pos becomes n_prompt
+    if ((st = sc ? launch_sample_pick(m) : launch_pick(m))) return st;
+    LQ8_HIP(hipEventRecord(m->e1, s));
+    for (size_t t = 1; t < max_new; t++) {
+        if (use_graph) {
+            LQ8_HIP(hipGraphLaunch(sc ? m->sgraph : m->graph, s));
+        } else {
+            if ((st = enqueue_decode(m, m->d_tok, m->d_pos, 0))) return st;
+            if ((st = sc ? launch_sample_pick(m) : launch_pick(m))) return st;
+        }
+    }
+    LQ8_HIP(hipEventRecord(m->e2, s));
+    LQ8_HIP(hipMemcpyAsync(out_tokens, m->d_tokens, max_new * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    LQ8_HIP(hipStreamSynchronize(s));
+    m->kv_len = n_prompt + max_new - 1;
+    if (stats) {
+        float a = 0, b = 0;
+        LQ8_HIP(hipEventElapsedTime(&a, m->e0, m->e1));
+        LQ8_HIP(hipEventElapsedTime(&b, m->e1, m->e2));
+        stats->prefill_ms = a;
+        stats->decode_ms = b;
+        stats->decode_tokens_per_s = (max_new > 1 && b > 0) ? (double)(max_new - 1) / (b * 1e-3) : 0.0;
+        stats->used_graph = use_graph ? 1u : 0u;
     }
     return LQ8_OK;
 }
@@ -604,60 +731,19 @@ lq8_status lq8_model_forward_with_intermediates(lq8_model* m, const uint32_t* id
 lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
                                uint32_t* out_tokens, lq8_gen_stats* stats) {
     CHECK_M(m);
-    if (!prompt || n_prompt == 0) return fail(LQ8_ERR_INVALID_ARG, "empty prompt");
-    if (max_new == 0 || !out_tokens) return fail(LQ8_ERR_INVALID_ARG, "max_new must be positive");
-    if (n_prompt + max_new - 1 > m->c.max_positions)
-        return fail(LQ8_ERR_DIM_OUT_OF_RANGE, "prompt + generated tokens exceed max_positions");
-    for (size_t i = 0; i < n_prompt; i++)
-        if (prompt[i] >= m->c.vocab_size) return fail(LQ8_ERR_INVALID_ARG, "token id out of range for vocab_size");
-    LQ8_HIP(hipSetDevice(m->ctx->device));
-    hipStream_t s = m->ctx->stream;
-    lq8_status st;
-    if ((st = ensure_ids(m, n_prompt))) return st;
-    if (max_new > m->tokens_cap) {
-        if (m->d_tokens) LQ8_HIP(hipFree(m->d_tokens));
-        m->d_tokens = nullptr;
-        if ((st = dalloc(&m->d_tokens, max_new))) return st;
-        m->tokens_cap = max_new;
-        if (m->graph) { (void)hipGraphExecDestroy(m->graph); m->graph = nullptr; }
-    }
-    if (n_prompt > 1 && (st = ensure_prefill(m, n_prompt))) return st;
-    const bool use_graph = std::getenv("LQ8_NO_GRAPH") == nullptr;
-    if (use_graph && max_new > 1 && (st = capture_decode_graph(m))) return st;
-    // clear_kv_cache (src/generate.rs:618), then prefill at offset 0
-    m->kv_len = 0;
-    const int zero = 0, pos0 = (int)n_prompt - 1;
-    LQ8_HIP(hipMemcpyAsync(m->d_ids, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, s));
-    LQ8_HIP(hipMemcpyAsync(m->d_step, &zero, sizeof(int), hipMemcpyHostToDevice, s));
-    LQ8_HIP(hipMemcpyAsync(m->d_pos, &pos0, sizeof(int), hipMemcpyHostToDevice, s));
-    LQ8_HIP(hipEventRecord(m->e0, s));
-    st = n_prompt == 1 ? enqueue_decode(m, m->d_ids, nullptr, 0) : enqueue_prefill(m, (int)n_prompt, 0);
+    return run_generate(m, prompt, n_prompt, max_new, nullptr, out_tokens, stats);
+}
+
+lq8_status lq8_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                        const lq8_sampling* cfg, uint32_t* out_tokens, lq8_gen_stats* stats) {
+    CHECK_M(m);
+    SampleCfg sc;
+    lq8_status st = check_sampling(cfg, &sc);
     if (st) return st;
-    // first token from the prefill logits; d_pos becomes n_prompt
-    if ((st = launch_pick(m))) return st;
-    LQ8_HIP(hipEventRecord(m->e1, s));
-    for (size_t t = 1; t < max_new; t++) {
-        if (use_graph) {
-            LQ8_HIP(hipGraphLaunch(m->graph, s));
-        } else {
-            if ((st = enqueue_decode(m, m->d_tok, m->d_pos, 0))) return st;
-            if ((st = launch_pick(m))) return st;
-        }
-    }
-    LQ8_HIP(hipEventRecord(m->e2, s));
-    LQ8_HIP(hipMemcpyAsync(out_tokens, m->d_tokens, max_new * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-    LQ8_HIP(hipStreamSynchronize(s));
-    m->kv_len = n_prompt + max_new - 1;
-    if (stats) {
-        float a = 0, b = 0;
-        LQ8_HIP(hipEventElapsedTime(&a, m->e0, m->e1));
-        LQ8_HIP(hipEventElapsedTime(&b, m->e1, m->e2));
-        stats->prefill_ms = a;
-        stats->decode_ms = b;
-        stats->decode_tokens_per_s = (max_new > 1 && b > 0) ? (double)(max_new - 1) / (b * 1e-3) : 0.0;
-        stats->used_graph = use_graph ? 1u : 0u;
-    }
-    return LQ8_OK;
+    // temperature 0 without a penalty is the greedy rule exactly
+    if (sc.temperature == 0.0f && std::fabs(sc.penalty - 1.0f) < 1e-6f)
+        return run_generate(m, prompt, n_prompt, max_new, nullptr, out_tokens, stats);
+    return run_generate(m, prompt, n_prompt, max_new, &sc, out_tokens, stats);
 }
 
 lq8_status lq8_model_free(lq8_model* m) {

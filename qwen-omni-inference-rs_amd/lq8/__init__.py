@@ -101,6 +101,11 @@ class GenStatsC(C.Structure):
                 ("used_graph", C.c_uint32)]
 
 
+class SamplingC(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
+                ("repetition_penalty", C.c_float), ("seed", C.c_uint64)]
+
+
 _lib: Optional[C.CDLL] = None
 
 # (name, restype, argtypes) of every exported entry point.
@@ -156,6 +161,10 @@ _SIGS = [
      [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p, C.c_void_p]),
     ("lq8_generate_greedy", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.POINTER(GenStatsC)]),
+    ("lq8_sample_device", C.c_int,
+     [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.POINTER(SamplingC), C.c_uint32, C.c_void_p]),
+    ("lq8_generate", C.c_int,
+     [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(SamplingC), C.c_void_p, C.POINTER(GenStatsC)]),
     ("lq8_model_free", C.c_int, [C.c_void_p]),
     ("lq8_moe_tensor_count", C.c_size_t, [C.POINTER(MoeConfigC)]),
     ("lq8_moe_tensor_bytes", C.c_int, [C.POINTER(MoeConfigC), C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -579,10 +588,67 @@ class Qwen3ForCausalLM:
         return out, {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
                      "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph)}
 
+    def generate(self, prompt: Sequence[int], config: "GenerationConfig", seed: int = 0):
+        """generate() (src/generate.rs:611-664) with the configuration's
+        sampling, config.max_new_tokens tokens; the loop stays on the device."""
+        ids = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(config.max_new_tokens, dtype=np.uint32)
+        st = GenStatsC()
+        sc = config.sampling(seed)
+        _check(lib().lq8_generate(self.handle, _ptr(ids), ids.size, config.max_new_tokens, C.byref(sc), _ptr(out),
+                                  C.byref(st)))
+        return out, {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
+                     "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph)}
+
     def free(self) -> None:
         if self.handle:
             _check(lib().lq8_model_free(self.handle))
             self.handle = None
+
+
+# ---- sampling --------------------------------------------------------------------
+
+@dataclass
+class GenerationConfig:
+    """GenerationConfig (src/generate.rs:40-128): the defaults are greedy;
+    ``new`` enforces the reference's ranges (InvalidArgument otherwise).  The
+    sampling rule itself is the library's (include/lq8.h, lq8_sampling): the
+    reference's samplers are argmax stubs."""
+
+    max_new_tokens: int = 100
+    temperature: float = 0.0
+    top_k: int = 0
+    top_p: float = 1.0
+    repetition_penalty: float = 1.0
+
+    @classmethod
+    def new(cls, max_new_tokens: int, temperature: float, top_k: int, top_p: float,
+            repetition_penalty: float) -> "GenerationConfig":
+        if temperature < 0.0:
+            raise InvalidArgument(f"temperature must be >= 0.0, got {temperature}", 0)
+        if not 0.0 <= top_p <= 1.0:
+            raise InvalidArgument(f"top_p must be in [0.0, 1.0], got {top_p}", 0)
+        if repetition_penalty < 1.0:
+            raise InvalidArgument(f"repetition_penalty must be >= 1.0, got {repetition_penalty}", 0)
+        return cls(max_new_tokens, temperature, top_k, top_p, repetition_penalty)
+
+    def sampling(self, seed: int) -> SamplingC:
+        return SamplingC(self.temperature, self.top_k, self.top_p, self.repetition_penalty, seed & (2**64 - 1))
+
+
+def sample_device(ctx: Context, logits: "DeviceBuffer", vocab: int, config: GenerationConfig, seed: int = 0,
+                  step: int = 0, counts: Optional["DeviceBuffer"] = None) -> int:
+    """sample_with_config (src/generate.rs:670-693) on device logits with the
+    library's sampling rule; counts: device uint32 [vocab] of the tokens
+    generated so far (repetition penalty)."""
+    tok = DeviceBuffer(ctx, 4)
+    try:
+        sc = config.sampling(seed)
+        _check(lib().lq8_sample_device(ctx.handle, logits.ptr, vocab, counts.ptr if counts is not None else None,
+                                       C.byref(sc), step, tok.ptr))
+        return int(tok.download(np.uint32, 1)[0])
+    finally:
+        tok.free()
 
 
 # ---- Qwen3-MoE decoder layers --------------------------------------------------
