@@ -11,10 +11,11 @@ generator, quantized to Q8_0 on the device.
 The headline value runs the step as one grouped launch (the 197 GEMVs are
 independent, so one kernel streams them back to back); the same step with one
 launch per GEMV replayed from a HIP graph, the lm_head alone, the single
-3072x1024 GEMV, the M = 512 W8A8 MFMA GEMM, and batch-1 greedy decode of the
-random-init Q8_0 Qwen3-0.6B (128-token prompt, 128 new tokens) are reported
-beside it.  The CPU oracle's GEMV, single-threaded over a bounded sample of the
-same workload, is the CPU baseline.
+3072x1024 GEMV, the M = 512 W8A8 MFMA GEMM, and batch-1 decode of the
+random-init Q8_0 Qwen3-0.6B (128-token prompt, 128 new tokens; greedy, and
+sampled with temperature 0.8, top-k 50, top-p 0.95, repetition penalty 1.1)
+are reported beside it.  The CPU oracle's GEMV, single-threaded over a
+bounded sample of the same workload, is the CPU baseline.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -265,9 +266,18 @@ def main():
         model.generate_greedy(prompt, 8)
         runs = [model.generate_greedy(prompt, 128)[1] for _ in range(3)]
         tps = sorted(r["decode_tokens_per_s"] for r in runs)[1]
+        # sampled decode: penalty, temperature, top-k and top-p on the device
+        gc = lq8.GenerationConfig(128, 0.8, 50, 0.95, 1.1)
+        model.generate(prompt, gc, seed=1)
+        sruns = [model.generate(prompt, gc, seed=1 + i)[1] for i in range(3)]
+        stps = sorted(r["decode_tokens_per_s"] for r in sruns)[1]
         decode = {"tokens_per_s": round(tps, 1), "prefill_ms": round(runs[0]["prefill_ms"], 2),
-                  "graph": runs[0]["used_graph"], "prompt": 128, "new_tokens": 128}
-        log(f"decode: {tps:.1f} tok/s (median of 3), prefill {runs[0]['prefill_ms']:.2f} ms")
+                  "graph": runs[0]["used_graph"], "prompt": 128, "new_tokens": 128,
+                  "sampled_tokens_per_s": round(stps, 1),
+                  "sampled_config": {"temperature": 0.8, "top_k": 50, "top_p": 0.95, "repetition_penalty": 1.1},
+                  "sampler_us_over_greedy": round(1e6 / stps - 1e6 / tps, 1)}
+        log(f"decode: {tps:.1f} tok/s (median of 3), prefill {runs[0]['prefill_ms']:.2f} ms; "
+            f"sampled {stps:.1f} tok/s ({1e6 / stps - 1e6 / tps:.1f} us/token over greedy)")
         model.free()
 
     moe = None if args.no_moe else moe_stack(ctx)

@@ -823,9 +823,12 @@ done:
  * stubs, src/generate.rs:191-329) ------------------------------------------
  * penalty per earlier occurrence (src/generate.rs:353-380), T = 0 greedy
  * (last index on ties), else z = x / T, order by z descending (lower index
- * first on ties), top_k, e = exp(z - z0), chunked prefix sums (chunks of 64:
- * totals sequential, then sequential over the chunks), nucleus end = first
- * C >= top_p * S, u from SplitMix64(seed + step * golden), first C > u * C_end. */
+ * first on ties), top_k, integer weights w = floor(2^32 * exp(z - z0)) (0 for
+ * NaN), prefix sums C exact in 64 bits, nucleus end = first C >= thr with
+ * thr = ceil(S * floor(top_p * 2^24) / 2^24), u24 = SplitMix64(seed + step *
+ * golden) >> 40, r = floor(C_end * u24 / 2^24), token = first C > r (the
+ * first entry when C_end = 0).  Sorting: qsort of distinct 64-bit keys
+ * (value bits above the index or its complement), sums sequential. */
 static uint32_t orc_order_bits(float z) {
     uint32_t b;
     memcpy(&b, &z, 4);
@@ -847,6 +850,11 @@ static uint64_t orc_splitmix64(uint64_t z) {
     z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
     return z ^ (z >> 31);
 }
+static uint64_t orc_weight(float z, float z0) {
+    const float e = orc_expf(z - z0);
+    if (!(e > 0.0f)) return 0;
+    return (uint64_t)fminf(e * 4294967296.0f, 4294967296.0f);
+}
 
 int64_t orc_sample(const float* logits, size_t V, const uint32_t* counts, float T, uint32_t top_k, float top_p,
                    float penalty, uint64_t seed, uint32_t step) {
@@ -865,71 +873,46 @@ int64_t orc_sample(const float* logits, size_t V, const uint32_t* counts, float 
         keys[i] = ((uint64_t)orc_order_bits(z) << 32) | lo;
     }
     qsort(keys, V, sizeof(uint64_t), orc_cmp_desc_u64);
-    int64_t token;
     if (!(T > 0.0f)) {
-        token = (uint32_t)keys[0];
+        const int64_t token = (uint32_t)keys[0];
         free(keys);
         return token;
     }
-    const size_t K = top_k > 0 && top_k < V ? top_k : V, nch = (K + 63) / 64;
+    const size_t K = top_k > 0 && top_k < V ? top_k : V;
     const float z0 = orc_from_order((uint32_t)(keys[0] >> 32));
-    float* tot = (float*)malloc(nch * sizeof(float));
-    if (!tot) {
+    uint64_t* C = (uint64_t*)malloc(K * sizeof(uint64_t));
+    if (!C) {
         free(keys);
         return -1;
     }
-    for (size_t c = 0; c < nch; c++) {
-        float t = 0.0f;
-        for (size_t j = c * 64; j < c * 64 + 64 && j < K; j++) t = t + orc_expf(orc_from_order((uint32_t)(keys[j] >> 32)) - z0);
-        tot[c] = t;
+    uint64_t acc = 0;
+    for (size_t j = 0; j < K; j++) {
+        acc += orc_weight(orc_from_order((uint32_t)(keys[j] >> 32)), z0);
+        C[j] = acc;
     }
-    float S = 0.0f;
-    for (size_t c = 0; c < nch; c++) S = S + tot[c];
-    size_t end = K - 1;
-    float Cend = S;
+    const uint64_t S = C[K - 1];
+    uint64_t c_end = S;
     if (top_p < 1.0f) {
-        const float thr = top_p * S;
-        float P = 0.0f;
-        size_t c = 0;
-        while (c + 1 < nch && !(P + tot[c] >= thr)) {
-            P = P + tot[c];
-            c++;
-        }
-        const size_t jl = (c * 64 + 64 < K ? c * 64 + 64 : K) - 1;
-        float I = 0.0f;
-        int64_t found = -1;
-        for (size_t j = c * 64; j <= jl; j++) {
-            I = I + orc_expf(orc_from_order((uint32_t)(keys[j] >> 32)) - z0);
-            Cend = P + I;
-            if (Cend >= thr) {
-                found = (int64_t)j;
+        const uint64_t p24 = (uint64_t)(top_p * 16777216.0f);
+        const unsigned __int128 prod = (unsigned __int128)S * p24;
+        const uint64_t thr = (uint64_t)(prod >> 24) + ((prod & 0xFFFFFFu) ? 1u : 0u);
+        for (size_t j = 0; j < K; j++)
+            if (C[j] >= thr) {
+                c_end = C[j];
                 break;
             }
-        }
-        end = found >= 0 ? (size_t)found : jl;
     }
-    const uint64_t h = orc_splitmix64(seed + (uint64_t)step * 0x9E3779B97F4A7C15ull);
-    const float u = (float)(uint32_t)(h >> 40) * 5.9604644775390625e-8f;
-    const float r = u * Cend;
-    const size_t ce = end / 64;
-    float P = 0.0f;
-    size_t c = 0;
-    while (c < ce && !(P + tot[c] > r)) {
-        P = P + tot[c];
-        c++;
-    }
-    const size_t jl = c < ce ? c * 64 + 63 : end;
-    float I = 0.0f;
-    int64_t found = -1;
-    for (size_t j = c * 64; j <= jl; j++) {
-        I = I + orc_expf(orc_from_order((uint32_t)(keys[j] >> 32)) - z0);
-        if (P + I > r) {
-            found = (int64_t)j;
-            break;
-        }
-    }
-    token = ~(uint32_t)keys[found >= 0 ? (size_t)found : end];
-    free(tot);
+    const uint64_t u24 = orc_splitmix64(seed + (uint64_t)step * 0x9E3779B97F4A7C15ull) >> 40;
+    const uint64_t r = (uint64_t)(((unsigned __int128)c_end * u24) >> 24);
+    size_t pick = 0;
+    if (c_end > 0)
+        for (size_t j = 0; j < K; j++)
+            if (C[j] > r) {
+                pick = j;
+                break;
+            }
+    const int64_t token = ~(uint32_t)keys[pick];
+    free(C);
     free(keys);
     return token;
 }

@@ -9,22 +9,23 @@
 //   T = 0: greedy -- the largest x_i, the last index on ties (sample_greedy)
 //   T > 0: z_i = x_i / T; entries ordered by z descending, ties by index
 //          ascending (the reference's stable sort); the first K = top_k are
-//          kept (all when top_k = 0); e_j = exp(z_j - z_0);
-//          prefix sums over the kept entries in chunks of 64: chunk totals
-//          t_c sequential from 0, P_c = t_0 + ... + t_{c-1} sequential from 0,
-//          C_j = P_c + (entries of j's chunk up to j, sequential from 0);
-//          S = C_{K-1}; the nucleus ends at the first j with
-//          C_j >= top_p * S (at K - 1 when top_p >= 1);
-//          u = (SplitMix64(seed + step * 0x9E3779B97F4A7C15) >> 40) * 2^-24,
-//          r = u * C_end; the token is the first j <= end with C_j > r (end
-//          when rounding leaves none).
+//          kept (all when top_k = 0); integer weights
+//          w_j = floor(2^32 * exp(z_j - z_0)) (0 for NaN), so every sum below
+//          is exact in 64 bits and independent of summation order;
+//          C_j = w_0 + ... + w_j, S = C_{K-1};
+//          top_p < 1: p24 = floor(top_p * 2^24), thr = ceil(S * p24 / 2^24),
+//          the nucleus ends at the first j with C_j >= thr (K - 1 otherwise);
+//          u24 = SplitMix64(seed + step * 0x9E3779B97F4A7C15) >> 40,
+//          r = floor(C_end * u24 / 2^24) < C_end; the token is the first j
+//          with C_j > r (the first entry when C_end = 0).
 // The order comes from a stable LSD radix sort (4 passes of 8 bits) of the
 // 32-bit keys ~order_bits(z) (ascending key = descending z) with the token
 // index as payload, fed in index order when T > 0 (ties: first index first)
-// and in reverse index order when T = 0 (ties: last index first).  Every
-// pass is a per-tile digit histogram and a scatter that sums the histogram
-// columns itself: no atomics in global memory and nothing to clear between
-// calls, so the whole sampler can be replayed from a captured graph.
+// and in reverse index order when T = 0 (ties: last index first).  Each pass
+// is a per-tile digit count and a scatter in which every tile sums its digit's
+// row of counts itself: no tile waits on another, no global atomics, and
+// nothing is cleared by a memset between calls, so the whole sampler replays
+// from a captured graph.
 #include "lq8_internal.h"
 #include "lq8_numerics.h"
 
@@ -32,8 +33,9 @@ namespace lq8 {
 
 namespace {
 
-constexpr int CHUNK = 64;
 constexpr int SORT_THREADS = 256, SORT_IPT = 8, SORT_TILE = SORT_THREADS * SORT_IPT, RADIX = 256;
+constexpr int PICK_THREADS = 1024, PICK_MAX_TILES = PICK_THREADS;  // vocab <= 2^21
+constexpr int MAX_VOCAB = PICK_MAX_TILES * SORT_TILE;
 
 __device__ __forceinline__ uint32_t order_bits(float z) {
     const uint32_t b = __float_as_uint(z);
@@ -54,6 +56,15 @@ __device__ __forceinline__ float penalized(float x, uint32_t count, float p) {
     return x;
 }
 
+// floor(2^32 * exp(z - z0)); z <= z0 unless NaN, so the weight is <= 2^32.
+__device__ __forceinline__ unsigned long long weight_of(float z, float z0) {
+    const float e = expf_cr(z - z0);
+    if (!(e > 0.0f)) return 0ull;
+    return (unsigned long long)fminf(e * 4294967296.0f, 4294967296.0f);
+}
+
+__device__ __forceinline__ int kept(const SampleCfg* cfg, int V) { return cfg->top_k > 0 ? min(cfg->top_k, V) : V; }
+
 // Sort input position p (< V): its token index and key.
 __device__ __forceinline__ uint32_t input_key(const float* __restrict__ logits, const uint32_t* __restrict__ counts,
                                               const SampleCfg* cfg, int V, int p, uint32_t* idx) {
@@ -71,6 +82,8 @@ struct SortIn {
     const uint32_t* keys;  // pass > 0
     const uint32_t* idx;   // pass > 0
     int V;
+    int nb;                // tiles
+    int row;               // stride of a digit's row of tile counts (nb rounded up to 4)
 };
 
 template <int PASS>
@@ -90,53 +103,86 @@ __device__ __forceinline__ void load_tile(const SortIn& in, int b, uint32_t (&k)
     }
 }
 
-// Digit counts of tile b -> hist[b][256].
+// Lanes of the wave holding the same digit d (among the valid lanes).
+__device__ __forceinline__ unsigned long long same_digit_lanes(uint32_t d, bool valid) {
+    unsigned long long m = __ballot(valid);
+#pragma unroll
+    for (int bit = 0; bit < 8; bit++) {
+        const bool on = (d >> bit) & 1u;
+        const unsigned long long bb = __ballot(on);
+        m &= on ? bb : ~bb;
+    }
+    return m;
+}
+__device__ __forceinline__ uint32_t lanes_below(unsigned long long m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Digit counts of tile b for pass PASS -> count plane PASS (a row of tile
+// counts per digit; the row padding zeroed).  One LDS add per distinct digit
+// of a wave: float keys concentrate on few values of their upper bytes.
 template <int PASS>
-__global__ __launch_bounds__(SORT_THREADS) void k_sort_hist(SortIn in, uint32_t* __restrict__ hist) {
+__global__ __launch_bounds__(SORT_THREADS) void k_sort_hist(SortIn in, uint32_t* __restrict__ planes) {
     __shared__ uint32_t cnt[RADIX];
     const int t = threadIdx.x, b = blockIdx.x;
     cnt[t] = 0;
+    uint32_t* plane = planes + (size_t)PASS * RADIX * in.row;
+    if (b == 0)
+        for (int q = in.nb; q < in.row; q++) plane[(size_t)t * in.row + q] = 0u;
     uint32_t k[SORT_IPT], ix[SORT_IPT];
     load_tile<PASS>(in, b, k, ix);
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < SORT_IPT; j++)
-        if (b * SORT_TILE + j * SORT_THREADS + t < in.V) atomicAdd(&cnt[(k[j] >> (8 * PASS)) & 255u], 1u);
+    for (int j = 0; j < SORT_IPT; j++) {
+        const bool valid = b * SORT_TILE + j * SORT_THREADS + t < in.V;
+        const uint32_t d = (k[j] >> (8 * PASS)) & 255u;
+        const unsigned long long m = same_digit_lanes(d, valid);
+        if (valid && lanes_below(m) == 0) atomicAdd(&cnt[d], (uint32_t)__popcll(m));
+    }
     __syncthreads();
-    hist[(size_t)b * RADIX + t] = cnt[t];
+    plane[(size_t)t * in.row + b] = cnt[t];
 }
 
 // Stable scatter of tile b: rank = keys of smaller digits everywhere + keys of
 // this digit in earlier tiles + earlier keys of this digit in this tile
 // (rounds of 256 in tile order; within a round, lane order from ballots).
+// One barrier per round: the per-wave counts rotate over three buffers and
+// the running digit bases over two, so a buffer is cleared or rewritten only
+// after a barrier that follows its last reader.
 template <int PASS>
-__global__ __launch_bounds__(SORT_THREADS) void k_sort_scatter(SortIn in, int nb, const uint32_t* __restrict__ hist,
+__global__ __launch_bounds__(SORT_THREADS) void k_sort_scatter(SortIn in, const uint32_t* __restrict__ planes,
                                                               uint32_t* __restrict__ keys_out,
                                                               uint32_t* __restrict__ idx_out) {
-    __shared__ uint32_t base[RADIX];
-    __shared__ uint32_t wcnt[SORT_THREADS / 64][RADIX];
-    __shared__ uint32_t wtot[SORT_THREADS / 64];
+    constexpr int W = SORT_THREADS / 64;
+    __shared__ uint32_t base[2][RADIX];
+    __shared__ uint32_t wcnt[3][W][RADIX];
+    __shared__ uint32_t wtot[W];
     const int t = threadIdx.x, b = blockIdx.x, w = t >> 6, lane = t & 63;
     uint32_t k[SORT_IPT], ix[SORT_IPT];
     load_tile<PASS>(in, b, k, ix);
-    // digit t: count over all tiles and over the tiles before b
+    // digit t: count over all tiles and over the tiles before b (one row)
+    const uint4* rowp = (const uint4*)(planes + (size_t)PASS * RADIX * in.row + (size_t)t * in.row);
     uint32_t tot = 0, pre = 0;
     {
-        int bb = 0;
-        for (; bb + 8 <= nb; bb += 8) {
-            uint32_t h[8];
+        const int n4 = in.row >> 2;
+        int q = 0;
+        for (; q + 8 <= n4; q += 8) {
+            uint4 h[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) h[u] = hist[(size_t)(bb + u) * RADIX + t];
+            for (int u = 0; u < 8; u++) h[u] = rowp[q + u];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
-                tot += h[u];
-                pre += bb + u < b ? h[u] : 0u;
+                const int b0 = 4 * (q + u);
+                tot += h[u].x + h[u].y + h[u].z + h[u].w;
+                pre += (b0 < b ? h[u].x : 0u) + (b0 + 1 < b ? h[u].y : 0u) + (b0 + 2 < b ? h[u].z : 0u) +
+                       (b0 + 3 < b ? h[u].w : 0u);
             }
         }
-        for (; bb < nb; bb++) {
-            const uint32_t h = hist[(size_t)bb * RADIX + t];
-            tot += h;
-            pre += bb < b ? h : 0u;
+        for (; q < n4; q++) {
+            const uint4 h = rowp[q];
+            const int b0 = 4 * q;
+            tot += h.x + h.y + h.z + h.w;
+            pre += (b0 < b ? h.x : 0u) + (b0 + 1 < b ? h.y : 0u) + (b0 + 2 < b ? h.z : 0u) + (b0 + 3 < b ? h.w : 0u);
         }
     }
     // exclusive scan of the digit totals over the block
@@ -148,60 +194,69 @@ __global__ __launch_bounds__(SORT_THREADS) void k_sort_scatter(SortIn in, int nb
     }
     if (lane == 63) wtot[w] = inc;
 #pragma unroll
-    for (int q = 0; q < SORT_THREADS / 64; q++) wcnt[q][t] = 0;
+    for (int r = 0; r < 3; r++)
+#pragma unroll
+        for (int q = 0; q < W; q++) wcnt[r][q][t] = 0;
     __syncthreads();
     uint32_t excl = inc - tot;
     for (int q = 0; q < w; q++) excl += wtot[q];
-    base[t] = excl + pre;
-    __syncthreads();
+    base[0][t] = excl + pre;
 #pragma unroll
     for (int j = 0; j < SORT_IPT; j++) {
+        const int cur = j % 3, nb2 = j & 1;
         const bool valid = b * SORT_TILE + j * SORT_THREADS + t < in.V;
         const uint32_t d = (k[j] >> (8 * PASS)) & 255u;
-        unsigned long long m = __ballot(valid);
-#pragma unroll
-        for (int bit = 0; bit < 8; bit++) {
-            const bool on = (d >> bit) & 1u;
-            const unsigned long long bb = __ballot(on);
-            m &= on ? bb : ~bb;
-        }
-        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-        if (valid && rank == 0) wcnt[w][d] = (uint32_t)__popcll(m);
+        const unsigned long long m = same_digit_lanes(d, valid);
+        const uint32_t rank = lanes_below(m);
+        if (valid && rank == 0) wcnt[cur][w][d] = (uint32_t)__popcll(m);
         __syncthreads();
+        // buffer of round j - 1: read before this barrier, written next in round j + 2
+#pragma unroll
+        for (int q = 0; q < W; q++) wcnt[(j + 2) % 3][q][t] = 0;
         if (valid) {
-            uint32_t pos = base[d] + rank;
-            for (int q = 0; q < w; q++) pos += wcnt[q][d];
+            uint32_t pos = base[nb2][d] + rank;
+            for (int q = 0; q < w; q++) pos += wcnt[cur][q][d];
             if (pos < (uint32_t)in.V) {
                 keys_out[pos] = k[j];
                 idx_out[pos] = ix[j];
             }
         }
-        __syncthreads();
         uint32_t add = 0;
 #pragma unroll
-        for (int q = 0; q < SORT_THREADS / 64; q++) {
-            add += wcnt[q][t];
-            wcnt[q][t] = 0;
-        }
-        base[t] += add;
-        __syncthreads();
+        for (int q = 0; q < W; q++) add += wcnt[cur][q][t];
+        base[nb2 ^ 1][t] = base[nb2][t] + add;
     }
 }
 
-__device__ __forceinline__ int kept(const SampleCfg* cfg, int V) { return cfg->top_k > 0 ? min(cfg->top_k, V) : V; }
+// Exact 64-bit sum over the block (any order).
+__device__ __forceinline__ unsigned long long block_sum_u64(unsigned long long v, unsigned long long* red) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    unsigned long long s = 0;
+    for (int q = 0; q < (int)(blockDim.x >> 6); q++) s += red[q];
+    return s;
+}
 
-// One thread per chunk of 64 kept entries: t_c.
-__global__ __launch_bounds__(256) void k_sample_chunks(const uint32_t* __restrict__ sorted, int V,
-                                                       const SampleCfg* cfg, float* __restrict__ tot) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
+// Weight sum of each tile of the sorted kept entries.
+__global__ __launch_bounds__(SORT_THREADS) void k_sample_weights(const uint32_t* __restrict__ sorted, int V,
+                                                                const SampleCfg* cfg,
+                                                                unsigned long long* __restrict__ part) {
+    __shared__ unsigned long long red[SORT_THREADS / 64];
     if (cfg->temperature <= 0.0f) return;
-    const int K = kept(cfg, V);
-    if (c * CHUNK >= K) return;
+    const int K = kept(cfg, V), b = blockIdx.x;
+    if (b * SORT_TILE >= K) return;
     const float z0 = key_value(sorted[0]);
-    const int j1 = min(c * CHUNK + CHUNK, K);
-    float t = 0.0f;
-    for (int j = c * CHUNK; j < j1; j++) t = t + expf_cr(key_value(sorted[j]) - z0);
-    tot[c] = t;
+    unsigned long long s = 0;
+#pragma unroll
+    for (int j = 0; j < SORT_IPT; j++) {
+        const int p = b * SORT_TILE + j * SORT_THREADS + (int)threadIdx.x;
+        if (p < K) s += weight_of(key_value(sorted[p]), z0);
+    }
+    s = block_sum_u64(s, red);
+    if (threadIdx.x == 0) part[b] = s;
 }
 
 __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
@@ -211,65 +266,105 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
     return z ^ (z >> 31);
 }
 
-// First j in chunk c (entries up to jlast) with P + C_j-in-chunk passing the
-// test (>= thr when ge, > thr otherwise); -1 when none.  *cj: that C_j.
-__device__ int chunk_search(const uint32_t* sorted, float z0, int c, int jlast, float P, float thr, bool ge,
-                            float* cj) {
-    float I = 0.0f;
-    for (int j = c * CHUNK; j <= jlast; j++) {
-        I = I + expf_cr(key_value(sorted[j]) - z0);
-        const float C = P + I;
-        if (ge ? C >= thr : C > thr) {
-            *cj = C;
-            return j;
-        }
-        *cj = C;
-    }
-    return -1;
+// floor (or ceil) of a * b / 2^24 for a < 2^63, b <= 2^24 (exact).
+__device__ __forceinline__ unsigned long long mul_shr24(unsigned long long a, unsigned long long b, bool round_up) {
+    const unsigned long long lo = a * b, hi = __umul64hi(a, b);
+    unsigned long long q = (hi << 40) | (lo >> 24);
+    if (round_up && (lo & 0xFFFFFFull)) q++;
+    return q;
 }
 
-// The pick (one thread): the token, then the step bookkeeping.
-__global__ void k_sample_pick(const uint32_t* __restrict__ sorted, const uint32_t* __restrict__ sidx, int V,
-                              const float* __restrict__ tot,
-                              const SampleCfg* cfg, int* d_step, uint32_t* d_tok, uint32_t* tokens_out, int* d_pos,
-                              uint32_t* counts_out) {
-    if (threadIdx.x != 0) return;
+// Inclusive scan over the threads of the pick block (exact).
+__device__ __forceinline__ unsigned long long block_scan_u64(unsigned long long v, unsigned long long* wsum) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const unsigned long long o = __shfl_up(v, d, 64);
+        if (lane >= d) v += o;
+    }
+    __syncthreads();
+    if (lane == 63) wsum[w] = v;
+    __syncthreads();
+    for (int q = 0; q < w; q++) v += wsum[q];
+    return v;
+}
+
+struct PickShared {
+    unsigned long long pre[PICK_MAX_TILES];  // inclusive prefix of the tile weights
+    unsigned long long wsum[PICK_THREADS / 64];
+    unsigned long long c_hit;
+    uint32_t first_tile, first_j;
+};
+
+// The first tile whose inclusive prefix passes the test (>= thr when ge,
+// > thr otherwise); nt when none.
+__device__ int first_tile(PickShared& sh, int nt, unsigned long long thr, bool ge) {
+    const int t = threadIdx.x;
+    __syncthreads();
+    if (t == 0) sh.first_tile = (uint32_t)nt;
+    __syncthreads();
+    if (t < nt && (ge ? sh.pre[t] >= thr : sh.pre[t] > thr)) atomicMin(&sh.first_tile, (uint32_t)t);
+    __syncthreads();
+    return (int)sh.first_tile;
+}
+
+// In tile tb (< nt): the first kept j with C_j passing the test, its C_j ->
+// sh.c_hit; -1 when none.
+__device__ int first_in_tile(PickShared& sh, const uint32_t* sorted, float z0, int K, int tb, unsigned long long thr,
+                             bool ge) {
+    const int t = threadIdx.x;
+    const int p0 = tb * SORT_TILE + 2 * t;
+    const unsigned long long w0 = p0 < K ? weight_of(key_value(sorted[p0]), z0) : 0ull;
+    const unsigned long long w1 = p0 + 1 < K ? weight_of(key_value(sorted[p0 + 1]), z0) : 0ull;
+    const unsigned long long before = tb > 0 ? sh.pre[tb - 1] : 0ull;
+    const unsigned long long inc = block_scan_u64(w0 + w1, sh.wsum);
+    const unsigned long long c0 = before + (inc - w1), c1 = before + inc;
+    if (t == 0) sh.first_j = 0xFFFFFFFFu;
+    __syncthreads();
+    const bool h0 = p0 < K && (ge ? c0 >= thr : c0 > thr), h1 = p0 + 1 < K && (ge ? c1 >= thr : c1 > thr);
+    if (h0 || h1) atomicMin(&sh.first_j, (uint32_t)(h0 ? p0 : p0 + 1));
+    __syncthreads();
+    const uint32_t j = sh.first_j;
+    if (j == (uint32_t)p0) sh.c_hit = c0;
+    if (j == (uint32_t)p0 + 1) sh.c_hit = c1;
+    __syncthreads();
+    return j == 0xFFFFFFFFu ? -1 : (int)j;
+}
+
+// The pick (one block): the token, then the step bookkeeping.
+__global__ __launch_bounds__(PICK_THREADS) void k_sample_pick(const uint32_t* __restrict__ sorted,
+                                                              const uint32_t* __restrict__ sidx, int V,
+                                                              const unsigned long long* __restrict__ part,
+                                                              const SampleCfg* cfg, int* d_step, uint32_t* d_tok,
+                                                              uint32_t* tokens_out, int* d_pos, uint32_t* counts_out) {
+    __shared__ PickShared sh;
+    const int t = threadIdx.x;
     const int step = *d_step;
-    uint32_t token;
-    if (cfg->temperature <= 0.0f) {
-        token = sidx[0];
-    } else {
-        const int K = kept(cfg, V), nch = (K + CHUNK - 1) / CHUNK;
+    uint32_t token = sidx[0];
+    if (cfg->temperature > 0.0f) {
+        const int K = kept(cfg, V), nt = (K + SORT_TILE - 1) / SORT_TILE;
         const float z0 = key_value(sorted[0]);
-        float S = 0.0f;
-        for (int c = 0; c < nch; c++) S = S + tot[c];
-        int end = K - 1;
-        float Cend = S;
+        sh.pre[t] = block_scan_u64(t < nt ? part[t] : 0ull, sh.wsum);
+        __syncthreads();
+        const unsigned long long S = sh.pre[nt - 1];
+        unsigned long long c_end = S;
         if (cfg->top_p < 1.0f) {
-            const float thr = cfg->top_p * S;
-            float P = 0.0f;
-            int c = 0;
-            while (c < nch - 1 && !(P + tot[c] >= thr)) {
-                P = P + tot[c];
-                c++;
-            }
-            const int j = chunk_search(sorted, z0, c, min(c * CHUNK + CHUNK, K) - 1, P, thr, true, &Cend);
-            end = j >= 0 ? j : min(c * CHUNK + CHUNK, K) - 1;
+            const unsigned long long p24 = (unsigned long long)(cfg->top_p * 16777216.0f);
+            const unsigned long long thr = mul_shr24(S, p24, true);
+            const int tb = first_tile(sh, nt, thr, true);
+            if (tb < nt && first_in_tile(sh, sorted, z0, K, tb, thr, true) >= 0) c_end = sh.c_hit;
         }
         const uint64_t h = splitmix64(cfg->seed + (uint64_t)(uint32_t)step * 0x9E3779B97F4A7C15ull);
-        const float u = (float)(uint32_t)(h >> 40) * 5.9604644775390625e-8f;  // 2^-24
-        const float r = u * Cend;
-        const int ce = end / CHUNK;
-        float P = 0.0f;
-        int c = 0;
-        while (c < ce && !(P + tot[c] > r)) {
-            P = P + tot[c];
-            c++;
+        const unsigned long long r = mul_shr24(c_end, h >> 40, false);
+        if (c_end > 0) {
+            const int tb = first_tile(sh, nt, r, false);
+            if (tb < nt) {
+                const int j = first_in_tile(sh, sorted, z0, K, tb, r, false);
+                if (j >= 0) token = sidx[j];
+            }
         }
-        float cj;
-        const int j = chunk_search(sorted, z0, c, c < ce ? c * CHUNK + CHUNK - 1 : end, P, r, false, &cj);
-        token = sidx[j >= 0 ? j : end];
     }
+    if (t != 0) return;
     *d_tok = token;
     if (tokens_out) tokens_out[step] = token;
     *d_step = step + 1;
@@ -277,38 +372,36 @@ __global__ void k_sample_pick(const uint32_t* __restrict__ sorted, const uint32_
     if (counts_out) counts_out[token] = counts_out[token] + 1u;
 }
 
-inline unsigned grid256(size_t n) { return (unsigned)((n + 255) / 256); }
 inline size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct SampleWork {
-    uint32_t *ka, *kb, *ia, *ib, *hist;
-    float* tot;
+    uint32_t *ka, *kb, *ia, *ib, *planes;
+    unsigned long long* part;
 };
 
 int sort_tiles(int vocab) { return (vocab + SORT_TILE - 1) / SORT_TILE; }
+int row_stride(int vocab) { return (sort_tiles(vocab) + 3) & ~3; }
 
-size_t sample_chunk_count(int vocab) { return (size_t)(vocab + CHUNK - 1) / CHUNK; }
-
-// ka | kb | ia | ib ([vocab] each) | hist [tiles][256] | chunk totals
+// ka | kb | ia | ib ([vocab] each) | count planes [4][256][row] | tile weights
 size_t work_layout(int vocab, void* base, SampleWork* w) {
-    const size_t v = up256((size_t)vocab * 4), h = up256((size_t)sort_tiles(vocab) * RADIX * 4);
+    const size_t v = up256((size_t)vocab * 4), h = up256((size_t)4 * RADIX * row_stride(vocab) * 4);
     char* p = (char*)base;
     if (w) {
         w->ka = (uint32_t*)p;
         w->kb = (uint32_t*)(p + v);
         w->ia = (uint32_t*)(p + 2 * v);
         w->ib = (uint32_t*)(p + 3 * v);
-        w->hist = (uint32_t*)(p + 4 * v);
-        w->tot = (float*)(p + 4 * v + h);
+        w->planes = (uint32_t*)(p + 4 * v);
+        w->part = (unsigned long long*)(p + 4 * v + h);
     }
-    return 4 * v + h + up256(sample_chunk_count(vocab) * 4);
+    return 4 * v + h + up256((size_t)sort_tiles(vocab) * 8);
 }
 
 template <int PASS>
-lq8_status sort_pass(hipStream_t s, SortIn in, int nb, uint32_t* hist, uint32_t* keys_out, uint32_t* idx_out) {
-    hipLaunchKernelGGL(k_sort_hist<PASS>, dim3(nb), dim3(SORT_THREADS), 0, s, in, hist);
+lq8_status sort_pass(hipStream_t s, SortIn in, uint32_t* planes, uint32_t* keys_out, uint32_t* idx_out) {
+    hipLaunchKernelGGL(k_sort_hist<PASS>, dim3(in.nb), dim3(SORT_THREADS), 0, s, in, planes);
     LQ8_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_sort_scatter<PASS>, dim3(nb), dim3(SORT_THREADS), 0, s, in, nb, (const uint32_t*)hist,
+    hipLaunchKernelGGL(k_sort_scatter<PASS>, dim3(in.nb), dim3(SORT_THREADS), 0, s, in, (const uint32_t*)planes,
                        keys_out, idx_out);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
@@ -319,35 +412,31 @@ lq8_status sort_pass(hipStream_t s, SortIn in, int nb, uint32_t* hist, uint32_t*
 size_t sample_work_bytes(int vocab) { return work_layout(vocab, nullptr, nullptr); }
 
 lq8_status launch_sample(hipStream_t s, const SampleLaunch& a) {
-    if (a.vocab <= 0) return fail(LQ8_ERR_INVALID_ARG, "sample: empty vocabulary");
+    if (a.vocab <= 0 || a.vocab > MAX_VOCAB) return fail(LQ8_ERR_INVALID_ARG, "sample: vocabulary outside 1 .. 2^21");
     if (!a.work) return fail(LQ8_ERR_INVALID_ARG, "sample: no workspace");
     SampleWork w;
     work_layout(a.vocab, a.work, &w);
-    const int nb = sort_tiles(a.vocab);
-    SortIn in{a.logits, a.counts, a.cfg, nullptr, nullptr, a.vocab};
+    SortIn in{a.logits, a.counts, a.cfg, nullptr, nullptr, a.vocab, sort_tiles(a.vocab), row_stride(a.vocab)};
     lq8_status st;
-    if ((st = sort_pass<0>(s, in, nb, w.hist, w.ka, w.ia))) return st;
+    if ((st = sort_pass<0>(s, in, w.planes, w.ka, w.ia))) return st;
     in.keys = w.ka;
     in.idx = w.ia;
-    if ((st = sort_pass<1>(s, in, nb, w.hist, w.kb, w.ib))) return st;
+    if ((st = sort_pass<1>(s, in, w.planes, w.kb, w.ib))) return st;
     in.keys = w.kb;
     in.idx = w.ib;
-    if ((st = sort_pass<2>(s, in, nb, w.hist, w.ka, w.ia))) return st;
+    if ((st = sort_pass<2>(s, in, w.planes, w.ka, w.ia))) return st;
     in.keys = w.ka;
     in.idx = w.ia;
-    if ((st = sort_pass<3>(s, in, nb, w.hist, w.kb, w.ib))) return st;
-    hipLaunchKernelGGL(k_sample_chunks, dim3(grid256(sample_chunk_count(a.vocab))), dim3(256), 0, s,
-                       (const uint32_t*)w.kb, a.vocab, a.cfg, w.tot);
+    if ((st = sort_pass<3>(s, in, w.planes, w.kb, w.ib))) return st;
+    hipLaunchKernelGGL(k_sample_weights, dim3(in.nb), dim3(SORT_THREADS), 0, s, (const uint32_t*)w.kb, a.vocab, a.cfg,
+                       w.part);
     LQ8_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_sample_pick, dim3(1), dim3(64), 0, s, (const uint32_t*)w.kb, (const uint32_t*)w.ib, a.vocab,
-                       (const float*)w.tot, a.cfg, a.d_step, a.d_tok, a.tokens_out, a.d_pos, a.counts_out);
+    hipLaunchKernelGGL(k_sample_pick, dim3(1), dim3(PICK_THREADS), 0, s, (const uint32_t*)w.kb, (const uint32_t*)w.ib,
+                       a.vocab, (const unsigned long long*)w.part, a.cfg, a.d_step, a.d_tok, a.tokens_out, a.d_pos,
+                       a.counts_out);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
-
-}  // namespace lq8
-
-namespace lq8 {
 
 lq8_status check_sampling(const lq8_sampling* c, SampleCfg* out) {
     if (!c) return fail(LQ8_ERR_INVALID_ARG, "sampling config is null");
@@ -364,6 +453,8 @@ lq8_status check_sampling(const lq8_sampling* c, SampleCfg* out) {
     return LQ8_OK;
 }
 
+bool sample_vocab_ok(size_t vocab) { return vocab >= 1 && vocab <= (size_t)MAX_VOCAB; }
+
 }  // namespace lq8
 
 using namespace lq8;
@@ -372,7 +463,7 @@ extern "C" lq8_status lq8_sample_device(lq8_ctx* ctx, const float* d_logits, siz
                                         const lq8_sampling* cfg, uint32_t step, uint32_t* d_token) {
     if (!registry_has(ctx)) return fail(LQ8_ERR_INVALID_ARG, "invalid or released context handle");
     if (!d_logits || !d_token) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
-    if (vocab == 0 || vocab > (size_t)INT32_MAX) return fail(LQ8_ERR_INVALID_ARG, "vocab out of range");
+    if (!sample_vocab_ok(vocab)) return fail(LQ8_ERR_INVALID_ARG, "vocab out of range (1 .. 2^21)");
     if (step > (uint32_t)INT32_MAX) return fail(LQ8_ERR_INVALID_ARG, "step out of range");
     SampleCfg sc;
     lq8_status st = check_sampling(cfg, &sc);

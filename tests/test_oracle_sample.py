@@ -3,9 +3,9 @@ the CPU) pinned by known answers that do not restate it:
 
 * greedy / penalty cases from the reference's own tests
   (src/generate.rs:419-545, 848-890), observed through the chosen token;
-* the random stream: with equal logits every candidate weighs exactly 1, so
-  the token is floor(u * C_end) with u the top 24 bits of a textbook
-  SplitMix64 output, written out here independently;
+* the random stream: with equal logits every candidate weighs exactly 2^32,
+  so the token is floor(n * u24 / 2^24) for n candidates, u24 the top 24 bits
+  of a textbook SplitMix64 output, written out here independently;
 * the distribution: chi-square of many draws against softmax(x / T),
   restricted to the top-k / nucleus support;
 * GenerationConfig defaults and validation (src/generate.rs:389-417).
@@ -28,10 +28,6 @@ def splitmix64(state: int) -> int:
     z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M64
     z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M64
     return z ^ (z >> 31)
-
-
-def uniform(seed: int, step: int) -> np.float32:
-    return np.float32((splitmix64((seed + step * GOLDEN) & M64) >> 40) * 2.0**-24)
 
 
 def draw(logits, n, seed=1, counts=None, **kw):
@@ -79,19 +75,36 @@ def test_repetition_penalty_known_answers():
 
 @pytest.mark.parametrize("seed", [0, 7, 2**64 - 5])
 def test_random_stream_equal_weights(seed):
-    """Equal logits: candidate j sits at sorted position j (lower index first)
-    and its prefix sum is exactly j + 1, so the token is floor(u * C_end)."""
+    """Equal logits: candidate j sits at sorted position j (lower index first),
+    every weight is 2^32 and C_j = (j + 1) 2^32, so with n candidates in the
+    draw the token is floor(n * u24 / 2^24)."""
     x = np.zeros(256, np.float32)
     for step in range(40):
-        u = uniform(seed, step)
-        assert oracle.sample(x, None, 1.0, 0, 1.0, 1.0, seed, step) == int(u * 256), step
-        # top_k 100: C_end = 100
-        assert oracle.sample(x, None, 0.7, 100, 1.0, 1.0, seed, step) == int(np.float32(u * np.float32(100))), step
+        u24 = splitmix64((seed + step * GOLDEN) & M64) >> 40
+        assert oracle.sample(x, None, 1.0, 0, 1.0, 1.0, seed, step) == (256 * u24) >> 24, step
+        # top_k 100: C_end = 100 * 2^32
+        assert oracle.sample(x, None, 0.7, 100, 1.0, 1.0, seed, step) == (100 * u24) >> 24, step
     x = np.zeros(300, np.float32)
     for step in range(40):
-        # nucleus 0.5 of 300 equal weights ends at the 150th candidate (third chunk of 64)
-        u = uniform(seed, step)
-        assert oracle.sample(x, None, 1.0, 0, 0.5, 1.0, seed, step) == int(np.float32(u * np.float32(150))), step
+        # nucleus 0.5 of 300 equal weights: thr = 150 * 2^32, reached at the 150th
+        u24 = splitmix64((seed + step * GOLDEN) & M64) >> 40
+        assert oracle.sample(x, None, 1.0, 0, 0.5, 1.0, seed, step) == (150 * u24) >> 24, step
+
+
+def test_integer_weights_known_answers():
+    """Two candidates z = (0, fl(-ln 2)): weights 2^32 and 2^32 * fl(exp(z_1))
+    (the exponential rounded once to float, here from numpy in double), so
+    C = (2^32, 2^32 + w_1) and the first candidate is drawn exactly when
+    r = floor(C_end * u24 / 2^24) < 2^32."""
+    x = np.array([0.0, -0.6931471805599453], np.float32)
+    w1 = int(np.float32(np.exp(np.float64(x[1]))) * np.float32(2**32))
+    for step in range(64):
+        u24 = splitmix64((9 + step * GOLDEN) & M64) >> 40
+        r = ((2**32 + w1) * u24) >> 24
+        assert oracle.sample(x, None, 1.0, 0, 1.0, 1.0, 9, step) == (0 if 2**32 > r else 1), step
+    # a weight below 2^-32 of the top is 0: never drawn
+    x = np.array([0.0, -30.0], np.float32)
+    assert set(draw(x, 200, seed=2)) == {0}
 
 
 def chi2_ok(counts, probs, n):
