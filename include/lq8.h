@@ -216,13 +216,14 @@ lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_pr
  *       occurrence of each token (src/generate.rs:353-380; off at 1.0);
  *   temperature 0: greedy, the largest x, the last index on ties;
  *   otherwise z = x / temperature; tokens ordered by z descending (ties: the
- *   lower index first); the first top_k kept (all for 0); e = exp(z - z_max);
- *   prefix sums C of e in that order, in chunks of 64 (chunk totals
- *   sequential, then sequential over the chunks); the nucleus ends at the
- *   first C >= top_p * C_last (the whole kept set for top_p = 1);
- *   u = (SplitMix64(seed + step * 0x9E3779B97F4A7C15) >> 40) * 2^-24, where
- *   step is the index of the generated token (0 for the token after the
- *   prompt); the token is the first one of the nucleus with C > u * C_end.
+ *   lower index first); the first top_k kept (all for 0); integer weights
+ *   w = floor(2^32 * exp(z - z_max)) (0 for NaN) and prefix sums C of w in
+ *   that order, exact in 64 bits; with top_p < 1 the nucleus ends at the
+ *   first C >= ceil(C_last * floor(top_p * 2^24) / 2^24) (the whole kept set
+ *   for top_p = 1); u24 = SplitMix64(seed + step * 0x9E3779B97F4A7C15) >> 40,
+ *   where step is the index of the generated token (0 for the token after
+ *   the prompt), r = floor(C_end * u24 / 2^24); the token is the first one
+ *   with C > r (the first one when C_end = 0).
  * Unlike the reference's dispatch (src/generate.rs:670-693), temperature 1
  * with no top-k / top-p samples (the stub returns the argmax there). */
 typedef struct {
@@ -234,9 +235,10 @@ typedef struct {
 } lq8_sampling;
 
 /* sample_with_config (src/generate.rs:670-693) on device logits [vocab]:
- * the token goes to *d_token (device).  d_counts: device [vocab] counts of
- * each token generated so far (the repetition penalty; NULL for none); step:
- * the RNG counter.  Blocks until the token is written. */
+ * the token goes to *d_token (device).  vocab: 1 .. 2^21.  d_counts: device
+ * [vocab] counts of each token generated so far (the repetition penalty;
+ * NULL for none); step: the RNG counter.  Works in the context's scratch
+ * buffer; blocks until the token is written. */
 lq8_status lq8_sample_device(lq8_ctx* ctx, const float* d_logits, size_t vocab, const uint32_t* d_counts,
                              const lq8_sampling* cfg, uint32_t step, uint32_t* d_token);
 
