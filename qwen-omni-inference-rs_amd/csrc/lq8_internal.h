@@ -233,6 +233,7 @@ constexpr int ATT_THREADS = 512;
 constexpr int ATT_F4 = ATT_SEG * 32 / ATT_THREADS;  // float4 of one segment's K (or V) per thread
 constexpr int ATT_PART_STRIDE = 132;                // o_c[128], m_c, l_c, pad
 constexpr int ATT_MAX_GROUP = 16;
+constexpr int ATT_EARLY_SEGS = 4;                  // decode: segments whose K/V loads precede the position
 bool attention_supported(int num_heads, int num_kv_heads, int head_dim);
 
 // Decode: one workgroup per (kv head, segment); normalizes and rotates q/k

@@ -45,12 +45,9 @@ __device__ __forceinline__ float wave_max64(float a) {
 // RmsNorm of one head vector (src/attention.rs:350-358 with src/rms_norm.rs:143-176)
 // then RoPE (src/rope.rs:270-297) at table row cs/sn; one wave, lane l has
 // elements l and l + 64 (head_dim 128).
-__device__ __forceinline__ void head_norm_rope(const float* src, const float* w, const float* cs, const float* sn,
-                                               float eps, float* dst) {
+__device__ __forceinline__ void head_norm_rope_vals(float s0, float s1, float w0, float w1, const float* cs,
+                                                    const float* sn, float eps, float* dst) {
     const int lane = threadIdx.x & 63;
-    // all loads first, then the arithmetic
-    const float s0 = src[lane], s1 = src[lane + 64];
-    const float w0 = w[lane], w1 = w[lane + 64];
     const float c = cs[lane & ~1], s = sn[lane & ~1];
     const float x0 = bf16_round(s0), x1 = bf16_round(s1);
     float acc = 0.0f;
@@ -62,6 +59,14 @@ __device__ __forceinline__ void head_norm_rope(const float* src, const float* w,
     const float y1 = bf16_round((x1 * inv) * bf16_round(w1));
     dst[lane] = y0 * c - y1 * s;
     dst[lane + 64] = y1 * c + y0 * s;
+}
+__device__ __forceinline__ void head_norm_rope(const float* src, const float* w, const float* cs, const float* sn,
+                                               float eps, float* dst) {
+    const int lane = threadIdx.x & 63;
+    // all loads first, then the arithmetic
+    const float s0 = src[lane], s1 = src[lane + 64];
+    const float w0 = w[lane], w1 = w[lane + 64];
+    head_norm_rope_vals(s0, s1, w0, w1, cs, sn, eps, dst);
 }
 
 // q/k RmsNorm per head, RoPE and KV-cache append for n rows (prefill).
@@ -102,6 +107,21 @@ __device__ __forceinline__ void seg_load(const float* __restrict__ Kc, const flo
         const int f = tid + u * ATT_THREADS;  // float4 index in the [64][32] segment
         const int j = f >> 5, c4 = f & 31;
         const size_t row = (size_t)js + (j < nj ? j : 0);
+        kreg[u] = *(const float4*)(Kc + row * 128 + c4 * 4);
+        vreg[u] = *(const float4*)(Vc + row * 128 + c4 * 4);
+    }
+}
+
+// The same loads before the position is known: rows js .. js + 63 clamped to
+// the cache capacity (rows past the position are loaded and never used).
+__device__ __forceinline__ void seg_load_capacity(const float* __restrict__ Kc, const float* __restrict__ Vc, int js,
+                                                  int max_pos, float4* kreg, float4* vreg) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < ATT_F4; u++) {
+        const int f = tid + u * ATT_THREADS;
+        const int j = f >> 5, c4 = f & 31;
+        const size_t row = (size_t)min(js + j, max_pos - 1);
         kreg[u] = *(const float4*)(Kc + row * 128 + c4 * 4);
         vreg[u] = *(const float4*)(Vc + row * 128 + c4 * 4);
     }
@@ -170,49 +190,68 @@ __device__ __forceinline__ void seg_stage_v(const float4* vreg, int nj, int vnew
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     extern __shared__ float sm[];
     const int kvh = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = a.num_heads / a.num_kv_heads;
-    const int pos = a.d_pos ? a.d_pos[b] : a.pos_base;
+    const int QD = a.num_heads * 128, KD = a.num_kv_heads * 128;
     a.qkv += b * a.qkv_stride;
     a.k_cache += b * a.kv_stride;
     a.v_cache += b * a.kv_stride;
     a.part += b * a.part_stride;
+    const float* Kc = a.k_cache + (size_t)kvh * a.max_pos * 128;
+    const float* Vc = a.v_cache + (size_t)kvh * a.max_pos * 128;
+    const int js = c * SEG;
+    // Loads that do not depend on the position go out before it arrives: the
+    // K/V rows of the first ATT_EARLY_SEGS segments (almost always in use;
+    // later segments wait, so a long cache's idle workgroups load nothing)
+    // and this wave's first head vector (q head `wave`, or the new k / v).
+    float4 kreg[ATT_F4], vreg[ATT_F4];
+    const bool early = c < ATT_EARLY_SEGS;
+    if (early) seg_load_capacity(Kc, Vc, js, a.max_pos, kreg, vreg);
+    float h0 = 0.0f, h1 = 0.0f, n0 = 0.0f, n1 = 0.0f;
+    if (wave < G + 2) {
+        const float* src = wave < G ? a.qkv + (kvh * G + wave) * 128
+                                    : a.qkv + QD + (wave == G ? 0 : KD) + kvh * 128;
+        h0 = src[lane];
+        h1 = src[lane + 64];
+        if (wave <= G) {
+            const float* w = wave < G ? a.q_norm : a.k_norm;
+            n0 = w[lane];
+            n1 = w[lane + 64];
+        }
+    }
+    const int pos = a.d_pos ? a.d_pos[b] : a.pos_base;
     const int L = pos + 1;
     const int C = (L + SEG - 1) / SEG;
     // before any barrier: the whole workgroup leaves (a position outside the
     // cache writes nothing)
     if (c >= C || pos < 0 || pos >= a.max_pos) return;
-    const int js = c * SEG, nj = min(SEG, L - js);
+    const int nj = min(SEG, L - js);
     const bool last = c == C - 1;
     const int newrow = last ? pos - js : -1;
-    const int QD = a.num_heads * 128, KD = a.num_kv_heads * 128;
-    const float* Kc = a.k_cache + (size_t)kvh * a.max_pos * 128;
-    const float* Vc = a.v_cache + (size_t)kvh * a.max_pos * 128;
     float* qs = sm;                      // [G][128]
     float* kn = qs + G * 128;            // [128]
     float* vn = kn + 128;                // [128]
     float* sc = vn + 128;                // [G][64]
     float* mlc = sc + G * SEG;           // [G][2]
     float* ks = sm + seg_ks_off(G);      // [64][KPAD], later vs [64][128]
-    float4 kreg[ATT_F4], vreg[ATT_F4];
-    seg_load(Kc, Vc, js, nj, kreg, vreg);
+    if (!early) seg_load(Kc, Vc, js, nj, kreg, vreg);
     const float* cs = a.cos_t + (size_t)pos * 64;
     const float* sn = a.sin_t + (size_t)pos * 64;
     for (int t = wave; t < G + 2; t += ATT_THREADS / 64) {
         if (t < G) {
-            head_norm_rope(a.qkv + (kvh * G + t) * 128, a.q_norm, cs, sn, a.eps, qs + t * 128);
+            if (t == wave) head_norm_rope_vals(h0, h1, n0, n1, cs, sn, a.eps, qs + t * 128);
+            else head_norm_rope(a.qkv + (kvh * G + t) * 128, a.q_norm, cs, sn, a.eps, qs + t * 128);
         } else if (t == G && last) {
-            head_norm_rope(a.qkv + QD + kvh * 128, a.k_norm, cs, sn, a.eps, kn);
-            const int lane = tid & 63;
+            if (t == wave) head_norm_rope_vals(h0, h1, n0, n1, cs, sn, a.eps, kn);
+            else head_norm_rope(a.qkv + QD + kvh * 128, a.k_norm, cs, sn, a.eps, kn);
             float* kr = a.k_cache + ((size_t)kvh * a.max_pos + pos) * 128;
             kr[lane] = kn[lane];
             kr[lane + 64] = kn[lane + 64];
         } else if (t == G + 1 && last) {
-            const int lane = tid & 63;
             const float* v = a.qkv + QD + KD + kvh * 128;
             float* vr = a.v_cache + ((size_t)kvh * a.max_pos + pos) * 128;
-            const float v0 = v[lane], v1 = v[lane + 64];
+            const float v0 = t == wave ? h0 : v[lane], v1 = t == wave ? h1 : v[lane + 64];
             vn[lane] = v0;
             vn[lane + 64] = v1;
             vr[lane] = v0;
