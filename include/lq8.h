@@ -235,7 +235,7 @@ typedef struct {
 } lq8_sampling;
 
 /* sample_with_config (src/generate.rs:670-693) on device logits [vocab]:
- * the token goes to *d_token (device).  vocab: 1 .. 2^21.  d_counts: device
+ * the token goes to *d_token (device).  vocab: 1 .. 2^20.  d_counts: device
  * [vocab] counts of each token generated so far (the repetition penalty;
  * NULL for none); step: the RNG counter.  Works in the context's scratch
  * buffer; blocks until the token is written. */

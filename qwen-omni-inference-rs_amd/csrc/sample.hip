@@ -33,8 +33,10 @@ namespace lq8 {
 
 namespace {
 
-constexpr int SORT_THREADS = 256, SORT_IPT = 8, SORT_TILE = SORT_THREADS * SORT_IPT, RADIX = 256;
-constexpr int PICK_THREADS = 1024, PICK_MAX_TILES = PICK_THREADS;  // vocab <= 2^21
+constexpr int SORT_THREADS = 256, SORT_IPT = 4, SORT_TILE = SORT_THREADS * SORT_IPT, RADIX = 256;
+constexpr int PICK_THREADS = 1024, PICK_MAX_TILES = PICK_THREADS;
+constexpr int PICK_PER = SORT_TILE / PICK_THREADS;  // sorted entries per pick thread in one tile (1 or 2)
+static_assert(PICK_PER == 1 || PICK_PER == 2, "pick covers a tile with 1 or 2 entries per thread");
 constexpr int MAX_VOCAB = PICK_MAX_TILES * SORT_TILE;
 
 __device__ __forceinline__ uint32_t order_bits(float z) {
@@ -313,20 +315,21 @@ __device__ int first_tile(PickShared& sh, int nt, unsigned long long thr, bool g
 __device__ int first_in_tile(PickShared& sh, const uint32_t* sorted, float z0, int K, int tb, unsigned long long thr,
                              bool ge) {
     const int t = threadIdx.x;
-    const int p0 = tb * SORT_TILE + 2 * t;
+    const int p0 = tb * SORT_TILE + PICK_PER * t;
     const unsigned long long w0 = p0 < K ? weight_of(key_value(sorted[p0]), z0) : 0ull;
-    const unsigned long long w1 = p0 + 1 < K ? weight_of(key_value(sorted[p0 + 1]), z0) : 0ull;
+    const unsigned long long w1 = PICK_PER == 2 && p0 + 1 < K ? weight_of(key_value(sorted[p0 + 1]), z0) : 0ull;
     const unsigned long long before = tb > 0 ? sh.pre[tb - 1] : 0ull;
     const unsigned long long inc = block_scan_u64(w0 + w1, sh.wsum);
     const unsigned long long c0 = before + (inc - w1), c1 = before + inc;
     if (t == 0) sh.first_j = 0xFFFFFFFFu;
     __syncthreads();
-    const bool h0 = p0 < K && (ge ? c0 >= thr : c0 > thr), h1 = p0 + 1 < K && (ge ? c1 >= thr : c1 > thr);
+    const bool h0 = p0 < K && (ge ? c0 >= thr : c0 > thr);
+    const bool h1 = PICK_PER == 2 && p0 + 1 < K && (ge ? c1 >= thr : c1 > thr);
     if (h0 || h1) atomicMin(&sh.first_j, (uint32_t)(h0 ? p0 : p0 + 1));
     __syncthreads();
     const uint32_t j = sh.first_j;
     if (j == (uint32_t)p0) sh.c_hit = c0;
-    if (j == (uint32_t)p0 + 1) sh.c_hit = c1;
+    if (PICK_PER == 2 && j == (uint32_t)p0 + 1) sh.c_hit = c1;
     __syncthreads();
     return j == 0xFFFFFFFFu ? -1 : (int)j;
 }
@@ -412,7 +415,7 @@ lq8_status sort_pass(hipStream_t s, SortIn in, uint32_t* planes, uint32_t* keys_
 size_t sample_work_bytes(int vocab) { return work_layout(vocab, nullptr, nullptr); }
 
 lq8_status launch_sample(hipStream_t s, const SampleLaunch& a) {
-    if (a.vocab <= 0 || a.vocab > MAX_VOCAB) return fail(LQ8_ERR_INVALID_ARG, "sample: vocabulary outside 1 .. 2^21");
+    if (a.vocab <= 0 || a.vocab > MAX_VOCAB) return fail(LQ8_ERR_INVALID_ARG, "sample: vocabulary outside 1 .. 2^20");
     if (!a.work) return fail(LQ8_ERR_INVALID_ARG, "sample: no workspace");
     SampleWork w;
     work_layout(a.vocab, a.work, &w);
@@ -463,7 +466,7 @@ extern "C" lq8_status lq8_sample_device(lq8_ctx* ctx, const float* d_logits, siz
                                         const lq8_sampling* cfg, uint32_t step, uint32_t* d_token) {
     if (!registry_has(ctx)) return fail(LQ8_ERR_INVALID_ARG, "invalid or released context handle");
     if (!d_logits || !d_token) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
-    if (!sample_vocab_ok(vocab)) return fail(LQ8_ERR_INVALID_ARG, "vocab out of range (1 .. 2^21)");
+    if (!sample_vocab_ok(vocab)) return fail(LQ8_ERR_INVALID_ARG, "vocab out of range (1 .. 2^20)");
     if (step > (uint32_t)INT32_MAX) return fail(LQ8_ERR_INVALID_ARG, "step out of range");
     SampleCfg sc;
     lq8_status st = check_sampling(cfg, &sc);

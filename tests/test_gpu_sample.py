@@ -65,10 +65,10 @@ def test_sample_qwen3_vocab_matches_oracle(ctx, cfg):
         dc.free()
 
 
-@pytest.mark.parametrize("V", [1, 2, 5, 63, 64, 65, 130, 2047, 2048, 2049, 4097])
+@pytest.mark.parametrize("V", [1, 2, 5, 63, 64, 65, 130, 1023, 1024, 1025, 2047, 2048, 2049, 4097])
 def test_sample_small_vocab_ties(ctx, V):
-    """Integer logits (many ties), sizes around the 64-entry chunk and the
-    2048-entry sort tile."""
+    """Integer logits (many ties), sizes around a wave, the 1024-entry sort
+    tile (also the pick's per-thread span) and several tiles."""
     rng = np.random.default_rng(V)
     logits = rng.integers(-3, 4, V).astype(np.float32)
     counts = rng.integers(0, 2, V).astype(np.uint32)
@@ -95,6 +95,10 @@ def test_sample_device_rejects_bad_config(ctx):
                     lq8.GenerationConfig(1, 1.0, 0, 1.0, 0.5)]:
             with pytest.raises(lq8.InvalidArgument):
                 lq8.sample_device(ctx, dl, 16, bad)
+        # vocabulary bounds are checked before any device work
+        for vocab in (0, 2**20 + 1):
+            with pytest.raises(lq8.InvalidArgument):
+                lq8.sample_device(ctx, dl, vocab, lq8.GenerationConfig(1, 1.0, 0, 1.0, 1.0))
     finally:
         dl.free()
 
