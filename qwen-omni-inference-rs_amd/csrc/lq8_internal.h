@@ -196,6 +196,7 @@ struct SampleLaunch {
 // GenerationConfig ranges (src/generate.rs:96-128) -> the device config.
 lq8_status check_sampling(const lq8_sampling* c, SampleCfg* out);
 size_t sample_work_bytes(int vocab);
+bool sample_vocab_ok(size_t vocab);  // 1 .. 2^20
 lq8_status launch_sample(hipStream_t s, const SampleLaunch& a);
 
 lq8_status launch_repack_aos(hipStream_t s, const uint8_t* aos, size_t n_rows, size_t row0, const lq8_weight* w);

@@ -743,6 +743,7 @@ lq8_status lq8_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     // temperature 0 without a penalty is the greedy rule exactly
     if (sc.temperature == 0.0f && std::fabs(sc.penalty - 1.0f) < 1e-6f)
         return run_generate(m, prompt, n_prompt, max_new, nullptr, out_tokens, stats);
+    if (!sample_vocab_ok(m->c.vocab_size)) return fail(LQ8_ERR_INVALID_ARG, "sampling: vocabulary above 2^20");
     return run_generate(m, prompt, n_prompt, max_new, &sc, out_tokens, stats);
 }
 
