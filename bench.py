@@ -271,7 +271,16 @@ def main():
         model.generate(prompt, gc, seed=1)
         sruns = [model.generate(prompt, gc, seed=1 + i)[1] for i in range(3)]
         stps = sorted(r["decode_tokens_per_s"] for r in sruns)[1]
-        decode = {"tokens_per_s": round(tps, 1), "prefill_ms": round(runs[0]["prefill_ms"], 2),
+        # every Q8_0 matrix of the model is read once per token (the tied
+        # embedding as the lm_head); the step is a chain of dependent kernels
+        wbytes = LAYERS * sum(n * k * 34 // 32 for _, n, k in LAYER_SHAPES) + LM_HEAD[1] * LM_HEAD[2] * 34 // 32
+        chain = 5 * LAYERS + 3
+        decode = {"tokens_per_s": round(tps, 1), "us_per_token": round(1e6 / tps, 1),
+                  "weight_bytes_per_token": wbytes, "weight_gbs": round(wbytes * tps / 1e9, 1),
+                  "kernels_per_token": chain, "us_per_kernel": round(1e6 / tps / chain, 2),
+                  "bound": "latency: a chain of dependent kernels per token (5 per layer, then lm_head, pick, "
+                           "embedding row)",
+                  "prefill_ms": round(runs[0]["prefill_ms"], 2),
                   "graph": runs[0]["used_graph"], "prompt": 128, "new_tokens": 128,
                   "sampled_tokens_per_s": round(stps, 1),
                   "sampled_config": {"temperature": 0.8, "top_k": 50, "top_p": 0.95, "repetition_penalty": 1.1},
