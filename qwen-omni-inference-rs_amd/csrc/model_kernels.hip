@@ -167,6 +167,30 @@ __device__ __forceinline__ void seg_scores(const float4* kreg, int nj, int knew_
     }
 }
 
+// o = sum_j e[j] * vs[j][d] for j = 0 .. nj - 1 in order, from +0.  Eight
+// steps per batch: their LDS reads go out together (e is 16-byte aligned and
+// wave-uniform), then the chain; the order of the adds is unchanged.
+__device__ __forceinline__ float pv_chain(const float* e, const float* vs, int d, int nj) {
+    float o = 0.0f;
+    int j = 0;
+    for (; j + 8 <= nj; j += 8) {
+        const float4 e0 = *(const float4*)(e + j), e1 = *(const float4*)(e + j + 4);
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = vs[(j + u) * 128 + d];
+        o = o + e0.x * v[0];
+        o = o + e0.y * v[1];
+        o = o + e0.z * v[2];
+        o = o + e0.w * v[3];
+        o = o + e1.x * v[4];
+        o = o + e1.y * v[5];
+        o = o + e1.z * v[6];
+        o = o + e1.w * v[7];
+    }
+    for (; j < nj; j++) o = o + e[j] * vs[j * 128 + d];
+    return o;
+}
+
 // V rows of the segment into vs [64][128] (row vnew_row from vnew).
 __device__ __forceinline__ void seg_stage_v(const float4* vreg, int nj, int vnew_row, const float* vnew, float* vs) {
     const int tid = threadIdx.x;
@@ -265,9 +289,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     __syncthreads();
     for (int t = tid; t < G * 128; t += ATT_THREADS) {
         const int h = t >> 7, d = t & 127;
-        const float* e = sc + h * SEG;
-        float o = 0.0f;
-        for (int j = 0; j < nj; j++) o = o + e[j] * ks[j * 128 + d];
+        const float o = pv_chain(sc + h * SEG, ks, d, nj);
         float* p = a.part + ((size_t)c * a.num_heads + kvh * G + h) * ATT_PART_STRIDE;
         p[d] = o;
         if (d == 0) {
@@ -403,9 +425,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_rows(AttnRowsLaunch a) {
                 const int rh = t >> 7, d = t & 127, rr = rh / G;
                 const int nj = min(SEG, a.pos_base + i0 + rr + 1 - js);
                 if (rr < nr && nj > 0) {
-                    const float* e = sc + rh * SEG;
-                    float o = 0.0f;
-                    for (int j = 0; j < nj; j++) o = o + e[j] * ks[j * 128 + d];
+                    const float o = pv_chain(sc + rh * SEG, ks, d, nj);
                     num[r] = num[r] * run[4 * rh + 2] + run[4 * rh + 3] * o;
                 }
             }
