@@ -103,6 +103,71 @@ def cpu_baseline(seconds_target=12.0):
                       f"({layer_bytes} B each), {el:.1f} s on one host core"}
 
 
+def host_cpu():
+    """Model name and logical cores available to this process."""
+    name = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": name, "logical_cores": len(os.sched_getaffinity(0))}
+
+
+def cpu_gemv_all_cores(seconds_target=4.0):
+    """The oracle's GEMV with one OpenMP thread per available core (each output
+    row still summed by one thread in the fixed order), labelled apart from
+    the single-core baseline."""
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    oracle.set_threads(threads)
+    rng = np.random.default_rng(5)
+    mats = []
+    for _, n, k in LAYER_SHAPES:
+        blocks = oracle.quantize_q8_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        mats.append((blocks, n, k, rng.standard_normal(k).astype(np.float32)))
+    layer_bytes = sum(gemv_bytes(n, k) for _, n, k, _ in mats)
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        for blocks, n, k, x in mats:
+            oracle.gemv_q8_0(blocks, n, k, x)
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= seconds_target:
+            break
+    oracle.set_threads(0)
+    return {"value": round(passes * layer_bytes / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{passes} passes over one decode layer's 7 Q8_0 GEMVs, {el:.1f} s"}
+
+
+def cpu_decode(cfg, tensors, prompt, steps=3):
+    """Config-4 decode on the host: the oracle's Qwen3-0.6B forward (the
+    reference's decoder numerics over Q8_0 weights), a few single-token steps
+    on one core after a 128-token prefill run on all cores (not timed)."""
+    import oracle
+
+    ref = oracle.Model(cfg, tensors)
+    try:
+        oracle.set_threads(len(os.sched_getaffinity(0)))
+        logits = ref.forward(prompt, 0)
+        oracle.set_threads(1)
+        tok, pos = int(np.argmax(logits)), prompt.size
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            logits = ref.forward([tok], pos)
+            tok, pos = int(np.argmax(logits)), pos + 1
+        el = time.perf_counter() - t0
+    finally:
+        oracle.set_threads(0)
+        ref.close()
+    return {"tokens_per_s": round(steps / el, 3), "cores": 1, "kind": "port",
+            "sample": f"{steps} decode steps at positions 128..{127 + steps} on one core, {el:.2f} s"}
+
+
 def rotating_gemv_us(ctx, n, k, copies):
     """Per-launch time of an n x k GEMV, graph-replayed over `copies` distinct
     weights (cold: the copies together exceed the Infinity Cache)."""
@@ -254,11 +319,17 @@ def main():
             lin.forward_device(x, 512, y)
         ms = ctx.timer_stop() / 20
         tops = 2 * 512 * n * k / (ms * 1e-3) / 1e12
-        gemm[name] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4)}
+        # compulsory bytes: Q8_0 weight + Q8_0 activations + f32 output
+        gbytes = n * k * 34 // 32 + 512 * k * 34 // 32 + 4 * 512 * n
+        floor_us = max(gbytes / HBM_PEAK_GBS / 1e3, 2 * 512 * n * k / INT8_PEAK_TOPS / 1e6)
+        gemm[name] = {"us": round(ms * 1e3, 2), "TOPS": round(tops, 1), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
+                      "bytes": gbytes, "floor_us": round(floor_us, 2),
+                      "mfma_ceiling_frac": round(2 * 512 * n * k / INT8_PEAK_TOPS / 1e6 / floor_us, 3)}
         log(f"GEMM {name} M=512: {ms * 1e3:.1f} us, {tops:.1f} TOPS (includes the activation quantize)")
         w.free(); x.free(); y.free()
 
     decode = None
+    cpu_model = None
     if not args.no_decode:
         cfg = lq8.qwen3_0_6b(max_positions=512)
         model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=2026)
@@ -287,6 +358,8 @@ def main():
                   "sampler_us_over_greedy": round(1e6 / stps - 1e6 / tps, 1)}
         log(f"decode: {tps:.1f} tok/s (median of 3), prefill {runs[0]['prefill_ms']:.2f} ms; "
             f"sampled {stps:.1f} tok/s ({1e6 / stps - 1e6 / tps:.1f} us/token over greedy)")
+        if not args.no_cpu:
+            cpu_model = (cfg, model.export_all(), prompt)
         model.free()
 
     moe = None if args.no_moe else moe_stack(ctx)
@@ -295,6 +368,12 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline()
     if cpu:
         log(f"cpu baseline: {cpu['value']} GB/s ({cpu['sample']})")
+        cpu["host"] = host_cpu()
+        cpu["all_cores"] = cpu_gemv_all_cores()
+        log(f"cpu all cores: {cpu['all_cores']['value']} GB/s on {cpu['all_cores']['cores']} threads")
+        if cpu_model is not None:
+            cpu["decode"] = cpu_decode(*cpu_model)
+            log(f"cpu decode: {cpu['decode']['tokens_per_s']} tok/s ({cpu['decode']['sample']})")
 
     traffic = measured_traffic()
     out = {
