@@ -618,6 +618,104 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
 #undef MV_LOAD_ITEM
 }
 
+// Routed expert down projections of one token fused with their combine
+// (batch 1): one workgroup per 16-row tile of the hidden state runs the GEMV
+// of every routed expert over that tile -- the arithmetic of k_gemv_mv
+// (16-code fmaf chains, the lane pair sums, the trees over a group's pairs
+// and over the groups) -- then h[row] = h2[row] + sum over the experts in
+// ascending index of w * y (k_moe_combine's order).  The expert outputs never
+// leave the workgroup.
+constexpr int MOE_DOWN_THREADS = 1024;
+
+template <int CH>
+__global__ __launch_bounds__(MOE_DOWN_THREADS) void k_moe_down_combine(MoeDownArgs a) {
+    extern __shared__ float smem[];
+    __shared__ int order[MOE_DOWN_MAX_K];
+    const int tile = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int K = a.K, k = a.k, k4 = k >> 2, nb = k >> 5, np = (nb + 1) >> 1;
+    const int G = (np + CH - 1) / CH, items = K * G;
+    float* xs = smem;                 // [K][np * 64]
+    float* gs = xs + K * np * 64;     // [K][G][16]
+    const int r = lane & 15, part = lane >> 4, bsel = part >> 1, half = part & 1;
+    if (tid < K) {
+        const uint32_t me = a.rids[tid];
+        int below = 0;
+        for (int q = 0; q < K; q++) below += a.rids[q] < me;
+        order[below] = tid;  // the routed experts of a token are distinct
+    }
+    // weights of item `it` = (rank-ordered expert q, group g), clamped
+    u32x4 pv[CH];
+    uint16_t ps[CH];
+    auto load_item = [&](int it_) {
+        const int itc = min(it_, items - 1), q = itc / G, g = itc - q * G;
+        const size_t gt = (size_t)a.rids[q] * a.prob_tiles + tile;  // rank q's expert (raw rank order)
+        const int8_t* cb = a.codes + gt * np * CHUNK_BYTES + lane * 16;
+        const uint16_t* sb = a.scales + gt * 2 * np * 16 + bsel * 16 + r;
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int c = min(g * CH + i, np - 1);
+            pv[i] = __builtin_nontemporal_load((const u32x4*)(cb + (size_t)c * CHUNK_BYTES));
+            ps[i] = sb[(size_t)c * 32];
+        }
+    };
+    load_item(wave);
+    // stage the K input vectors in rank order (silu(gate) * up of each expert)
+    for (int q = 0; q < K; q++) {
+        const float* x = a.x + (size_t)q * a.x_stride;
+        float* xv = xs + q * np * 64;
+        for (int i4 = tid; i4 < k4; i4 += MOE_DOWN_THREADS) *(float4*)(xv + 4 * i4) = *(const float4*)(x + 4 * i4);
+        if ((nb & 1) && tid < 32) xv[k + tid] = 0.0f;
+    }
+    __syncthreads();
+    for (int it = wave; it < items; it += MOE_DOWN_THREADS / 64) {
+        const int q = it / G, g = it - q * G;
+        u32x4 cv[CH];
+        uint16_t ds[CH];
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            cv[i] = pv[i];
+            ds[i] = ps[i];
+        }
+        load_item(it + MOE_DOWN_THREADS / 64);  // the next item's weights while this one computes
+        const float* xv = xs + q * np * 64;
+        const int cnt = min(CH, np - g * CH);
+        float t[CH];
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int p = min(g * CH + i, np - 1);
+            const float h = dot16(cv[i], xv + (2 * p + bsel) * 32 + half * 16);
+            const LanePair hh = lanes16(h);
+            const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(ds[i]);
+            const LanePair vv = lanes32(vb);
+            t[i] = 2 * p + 1 >= nb ? vv.lo : vv.lo + vv.hi;
+        }
+#pragma unroll
+        for (int s2 = 1; s2 < CH; s2 *= 2)
+#pragma unroll
+            for (int i = 0; i + s2 < CH; i += 2 * s2)
+                if (i + s2 < cnt) t[i] = t[i] + t[i + s2];
+        if (lane < 16) gs[(q * G + g) * 16 + lane] = t[0];
+    }
+    __syncthreads();
+    // tree over the group sums, one thread per (rank, row)
+    if (tid < K * 16) {
+        float* col = gs + (tid >> 4) * G * 16 + (tid & 15);
+        for (int s2 = 1; s2 < G; s2 *= 2)
+            for (int i = 0; i + s2 < G; i += 2 * s2) col[i * 16] = col[i * 16] + col[(i + s2) * 16];
+    }
+    __syncthreads();
+    if (tid < 16) {
+        const int row = tile * TILE_ROWS + tid;
+        float acc = 0.0f;
+        for (int q = 0; q < K; q++) {
+            const int rk = order[q];
+            acc = acc + a.rw[rk] * gs[rk * G * 16 + tid];
+        }
+        if (row < a.rows) a.out[row] = a.h2[row] + acc;
+    }
+}
+
 // Greedy pick (src/generate.rs:153-174 via src/tensor.rs:2451-2480):
 // maximum over the tiles' partials, last index on ties.
 __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__ val, const int* __restrict__ idx,
@@ -786,6 +884,25 @@ lq8_status launch_gemv_mv(hipStream_t s, XSource xs, Epilogue epi, const MvArgs&
         default: return resid ? mv_ch<XS_SILU, EPI_RESID>(s, a, max_probs, vsplit)
                               : mv_ch<XS_SILU, EPI_STORE>(s, a, max_probs, vsplit);
     }
+}
+
+bool moe_down_combine_supported(int K, int k) {
+    const int nb = k >> 5, np = (nb + 1) >> 1, ch = pick_ch(np, 4), G = (np + ch - 1) / ch;
+    const size_t smem = ((size_t)K * np * 64 + (size_t)K * G * 16) * sizeof(float);
+    return K >= 1 && K <= MOE_DOWN_MAX_K && k > 0 && k % 32 == 0 && smem <= 48 * 1024;
+}
+
+lq8_status launch_moe_down_combine(hipStream_t s, const MoeDownArgs& a) {
+    if (!moe_down_combine_supported(a.K, a.k) || a.rows <= 0 || a.rows % TILE_ROWS)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe down+combine: unsupported shape");
+    const int nb = a.k >> 5, np = (nb + 1) >> 1, ch = pick_ch(np, 4), G = (np + ch - 1) / ch;
+    const size_t smem = ((size_t)a.K * np * 64 + (size_t)a.K * G * 16) * sizeof(float);
+    const dim3 grid((unsigned)(a.rows / TILE_ROWS));
+    if (ch == 1) hipLaunchKernelGGL(k_moe_down_combine<1>, grid, dim3(MOE_DOWN_THREADS), smem, s, a);
+    else if (ch == 2) hipLaunchKernelGGL(k_moe_down_combine<2>, grid, dim3(MOE_DOWN_THREADS), smem, s, a);
+    else hipLaunchKernelGGL(k_moe_down_combine<4>, grid, dim3(MOE_DOWN_THREADS), smem, s, a);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
 }
 
 lq8_status launch_argmax_final(hipStream_t s, const float* arg_val, const int* arg_idx, int count, uint32_t* d_tok,

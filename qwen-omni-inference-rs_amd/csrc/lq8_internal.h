@@ -149,6 +149,26 @@ struct MvArgs {
 // vsplit: workgroups per tile sharing the vectors of a problem.
 lq8_status launch_gemv_mv(hipStream_t s, XSource xs, Epilogue epi, const MvArgs& a, int max_probs, int vsplit);
 
+// Batch-1 routed expert down projections fused with their combine:
+// out[row] = h2[row] + sum over the K experts in ascending index of
+// rw[rank] * (down_expert(rank) x[rank])[row].
+constexpr int MOE_DOWN_MAX_K = 16;
+struct MoeDownArgs {
+    const int8_t* codes;    // expert e's tiles start at tile e * prob_tiles
+    const uint16_t* scales;
+    int rows, k;            // hidden size, expert intermediate size
+    int prob_tiles;
+    const uint32_t* rids;   // device [K]: expert of each rank
+    const float* rw;        // device [K]: routing weight of each rank
+    int K;
+    const float* x;         // rank q's input: x + q * x_stride
+    int x_stride;
+    const float* h2;        // residual [rows]
+    float* out;             // [rows]
+};
+bool moe_down_combine_supported(int K, int k);
+lq8_status launch_moe_down_combine(hipStream_t s, const MoeDownArgs& a);
+
 // Final greedy pick over the per-tile argmax partials: token -> *d_tok and
 // tokens_out[*d_step], then *d_pos and *d_step advance (device scalars).
 lq8_status launch_argmax_final(hipStream_t s, const float* arg_val, const int* arg_idx, int count, uint32_t* d_tok,

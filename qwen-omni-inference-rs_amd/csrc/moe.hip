@@ -474,7 +474,12 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
             g.x = m->xn;
             if ((st = launch_gemv_mv(s, XS_PLAIN, EPI_SWIGLU, g, max_probs, 1))) return st;
         }
-        // down of each routed expert
+        // down of each routed expert; batch 1: fused with the combine
+        if (T == 1 && moe_down_combine_supported(K, I)) {
+            MoeDownArgs dc{L.down->codes, L.down->scales, H, I, H / TILE_ROWS, rids, rw, K, m->gu, I, m->h2, d_hidden};
+            if ((st = launch_moe_down_combine(s, dc))) return st;
+            continue;
+        }
         MvArgs d{};
         d.codes = L.down->codes; d.scales = L.down->scales; d.rows = H; d.k = I; d.prob_tiles = H / TILE_ROWS;
         d.n_prob = n_act; d.prob_id = act_e; d.vec_begin = vbeg; d.vec_count = vcnt; d.slots = slots;
