@@ -243,11 +243,18 @@ lq8_status lq8_sample_device(lq8_ctx* ctx, const float* d_logits, size_t vocab, 
                              const lq8_sampling* cfg, uint32_t step, uint32_t* d_token);
 
 /* generate (src/generate.rs:611-664) with a sampling configuration: prefill,
- * the first token from the prefill logits, then max_new - 1 decode steps,
- * each sampled on the device (the repetition penalty counts the generated
- * tokens, as the reference's generated_tokens).  out_tokens: max_new. */
+ * the first token from the prefill logits, then up to max_new - 1 decode
+ * steps, each sampled on the device (the repetition penalty counts the
+ * generated tokens, as the reference's generated_tokens).  eos_ids[n_eos]
+ * (may be empty): generation ends at the first generated token in the set,
+ * which is kept (is_eos_token, src/generate.rs:639-659); *n_out receives the
+ * number of tokens written to out_tokens (capacity max_new), and the KV cache
+ * is left as the reference's early stop leaves it (the last token is not
+ * forwarded).  The loop runs on the device without per-token host
+ * synchronisation, so steps after an EOS are computed and discarded. */
 lq8_status lq8_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
-                        const lq8_sampling* cfg, uint32_t* out_tokens, lq8_gen_stats* stats);
+                        const lq8_sampling* cfg, const uint32_t* eos_ids, size_t n_eos, uint32_t* out_tokens,
+                        size_t* n_out, lq8_gen_stats* stats);
 lq8_status lq8_model_free(lq8_model* m);
 
 /* ---- Qwen3-MoE decoder layers (Qwen3-30B-A3B style), decode steps --------

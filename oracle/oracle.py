@@ -277,22 +277,26 @@ class Model:
         return toks, margins
 
     def generate_sampled(self, prompt, max_new: int, temperature: float, top_k: int, top_p: float,
-                         repetition_penalty: float, seed: int) -> np.ndarray:
-        """generate() with the sampling rule: prefill, then one sampled token
-        per step (step t draws with counter t; the penalty counts the tokens
-        generated before it)."""
+                         repetition_penalty: float, seed: int, eos_token_ids=()) -> np.ndarray:
+        """generate() (src/generate.rs:611-664) with the sampling rule:
+        prefill, then one sampled token per step (step t draws with counter t;
+        the penalty counts the tokens generated before it); the loop ends at
+        the first token in eos_token_ids, which is kept and not forwarded."""
         ids = np.ascontiguousarray(prompt, dtype=np.uint32)
+        eos = set(int(e) for e in eos_token_ids)
         self.clear_kv_cache()
         logits = self.forward(ids, 0)
         counts = np.zeros(self.cfg.vocab_size, dtype=np.uint32)
-        toks = np.empty(max_new, dtype=np.uint32)
+        toks = []
         for t in range(max_new):
             tok = sample(logits, counts, temperature, top_k, top_p, repetition_penalty, seed, t)
-            toks[t] = tok
+            toks.append(tok)
             counts[tok] += 1
+            if tok in eos:
+                break
             if t + 1 < max_new:
                 logits = self.forward([tok], ids.size + t)
-        return toks
+        return np.array(toks, dtype=np.uint32)
 
 
 def random_q8_tensors(cfg, seed: int, std: float = 0.02):

@@ -735,16 +735,30 @@ lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_pr
 }
 
 lq8_status lq8_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
-                        const lq8_sampling* cfg, uint32_t* out_tokens, lq8_gen_stats* stats) {
+                        const lq8_sampling* cfg, const uint32_t* eos_ids, size_t n_eos, uint32_t* out_tokens,
+                        size_t* n_out, lq8_gen_stats* stats) {
     CHECK_M(m);
+    if (n_eos && !eos_ids) return fail(LQ8_ERR_INVALID_ARG, "eos_ids is null");
+    if (!n_out) return fail(LQ8_ERR_INVALID_ARG, "n_out is null");
     SampleCfg sc;
     lq8_status st = check_sampling(cfg, &sc);
     if (st) return st;
     // temperature 0 without a penalty is the greedy rule exactly
-    if (sc.temperature == 0.0f && std::fabs(sc.penalty - 1.0f) < 1e-6f)
-        return run_generate(m, prompt, n_prompt, max_new, nullptr, out_tokens, stats);
-    if (!sample_vocab_ok(m->c.vocab_size)) return fail(LQ8_ERR_INVALID_ARG, "sampling: vocabulary above 2^20");
-    return run_generate(m, prompt, n_prompt, max_new, &sc, out_tokens, stats);
+    const bool greedy = sc.temperature == 0.0f && std::fabs(sc.penalty - 1.0f) < 1e-6f;
+    if (!greedy && !sample_vocab_ok(m->c.vocab_size))
+        return fail(LQ8_ERR_INVALID_ARG, "sampling: vocabulary above 2^20");
+    if ((st = run_generate(m, prompt, n_prompt, max_new, greedy ? nullptr : &sc, out_tokens, stats))) return st;
+    // the first EOS ends the generation (kept); the cache as after the early stop
+    size_t n = max_new;
+    for (size_t t = 0; t < max_new && n == max_new; t++)
+        for (size_t e = 0; e < n_eos; e++)
+            if (out_tokens[t] == eos_ids[e]) {
+                n = t + 1;
+                break;
+            }
+    m->kv_len = n_prompt + n - 1;
+    *n_out = n;
+    return LQ8_OK;
 }
 
 lq8_status lq8_model_free(lq8_model* m) {

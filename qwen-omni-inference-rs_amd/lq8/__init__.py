@@ -164,7 +164,8 @@ _SIGS = [
     ("lq8_sample_device", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.POINTER(SamplingC), C.c_uint32, C.c_void_p]),
     ("lq8_generate", C.c_int,
-     [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(SamplingC), C.c_void_p, C.POINTER(GenStatsC)]),
+     [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(SamplingC), C.c_void_p, C.c_size_t, C.c_void_p,
+      C.POINTER(C.c_size_t), C.POINTER(GenStatsC)]),
     ("lq8_model_free", C.c_int, [C.c_void_p]),
     ("lq8_moe_tensor_count", C.c_size_t, [C.POINTER(MoeConfigC)]),
     ("lq8_moe_tensor_bytes", C.c_int, [C.POINTER(MoeConfigC), C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -588,17 +589,21 @@ class Qwen3ForCausalLM:
         return out, {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
                      "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph)}
 
-    def generate(self, prompt: Sequence[int], config: "GenerationConfig", seed: int = 0):
+    def generate(self, prompt: Sequence[int], config: "GenerationConfig", seed: int = 0,
+                 eos_token_ids: Sequence[int] = ()):
         """generate() (src/generate.rs:611-664) with the configuration's
-        sampling, config.max_new_tokens tokens; the loop stays on the device."""
+        sampling: up to config.max_new_tokens tokens, ending at the first one
+        in eos_token_ids (kept); the loop stays on the device."""
         ids = np.ascontiguousarray(prompt, dtype=np.uint32)
+        eos = np.ascontiguousarray(list(eos_token_ids), dtype=np.uint32)
         out = np.empty(config.max_new_tokens, dtype=np.uint32)
+        n = C.c_size_t(0)
         st = GenStatsC()
         sc = config.sampling(seed)
-        _check(lib().lq8_generate(self.handle, _ptr(ids), ids.size, config.max_new_tokens, C.byref(sc), _ptr(out),
-                                  C.byref(st)))
-        return out, {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
-                     "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph)}
+        _check(lib().lq8_generate(self.handle, _ptr(ids), ids.size, config.max_new_tokens, C.byref(sc),
+                                  _ptr(eos) if eos.size else None, eos.size, _ptr(out), C.byref(n), C.byref(st)))
+        return out[:n.value].copy(), {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
+                                      "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph)}
 
     def free(self) -> None:
         if self.handle:

@@ -116,12 +116,12 @@ def small_pair(ctx):
     ref.close()
 
 
-def generate(model, prompt, cfg, seed, graph):
+def generate(model, prompt, cfg, seed, graph, eos=()):
     old = os.environ.pop("LQ8_NO_GRAPH", None)
     if not graph:
         os.environ["LQ8_NO_GRAPH"] = "1"
     try:
-        return model.generate(prompt, cfg, seed)
+        return model.generate(prompt, cfg, seed, eos)
     finally:
         os.environ.pop("LQ8_NO_GRAPH", None)
         if old is not None:
@@ -162,6 +162,32 @@ def test_generate_sampled_replays_repeatable(small_pair):
     assert a.tolist() == b.tolist() == d.tolist()
     assert a.tolist() != c.tolist()
     assert g.size == 5
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_generate_stops_at_eos(small_pair, graph):
+    """generate() ends at the first EOS token (kept), as the reference's loop
+    does; the cache is left at the early stop's length, so a forward at the
+    next offset continues bit for bit like the oracle's."""
+    model, ref = small_pair
+    prompt = np.random.default_rng(31).integers(0, SMALL.vocab_size, 15).astype(np.uint32)
+    cfg = (0.9, 0, 1.0, 1.2)
+    full = ref.generate_sampled(prompt, 30, *cfg, 5)
+    eos = [int(full[11]), 2047]  # a token first drawn at step 11, and one never drawn
+    first = next(t for t in range(30) if int(full[t]) in eos)
+    toks, _ = generate(model, prompt, lq8.GenerationConfig(30, *cfg), 5, graph, eos)
+    ref_toks = ref.generate_sampled(prompt, 30, *cfg, 5, eos_token_ids=eos)
+    assert toks.tolist() == ref_toks.tolist() == full[:first + 1].tolist()
+    nxt = [int(toks[-1])]
+    pos = prompt.size + toks.size - 1
+    assert same_bits(model.forward(nxt, pos), ref.forward(nxt, pos))
+    # no EOS among the tokens: all of them
+    toks, _ = generate(model, prompt, lq8.GenerationConfig(30, *cfg), 5, graph, [2047] if 2047 not in full else [])
+    assert toks.size == 30
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
 
 def test_generate_rejects_bad_config(small_pair):
