@@ -376,7 +376,18 @@ lq8_status launch_pick(lq8_model* m) {
 
 // Sampling buffers (allocated on first use, vocabulary-sized).
 lq8_status ensure_sampler(lq8_model* m) {
-    if (m->d_scfg) return LQ8_OK;
+    if (m->d_scfg && m->d_counts && m->s_work) return LQ8_OK;
+    // a failed earlier attempt may have left some of them: start over (and
+    // drop any graph that captured the old buffers)
+    if (m->sgraph) {
+        (void)hipGraphExecDestroy(m->sgraph);
+        m->sgraph = nullptr;
+    }
+    auto F = [](void* p) { if (p) (void)hipFree(p); };
+    F(m->d_scfg); F(m->d_counts); F(m->s_work);
+    m->d_scfg = nullptr;
+    m->d_counts = nullptr;
+    m->s_work = nullptr;
     const int V = (int)m->c.vocab_size;
     lq8_status st;
     if ((st = dalloc(&m->d_scfg, 1)) || (st = dalloc(&m->d_counts, (size_t)V)) ||
