@@ -1,7 +1,8 @@
 """ctypes wrapper of the CPU oracle (TEST INFRASTRUCTURE).
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
-this module, and only as the checker.  The shipped library never uses it.
+this module, and only to check results against it.  The shipped library never
+uses it.
 Build with ``make -C oracle`` (done by __graft_entry__.build()).
 """
 from __future__ import annotations
