@@ -237,8 +237,8 @@ def main():
     if args.only_step:
         args.no_decode = args.no_cpu = args.no_moe = True
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only (--gpus 1); multi-GPU sharding is a design "
-                                   "note, not built"}))
+        print(json.dumps({"error": "the Q8_0 path runs on one GPU (--gpus 1); sharding it across GPUs is "
+                                   "designed, not built"}))
         sys.exit(2)
 
     ctx = lq8.Context(0)
