@@ -190,6 +190,22 @@ def same_bits(a, b):
     return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
 
+def test_generate_vocabulary_bound(ctx):
+    """Sampling is bounded to vocabularies of 2^20 (checked before any device
+    work); temperature 0 without a penalty is the greedy path, which is not."""
+    cfg = lq8.Qwen3Config(vocab_size=2**20 + 1, hidden_size=64, intermediate_size=64, num_hidden_layers=1,
+                          num_attention_heads=1, num_key_value_heads=1, head_dim=128, max_position_embeddings=16)
+    model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=1)
+    try:
+        with pytest.raises(lq8.InvalidArgument):
+            model.generate([1, 2, 3], lq8.GenerationConfig(4, 1.0, 0, 1.0, 1.0))
+        toks, _ = model.generate([1, 2, 3], lq8.GenerationConfig(4))
+        greedy, _ = model.generate_greedy([1, 2, 3], 4)
+        assert toks.tolist() == greedy.tolist()
+    finally:
+        model.free()
+
+
 def test_generate_rejects_bad_config(small_pair):
     model, _ = small_pair
     with pytest.raises(lq8.InvalidArgument):
