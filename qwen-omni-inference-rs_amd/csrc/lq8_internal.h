@@ -212,10 +212,17 @@ struct SampleLaunch {
     uint32_t* tokens_out;     // device [steps] (null: not kept)
     int* d_pos;               // device position, advanced (null: none)
     void* work;               // device, sample_work_bytes(vocab): sort buffers, histograms, chunk sums
+    bool topk;                // host: sample_topk_path(config) -- candidate selection instead of the full sort
 };
 // GenerationConfig ranges (src/generate.rs:96-128) -> the device config.
 lq8_status check_sampling(const lq8_sampling* c, SampleCfg* out);
+// T > 0 and 1 <= top_k <= 1024: the top-k candidates are selected and sorted
+// alone (same rule, same result as the full sort)
+bool sample_topk_path(const SampleCfg& c);
 size_t sample_work_bytes(int vocab);
+// bytes at the start of the workspace that must be zero before its first use
+// (the top-k path's histogram and counter; every top-k pick clears them again)
+size_t sample_work_zero_bytes(int vocab);
 bool sample_vocab_ok(size_t vocab);  // 1 .. 2^20
 lq8_status launch_sample(hipStream_t s, const SampleLaunch& a);
 

@@ -63,6 +63,8 @@ struct lq8_model {
     uint32_t* d_counts = nullptr;
     uint8_t* s_work = nullptr;  // sampler workspace (sample_work_bytes(vocab))
     hipGraphExec_t sgraph = nullptr;
+    bool s_topk = false;         // the sampling path of the next sampler launches (host copy of the choice)
+    bool sgraph_topk = false;    // the path sgraph was captured with
     hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
 };
 
@@ -410,11 +412,16 @@ lq8_status launch_sample_pick(lq8_model* m) {
     a.tokens_out = m->d_tokens;
     a.d_pos = m->d_pos;
     a.work = m->s_work;
+    a.topk = m->s_topk;
     return launch_sample(m->ctx->stream, a);
 }
 
 lq8_status capture_sample_graph(lq8_model* m) {
-    if (m->sgraph) return LQ8_OK;
+    if (m->sgraph && m->sgraph_topk == m->s_topk) return LQ8_OK;
+    if (m->sgraph) {
+        (void)hipGraphExecDestroy(m->sgraph);
+        m->sgraph = nullptr;
+    }
     hipStream_t s = m->ctx->stream;
     hipGraph_t g = nullptr;
     LQ8_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
@@ -432,6 +439,7 @@ lq8_status capture_sample_graph(lq8_model* m) {
         m->sgraph = nullptr;
         return hip_fail(e, "hipGraphInstantiate");
     }
+    m->sgraph_topk = m->s_topk;
     return LQ8_OK;
 }
 
@@ -485,6 +493,7 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     if (n_prompt > 1 && (st = ensure_prefill(m, n_prompt))) return st;
     const bool use_graph = std::getenv("LQ8_NO_GRAPH") == nullptr;
     if (sc && (st = ensure_sampler(m))) return st;
+    if (sc) m->s_topk = sample_topk_path(*sc);
     if (use_graph && max_new > 1 && (st = sc ? capture_sample_graph(m) : capture_decode_graph(m))) return st;
     // clear_kv_cache (src/generate.rs:618), then prefill at offset 0
     m->kv_len = 0;
@@ -496,6 +505,7 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
         // the penalty counts the generated tokens only (generated_tokens, src/generate.rs:627-660)
         LQ8_HIP(hipMemcpyAsync(m->d_scfg, sc, sizeof(SampleCfg), hipMemcpyHostToDevice, s));
         LQ8_HIP(hipMemsetAsync(m->d_counts, 0, m->c.vocab_size * sizeof(uint32_t), s));
+        LQ8_HIP(hipMemsetAsync(m->s_work, 0, sample_work_zero_bytes((int)m->c.vocab_size), s));
     }
     LQ8_HIP(hipEventRecord(m->e0, s));
     st = n_prompt == 1 ? enqueue_decode(m, m->d_ids, nullptr, 0) : enqueue_prefill(m, (int)n_prompt, 0);

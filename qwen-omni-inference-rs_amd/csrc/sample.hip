@@ -38,6 +38,8 @@ constexpr int PICK_THREADS = 1024, PICK_MAX_TILES = PICK_THREADS;
 constexpr int PICK_PER = SORT_TILE / PICK_THREADS;  // sorted entries per pick thread in one tile (1 or 2)
 static_assert(PICK_PER == 1 || PICK_PER == 2, "pick covers a tile with 1 or 2 entries per thread");
 constexpr int MAX_VOCAB = PICK_MAX_TILES * SORT_TILE;
+// top-k path: candidates by the top 12 bits of the key, at most TK_CAP of them
+constexpr int TK_BINS = 4096, TK_CAP = 4096, TK_MAXK = PICK_THREADS;
 
 __device__ __forceinline__ uint32_t order_bits(float z) {
     const uint32_t b = __float_as_uint(z);
@@ -375,21 +377,294 @@ __global__ __launch_bounds__(PICK_THREADS) void k_sample_pick(const uint32_t* __
     if (counts_out) counts_out[token] = counts_out[token] + 1u;
 }
 
+// ---- top-k path ----------------------------------------------------------
+// The kept set of the rule is the K smallest 64-bit keys (key32 << 32 | index),
+// key32 = ~order_bits(z).  With a histogram of key32's top 12 bits the bucket
+// holding the K-th key is known; the keys of that bucket and of every smaller
+// one are the candidates (usually a few hundred), gathered and sorted in one
+// workgroup's LDS.  When they exceed TK_CAP, the pick selects the K keys
+// exactly with three more histogram levels over all keys and a scan in index
+// order for ties -- slower, same result.
+
+// Keys in index order (T > 0) and the bucket counts of their top 12 bits.
+__global__ __launch_bounds__(SORT_THREADS) void k_topk_hist(SortIn in, uint32_t* __restrict__ keys32,
+                                                           uint32_t* __restrict__ ghist) {
+    __shared__ uint32_t h[TK_BINS];
+    const int t = threadIdx.x, b = blockIdx.x;
+    for (int i = t; i < TK_BINS; i += SORT_THREADS) h[i] = 0u;
+    uint32_t k[SORT_IPT], ix[SORT_IPT];
+    load_tile<0>(in, b, k, ix);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < SORT_IPT; j++) {
+        const int p = b * SORT_TILE + j * SORT_THREADS + t;
+        if (p < in.V) {
+            keys32[p] = k[j];
+            atomicAdd(&h[k[j] >> 20], 1u);
+        }
+    }
+    __syncthreads();
+    for (int i = t; i < TK_BINS; i += SORT_THREADS)
+        if (h[i]) atomicAdd(&ghist[i], h[i]);
+}
+
+// Block-wide: the smallest bin whose inclusive prefix count reaches `need`
+// (bins [0, PER * blockDim)); *cum: that prefix.  `hist` may be global or
+// LDS; sh: [blockDim / 64 + 2] scratch.  The bin is clamped into range (the
+// callers' totals always reach `need`).
+template <int PER>
+__device__ void prefix_bin(const uint32_t* hist, uint32_t need, uint32_t* sh, int* bin, uint32_t* cum) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6, nw = blockDim.x >> 6;
+    const int nbins = PER * (int)blockDim.x;
+    uint32_t v[PER];
+    uint32_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        v[i] = hist[t * PER + i];
+        mine += v[i];
+    }
+    uint32_t inc = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += o;
+    }
+    __syncthreads();
+    if (lane == 63) sh[w] = inc;
+    __syncthreads();
+    uint32_t run = inc - mine;
+    for (int q = 0; q < w; q++) run += sh[q];
+    if (t == 0) {
+        sh[nw] = (uint32_t)(nbins - 1);
+        sh[nw + 1] = 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        if (run < need && run + v[i] >= need) {
+            sh[nw] = (uint32_t)(t * PER + i);
+            sh[nw + 1] = run + v[i];
+        }
+        run += v[i];
+    }
+    __syncthreads();
+    *bin = min((int)sh[nw], nbins - 1);
+    *cum = sh[nw + 1];
+    __syncthreads();
+}
+
+// Candidates: every key whose top 12 bits are at most the boundary bucket's.
+__global__ __launch_bounds__(SORT_THREADS) void k_topk_gather(SortIn in, const uint32_t* __restrict__ keys32,
+                                                             const uint32_t* __restrict__ ghist,
+                                                             uint32_t* __restrict__ counter,
+                                                             unsigned long long* __restrict__ cand) {
+    __shared__ uint32_t sh[SORT_THREADS / 64 + 2];
+    const int t = threadIdx.x, b = blockIdx.x, lane = t & 63;
+    int beta;
+    uint32_t cum;
+    prefix_bin<TK_BINS / SORT_THREADS>(ghist, (uint32_t)kept(in.cfg, in.V), sh, &beta, &cum);
+    if (cum > (uint32_t)TK_CAP) return;  // the pick selects exactly instead
+#pragma unroll
+    for (int j = 0; j < SORT_IPT; j++) {
+        const int p = b * SORT_TILE + j * SORT_THREADS + t;
+        const uint32_t key = p < in.V ? keys32[p] : 0xFFFFFFFFu;
+        const bool take = p < in.V && (int)(key >> 20) <= beta;
+        const unsigned long long m = __ballot(take);
+        uint32_t base = 0;
+        if (lane == 0 && m) base = atomicAdd(counter, (uint32_t)__popcll(m));
+        base = __shfl(base, 0, 64);
+        const uint32_t pos = base + lanes_below(m);
+        if (take && pos < (uint32_t)TK_CAP) cand[pos] = ((unsigned long long)key << 32) | (uint32_t)p;
+    }
+}
+
+// Exclusive count of `flag` over the threads before this one (block-wide);
+// *total: the block's count.  sh: [blockDim / 64 + 1].
+__device__ uint32_t block_excl_count(bool flag, uint32_t* sh, uint32_t* total) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6, nw = blockDim.x >> 6;
+    const unsigned long long m = __ballot(flag);
+    __syncthreads();
+    if (lane == 0) sh[w] = (uint32_t)__popcll(m);
+    __syncthreads();
+    uint32_t before = lanes_below(m), tot = 0;
+    for (int q = 0; q < nw; q++) {
+        if (q < w) before += sh[q];
+        tot += sh[q];
+    }
+    *total = tot;
+    return before;
+}
+
+// Bucket counts of (key >> shift) & mask over the keys whose key >> pshift
+// equals prefix, all V keys read by the block (loads eight deep).
+__device__ void refine_hist(const uint32_t* __restrict__ keys32, int V, int pshift, uint32_t prefix, int shift,
+                            uint32_t mask, uint32_t* hist) {
+    for (int i0 = threadIdx.x; i0 < V; i0 += 8 * PICK_THREADS) {
+        uint32_t k[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) k[u] = keys32[min(i0 + u * PICK_THREADS, V - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i0 + u * PICK_THREADS < V && (k[u] >> pshift) == prefix) atomicAdd(&hist[(k[u] >> shift) & mask], 1u);
+    }
+}
+
+struct TopkShared {
+    unsigned long long sb[TK_CAP];  // candidate keys, then the sorted kept set
+    uint32_t hist[TK_BINS];
+    unsigned long long wsum[PICK_THREADS / 64];
+    uint32_t sh[PICK_THREADS / 64 + 2];
+    unsigned long long c_hit;
+    uint32_t first_j, n_taken;
+};
+
+// The kept set sorted into sb[0, K): the candidates when they fit, else the
+// exact selection.
+__device__ void topk_select(TopkShared& s, const uint32_t* __restrict__ keys32, const uint32_t* __restrict__ ghist,
+                            const unsigned long long* __restrict__ cand, int V, int K) {
+    const int t = threadIdx.x;
+    int beta;
+    uint32_t cum;
+    prefix_bin<TK_BINS / PICK_THREADS>(ghist, (uint32_t)K, s.sh, &beta, &cum);
+    int n = (int)cum;
+    if (cum <= (uint32_t)TK_CAP) {
+        for (int i = t; i < n; i += PICK_THREADS) s.sb[i] = cand[i];
+    } else {
+        // level 2: bits 19..8 inside bucket beta
+        const uint32_t need1 = (uint32_t)K - (cum - ghist[beta]);
+        for (int i = t; i < TK_BINS; i += PICK_THREADS) s.hist[i] = 0u;
+        __syncthreads();
+        refine_hist(keys32, V, 20, (uint32_t)beta, 8, 0xFFFu, s.hist);
+        __syncthreads();
+        int b2;
+        uint32_t c2;
+        prefix_bin<TK_BINS / PICK_THREADS>(s.hist, need1, s.sh, &b2, &c2);
+        const uint32_t need2 = need1 - (c2 - s.hist[b2]);
+        const uint32_t p24 = ((uint32_t)beta << 12) | (uint32_t)b2;
+        // level 3: bits 7..0 inside that bucket
+        __syncthreads();
+        for (int i = t; i < PICK_THREADS; i += PICK_THREADS) s.hist[i] = 0u;
+        __syncthreads();
+        refine_hist(keys32, V, 8, p24, 0, 0xFFu, s.hist);
+        __syncthreads();
+        int b3;
+        uint32_t c3;
+        prefix_bin<1>(s.hist, need2, s.sh, &b3, &c3);  // bins 256 .. 1023 stay zero
+        const uint32_t need3 = need2 - (c3 - s.hist[b3]);
+        const uint32_t v = (p24 << 8) | (uint32_t)b3;
+        // every key below v, and the need3 lowest indices holding v
+        if (t == 0) s.n_taken = 0u;
+        uint32_t eq_seen = 0;
+        for (int c0 = 0; c0 < V; c0 += PICK_THREADS) {
+            const int i = c0 + t;
+            const uint32_t key = i < V ? keys32[i] : 0xFFFFFFFFu;
+            const bool less = i < V && key < v, eq = i < V && key == v;
+            uint32_t eq_tot;
+            const uint32_t eq_rank = block_excl_count(eq, s.sh, &eq_tot);
+            if (less || (eq && eq_seen + eq_rank < need3)) {
+                const uint32_t pos = atomicAdd(&s.n_taken, 1u);
+                if (pos < (uint32_t)TK_CAP) s.sb[pos] = ((unsigned long long)key << 32) | (uint32_t)i;
+            }
+            eq_seen += eq_tot;
+        }
+        __syncthreads();
+        n = (int)min(s.n_taken, (uint32_t)TK_CAP);
+    }
+    // bitonic sort of sb[0, N), N the power of two >= n, padding at the top
+    int N = 2;
+    while (N < n) N <<= 1;
+    for (int i = n + t; i < N; i += PICK_THREADS) s.sb[i] = ~0ull;
+    __syncthreads();
+    for (int kk = 2; kk <= N; kk <<= 1)
+        for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+            for (int i = t; i < N; i += PICK_THREADS) {
+                const int ixj = i ^ jj;
+                if (ixj > i) {
+                    const unsigned long long a = s.sb[i], c = s.sb[ixj];
+                    if ((i & kk) == 0 ? a > c : a < c) {
+                        s.sb[i] = c;
+                        s.sb[ixj] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+}
+
+// The pick over the sorted kept set (K <= 1024 entries, one per thread), the
+// step bookkeeping, and the histogram and counter cleared for the next call.
+__global__ __launch_bounds__(PICK_THREADS) void k_topk_pick(const uint32_t* __restrict__ keys32,
+                                                            uint32_t* __restrict__ ghist, uint32_t* __restrict__ counter,
+                                                            const unsigned long long* __restrict__ cand, int V,
+                                                            const SampleCfg* cfg, int* d_step, uint32_t* d_tok,
+                                                            uint32_t* tokens_out, int* d_pos, uint32_t* counts_out) {
+    __shared__ TopkShared s;
+    const int t = threadIdx.x;
+    const int step = *d_step;
+    const int K = kept(cfg, V);
+    topk_select(s, keys32, ghist, cand, V, K);
+    const float z0 = key_value((uint32_t)(s.sb[0] >> 32));
+    const unsigned long long w = t < K ? weight_of(key_value((uint32_t)(s.sb[t] >> 32)), z0) : 0ull;
+    const unsigned long long C = block_scan_u64(w, s.wsum);
+    if (t == K - 1) s.c_hit = C;
+    __syncthreads();
+    const unsigned long long S = s.c_hit;
+    unsigned long long c_end = S;
+    __syncthreads();
+    if (cfg->top_p < 1.0f) {
+        const unsigned long long p24 = (unsigned long long)(cfg->top_p * 16777216.0f);
+        const unsigned long long thr = mul_shr24(S, p24, true);
+        if (t == 0) s.first_j = 0xFFFFFFFFu;
+        __syncthreads();
+        if (t < K && C >= thr) atomicMin(&s.first_j, (uint32_t)t);
+        __syncthreads();
+        if ((uint32_t)t == s.first_j) s.c_hit = C;
+        __syncthreads();
+        if (s.first_j != 0xFFFFFFFFu) c_end = s.c_hit;
+    }
+    const uint64_t h = splitmix64(cfg->seed + (uint64_t)(uint32_t)step * 0x9E3779B97F4A7C15ull);
+    const unsigned long long r = mul_shr24(c_end, h >> 40, false);
+    __syncthreads();
+    if (t == 0) s.first_j = 0xFFFFFFFFu;
+    __syncthreads();
+    if (c_end > 0 && t < K && C > r) atomicMin(&s.first_j, (uint32_t)t);
+    __syncthreads();
+    const uint32_t j = s.first_j;
+    const uint32_t token = (uint32_t)s.sb[j < (uint32_t)K ? j : 0u];
+    for (int i = t; i < TK_BINS; i += PICK_THREADS) ghist[i] = 0u;
+    if (t != 0) return;
+    *counter = 0u;
+    *d_tok = token;
+    if (tokens_out) tokens_out[step] = token;
+    *d_step = step + 1;
+    if (d_pos) *d_pos = *d_pos + 1;
+    if (counts_out) counts_out[token] = counts_out[token] + 1u;
+}
+
 inline size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct SampleWork {
+    uint32_t *ghist, *counter;
+    unsigned long long* cand;
     uint32_t *ka, *kb, *ia, *ib, *planes;
     unsigned long long* part;
 };
 
 int sort_tiles(int vocab) { return (vocab + SORT_TILE - 1) / SORT_TILE; }
 int row_stride(int vocab) { return (sort_tiles(vocab) + 3) & ~3; }
+constexpr size_t ZERO_BYTES = ((size_t)TK_BINS * 4 + 4 + 255) & ~(size_t)255;
 
+// top-k histogram | counter (zeroed region) | candidates [TK_CAP] |
 // ka | kb | ia | ib ([vocab] each) | count planes [4][256][row] | tile weights
 size_t work_layout(int vocab, void* base, SampleWork* w) {
+    const size_t z = ZERO_BYTES, c = up256((size_t)TK_CAP * 8);
     const size_t v = up256((size_t)vocab * 4), h = up256((size_t)4 * RADIX * row_stride(vocab) * 4);
     char* p = (char*)base;
     if (w) {
+        w->ghist = (uint32_t*)p;
+        w->counter = (uint32_t*)(p + (size_t)TK_BINS * 4);
+        w->cand = (unsigned long long*)(p + z);
+        p += z + c;
         w->ka = (uint32_t*)p;
         w->kb = (uint32_t*)(p + v);
         w->ia = (uint32_t*)(p + 2 * v);
@@ -397,7 +672,7 @@ size_t work_layout(int vocab, void* base, SampleWork* w) {
         w->planes = (uint32_t*)(p + 4 * v);
         w->part = (unsigned long long*)(p + 4 * v + h);
     }
-    return 4 * v + h + up256((size_t)sort_tiles(vocab) * 8);
+    return z + c + 4 * v + h + up256((size_t)sort_tiles(vocab) * 8);
 }
 
 template <int PASS>
@@ -413,6 +688,8 @@ lq8_status sort_pass(hipStream_t s, SortIn in, uint32_t* planes, uint32_t* keys_
 }  // namespace
 
 size_t sample_work_bytes(int vocab) { return work_layout(vocab, nullptr, nullptr); }
+size_t sample_work_zero_bytes(int) { return ZERO_BYTES; }
+bool sample_topk_path(const SampleCfg& c) { return c.temperature > 0.0f && c.top_k >= 1 && c.top_k <= TK_MAXK; }
 
 lq8_status launch_sample(hipStream_t s, const SampleLaunch& a) {
     if (a.vocab <= 0 || a.vocab > MAX_VOCAB) return fail(LQ8_ERR_INVALID_ARG, "sample: vocabulary outside 1 .. 2^20");
@@ -420,6 +697,18 @@ lq8_status launch_sample(hipStream_t s, const SampleLaunch& a) {
     SampleWork w;
     work_layout(a.vocab, a.work, &w);
     SortIn in{a.logits, a.counts, a.cfg, nullptr, nullptr, a.vocab, sort_tiles(a.vocab), row_stride(a.vocab)};
+    if (a.topk) {
+        hipLaunchKernelGGL(k_topk_hist, dim3(in.nb), dim3(SORT_THREADS), 0, s, in, w.ka, w.ghist);
+        LQ8_HIP(hipGetLastError());
+        hipLaunchKernelGGL(k_topk_gather, dim3(in.nb), dim3(SORT_THREADS), 0, s, in, (const uint32_t*)w.ka,
+                           (const uint32_t*)w.ghist, w.counter, w.cand);
+        LQ8_HIP(hipGetLastError());
+        hipLaunchKernelGGL(k_topk_pick, dim3(1), dim3(PICK_THREADS), 0, s, (const uint32_t*)w.ka, w.ghist, w.counter,
+                           (const unsigned long long*)w.cand, a.vocab, a.cfg, a.d_step, a.d_tok, a.tokens_out, a.d_pos,
+                           a.counts_out);
+        LQ8_HIP(hipGetLastError());
+        return LQ8_OK;
+    }
     lq8_status st;
     if ((st = sort_pass<0>(s, in, w.planes, w.ka, w.ia))) return st;
     in.keys = w.ka;
@@ -488,6 +777,8 @@ extern "C" lq8_status lq8_sample_device(lq8_ctx* ctx, const float* d_logits, siz
     a.d_step = (int*)(base + 64);
     a.d_tok = d_token;
     a.work = base + 256;
+    a.topk = sample_topk_path(sc);
+    LQ8_HIP(hipMemsetAsync(a.work, 0, sample_work_zero_bytes(V), ctx->stream));
     if ((st = launch_sample(ctx->stream, a))) return st;
     LQ8_HIP(hipStreamSynchronize(ctx->stream));
     return LQ8_OK;

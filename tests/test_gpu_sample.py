@@ -79,6 +79,36 @@ def test_sample_small_vocab_ties(ctx, V):
             assert g == o, (V, cfg, step, g, o)
 
 
+@pytest.mark.parametrize("case", ["flat", "integer", "dense"])
+def test_sample_topk_exact_selection(ctx, case):
+    """top_k up to 1024 selects candidates by the top 12 bits of the key; when
+    the boundary bucket holds more than 4096 keys the pick selects the K keys
+    exactly (two more histogram levels, ties by index).  Flat logits (every key
+    tied), integer logits (few values) and 151936 distinct values packed into
+    one bucket all take that route; top_k 1024 / 1025 sit on either side of
+    the path boundary."""
+    V = 151936
+    rng = np.random.default_rng(17)
+    if case == "flat":
+        logits = np.zeros(V, np.float32)
+    elif case == "integer":
+        logits = rng.integers(-3, 4, V).astype(np.float32)
+    else:
+        logits = (np.float32(1.0) + rng.permutation(V).astype(np.float32) * np.float32(2.0**-23)).astype(np.float32)
+    counts = np.zeros(V, np.uint32)
+    counts[rng.integers(0, V, 200)] = 1
+    dl, dc = lq8.DeviceBuffer.from_array(ctx, logits), lq8.DeviceBuffer.from_array(ctx, counts)
+    try:
+        for cfg in [(1.0, 50, 1.0, 1.0), (0.7, 1024, 0.9, 1.0), (1.3, 1, 1.0, 1.0), (1.0, 700, 0.5, 1.2),
+                    (1.0, 1025, 1.0, 1.0)]:
+            for step in range(3):
+                g, o = run_pair(ctx, logits, counts, cfg, 3, step, dl, dc)
+                assert g == o, (case, cfg, step, g, o)
+    finally:
+        dl.free()
+        dc.free()
+
+
 def test_sample_extreme_values(ctx):
     """Signed zeros, huge magnitudes and a single finite winner."""
     x = np.array([-0.0, 0.0, 3e38, -3e38, 1e-45, -1e-45, 5.0, 5.0], np.float32)
