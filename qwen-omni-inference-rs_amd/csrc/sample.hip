@@ -454,15 +454,20 @@ __device__ void prefix_bin(const uint32_t* hist, uint32_t need, uint32_t* sh, in
 }
 
 // Candidates: every key whose top 12 bits are at most the boundary bucket's.
+// Block 0 also leaves the boundary bucket and its prefix count in meta[0..1].
 __global__ __launch_bounds__(SORT_THREADS) void k_topk_gather(SortIn in, const uint32_t* __restrict__ keys32,
                                                              const uint32_t* __restrict__ ghist,
-                                                             uint32_t* __restrict__ counter,
+                                                             uint32_t* __restrict__ counter, uint32_t* __restrict__ meta,
                                                              unsigned long long* __restrict__ cand) {
     __shared__ uint32_t sh[SORT_THREADS / 64 + 2];
     const int t = threadIdx.x, b = blockIdx.x, lane = t & 63;
     int beta;
     uint32_t cum;
     prefix_bin<TK_BINS / SORT_THREADS>(ghist, (uint32_t)kept(in.cfg, in.V), sh, &beta, &cum);
+    if (b == 0 && t == 0) {
+        meta[0] = (uint32_t)beta;
+        meta[1] = cum;
+    }
     if (cum > (uint32_t)TK_CAP) return;  // the pick selects exactly instead
 #pragma unroll
     for (int j = 0; j < SORT_IPT; j++) {
@@ -518,14 +523,15 @@ struct TopkShared {
     uint32_t first_j, n_taken;
 };
 
-// The kept set sorted into sb[0, K): the candidates when they fit, else the
-// exact selection.
-__device__ void topk_select(TopkShared& s, const uint32_t* __restrict__ keys32, const uint32_t* __restrict__ ghist,
-                            const unsigned long long* __restrict__ cand, int V, int K) {
+// The kept set sorted, returned (its first K entries): the candidates when
+// they fit, else the exact selection.  Up to 1024 entries: a rank sort (keys
+// are distinct) into the histogram's space; more: bitonic in place.
+__device__ const unsigned long long* topk_select(TopkShared& s, const uint32_t* __restrict__ keys32,
+                                                 const uint32_t* __restrict__ ghist, const uint32_t* __restrict__ meta,
+                                                 const unsigned long long* __restrict__ cand, int V, int K) {
     const int t = threadIdx.x;
-    int beta;
-    uint32_t cum;
-    prefix_bin<TK_BINS / PICK_THREADS>(ghist, (uint32_t)K, s.sh, &beta, &cum);
+    const int beta = min((int)meta[0], TK_BINS - 1);
+    const uint32_t cum = meta[1];
     int n = (int)cum;
     if (cum <= (uint32_t)TK_CAP) {
         for (int i = t; i < n; i += PICK_THREADS) s.sb[i] = cand[i];
@@ -570,6 +576,18 @@ __device__ void topk_select(TopkShared& s, const uint32_t* __restrict__ keys32, 
         __syncthreads();
         n = (int)min(s.n_taken, (uint32_t)TK_CAP);
     }
+    __syncthreads();
+    if (n <= PICK_THREADS) {
+        unsigned long long* out = (unsigned long long*)s.hist;
+        const unsigned long long mine = t < n ? s.sb[t] : 0ull;
+        uint32_t rank = 0;
+        if (t < n)
+            for (int j = 0; j < n; j++) rank += s.sb[j] < mine ? 1u : 0u;
+        __syncthreads();
+        if (t < n) out[rank] = mine;
+        __syncthreads();
+        return out;
+    }
     // bitonic sort of sb[0, N), N the power of two >= n, padding at the top
     int N = 2;
     while (N < n) N <<= 1;
@@ -589,12 +607,14 @@ __device__ void topk_select(TopkShared& s, const uint32_t* __restrict__ keys32, 
             }
             __syncthreads();
         }
+    return s.sb;
 }
 
 // The pick over the sorted kept set (K <= 1024 entries, one per thread), the
 // step bookkeeping, and the histogram and counter cleared for the next call.
 __global__ __launch_bounds__(PICK_THREADS) void k_topk_pick(const uint32_t* __restrict__ keys32,
                                                             uint32_t* __restrict__ ghist, uint32_t* __restrict__ counter,
+                                                            const uint32_t* __restrict__ meta,
                                                             const unsigned long long* __restrict__ cand, int V,
                                                             const SampleCfg* cfg, int* d_step, uint32_t* d_tok,
                                                             uint32_t* tokens_out, int* d_pos, uint32_t* counts_out) {
@@ -602,9 +622,9 @@ __global__ __launch_bounds__(PICK_THREADS) void k_topk_pick(const uint32_t* __re
     const int t = threadIdx.x;
     const int step = *d_step;
     const int K = kept(cfg, V);
-    topk_select(s, keys32, ghist, cand, V, K);
-    const float z0 = key_value((uint32_t)(s.sb[0] >> 32));
-    const unsigned long long w = t < K ? weight_of(key_value((uint32_t)(s.sb[t] >> 32)), z0) : 0ull;
+    const unsigned long long* sorted = topk_select(s, keys32, ghist, meta, cand, V, K);
+    const float z0 = key_value((uint32_t)(sorted[0] >> 32));
+    const unsigned long long w = t < K ? weight_of(key_value((uint32_t)(sorted[t] >> 32)), z0) : 0ull;
     const unsigned long long C = block_scan_u64(w, s.wsum);
     if (t == K - 1) s.c_hit = C;
     __syncthreads();
@@ -630,7 +650,7 @@ __global__ __launch_bounds__(PICK_THREADS) void k_topk_pick(const uint32_t* __re
     if (c_end > 0 && t < K && C > r) atomicMin(&s.first_j, (uint32_t)t);
     __syncthreads();
     const uint32_t j = s.first_j;
-    const uint32_t token = (uint32_t)s.sb[j < (uint32_t)K ? j : 0u];
+    const uint32_t token = (uint32_t)sorted[j < (uint32_t)K ? j : 0u];
     for (int i = t; i < TK_BINS; i += PICK_THREADS) ghist[i] = 0u;
     if (t != 0) return;
     *counter = 0u;
@@ -644,7 +664,7 @@ __global__ __launch_bounds__(PICK_THREADS) void k_topk_pick(const uint32_t* __re
 inline size_t up256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct SampleWork {
-    uint32_t *ghist, *counter;
+    uint32_t *ghist, *counter, *meta;
     unsigned long long* cand;
     uint32_t *ka, *kb, *ia, *ib, *planes;
     unsigned long long* part;
@@ -653,16 +673,18 @@ struct SampleWork {
 int sort_tiles(int vocab) { return (vocab + SORT_TILE - 1) / SORT_TILE; }
 int row_stride(int vocab) { return (sort_tiles(vocab) + 3) & ~3; }
 constexpr size_t ZERO_BYTES = ((size_t)TK_BINS * 4 + 4 + 255) & ~(size_t)255;
+constexpr size_t META_OFF = ZERO_BYTES;  // boundary bucket and prefix count, written by the gather
 
-// top-k histogram | counter (zeroed region) | candidates [TK_CAP] |
+// top-k histogram | counter (zeroed region) | meta | candidates [TK_CAP] |
 // ka | kb | ia | ib ([vocab] each) | count planes [4][256][row] | tile weights
 size_t work_layout(int vocab, void* base, SampleWork* w) {
-    const size_t z = ZERO_BYTES, c = up256((size_t)TK_CAP * 8);
+    const size_t z = ZERO_BYTES + 256, c = up256((size_t)TK_CAP * 8);
     const size_t v = up256((size_t)vocab * 4), h = up256((size_t)4 * RADIX * row_stride(vocab) * 4);
     char* p = (char*)base;
     if (w) {
         w->ghist = (uint32_t*)p;
         w->counter = (uint32_t*)(p + (size_t)TK_BINS * 4);
+        w->meta = (uint32_t*)(p + META_OFF);
         w->cand = (unsigned long long*)(p + z);
         p += z + c;
         w->ka = (uint32_t*)p;
@@ -701,10 +723,10 @@ lq8_status launch_sample(hipStream_t s, const SampleLaunch& a) {
         hipLaunchKernelGGL(k_topk_hist, dim3(in.nb), dim3(SORT_THREADS), 0, s, in, w.ka, w.ghist);
         LQ8_HIP(hipGetLastError());
         hipLaunchKernelGGL(k_topk_gather, dim3(in.nb), dim3(SORT_THREADS), 0, s, in, (const uint32_t*)w.ka,
-                           (const uint32_t*)w.ghist, w.counter, w.cand);
+                           (const uint32_t*)w.ghist, w.counter, w.meta, w.cand);
         LQ8_HIP(hipGetLastError());
         hipLaunchKernelGGL(k_topk_pick, dim3(1), dim3(PICK_THREADS), 0, s, (const uint32_t*)w.ka, w.ghist, w.counter,
-                           (const unsigned long long*)w.cand, a.vocab, a.cfg, a.d_step, a.d_tok, a.tokens_out, a.d_pos,
+                           (const uint32_t*)w.meta, (const unsigned long long*)w.cand, a.vocab, a.cfg, a.d_step, a.d_tok, a.tokens_out, a.d_pos,
                            a.counts_out);
         LQ8_HIP(hipGetLastError());
         return LQ8_OK;
