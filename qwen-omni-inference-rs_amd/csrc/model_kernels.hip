@@ -226,11 +226,12 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     const float* Vc = a.v_cache + (size_t)kvh * a.max_pos * 128;
     const int js = c * SEG;
     // Loads that do not depend on the position go out before it arrives: the
-    // K/V rows of the first ATT_EARLY_SEGS segments (almost always in use;
-    // later segments wait, so a long cache's idle workgroups load nothing)
-    // and this wave's first head vector (q head `wave`, or the new k / v).
+    // K/V rows of the first ATT_EARLY_SEGS segments of a single sequence
+    // (almost always in use; later segments, and batches, whose idle
+    // workgroups would multiply the waste, wait) and this wave's first head
+    // vector (q head `wave`, or the new k / v).
     float4 kreg[ATT_F4], vreg[ATT_F4];
-    const bool early = c < ATT_EARLY_SEGS;
+    const bool early = c < ATT_EARLY_SEGS && gridDim.z == 1;
     if (early) seg_load_capacity(Kc, Vc, js, a.max_pos, kreg, vreg);
     float h0 = 0.0f, h1 = 0.0f, n0 = 0.0f, n1 = 0.0f;
     if (wave < G + 2) {
