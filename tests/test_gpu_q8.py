@@ -119,6 +119,34 @@ def test_gemv_edge_shapes(ctx, n, k):
     assert_parity(y, ref)
 
 
+@pytest.mark.parametrize("n,k", [(48, 12288), (17, 12256)])
+def test_gemv_maximum_k(ctx, n, k):
+    """The largest input the GEMV stages (12288 = 384 blocks, and one block
+    short of it: an odd block count at the limit)."""
+    y, ref = gemv_case(ctx, n, k, 3 * n + k)
+    assert_parity(y, ref)
+
+
+def test_gemv_above_maximum_k_is_an_error(ctx):
+    """k past the staging limit is refused (ShapeMismatch), never run on a
+    fallback; the same weight still multiplies through the GEMM at m > 1."""
+    k = 12288 + 32
+    blocks = oracle.quantize_q8_0(normal((16, k), 0.02, 5))
+    w = lq8.Q8Weight.from_blocks(ctx, blocks, 16, k)
+    dx = lq8.DeviceBuffer(ctx, 2 * k * 4)
+    dy = lq8.DeviceBuffer(ctx, 2 * 16 * 4)
+    try:
+        with pytest.raises(lq8.ShapeMismatch):
+            lq8._check(lq8.lib().lq8_gemv_q8_0_device(ctx.handle, w.handle, dx.ptr, dy.ptr))
+        x = normal((2, k), 1.0, 6)
+        dx.upload(x)
+        lq8._check(lq8.lib().lq8_gemm_q8_0_device(ctx.handle, w.handle, dx.ptr, 2, dy.ptr))
+        y = dy.download(np.float32, 32).reshape(2, 16)
+        assert np.array_equal(y, oracle.gemm_q8_0(blocks, 16, k, x).reshape(2, 16))
+    finally:
+        dx.free(); dy.free(); w.free()
+
+
 def test_gemv_known_answer(ctx):
     """test_linear_forward (src/attention.rs:605) on Q8_0-exact weights.
 
