@@ -421,8 +421,9 @@ __global__ __launch_bounds__(256) void k_gemv_grouped(const GemvProblemDev* __re
 // group of CH pairs) items, unpacks each 16-byte code chunk to floats once
 // and runs the GEMV order of gemv_tiles for every staged vector; the group
 // sums go to LDS and one thread per (vector, row) runs the tree over the
-// groups.  PF (one vector per problem): the wave's first item's weights are
-// issued before the input staging and every item prefetches the next one.
+// groups.  PF: the wave's first item's weights are issued before the input
+// staging and every item prefetches the wave's next one (across staging
+// passes too).
 template <int XS, int EPI, int CH, int VB, bool PF>
 __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
     extern __shared__ float smem[];
@@ -439,8 +440,11 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int k = a.k, k4 = k >> 2, nb = k >> 5, np = (nb + 1) >> 1;
     const int G = (np + CH - 1) / CH;
-    float* xs = smem;                    // [VB][np * 64]
-    float* gs = xs + VB * np * 64;       // [VB][NT][G][16]
+    // a staged vector spans G * CH pairs: a group's chunks past np read this
+    // padding (in bounds, values unused) at fixed offsets from the group's first
+    const int xstride = G * CH * 64;
+    float* xs = smem;                    // [VB][xstride]
+    float* gs = xs + VB * xstride;       // [VB][NT][G][16]
     float* red = gs + VB * NT * G * 16;  // [VB]
     const int r = lane & 15, part = lane >> 4, bsel = part >> 1, half = part & 1;
     const size_t gt = (size_t)e * a.prob_tiles + tile;
@@ -460,12 +464,18 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
             ps[i] = sbase[ttc * sstep + (size_t)c * 32];                                                    \
         }                                                                                                   \
     }
-    if (PF) MV_LOAD_ITEM(wave);
-    // norm weights with the inputs (4 float4 per thread cover k <= 4096)
+    // norm weights first (4 float4 per thread cover k <= 4096), then the PF
+    // weights: memory counters complete in issue order, so the norm weights'
+    // early use (their bf16 rounding) does not wait for the codes
     float4 nw[4];
     if (XS == XS_RMSNORM) {
 #pragma unroll
         for (int j = 0; j < 4; j++) nw[j] = *(const float4*)(a.norm_w + 4 * min(tid + 256 * j, k4 - 1));
+    }
+    if (PF) {
+        if (XS == XS_RMSNORM) __builtin_amdgcn_sched_barrier(0);
+        MV_LOAD_ITEM(wave);
+        __builtin_amdgcn_sched_barrier(0);  // the codes ahead of the input staging's waits
     }
     for (int v0 = blockIdx.y * VB; v0 < vcnt; v0 += gridDim.y * VB) {
         const int nv = min(VB, vcnt - v0);
@@ -474,7 +484,7 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
             const int ent = vbeg + v0 + v;
             const int slot = a.slots ? a.slots[ent] : ent;
             const float* x = a.x + (size_t)(slot / a.x_div) * a.x_stride;
-            float* xv = xs + v * np * 64;
+            float* xv = xs + v * xstride;
             for (int i4 = tid; i4 < k4; i4 += 256) {
                 const float4 g = *(const float4*)(x + 4 * i4);
                 float4 o;
@@ -494,7 +504,7 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
         if (XS == XS_RMSNORM) {
             // SUM64 order per vector (wave v), as the single-vector staging
             if (wave < nv) {
-                const float* xv = xs + wave * np * 64;
+                const float* xv = xs + wave * xstride;
                 float acc = 0.0f;
                 for (int i0 = lane; i0 < k; i0 += 64 * 8) {
                     float v[8];
@@ -510,7 +520,7 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
             __syncthreads();
             for (int v = 0; v < nv; v++) {
                 const float inv = red[v];
-                float* xv = xs + v * np * 64;
+                float* xv = xs + v * xstride;
 #pragma unroll
                 for (int j = 0; j < 4; j++)
                     if (tid + 256 * j < k4) {
@@ -535,52 +545,146 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
                 cv[i] = pv[i];
                 ds[i] = ps[i];
             }
-            if (PF) MV_LOAD_ITEM(it + 4);  // the next item's weights while this one computes
-            float wf[CH][16];
-#pragma unroll
-            for (int i = 0; i < CH; i++) {
-                const uint32_t w4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    wf[i][4 * q] = (float)(int8_t)(w4[q] & 0xFF);
-                    wf[i][4 * q + 1] = (float)(int8_t)((w4[q] >> 8) & 0xFF);
-                    wf[i][4 * q + 2] = (float)(int8_t)((w4[q] >> 16) & 0xFF);
-                    wf[i][4 * q + 3] = (float)(int8_t)(w4[q] >> 24);
-                }
+            if (PF) {
+                // the wave's next item while this one computes: the next of this
+                // pass, else the wave's first of the next pass (after the last
+                // item a clamped reload: unconditional, so that no wait for it is
+                // placed where the paths join)
+                const int nx = it + 4 < items || v0 + (int)gridDim.y * VB >= vcnt ? it + 4 : wave;
+                MV_LOAD_ITEM(nx);
             }
             const int cnt = min(CH, np - g * CH);
             float dsf[CH];
 #pragma unroll
             for (int i = 0; i < CH; i++) dsf[i] = f16_bits_to_f32(ds[i]);
-            for (int v = 0; v < nv; v++) {
-                const float* xv = xs + v * np * 64;
-                float t[CH];
+            if constexpr (VB > 1) {
+                // Vector pairs (a, b) = (2pp, 2pp + 1) share every lane exchange; a
+                // vector left over pairs with itself (b = a, no second chain).
+                // Chunk-outer: one chunk's codes are unpacked at a time and used by
+                // every staged vector.  After rows16 and the scale, s[pp][i] holds
+                // in its rows (a, 2p) (b, 2p) (a, 2p+1) (b, 2p+1) of pair
+                // p = g*CH + i; halves32 of s[pp][i] and s[pp][i + CH/2] gives the
+                // pair values of chunk i (rows 0, 1) and chunk i + CH/2 (rows 2, 3),
+                // so the tree over t[] runs the lower and upper half of the group
+                // side by side and the last halves32 adds the halves.  A chunk past
+                // np enters as -0.0, which leaves any sum unchanged (a + -0.0 == a
+                // bit for bit), so partial groups keep the one-vector order.
+                constexpr int NPP = VB / 2;
+                float s[NPP][CH];
 #pragma unroll
                 for (int i = 0; i < CH; i++) {
-                    const int p = min(g * CH + i, np - 1);
-                    const float* xp = xv + (2 * p + bsel) * 32 + half * 16;
-                    float h = 0.0f;
+                    float w[16];
+                    const uint32_t w4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        const float4 xq = *(const float4*)(xp + 4 * q);
-                        h = fmaf(wf[i][4 * q], xq.x, h);
-                        h = fmaf(wf[i][4 * q + 1], xq.y, h);
-                        h = fmaf(wf[i][4 * q + 2], xq.z, h);
-                        h = fmaf(wf[i][4 * q + 3], xq.w, h);
+                        w[4 * q] = (float)(int8_t)(w4[q] & 0xFF);
+                        w[4 * q + 1] = (float)(int8_t)((w4[q] >> 8) & 0xFF);
+                        w[4 * q + 2] = (float)(int8_t)((w4[q] >> 16) & 0xFF);
+                        w[4 * q + 3] = (float)(int8_t)(w4[q] >> 24);
                     }
-                    // h0 + h1 (half-0 lane's sum first) and v_2p + v_2p+1, v_2p alone
-                    // when block 2p + 1 is the padding of an odd nb
-                    const LanePair hh = lanes16(h);
-                    const float vb = (hh.lo + hh.hi) * dsf[i];
-                    const LanePair vv = lanes32(vb);
-                    t[i] = 2 * p + 1 >= nb ? vv.lo : vv.lo + vv.hi;
+                    const int off = (2 * (g * CH + i) + bsel) * 32 + half * 16;
+#pragma unroll
+                    for (int pp = 0; pp < NPP; pp++) {
+                        if (2 * pp >= nv) continue;
+                        const float* xa = xs + 2 * pp * xstride + off;
+                        float ha = 0.0f, hb = 0.0f;
+                        if (2 * pp + 1 < nv) {
+                            const float* xb = xa + xstride;
+#pragma unroll
+                            for (int q = 0; q < 4; q++) {
+                                const float4 xq = *(const float4*)(xa + 4 * q);
+                                const float4 xr = *(const float4*)(xb + 4 * q);
+                                ha = fmaf(w[4 * q], xq.x, ha);
+                                hb = fmaf(w[4 * q], xr.x, hb);
+                                ha = fmaf(w[4 * q + 1], xq.y, ha);
+                                hb = fmaf(w[4 * q + 1], xr.y, hb);
+                                ha = fmaf(w[4 * q + 2], xq.z, ha);
+                                hb = fmaf(w[4 * q + 2], xr.z, hb);
+                                ha = fmaf(w[4 * q + 3], xq.w, ha);
+                                hb = fmaf(w[4 * q + 3], xr.w, hb);
+                            }
+                        } else {
+#pragma unroll
+                            for (int q = 0; q < 4; q++) {
+                                const float4 xq = *(const float4*)(xa + 4 * q);
+                                ha = fmaf(w[4 * q], xq.x, ha);
+                                ha = fmaf(w[4 * q + 1], xq.y, ha);
+                                ha = fmaf(w[4 * q + 2], xq.z, ha);
+                                ha = fmaf(w[4 * q + 3], xq.w, ha);
+                            }
+                            hb = ha;
+                        }
+                        const LanePair hh = rows16(ha, hb);
+                        s[pp][i] = (hh.lo + hh.hi) * dsf[i];
+                    }
                 }
 #pragma unroll
-                for (int s = 1; s < CH; s *= 2)
+                for (int pp = 0; pp < NPP; pp++) {
+                    if (2 * pp >= nv) continue;
+                    float t[CH > 1 ? CH / 2 : 1];
+                    if constexpr (CH == 1) {
+                        const LanePair vv = halves32(s[pp][0], s[pp][0]);
+                        t[0] = 2 * g + 1 >= nb ? vv.lo : vv.lo + vv.hi;
+                    } else {
 #pragma unroll
-                    for (int i = 0; i + s < CH; i += 2 * s)
-                        if (i + s < cnt) t[i] = t[i] + t[i + s];
-                if (lane < 16) gs[((v * NT + tt) * G + g) * 16 + lane] = t[0];
+                        for (int i = 0; i < CH / 2; i++) {
+                            const LanePair vv = halves32(s[pp][i], s[pp][i + CH / 2]);
+                            const int p = g * CH + i + (lane >= 32 ? CH / 2 : 0);
+                            t[i] = p >= np ? -0.0f : 2 * p + 1 >= nb ? vv.lo : vv.lo + vv.hi;
+                        }
+#pragma unroll
+                        for (int s2 = 1; s2 < CH / 2; s2 *= 2)
+#pragma unroll
+                            for (int i = 0; i + s2 < CH / 2; i += 2 * s2) t[i] = t[i] + t[i + s2];
+                        const LanePair hl = halves32(t[0], t[0]);
+                        t[0] = hl.lo + hl.hi;
+                    }
+                    if (lane < (2 * pp + 1 < nv ? 32 : 16))
+                        gs[(((2 * pp + (lane >> 4)) * NT + tt) * G + g) * 16 + (lane & 15)] = t[0];
+                }
+            } else {
+                float wf[CH][16];
+#pragma unroll
+                for (int i = 0; i < CH; i++) {
+                    const uint32_t w4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        wf[i][4 * q] = (float)(int8_t)(w4[q] & 0xFF);
+                        wf[i][4 * q + 1] = (float)(int8_t)((w4[q] >> 8) & 0xFF);
+                        wf[i][4 * q + 2] = (float)(int8_t)((w4[q] >> 16) & 0xFF);
+                        wf[i][4 * q + 3] = (float)(int8_t)(w4[q] >> 24);
+                    }
+                }
+                for (int v = 0; v < nv; v++) {
+                    const float* xv = xs + v * xstride;
+                    float t[CH];
+#pragma unroll
+                    for (int i = 0; i < CH; i++) {
+                        const int p = g * CH + i;  // past np: padding, skipped by the tree
+                        const float* xp = xv + (2 * p + bsel) * 32 + half * 16;
+                        float h = 0.0f;
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const float4 xq = *(const float4*)(xp + 4 * q);
+                            h = fmaf(wf[i][4 * q], xq.x, h);
+                            h = fmaf(wf[i][4 * q + 1], xq.y, h);
+                            h = fmaf(wf[i][4 * q + 2], xq.z, h);
+                            h = fmaf(wf[i][4 * q + 3], xq.w, h);
+                        }
+                        // h0 + h1 (half-0 lane's sum first) and v_2p + v_2p+1, v_2p alone
+                        // when block 2p + 1 is the padding of an odd nb
+                        const LanePair hh = lanes16(h);
+                        const float vb = (hh.lo + hh.hi) * dsf[i];
+                        const LanePair vv = lanes32(vb);
+                        t[i] = 2 * p + 1 >= nb ? vv.lo : vv.lo + vv.hi;
+                    }
+#pragma unroll
+                    for (int s = 1; s < CH; s *= 2)
+#pragma unroll
+                        for (int i = 0; i + s < CH; i += 2 * s)
+                            if (i + s < cnt) t[i] = t[i] + t[i + s];
+                    if (lane < 16) gs[((v * NT + tt) * G + g) * 16 + lane] = t[0];
+                }
             }
         }
         __syncthreads();
@@ -834,7 +938,8 @@ lq8_status mv_vb(hipStream_t s, const MvArgs& a, dim3 grid, int vb, size_t xs_fl
     const size_t NT = EPI == EPI_SWIGLU ? 2 : 1;
     const size_t smem = ((size_t)vb * xs_floats_per_vec + (size_t)vb * NT * G * 16 + 4) * sizeof(float);
     if (smem > 64 * 1024) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: input staging exceeds 64 KiB of LDS");
-    // single vector and more items than waves: the pipelined variant
+    // single vector and more items than waves: the pipelined variant (with
+    // several vectors the prefetch registers cost more occupancy than it hides)
     if (a.max_vec == 1 && NT * G > 4) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 1, true>), grid, dim3(256), smem, s, a);
     else if (vb == 4) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 4, false>), grid, dim3(256), smem, s, a);
     else if (vb == 2) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 2, false>), grid, dim3(256), smem, s, a);
@@ -848,7 +953,7 @@ lq8_status mv_ch(hipStream_t s, const MvArgs& a, int max_probs, int vsplit) {
     const int nb = a.k >> 5, np = (nb + 1) >> 1;
     const int ch = pick_ch(np, 4);
     const int G = (np + ch - 1) / ch;
-    const size_t per_vec = (size_t)np * 64;
+    const size_t per_vec = (size_t)G * ch * 64;  // np pairs padded to whole groups
     // vectors staged per pass: as many as fit in 40 KiB
     int vb = per_vec * 4 * sizeof(float) <= 40 * 1024 ? 4 : per_vec * 2 * sizeof(float) <= 40 * 1024 ? 2 : 1;
     if (a.max_vec == 1 && (EPI == EPI_SWIGLU ? 2 : 1) * G > 4) vb = 1;  // the pipelined variant stages one vector

@@ -89,6 +89,21 @@ __device__ __forceinline__ LanePair lanes16(float v) {
     return {__uint_as_float(p[0]), __uint_as_float(p[1])};
 }
 
+// Two registers through one swap (rows are 16-lane groups, halves 32-lane
+// groups; a == b gives lanes16 / lanes32):
+//   rows16(a, b):   .lo = rows (a0, b0, a2, b2), .hi = rows (a1, b1, a3, b3)
+//   halves32(a, b): .lo = halves (a0, b0),       .hi = halves (a1, b1)
+// so .lo + .hi sums the row (half) pairs of both registers at once.
+__device__ __forceinline__ LanePair rows16(float a, float b) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return {__uint_as_float(p[0]), __uint_as_float(p[1])};
+}
+
+__device__ __forceinline__ LanePair halves32(float a, float b) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return {__uint_as_float(p[0]), __uint_as_float(p[1])};
+}
+
 template <int D>
 __device__ __forceinline__ float lane_xor(float v) {
     static_assert(D == 1 || D == 2 || D == 4 || D == 8 || D == 16 || D == 32, "xor distance");
