@@ -424,13 +424,15 @@ __global__ __launch_bounds__(256) void k_gemv_grouped(const GemvProblemDev* __re
 // groups.  PF: the wave's first item's weights are issued before the input
 // staging and every item prefetches the wave's next one (across staging
 // passes too).
-template <int XS, int EPI, int CH, int VB, bool PF>
+template <int XS, int EPI, int CH, int VB, bool PF, int NTS>
 __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
     extern __shared__ float smem[];
-    constexpr int NT = EPI == EPI_SWIGLU ? 2 : 1;  // tiles per workgroup
+    // tiles per workgroup: gate tile i with up tile i + rows/32 (EPI_SWIGLU),
+    // else NTS consecutive tiles from `tile` (the host keeps tiles % NTS == 0)
+    constexpr int NT = EPI == EPI_SWIGLU ? 2 : NTS;
     const int tiles_all = (a.rows + TILE_ROWS - 1) / TILE_ROWS;
-    const int tiles_p = tiles_all / NT, tstride = tiles_all / NT;
-    const int j = blockIdx.x / tiles_p, tile = blockIdx.x - j * tiles_p;
+    const int tiles_p = tiles_all / NT, tstride = EPI == EPI_SWIGLU ? tiles_all / 2 : 1;
+    const int j = blockIdx.x / tiles_p, tile = (blockIdx.x - j * tiles_p) * (EPI == EPI_SWIGLU ? 1 : NTS);
     if (j >= (a.n_prob ? *a.n_prob : 1)) return;
     const int e = a.prob_id ? a.prob_id[j] : j;
     const int vbeg = a.vec_begin ? a.vec_begin[j] : 0;
@@ -696,7 +698,7 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
                 for (int i = 0; i + s < G; i += 2 * s) col[i * 16] = col[i * 16] + col[(i + s) * 16];
             if (EPI != EPI_SWIGLU) {
                 const float acc = col[0];
-                const int row = tile * TILE_ROWS + rr;
+                const int row = (tile + tt) * TILE_ROWS + rr;
                 if (row < a.rows) {
                     const int ent = vbeg + v0 + v;
                     const int slot = a.slots ? a.slots[ent] : ent;
@@ -933,35 +935,48 @@ lq8_status launch_gemv_grouped(hipStream_t s, const GemvProblemDev* d_probs, int
 
 namespace {
 
-template <int XS, int EPI, int CH>
+template <int XS, int EPI, int CH, int NTS>
 lq8_status mv_vb(hipStream_t s, const MvArgs& a, dim3 grid, int vb, size_t xs_floats_per_vec, int G) {
-    const size_t NT = EPI == EPI_SWIGLU ? 2 : 1;
+    const size_t NT = EPI == EPI_SWIGLU ? 2 : NTS;
     const size_t smem = ((size_t)vb * xs_floats_per_vec + (size_t)vb * NT * G * 16 + 4) * sizeof(float);
     if (smem > 64 * 1024) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: input staging exceeds 64 KiB of LDS");
     // single vector and more items than waves: the pipelined variant (with
     // several vectors the prefetch registers cost more occupancy than it hides)
-    if (a.max_vec == 1 && NT * G > 4) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 1, true>), grid, dim3(256), smem, s, a);
-    else if (vb == 4) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 4, false>), grid, dim3(256), smem, s, a);
-    else if (vb == 2) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 2, false>), grid, dim3(256), smem, s, a);
-    else hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 1, false>), grid, dim3(256), smem, s, a);
+    if (a.max_vec == 1 && NT * G > 4)
+        hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 1, true, NTS>), grid, dim3(256), smem, s, a);
+    else if (vb == 4) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 4, false, NTS>), grid, dim3(256), smem, s, a);
+    else if (vb == 2) hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 2, false, NTS>), grid, dim3(256), smem, s, a);
+    else hipLaunchKernelGGL((k_gemv_mv<XS, EPI, CH, 1, false, NTS>), grid, dim3(256), smem, s, a);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
 
-template <int XS, int EPI>
-lq8_status mv_ch(hipStream_t s, const MvArgs& a, int max_probs, int vsplit) {
+template <int XS, int EPI, int NTS>
+lq8_status mv_nts(hipStream_t s, const MvArgs& a, int max_probs, int vsplit) {
     const int nb = a.k >> 5, np = (nb + 1) >> 1;
     const int ch = pick_ch(np, 4);
     const int G = (np + ch - 1) / ch;
     const size_t per_vec = (size_t)G * ch * 64;  // np pairs padded to whole groups
     // vectors staged per pass: as many as fit in 40 KiB
     int vb = per_vec * 4 * sizeof(float) <= 40 * 1024 ? 4 : per_vec * 2 * sizeof(float) <= 40 * 1024 ? 2 : 1;
-    if (a.max_vec == 1 && (EPI == EPI_SWIGLU ? 2 : 1) * G > 4) vb = 1;  // the pipelined variant stages one vector
-    const int tiles_p = (a.rows + TILE_ROWS - 1) / TILE_ROWS / (EPI == EPI_SWIGLU ? 2 : 1);
+    if (a.max_vec == 1 && (EPI == EPI_SWIGLU ? 2 : NTS) * G > 4) vb = 1;  // the pipelined variant stages one vector
+    const int tiles_p = (a.rows + TILE_ROWS - 1) / TILE_ROWS / (EPI == EPI_SWIGLU ? 2 : NTS);
     const dim3 grid((unsigned)(tiles_p * max_probs), (unsigned)vsplit);
-    if (ch == 1) return mv_vb<XS, EPI, 1>(s, a, grid, vb, per_vec, G);
-    if (ch == 2) return mv_vb<XS, EPI, 2>(s, a, grid, vb, per_vec, G);
-    return mv_vb<XS, EPI, 4>(s, a, grid, vb, per_vec, G);
+    if (ch == 1) return mv_vb<XS, EPI, 1, NTS>(s, a, grid, vb, per_vec, G);
+    if (ch == 2) return mv_vb<XS, EPI, 2, NTS>(s, a, grid, vb, per_vec, G);
+    return mv_vb<XS, EPI, 4, NTS>(s, a, grid, vb, per_vec, G);
+}
+
+template <int XS, int EPI>
+lq8_status mv_ch(hipStream_t s, const MvArgs& a, int max_probs, int vsplit) {
+    if constexpr (XS == XS_PLAIN && EPI == EPI_STORE) {
+        // routed problem lists of several vectors (the experts' down
+        // projections at batch > 1): 4 consecutive tiles per workgroup, the
+        // inputs staged once for all of them
+        const int tiles_all = (a.rows + TILE_ROWS - 1) / TILE_ROWS;
+        if (max_probs > 1 && a.max_vec > 1 && tiles_all % 4 == 0) return mv_nts<XS, EPI, 4>(s, a, max_probs, vsplit);
+    }
+    return mv_nts<XS, EPI, 1>(s, a, max_probs, vsplit);
 }
 
 }  // namespace

@@ -58,14 +58,17 @@ def test_moe_batched_decode(ctx):
     run_steps(ctx, cfg, tens, 5, [0, 3, 63, 64, 130], 3, 24)
 
 
-def test_moe_partial_groups_odd_blocks(ctx):
+@pytest.mark.parametrize("hidden", [320, 288])
+def test_moe_partial_groups_odd_blocks(ctx, hidden):
     """Shapes whose block-pair groups end part-way: hidden 320 (10 blocks, 5
-    pairs in groups of 2: the last group holds one pair) and expert
-    intermediate 672 (21 blocks, the last pair half padding; 11 pairs in
-    groups of 4: the last holds three), with 6 experts top-4 over 7 sequences
-    so that experts see 3 to 7 vectors (pairs of vectors, a vector left over,
-    more than one staging pass)."""
-    cfg = MoeCfg(hidden_size=320, expert_intermediate_size=672, num_experts=6, top_k=4, max_positions=96,
+    pairs in groups of 2: the last group holds one pair; 20 output tiles, so
+    the batched down projection takes 4 tiles per workgroup) or 288 (9
+    blocks, the last pair half padding; 18 tiles: one per workgroup), and
+    expert intermediate 672 (21 blocks; 11 pairs in groups of 4: the last
+    holds three), with 6 experts top-4 over 7 sequences so that experts see 3
+    to 7 vectors (pairs of vectors, a vector left over, more than one staging
+    pass)."""
+    cfg = MoeCfg(hidden_size=hidden, expert_intermediate_size=672, num_experts=6, top_k=4, max_positions=96,
                  max_batch=8, num_layers=2)
     tens = moe_tensors(cfg, 41)
     run_steps(ctx, cfg, tens, 7, [0, 1, 2, 40, 63, 64, 90], 2, 42)
