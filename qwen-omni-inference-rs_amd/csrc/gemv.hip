@@ -645,34 +645,15 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
                         gs[(((2 * pp + (lane >> 4)) * NT + tt) * G + g) * 16 + (lane & 15)] = t[0];
                 }
             } else {
-                float wf[CH][16];
-#pragma unroll
-                for (int i = 0; i < CH; i++) {
-                    const uint32_t w4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        wf[i][4 * q] = (float)(int8_t)(w4[q] & 0xFF);
-                        wf[i][4 * q + 1] = (float)(int8_t)((w4[q] >> 8) & 0xFF);
-                        wf[i][4 * q + 2] = (float)(int8_t)((w4[q] >> 16) & 0xFF);
-                        wf[i][4 * q + 3] = (float)(int8_t)(w4[q] >> 24);
-                    }
-                }
+                // one vector per pass: each chunk's codes are unpacked as the
+                // chain uses them (no unpacked copy held across chunks)
                 for (int v = 0; v < nv; v++) {
                     const float* xv = xs + v * xstride;
                     float t[CH];
 #pragma unroll
                     for (int i = 0; i < CH; i++) {
                         const int p = g * CH + i;  // past np: padding, skipped by the tree
-                        const float* xp = xv + (2 * p + bsel) * 32 + half * 16;
-                        float h = 0.0f;
-#pragma unroll
-                        for (int q = 0; q < 4; q++) {
-                            const float4 xq = *(const float4*)(xp + 4 * q);
-                            h = fmaf(wf[i][4 * q], xq.x, h);
-                            h = fmaf(wf[i][4 * q + 1], xq.y, h);
-                            h = fmaf(wf[i][4 * q + 2], xq.z, h);
-                            h = fmaf(wf[i][4 * q + 3], xq.w, h);
-                        }
+                        const float h = dot16(cv[i], xv + (2 * p + bsel) * 32 + half * 16);
                         // h0 + h1 (half-0 lane's sum first) and v_2p + v_2p+1, v_2p alone
                         // when block 2p + 1 is the padding of an odd nb
                         const LanePair hh = lanes16(h);
