@@ -95,6 +95,36 @@ def test_moe_batch_invariance(ctx):
         one.free()
 
 
+def test_moe_forward_device_equals_host(ctx):
+    """lq8_moe_forward_device (hidden state, scores and positions in HBM, the
+    hidden state updated in place) gives the bits of lq8_moe_forward, at
+    batch 1 and 5, from a cleared cache."""
+    cfg = MoeCfg(num_experts=16, top_k=4, max_positions=96, max_batch=8, num_layers=2)
+    gpu = lq8.Qwen3MoeLayers.load(ctx, lq8_cfg(cfg), moe_tensors(cfg, 51))
+    rng = np.random.default_rng(52)
+    try:
+        for T, pos in ((1, [7]), (5, [0, 9, 63, 64, 90])):
+            x = rng.standard_normal((T, cfg.hidden_size)).astype(np.float32)
+            scores = rng.standard_normal((cfg.num_layers, T, cfg.num_experts)).astype(np.float32)
+            p = np.array(pos, np.int32)
+            gpu.clear_kv_cache()
+            host = gpu.forward(x, scores, p)
+            gpu.clear_kv_cache()
+            dh = lq8.DeviceBuffer.from_array(ctx, x)
+            ds = lq8.DeviceBuffer.from_array(ctx, scores)
+            dp = lq8.DeviceBuffer.from_array(ctx, p)
+            try:
+                gpu.forward_device(dh, ds, dp, T)
+                dev = dh.download(np.float32, T * cfg.hidden_size).reshape(T, cfg.hidden_size)
+            finally:
+                dh.free()
+                ds.free()
+                dp.free()
+            assert_bits(dev, host, f"T={T}")
+    finally:
+        gpu.free()
+
+
 def test_moe_rejects_bad_calls(ctx):
     cfg = MoeCfg(num_experts=16, top_k=4, max_positions=64, max_batch=2)
     gpu = lq8.Qwen3MoeLayers.load(ctx, lq8_cfg(cfg), moe_tensors(cfg, 27))

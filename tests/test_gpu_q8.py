@@ -247,6 +247,29 @@ def test_linear_forward_dispatch(ctx):
     lin.weight.free()
 
 
+def test_linear_forward_device_equals_host(ctx):
+    """lq8_linear_forward_device (inputs and outputs already in HBM) gives the
+    bits of lq8_linear_forward, on the GEMV (m = 1) and GEMM (m > 1) paths."""
+    n, k = 384, 1024
+    blocks = oracle.quantize_q8_0(normal((n, k), 0.02, 31))
+    lin = lq8.Linear.new(lq8.Q8Weight.from_blocks(ctx, blocks, n, k))
+    try:
+        for m in (1, 5):
+            x = normal((m, k), 1.0, 32 + m)
+            host = lin.forward(x.reshape(1, m, k)).reshape(m, n)
+            dx = lq8.DeviceBuffer.from_array(ctx, x)
+            dy = lq8.DeviceBuffer(ctx, m * n * 4)
+            try:
+                lin.forward_device(dx, m, dy)
+                dev = dy.download(np.float32, m * n).reshape(m, n)
+            finally:
+                dx.free()
+                dy.free()
+            assert np.array_equal(dev.view(np.uint32), host.view(np.uint32)), m
+    finally:
+        lin.weight.free()
+
+
 def test_grouped_gemv(ctx):
     shapes = [(2048, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (1024, 3072), (100, 96)]
     probs, refs, bufs, ws = [], [], [], []
