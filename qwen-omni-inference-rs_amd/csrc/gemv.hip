@@ -850,15 +850,17 @@ template <int XS, int EPI>
 lq8_status launch_one(hipStream_t s, const GemvArgs& a) {
     const int nb = a.k >> 5, np = (nb + 1) >> 1;
     const int tiles = (a.n + TILE_ROWS - 1) / TILE_ROWS;
-    // Many tiles (lm_head): 4 pairs per item, 4 tiles per 4-wave workgroup
-    // (one staged input serves 64 rows, each wave loops over its items with
-    // the next item's weights prefetched); few tiles: one tile per workgroup
-    // and up to 16 waves to spread it over the CU.
+    // Many tiles (lm_head): 4 pairs per item, 4-wave workgroups with the next
+    // item's weights prefetched; a plain input takes one tile per workgroup,
+    // a transformed one (RMSNorm) is staged once for 2 tiles (151936 x 1024:
+    // 26.8 / 27.9 / 29.2 us plain and 1246 / 1248 / 1244 decode tok/s at 1 / 2
+    // / 4 tiles).  Few tiles: one tile per workgroup and up to 16 waves to
+    // spread it over the CU.
     int ch, tpw, waves;
     const int wmax = tiles >= 1024 ? 4 : MAX_WAVES;
     if (tiles >= 1024) {
         ch = MAX_CH;
-        tpw = 4;
+        tpw = XS == XS_PLAIN ? 1 : 2;
     } else {
         ch = pick_ch(np, MAX_WAVES);
         tpw = 1;
