@@ -145,7 +145,7 @@ def cpu_gemv_all_cores(seconds_target=4.0):
 
 
 def cpu_decode(cfg, tensors, prompt, steps=3):
-    """Config-4 decode on the host: the oracle's Qwen3-0.6B forward (the
+    """Qwen3-0.6B batch-1 decode on the host: the oracle's forward (the
     reference's decoder numerics over Q8_0 weights), a few single-token steps
     on one core after a 128-token prefill run on all cores (not timed)."""
     import oracle
