@@ -97,7 +97,7 @@ def gemv_case(ctx, n, k, seed, x_std=1.0):
     return y, oracle.gemv_q8_0(blocks, n, k, x)
 
 
-def test_gemv_config1_3072x1024(ctx):
+def test_gemv_3072x1024(ctx):
     y, ref = gemv_case(ctx, 3072, 1024, 11)
     assert_parity(y, ref)
 
@@ -180,7 +180,7 @@ def gemm_case(ctx, m, n, k, seed):
 
 
 @pytest.mark.parametrize("n,k", [(3072, 1024), (1024, 3072)])
-def test_gemm_config3_m512(ctx, n, k):
+def test_gemm_m512(ctx, n, k):
     y, ref = gemm_case(ctx, 512, n, k, n)
     assert_parity(y, ref)
 
