@@ -223,6 +223,31 @@ def moe_stack(ctx, layers=48, reps=10):
     return out
 
 
+def gemm_sweep(ctx):
+    """W8A8 GEMM (activation quantize + int8 MFMA) of the gate/up (3072 x 1024)
+    and down (1024 x 3072) weights at M = 512 ... 8192: per-call time by HIP
+    events over 20 calls and the fraction of the dense int8 peak."""
+    for n, k in ((3072, 1024), (1024, 3072)):
+        w = lq8.Q8Weight.random(ctx, n, k, seed=3, stream=n)
+        lin = lq8.Linear.new(w)
+        for m in (512, 1024, 2048, 4096, 8192):
+            x = lq8.DeviceBuffer.from_array(ctx, np.random.default_rng(m).standard_normal((m, k)).astype(np.float32))
+            y = lq8.DeviceBuffer(ctx, m * n * 4)
+            for _ in range(3):
+                lin.forward_device(x, m, y)
+            ctx.synchronize()
+            ctx.timer_start()
+            for _ in range(20):
+                lin.forward_device(x, m, y)
+            ms = ctx.timer_stop() / 20
+            tops = 2 * m * n * k / (ms * 1e-3) / 1e12
+            print(f"{n}x{k} M={m}: {ms * 1e3:8.2f} us  {tops:7.1f} TOPS  {tops / INT8_PEAK_TOPS * 100:5.2f} % of int8 peak",
+                  flush=True)
+            x.free()
+            y.free()
+        w.free()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -233,7 +258,12 @@ def main():
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--only-step", action="store_true",
                     help="only the headline step and the calibration copy (for hardware-counter runs)")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="only the W8A8 GEMM at M = 512 ... 8192 (gate/up and down shapes), one line each")
     args = ap.parse_args()
+    if args.gemm_sweep:
+        gemm_sweep(lq8.Context(0))
+        return
     if args.only_step:
         args.no_decode = args.no_cpu = args.no_moe = True
     if args.gpus != 1:
