@@ -63,6 +63,15 @@
 static int g_seq_sums = 0;
 void orc_set_sequential_sums(int on) { g_seq_sums = on ? 1 : 0; }
 
+/* 1 (default): RmsNorm rounds its input, weight and output to bf16 as the
+ * reference does.  0: those roundings are skipped.  Used only by the tests
+ * that pin the decoder's structure against a float64 restatement, where a
+ * bf16 rounding that lands on the other side of a midpoint (an f32-vs-f64
+ * difference of one ulp) would otherwise hide everything else. */
+static int g_bf16_sites = 1;
+void orc_set_bf16_rounding(int on) { g_bf16_sites = on ? 1 : 0; }
+static inline float site_bf16(float x) { return g_bf16_sites ? orc_bf16_round(x) : x; }
+
 /* Thread count of the parallel loops (each output is still summed by one
  * thread in the fixed order, so results do not depend on it). */
 void orc_set_threads(int n) {
@@ -321,8 +330,22 @@ int orc_gemm_q8_0(const uint8_t* w, size_t n_out, size_t k_in, const float* x, s
     return 0;
 }
 
+/* 1 (default): more than one row goes through the W8A8 GEMM (activation
+ * rows quantized to Q8_0).  0: every row goes through the W8A32 GEMV, which
+ * the structure-pinning tests use so that an activation code landing on the
+ * other side of a rounding midpoint cannot hide the rest of the decoder. */
+static int g_act_quant = 1;
+void orc_set_activation_quantization(int on) { g_act_quant = on ? 1 : 0; }
+
 int orc_linear_forward(const uint8_t* w, size_t n_out, size_t k_in, const float* x, size_t m, float* y) {
     if (m == 1) return orc_gemv_q8_0(w, n_out, k_in, x, y);
+    if (!g_act_quant) {
+        for (size_t i = 0; i < m; i++) {
+            int rc = orc_gemv_q8_0(w, n_out, k_in, x + i * k_in, y + i * n_out);
+            if (rc) return rc;
+        }
+        return 0;
+    }
     return orc_gemm_q8_0(w, n_out, k_in, x, m, y);
 }
 
@@ -334,15 +357,15 @@ int orc_linear_forward(const uint8_t* w, size_t n_out, size_t k_in, const float*
  * inv = 1/sqrt(mean + eps), out = bf16((x*inv)*w). */
 static void rms_norm_row(const float* x, const float* w, size_t dim, float eps, float* y, float* scratch) {
     for (size_t i = 0; i < dim; i++) {
-        float v = orc_bf16_round(x[i]);
+        float v = site_bf16(x[i]);
         scratch[i] = v * v;
     }
     float ss = sum64(scratch, dim);
     float mean = ss / (float)dim;
     float inv = 1.0f / sqrtf(mean + eps);
     for (size_t i = 0; i < dim; i++) {
-        float v = orc_bf16_round(x[i]);
-        y[i] = orc_bf16_round((v * inv) * orc_bf16_round(w[i]));
+        float v = site_bf16(x[i]);
+        y[i] = site_bf16((v * inv) * site_bf16(w[i]));
     }
 }
 

@@ -36,6 +36,12 @@ void orc_expf_n(const float* x, float* y, size_t n);
 /* 0 = canonical orders (what the GPU computes), 1 = the reference's plain
  * sequential sums.  Global switch, used only to compare the two. */
 void orc_set_sequential_sums(int on);
+/* 1 (default) = RmsNorm's bf16 roundings as the reference; 0 = skipped (tests
+ * that pin the decoder structure against a float64 restatement). */
+void orc_set_bf16_rounding(int on);
+/* 1 (default) = rows > 1 through the W8A8 GEMM; 0 = every row through the
+ * W8A32 GEMV (the same structure-pinning tests). */
+void orc_set_activation_quantization(int on);
 void orc_set_threads(int n);
 
 /* ---- Q8_0 format ---- */

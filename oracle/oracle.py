@@ -59,6 +59,8 @@ def lib():
             "orc_expf_n": (None, [vp, vp, sz]),
             "orc_set_sequential_sums": (None, [C.c_int]),
             "orc_set_threads": (None, [C.c_int]),
+            "orc_set_bf16_rounding": (None, [C.c_int]),
+            "orc_set_activation_quantization": (None, [C.c_int]),
             "orc_quantize_q8_0": (C.c_int, [vp, sz, vp]),
             "orc_dequantize_q8_0": (C.c_int, [vp, sz, vp]),
             "orc_gemv_q8_0": (C.c_int, [vp, sz, sz, vp, vp]),
@@ -124,6 +126,18 @@ def expf(x) -> np.ndarray:
 
 def set_sequential_sums(on: bool) -> None:
     lib().orc_set_sequential_sums(1 if on else 0)
+
+
+def set_bf16_rounding(on: bool) -> None:
+    """RmsNorm's bf16 roundings on (the default, the reference's numerics)
+    or off (only to pin the decoder structure against a float64 restatement)."""
+    lib().orc_set_bf16_rounding(1 if on else 0)
+
+
+def set_activation_quantization(on: bool) -> None:
+    """Rows > 1 through the W8A8 GEMM (the default) or every row through
+    the W8A32 GEMV (only to pin the decoder structure)."""
+    lib().orc_set_activation_quantization(1 if on else 0)
 
 
 def set_threads(n: int) -> None:
