@@ -110,6 +110,23 @@ lq8_status lq8_weight_free(lq8_weight* w);
  * Activation quantizer of the W8A8 path, as a standalone op: d_x f32 [n] ->
  * d_blocks AoS Q8_0 on the device.  Bit-exact with lq8_quantize_q8_0. */
 lq8_status lq8_quantize_q8_0_device(lq8_ctx* ctx, const float* d_x, size_t n, void* d_blocks);
+/* The activation operand of the W8A8 GEMM, as GGUF blocks [m][k / 32]:
+ * rows quantized by the very kernels lq8_linear_forward (m > 1) and the
+ * model's prefill run, each bit-exact with lq8_quantize_q8_0 of its input.
+ *   LQ8_ACT_PLAIN:    rows d_x [m][k] as they are;
+ *   LQ8_ACT_RMSNORM:  RmsNorm (src/rms_norm.rs:143-176) of rows d_x [m][k]
+ *                     with weight d_w [k] and eps, fused into the quantizer
+ *                     (the prefill input norms);
+ *   LQ8_ACT_SILU_MUL: silu(gate) * up of rows d_x [m][2k] = [gate | up]
+ *                     (src/mlp.rs:151-164), fused (the prefill down input).
+ * Works in the context's scratch buffer; enqueued without synchronizing.
+ * Replaces: the planned activation quantizer of the Q8_0 matmul
+ * (docs/architecture/arch-2026-01-31-qwen3-omni-q8-rust.md:36-39). */
+#define LQ8_ACT_PLAIN 0
+#define LQ8_ACT_RMSNORM 1
+#define LQ8_ACT_SILU_MUL 2
+lq8_status lq8_quantize_activations_device(lq8_ctx* ctx, int source, const float* d_x, const float* d_w, size_t m,
+                                          size_t k, float eps, void* d_blocks);
 /* Rows [row0, row0+nrows) of W dequantized to f32 [nrows, k_in]: the
  * Embedding::forward row gather on a Q8_0 table (src/embedding.rs:137-152). */
 lq8_status lq8_weight_dequantize_rows_device(lq8_ctx* ctx, const lq8_weight* w, size_t row0, size_t nrows,
@@ -201,7 +218,14 @@ typedef struct {
     double decode_tokens_per_s;
     uint32_t used_graph;    /* 1 if the decode step ran as a replayed HIP graph */
 } lq8_gen_stats;
-/* Greedy generation; the token loop stays on the device.  out_tokens: max_new. */
+/* Greedy generation; the token loop stays on the device.  out_tokens: max_new.
+ * Each decode step forwards the token generated last.  The reference's loop
+ * as written does not: the `let next_token` in its loop body
+ * (src/generate.rs:650) shadows the binding of src/generate.rs:632 only for
+ * the rest of that iteration, so src/generate.rs:647 forwards the FIRST
+ * generated token at every step.  lq8_generate_ex with
+ * LQ8_GEN_FEED_FIRST_TOKEN reproduces that loop; the two agree only while
+ * the model repeats its first token. */
 lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
                                uint32_t* out_tokens, lq8_gen_stats* stats);
 
@@ -255,6 +279,14 @@ lq8_status lq8_sample_device(lq8_ctx* ctx, const float* d_logits, size_t vocab, 
 lq8_status lq8_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
                         const lq8_sampling* cfg, const uint32_t* eos_ids, size_t n_eos, uint32_t* out_tokens,
                         size_t* n_out, lq8_gen_stats* stats);
+/* lq8_generate with flags.  LQ8_GEN_FEED_FIRST_TOKEN: every decode step
+ * forwards the first generated token, the reference's generate() loop as
+ * written (src/generate.rs:632-650; see lq8_generate_greedy).  Replaces the
+ * same generate() as lq8_generate. */
+#define LQ8_GEN_FEED_FIRST_TOKEN 1u
+lq8_status lq8_generate_ex(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                           const lq8_sampling* cfg, const uint32_t* eos_ids, size_t n_eos, uint32_t flags,
+                           uint32_t* out_tokens, size_t* n_out, lq8_gen_stats* stats);
 lq8_status lq8_model_free(lq8_model* m);
 
 /* ---- Qwen3-MoE decoder layers (Qwen3-30B-A3B style), decode steps --------

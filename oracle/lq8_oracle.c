@@ -247,7 +247,7 @@ int orc_dequantize_q8_0(const uint8_t* blocks, size_t n, float* y) {
 /* Q8_0 GEMV (W8A32) and GEMM (W8A8)                                        */
 /* ------------------------------------------------------------------------ */
 
-#define ORC_MAX_NB 2048 /* k_in <= 65536 */
+#define ORC_MAX_NB 4096 /* k_in <= 131072 */
 
 /* GEMV canonical order (header comment); v is scratch of nb floats. */
 static float gemv_row(const uint8_t* row, size_t nb, const float* x, float* v) {
@@ -662,9 +662,15 @@ static int model_forward(orc_model* m, const uint32_t* ids, size_t n, size_t off
     return 0;
 }
 
-/* src/generate.rs:611-664 with the greedy sampler; no EOS stop. */
-int orc_generate_greedy(orc_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
-                        uint32_t* out_tokens, float* out_margins) {
+/* src/generate.rs:611-664 with the greedy sampler; no EOS stop.
+ * feed_first = 0: each decode step forwards the token generated last (the
+ * loop the library implements).  feed_first = 1: the loop as the reference
+ * writes it -- the `let next_token` inside the loop body (generate.rs:650)
+ * shadows the outer binding (generate.rs:632) only for the rest of that
+ * iteration, so every decode step forwards the FIRST generated token
+ * (generate.rs:647) at offset prefill_len + generated - 1. */
+int orc_generate_greedy_ex(orc_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new, int feed_first,
+                           uint32_t* out_tokens, float* out_margins) {
     if (n_prompt == 0 || max_new == 0) return 1;
     float* logits = (float*)malloc((size_t)m->c.vocab_size * sizeof(float));
     if (!logits) return 2;
@@ -673,7 +679,7 @@ int orc_generate_greedy(orc_model* m, const uint32_t* prompt, size_t n_prompt, s
     uint32_t tok = 0;
     for (size_t t = 0; t < max_new; t++) {
         if (t == 0) rc = orc_model_forward(m, prompt, n_prompt, 0, logits);
-        else rc = orc_model_forward(m, &tok, 1, n_prompt + t - 1, logits);
+        else rc = orc_model_forward(m, feed_first ? &out_tokens[0] : &tok, 1, n_prompt + t - 1, logits);
         if (rc) break;
         tok = orc_argmax_last(logits, m->c.vocab_size);
         out_tokens[t] = tok;
@@ -686,6 +692,11 @@ int orc_generate_greedy(orc_model* m, const uint32_t* prompt, size_t n_prompt, s
     }
     free(logits);
     return rc;
+}
+
+int orc_generate_greedy(orc_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                        uint32_t* out_tokens, float* out_margins) {
+    return orc_generate_greedy_ex(m, prompt, n_prompt, max_new, 0, out_tokens, out_margins);
 }
 
 /* ------------------------------------------------------------------------ */

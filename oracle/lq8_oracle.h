@@ -89,6 +89,10 @@ int orc_model_forward_with_intermediates(orc_model* m, const uint32_t* ids, size
                                          float* final_norm, float* logits);
 int orc_generate_greedy(orc_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
                         uint32_t* out_tokens, float* out_margins);
+/* feed_first = 1: the reference's loop as written (every decode step
+ * forwards the first generated token, src/generate.rs:632-650). */
+int orc_generate_greedy_ex(orc_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new, int feed_first,
+                           uint32_t* out_tokens, float* out_margins);
 
 /* ---- Qwen3-MoE decoder layers (decode step of T independent sequences) ----
  * Tensor table, per layer l, base = (8 + 3 * num_experts) * l:

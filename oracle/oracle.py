@@ -79,6 +79,7 @@ def lib():
             "orc_model_forward": (C.c_int, [vp, vp, sz, sz, vp]),
             "orc_model_forward_with_intermediates": (C.c_int, [vp, vp, sz, sz, vp, vp, vp]),
             "orc_generate_greedy": (C.c_int, [vp, vp, sz, sz, vp, vp]),
+            "orc_generate_greedy_ex": (C.c_int, [vp, vp, sz, sz, C.c_int, vp, vp]),
             "orc_moe_new": (vp, [C.POINTER(OrcMoeConfig), vp]),
             "orc_moe_free": (None, [vp]),
             "orc_moe_route": (C.c_int, [vp, sz, sz, sz, vp, vp]),
@@ -282,21 +283,27 @@ class Model:
             raise ValueError(f"oracle forward failed ({rc})")
         return hidden, fin, logits
 
-    def generate_greedy(self, prompt, max_new: int):
+    def generate_greedy(self, prompt, max_new: int, feed_first: bool = False):
+        """generate() with the greedy sampler.  feed_first: the reference's
+        loop as written, where every decode step forwards the first
+        generated token (src/generate.rs:632-650)."""
         ids = np.ascontiguousarray(prompt, dtype=np.uint32)
         toks = np.empty(max_new, dtype=np.uint32)
         margins = np.empty(max_new, dtype=np.float32)
-        rc = lib().orc_generate_greedy(self.h, _p(ids), ids.size, max_new, _p(toks), _p(margins))
+        rc = lib().orc_generate_greedy_ex(self.h, _p(ids), ids.size, max_new, 1 if feed_first else 0, _p(toks),
+                                          _p(margins))
         if rc:
             raise ValueError(f"oracle generate failed ({rc})")
         return toks, margins
 
     def generate_sampled(self, prompt, max_new: int, temperature: float, top_k: int, top_p: float,
-                         repetition_penalty: float, seed: int, eos_token_ids=()) -> np.ndarray:
+                         repetition_penalty: float, seed: int, eos_token_ids=(), feed_first: bool = False) -> np.ndarray:
         """generate() (src/generate.rs:611-664) with the sampling rule:
         prefill, then one sampled token per step (step t draws with counter t;
         the penalty counts the tokens generated before it); the loop ends at
-        the first token in eos_token_ids, which is kept and not forwarded."""
+        the first token in eos_token_ids, which is kept and not forwarded.
+        feed_first: every decode step forwards the first generated token (the
+        reference's loop as written)."""
         ids = np.ascontiguousarray(prompt, dtype=np.uint32)
         eos = set(int(e) for e in eos_token_ids)
         self.clear_kv_cache()
@@ -310,20 +317,27 @@ class Model:
             if tok in eos:
                 break
             if t + 1 < max_new:
-                logits = self.forward([tok], ids.size + t)
+                logits = self.forward([toks[0] if feed_first else tok], ids.size + t)
         return np.array(toks, dtype=np.uint32)
 
 
-def random_q8_tensors(cfg, seed: int, std: float = 0.02):
-    """Small random model in table order (numpy normal draws, oracle quantizer)."""
+def random_q8_tensors(cfg, seed: int, std: float = 0.02, layer_std: float = None, norm_jitter: float = 0.0):
+    """Small random model in table order (numpy normal draws, oracle quantizer).
+    layer_std: the std of the decoder layers' matrices (default std, the
+    embedding keeps std); norm_jitter: norm weights 1 + jitter * N(0, 1)
+    instead of 1.  A layer_std of 0.08 with norm_jitter 0.1 gives greedy
+    tokens that vary from step to step (the plain N(0, 0.02) model repeats
+    one token)."""
     rng = np.random.default_rng(seed)
     out = []
     for i in range(cfg.tensor_count()):
         kind, shape = cfg.tensor_shape(i)
         if kind == "f32":
-            out.append(np.ones(shape, dtype=np.float32))
+            out.append((1.0 + norm_jitter * rng.standard_normal(shape)).astype(np.float32) if norm_jitter
+                       else np.ones(shape, dtype=np.float32))
         else:
-            w = (rng.standard_normal(shape) * std).astype(np.float32)
+            sd = std if (i == 0 or layer_std is None) else layer_std
+            w = (rng.standard_normal(shape) * sd).astype(np.float32)
             out.append(quantize_q8_0(w))
     return out
 

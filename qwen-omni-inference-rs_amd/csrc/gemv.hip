@@ -413,6 +413,77 @@ __global__ __launch_bounds__(256) void k_gemv_grouped(const GemvProblemDev* __re
     gemv_tiles<XS_PLAIN, EPI_STORE, MAX_CH>(a, t - p.tile_begin, 1, smem);
 }
 
+// ---- inputs longer than the staging limit --------------------------------------
+//
+// k > GEMV_MAX_K (plain input, plain store): one 16-row tile per workgroup; the input is
+// staged LONG_PAIRS block pairs at a time.  LONG_PAIRS is a multiple of
+// LONG_CH, so every group of LONG_CH pairs lies inside one stage, and the
+// group sums meet in the same pairwise tree as in gemv_tiles: the order (and
+// so every bit of y) is the GEMV order of the oracle.
+constexpr int LONG_PAIRS = 128;  // 256 blocks = 8192 values = 32 KiB of LDS per stage
+constexpr int LONG_CH = 4;
+constexpr int LONG_THREADS = 512;
+
+__global__ __launch_bounds__(LONG_THREADS) void k_gemv_long(GemvArgs a) {
+    extern __shared__ float smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int W = blockDim.x >> 6;
+    const int nb = a.k >> 5, np = (nb + 1) >> 1;
+    const int G = (np + LONG_CH - 1) / LONG_CH;
+    float* xs = smem;                    // [LONG_PAIRS * 64] the staged stage
+    float* gs = xs + LONG_PAIRS * 64;    // [G][16] group sums
+    const int tile = blockIdx.x;
+    const int r = lane & 15, part = lane >> 4, bsel = part >> 1, half = part & 1;
+    const int8_t* cbase = a.codes + (size_t)tile * np * CHUNK_BYTES + lane * 16;
+    const uint16_t* sbase = a.scales + (size_t)tile * 2 * np * 16 + bsel * 16 + r;
+    for (int p0 = 0; p0 < np; p0 += LONG_PAIRS) {
+        const int pairs = min(LONG_PAIRS, np - p0);
+        const int e0 = p0 * 64, e1 = min(a.k, (p0 + pairs) * 64);
+        // values past k (the padding block of an odd nb) stage as 0
+        for (int i4 = threadIdx.x; 4 * i4 < pairs * 64; i4 += blockDim.x) {
+            const int e = e0 + 4 * i4;
+            *(float4*)(xs + 4 * i4) = e < e1 ? *(const float4*)(a.x + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        __syncthreads();
+        const int gn = (pairs + LONG_CH - 1) / LONG_CH;
+        for (int g = wave; g < gn; g += W) {
+            u32x4 cv[LONG_CH];
+            uint16_t ds[LONG_CH];
+#pragma unroll
+            for (int i = 0; i < LONG_CH; i++) {
+                const int c = min(p0 + g * LONG_CH + i, np - 1);
+                cv[i] = __builtin_nontemporal_load((const u32x4*)(cbase + (size_t)c * CHUNK_BYTES));
+                ds[i] = sbase[(size_t)c * 32];
+            }
+            const int cnt = min(LONG_CH, pairs - g * LONG_CH);
+            float v[LONG_CH];
+#pragma unroll
+            for (int i = 0; i < LONG_CH; i++) {
+                const int pl = min(g * LONG_CH + i, pairs - 1);  // pair within the stage
+                const float h = dot16(cv[i], xs + (2 * pl + bsel) * 32 + half * 16);
+                const LanePair hh = lanes16(h);
+                const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(ds[i]);
+                const LanePair vv = lanes32(vb);
+                v[i] = 2 * (p0 + pl) + 1 >= nb ? vv.lo : vv.lo + vv.hi;
+            }
+#pragma unroll
+            for (int s = 1; s < LONG_CH; s *= 2)
+#pragma unroll
+                for (int i = 0; i + s < LONG_CH; i += 2 * s)
+                    if (i + s < cnt) v[i] = v[i] + v[i + s];
+            if (lane < 16) gs[(p0 / LONG_CH + g) * 16 + lane] = v[0];
+        }
+        __syncthreads();  // the stage is overwritten next; the group sums are read below
+    }
+    if (wave == 0 && lane < 16) {
+        for (int s = 1; s < G; s *= 2)
+            for (int i = 0; i + s < G; i += 2 * s) gs[i * 16 + lane] = gs[i * 16 + lane] + gs[(i + s) * 16 + lane];
+        const int row = tile * TILE_ROWS + lane;
+        if (row < a.n) a.y[row] = gs[lane];
+    }
+}
+
 // ---- multi-vector GEMV ------------------------------------------------------
 //
 // One workgroup (4 waves) per (problem, 16-row tile, vector split); with
@@ -891,7 +962,18 @@ lq8_status launch_epi(hipStream_t s, Epilogue epi, const GemvArgs& a) {
 
 lq8_status launch_gemv(hipStream_t s, XSource xs, Epilogue epi, const GemvArgs& a) {
     if (a.k <= 0 || a.k % 32 || a.n <= 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k must be a positive multiple of 32");
-    if (a.k > GEMV_MAX_K) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k above 12288 is not supported");
+    if (a.k > GEMV_MAX_K) {
+        // a plain input streams through LDS in stages; the fused inputs need the whole vector staged
+        if (xs != XS_PLAIN || epi != EPI_STORE)
+            return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k above 12288 is supported for a plain input only");
+        if (a.k > GEMV_LONG_MAX_K) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: k above 131072 is not supported");
+        const int np = ((a.k >> 5) + 1) >> 1, G = (np + LONG_CH - 1) / LONG_CH;
+        const size_t smem = ((size_t)LONG_PAIRS * 64 + (size_t)G * 16) * sizeof(float);
+        const dim3 grid((unsigned)((a.n + TILE_ROWS - 1) / TILE_ROWS));
+        hipLaunchKernelGGL(k_gemv_long, grid, dim3(LONG_THREADS), smem, s, a);
+        LQ8_HIP(hipGetLastError());
+        return LQ8_OK;
+    }
     if (epi == EPI_RESID && !a.resid) return fail(LQ8_ERR_INVALID_ARG, "gemv: residual is null");
     if (epi == EPI_ARGMAX && (!a.arg_val || !a.arg_idx)) return fail(LQ8_ERR_INVALID_ARG, "gemv: argmax buffers are null");
     if (xs == XS_ATTN && (a.attn_heads * 128 != a.k || a.attn_cmax <= 0))

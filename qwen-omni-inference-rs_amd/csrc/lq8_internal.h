@@ -30,6 +30,7 @@ constexpr int TILE_ROWS = 16;
 constexpr int CHUNK_BYTES = 1024;   // one (tile, pair) chunk of codes
 constexpr int GEMM_GROUP = 8;       // blocks per accumulation group of the W8A8 GEMM
 constexpr int GEMV_MAX_K = 12288;  // staged input + group sums stay under 64 KiB of LDS
+constexpr int GEMV_LONG_MAX_K = 131072;  // plain inputs above GEMV_MAX_K stream through LDS in stages
 
 __host__ __device__ inline size_t code_off(size_t tile, size_t np, size_t b, int half, int r) {
     return ((tile * np + (b >> 1)) * 64 + ((b & 1) * 2 + half) * 16 + r) * 16;
@@ -66,6 +67,11 @@ struct lq8_ctx {
     size_t scratch_bytes = 0;
     void* problems = nullptr;  // device copy of grouped GEMV descriptors
     size_t problems_bytes = 0;
+    // host-pointer linear forward: device and pinned host staging of x and y,
+    // grown on demand (never per call)
+    void* io_dev = nullptr;
+    void* io_host = nullptr;
+    size_t io_bytes = 0;
 };
 
 struct lq8_weight {
@@ -187,6 +193,9 @@ lq8_status launch_silu_quantize_act(hipStream_t s, const float* gu, int m, int i
                                     uint32_t* scales);
 size_t act_code_bytes(int m, int k);
 size_t act_scale_bytes(int m, int k);
+// The activation operand back to GGUF blocks [m][k / 32] (tests, inspection).
+lq8_status launch_unpack_act(hipStream_t s, const int8_t* codes, const uint32_t* scales, int m, int k,
+                             uint8_t* blocks);
 // AoS quantization (public device quantizer).
 lq8_status launch_quantize_aos(hipStream_t s, const float* x, size_t nblocks, uint8_t* blocks);
 // W8A8 GEMM: y[m, n] (+ resid) from tiled activations and a tiled weight.

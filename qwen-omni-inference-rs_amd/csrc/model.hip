@@ -57,18 +57,29 @@ struct lq8_model {
     float *P_h = nullptr, *P_x = nullptr, *P_qkv = nullptr, *P_qr = nullptr, *P_attn = nullptr, *P_gu = nullptr,
           *P_xs = nullptr;
     int8_t* P_xq = nullptr;
-    hipGraphExec_t graph = nullptr;
-    // sampling: device config, token counts, sort buffers, the sampled decode graph
+    // replayed decode steps, indexed by the token they forward: [0] the token
+    // generated last (d_tok), [1] the first generated token (d_tokens[0], the
+    // reference loop as written)
+    hipGraphExec_t graph[2] = {nullptr, nullptr};
+    // sampling: device config, token counts, sort buffers, the sampled decode graphs
     SampleCfg* d_scfg = nullptr;
     uint32_t* d_counts = nullptr;
     uint8_t* s_work = nullptr;  // sampler workspace (sample_work_bytes(vocab))
-    hipGraphExec_t sgraph = nullptr;
-    bool s_topk = false;         // the sampling path of the next sampler launches (host copy of the choice)
-    bool sgraph_topk = false;    // the path sgraph was captured with
+    hipGraphExec_t sgraph[2] = {nullptr, nullptr};
+    bool s_topk = false;            // the sampling path of the next sampler launches (host copy of the choice)
+    bool sgraph_topk[2] = {false, false};  // the path each sgraph was captured with
     hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
 };
 
 namespace {
+
+void drop_graphs(lq8_model* m) {
+    for (int i = 0; i < 2; i++) {
+        if (m->graph[i]) (void)hipGraphExecDestroy(m->graph[i]);
+        if (m->sgraph[i]) (void)hipGraphExecDestroy(m->sgraph[i]);
+        m->graph[i] = m->sgraph[i] = nullptr;
+    }
+}
 
 lq8_status validate(const lq8_qwen3_config* c) {
     if (!c) return fail(LQ8_ERR_INVALID_ARG, "config is null");
@@ -97,8 +108,7 @@ void release(lq8_model* m) {
     if (!m) return;
     registry_remove(m);
     auto F = [](void* p) { if (p) (void)hipFree(p); };
-    if (m->graph) (void)hipGraphExecDestroy(m->graph);
-    if (m->sgraph) (void)hipGraphExecDestroy(m->sgraph);
+    drop_graphs(m);
     if (m->e0) (void)hipEventDestroy(m->e0);
     if (m->e1) (void)hipEventDestroy(m->e1);
     if (m->e2) (void)hipEventDestroy(m->e2);
@@ -381,9 +391,9 @@ lq8_status ensure_sampler(lq8_model* m) {
     if (m->d_scfg && m->d_counts && m->s_work) return LQ8_OK;
     // a failed earlier attempt may have left some of them: start over (and
     // drop any graph that captured the old buffers)
-    if (m->sgraph) {
-        (void)hipGraphExecDestroy(m->sgraph);
-        m->sgraph = nullptr;
+    for (auto& g : m->sgraph) {
+        if (g) (void)hipGraphExecDestroy(g);
+        g = nullptr;
     }
     auto F = [](void* p) { if (p) (void)hipFree(p); };
     F(m->d_scfg); F(m->d_counts); F(m->s_work);
@@ -416,16 +426,21 @@ lq8_status launch_sample_pick(lq8_model* m) {
     return launch_sample(m->ctx->stream, a);
 }
 
-lq8_status capture_sample_graph(lq8_model* m) {
-    if (m->sgraph && m->sgraph_topk == m->s_topk) return LQ8_OK;
-    if (m->sgraph) {
-        (void)hipGraphExecDestroy(m->sgraph);
-        m->sgraph = nullptr;
+// The decode step's input token: the one generated last, or (feed_first) the
+// first generated token, which the reference's loop forwards at every step.
+const uint32_t* step_token(lq8_model* m, bool feed_first) { return feed_first ? m->d_tokens : m->d_tok; }
+
+lq8_status capture_sample_graph(lq8_model* m, bool feed_first) {
+    hipGraphExec_t& slot = m->sgraph[feed_first];
+    if (slot && m->sgraph_topk[feed_first] == m->s_topk) return LQ8_OK;
+    if (slot) {
+        (void)hipGraphExecDestroy(slot);
+        slot = nullptr;
     }
     hipStream_t s = m->ctx->stream;
     hipGraph_t g = nullptr;
     LQ8_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
-    lq8_status st = enqueue_decode(m, m->d_tok, m->d_pos, 0);
+    lq8_status st = enqueue_decode(m, step_token(m, feed_first), m->d_pos, 0);
     if (!st) st = launch_sample_pick(m);
     hipError_t e = hipStreamEndCapture(s, &g);
     if (st) {
@@ -433,22 +448,23 @@ lq8_status capture_sample_graph(lq8_model* m) {
         return st;
     }
     if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
-    e = hipGraphInstantiate(&m->sgraph, g, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(&slot, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) {
-        m->sgraph = nullptr;
+        slot = nullptr;
         return hip_fail(e, "hipGraphInstantiate");
     }
-    m->sgraph_topk = m->s_topk;
+    m->sgraph_topk[feed_first] = m->s_topk;
     return LQ8_OK;
 }
 
-lq8_status capture_decode_graph(lq8_model* m) {
-    if (m->graph) return LQ8_OK;
+lq8_status capture_decode_graph(lq8_model* m, bool feed_first) {
+    hipGraphExec_t& slot = m->graph[feed_first];
+    if (slot) return LQ8_OK;
     hipStream_t s = m->ctx->stream;
     hipGraph_t g = nullptr;
     LQ8_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
-    lq8_status st = enqueue_decode(m, m->d_tok, m->d_pos, 0);
+    lq8_status st = enqueue_decode(m, step_token(m, feed_first), m->d_pos, 0);
     if (!st) st = launch_pick(m);
     hipError_t e = hipStreamEndCapture(s, &g);
     if (st) {
@@ -456,10 +472,10 @@ lq8_status capture_decode_graph(lq8_model* m) {
         return st;
     }
     if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
-    e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(&slot, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) {
-        m->graph = nullptr;
+        slot = nullptr;
         return hip_fail(e, "hipGraphInstantiate");
     }
     return LQ8_OK;
@@ -469,9 +485,10 @@ lq8_status capture_decode_graph(lq8_model* m) {
 
 namespace {
 
-// generate (src/generate.rs:611-664): greedy picks (sc null) or sampled ones.
+// generate (src/generate.rs:611-664): greedy picks (sc null) or sampled ones;
+// feed_first: every decode step forwards the first generated token.
 lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new, const SampleCfg* sc,
-                        uint32_t* out_tokens, lq8_gen_stats* stats) {
+                        bool feed_first, uint32_t* out_tokens, lq8_gen_stats* stats) {
     if (!prompt || n_prompt == 0) return fail(LQ8_ERR_INVALID_ARG, "empty prompt");
     if (max_new == 0 || !out_tokens) return fail(LQ8_ERR_INVALID_ARG, "max_new must be positive");
     if (n_prompt + max_new - 1 > m->c.max_positions)
@@ -487,14 +504,15 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
         m->d_tokens = nullptr;
         if ((st = dalloc(&m->d_tokens, max_new))) return st;
         m->tokens_cap = max_new;
-        if (m->graph) { (void)hipGraphExecDestroy(m->graph); m->graph = nullptr; }
-        if (m->sgraph) { (void)hipGraphExecDestroy(m->sgraph); m->sgraph = nullptr; }
+        drop_graphs(m);  // they captured the old token buffer
     }
     if (n_prompt > 1 && (st = ensure_prefill(m, n_prompt))) return st;
     const bool use_graph = std::getenv("LQ8_NO_GRAPH") == nullptr;
     if (sc && (st = ensure_sampler(m))) return st;
     if (sc) m->s_topk = sample_topk_path(*sc);
-    if (use_graph && max_new > 1 && (st = sc ? capture_sample_graph(m) : capture_decode_graph(m))) return st;
+    if (use_graph && max_new > 1 &&
+        (st = sc ? capture_sample_graph(m, feed_first) : capture_decode_graph(m, feed_first)))
+        return st;
     // clear_kv_cache (src/generate.rs:618), then prefill at offset 0
     m->kv_len = 0;
     const int zero = 0, pos0 = (int)n_prompt - 1;
@@ -515,9 +533,9 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     LQ8_HIP(hipEventRecord(m->e1, s));
     for (size_t t = 1; t < max_new; t++) {
         if (use_graph) {
-            LQ8_HIP(hipGraphLaunch(sc ? m->sgraph : m->graph, s));
+            LQ8_HIP(hipGraphLaunch(sc ? m->sgraph[feed_first] : m->graph[feed_first], s));
         } else {
-            if ((st = enqueue_decode(m, m->d_tok, m->d_pos, 0))) return st;
+            if ((st = enqueue_decode(m, step_token(m, feed_first), m->d_pos, 0))) return st;
             if ((st = sc ? launch_sample_pick(m) : launch_pick(m))) return st;
         }
     }
@@ -752,15 +770,17 @@ lq8_status lq8_model_forward_with_intermediates(lq8_model* m, const uint32_t* id
 lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
                                uint32_t* out_tokens, lq8_gen_stats* stats) {
     CHECK_M(m);
-    return run_generate(m, prompt, n_prompt, max_new, nullptr, out_tokens, stats);
+    return run_generate(m, prompt, n_prompt, max_new, nullptr, false, out_tokens, stats);
 }
 
-lq8_status lq8_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
-                        const lq8_sampling* cfg, const uint32_t* eos_ids, size_t n_eos, uint32_t* out_tokens,
-                        size_t* n_out, lq8_gen_stats* stats) {
+lq8_status lq8_generate_ex(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                           const lq8_sampling* cfg, const uint32_t* eos_ids, size_t n_eos, uint32_t flags,
+                           uint32_t* out_tokens, size_t* n_out, lq8_gen_stats* stats) {
     CHECK_M(m);
     if (n_eos && !eos_ids) return fail(LQ8_ERR_INVALID_ARG, "eos_ids is null");
     if (!n_out) return fail(LQ8_ERR_INVALID_ARG, "n_out is null");
+    if (flags & ~(uint32_t)LQ8_GEN_FEED_FIRST_TOKEN) return fail(LQ8_ERR_INVALID_ARG, "unknown generation flag");
+    const bool feed_first = (flags & LQ8_GEN_FEED_FIRST_TOKEN) != 0;
     SampleCfg sc;
     lq8_status st = check_sampling(cfg, &sc);
     if (st) return st;
@@ -768,7 +788,8 @@ lq8_status lq8_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     const bool greedy = sc.temperature == 0.0f && std::fabs(sc.penalty - 1.0f) < 1e-6f;
     if (!greedy && !sample_vocab_ok(m->c.vocab_size))
         return fail(LQ8_ERR_INVALID_ARG, "sampling: vocabulary above 2^20");
-    if ((st = run_generate(m, prompt, n_prompt, max_new, greedy ? nullptr : &sc, out_tokens, stats))) return st;
+    if ((st = run_generate(m, prompt, n_prompt, max_new, greedy ? nullptr : &sc, feed_first, out_tokens, stats)))
+        return st;
     // the first EOS ends the generation (kept); the cache as after the early stop
     size_t n = max_new;
     for (size_t t = 0; t < max_new && n == max_new; t++)
@@ -780,6 +801,12 @@ lq8_status lq8_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     m->kv_len = n_prompt + n - 1;
     *n_out = n;
     return LQ8_OK;
+}
+
+lq8_status lq8_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                        const lq8_sampling* cfg, const uint32_t* eos_ids, size_t n_eos, uint32_t* out_tokens,
+                        size_t* n_out, lq8_gen_stats* stats) {
+    return lq8_generate_ex(m, prompt, n_prompt, max_new, cfg, eos_ids, n_eos, 0, out_tokens, n_out, stats);
 }
 
 lq8_status lq8_model_free(lq8_model* m) {

@@ -108,6 +108,27 @@ __global__ void k_unpack_aos(const int8_t* __restrict__ codes, const uint16_t* _
     }
 }
 
+// The GEMM's activation operand (tiled codes, f16 scales in the operand
+// layout [m/32][2 groups][64 lanes][4 blocks]) back to GGUF blocks, one
+// thread per (row, block).
+__global__ void k_unpack_act(const int8_t* __restrict__ codes, const uint32_t* __restrict__ xs, int m, int nb, int np,
+                             int nbp4, uint8_t* __restrict__ aos) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)m * nb) return;
+    const int row = (int)(idx / nb), b = (int)(idx % nb);
+    const uint32_t d = xs[((size_t)((row >> 5) * nbp4 + (b >> 2)) * 64 + (row & 31)) * 4 + (b & 3)];
+    uint8_t* o = aos + idx * BLOCK_BYTES;
+    o[0] = (uint8_t)(d & 0xFF);
+    o[1] = (uint8_t)((d >> 8) & 0xFF);
+    const int8_t* lo = codes + code_off(row / TILE_ROWS, np, b, 0, row % TILE_ROWS);
+    const int8_t* hi = codes + code_off(row / TILE_ROWS, np, b, 1, row % TILE_ROWS);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        o[2 + j] = (uint8_t)lo[j];
+        o[18 + j] = (uint8_t)hi[j];
+    }
+}
+
 __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
     z += 0x9E3779B97F4A7C15ull;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -597,6 +618,16 @@ lq8_status launch_silu_quantize_act(hipStream_t s, const float* gu, int m, int i
     if (waves > (size_t)INT32_MAX) return fail(LQ8_ERR_SHAPE_MISMATCH, "silu_quantize_act: too many rows");
     hipLaunchKernelGGL(k_silu_quantize_act, dim3(grid1(waves, 4)), dim3(256), 0, s, gu, m, inter, (int)waves, groups,
                        np, codes, scales);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
+lq8_status launch_unpack_act(hipStream_t s, const int8_t* codes, const uint32_t* scales, int m, int k,
+                             uint8_t* blocks) {
+    const int nb = k / 32, np = (nb + 1) / 2, groups = (nb + GEMM_GROUP - 1) / GEMM_GROUP;
+    const size_t n = (size_t)m * nb;
+    if (!n) return LQ8_OK;
+    hipLaunchKernelGGL(k_unpack_act, dim3(grid1(n, WG)), dim3(WG), 0, s, codes, scales, m, nb, np, 2 * groups, blocks);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

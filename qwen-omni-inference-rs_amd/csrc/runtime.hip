@@ -234,6 +234,8 @@ lq8_status lq8_shutdown(lq8_ctx* ctx) {
     registry_remove(ctx);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->problems) (void)hipFree(ctx->problems);
+    if (ctx->io_dev) (void)hipFree(ctx->io_dev);
+    if (ctx->io_host) (void)hipHostFree(ctx->io_host);
     (void)hipEventDestroy(ctx->t0);
     (void)hipEventDestroy(ctx->t1);
     (void)hipStreamDestroy(ctx->stream);
@@ -438,6 +440,40 @@ lq8_status lq8_quantize_q8_0_device(lq8_ctx* ctx, const float* d_x, size_t n, vo
     return launch_quantize_aos(ctx->stream, d_x, n / QK, (uint8_t*)d_blocks);
 }
 
+lq8_status lq8_quantize_activations_device(lq8_ctx* ctx, int source, const float* d_x, const float* d_w, size_t m,
+                                          size_t k, float eps, void* d_blocks) {
+    CHECK_CTX(ctx);
+    if (!d_x || !d_blocks || (source == LQ8_ACT_RMSNORM && !d_w)) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (source < LQ8_ACT_PLAIN || source > LQ8_ACT_SILU_MUL) return fail(LQ8_ERR_INVALID_ARG, "unknown activation source");
+    if (k == 0 || k % QK || k > (size_t)INT32_MAX / 4) return fail(LQ8_ERR_SHAPE_MISMATCH, "k must be a positive multiple of 32");
+    if (m == 0) return LQ8_OK;
+    if (m > (size_t)INT32_MAX / 2) return fail(LQ8_ERR_SHAPE_MISMATCH, "m too large");
+    if (((uintptr_t)d_x & 15) != 0) return fail(LQ8_ERR_INVALID_ARG, "x must be 16-byte aligned");
+    const int mi = (int)m, ki = (int)k;
+    const size_t cb = act_code_bytes(mi, ki), sb = act_scale_bytes(mi, ki);
+    // RmsNorm rows wider than the fused kernel handles go through normed rows first (the prefill path)
+    const bool two_step = source == LQ8_ACT_RMSNORM && !rms_quantize_supported(ki);
+    const size_t rows_bytes = two_step ? m * k * sizeof(float) : 0;
+    void* sc = nullptr;
+    lq8_status st = ctx_scratch(ctx, cb + sb + rows_bytes, &sc);
+    if (st) return st;
+    int8_t* xq = (int8_t*)sc;
+    uint32_t* xs = (uint32_t*)((char*)sc + cb);
+    if (source == LQ8_ACT_PLAIN) {
+        st = launch_quantize_act(ctx->stream, d_x, mi, ki, xq, xs);
+    } else if (source == LQ8_ACT_SILU_MUL) {
+        st = launch_silu_quantize_act(ctx->stream, d_x, mi, ki, xq, xs);
+    } else if (two_step) {
+        float* rows = (float*)((char*)sc + cb + sb);
+        st = launch_rms_norm_rows(ctx->stream, d_x, d_w, mi, ki, eps, rows);
+        if (!st) st = launch_quantize_act(ctx->stream, rows, mi, ki, xq, xs);
+    } else {
+        st = launch_rms_quantize_act(ctx->stream, d_x, d_w, mi, ki, eps, xq, xs);
+    }
+    if (st) return st;
+    return launch_unpack_act(ctx->stream, xq, xs, mi, ki, (uint8_t*)d_blocks);
+}
+
 lq8_status lq8_weight_dequantize_rows_device(lq8_ctx* ctx, const lq8_weight* w, size_t row0, size_t nrows,
                                              float* d_y) {
     CHECK_CTX(ctx);
@@ -498,25 +534,46 @@ lq8_status lq8_linear_forward_device(lq8_ctx* ctx, const lq8_weight* w, const fl
     return lq8_gemm_q8_0_device(ctx, w, d_x, m, d_y);
 }
 
+// Device and pinned host staging for the host-pointer entry points: grows
+// (after a synchronize) only when a call needs more than any call before.
+static lq8_status ctx_io(lq8_ctx* ctx, size_t bytes) {
+    if (bytes <= ctx->io_bytes) return LQ8_OK;
+    LQ8_HIP(hipStreamSynchronize(ctx->stream));
+    if (ctx->io_dev) LQ8_HIP(hipFree(ctx->io_dev));
+    if (ctx->io_host) LQ8_HIP(hipHostFree(ctx->io_host));
+    ctx->io_dev = ctx->io_host = nullptr;
+    ctx->io_bytes = 0;
+    const size_t want = std::max(bytes, (size_t)1 << 20);
+    LQ8_HIP(hipMalloc(&ctx->io_dev, want));
+    LQ8_HIP(hipHostMalloc(&ctx->io_host, want, hipHostMallocDefault));
+    ctx->io_bytes = want;
+    return LQ8_OK;
+}
+
 lq8_status lq8_linear_forward(lq8_ctx* ctx, const lq8_weight* w, const float* x, size_t m, float* y) {
     CHECK_CTX(ctx);
     CHECK_W(w);
     if (!x || !y) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
     if (m == 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "linear: m must be positive");
     if (set_device(ctx)) return LQ8_ERR_DEVICE;
-    size_t xb = m * w->k_in * sizeof(float), yb = m * w->n_out * sizeof(float);
-    void *dx = nullptr, *dy = nullptr;
-    hipError_t e = hipMalloc(&dx, xb);
-    if (e == hipSuccess) e = hipMalloc(&dy, yb);
-    if (e == hipSuccess) e = hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream);
-    lq8_status st = LQ8_OK;
-    if (e == hipSuccess) st = lq8_linear_forward_device(ctx, w, (const float*)dx, m, (float*)dy);
-    if (e == hipSuccess && !st) e = hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    if (dx) (void)hipFree(dx);
-    if (dy) (void)hipFree(dy);
+    // x at offset 0, y after it (256-byte aligned), in the context's staging:
+    // host x -> pinned -> HBM, the device forward, HBM -> pinned -> host y
+    const size_t xb = m * w->k_in * sizeof(float), yb = m * w->n_out * sizeof(float);
+    const size_t yoff = (xb + 255) & ~(size_t)255;
+    lq8_status st = ctx_io(ctx, yoff + yb);
     if (st) return st;
-    if (e != hipSuccess) return hip_fail(e, "linear forward");
+    char* dio = (char*)ctx->io_dev;
+    char* hio = (char*)ctx->io_host;
+    std::memcpy(hio, x, xb);
+    LQ8_HIP(hipMemcpyAsync(dio, hio, xb, hipMemcpyHostToDevice, ctx->stream));
+    st = lq8_linear_forward_device(ctx, w, (const float*)dio, m, (float*)(dio + yoff));
+    if (st) {
+        (void)hipStreamSynchronize(ctx->stream);
+        return st;
+    }
+    LQ8_HIP(hipMemcpyAsync(hio + yoff, dio + yoff, yb, hipMemcpyDeviceToHost, ctx->stream));
+    LQ8_HIP(hipStreamSynchronize(ctx->stream));
+    std::memcpy(y, hio + yoff, yb);
     return LQ8_OK;
 }
 

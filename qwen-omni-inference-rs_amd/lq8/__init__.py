@@ -106,6 +106,11 @@ class SamplingC(C.Structure):
                 ("repetition_penalty", C.c_float), ("seed", C.c_uint64)]
 
 
+# lq8_generate_ex flag: the reference's generate() loop as written
+GEN_FEED_FIRST_TOKEN = 1
+# lq8_quantize_activations_device sources
+ACT_PLAIN, ACT_RMSNORM, ACT_SILU_MUL = 0, 1, 2
+
 _lib: Optional[C.CDLL] = None
 
 # (name, restype, argtypes) of every exported entry point.
@@ -166,6 +171,11 @@ _SIGS = [
     ("lq8_generate", C.c_int,
      [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(SamplingC), C.c_void_p, C.c_size_t, C.c_void_p,
       C.POINTER(C.c_size_t), C.POINTER(GenStatsC)]),
+    ("lq8_generate_ex", C.c_int,
+     [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(SamplingC), C.c_void_p, C.c_size_t, C.c_uint32,
+      C.c_void_p, C.POINTER(C.c_size_t), C.POINTER(GenStatsC)]),
+    ("lq8_quantize_activations_device", C.c_int,
+     [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_float, C.c_void_p]),
     ("lq8_model_free", C.c_int, [C.c_void_p]),
     ("lq8_moe_tensor_count", C.c_size_t, [C.POINTER(MoeConfigC)]),
     ("lq8_moe_tensor_bytes", C.c_int, [C.POINTER(MoeConfigC), C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -581,27 +591,40 @@ class Qwen3ForCausalLM:
                                                           _ptr(logits)))
         return hidden, fin, logits
 
-    def generate_greedy(self, prompt: Sequence[int], max_new_tokens: int):
+    def generate_greedy(self, prompt: Sequence[int], max_new_tokens: int, feed_first: bool = False):
+        """generate() with greedy sampling.  feed_first: every decode step
+        forwards the first generated token, as the reference's loop does as
+        written (src/generate.rs:632-650); otherwise the token generated last."""
         ids = np.ascontiguousarray(prompt, dtype=np.uint32)
         out = np.empty(max_new_tokens, dtype=np.uint32)
         st = GenStatsC()
-        _check(lib().lq8_generate_greedy(self.handle, _ptr(ids), ids.size, max_new_tokens, _ptr(out), C.byref(st)))
+        if feed_first:
+            n = C.c_size_t(0)
+            sc = SamplingC(0.0, 0, 1.0, 1.0, 0)
+            _check(lib().lq8_generate_ex(self.handle, _ptr(ids), ids.size, max_new_tokens, C.byref(sc), None, 0,
+                                         GEN_FEED_FIRST_TOKEN, _ptr(out), C.byref(n), C.byref(st)))
+        else:
+            _check(lib().lq8_generate_greedy(self.handle, _ptr(ids), ids.size, max_new_tokens, _ptr(out),
+                                             C.byref(st)))
         return out, {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
                      "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph)}
 
     def generate(self, prompt: Sequence[int], config: "GenerationConfig", seed: int = 0,
-                 eos_token_ids: Sequence[int] = ()):
+                 eos_token_ids: Sequence[int] = (), feed_first: bool = False):
         """generate() (src/generate.rs:611-664) with the configuration's
         sampling: up to config.max_new_tokens tokens, ending at the first one
-        in eos_token_ids (kept); the loop stays on the device."""
+        in eos_token_ids (kept); the loop stays on the device.  feed_first:
+        the reference's loop as written (see generate_greedy)."""
         ids = np.ascontiguousarray(prompt, dtype=np.uint32)
         eos = np.ascontiguousarray(list(eos_token_ids), dtype=np.uint32)
         out = np.empty(config.max_new_tokens, dtype=np.uint32)
         n = C.c_size_t(0)
         st = GenStatsC()
         sc = config.sampling(seed)
-        _check(lib().lq8_generate(self.handle, _ptr(ids), ids.size, config.max_new_tokens, C.byref(sc),
-                                  _ptr(eos) if eos.size else None, eos.size, _ptr(out), C.byref(n), C.byref(st)))
+        _check(lib().lq8_generate_ex(self.handle, _ptr(ids), ids.size, config.max_new_tokens, C.byref(sc),
+                                     _ptr(eos) if eos.size else None, eos.size,
+                                     GEN_FEED_FIRST_TOKEN if feed_first else 0, _ptr(out), C.byref(n),
+                                     C.byref(st)))
         return out[:n.value].copy(), {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
                                       "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph)}
 

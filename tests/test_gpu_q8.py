@@ -61,6 +61,61 @@ def test_device_quantizer_bit_exact(ctx):
     assert bad.size == 0, f"blocks differ at bytes {bad[:8]} (block {bad[0] // 34})"
 
 
+def act_operand(ctx, source, x, m, k, w=None, eps=1e-6):
+    """The GEMM's activation operand for rows x, as GGUF blocks."""
+    dx = lq8.DeviceBuffer.from_array(ctx, x)
+    dw = lq8.DeviceBuffer.from_array(ctx, w) if w is not None else None
+    db = lq8.DeviceBuffer(ctx, m * k // 32 * 34)
+    try:
+        lq8._check(lq8.lib().lq8_quantize_activations_device(ctx.handle, source, dx.ptr, dw.ptr if dw else None, m, k,
+                                                             eps, db.ptr))
+        return db.download(np.uint8, m * k // 32 * 34)
+    finally:
+        dx.free(); db.free()
+        if dw:
+            dw.free()
+
+
+def assert_blocks_equal(got, ref):
+    bad = np.flatnonzero(got != ref)
+    assert bad.size == 0, f"{bad.size} bytes differ, first in block {bad[0] // 34} (byte {bad[0] % 34})"
+
+
+@pytest.mark.parametrize("m,k", [(512, 1024), (512, 3072), (37, 96), (130, 224)])
+def test_activation_quantizer_codes_and_scales(ctx, m, k):
+    """k_quantize_act -- the activation quantizer the W8A8 GEMM runs -- gives
+    the codes and f16 scales of the Q8_0 quantizer (the oracle's, itself
+    pinned by the numpy restatement) for every block, including ragged row
+    counts, odd block counts and the special blocks."""
+    x = normal((m, k), 1.0, m + k)
+    e = edge_blocks()
+    x.reshape(-1)[:e.size] = e                      # special blocks in the first rows
+    assert_blocks_equal(act_operand(ctx, lq8.ACT_PLAIN, x, m, k), oracle.quantize_q8_0(x))
+
+
+@pytest.mark.parametrize("m,k", [(512, 1024), (128, 1568), (33, 2112)])
+def test_rmsnorm_activation_quantizer(ctx, m, k):
+    """k_rms_quantize_act (RmsNorm fused into the quantizer; 2112 takes the
+    RmsNorm-rows-then-quantize path of prefill): the blocks of
+    quantize(RmsNorm(x)) exactly."""
+    x = normal((m, k), 1.0, 7 * k)
+    w = (1.0 + 0.1 * normal(k, 1.0, 8 * k)).astype(np.float32)
+    ref = oracle.quantize_q8_0(oracle.rms_norm(x, w, 1e-6))
+    assert_blocks_equal(act_operand(ctx, lq8.ACT_RMSNORM, x, m, k, w), ref)
+
+
+@pytest.mark.parametrize("m,inter", [(512, 3072), (45, 800)])
+def test_silu_activation_quantizer(ctx, m, inter):
+    """k_silu_quantize_act (silu(gate) * up fused into the quantizer): the
+    blocks of quantize(silu(g) * u), silu(g) = g / (1 + exp(-g)) with the
+    oracle's exp, every step an f32 operation."""
+    gu = normal((m, 2 * inter), 2.0, inter)
+    g, u = gu[:, :inter], gu[:, inter:]
+    e = oracle.expf(-g).reshape(g.shape)
+    act = (g / (np.float32(1.0) + e)).astype(np.float32) * u
+    assert_blocks_equal(act_operand(ctx, lq8.ACT_SILU_MUL, gu, m, inter), oracle.quantize_q8_0(act))
+
+
 def test_weight_upload_download_roundtrip(ctx):
     n, k = 200, 96  # ragged: 200 rows is not a multiple of the 64-row tile
     blocks = oracle.quantize_q8_0(normal((n, k), 0.02, 3))
@@ -127,24 +182,36 @@ def test_gemv_maximum_k(ctx, n, k):
     assert_parity(y, ref)
 
 
-def test_gemv_above_maximum_k_is_an_error(ctx):
-    """k past the staging limit is refused (ShapeMismatch), never run on a
-    fallback; the same weight still multiplies through the GEMM at m > 1."""
-    k = 12288 + 32
-    blocks = oracle.quantize_q8_0(normal((16, k), 0.02, 5))
-    w = lq8.Q8Weight.from_blocks(ctx, blocks, 16, k)
-    dx = lq8.DeviceBuffer(ctx, 2 * k * 4)
-    dy = lq8.DeviceBuffer(ctx, 2 * 16 * 4)
+@pytest.mark.parametrize("n,k", [(16, 12320), (1024, 17408), (37, 8224 * 3), (5, 131040)])
+def test_gemv_above_staging_limit(ctx, n, k):
+    """Inputs past the single-stage limit (12288) stream through LDS in
+    8192-value stages with the same block tree: bit-exact with the oracle.
+    17408 is a down_proj input (intermediate size) of the larger Qwen3
+    models; 24672 = 771 blocks (odd, the padding block in the last stage);
+    131040 sits one block under the staged limit."""
+    y, ref = gemv_case(ctx, n, k, 5 * n + k)
+    assert_parity(y, ref)
+
+
+def test_gemv_limits_and_long_k_linear_forward(ctx):
+    """k above 131072 is refused (ShapeMismatch), never run on a fallback;
+    Linear::forward at m = 1 (host pointers) on a 17408-long input is the
+    oracle's GEMV bit for bit, and the same weight runs the GEMM at m = 2."""
+    k = 17408
+    blocks = oracle.quantize_q8_0(normal((48, k), 0.02, 5))
+    lin = lq8.Linear.new(lq8.Q8Weight.from_blocks(ctx, blocks, 48, k))
+    big = lq8.Q8Weight.random(ctx, 16, 131072 + 32, seed=2)
+    dx = lq8.DeviceBuffer(ctx, (131072 + 32) * 4)
+    dy = lq8.DeviceBuffer(ctx, 16 * 4)
     try:
         with pytest.raises(lq8.ShapeMismatch):
-            lq8._check(lq8.lib().lq8_gemv_q8_0_device(ctx.handle, w.handle, dx.ptr, dy.ptr))
+            lq8._check(lq8.lib().lq8_gemv_q8_0_device(ctx.handle, big.handle, dx.ptr, dy.ptr))
         x = normal((2, k), 1.0, 6)
-        dx.upload(x)
-        lq8._check(lq8.lib().lq8_gemm_q8_0_device(ctx.handle, w.handle, dx.ptr, 2, dy.ptr))
-        y = dy.download(np.float32, 32).reshape(2, 16)
-        assert np.array_equal(y, oracle.gemm_q8_0(blocks, 16, k, x).reshape(2, 16))
+        assert_parity(lin.forward(x[:1]).reshape(48), oracle.gemv_q8_0(blocks, 48, k, x[0]))
+        y2 = lin.forward(x)
+        assert np.array_equal(y2.view(np.uint32), oracle.gemm_q8_0(blocks, 48, k, x).view(np.uint32))
     finally:
-        dx.free(); dy.free(); w.free()
+        dx.free(); dy.free(); big.free(); lin.weight.free()
 
 
 def test_gemv_known_answer(ctx):

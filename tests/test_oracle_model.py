@@ -132,3 +132,32 @@ def test_sequential_sum_order_close_to_canonical():
         oracle.set_sequential_sums(False)
         m.close()
     assert np.max(np.abs(a - b)) <= 1e-3 * np.max(np.abs(b))
+
+
+VARIED = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                         num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=96)
+
+
+def test_reference_loop_as_written_diverges_from_feeding_the_latest_token():
+    """src/generate.rs:632-650: the `let next_token` inside the loop body
+    shadows the outer binding only for the rest of that iteration, so each
+    decode step of the reference forwards the FIRST generated token.  On a
+    model whose greedy tokens vary, that loop (feed_first) and the loop that
+    forwards the latest token -- the library's default -- part after the
+    second token; each equals its manual restatement."""
+    m = oracle.Model(VARIED, oracle.random_q8_tensors(VARIED, seed=3, layer_std=0.08, norm_jitter=0.1))
+    prompt = np.random.default_rng(1).integers(0, VARIED.vocab_size, 16).astype(np.uint32)
+    try:
+        latest, _ = m.generate_greedy(prompt, 24)
+        first, _ = m.generate_greedy(prompt, 24, feed_first=True)
+        m.clear_kv_cache()
+        logits = m.forward(prompt, 0)
+        manual = [oracle.argmax_last(logits)]
+        for t in range(1, 24):
+            manual.append(oracle.argmax_last(m.forward([manual[0]], prompt.size + t - 1)))
+    finally:
+        m.close()
+    assert first.tolist() == manual
+    assert latest[:2].tolist() == first[:2].tolist()      # same prefill token and first decode input
+    assert latest.tolist() != first.tolist()
+    assert len(set(latest.tolist())) >= 10                 # the model's tokens really vary
