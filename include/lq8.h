@@ -148,6 +148,17 @@ lq8_status lq8_silu_device(lq8_ctx* ctx, const float* d_x, size_t n, float* d_y)
  * Q8_0 per row, W8A8 int8 MFMA GEMM, int32 per block, f32 rescale. */
 lq8_status lq8_linear_forward(lq8_ctx* ctx, const lq8_weight* w, const float* x, size_t m, float* y);
 lq8_status lq8_linear_forward_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m, float* d_y);
+/* lq8_linear_forward_device that allocates nothing.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * m > 1 activation operand goes to an 8 MiB array of the library's own,
+ * one per GPU (held until the process ends): act codes + scales of about
+ * 1.25 * m * k_in bytes (e.g. m = 2048 at k_in = 3072), LQ8_ERR_SHAPE_MISMATCH
+ * above.  Every call on a GPU shares that array, so calls that overlap on one
+ * GPU (two contexts, two threads) race.  Results are bit-identical to
+ * lq8_linear_forward_device. */
+lq8_status lq8_linear_forward_device_noalloc(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m,
+                                             float* d_y);
 /* The two kernels behind it, callable directly (any m for the GEMM). */
 lq8_status lq8_gemv_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, float* d_y);
 lq8_status lq8_gemm_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m, float* d_y);

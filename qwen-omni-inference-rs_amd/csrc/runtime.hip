@@ -144,6 +144,40 @@ static lq8_status set_device(lq8_ctx* ctx) {
     return LQ8_OK;
 }
 
+// ---- scratch of the allocation-free linear forward ---------------------------
+// lq8_linear_forward_device_noalloc quantizes its activation rows into this
+// file-scope device array instead of context memory: one copy per GPU, held
+// until the process ends, shared by every call on that GPU (calls that
+// overlap on one GPU race).  Host code never hands `scratch` itself to a
+// kernel -- in host code the name is a stand-in, not a device address: each
+// device's copy is resolved once by hipGetSymbolAddress at lq8_init (with
+// that device current) and only that address is used.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)8 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};  // per device: the address of its copy of `scratch`
+}  // namespace
+
+// With `device` current: resolve its copy of the scratch array once.
+static lq8_status resolve_scratch(int device) {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (device < 0 || device >= MAX_DEVICES) return fail(LQ8_ERR_NO_DEVICE, "device index above 63");
+    if (g_scratch_ptr[device]) return LQ8_OK;
+    void* p = nullptr;
+    LQ8_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(LQ8_ERR_DEVICE, "scratch: no device address");
+    g_scratch_ptr[device] = p;
+    return LQ8_OK;
+}
+
+static void* device_scratch(int device) {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    return device >= 0 && device < MAX_DEVICES ? g_scratch_ptr[device] : nullptr;
+}
+
 extern "C" {
 
 const char* lq8_version(void) { return "lq8 0.1.0 (gfx950, Q8_0)"; }
@@ -211,6 +245,8 @@ lq8_status lq8_init(int device, lq8_ctx** out) {
     LQ8_HIP(hipGetDeviceProperties(&prop, device));
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(LQ8_ERR_NO_DEVICE, std::string("device is ") + prop.gcnArchName + ", this library targets gfx950");
+    lq8_status st = resolve_scratch(device);
+    if (st) return st;
     lq8_ctx* ctx = new lq8_ctx();
     ctx->device = device;
     ctx->num_cus = prop.multiProcessorCount;
@@ -532,6 +568,31 @@ lq8_status lq8_gemm_q8_0_device(lq8_ctx* ctx, const lq8_weight* w, const float* 
 lq8_status lq8_linear_forward_device(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m, float* d_y) {
     if (m == 1) return lq8_gemv_q8_0_device(ctx, w, d_x, d_y);
     return lq8_gemm_q8_0_device(ctx, w, d_x, m, d_y);
+}
+
+lq8_status lq8_linear_forward_device_noalloc(lq8_ctx* ctx, const lq8_weight* w, const float* d_x, size_t m,
+                                             float* d_y) {
+    CHECK_CTX(ctx);
+    CHECK_W(w);
+    if (!d_x || !d_y) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (m == 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "linear: m must be positive");
+    if (((uintptr_t)d_x & 15) != 0) return fail(LQ8_ERR_INVALID_ARG, "x must be 16-byte aligned");
+    if (m == 1) return lq8_gemv_q8_0_device(ctx, w, d_x, d_y);  // the GEMV needs no scratch
+    if (m > (size_t)INT32_MAX / 2) return fail(LQ8_ERR_SHAPE_MISMATCH, "linear: m too large");
+    const size_t cb = act_code_bytes((int)m, (int)w->k_in), sb = act_scale_bytes((int)m, (int)w->k_in);
+    if (cb + sb > NOALLOC_SCRATCH_BYTES)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "linear (no allocation): the activation operand of " + std::to_string(m) +
+                                                " x " + std::to_string(w->k_in) + " needs " + std::to_string(cb + sb) +
+                                                " bytes, above the 8 MiB static scratch");
+    char* base = (char*)device_scratch(ctx->device);
+    if (!base) return fail(LQ8_ERR_DEVICE, "scratch: not resolved for this device");
+    // the quantizer writes every code and scale the GEMM reads (zeros in the
+    // padding), so nothing in the array has to be cleared between calls
+    int8_t* xq = (int8_t*)base;
+    uint32_t* xs = (uint32_t*)(base + cb);
+    lq8_status st = launch_quantize_act(ctx->stream, d_x, (int)m, (int)w->k_in, xq, xs);
+    if (st) return st;
+    return launch_gemm(ctx->stream, xq, xs, (int)m, w, d_y, nullptr);
 }
 
 // Device and pinned host staging for the host-pointer entry points: grows

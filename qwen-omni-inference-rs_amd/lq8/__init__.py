@@ -176,6 +176,7 @@ _SIGS = [
       C.c_void_p, C.POINTER(C.c_size_t), C.POINTER(GenStatsC)]),
     ("lq8_quantize_activations_device", C.c_int,
      [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_float, C.c_void_p]),
+    ("lq8_linear_forward_device_noalloc", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("lq8_model_free", C.c_int, [C.c_void_p]),
     ("lq8_moe_tensor_count", C.c_size_t, [C.POINTER(MoeConfigC)]),
     ("lq8_moe_tensor_bytes", C.c_int, [C.POINTER(MoeConfigC), C.c_size_t, C.POINTER(C.c_size_t)]),
