@@ -248,6 +248,19 @@ def gemm_sweep(ctx):
         w.free()
 
 
+def sync_bench(ctx):
+    """Grid-wide synchronisation (lq8_bench_grid_sync) per kind and grid size:
+    device time per synchronisation over 2000 synchronisations with a data
+    exchange checked every round."""
+    names = {0: "one counter, release/acquire fences", 1: "one counter, data by agent-scope atomics",
+             2: "per-XCD counters + global counter", 3: "per-XCD counters + per-XCD flags"}
+    for kind in range(4):
+        for nwg in (256, 512):
+            us, bad, gave = lq8.bench_grid_sync(ctx, kind, nwg, 1000)
+            print(f"kind {kind} ({names[kind]}), {nwg} workgroups x 256 threads: {us:6.2f} us per sync, "
+                  f"{bad} values wrong, gave up: {gave}", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -260,9 +273,14 @@ def main():
                     help="only the headline step and the calibration copy (for hardware-counter runs)")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="only the W8A8 GEMM at M = 512 ... 8192 (gate/up and down shapes), one line each")
+    ap.add_argument("--sync-bench", action="store_true",
+                    help="only the grid-wide synchronisation microbenchmark, one line per kind and grid size")
     args = ap.parse_args()
     if args.gemm_sweep:
         gemm_sweep(lq8.Context(0))
+        return
+    if args.sync_bench:
+        sync_bench(lq8.Context(0))
         return
     if args.only_step:
         args.no_decode = args.no_cpu = args.no_moe = True

@@ -180,6 +180,18 @@ lq8_status lq8_gemv_grouped_device(lq8_ctx* ctx, const lq8_gemv_problem* problem
 lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t count, int mode, int reps,
                           float* ms);
 
+/* Microbenchmark of the workgroup-to-workgroup hand-off a persistent decode
+ * kernel needs (no reference counterpart): `rounds` rounds of a data
+ * exchange between all nwg workgroups of one cooperative launch, each round
+ * two grid-wide synchronisations.  kind 0: one counter with agent-scope
+ * release/acquire fences; 1: one counter, the data itself written and read
+ * with agent-scope atomics (no cache-wide fences); 2: per-XCD counters
+ * under a global one; 3: per-XCD counters and per-XCD release flags.
+ * Returns the device time per synchronisation, the values read wrong (must
+ * be 0) and whether a bounded wait gave up (must be 0). */
+lq8_status lq8_bench_grid_sync(lq8_ctx* ctx, int kind, int nwg, int rounds, float* us_per_sync,
+                               uint32_t* mismatches, uint32_t* gave_up);
+
 /* ---- Qwen3 model ---------------------------------------------------------
  * Replaces: Qwen3ForCausalLM::load/forward/clear_kv_cache
  * (src/model.rs:273-302, 345-372, 396-398) and generate() with greedy

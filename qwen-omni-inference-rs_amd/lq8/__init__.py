@@ -177,6 +177,8 @@ _SIGS = [
     ("lq8_quantize_activations_device", C.c_int,
      [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_float, C.c_void_p]),
     ("lq8_linear_forward_device_noalloc", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("lq8_bench_grid_sync", C.c_int,
+     [C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
     ("lq8_model_free", C.c_int, [C.c_void_p]),
     ("lq8_moe_tensor_count", C.c_size_t, [C.POINTER(MoeConfigC)]),
     ("lq8_moe_tensor_bytes", C.c_int, [C.POINTER(MoeConfigC), C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -793,6 +795,14 @@ class Qwen3MoeLayers:
         if self.handle:
             _check(lib().lq8_moe_free(self.handle))
             self.handle = None
+
+
+def bench_grid_sync(ctx: "Context", kind: int, nwg: int, rounds: int):
+    """(us per grid-wide synchronisation, values read wrong, waits given up)
+    of lq8_bench_grid_sync."""
+    us, bad, gave = C.c_float(0), C.c_uint32(0), C.c_uint32(0)
+    _check(lib().lq8_bench_grid_sync(ctx.handle, kind, nwg, rounds, C.byref(us), C.byref(bad), C.byref(gave)))
+    return float(us.value), int(bad.value), int(gave.value)
 
 
 def gemv_grouped_device(ctx: Context, problems) -> None:
