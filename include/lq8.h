@@ -240,6 +240,7 @@ typedef struct {
     double decode_ms;       /* the max_new-1 single-token steps, device time */
     double decode_tokens_per_s;
     uint32_t used_graph;    /* 1 if the decode step ran as a replayed HIP graph */
+    uint32_t used_persistent; /* 1 if the decode steps ran as one persistent kernel (greedy) */
 } lq8_gen_stats;
 /* Greedy generation; the token loop stays on the device.  out_tokens: max_new.
  * Each decode step forwards the token generated last.  The reference's loop

@@ -19,6 +19,7 @@
 #include <utility>
 #include <vector>
 
+#include "decode_persistent.h"
 #include "lq8_internal.h"
 
 using namespace lq8;
@@ -69,6 +70,16 @@ struct lq8_model {
     bool s_topk = false;            // the sampling path of the next sampler launches (host copy of the choice)
     bool sgraph_topk[2] = {false, false};  // the path each sgraph was captured with
     hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+    // persistent greedy decode (decode_persistent.hip): per-layer weight
+    // pointers, tagged hand-off buffers, the argument block, the abort flag
+    PLayer* d_player = nullptr;
+    uint64_t* hand = nullptr;  // qkvb | partb | h2b | actb | hb | argb
+    size_t hand_words = 0;
+    PersistArgs* d_pargs = nullptr;
+    PersistArgs h_pargs{};     // host copy (the source of the argument upload)
+    unsigned* d_abort = nullptr;
+    unsigned tag = 1;          // tag of the next persistent step (0 never used)
+    int persist_wg = 0;        // workgroups of the cooperative launch (0: not set up)
 };
 
 namespace {
@@ -123,6 +134,7 @@ void release(lq8_model* m) {
     F(m->d_ids); F(m->d_pos); F(m->d_step); F(m->d_tok); F(m->d_tokens);
     F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_xs); F(m->P_xq);
     F(m->d_scfg); F(m->d_counts); F(m->s_work);
+    F(m->d_player); F(m->hand); F(m->d_pargs); F(m->d_abort);
     delete m;
 }
 
@@ -485,6 +497,99 @@ lq8_status capture_decode_graph(lq8_model* m, bool feed_first) {
 
 namespace {
 
+PersistShape persist_shape(const lq8_model* m) {
+    const lq8_qwen3_config& c = m->c;
+    return PersistShape{(int)c.hidden_size, (int)c.intermediate_size, (int)c.num_heads, (int)c.num_kv_heads,
+                        (int)c.head_dim, (int)c.max_positions};
+}
+
+// Whether greedy decode runs as the persistent kernel: LQ8_PERSIST is set
+// and the shape is supported.
+bool persist_wanted(const lq8_model* m) {
+    if (std::getenv("LQ8_PERSIST") == nullptr) return false;
+    return persist_supported(persist_shape(m), m->ctx->num_cus);
+}
+
+// Device state of the persistent decode (allocated once per model).
+lq8_status persist_setup(lq8_model* m) {
+    if (m->persist_wg) return LQ8_OK;
+    const lq8_qwen3_config& c = m->c;
+    int coop = 0;
+    LQ8_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, m->ctx->device));
+    if (!coop) return fail(LQ8_ERR_DEVICE, "persistent decode: no cooperative launch on this device");
+    const int P = m->ctx->num_cus;
+    const PersistShape sh = persist_shape(m);
+    const size_t L = c.num_layers, H = c.hidden_size, I = c.intermediate_size, NH = c.num_heads;
+    const size_t cmax = (size_t)m->cmax;
+    const size_t qkv = L * m->QKV, part = L * cmax * NH * ATT_PART_STRIDE, h2 = L * H, act = L * I, h = L * H;
+    m->hand_words = qkv + part + h2 + act + h + 2 * (size_t)P;
+    std::vector<PLayer> pl(L);
+    for (size_t l = 0; l < L; l++) {
+        const Layer& Ly = m->layers[l];
+        pl[l] = PLayer{Ly.qkv->codes, Ly.o->codes, Ly.gu->codes, Ly.down->codes, Ly.qkv->scales, Ly.o->scales,
+                       Ly.gu->scales, Ly.down->scales, Ly.in_norm, Ly.post_norm, Ly.q_norm, Ly.k_norm};
+    }
+    lq8_status st;
+    if ((st = dalloc(&m->d_player, L)) || (st = dalloc(&m->hand, m->hand_words)) || (st = dalloc(&m->d_pargs, 1)) ||
+        (st = dalloc(&m->d_abort, 1)))
+        return st;
+    LQ8_HIP(hipMemcpy(m->d_player, pl.data(), L * sizeof(PLayer), hipMemcpyHostToDevice));
+    LQ8_HIP(hipMemset(m->hand, 0, m->hand_words * sizeof(uint64_t)));  // tag 0: never a step's
+    PersistArgs& a = m->h_pargs;
+    a = PersistArgs{};
+    a.layers = m->d_player;
+    a.L = (int)L;
+    a.emb_c = m->embed->codes;
+    a.emb_s = m->embed->scales;
+    a.final_norm = m->final_norm;
+    a.cos_t = m->cos_t;
+    a.sin_t = m->sin_t;
+    a.kc = m->kc;
+    a.vc = m->vc;
+    a.H = (int)H; a.I = (int)I; a.NH = (int)NH; a.NKV = (int)c.num_kv_heads;
+    a.max_pos = (int)c.max_positions; a.cmax = m->cmax; a.vocab = (int)c.vocab_size;
+    a.eps = c.rms_norm_eps;
+    a.scale = 1.0f / std::sqrt((float)c.head_dim);
+    a.qkvb = m->hand;
+    a.partb = a.qkvb + qkv;
+    a.h2b = a.partb + part;
+    a.actb = a.h2b + h2;
+    a.hb = a.actb + act;
+    a.argb = a.hb + h;
+    a.abort_flag = m->d_abort;
+    a.xs_floats = (int)persist_xs_floats(sh);
+    a.region_a = (int)persist_region_a(sh);
+    a.smem_bytes = (int)persist_smem_bytes(sh);
+    m->persist_wg = P;
+    return LQ8_OK;
+}
+
+// The decode steps of generate() at positions pos0 .. pos0 + steps - 1 as one
+// cooperative launch (the input token is in d_tok; tokens_out[1 + s] gets
+// step s's pick).  The host argument copy stays unchanged until the caller
+// synchronizes the stream.
+lq8_status launch_persist(lq8_model* m, int pos0, int steps, bool feed_first) {
+    hipStream_t s = m->ctx->stream;
+    if ((uint64_t)m->tag + (uint64_t)steps >= 0xFFFFFF00ull) {  // tags wrap: clear every word back to tag 0
+        LQ8_HIP(hipMemsetAsync(m->hand, 0, m->hand_words * sizeof(uint64_t), s));
+        m->tag = 1;
+    }
+    PersistArgs& a = m->h_pargs;
+    a.pos0 = pos0;
+    a.steps = steps;
+    a.step0 = 1;
+    a.feed_first = feed_first ? 1 : 0;
+    a.tag0 = m->tag;
+    a.d_tok = m->d_tok;
+    a.tokens_out = m->d_tokens;
+    a.d_pos = m->d_pos;
+    a.d_step = m->d_step;
+    m->tag += (unsigned)steps;
+    LQ8_HIP(hipMemcpyAsync(m->d_pargs, &a, sizeof(PersistArgs), hipMemcpyHostToDevice, s));
+    LQ8_HIP(hipMemsetAsync(m->d_abort, 0, sizeof(unsigned), s));
+    return launch_decode_persistent(s, m->d_pargs, a.smem_bytes, m->persist_wg);
+}
+
 // generate (src/generate.rs:611-664): greedy picks (sc null) or sampled ones;
 // feed_first: every decode step forwards the first generated token.
 lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new, const SampleCfg* sc,
@@ -510,7 +615,9 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     const bool use_graph = std::getenv("LQ8_NO_GRAPH") == nullptr;
     if (sc && (st = ensure_sampler(m))) return st;
     if (sc) m->s_topk = sample_topk_path(*sc);
-    if (use_graph && max_new > 1 &&
+    const bool use_persist = !sc && max_new > 1 && persist_wanted(m);
+    if (use_persist && (st = persist_setup(m))) return st;
+    if (!use_persist && use_graph && max_new > 1 &&
         (st = sc ? capture_sample_graph(m, feed_first) : capture_decode_graph(m, feed_first)))
         return st;
     // clear_kv_cache (src/generate.rs:618), then prefill at offset 0
@@ -531,7 +638,8 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     // first token from the prefill logits; d_pos becomes n_prompt
     if ((st = sc ? launch_sample_pick(m) : launch_pick(m))) return st;
     LQ8_HIP(hipEventRecord(m->e1, s));
-    for (size_t t = 1; t < max_new; t++) {
+    if (use_persist && (st = launch_persist(m, (int)n_prompt, (int)max_new - 1, feed_first))) return st;
+    for (size_t t = 1; t < max_new && !use_persist; t++) {
         if (use_graph) {
             LQ8_HIP(hipGraphLaunch(sc ? m->sgraph[feed_first] : m->graph[feed_first], s));
         } else {
@@ -541,7 +649,11 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     }
     LQ8_HIP(hipEventRecord(m->e2, s));
     LQ8_HIP(hipMemcpyAsync(out_tokens, m->d_tokens, max_new * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    unsigned aborted = 0;
+    if (use_persist) LQ8_HIP(hipMemcpyAsync(&aborted, m->d_abort, sizeof(unsigned), hipMemcpyDeviceToHost, s));
     LQ8_HIP(hipStreamSynchronize(s));
+    if (aborted)
+        return fail(LQ8_ERR_DEVICE, "persistent decode: a workgroup hand-off did not arrive in time (aborted)");
     m->kv_len = n_prompt + max_new - 1;
     if (stats) {
         float a = 0, b = 0;
@@ -550,7 +662,8 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
         stats->prefill_ms = a;
         stats->decode_ms = b;
         stats->decode_tokens_per_s = (max_new > 1 && b > 0) ? (double)(max_new - 1) / (b * 1e-3) : 0.0;
-        stats->used_graph = use_graph ? 1u : 0u;
+        stats->used_graph = (use_graph && !use_persist) ? 1u : 0u;
+        stats->used_persistent = use_persist ? 1u : 0u;
     }
     return LQ8_OK;
 }

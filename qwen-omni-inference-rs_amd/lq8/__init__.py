@@ -98,7 +98,7 @@ class MoeConfigC(C.Structure):
 
 class GenStatsC(C.Structure):
     _fields_ = [("prefill_ms", C.c_double), ("decode_ms", C.c_double), ("decode_tokens_per_s", C.c_double),
-                ("used_graph", C.c_uint32)]
+                ("used_graph", C.c_uint32), ("used_persistent", C.c_uint32)]
 
 
 class SamplingC(C.Structure):
@@ -610,7 +610,8 @@ class Qwen3ForCausalLM:
             _check(lib().lq8_generate_greedy(self.handle, _ptr(ids), ids.size, max_new_tokens, _ptr(out),
                                              C.byref(st)))
         return out, {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
-                     "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph)}
+                     "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph),
+                     "used_persistent": bool(st.used_persistent)}
 
     def generate(self, prompt: Sequence[int], config: "GenerationConfig", seed: int = 0,
                  eos_token_ids: Sequence[int] = (), feed_first: bool = False):
@@ -629,7 +630,8 @@ class Qwen3ForCausalLM:
                                      GEN_FEED_FIRST_TOKEN if feed_first else 0, _ptr(out), C.byref(n),
                                      C.byref(st)))
         return out[:n.value].copy(), {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms,
-                                      "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph)}
+                                      "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph),
+                                      "used_persistent": bool(st.used_persistent)}
 
     def free(self) -> None:
         if self.handle:

@@ -70,21 +70,33 @@ def test_offset_must_match_cache(small_pair):
         model.forward([SMALL.vocab_size], 3)
 
 
-@pytest.mark.parametrize("graph", [True, False])
-def test_generate_greedy_matches_oracle(small_pair, graph):
-    model, ref = small_pair
-    prompt = np.random.default_rng(12).integers(0, SMALL.vocab_size, 20).astype(np.uint32)
-    old = os.environ.pop("LQ8_NO_GRAPH", None)
-    if not graph:
+def with_path(path, fn):
+    """Run fn with the greedy decode path forced: "persistent" (LQ8_PERSIST:
+    the persistent kernel), "graph" (the replayed graph, the default) or
+    "plain" (LQ8_NO_GRAPH: kernel launches)."""
+    keys = ("LQ8_PERSIST", "LQ8_NO_GRAPH")
+    old = {k: os.environ.pop(k, None) for k in keys}
+    if path == "persistent":
+        os.environ["LQ8_PERSIST"] = "1"
+    if path == "plain":
         os.environ["LQ8_NO_GRAPH"] = "1"
     try:
-        toks, stats = model.generate_greedy(prompt, 24)
+        return fn()
     finally:
-        os.environ.pop("LQ8_NO_GRAPH", None)
-        if old is not None:
-            os.environ["LQ8_NO_GRAPH"] = old
+        for k in keys:
+            os.environ.pop(k, None)
+            if old[k] is not None:
+                os.environ[k] = old[k]
+
+
+@pytest.mark.parametrize("path", ["persistent", "graph", "plain"])
+def test_generate_greedy_matches_oracle(small_pair, path):
+    model, ref = small_pair
+    prompt = np.random.default_rng(12).integers(0, SMALL.vocab_size, 20).astype(np.uint32)
+    toks, stats = with_path(path, lambda: model.generate_greedy(prompt, 24))
     ref_toks, _ = ref.generate_greedy(prompt, 24)
-    assert stats["used_graph"] == graph
+    assert stats["used_persistent"] == (path == "persistent")
+    assert stats["used_graph"] == (path == "graph")
     assert toks.tolist() == ref_toks.tolist()
 
 
@@ -176,8 +188,8 @@ VARIED = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512
                          num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=96)
 
 
-@pytest.mark.parametrize("graph", [True, False])
-def test_reference_loop_feed_first_token(ctx, graph):
+@pytest.mark.parametrize("path", ["persistent", "graph"])
+def test_reference_loop_feed_first_token(ctx, path):
     """The reference's generate() loop as written forwards the first generated
     token at every decode step (src/generate.rs:632-650); lq8_generate_ex with
     LQ8_GEN_FEED_FIRST_TOKEN reproduces it, greedy and sampled, on a model
@@ -187,18 +199,16 @@ def test_reference_loop_feed_first_token(ctx, graph):
     model = lq8.Qwen3ForCausalLM.load(ctx, VARIED, tensors)
     ref = oracle.Model(VARIED, tensors)
     prompt = np.random.default_rng(1).integers(0, VARIED.vocab_size, 16).astype(np.uint32)
-    old = os.environ.pop("LQ8_NO_GRAPH", None)
-    if not graph:
-        os.environ["LQ8_NO_GRAPH"] = "1"
-    try:
-        first, _ = model.generate_greedy(prompt, 24, feed_first=True)
+
+    def run():
+        first, st = model.generate_greedy(prompt, 24, feed_first=True)
         latest, _ = model.generate_greedy(prompt, 24)
-        cfg = lq8.GenerationConfig(20, 0.8, 40, 0.95, 1.1)
-        sampled_first, _ = model.generate(prompt, cfg, seed=5, feed_first=True)
-    finally:
-        os.environ.pop("LQ8_NO_GRAPH", None)
-        if old is not None:
-            os.environ["LQ8_NO_GRAPH"] = old
+        sampled_first, _ = model.generate(prompt, lq8.GenerationConfig(20, 0.8, 40, 0.95, 1.1), seed=5,
+                                          feed_first=True)
+        return first, latest, sampled_first, st
+
+    first, latest, sampled_first, st = with_path(path, run)
+    assert st["used_persistent"] == (path == "persistent")
     ref_first, _ = ref.generate_greedy(prompt, 24, feed_first=True)
     ref_latest, _ = ref.generate_greedy(prompt, 24)
     ref_sampled_first = ref.generate_sampled(prompt, 20, 0.8, 40, 0.95, 1.1, 5, feed_first=True)
@@ -257,8 +267,11 @@ def check_0_6b(ctx, cfg, tensors_model, tensors, prompt, label):
     t0 = time.time()
     ref = oracle.Model(cfg, tensors)
     toks, stats = model.generate_greedy(prompt, 128)
+    ptoks, pstats = with_path("persistent", lambda: model.generate_greedy(prompt, 128))
     ref_toks, margins = ref.generate_greedy(prompt, 128)
+    assert pstats["used_persistent"]
     assert toks.tolist() == ref_toks.tolist()
+    assert ptoks.tolist() == ref_toks.tolist()
     K = 32
     canon = chain_logits(ref, prompt, toks, K)
     oracle.set_sequential_sums(True)
@@ -271,7 +284,8 @@ def check_0_6b(ctx, cfg, tensors_model, tensors, prompt, label):
     margin = top2[:, 1] - top2[:, 0]
     decided = margin > 2 * dev
     agree = np.argmax(canon, axis=1) == np.argmax(seq, axis=1)
-    print(f"\n{label}: oracle {time.time() - t0:.1f}s; gpu {stats}; distinct tokens {len(set(toks.tolist()))}; "
+    print(f"\n{label}: oracle {time.time() - t0:.1f}s; gpu {stats}; persistent {pstats}; "
+          f"distinct tokens {len(set(toks.tolist()))}; "
           f"min top-2 margin {float(margins.min()):.3g}; sequential order: max |d logit| {float(dev.max()):.3g}, "
           f"{int(decided.sum())}/{K + 1} steps decided, all agree: {bool(agree[decided].all())}")
     assert np.all(dev <= 0.1 * np.max(np.abs(canon), axis=1))
