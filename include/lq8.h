@@ -192,6 +192,38 @@ lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t
 lq8_status lq8_bench_grid_sync(lq8_ctx* ctx, int kind, int nwg, int rounds, float* us_per_sync,
                                uint32_t* mismatches, uint32_t* gave_up);
 
+/* Phase timeline of the persistent greedy decode (LQ8_PERSIST, see
+ * lq8_generate_greedy), a diagnostic without counterpart in the reference:
+ * in a library built with LQ8_PERSIST_TRACE (make trace -> liblq8_trace.so)
+ * thread 0 of every workgroup stamps the 100 MHz real-time clock at the
+ * LQ8_PT_* marks of the fourth step of each launch, for the first
+ * LQ8_PTRACE_LAYERS layers (the lm_head marks in layer 0's row); words of
+ * marks not passed stay as they were.  out[(wg * LQ8_PTRACE_LAYERS + layer)
+ * * LQ8_PTRACE_POINTS + mark], count = LQ8_PTRACE_WG * LQ8_PTRACE_LAYERS *
+ * LQ8_PTRACE_POINTS.  Other builds return LQ8_ERR_INVALID_ARG. */
+#define LQ8_PTRACE_WG 512
+#define LQ8_PTRACE_LAYERS 64
+#define LQ8_PTRACE_POINTS 16
+enum {
+    LQ8_PT_P1_START = 0,     /* RmsNorm + q|k|v: workgroup enters */
+    LQ8_PT_P1_NORMED = 1,    /* the layer input has arrived and is normalised */
+    LQ8_PT_P2_START = 2,     /* attention: workgroup enters (its q|k|v tile is out) */
+    LQ8_PT_P2_QKV_IN = 3,    /* the segment item's q, k, v have arrived */
+    LQ8_PT_P2_SCORES = 4,    /* scores and softmax partials done */
+    LQ8_PT_P2_PARTIALS = 5,  /* the segment's partials are out */
+    LQ8_PT_P3_START = 6,     /* o GEMV: workgroup enters (combine done where it ran) */
+    LQ8_PT_P3_STAGED = 7,    /* the attention output has arrived */
+    LQ8_PT_P4_START = 8,     /* RmsNorm + gate|up: workgroup enters */
+    LQ8_PT_P4_STAGED = 9,    /* h2 has arrived */
+    LQ8_PT_P5_START = 10,    /* down GEMV: workgroup enters */
+    LQ8_PT_P5_STAGED = 11,   /* silu(gate) * up has arrived */
+    LQ8_PT_P5_DONE = 12,     /* the down tile + residual is out */
+    LQ8_PT_P6_START = 13,    /* lm_head: workgroup enters */
+    LQ8_PT_P6_NORMED = 14,   /* the last layer's output has arrived and is normalised */
+    LQ8_PT_P6_DONE = 15      /* the workgroup's greedy pick is out */
+};
+lq8_status lq8_persist_trace(lq8_ctx* ctx, uint64_t* out, size_t count);
+
 /* ---- Qwen3 model ---------------------------------------------------------
  * Replaces: Qwen3ForCausalLM::load/forward/clear_kv_cache
  * (src/model.rs:273-302, 345-372, 396-398) and generate() with greedy

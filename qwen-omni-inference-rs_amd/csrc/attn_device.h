@@ -3,7 +3,9 @@
 // (decode_persistent.hip): per-head RmsNorm + RoPE, the segment's scores,
 // softmax partials and P.V chain, in the orders the CPU oracle restates
 // (SUM64 denominators, q.k sequential over head_dim, P.V sequential over
-// positions).  Workgroups of ATT_THREADS threads.
+// positions).  Workgroups of NT threads (ATT_THREADS unless stated).
+// PIN_TID: the thread index is taken through tid_here() (for callers inside
+// long-lived loops, where hoisted index math would stay live throughout).
 #pragma once
 
 #include "lq8_internal.h"
@@ -12,6 +14,11 @@
 namespace lq8 {
 
 constexpr int SEG = ATT_SEG;
+
+template <bool PIN>
+__device__ __forceinline__ int thread_x() {
+    return PIN ? tid_here() : (int)threadIdx.x;
+}
 constexpr int KPAD = 129;  // LDS row stride of staged keys (bank-conflict free scores)
 
 // LDS float offsets of the staged K/V rows (16-byte aligned for float4 stores)
@@ -62,20 +69,21 @@ __device__ __forceinline__ void head_norm_rope(const float* src, const float* w,
     head_norm_rope_vals(s0, s1, w0, w1, cs, sn, eps, dst);
 }
 
-// Shared per-segment work of the attention kernels (block ATT_THREADS).
+// Shared per-segment work of the attention kernels (blocks of NT threads).
 // Stages the keys of positions [js, js + nj) into ks (row `knew_row` of the
 // segment, if >= 0, from knew), computes the scores of the G query heads in
 // qs into sc[h][j], then per head m_c, e_j (into sc) and l_c (mlc[2h], mlc[2h+1]).
-// kreg/vreg: this thread's prefetched float4s of the segment's K and V rows.
+// kreg/vreg: this thread's prefetched float4s (ATT_SEG * 32 / NT) of the segment's K and V rows.
 // The loads are unconditional (rows past the segment read row js instead) so
 // they are all in flight together; the values of those rows, and of the new
 // position's row (written by this kernel), are never used.
+template <int NT = ATT_THREADS, bool PIN_TID = false>
 __device__ __forceinline__ void seg_load(const float* __restrict__ Kc, const float* __restrict__ Vc, int js, int nj,
                                          float4* kreg, float4* vreg) {
-    const int tid = threadIdx.x;
+    const int tid = thread_x<PIN_TID>();
 #pragma unroll
-    for (int u = 0; u < ATT_F4; u++) {
-        const int f = tid + u * ATT_THREADS;  // float4 index in the [64][32] segment
+    for (int u = 0; u < ATT_SEG * 32 / NT; u++) {
+        const int f = tid + u * NT;  // float4 index in the [64][32] segment
         const int j = f >> 5, c4 = f & 31;
         const size_t row = (size_t)js + (j < nj ? j : 0);
         kreg[u] = *(const float4*)(Kc + row * 128 + c4 * 4);
@@ -85,12 +93,13 @@ __device__ __forceinline__ void seg_load(const float* __restrict__ Kc, const flo
 
 // The same loads before the position is known: rows js .. js + 63 clamped to
 // the cache capacity (rows past the position are loaded and never used).
+template <int NT = ATT_THREADS, bool PIN_TID = false>
 __device__ __forceinline__ void seg_load_capacity(const float* __restrict__ Kc, const float* __restrict__ Vc, int js,
                                                   int max_pos, float4* kreg, float4* vreg) {
-    const int tid = threadIdx.x;
+    const int tid = thread_x<PIN_TID>();
 #pragma unroll
-    for (int u = 0; u < ATT_F4; u++) {
-        const int f = tid + u * ATT_THREADS;
+    for (int u = 0; u < ATT_SEG * 32 / NT; u++) {
+        const int f = tid + u * NT;
         const int j = f >> 5, c4 = f & 31;
         const size_t row = (size_t)min(js + j, max_pos - 1);
         kreg[u] = *(const float4*)(Kc + row * 128 + c4 * 4);
@@ -98,13 +107,14 @@ __device__ __forceinline__ void seg_load_capacity(const float* __restrict__ Kc, 
     }
 }
 
+template <int NT = ATT_THREADS, bool PIN_TID = false>
 __device__ __forceinline__ void seg_scores(const float4* kreg, int nj, int knew_row, const float* knew, const float* qs,
                                            int G, float scale, float* ks, float* sc, float* mlc) {
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = thread_x<PIN_TID>(), lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 #pragma unroll
-    for (int u = 0; u < ATT_F4; u++) {
-        const int f = tid + u * ATT_THREADS;
+    for (int u = 0; u < ATT_SEG * 32 / NT; u++) {
+        const int f = tid + u * NT;
         const int j = f >> 5, c4 = f & 31;
         if (j < nj) {
             float4 v = kreg[u];
@@ -114,7 +124,7 @@ __device__ __forceinline__ void seg_scores(const float4* kreg, int nj, int knew_
         }
     }
     __syncthreads();
-    for (int t = tid; t < G * SEG; t += ATT_THREADS) {
+    for (int t = tid; t < G * SEG; t += NT) {
         const int h = t / SEG, j = t % SEG;
         if (j < nj) {
             const float* q = qs + h * 128;
@@ -125,7 +135,7 @@ __device__ __forceinline__ void seg_scores(const float4* kreg, int nj, int knew_
         }
     }
     __syncthreads();
-    for (int h = wave; h < G; h += ATT_THREADS / 64) {
+    for (int h = wave; h < G; h += NT / 64) {
         const float s = lane < nj ? sc[h * SEG + lane] : -__builtin_huge_valf();
         const float mc = wave_max64(s);
         const float e = lane < nj ? expf_cr(s - mc) : 0.0f;
@@ -163,11 +173,12 @@ __device__ __forceinline__ float pv_chain(const float* e, const float* vs, int d
 }
 
 // V rows of the segment into vs [64][128] (row vnew_row from vnew).
+template <int NT = ATT_THREADS, bool PIN_TID = false>
 __device__ __forceinline__ void seg_stage_v(const float4* vreg, int nj, int vnew_row, const float* vnew, float* vs) {
-    const int tid = threadIdx.x;
+    const int tid = thread_x<PIN_TID>();
 #pragma unroll
-    for (int u = 0; u < ATT_F4; u++) {
-        const int f = tid + u * ATT_THREADS;
+    for (int u = 0; u < ATT_SEG * 32 / NT; u++) {
+        const int f = tid + u * NT;
         const int j = f >> 5, c4 = f & 31;
         if (j < nj) {
             float4 v = vreg[u];

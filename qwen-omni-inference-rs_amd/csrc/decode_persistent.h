@@ -6,7 +6,7 @@
 
 namespace lq8 {
 
-constexpr int PERSIST_THREADS = 512;
+constexpr int PERSIST_THREADS = 256;
 
 // Device pointers of one decoder layer.
 struct PLayer {
@@ -30,10 +30,12 @@ struct PersistArgs {
     // tagged hand-off words (f32 bits | tag << 32), per layer
     uint64_t* qkvb;   // [L][QKV]
     uint64_t* partb;  // [L][cmax][NH][ATT_PART_STRIDE]
+    uint64_t* attnb;  // [L][NH * 128]: the combined attention output
     uint64_t* h2b;    // [L][H]
     uint64_t* actb;   // [L][I]
     uint64_t* hb;     // [L][H]
     uint64_t* argb;   // [P][2]: each workgroup's greedy pick (value, index bits)
+    unsigned* cntb;   // [L][NKV][16]: per kv head, the step's segment arrivals (back to 0 after the last)
     unsigned* abort_flag;
     // steps: positions pos0 .. pos0 + steps - 1; tokens_out[step0 + s] gets step s's pick
     int pos0, steps, step0, feed_first;

@@ -5,8 +5,10 @@
 //
 // Work of one step (position pos), per layer:
 //   P1  RmsNorm(h) + q|k|v GEMV, one 16-row tile per item
-//   P2  attention, one (kv head, 64-position segment) per item
-//   P3  o GEMV on the combined attention output + residual -> h2, one tile per item
+//   P2  attention, one (kv head, 64-position segment) per item; the last of
+//       a kv head's segment items to finish (an arrival counter) combines the
+//       segments into the head group's attention output
+//   P3  o GEMV on the attention output + residual -> h2, one tile per item
 //   P4  RmsNorm(h2) + gate and up GEMV (tile i of each) -> silu(gate) * up
 //   P5  down GEMV + residual -> h, the next layer's input
 // then P6: final RmsNorm and the lm_head, one wave per 16-row tile, each
@@ -50,12 +52,32 @@ namespace lq8 {
 
 namespace {
 
+#ifdef LQ8_PERSIST_TRACE
+// Phase timeline (built with -DLQ8_PERSIST_TRACE only): thread 0 of every
+// workgroup stamps s_memrealtime (100 MHz) at the marks of the fourth step of
+// each launch, for the first LQ8_PTRACE_LAYERS layers.
+__device__ uint64_t g_ptrace[LQ8_PTRACE_WG * LQ8_PTRACE_LAYERS * LQ8_PTRACE_POINTS];
+__device__ __forceinline__ void ptrace_mark(int w, int s, int l, int pt) {
+    if (s == 3 && threadIdx.x == 0 && w < LQ8_PTRACE_WG && l < LQ8_PTRACE_LAYERS)
+        g_ptrace[((size_t)w * LQ8_PTRACE_LAYERS + l) * LQ8_PTRACE_POINTS + pt] = __builtin_amdgcn_s_memrealtime();
+}
+#define PTRACE(pt) ptrace_mark(w, s, l, pt)
+#else
+#define PTRACE(pt) ((void)0)
+#endif
+
 constexpr int PT = PERSIST_THREADS;
 constexpr int PW = PT / 64;    // waves per workgroup
-constexpr int SLOTS = 16;      // weight chunks a wave holds in registers (two tiles of up to 8)
+// Largest GEMV inputs: hidden (q|k|v, gate/up, lm_head), the attention
+// output (o) and the intermediate size (down).
+constexpr int K_H_MAX = 1024, K_Q_MAX = 2048, K_I_MAX = 4096;
+// groups of two block pairs a wave holds for one tile of input length k
+constexpr int groups_per_wave(int k) { return ((k / 64 + 1) / 2 + PW - 1) / PW; }
+constexpr int NG_H = groups_per_wave(K_H_MAX), NG_Q = groups_per_wave(K_Q_MAX), NG_I = groups_per_wave(K_I_MAX);
+constexpr int SLOTS = 2 * NG_I;  // weight chunks a wave holds in registers
 constexpr int LM_MAX_NP = 16;  // lm_head tiles held per wave: up to 16 block pairs (hidden <= 1024)
-constexpr int GPW = 4;         // groups of two block pairs a wave holds for one tile
-constexpr int GS_TILE = PW * GPW * 16;  // group sums of one tile (floats)
+constexpr int GS_TILE = PW * NG_I * 16;  // group sums of one tile (floats)
+constexpr int CNT_STRIDE = 16;  // u32 per arrival counter (one per 64 bytes)
 
 // A value the compiler must treat as produced here: per-thread index math
 // derived from it is recomputed in each loop iteration instead of being
@@ -107,15 +129,15 @@ __device__ __forceinline__ float tget(const uint64_t* p, unsigned tag, unsigned*
     return tok_tag(v, tag) ? __uint_as_float((unsigned)v) : twait(p, v, tag, abort_flag, bad);
 }
 
-// dst[i] = src[i] for i < n (tagged words), 4 loads per thread in flight.
+// dst[i] = src[i] for i < n (tagged words), 8 loads per thread in flight.
 __device__ __forceinline__ void tfetch(const uint64_t* src, int n, unsigned tag, float* dst, unsigned* abort_flag,
                                        volatile int* bad) {
-    for (int i0 = threadIdx.x; i0 < n; i0 += 4 * PT) {
-        uint64_t v[4];
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * PT) {
+        uint64_t v[8];
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = traw(src + min(i0 + u * PT, n - 1));
+        for (int u = 0; u < 8; u++) v[u] = traw(src + min(i0 + u * PT, n - 1));
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < 8; u++) {
             const int i = i0 + u * PT;
             if (i < n)
                 dst[i] = tok_tag(v[u], tag) ? __uint_as_float((unsigned)v[u]) : twait(src + i, v[u], tag, abort_flag, bad);
@@ -132,7 +154,7 @@ __device__ __forceinline__ float q8_elem(const int8_t* codes, const uint16_t* sc
 
 // ---- GEMV of one 16-row tile by the whole workgroup ----------------------------
 // The tile's np block pairs form G = ceil(np / 2) groups of two pairs; wave w
-// takes groups w, w + PW, ... (at most GPW of them: np <= 2 * PW * GPW), with
+// takes groups w, w + PW, ... (at most NG of them: np <= 2 * PW * NG), with
 // the chunk loads of its gi-th group held in slots S0 + 2 gi, S0 + 2 gi + 1.
 // The group sums meet in the pairwise tree over the groups: together the
 // block tree of the GEMV order (gemv_tiles), bit for bit.
@@ -141,7 +163,7 @@ struct WRegs {
     uint16_t d[SLOTS];
 };
 
-template <int S0>
+template <int S0, int NG>
 __device__ __forceinline__ void tile_load(const int8_t* codes, const uint16_t* scales, int np, int tile, WRegs& R) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -149,10 +171,13 @@ __device__ __forceinline__ void tile_load(const int8_t* codes, const uint16_t* s
     const int r = lane & 15, bsel = (lane >> 4) >> 1;
     const int8_t* cb = codes + (size_t)tile * np * CHUNK_BYTES + lane * 16;
     const uint16_t* sb = scales + (size_t)tile * 2 * np * 16 + bsel * 16 + r;
+    // groups are taken in pairs: a wave with an odd group count also loads
+    // (a copy of) the tile's last group as its last pair's partner
+    const int ngr = G > wave ? (G - wave + PW - 1) / PW : 0;
 #pragma unroll
-    for (int gi = 0; gi < GPW; gi++) {
-        const int g = wave + gi * PW;
-        if (g < G) {
+    for (int gi = 0; gi < NG; gi++) {
+        if (gi < ((ngr + 1) & ~1)) {
+            const int g = min(wave + gi * PW, G - 1);
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const int p = min(2 * g + i, np - 1);
@@ -171,42 +196,90 @@ __device__ __forceinline__ float dot16_pinned(u32x4 c, const float* __restrict__
     return dot16(c, x);
 }
 
-// Group sums of the wave's groups into gs[g * 16 + row].
-template <int S0>
+// Four chunk dots at once: the GEMV's 16-term chains (each in its order,
+// from +0, as dot16), interleaved so that the four dependency chains overlap
+// -- with one wave per SIMD nothing else hides their latency.  The codes are
+// pinned here (see dot16_pinned).
+__device__ __forceinline__ void dot16x4_pinned(u32x4 c0, u32x4 c1, u32x4 c2, u32x4 c3, const float* x0,
+                                               const float* x1, const float* x2, const float* x3, float* out) {
+    asm volatile("" : "+v"(c0.x), "+v"(c0.y), "+v"(c0.z), "+v"(c0.w), "+v"(c1.x), "+v"(c1.y), "+v"(c1.z), "+v"(c1.w),
+                      "+v"(c2.x), "+v"(c2.y), "+v"(c2.z), "+v"(c2.w), "+v"(c3.x), "+v"(c3.y), "+v"(c3.z), "+v"(c3.w));
+    const uint32_t w[4][4] = {{c0.x, c0.y, c0.z, c0.w}, {c1.x, c1.y, c1.z, c1.w}, {c2.x, c2.y, c2.z, c2.w},
+                              {c3.x, c3.y, c3.z, c3.w}};
+    const float* x[4] = {x0, x1, x2, x3};
+    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float4 xv[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) xv[k] = *(const float4*)(x[k] + 4 * i);
+#pragma unroll
+        for (int k = 0; k < 4; k++) p[k] = fmaf((float)(int8_t)(w[k][i] & 0xFF), xv[k].x, p[k]);
+#pragma unroll
+        for (int k = 0; k < 4; k++) p[k] = fmaf((float)(int8_t)((w[k][i] >> 8) & 0xFF), xv[k].y, p[k]);
+#pragma unroll
+        for (int k = 0; k < 4; k++) p[k] = fmaf((float)(int8_t)((w[k][i] >> 16) & 0xFF), xv[k].z, p[k]);
+#pragma unroll
+        for (int k = 0; k < 4; k++) p[k] = fmaf((float)(int8_t)(w[k][i] >> 24), xv[k].w, p[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) out[k] = p[k];
+}
+
+// Group sums of the wave's groups into gs[g * 16 + row], two groups (four
+// chunks) at a time.
+template <int S0, int NG>
 __device__ __forceinline__ void tile_dot(const WRegs& R, const float* xs, int np, int nb, float* gs) {
+    static_assert(NG % 2 == 0, "groups are taken in pairs");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int G = (np + 1) >> 1;
     const int part = lane >> 4, bsel = part >> 1, half = part & 1;
     const int ngr = G > wave ? (G - wave + PW - 1) / PW : 0;  // the wave's groups
 #pragma unroll
-    for (int gi = 0; gi < GPW; gi++) {
+    for (int gi = 0; gi < NG; gi += 2) {
         if (gi < ngr) {
-            const int g = wave + gi * PW;
-            float v[2];
+            const bool two = gi + 1 < ngr;  // else the partner is the copy tile_load took (result unused)
+            const int g0 = wave + gi * PW, g1 = min(g0 + PW, G - 1);
+            const int p[4] = {min(2 * g0, np - 1), min(2 * g0 + 1, np - 1), min(2 * g1, np - 1), min(2 * g1 + 1, np - 1)};
+            constexpr int s0 = S0 + 0;
+            float h[4];
+            dot16x4_pinned(R.c[s0 + 2 * gi], R.c[s0 + 2 * gi + 1], R.c[s0 + 2 * gi + 2], R.c[s0 + 2 * gi + 3],
+                           xs + (2 * p[0] + bsel) * 32 + half * 16, xs + (2 * p[1] + bsel) * 32 + half * 16,
+                           xs + (2 * p[2] + bsel) * 32 + half * 16, xs + (2 * p[3] + bsel) * 32 + half * 16, h);
+            float v[4];
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int p = min(2 * g + i, np - 1);
-                const float h = dot16_pinned(R.c[S0 + 2 * gi + i], xs + (2 * p + bsel) * 32 + half * 16);
-                const LanePair hh = lanes16(h);
-                const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(R.d[S0 + 2 * gi + i]);
+            for (int k = 0; k < 4; k++) {
+                const LanePair hh = lanes16(h[k]);
+                const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(R.d[s0 + 2 * gi + k]);
                 const LanePair vv = lanes32(vb);
-                v[i] = 2 * p + 1 >= nb ? vv.lo : vv.lo + vv.hi;
+                v[k] = 2 * p[k] + 1 >= nb ? vv.lo : vv.lo + vv.hi;
             }
-            const float vg = 2 * g + 1 < np ? v[0] + v[1] : v[0];
-            if (lane < 16) gs[g * 16 + lane] = vg;
+            const float vg0 = 2 * g0 + 1 < np ? v[0] + v[1] : v[0];
+            const float vg1 = 2 * g1 + 1 < np ? v[2] + v[3] : v[2];
+            if (lane < 16) {
+                gs[g0 * 16 + lane] = vg0;
+                if (two) gs[g1 * 16 + lane] = vg1;
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
 
-// Row `lane` (< 16) of the tile: the tree over the G group sums, in place in
-// gs (16 lanes, each its own column).
+// Row `lane` (< 16) of the tile: the pairwise tree over the G group sums, in
+// place in gs (column `lane` per row).  Called by a whole wave: the four
+// 16-lane quarters take the disjoint pairs of a level in turn, so the level's
+// additions are the same ones in the same places as one lane per row doing
+// them in order.
 __device__ __forceinline__ float tile_final(float* gs, int G) {
-    const int lane = threadIdx.x & 63;
-    for (int s = 1; s < G; s *= 2)
-        for (int i = 0; i + s < G; i += 2 * s) gs[i * 16 + lane] = gs[i * 16 + lane] + gs[(i + s) * 16 + lane];
-    return gs[lane];
+    const int lane = threadIdx.x & 63, col = lane & 15, q = lane >> 4;
+    for (int s = 1; s < G; s *= 2) {
+        for (int i = 2 * s * q; i + s < G; i += 8 * s) gs[i * 16 + col] = gs[i * 16 + col] + gs[(i + s) * 16 + col];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    return gs[col];
 }
 
 // RmsNorm (src/rms_norm.rs:143-176) of xs[0, k) in place, in the order of
@@ -233,6 +306,60 @@ __device__ __forceinline__ void stage_pad(float* xs, int k, int np) {
     for (int i = k + threadIdx.x; i < np * 64; i += PT) xs[i] = 0.0f;
 }
 
+// The attention output of kv head g's query heads (g G .. g G + G - 1) from
+// the partials (o_c[128], m_c, l_c) of its C segments, in segment order: per
+// head the running max m and denominator den with the coefficients
+// a_c = exp(m - m'), b_c = exp(m_c - m'), then per element
+// num = num * a_c + b_c * o_c and out = num / den -- the combine that the
+// separate kernels do in the o GEMV's input staging.  lds: 33 G floats.
+// Not inlined: only one workgroup per kv head runs it, and its registers stay
+// out of the attention phase's allocation.
+__device__ __noinline__ void combine_group(const uint64_t* partb, uint64_t* out, int g, int C, int NH, int G,
+                                              unsigned tag, float* lds, unsigned* abort_flag, volatile int* bad) {
+    const int tid = threadIdx.x;
+    float* mcl = lds;                  // [C][G][2]
+    float* coef = mcl + 2 * 8 * G;     // [C][G][2]
+    float* dens = coef + 2 * 8 * G;    // [G]
+    for (int q = tid; q < C * G; q += PT) {
+        const uint64_t* p = partb + ((size_t)(q / G) * NH + g * G + q % G) * ATT_PART_STRIDE;
+        mcl[2 * q] = tget(p + 128, tag, abort_flag, bad);
+        mcl[2 * q + 1] = tget(p + 129, tag, abort_flag, bad);
+    }
+    __syncthreads();
+    if (tid < G) {
+        float m = -__builtin_huge_valf(), den = 0.0f;
+        for (int c = 0; c < C; c++) {
+            const int q = c * G + tid;
+            const float mc = mcl[2 * q], lc = mcl[2 * q + 1];
+            const float mn = m > mc ? m : mc;
+            const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
+            coef[2 * q] = ea;
+            coef[2 * q + 1] = eb;
+            den = den * ea + eb * lc;
+            m = mn;
+        }
+        dens[tid] = den;
+    }
+    __syncthreads();
+    for (int i = tid; i < G * 128; i += PT) {
+        const int hh = i >> 7, d = i & 127;
+        uint64_t ro[8];  // C <= 8: every segment's word in flight together
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+            ro[c] = traw(partb + ((size_t)min(c, C - 1) * NH + g * G + hh) * ATT_PART_STRIDE + d);
+        float num = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            if (c < C) {
+                const uint64_t* p = partb + ((size_t)c * NH + g * G + hh) * ATT_PART_STRIDE + d;
+                const float o = tok_tag(ro[c], tag) ? __uint_as_float((unsigned)ro[c]) : twait(p, ro[c], tag, abort_flag, bad);
+                num = num * coef[2 * (c * G + hh)] + coef[2 * (c * G + hh) + 1] * o;
+            }
+        }
+        tput(out + i, __fdiv_rn(num, dens[hh]), tag);
+    }
+}
+
 struct Dims {
     int H, I, NH, NKV, G, QD, KD, QKV, npH, nbH, GH, npQ, nbQ, GQ, npI, nbI, GI;  // G*: groups of two pairs
 };
@@ -249,8 +376,8 @@ __device__ __forceinline__ Dims dims_of(const PersistArgs& a) {
 
 // Per-phase locals, recomputed where used (from the opaque argument block):
 // the model's dimensions, the phase item counts, the per-layer strides and
-// the LDS layout -- region A (the staged GEMV input and the combine
-// coefficients, or the attention segment), then the group sums and the
+// the LDS layout -- region A (the staged GEMV input, or the attention
+// segment and then the combine's scratch), then the group sums and the
 // RmsNorm reduction.
 #define PHASE_LOCALS                                                                                        \
     const Dims D = dims_of(a);                                                                              \
@@ -259,7 +386,6 @@ __device__ __forceinline__ Dims dims_of(const PersistArgs& a) {
     const size_t kv_layer = (size_t)D.NKV * a.max_pos * 128;                                                \
     const size_t part_layer = (size_t)a.cmax * D.NH * ATT_PART_STRIDE;                                      \
     float* xs = sm;                                                                                         \
-    float* coef = sm + a.xs_floats; /* [cmax][NH][2], dens [NH], (m, l) [cmax][NH][2] */                      \
     float* gs = sm + a.region_a;    /* [2][GS_TILE] */                                                      \
     float* red = gs + 2 * GS_TILE;  /* [16] */                                                              \
     float* qs = sm;                 /* attention: [G][128] */                                               \
@@ -269,11 +395,12 @@ __device__ __forceinline__ Dims dims_of(const PersistArgs& a) {
     float* mlc = sc + D.G * ATT_SEG; /* [G][2] */                                                           \
     float* ks = sm + seg_ks_off(D.G); /* [64][KPAD], later the V rows [64][128] */                           \
     (void)T1; (void)TH; (void)TI; (void)T6; (void)items2; (void)kv_layer; (void)part_layer; (void)xs;      \
-    (void)coef; (void)gs; (void)red; (void)qs; (void)kn; (void)vn; (void)sc; (void)mlc; (void)ks
+    (void)gs; (void)red; (void)qs; (void)kn; (void)vn; (void)sc; (void)mlc; (void)ks
 
 __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __restrict__ pa) {
     extern __shared__ float sm[];
     __shared__ int bad_s;
+    __shared__ int last_s;
     __shared__ float pick_v[PW];
     __shared__ int pick_i[PW];
     volatile int* bad = &bad_s;
@@ -326,6 +453,8 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             const PLayer Lw = a.layers[l];
             uint64_t* qkvb = a.qkvb + (size_t)l * D.QKV;
             uint64_t* partb = a.partb + (size_t)l * part_layer;
+            uint64_t* attnb = a.attnb + (size_t)l * D.QD;
+            unsigned* cntb = a.cntb + (size_t)l * D.NKV * CNT_STRIDE;
             uint64_t* h2b = a.h2b + (size_t)l * D.H;
             uint64_t* actb = a.actb + (size_t)l * D.I;
             uint64_t* hb = a.hb + (size_t)l * D.H;
@@ -335,8 +464,9 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
 
             // ---- P1: RmsNorm(h) + q|k|v tiles
             if (w < T1) {
+                PTRACE(LQ8_PT_P1_START);
                 WRegs R;
-                tile_load<0>(Lw.qkv_c, Lw.qkv_s, D.npH, w, R);
+                tile_load<0, NG_H>(Lw.qkv_c, Lw.qkv_s, D.npH, w, R);
                 if (hin) tfetch(hin, D.H, tag, xs, a.abort_flag, bad);
                 else
                     for (int j = tid; j < D.H; j += PT) xs[j] = q8_elem(a.emb_c, a.emb_s, D.npH, (int)tok, j);
@@ -344,20 +474,22 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 __syncthreads();
                 if (*bad) goto done;
                 stage_rmsnorm(xs, D.H, Lw.in_norm, a.eps, red);
+                PTRACE(LQ8_PT_P1_NORMED);
                 for (int t = w; t < T1; t += P) {
-                    if (t != w) tile_load<0>(Lw.qkv_c, Lw.qkv_s, D.npH, t, R);
-                    tile_dot<0>(R, xs, D.npH, D.nbH, gs);
+                    if (t != w) tile_load<0, NG_H>(Lw.qkv_c, Lw.qkv_s, D.npH, t, R);
+                    tile_dot<0, NG_H>(R, xs, D.npH, D.nbH, gs);
                     __syncthreads();
-                    if (tid < 16) {
+                    if (tid < 64) {
                         const float y = tile_final(gs, D.GH);
                         const int row = t * 16 + tid;
-                        if (row < D.QKV) tput(qkvb + row, y, tag);
+                        if (tid < 16 && row < D.QKV) tput(qkvb + row, y, tag);
                     }
                     __syncthreads();
                 }
             }
 
             // ---- P2: attention per (kv head, segment)
+            PTRACE(LQ8_PT_P2_START);
             {
                 const int L1 = pos + 1, C = (L1 + ATT_SEG - 1) / ATT_SEG;
                 for (int it = w; it < items2; it += P) {
@@ -368,8 +500,8 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     const int newrow = last ? pos - js : -1;
                     float* Kc = Kl + (size_t)g * a.max_pos * 128;
                     float* Vc = Vl + (size_t)g * a.max_pos * 128;
-                    float4 kreg[ATT_F4], vreg[ATT_F4];
-                    seg_load(Kc, Vc, js, nj, kreg, vreg);
+                    float4 kreg[ATT_SEG * 32 / PT], vreg[ATT_SEG * 32 / PT];
+                    seg_load<PT, true>(Kc, Vc, js, nj, kreg, vreg);
                     const float* cs = a.cos_t + (size_t)pos * 64;
                     const float* sn = a.sin_t + (size_t)pos * 64;
                     for (int t = wave; t < D.G + 2; t += PW) {
@@ -399,9 +531,11 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     }
                     __syncthreads();
                     if (*bad) goto done;
-                    seg_scores(kreg, nj, newrow, kn, qs, D.G, a.scale, ks, sc, mlc);
+                    PTRACE(LQ8_PT_P2_QKV_IN);
+                    seg_scores<PT, true>(kreg, nj, newrow, kn, qs, D.G, a.scale, ks, sc, mlc);
                     __syncthreads();
-                    seg_stage_v(vreg, nj, newrow, vn, ks);
+                    PTRACE(LQ8_PT_P2_SCORES);
+                    seg_stage_v<PT, true>(vreg, nj, newrow, vn, ks);
                     __syncthreads();
                     for (int t = tid; t < D.G * 128; t += PT) {
                         const int h = t >> 7, d = t & 127;
@@ -413,130 +547,82 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                             tput(p + 129, mlc[2 * h + 1], tag);
                         }
                     }
+                    // every partial of the item is stored (write-through) before
+                    // the item arrives at kv head g's counter; the C-th arrival
+                    // resets the counter for the next step and combines
+                    PTRACE(LQ8_PT_P2_PARTIALS);
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __syncthreads();
+                    if (tid == 0) {
+                        unsigned* cn = cntb + (size_t)g * CNT_STRIDE;
+                        const bool lastc = sync_add(cn, 1u) + 1 == (unsigned)C;
+                        if (lastc) {
+                            sync_store(cn, 0u);
+                            __builtin_amdgcn_s_waitcnt(0);  // the reset lands before the output is published
+                        }
+                        last_s = lastc ? 1 : 0;
+                    }
+                    __syncthreads();
+                    if (last_s) combine_group(partb, attnb + (size_t)g * D.G * 128, g, C, D.NH, D.G, tag, sm,
+                                              a.abort_flag, bad);
                     __syncthreads();
                 }
             }
 
-            // ---- P3: combine the segments, o tile, + residual -> h2
+            // ---- P3: o tile on the attention output, + residual -> h2
+            PTRACE(LQ8_PT_P3_START);
             for (int t = w; t < TH; t += P) {
                 WRegs R;
-                tile_load<0>(Lw.o_c, Lw.o_s, D.npQ, t, R);
+                tile_load<0, NG_Q>(Lw.o_c, Lw.o_s, D.npQ, t, R);
                 const int row = t * 16 + tid;
                 uint64_t rres = 0;  // the residual word, loaded early
                 if (tid < 16 && row < D.H && hin) rres = traw(hin + row);
-                const int C = (pos + 1 + ATT_SEG - 1) / ATT_SEG;
-                float* dens = coef + a.cmax * D.NH * 2;
-                // the partials of this thread's (up to 4) elements are issued
-                // first, before the coefficient chain (C <= 8 segments)
-                uint64_t ro[4][8];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int i = min(tid + e * PT, D.QD - 1), h = i >> 7, d = i & 127;
-#pragma unroll
-                    for (int c = 0; c < 8; c++)
-                        ro[e][c] = traw(partb + ((size_t)min(c, C - 1) * D.NH + h) * ATT_PART_STRIDE + d);
-                }
-                // (m_c, l_c) of every (segment, head) into LDS, then per head the
-                // running max / denominator over the segments in order
-                float* mcl = dens + D.NH;  // [C][NH][2]
-                for (int q = tid; q < C * D.NH; q += PT) {
-                    const uint64_t* p = partb + (size_t)q * ATT_PART_STRIDE;  // (c, h) = (q / NH, q % NH)
-                    mcl[2 * q] = tget(p + 128, tag, a.abort_flag, bad);
-                    mcl[2 * q + 1] = tget(p + 129, tag, a.abort_flag, bad);
-                }
-                __syncthreads();
-                if (*bad) goto done;
-                if (tid < D.NH) {
-                    const int h = tid;
-                    float m = -__builtin_huge_valf(), den = 0.0f;
-#pragma unroll 1
-                    for (int c = 0; c < C; c++) {
-                        const float mc = mcl[2 * (c * D.NH + h)], lc = mcl[2 * (c * D.NH + h) + 1];
-                        const float mn = m > mc ? m : mc;
-                        const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
-                        coef[(c * D.NH + h) * 2] = ea;
-                        coef[(c * D.NH + h) * 2 + 1] = eb;
-                        den = den * ea + eb * lc;
-                        m = mn;
-                    }
-                    dens[h] = den;
-                }
-                __syncthreads();
-                // the words that arrived after their first load are loaded
-                // again, each until it carries the tag (one shared slow path)
-                {
-                    bool late = false;
-#pragma unroll
-                    for (int e = 0; e < 4; e++)
-#pragma unroll
-                        for (int c = 0; c < 8; c++) late |= (tid + e * PT < D.QD && c < C && !tok_tag(ro[e][c], tag));
-                    if (late) {
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            const int i = min(tid + e * PT, D.QD - 1), h = i >> 7, d = i & 127;
-#pragma unroll
-                            for (int c = 0; c < 8; c++) {
-                                const uint64_t* p = partb + ((size_t)min(c, C - 1) * D.NH + h) * ATT_PART_STRIDE + d;
-                                if (!tok_tag(ro[e][c], tag))
-                                    ro[e][c] = ((uint64_t)tag << 32) | __float_as_uint(tget(p, tag, a.abort_flag, bad));
-                            }
-                        }
-                    }
-                }
-                // num = num * a_c + b_c * o_c over the segments in order; x = num / den
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int i = tid + e * PT;
-                    if (i < D.QD) {
-                        const int h = i >> 7;
-                        float num = 0.0f;
-#pragma unroll
-                        for (int c = 0; c < 8; c++)
-                            if (c < C)
-                                num = num * coef[(c * D.NH + h) * 2] +
-                                      coef[(c * D.NH + h) * 2 + 1] * __uint_as_float((unsigned)ro[e][c]);
-                        xs[i] = __fdiv_rn(num, dens[h]);
-                    }
-                }
+                tfetch(attnb, D.QD, tag, xs, a.abort_flag, bad);
                 stage_pad(xs, D.QD, D.npQ);
                 __syncthreads();
                 if (*bad) goto done;
-                tile_dot<0>(R, xs, D.npQ, D.nbQ, gs);
+                PTRACE(LQ8_PT_P3_STAGED);
+                tile_dot<0, NG_Q>(R, xs, D.npQ, D.nbQ, gs);
                 __syncthreads();
-                if (tid < 16 && row < D.H) {
+                if (tid < 64) {
                     const float acc = tile_final(gs, D.GQ);
-                    const float res = hin ? (tok_tag(rres, tag) ? __uint_as_float((unsigned)rres)
-                                                                : twait(hin + row, rres, tag, a.abort_flag, bad))
-                                          : q8_elem(a.emb_c, a.emb_s, D.npH, (int)tok, row);
-                    tput(h2b + row, res + acc, tag);
+                    if (tid < 16 && row < D.H) {
+                        const float res = hin ? (tok_tag(rres, tag) ? __uint_as_float((unsigned)rres)
+                                                                    : twait(hin + row, rres, tag, a.abort_flag, bad))
+                                              : q8_elem(a.emb_c, a.emb_s, D.npH, (int)tok, row);
+                        tput(h2b + row, res + acc, tag);
+                    }
                 }
                 __syncthreads();
             }
 
             // ---- P4: RmsNorm(h2) + gate / up tile pair -> silu(gate) * up
+            PTRACE(LQ8_PT_P4_START);
             for (int t = w; t < TI; t += P) {
                 WRegs R;
-                tile_load<0>(Lw.gu_c, Lw.gu_s, D.npH, t, R);
-                tile_load<8>(Lw.gu_c, Lw.gu_s, D.npH, TI + t, R);
+                tile_load<0, NG_H>(Lw.gu_c, Lw.gu_s, D.npH, t, R);
+                tile_load<2 * NG_H, NG_H>(Lw.gu_c, Lw.gu_s, D.npH, TI + t, R);
                 tfetch(h2b, D.H, tag, xs, a.abort_flag, bad);
                 stage_pad(xs, D.H, D.npH);
                 __syncthreads();
                 if (*bad) goto done;
+                PTRACE(LQ8_PT_P4_STAGED);
                 stage_rmsnorm(xs, D.H, Lw.post_norm, a.eps, red);
-                tile_dot<0>(R, xs, D.npH, D.nbH, gs);
-                tile_dot<8>(R, xs, D.npH, D.nbH, gs + GS_TILE);
+                tile_dot<0, NG_H>(R, xs, D.npH, D.nbH, gs);
+                tile_dot<2 * NG_H, NG_H>(R, xs, D.npH, D.nbH, gs + GS_TILE);
                 __syncthreads();
-                if (tid < 16) {
+                if (tid < 64) {
                     const float g = tile_final(gs, D.GH), u = tile_final(gs + GS_TILE, D.GH);
-                    tput(actb + t * 16 + tid, silu_mul(g, u), tag);
+                    if (tid < 16) tput(actb + t * 16 + tid, silu_mul(g, u), tag);
                 }
                 __syncthreads();
             }
 
             // ---- P5: down tile + residual -> h
+            PTRACE(LQ8_PT_P5_START);
             for (int t = w; t < TH; t += P) {
                 WRegs R;
-                tile_load<0>(Lw.dn_c, Lw.dn_s, D.npI, t, R);
+                tile_load<0, NG_I>(Lw.dn_c, Lw.dn_s, D.npI, t, R);
                 const int row = t * 16 + tid;
                 uint64_t rres = 0;
                 if (tid < 16 && row < D.H) rres = traw(h2b + row);
@@ -544,20 +630,26 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 stage_pad(xs, D.I, D.npI);
                 __syncthreads();
                 if (*bad) goto done;
-                tile_dot<0>(R, xs, D.npI, D.nbI, gs);
+                PTRACE(LQ8_PT_P5_STAGED);
+                tile_dot<0, NG_I>(R, xs, D.npI, D.nbI, gs);
                 __syncthreads();
-                if (tid < 16 && row < D.H) {
+                if (tid < 64) {
                     const float acc = tile_final(gs, D.GI);
-                    const float res = tok_tag(rres, tag) ? __uint_as_float((unsigned)rres)
-                                                         : twait(h2b + row, rres, tag, a.abort_flag, bad);
-                    tput(hb + row, res + acc, tag);
+                    if (tid < 16 && row < D.H) {
+                        const float res = tok_tag(rres, tag) ? __uint_as_float((unsigned)rres)
+                                                             : twait(h2b + row, rres, tag, a.abort_flag, bad);
+                        tput(hb + row, res + acc, tag);
+                    }
                 }
                 __syncthreads();
+                PTRACE(LQ8_PT_P5_DONE);
             }
         }
 
         // ---- P6: final RmsNorm, lm_head tiles (one wave each), greedy pick
         {
+            [[maybe_unused]] const int l = 0;  // the P6 marks sit in layer 0's row
+            PTRACE(LQ8_PT_P6_START);
             const PersistArgs& a = *opaque_args(pa);
             const int tid = opaque((int)threadIdx.x), lane = tid & 63;
             PHASE_LOCALS;
@@ -583,6 +675,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             __syncthreads();
             if (*bad) goto done;
             stage_rmsnorm(xs, D.H, a.final_norm, a.eps, red);
+            PTRACE(LQ8_PT_P6_NORMED);
             float bv = -__builtin_huge_valf();
             int bi = -1;
             for (int t = t0; t < T6; t += tstride) {
@@ -626,6 +719,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 tput(a.argb + 2 * w + 1, __uint_as_float((unsigned)wi), tag);
             }
             __syncthreads();
+            PTRACE(LQ8_PT_P6_DONE);
         }
     }
 
@@ -667,12 +761,11 @@ bool persist_supported(const PersistShape& s, int num_cus) {
     if (s.head_dim != 128 || s.NKV <= 0 || s.NH % s.NKV) return false;
     const int G = s.NH / s.NKV;
     if (G > ATT_MAX_GROUP) return false;
-    // hidden <= 1024: a wave holds a whole lm_head tile (16 block pairs)
-    // the o-projection's combine: up to 4 elements per thread, up to 8 segments
-    if (s.H % 32 || s.H > 1024 || s.I % 32 || s.I > 4096 || s.NH * 128 > 4 * PT) return false;
+    // GEMV inputs within the groups a wave holds for a tile (hidden <= 1024
+    // also lets a wave hold a whole lm_head tile, 16 block pairs); the
+    // combine: up to 8 segments
+    if (s.H % 32 || s.H > K_H_MAX || s.I % 32 || s.I > K_I_MAX || s.NH * 128 > K_Q_MAX) return false;
     if (s.max_pos > 8 * ATT_SEG || num_cus <= 0) return false;
-    // a wave holds at most GPW groups of two block pairs of a tile: k <= 4096
-    if (s.I > 2 * PW * GPW * 64 || s.NH * 128 > 2 * PW * GPW * 64) return false;
     return persist_smem_bytes(s) <= 64 * 1024;
 }
 
@@ -683,9 +776,9 @@ size_t persist_xs_floats(const PersistShape& s) {
 
 size_t persist_region_a(const PersistShape& s) {
     const int G = s.NH / s.NKV;
-    const int cmax = (s.max_pos + ATT_SEG - 1) / ATT_SEG;
-    const size_t a1 = persist_xs_floats(s) + (size_t)cmax * s.NH * 4 + s.NH;  // coef, dens, (m, l)
-    const size_t a2 = (size_t)seg_ks_off(G) + (size_t)ATT_SEG * KPAD;
+    const size_t a1 = persist_xs_floats(s);
+    // the attention segment; the combine's scratch (33 G floats) reuses it
+    const size_t a2 = std::max((size_t)seg_ks_off(G) + (size_t)ATT_SEG * KPAD, (size_t)33 * G);
     return (std::max(a1, a2) + 3) & ~(size_t)3;
 }
 
@@ -704,3 +797,18 @@ lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, i
 }
 
 }  // namespace lq8
+
+using namespace lq8;
+
+extern "C" lq8_status lq8_persist_trace(lq8_ctx* ctx, uint64_t* out, size_t count) {
+    if (!registry_has(ctx)) return fail(LQ8_ERR_INVALID_ARG, "invalid context handle");
+    if (!out || count != (size_t)LQ8_PTRACE_WG * LQ8_PTRACE_LAYERS * LQ8_PTRACE_POINTS)
+        return fail(LQ8_ERR_INVALID_ARG, "trace buffer must hold LQ8_PTRACE_WG * LQ8_PTRACE_LAYERS * LQ8_PTRACE_POINTS words");
+#ifdef LQ8_PERSIST_TRACE
+    LQ8_HIP(hipSetDevice(ctx->device));
+    LQ8_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(lq8::g_ptrace), count * sizeof(uint64_t)));
+    return LQ8_OK;
+#else
+    return fail(LQ8_ERR_INVALID_ARG, "library built without LQ8_PERSIST_TRACE (make trace)");
+#endif
+}

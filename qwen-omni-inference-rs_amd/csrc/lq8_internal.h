@@ -265,6 +265,16 @@ lq8_status launch_qk_rope_kv(hipStream_t s, const QkRopeLaunch& a);
 
 // Attention (head_dim 128, G = num_heads / num_kv_heads <= ATT_MAX_GROUP
 // query heads per kv head), positions in segments of ATT_SEG.
+// threadIdx.x as a value the compiler must treat as produced here: index
+// math derived from it stays next to its use instead of being hoisted out of
+// enclosing loops (in a persistent kernel: held in registers through every
+// phase).
+__device__ __forceinline__ int tid_here() {
+    int x = (int)threadIdx.x;
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 constexpr int ATT_SEG = 64;
 constexpr int ATT_THREADS = 512;
 constexpr int ATT_F4 = ATT_SEG * 32 / ATT_THREADS;  // float4 of one segment's K (or V) per thread

@@ -73,7 +73,7 @@ struct lq8_model {
     // persistent greedy decode (decode_persistent.hip): per-layer weight
     // pointers, tagged hand-off buffers, the argument block, the abort flag
     PLayer* d_player = nullptr;
-    uint64_t* hand = nullptr;  // qkvb | partb | h2b | actb | hb | argb
+    uint64_t* hand = nullptr;  // qkvb | partb | attnb | h2b | actb | hb | argb | arrival counters
     size_t hand_words = 0;
     PersistArgs* d_pargs = nullptr;
     PersistArgs h_pargs{};     // host copy (the source of the argument upload)
@@ -521,8 +521,9 @@ lq8_status persist_setup(lq8_model* m) {
     const PersistShape sh = persist_shape(m);
     const size_t L = c.num_layers, H = c.hidden_size, I = c.intermediate_size, NH = c.num_heads;
     const size_t cmax = (size_t)m->cmax;
-    const size_t qkv = L * m->QKV, part = L * cmax * NH * ATT_PART_STRIDE, h2 = L * H, act = L * I, h = L * H;
-    m->hand_words = qkv + part + h2 + act + h + 2 * (size_t)P;
+    const size_t qkv = L * m->QKV, part = L * cmax * NH * ATT_PART_STRIDE, attn = L * NH * 128, h2 = L * H,
+                 act = L * I, h = L * H, cnt = L * c.num_kv_heads * 16 / 2;  // counters: 16 u32 each
+    m->hand_words = qkv + part + attn + h2 + act + h + 2 * (size_t)P + cnt;
     std::vector<PLayer> pl(L);
     for (size_t l = 0; l < L; l++) {
         const Layer& Ly = m->layers[l];
@@ -552,10 +553,12 @@ lq8_status persist_setup(lq8_model* m) {
     a.scale = 1.0f / std::sqrt((float)c.head_dim);
     a.qkvb = m->hand;
     a.partb = a.qkvb + qkv;
-    a.h2b = a.partb + part;
+    a.attnb = a.partb + part;
+    a.h2b = a.attnb + attn;
     a.actb = a.h2b + h2;
     a.hb = a.actb + act;
     a.argb = a.hb + h;
+    a.cntb = (unsigned*)(a.argb + 2 * (size_t)P);
     a.abort_flag = m->d_abort;
     a.xs_floats = (int)persist_xs_floats(sh);
     a.region_a = (int)persist_region_a(sh);
@@ -652,8 +655,14 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     unsigned aborted = 0;
     if (use_persist) LQ8_HIP(hipMemcpyAsync(&aborted, m->d_abort, sizeof(unsigned), hipMemcpyDeviceToHost, s));
     LQ8_HIP(hipStreamSynchronize(s));
-    if (aborted)
+    if (aborted) {
+        // the arrival counters and tags an aborted launch leaves are not
+        // trusted: the next launch starts from zeroed words
+        LQ8_HIP(hipMemsetAsync(m->hand, 0, m->hand_words * sizeof(uint64_t), s));
+        LQ8_HIP(hipStreamSynchronize(s));
+        m->tag = 1;
         return fail(LQ8_ERR_DEVICE, "persistent decode: a workgroup hand-off did not arrive in time (aborted)");
+    }
     m->kv_len = n_prompt + max_new - 1;
     if (stats) {
         float a = 0, b = 0;

@@ -179,6 +179,7 @@ _SIGS = [
     ("lq8_linear_forward_device_noalloc", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("lq8_bench_grid_sync", C.c_int,
      [C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
+    ("lq8_persist_trace", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     ("lq8_model_free", C.c_int, [C.c_void_p]),
     ("lq8_moe_tensor_count", C.c_size_t, [C.POINTER(MoeConfigC)]),
     ("lq8_moe_tensor_bytes", C.c_int, [C.POINTER(MoeConfigC), C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -805,6 +806,20 @@ def bench_grid_sync(ctx: "Context", kind: int, nwg: int, rounds: int):
     us, bad, gave = C.c_float(0), C.c_uint32(0), C.c_uint32(0)
     _check(lib().lq8_bench_grid_sync(ctx.handle, kind, nwg, rounds, C.byref(us), C.byref(bad), C.byref(gave)))
     return float(us.value), int(bad.value), int(gave.value)
+
+
+PTRACE_WG, PTRACE_LAYERS, PTRACE_POINTS = 512, 64, 16
+PTRACE_MARKS = ("P1_START", "P1_NORMED", "P2_START", "P2_QKV_IN", "P2_SCORES", "P2_PARTIALS", "P3_START",
+                "P3_STAGED", "P4_START", "P4_STAGED", "P5_START", "P5_STAGED", "P5_DONE", "P6_START", "P6_NORMED",
+                "P6_DONE")
+
+
+def persist_trace(ctx: "Context") -> np.ndarray:
+    """The persistent decode's phase marks (lq8_persist_trace) as uint64
+    [PTRACE_WG][PTRACE_LAYERS][PTRACE_POINTS], 100 MHz ticks (0: not passed)."""
+    out = np.zeros(PTRACE_WG * PTRACE_LAYERS * PTRACE_POINTS, dtype=np.uint64)
+    _check(lib().lq8_persist_trace(ctx.handle, _ptr(out), out.size))
+    return out.reshape(PTRACE_WG, PTRACE_LAYERS, PTRACE_POINTS)
 
 
 def gemv_grouped_device(ctx: Context, problems) -> None:
