@@ -14,8 +14,12 @@ launch per GEMV replayed from a HIP graph, the lm_head alone, the single
 3072x1024 GEMV, the M = 512 W8A8 MFMA GEMM, and batch-1 decode of the
 random-init Q8_0 Qwen3-0.6B (128-token prompt, 128 new tokens; greedy, and
 sampled with temperature 0.8, top-k 50, top-p 0.95, repetition penalty 1.1)
-are reported beside it.  The CPU oracle's GEMV, single-threaded over a
-bounded sample of the same workload, is the CPU baseline.
+are reported beside it, and so are the host-pointer Linear::forward per call
+at the seven layer shapes and the opt-in persistent decode kernel.  The CPU
+baseline is a C restatement of the reference's own CPU Linear::forward (BF16
+weight, per-call transpose, BF16 -> F32 copy, naive matmul_2d) timed on one
+pinned host core over a bounded sample of the same workload; the CPU oracle's
+Q8_0 GEMV is reported beside it.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -77,6 +81,54 @@ def measured_traffic():
         return None
 
 
+def pinned_core():
+    """One core this process may use (the lowest), for single-core baselines."""
+    return min(os.sched_getaffinity(0))
+
+
+def cpu_reference_linear(seconds_target=12.0):
+    """The reference's CPU Linear::forward restated (oracle/ref_linear_bf16.c:
+    BF16 weight, per-call transpose, BF16 -> F32, naive matmul_2d, one
+    thread) over one decode layer's 7 linears at batch 1, pinned to one core,
+    repeated for ~seconds_target.  value: the workload's algorithmic (Q8_0)
+    bytes per second, so that it divides the GPU value directly."""
+    import oracle
+
+    rng = np.random.default_rng(5)
+    mats = []
+    for _, n, k in LAYER_SHAPES:
+        w = (rng.standard_normal((n, k)).astype(np.float32) * 0.02).view(np.uint32)
+        mats.append(((w >> 16).astype(np.uint16), rng.standard_normal((1, k)).astype(np.float32)))
+    layer_bytes = sum(gemv_bytes(n, k) for _, n, k in LAYER_SHAPES)
+    bf16_bytes = sum(2 * n * k for _, n, k in LAYER_SHAPES)
+    aff = os.sched_getaffinity(0)
+    core = pinned_core()
+    os.sched_setaffinity(0, {core})
+    try:
+        oracle.ref_linear_forward_bf16(*mats[0])  # first touch
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            for w, x in mats:
+                oracle.ref_linear_forward_bf16(w, x)
+            passes += 1
+            el = time.perf_counter() - t0
+            if el >= seconds_target:
+                break
+    finally:
+        os.sched_setaffinity(0, aff)
+    layer_s = el / passes
+    # a token: 28 such layers plus the 151936 x 1024 lm_head (its share scaled by weight count)
+    lm_frac = LM_HEAD[1] * LM_HEAD[2] / sum(n * k for _, n, k in LAYER_SHAPES)
+    token_s = layer_s * (LAYERS + lm_frac)
+    return {"value": round(passes * layer_bytes / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"restatement of the reference's CPU Linear::forward (src/attention.rs:101-136, "
+                      f"src/tensor.rs:439-467, 957-958, 2716-2753) on BF16 weights: {passes} passes over one "
+                      f"Qwen3-0.6B decode layer's 7 linears at batch 1, {el:.1f} s on core {core} "
+                      f"(value counts the workload's Q8_0 bytes, {layer_bytes} per pass)",
+            "bf16_weight_gbs": round(passes * bf16_bytes / el / 1e9, 4),
+            "layer_ms": round(layer_s * 1e3, 1), "token_s_extrapolated": round(token_s, 2)}
+
+
 def cpu_baseline(seconds_target=12.0):
     """Oracle Q8_0 GEMV (1 thread) over one decode layer's 7 linears, repeated
     for ~seconds_target; reported as GB/s of algorithmic bytes."""
@@ -89,18 +141,24 @@ def cpu_baseline(seconds_target=12.0):
         blocks = oracle.quantize_q8_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
         mats.append((blocks, n, k, rng.standard_normal(k).astype(np.float32)))
     layer_bytes = sum(gemv_bytes(n, k) for _, n, k, _ in mats)
-    passes, t0 = 0, time.perf_counter()
-    while True:
-        for blocks, n, k, x in mats:
-            oracle.gemv_q8_0(blocks, n, k, x)
-        passes += 1
-        el = time.perf_counter() - t0
-        if el >= seconds_target:
-            break
-    oracle.set_threads(0)
+    aff = os.sched_getaffinity(0)
+    core = pinned_core()
+    os.sched_setaffinity(0, {core})
+    try:
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            for blocks, n, k, x in mats:
+                oracle.gemv_q8_0(blocks, n, k, x)
+            passes += 1
+            el = time.perf_counter() - t0
+            if el >= seconds_target:
+                break
+    finally:
+        os.sched_setaffinity(0, aff)
+        oracle.set_threads(0)
     return {"value": round(passes * layer_bytes / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{passes} passes over one Qwen3-0.6B decode layer's 7 Q8_0 GEMVs "
-                      f"({layer_bytes} B each), {el:.1f} s on one host core"}
+            "sample": f"the oracle's Q8_0 GEMV: {passes} passes over one Qwen3-0.6B decode layer's 7 Q8_0 GEMVs "
+                      f"({layer_bytes} B each), {el:.1f} s on core {core}"}
 
 
 def host_cpu():
@@ -182,6 +240,28 @@ def rotating_gemv_us(ctx, n, k, copies):
     x.free()
     y.free()
     return us
+
+
+def linear_forward_host(ctx, calls=200):
+    """Host-pointer Linear::forward (lq8_linear_forward: host x in, host y
+    out, through the context's pinned staging) per call at batch 1, at the
+    seven decoder-layer shapes: median wall time of `calls` calls each."""
+    out = {}
+    for name, n, k in LAYER_SHAPES:
+        w = lq8.Q8Weight.random(ctx, n, k, seed=21, stream=n + k)
+        lin = lq8.Linear.new(w)
+        x = np.random.default_rng(n).standard_normal((1, k)).astype(np.float32)
+        for _ in range(10):
+            lin.forward(x)
+        ts = []
+        for _ in range(calls):
+            t0 = time.perf_counter()
+            lin.forward(x)
+            ts.append(time.perf_counter() - t0)
+        out[f"{name}_{n}x{k}_us"] = round(float(np.median(ts)) * 1e6, 1)
+        w.free()
+    out["layer_us"] = round(sum(v for v in out.values()), 1)
+    return out
 
 
 def moe_stack(ctx, layers=48, reps=10):
@@ -317,17 +397,18 @@ def main():
         ms_chain = lq8.bench_gemv(ctx, probs, mode=2, reps=max(5, args.steps // 5)) / max(5, args.steps // 5)
         log(f"one launch per GEMV (graph): {ms_chain * 1e3:.1f} us/step, "
             f"{step_bytes / (ms_chain * 1e-3) / 1e9:.1f} GB/s")
-        # lm_head alone (165 MB: the largest single GEMV)
-        lm = [probs[-1]]
-        lq8.bench_gemv(ctx, lm, mode=0, reps=3)
-        ms_lm = lq8.bench_gemv(ctx, lm, mode=0, reps=20) / 20
-        log(f"lm_head: {ms_lm * 1e3:.1f} us, {gemv_bytes(*LM_HEAD[1:]) / (ms_lm * 1e-3) / 1e9:.1f} GB/s")
     chain_gbs = step_bytes / (ms_chain * 1e-3) / 1e9
-    lm_gbs = gemv_bytes(*LM_HEAD[1:]) / (ms_lm * 1e-3) / 1e9
     for w, _, _ in probs:
         w.free()
     for b in bufs:
         b.free()
+    if not args.only_step:
+        # lm_head alone (165 MB, the largest single GEMV), cold: graph-replayed
+        # over 4 distinct copies (661 MB, beyond the 256 MB Infinity Cache)
+        ms_lm = rotating_gemv_us(ctx, LM_HEAD[1], LM_HEAD[2], 4) * 1e-3
+        log(f"lm_head (cold, 4 rotating copies): {ms_lm * 1e3:.1f} us, "
+            f"{gemv_bytes(*LM_HEAD[1:]) / (ms_lm * 1e-3) / 1e9:.1f} GB/s")
+    lm_gbs = gemv_bytes(*LM_HEAD[1:]) / (ms_lm * 1e-3) / 1e9
 
     # known-size copy: calibrates FETCH_SIZE / WRITE_SIZE when profiled
     # (also the measured stream-copy peak: read + write bytes per second)
@@ -346,11 +427,14 @@ def main():
     src.free()
     dst.free()
 
-    # the single 3072 x 1024 GEMV (cold: 64 rotating copies)
+    # the single 3072 x 1024 GEMV (cold: 160 rotating copies, 535 MB)
     c1_us = float("nan")
+    linear_host = None
     if not args.only_step:
-        c1_us = rotating_gemv_us(ctx, 3072, 1024, 64)
+        c1_us = rotating_gemv_us(ctx, 3072, 1024, 160)
         log(f"GEMV 3072x1024: {c1_us:.2f} us, {gemv_bytes(3072, 1024) / c1_us / 1e3:.1f} GB/s")
+        linear_host = linear_forward_host(ctx)
+        log(f"host-pointer Linear::forward per call: {linear_host}")
 
     # prefill-shaped W8A8 GEMM, M = 512 (activation quantize + int8 MFMA)
     gemm = {}
@@ -390,6 +474,14 @@ def main():
         model.generate(prompt, gc, seed=1)
         sruns = [model.generate(prompt, gc, seed=1 + i)[1] for i in range(3)]
         stps = sorted(r["decode_tokens_per_s"] for r in sruns)[1]
+        # the opt-in persistent kernel (one cooperative launch for all steps)
+        os.environ["LQ8_PERSIST"] = "1"
+        try:
+            model.generate_greedy(prompt, 8)
+            pruns = [model.generate_greedy(prompt, 128)[1] for _ in range(3)]
+        finally:
+            del os.environ["LQ8_PERSIST"]
+        ptps = sorted(r["decode_tokens_per_s"] for r in pruns)[1] if all(r["used_persistent"] for r in pruns) else None
         # every Q8_0 matrix of the model is read once per token (the tied
         # embedding as the lm_head); the step is a chain of dependent kernels
         wbytes = LAYERS * sum(n * k * 34 // 32 for _, n, k in LAYER_SHAPES) + LM_HEAD[1] * LM_HEAD[2] * 34 // 32
@@ -403,9 +495,11 @@ def main():
                   "graph": runs[0]["used_graph"], "prompt": 128, "new_tokens": 128,
                   "sampled_tokens_per_s": round(stps, 1),
                   "sampled_config": {"temperature": 0.8, "top_k": 50, "top_p": 0.95, "repetition_penalty": 1.1},
-                  "sampler_us_over_greedy": round(1e6 / stps - 1e6 / tps, 1)}
+                  "sampler_us_over_greedy": round(1e6 / stps - 1e6 / tps, 1),
+                  "persistent_tokens_per_s": None if ptps is None else round(ptps, 1)}
         log(f"decode: {tps:.1f} tok/s (median of 3), prefill {runs[0]['prefill_ms']:.2f} ms; "
-            f"sampled {stps:.1f} tok/s ({1e6 / stps - 1e6 / tps:.1f} us/token over greedy)")
+            f"sampled {stps:.1f} tok/s ({1e6 / stps - 1e6 / tps:.1f} us/token over greedy); "
+            f"persistent kernel {ptps} tok/s")
         if not args.no_cpu:
             cpu_model = (cfg, model.export_all(), prompt)
         model.free()
@@ -413,9 +507,12 @@ def main():
     moe = None if args.no_moe else moe_stack(ctx)
     ctx.close()
 
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None if args.no_cpu else cpu_reference_linear()
     if cpu:
-        log(f"cpu baseline: {cpu['value']} GB/s ({cpu['sample']})")
+        log(f"cpu baseline: {cpu['value']} GB/s ({cpu['sample']}); {cpu['layer_ms']} ms per layer, "
+            f"~{cpu['token_s_extrapolated']} s per token")
+        cpu["q8_oracle"] = cpu_baseline(seconds_target=6.0)
+        log(f"cpu Q8_0 oracle: {cpu['q8_oracle']['value']} GB/s on one core")
         cpu["host"] = host_cpu()
         cpu["all_cores"] = cpu_gemv_all_cores()
         log(f"cpu all cores: {cpu['all_cores']['value']} GB/s on {cpu['all_cores']['cores']} threads")
@@ -448,9 +545,13 @@ def main():
                      "bytes_per_launch": step_bytes},
         "copy_peak_gbs": None if copy_gbs is None else round(copy_gbs, 1),
         "one_launch_per_gemv_gbs": None if args.only_step else round(chain_gbs, 1),
+        "one_launch_per_gemv_frac": None if args.only_step else round(chain_gbs / HBM_PEAK_GBS, 4),
         "one_launch_per_gemv_us_per_step": None if args.only_step else round(ms_chain * 1e3, 1),
-        "lm_head_gbs": None if args.only_step else round(lm_gbs, 1),
+        "lm_head_cold_gbs": None if args.only_step else round(lm_gbs, 1),
+        "lm_head_cold_us": None if args.only_step else round(ms_lm * 1e3, 2),
         "gemv_3072x1024_us": None if args.only_step else round(c1_us, 3),
+        "gemv_3072x1024_gbs": None if args.only_step else round(gemv_bytes(3072, 1024) / c1_us / 1e3, 1),
+        "linear_forward_host_us": linear_host,
         "gemm_m512": gemm,
         "decode": decode,
         "moe_qwen3_30b_a3b_48_layers": moe,

@@ -190,6 +190,34 @@ def linear_forward(blocks, n_out: int, k_in: int, x) -> np.ndarray:
     return y
 
 
+REF_LINEAR_PATH = os.path.join(_HERE, "_build", "libref_linear_bf16.so")
+_ref_lib = None
+
+
+def ref_linear_forward_bf16(w_bf16, x) -> np.ndarray:
+    """The reference's CPU Linear::forward on a BF16 weight (ref_linear_bf16.c):
+    w_bf16 uint16 [n_out, k_in] (BF16 bits), x f32 [m, k_in] -> y f32 [m, n_out]."""
+    global _ref_lib
+    if _ref_lib is None:
+        if not os.path.exists(REF_LINEAR_PATH):
+            raise RuntimeError(f"{REF_LINEAR_PATH} not built (make -C oracle)")
+        _ref_lib = C.CDLL(REF_LINEAR_PATH)
+        _ref_lib.ref_linear_forward_bf16.restype = C.c_int
+        _ref_lib.ref_linear_forward_bf16.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t,
+                                                     C.c_void_p]
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    xa = np.ascontiguousarray(x, dtype=np.float32)
+    if xa.ndim == 1:
+        xa = xa[None, :]
+    n, k = w.shape
+    if xa.shape[1] != k:
+        raise ValueError(f"x has {xa.shape[1]} columns, the weight {k}")
+    y = np.empty((xa.shape[0], n), dtype=np.float32)
+    if _ref_lib.ref_linear_forward_bf16(_p(w), n, k, _p(xa), xa.shape[0], _p(y)) != 0:
+        raise MemoryError("ref_linear_forward_bf16: allocation failed")
+    return y
+
+
 def rms_norm(x, weight, eps: float) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     w = np.ascontiguousarray(weight, dtype=np.float32)
