@@ -6,6 +6,8 @@
 // v_mfma_i32_32x32x32_i8; s_b = dw_b * dx_b (exact: two f16 values);
 // a_g = fmaf((float)I_b, s_b, a_g) over the blocks of a group of 8, from 0;
 // y = y + a_g over the groups, from 0.
+#include <algorithm>
+
 #include "lq8_internal.h"
 #include "lq8_numerics.h"
 
@@ -405,61 +407,84 @@ struct GemmArgs {
     int xq_bytes, xs_bytes, wc_bytes, ws_bytes;
 };
 
-// Buffer resources and per-lane byte offsets of one wave's operands.
+// Buffer resources and per-lane byte offsets of one wave's operands: TM
+// activation m-tiles and TN weight n-tiles of 32 rows each.
+template <int TM, int TN>
 struct GemmSrc {
     __amdgpu_buffer_rsrc_t ra, rb, rx, rw;
-    int oa, ob, ox, ow;
+    int oa[TM], ob[TN], ox[TM], ow[TN];
 };
 
-// Operands of 4 consecutive blocks b0 .. b0 + 3 (b0 % 4 == 0).  Codes and
-// weight scales of blocks past nb are read from block nb - 1 (in bounds);
-// their products are cancelled by zero scales in the compute step.
+// Operands of 4 consecutive blocks b0 .. b0 + 3 (b0 % 4 == 0) for a TM x TN
+// wave tile.  Codes and weight scales of blocks past nb are read from block
+// nb - 1 (in bounds); their products are cancelled by zero scales in the
+// compute step.
+template <int TM, int TN>
 struct Quad {
-    v4i dx;       // activation scales of the 4 blocks (lanes 32..63: 0)
-    v4i a[4], w[4];
-    uint32_t dw[4];
+    v4i dx[TM];   // activation scales of the 4 blocks (lanes 32..63: 0)
+    v4i a[TM][4], w[TN][4];
+    uint32_t dw[TN][4];
 };
 
-__device__ __forceinline__ void gemm_load(const GemmSrc& o, int b0, int nb, Quad& q) {
-    q.dx = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(o.rx, o.ox, (b0 >> 2) * 1024, 0));
+template <int TM, int TN>
+__device__ __forceinline__ void gemm_load(const GemmSrc<TM, TN>& o, int b0, int nb, Quad<TM, TN>& q) {
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+        q.dx[t] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(o.rx, o.ox[t], (b0 >> 2) * 1024, 0));
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int bc = min(b0 + i, nb - 1);
         const int cs = (bc >> 1) * 1024 + (bc & 1) * 512;
-        q.a[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(o.ra, o.oa, cs, 0));
-        q.w[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(o.rb, o.ob, cs, 0));
-        q.dw[i] = __builtin_amdgcn_raw_buffer_load_b16(o.rw, o.ow, bc * 32, 0);
+#pragma unroll
+        for (int t = 0; t < TM; t++)
+            q.a[t][i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(o.ra, o.oa[t], cs, 0));
+#pragma unroll
+        for (int t = 0; t < TN; t++) {
+            q.w[t][i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(o.rb, o.ob[t], cs, 0));
+            q.dw[t][i] = __builtin_amdgcn_raw_buffer_load_b16(o.rw, o.ow[t], bc * 32, 0);
+        }
     }
 }
 
-// acc[r] = fmaf((float)I_b[r], dw_b * dx_b[r], acc[r]) for the 4 blocks in
-// order.  The scale products come from one v_mfma_f32_32x32x8f16 per block:
-// A = (dx[row], 0, 0, 0) in lanes 0..31 and 0 in lanes 32..63, B = (dw[col],
-// 0, 0, 0) in lanes 0..31 of a real block and 0 elsewhere, so D[row][col] =
-// dx * dw exactly (a product of two f16 values fits f32) -- the same value
-// the VALU product gives -- and exactly 0 for a block past nb.
-__device__ __forceinline__ void gemm_quad(const Quad& q, int b0, int nb, bool lo, float* acc) {
+// acc[tile][r] = fmaf((float)I_b[r], dw_b * dx_b[r], acc[tile][r]) for the 4
+// blocks in order, for every (m, n) tile of the wave.  The scale products
+// come from one v_mfma_f32_32x32x8f16 per block and tile: A = (dx[row], 0, 0,
+// 0) in lanes 0..31 and 0 in lanes 32..63, B = (dw[col], 0, 0, 0) in lanes
+// 0..31 of a real block and 0 elsewhere, so D[row][col] = dx * dw exactly (a
+// product of two f16 values fits f32) -- the same value the VALU product
+// gives -- and exactly 0 for a block past nb.
+template <int TM, int TN>
+__device__ __forceinline__ void gemm_quad(const Quad<TM, TN>& q, int b0, int nb, bool lo, float (*acc)[16]) {
     const v16i zi = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.a[i], q.w[i], zi, 0, 0, 0);
-        const uint2 au = {(uint32_t)q.dx[i], 0u};
-        const uint2 bu = {(lo && b0 + i < nb) ? q.dw[i] : 0u, 0u};
-        const v16f P = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, au), __builtin_bit_cast(v4h, bu),
-                                                            zf, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 16; r++) acc[r] = fmaf((float)I[r], P[r], acc[r]);
+        for (int tm = 0; tm < TM; tm++) {
+#pragma unroll
+            for (int tn = 0; tn < TN; tn++) {
+                const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(q.a[tm][i], q.w[tn][i], zi, 0, 0, 0);
+                const uint2 au = {(uint32_t)q.dx[tm][i], 0u};
+                const uint2 bu = {(lo && b0 + i < nb) ? q.dw[tn][i] : 0u, 0u};
+                const v16f P = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, au),
+                                                                    __builtin_bit_cast(v4h, bu), zf, 0, 0, 0);
+                float* a = acc[tm * TN + tn];
+#pragma unroll
+                for (int r = 0; r < 16; r++) a[r] = fmaf((float)I[r], P[r], a[r]);
+            }
+        }
     }
 }
 
 // One round: the wave's group g (8 blocks in two quads q0, q1), with the
 // loads of the next round's group gn issued behind each quad's compute.
-template <bool NEXT>
-__device__ __forceinline__ void gemm_group(const GemmSrc& o, int g, int gn, int nb, bool lo, Quad& q0, Quad& q1,
-                                           float* acc) {
+template <bool NEXT, int TM, int TN>
+__device__ __forceinline__ void gemm_group(const GemmSrc<TM, TN>& o, int g, int gn, int nb, bool lo,
+                                           Quad<TM, TN>& q0, Quad<TM, TN>& q1, float (*acc)[16]) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    for (int t = 0; t < TM * TN; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
     gemm_quad(q0, g * GEMM_GROUP, nb, lo, acc);
     if (NEXT) gemm_load(o, gn * GEMM_GROUP, nb, q0);
     gemm_quad(q1, g * GEMM_GROUP + 4, nb, lo, acc);
@@ -467,72 +492,107 @@ __device__ __forceinline__ void gemm_group(const GemmSrc& o, int g, int gn, int 
 }
 
 // Round combine: wave 0 adds its own group, then the other waves' groups
-// from LDS, in group order (y = y + a_g).  part is double-buffered by round
-// parity, so one barrier per round suffices.
-template <int S>
-__device__ __forceinline__ void gemm_combine(float4 (*part)[S > 1 ? S - 1 : 1][4][64], int j, int s, int lane,
-                                             int G, const float* acc, float* y) {
+// from LDS, in group order (y = y + a_g).  Two barriers: the partials are
+// written, read, and free again before the next round writes them.
+template <int S, int T, bool ONE>
+__device__ __forceinline__ void gemm_combine(float4* part, int j, int s, int lane, int G, float (*acc)[16],
+                                             float (*y)[16]) {
     if (S == 1) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) y[r] = y[r] + acc[r];
+        for (int t = 0; t < T; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) y[t][r] = (ONE ? 0.0f : y[t][r]) + acc[t][r];
         return;
     }
     if (s > 0 && j * S + s < G) {
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            part[j & 1][s - 1][q][lane] = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+        for (int t = 0; t < T; t++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                part[(((s - 1) * T + t) * 4 + q) * 64 + lane] =
+                    make_float4(acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]);
     }
     __syncthreads();
     if (s == 0) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) y[r] = y[r] + acc[r];
-        for (int t = 1; t < S && j * S + t < G; t++) {
+        for (int t = 0; t < T; t++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 v = part[j & 1][t - 1][q][lane];
-                y[4 * q] = y[4 * q] + v.x;
-                y[4 * q + 1] = y[4 * q + 1] + v.y;
-                y[4 * q + 2] = y[4 * q + 2] + v.z;
-                y[4 * q + 3] = y[4 * q + 3] + v.w;
-            }
+            for (int r = 0; r < 16; r++) y[t][r] = (ONE ? 0.0f : y[t][r]) + acc[t][r];
+        for (int u = 1; u < S && j * S + u < G; u++) {
+#pragma unroll
+            for (int t = 0; t < T; t++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 v = part[(((u - 1) * T + t) * 4 + q) * 64 + lane];
+                    y[t][4 * q] = y[t][4 * q] + v.x;
+                    y[t][4 * q + 1] = y[t][4 * q + 1] + v.y;
+                    y[t][4 * q + 2] = y[t][4 * q + 2] + v.z;
+                    y[t][4 * q + 3] = y[t][4 * q + 3] + v.w;
+                }
         }
     }
+    __syncthreads();
 }
 
-// One 32 (m) x 32 (n) output tile per workgroup of S waves; wave s takes the
-// groups g = s, s + S, s + 2S, ... (one per round).  Tiles are numbered so
+// One (32 TM) x (32 TN) output block per workgroup of S waves, as TM x TN
+// MFMA tiles of 32 x 32 that share each fetched operand fragment (a weight
+// fragment serves TM tiles, an activation fragment TN); wave s takes the
+// groups g = s, s + S, s + 2S, ... (one per round).  Blocks are numbered so
 // that the workgroups one XCD receives (workgroup ids congruent mod 8) cover
-// a contiguous run of n-tiles over all m-tiles: each XCD's L2 holds its own
+// a contiguous run of n-blocks over all m-blocks: each XCD's L2 holds its own
 // slice of the weight.  Operand lane l: row l % 32 of the 32-row tile, codes
 // of half l / 32 of the block (A and B split the block's 32 k-values alike,
 // so the int32 dot is exact).  Accumulator layout: lane l holds column
-// l % 32, register i holds row 8 * (i / 4) + 4 * (l / 32) + i % 4.
-template <int S>
-__global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(S == 1 ? 2 : 3))) void k_gemm(GemmArgs g) {
-    __shared__ float4 part[2][S > 1 ? S - 1 : 1][4][64];
+// l % 32, register i holds row 8 * (i / 4) + 4 * (l / 32) + i % 4.  Tiles
+// past the matrix (a last block of one 32-row tile) read the last tile again
+// and are not stored.
+// ONE: every wave has exactly one group (S = number of groups): no running
+// sum across rounds, wave 0 sums into its own accumulators (y = 0 + a_0,
+// then + a_1, ...).
+template <int S, int TM, int TN, bool ONE>
+__global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm(GemmArgs g) {
+    extern __shared__ float4 part[];  // [S - 1][TM * TN][4][64]
+    constexpr int T = TM * TN;
     const int lane = threadIdx.x & 63;
     const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ntm = g.ntm, ntn = (g.n + 31) / 32;
+    const int nbm = (ntm + TM - 1) / TM;  // m-blocks of TM tiles
     const int wgi = blockIdx.x, per = g.ntiles >> 3, rem = g.ntiles & 7, xcd = wgi & 7, j8 = wgi >> 3;
     const int tl = xcd < rem ? xcd * (per + 1) + j8 : rem * (per + 1) + (xcd - rem) * per + j8;
-    const int nt = tl / g.ntm, mt = tl - nt * g.ntm;
+    const int bn = tl / nbm, bm = tl - bn * nbm;
     const int half = lane >> 5, r32 = lane & 31;
     const bool lo = lane < 32;
     const int nb = g.nb, G = g.groups;
-    GemmSrc o;
+    GemmSrc<TM, TN> o;
     o.ra = __builtin_amdgcn_make_buffer_rsrc((void*)g.xq, (short)0, g.xq_bytes, RSRC_CFG);
     o.rb = __builtin_amdgcn_make_buffer_rsrc((void*)g.wc, (short)0, g.wc_bytes, RSRC_CFG);
     o.rx = __builtin_amdgcn_make_buffer_rsrc((void*)g.xs, (short)0, g.xs_bytes, RSRC_CFG);
     o.rw = __builtin_amdgcn_make_buffer_rsrc((void*)g.ws, (short)0, g.ws_bytes, RSRC_CFG);
-    o.oa = ((mt * 2 + (r32 >> 4)) * g.np * 64 + half * 16 + (r32 & 15)) * 16;
-    o.ob = ((nt * 2 + (r32 >> 4)) * g.np * 64 + half * 16 + (r32 & 15)) * 16;
-    o.ox = (mt * 2 * G * 64 + lane) * 16;
-    o.ow = ((nt * 2 + (r32 >> 4)) * 2 * g.np * 16 + (r32 & 15)) * 2;
-
-    float y[16], acc[16];
+    int mts[TM], nts[TN];
 #pragma unroll
-    for (int r = 0; r < 16; r++) y[r] = 0.0f;
-    Quad q0, q1;
-    const int R = (G + S - 1) / S;
+    for (int t = 0; t < TM; t++) {
+        mts[t] = min(bm * TM + t, ntm - 1);
+        o.oa[t] = ((mts[t] * 2 + (r32 >> 4)) * g.np * 64 + half * 16 + (r32 & 15)) * 16;
+        o.ox[t] = (mts[t] * 2 * G * 64 + lane) * 16;
+    }
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+        nts[t] = min(bn * TN + t, ntn - 1);
+        o.ob[t] = ((nts[t] * 2 + (r32 >> 4)) * g.np * 64 + half * 16 + (r32 & 15)) * 16;
+        o.ow[t] = ((nts[t] * 2 + (r32 >> 4)) * 2 * g.np * 16 + (r32 & 15)) * 2;
+    }
+
+    float acc[T][16];
+    float y[ONE ? 1 : T][16];  // the running sum over rounds (ONE: acc itself)
+    float (*yy)[16] = ONE ? acc : y;
+    if (!ONE) {
+#pragma unroll
+        for (int t = 0; t < T; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) yy[t][r] = 0.0f;
+    }
+    Quad<TM, TN> q0, q1;
+    const int R = ONE ? 1 : (G + S - 1) / S;
     {
         const int g0 = min(s, G - 1);
         gemm_load(o, g0 * GEMM_GROUP, nb, q0);
@@ -540,22 +600,29 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(S == 1 ?
     }
     for (int j = 0; j + 1 < R; j++) {
         gemm_group<true>(o, j * S + s, min((j + 1) * S + s, G - 1), nb, lo, q0, q1, acc);
-        gemm_combine<S>(part, j, s, lane, G, acc, y);
+        gemm_combine<S, T, false>(part, j, s, lane, G, acc, yy);
     }
     if (s == 0 || (R - 1) * S + s < G) gemm_group<false>(o, (R - 1) * S + s, 0, nb, lo, q0, q1, acc);
-    gemm_combine<S>(part, R - 1, s, lane, G, acc, y);
+    gemm_combine<S, T, ONE>(part, R - 1, s, lane, G, acc, yy);
 
     if (s != 0) return;
-    const int col = nt * 32 + r32;
-    if (col >= g.n) return;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int row = mt * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
-        if (row < g.m) {
-            const size_t off = (size_t)row * g.n + col;
-            float v = y[i];
-            if (g.resid) v = g.resid[off] + v;
-            g.y[off] = v;
+    for (int tn = 0; tn < TN; tn++) {
+        const int col = nts[tn] * 32 + r32;
+        if (bn * TN + tn >= ntn || col >= g.n) continue;
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++) {
+            if (bm * TM + tm >= ntm) continue;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int row = mts[tm] * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
+                if (row < g.m) {
+                    const size_t off = (size_t)row * g.n + col;
+                    float v = yy[tm * TN + tn][i];
+                    if (g.resid) v = g.resid[off] + v;
+                    g.y[off] = v;
+                }
+            }
         }
     }
 }
@@ -660,27 +727,46 @@ lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const uint32_t* xs, int 
     g.np = (int)w->np;
     g.groups = (g.nb + GEMM_GROUP - 1) / GEMM_GROUP;
     g.ntm = (m + 31) / 32;
-    const int ntn = (g.n + 31) / 32;
-    if ((size_t)g.ntm * ntn > lim) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemm: too many tiles");
-    g.ntiles = g.ntm * ntn;
     g.xq_bytes = (int)xq_bytes;
     g.xs_bytes = (int)xs_bytes;
     g.wc_bytes = (int)wc_bytes;
     g.ws_bytes = (int)ws_bytes;
-    // K-split: the fewest waves per tile (at least 2 when K spans more than one
-    // group: the single-wave variant runs short of registers in its round loop)
-    // that give >= 2 waves per SIMD (1024 SIMDs).
-    int S = g.groups > 1 ? 2 : 1;
-    while (S < 8 && S < g.groups && (size_t)g.ntiles * S < 2048) S = S == 4 ? 6 : S == 6 ? 8 : S + 1;
-    const dim3 grid((unsigned)g.ntiles);
-    switch (S) {
-        case 1: hipLaunchKernelGGL(k_gemm<1>, grid, dim3(64), 0, s, g); break;
-        case 2: hipLaunchKernelGGL(k_gemm<2>, grid, dim3(128), 0, s, g); break;
-        case 3: hipLaunchKernelGGL(k_gemm<3>, grid, dim3(192), 0, s, g); break;
-        case 4: hipLaunchKernelGGL(k_gemm<4>, grid, dim3(256), 0, s, g); break;
-        case 6: hipLaunchKernelGGL(k_gemm<6>, grid, dim3(384), 0, s, g); break;
-        default: hipLaunchKernelGGL(k_gemm<8>, grid, dim3(512), 0, s, g); break;
+    // One 32 x 32 tile per workgroup, K split over S waves (one group per wave
+    // per round).  Register-blocked 2 x 1 and 2 x 2 tiles per wave (the
+    // template's TM, TN) measured slower at M = 512 and 2048: a wave's time
+    // goes to issuing its operand loads, and larger tiles give fewer waves.
+    // S: every group its own wave (one round, no running sum) when the groups
+    // are few (<= 4) or the waves that gives stay <= 8192; otherwise the
+    // fewest of 2, 3, 4, 6, 8, 12, 16 that give >= 2048 waves.
+    const int ntn = (g.n + 31) / 32;
+    const size_t tiles = (size_t)g.ntm * ntn;
+    if (tiles > lim) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemm: too many tiles");
+    g.ntiles = (int)tiles;
+    int S;
+    if (g.groups <= 16 && (g.groups <= 4 || tiles * g.groups <= 8192)) {
+        S = g.groups;
+    } else {
+        static const int kS[] = {2, 3, 4, 6, 8, 12, 16};
+        S = 16;
+        for (int c : kS)
+            if (tiles * c >= 2048) { S = c; break; }
+        S = std::min(S, g.groups);
     }
+    const bool one = S == g.groups;
+    const size_t smem = S > 1 ? (size_t)(S - 1) * 4 * 64 * sizeof(float4) : 0;
+    const dim3 grid((unsigned)g.ntiles);
+#define LQ8_GEMM_CASE(SS)                                                                          \
+    case SS:                                                                                       \
+        if (one) hipLaunchKernelGGL((k_gemm<SS, 1, 1, true>), grid, dim3(64 * SS), smem, s, g);     \
+        else hipLaunchKernelGGL((k_gemm<SS, 1, 1, false>), grid, dim3(64 * SS), smem, s, g);        \
+        break;
+    switch (S) {
+        LQ8_GEMM_CASE(1) LQ8_GEMM_CASE(2) LQ8_GEMM_CASE(3) LQ8_GEMM_CASE(4) LQ8_GEMM_CASE(5) LQ8_GEMM_CASE(6)
+        LQ8_GEMM_CASE(7) LQ8_GEMM_CASE(8) LQ8_GEMM_CASE(9) LQ8_GEMM_CASE(10) LQ8_GEMM_CASE(11) LQ8_GEMM_CASE(12)
+        LQ8_GEMM_CASE(13) LQ8_GEMM_CASE(14) LQ8_GEMM_CASE(15) LQ8_GEMM_CASE(16)
+        default: return fail(LQ8_ERR_DEVICE, "gemm: no kernel for this split");
+    }
+#undef LQ8_GEMM_CASE
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
