@@ -773,6 +773,12 @@ int orc_moe_route(const float* scores, size_t T, size_t E, size_t k, uint32_t* i
     return 0;
 }
 
+/* One decode step of T sequences (sequence t in KV slot t at pos[t]).  The
+ * attention projections of all T tokens are one Linear::forward each
+ * (orc_linear_forward: the GEMV at T = 1, the W8A8 GEMM at T > 1, as the
+ * reference's Linear::forward over an [T, hidden] input), so a token's
+ * result depends on whether it runs alone or in a batch, never on the other
+ * tokens of the batch; the experts run per token (single-vector GEMVs). */
 int orc_moe_forward(orc_moe* m, float* hidden, const float* scores, const uint32_t* pos, size_t T) {
     const orc_moe_config* c = &m->c;
     size_t H = c->hidden_size, hd = c->head_dim, NH = c->num_heads, NKV = c->num_kv_heads;
@@ -780,12 +786,12 @@ int orc_moe_forward(orc_moe* m, float* hidden, const float* scores, const uint32
     size_t QD = NH * hd, KD = NKV * hd, R = hd / 2, groups = NH / NKV;
     if (T == 0 || T > c->max_batch) return 1;
     for (size_t t = 0; t < T; t++) if (pos[t] >= P) return 3;
-    float* X = (float*)malloc(H * sizeof(float));
-    float* Q = (float*)malloc(QD * sizeof(float));
-    float* Kx = (float*)malloc(KD * sizeof(float));
-    float* Vx = (float*)malloc(KD * sizeof(float));
-    float* A = (float*)malloc(QD * sizeof(float));
-    float* O = (float*)malloc(H * sizeof(float));
+    float* X = (float*)malloc(T * H * sizeof(float));
+    float* Q = (float*)malloc(T * QD * sizeof(float));
+    float* Kx = (float*)malloc(T * KD * sizeof(float));
+    float* Vx = (float*)malloc(T * KD * sizeof(float));
+    float* A = (float*)malloc(T * QD * sizeof(float));
+    float* O = (float*)malloc(T * H * sizeof(float));
     float* G = (float*)malloc(I * sizeof(float));
     float* U = (float*)malloc(I * sizeof(float));
     float* Y = (float*)malloc(H * sizeof(float));
@@ -801,20 +807,21 @@ int orc_moe_forward(orc_moe* m, float* hidden, const float* scores, const uint32
         const float *in_norm = (const float*)b[0], *post_norm = (const float*)b[1];
         const float *q_norm = (const float*)b[2], *k_norm = (const float*)b[3];
         orc_moe_route(scores + l * T * E, T, E, K, ids, wts);
+        orc_rms_norm(hidden, in_norm, T, H, c->rms_norm_eps, X);
+        if ((rc = orc_linear_forward((const uint8_t*)b[4], QD, H, X, T, Q)) ||
+            (rc = orc_linear_forward((const uint8_t*)b[5], KD, H, X, T, Kx)) ||
+            (rc = orc_linear_forward((const uint8_t*)b[6], KD, H, X, T, Vx)))
+            goto done;
         for (size_t t = 0; t < T; t++) {
-            float* h = hidden + t * H;
             size_t p = pos[t];
             float* kc = m->kc + ((l * c->max_batch + t) * NKV) * P * hd;
             float* vc = m->vc + ((l * c->max_batch + t) * NKV) * P * hd;
-            orc_rms_norm(h, in_norm, 1, H, c->rms_norm_eps, X);
-            orc_gemv_q8_0((const uint8_t*)b[4], QD, H, X, Q);
-            orc_gemv_q8_0((const uint8_t*)b[5], KD, H, X, Kx);
-            orc_gemv_q8_0((const uint8_t*)b[6], KD, H, X, Vx);
+            float *Qt = Q + t * QD, *Kt = Kx + t * KD, *Vt = Vx + t * KD;
             const float* cs = m->cos_t + p * R;
             const float* sn = m->sin_t + p * R;
             for (size_t hh = 0; hh < NH + NKV; hh++) {
                 int isq = hh < NH;
-                float* src = isq ? Q + hh * hd : Kx + (hh - NH) * hd;
+                float* src = isq ? Qt + hh * hd : Kt + (hh - NH) * hd;
                 rms_norm_row(src, isq ? q_norm : k_norm, hd, c->rms_norm_eps, tmp, sc);
                 float* dst = isq ? src : kc + ((hh - NH) * P + p) * hd;
                 for (size_t d = 0; d < R; d++) {
@@ -824,13 +831,16 @@ int orc_moe_forward(orc_moe* m, float* hidden, const float* scores, const uint32
                     dst[d + R] = x2 * cv + x1 * sv;
                 }
             }
-            for (size_t hh = 0; hh < NKV; hh++) memcpy(vc + (hh * P + p) * hd, Vx + hh * hd, hd * sizeof(float));
+            for (size_t hh = 0; hh < NKV; hh++) memcpy(vc + (hh * P + p) * hd, Vt + hh * hd, hd * sizeof(float));
             for (size_t hh = 0; hh < NH; hh++) {
                 size_t kvh = hh / groups;
-                attend_kv(kc + kvh * P * hd, vc + kvh * P * hd, hd, Q + hh * hd, p + 1, A + hh * hd, sc);
+                attend_kv(kc + kvh * P * hd, vc + kvh * P * hd, hd, Qt + hh * hd, p + 1, A + t * QD + hh * hd, sc);
             }
-            orc_gemv_q8_0((const uint8_t*)b[7], H, QD, A, O);
-            for (size_t i = 0; i < H; i++) h[i] = h[i] + O[i];   /* h2 */
+        }
+        if ((rc = orc_linear_forward((const uint8_t*)b[7], H, QD, A, T, O))) goto done;
+        for (size_t i = 0; i < T * H; i++) hidden[i] = hidden[i] + O[i];   /* h2 */
+        for (size_t t = 0; t < T; t++) {
+            float* h = hidden + t * H;
             orc_rms_norm(h, post_norm, 1, H, c->rms_norm_eps, X);
             for (size_t i = 0; i < H; i++) acc[i] = 0.0f;
             for (size_t e = 0; e < E; e++) {

@@ -3,18 +3,23 @@
 // expert combine, and the layer runtime behind the lq8_moe_* C ABI.
 //
 // Per layer (T sequences, one token each):
-//   qkv   = [q|k|v](RmsNorm(h))               GEMV (T = 1) / multi-vector GEMV
+//   qkv   = [q|k|v](RmsNorm(h))               GEMV (T = 1) / W8A8 GEMM (T > 1)
 //   part  = attention segments per sequence    (q/k norm, RoPE, KV append)
 //   h2    = h + o(attention(part))             GEMV with the combine fused (T = 1),
-//                                              combine kernel + multi-vector GEMV (T > 1)
+//                                              combine kernel + W8A8 GEMM (T > 1)
 //   route = top_k of softmax(scores)           all layers in one launch before the first
 //                                              layer (scores are inputs); expert lists on the device
 //   act   = silu(gate_e x) * up_e x, x = RmsNorm(h2)   grouped multi-vector GEMV over the
 //                                              routed experts (gate and up tiles in one workgroup)
 //   eo    = down_e(act)                        grouped multi-vector GEMV
 //   h     = h2 + sum_e w_e * eo_e              ascending expert index
-// Every projection is the single-vector GEMV order per token, so each
-// token's result is independent of the batch it runs in.
+// The attention projections follow Linear::forward over the [T, hidden]
+// input (src/attention.rs:101-136): the W8A32 GEMV for one token, the W8A8
+// GEMM (activation rows quantized to Q8_0, per-row and per-element results)
+// for more, so a token's result depends on whether it runs alone or in a
+// batch, never on the other tokens of the batch.  The experts run the
+// single-vector GEMV order per token.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <vector>
@@ -49,6 +54,8 @@ struct lq8_moe {
     float *kc = nullptr, *vc = nullptr;  // [layer][seq][kv_head][max_pos][128]
     float *h2 = nullptr, *qkv = nullptr, *apart = nullptr, *aout = nullptr;
     float* xn = nullptr;  // [max_batch][hidden]: RmsNorm rows (batched decode)
+    int8_t* xq = nullptr;    // activation operand of the batched GEMMs (codes)
+    uint32_t* xs = nullptr;  // and its scales
     float *gu = nullptr;  // [max_batch * top_k][expert_intermediate]: silu(gate) * up per slot
     float *eo = nullptr;  // [max_batch * top_k][hidden]: expert outputs per slot
     uint32_t* rids = nullptr;  // [layer][max_batch][top_k]
@@ -298,7 +305,7 @@ void release(lq8_moe* m) {
         F(L.in_norm); F(L.post_norm); F(L.q_norm); F(L.k_norm);
     }
     F(m->cos_t); F(m->sin_t); F(m->kc); F(m->vc);
-    F(m->h2); F(m->xn); F(m->qkv); F(m->apart); F(m->aout); F(m->gu); F(m->eo);
+    F(m->h2); F(m->xn); F(m->xq); F(m->xs); F(m->qkv); F(m->apart); F(m->aout); F(m->gu); F(m->eo);
     F(m->rids); F(m->rw); F(m->n_act); F(m->act_e); F(m->vbeg); F(m->vcnt); F(m->slots);
     F(m->hid_tmp); F(m->scores_tmp); F(m->pos_tmp);
     delete m;
@@ -349,6 +356,9 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_moe_config* c, lq8_moe* m) {
         (st = dalloc(&m->act_e, NL * E)) || (st = dalloc(&m->vbeg, NL * E)) || (st = dalloc(&m->vcnt, NL * E)) ||
         (st = dalloc(&m->slots, NL * B * K)) || (st = dalloc(&m->hid_tmp, B * H)) ||
         (st = dalloc(&m->scores_tmp, NL * B * E)) || (st = dalloc(&m->pos_tmp, B)))
+        return st;
+    const int kmax = (int)std::max(H, m->QD);
+    if ((st = dalloc(&m->xq, act_code_bytes((int)B, kmax))) || (st = dalloc(&m->xs, act_scale_bytes((int)B, kmax) / 4)))
         return st;
     return LQ8_OK;
 }
@@ -404,7 +414,6 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
     const size_t seq_kv = (size_t)c.num_kv_heads * P * 128, layer_kv = (size_t)B * seq_kv;
     const size_t part_stride = (size_t)m->cmax * NH * ATT_PART_STRIDE;
     const float scale = 1.0f / std::sqrt((float)c.head_dim);
-    const int vsplit = (T + 3) / 4;
     const int max_probs = std::min(E, T * K);
     lq8_status st;
     // the router reads only the given scores: every layer's routing in one launch
@@ -419,18 +428,21 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
         int* vcnt = m->vcnt + l * E;
         int* slots = m->slots + l * (size_t)B * K;
         // input_layernorm + q|k|v.  T = 1: the norm is fused into the GEMV's
-        // input staging; T > 1: the rows are normed once (the same arithmetic)
-        // instead of once per output tile.
+        // input staging; T > 1: the norm is fused into the activation
+        // quantizer of the GEMM (the operand rms_norm_rows + quantize_act give)
         if (T == 1) {
             GemvArgs g{L.qkv->codes, L.qkv->scales, d_hidden, L.in_norm, m->qkv, nullptr, nullptr, nullptr,
                        (int)m->QKV, H, c.rms_norm_eps};
             if ((st = launch_gemv(s, XS_RMSNORM, EPI_STORE, g))) return st;
         } else {
-            if ((st = launch_rms_norm_rows(s, d_hidden, L.in_norm, T, H, c.rms_norm_eps, m->xn))) return st;
-            MvArgs a{};
-            a.codes = L.qkv->codes; a.scales = L.qkv->scales; a.rows = (int)m->QKV; a.k = H;
-            a.nvec = T; a.x = m->xn; a.x_stride = H; a.x_div = 1; a.y = m->qkv; a.y_stride = (int)m->QKV;
-            if ((st = launch_gemv_mv(s, XS_PLAIN, EPI_STORE, a, 1, vsplit))) return st;
+            if (rms_quantize_supported(H)) {
+                if ((st = launch_rms_quantize_act(s, d_hidden, L.in_norm, T, H, c.rms_norm_eps, m->xq, m->xs)))
+                    return st;
+            } else {
+                if ((st = launch_rms_norm_rows(s, d_hidden, L.in_norm, T, H, c.rms_norm_eps, m->xn))) return st;
+                if ((st = launch_quantize_act(s, m->xn, T, H, m->xq, m->xs))) return st;
+            }
+            if ((st = launch_gemm(s, m->xq, m->xs, T, L.qkv, m->qkv, nullptr))) return st;
         }
         // q/k norm, RoPE, KV append, attention per segment, per sequence
         AttnSegLaunch at{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->kc + l * layer_kv, m->vc + l * layer_kv,
@@ -450,11 +462,8 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
             if ((st = launch_gemv(s, XS_ATTN, EPI_RESID, g))) return st;
         } else {
             if ((st = launch_attention_combine(s, m->apart, part_stride, d_pos, T, NH, m->cmax, m->aout))) return st;
-            MvArgs a{};
-            a.codes = L.o->codes; a.scales = L.o->scales; a.rows = H; a.k = (int)m->QD;
-            a.nvec = T; a.x = m->aout; a.x_stride = (int)m->QD; a.x_div = 1; a.y = m->h2; a.y_stride = H;
-            a.resid = d_hidden; a.resid_stride = H;
-            if ((st = launch_gemv_mv(s, XS_PLAIN, EPI_RESID, a, 1, vsplit))) return st;
+            if ((st = launch_quantize_act(s, m->aout, T, (int)m->QD, m->xq, m->xs))) return st;
+            if ((st = launch_gemm(s, m->xq, m->xs, T, L.o, m->h2, d_hidden))) return st;
         }
         uint32_t* rids = m->rids + l * B * K;
         float* rw = m->rw + l * B * K;

@@ -222,10 +222,11 @@ class NumpyMoeStack:
     p = softmax(scores), the top_k experts by p (ties to the lower index),
     weights renormalised over them, expert down(silu(gate x) * up x), combined
     as h2 + sum of w_e y_e.  Every projection is applied to one token at a
-    time unless w8a8_batch is set, in which case the attention projections
-    of a batch of T > 1 tokens quantize their activation rows (W8A8)."""
+    time unless w8a8_batch is set (the library's rule, the default), in which
+    case the attention projections of a batch of T > 1 tokens quantize their
+    activation rows (W8A8)."""
 
-    def __init__(self, cfg, tensors, w8a8_batch=False):
+    def __init__(self, cfg, tensors, w8a8_batch=True):
         self.cfg = cfg
         self.w8a8_batch = w8a8_batch
         H, hd, E, I = cfg.hidden_size, cfg.head_dim, cfg.num_experts, cfg.expert_intermediate_size

@@ -9,7 +9,10 @@
   bit, position by position.
 - Combine: identical experts with top_k = num_experts give h2 + y (the
   renormalised weights sum to 1), up to rounding.
-- Batch: a batch of sequences equals the sequences run one by one.
+- Batch: the attention projections of a batch of T > 1 tokens are one
+  Linear::forward each (the W8A8 GEMM), so a token's bits do not depend on
+  the other tokens of its batch; with the activation quantization switched
+  off a batch equals its sequences run one by one.
 """
 from dataclasses import dataclass
 
@@ -136,19 +139,57 @@ def test_identical_experts_combine_to_one_expert():
     m4.close()
 
 
-@pytest.mark.parametrize("T", [3])
-def test_batch_equals_sequences_one_by_one(T):
+def moe_batch_case(T=3):
     cfg = MoeCfg(num_layers=2)
     tens = moe_tensors(cfg, 9)
     rng = np.random.default_rng(10)
     x = rng.standard_normal((T, cfg.hidden_size)).astype(np.float32)
     scores = rng.standard_normal((cfg.num_layers, T, cfg.num_experts)).astype(np.float32)
-    pos = [0, 7, 70]
+    return cfg, tens, x, scores, [0, 7, 70][:T]
+
+
+def test_batch_result_independent_of_the_other_tokens():
+    """Each token of a batch of 3 gets the same bits in a batch of 2 with a
+    different partner (per-row activation quantization, per-element GEMM)."""
+    cfg, tens, x, scores, pos = moe_batch_case()
     batch = oracle.MoeStack(cfg, tens)
     yb = batch.forward(x, scores, pos)
+    batch.close()
+    T = len(pos)
     for t in range(T):
+        u = (t + 1) % T
+        pair = oracle.MoeStack(cfg, tens)
+        yp = pair.forward(x[[t, u]], scores[:, [t, u]], [pos[t], pos[u]])
+        pair.close()
+        assert np.array_equal(yp[0].view(np.uint32), yb[t].view(np.uint32)), t
+
+
+def test_batch_equals_sequences_one_by_one_without_activation_quantization():
+    cfg, tens, x, scores, pos = moe_batch_case()
+    oracle.set_activation_quantization(False)
+    try:
+        batch = oracle.MoeStack(cfg, tens)
+        yb = batch.forward(x, scores, pos)
+        batch.close()
+        for t in range(len(pos)):
+            one = oracle.MoeStack(cfg, tens)
+            yt = one.forward(x[t:t + 1], scores[:, t:t + 1], [pos[t]])
+            one.close()
+            assert np.array_equal(yt[0].view(np.uint32), yb[t].view(np.uint32))
+    finally:
+        oracle.set_activation_quantization(True)
+
+
+def test_batch_differs_from_single_only_by_activation_quantization():
+    """With the quantization on, a token's batched result stays within the
+    error Q8_0 activations add (~1e-2 relative) of its single-token result."""
+    cfg, tens, x, scores, pos = moe_batch_case()
+    batch = oracle.MoeStack(cfg, tens)
+    yb = batch.forward(x, scores, pos)
+    batch.close()
+    for t in range(len(pos)):
         one = oracle.MoeStack(cfg, tens)
         yt = one.forward(x[t:t + 1], scores[:, t:t + 1], [pos[t]])
-        assert np.array_equal(yt[0].view(np.uint32), yb[t].view(np.uint32))
         one.close()
-    batch.close()
+        err = np.max(np.abs(yt[0] - yb[t])) / np.max(np.abs(yt[0]))
+        assert 0 < err < 2e-2, err
