@@ -14,7 +14,9 @@ from typing import Sequence
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "_build", "liblq8_oracle.so")
+# LQ8_ORACLE_BUILD: another build directory (the sanitizer build, _build_san)
+_BUILD = os.environ.get("LQ8_ORACLE_BUILD") or os.path.join(_HERE, "_build")
+LIB_PATH = os.path.join(_BUILD, "liblq8_oracle.so")
 
 QK = 32
 BLOCK_BYTES = 34
@@ -190,7 +192,7 @@ def linear_forward(blocks, n_out: int, k_in: int, x) -> np.ndarray:
     return y
 
 
-REF_LINEAR_PATH = os.path.join(_HERE, "_build", "libref_linear_bf16.so")
+REF_LINEAR_PATH = os.path.join(_BUILD, "libref_linear_bf16.so")
 _ref_lib = None
 
 

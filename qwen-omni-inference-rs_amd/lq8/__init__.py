@@ -19,7 +19,8 @@ from typing import Optional, Sequence
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "liblq8.so")
+# LQ8_LIBRARY: another build of the library (the sanitizer or trace build)
+LIB_PATH = os.environ.get("LQ8_LIBRARY") or os.path.join(_HERE, "liblq8.so")
 
 QK = 32
 BLOCK_BYTES = 34
