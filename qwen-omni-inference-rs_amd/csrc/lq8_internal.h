@@ -191,6 +191,11 @@ lq8_status launch_rms_quantize_act(hipStream_t s, const float* x, const float* w
                                    int8_t* codes, uint32_t* scales);
 lq8_status launch_silu_quantize_act(hipStream_t s, const float* gu, int m, int inter, int8_t* codes,
                                     uint32_t* scales);
+// The attention outputs of launch_attention_combine (head_dim 128) quantized
+// straight into the operand layout: the values launch_attention_combine
+// followed by launch_quantize_act give.
+lq8_status launch_attention_combine_quant(hipStream_t s, const float* part, size_t part_stride, const int* d_pos,
+                                          int batch, int num_heads, int cmax, int8_t* codes, uint32_t* scales);
 size_t act_code_bytes(int m, int k);
 size_t act_scale_bytes(int m, int k);
 // The activation operand back to GGUF blocks [m][k / 32] (tests, inspection).

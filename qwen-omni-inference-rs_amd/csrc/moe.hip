@@ -6,7 +6,8 @@
 //   qkv   = [q|k|v](RmsNorm(h))               GEMV (T = 1) / W8A8 GEMM (T > 1)
 //   part  = attention segments per sequence    (q/k norm, RoPE, KV append)
 //   h2    = h + o(attention(part))             GEMV with the combine fused (T = 1),
-//                                              combine kernel + W8A8 GEMM (T > 1)
+//                                              combine fused into the activation
+//                                              quantizer + W8A8 GEMM (T > 1)
 //   route = top_k of softmax(scores)           all layers in one launch before the first
 //                                              layer (scores are inputs); expert lists on the device
 //   act   = silu(gate_e x) * up_e x, x = RmsNorm(h2)   grouped multi-vector GEMV over the
@@ -52,7 +53,7 @@ struct lq8_moe {
     std::vector<MoeLayer> layers;
     float *cos_t = nullptr, *sin_t = nullptr;
     float *kc = nullptr, *vc = nullptr;  // [layer][seq][kv_head][max_pos][128]
-    float *h2 = nullptr, *qkv = nullptr, *apart = nullptr, *aout = nullptr;
+    float *h2 = nullptr, *qkv = nullptr, *apart = nullptr;
     float* xn = nullptr;  // [max_batch][hidden]: RmsNorm rows (batched decode)
     int8_t* xq = nullptr;    // activation operand of the batched GEMMs (codes)
     uint32_t* xs = nullptr;  // and its scales
@@ -305,7 +306,7 @@ void release(lq8_moe* m) {
         F(L.in_norm); F(L.post_norm); F(L.q_norm); F(L.k_norm);
     }
     F(m->cos_t); F(m->sin_t); F(m->kc); F(m->vc);
-    F(m->h2); F(m->xn); F(m->xq); F(m->xs); F(m->qkv); F(m->apart); F(m->aout); F(m->gu); F(m->eo);
+    F(m->h2); F(m->xn); F(m->xq); F(m->xs); F(m->qkv); F(m->apart); F(m->gu); F(m->eo);
     F(m->rids); F(m->rw); F(m->n_act); F(m->act_e); F(m->vbeg); F(m->vcnt); F(m->slots);
     F(m->hid_tmp); F(m->scores_tmp); F(m->pos_tmp);
     delete m;
@@ -350,7 +351,7 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_moe_config* c, lq8_moe* m) {
     LQ8_HIP(hipMemset(m->kc, 0, kv * sizeof(float)));
     LQ8_HIP(hipMemset(m->vc, 0, kv * sizeof(float)));
     if ((st = dalloc(&m->h2, B * H)) || (st = dalloc(&m->xn, B * H)) || (st = dalloc(&m->qkv, B * m->QKV)) ||
-        (st = dalloc(&m->apart, B * m->cmax * c->num_heads * ATT_PART_STRIDE)) || (st = dalloc(&m->aout, B * m->QD)) ||
+        (st = dalloc(&m->apart, B * m->cmax * c->num_heads * ATT_PART_STRIDE)) ||
         (st = dalloc(&m->gu, B * K * I)) || (st = dalloc(&m->eo, B * K * H)) ||
         (st = dalloc(&m->rids, NL * B * K)) || (st = dalloc(&m->rw, NL * B * K)) || (st = dalloc(&m->n_act, NL)) ||
         (st = dalloc(&m->act_e, NL * E)) || (st = dalloc(&m->vbeg, NL * E)) || (st = dalloc(&m->vcnt, NL * E)) ||
@@ -461,8 +462,9 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
             g.attn_cmax = m->cmax;
             if ((st = launch_gemv(s, XS_ATTN, EPI_RESID, g))) return st;
         } else {
-            if ((st = launch_attention_combine(s, m->apart, part_stride, d_pos, T, NH, m->cmax, m->aout))) return st;
-            if ((st = launch_quantize_act(s, m->aout, T, (int)m->QD, m->xq, m->xs))) return st;
+            // the segment combine fused into the activation quantizer
+            if ((st = launch_attention_combine_quant(s, m->apart, part_stride, d_pos, T, NH, m->cmax, m->xq, m->xs)))
+                return st;
             if ((st = launch_gemm(s, m->xq, m->xs, T, L.o, m->h2, d_hidden))) return st;
         }
         uint32_t* rids = m->rids + l * B * K;

@@ -387,6 +387,59 @@ __global__ __launch_bounds__(256) void k_silu_quantize_act(const float* __restri
         xs[((size_t)((row >> 5) * 2 * groups + (b >> 2)) * 64 + hf * 32 + (row & 31)) * 4 + (b & 3)] = hf ? 0u : d16;
 }
 
+// Attention outputs of one (head, sequence) combined from the segment
+// partials (the arithmetic of k_attn_combine, thread by thread) and quantized
+// straight into the GEMM operand layout (the values k_quantize_act gives for
+// those outputs): 128 threads, thread d element d of the head; the head's 4
+// blocks are 8 half-blocks, which threads 0..7 quantize from LDS (the two
+// halves of a block are neighbouring threads).  The workgroup of the last
+// head also writes the zero scales of the padding blocks past nb (the GEMM
+// reads them with the block's quad).
+__global__ __launch_bounds__(128) void k_attn_combine_quant(const float* __restrict__ part, size_t part_stride,
+                                                            const int* __restrict__ d_pos, int H, int cmax, int np,
+                                                            int nbp4, int8_t* __restrict__ codes,
+                                                            uint32_t* __restrict__ xs) {
+    __shared__ __attribute__((aligned(16))) float o[128];
+    const int h = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
+    const int C = min(max(d_pos[row], 0) / ATT_SEG + 1, cmax);
+    const float* pb = part + row * part_stride;
+    float m = -__builtin_huge_valf(), den = 0.0f, num = 0.0f;
+    for (int c = 0; c < C; c++) {
+        const float* p = pb + ((size_t)c * H + h) * ATT_PART_STRIDE;
+        const float mc = p[128], lc = p[129];
+        const float mn = m > mc ? m : mc;
+        const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
+        den = den * ea + eb * lc;
+        num = num * ea + eb * p[d];
+        m = mn;
+    }
+    o[d] = __fdiv_rn(num, den);
+    __syncthreads();
+    const int nb = H * 4;
+    if (d < 8) {
+        const int hf = d & 1, b = h * 4 + (d >> 1);
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 t = *(const float4*)&o[(d >> 1) * 32 + hf * 16 + 4 * i];
+            v[4 * i] = t.x;
+            v[4 * i + 1] = t.y;
+            v[4 * i + 2] = t.z;
+            v[4 * i + 3] = t.w;
+        }
+        float amax = half_amax(v);
+        amax = fmaxf(amax, lane_xor<1>(amax));
+        put_act_half(codes, xs, np, nbp4, nb, row, b, hf, v, amax);
+    }
+    if (h == H - 1) {
+        // padding blocks nb .. 4 nbp4 - 1: zero scale words (both halves)
+        for (int i = d; i < 2 * (4 * nbp4 - nb); i += 128) {
+            const int b = nb + (i >> 1), hf = i & 1;
+            xs[((size_t)((row >> 5) * nbp4 + (b >> 2)) * 64 + hf * 32 + (row & 31)) * 4 + (b & 3)] = 0u;
+        }
+    }
+}
+
 // ---- GEMM (W8A8, v_mfma_i32_32x32x32_i8) -------------------------------------
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -685,6 +738,16 @@ lq8_status launch_silu_quantize_act(hipStream_t s, const float* gu, int m, int i
     if (waves > (size_t)INT32_MAX) return fail(LQ8_ERR_SHAPE_MISMATCH, "silu_quantize_act: too many rows");
     hipLaunchKernelGGL(k_silu_quantize_act, dim3(grid1(waves, 4)), dim3(256), 0, s, gu, m, inter, (int)waves, groups,
                        np, codes, scales);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
+lq8_status launch_attention_combine_quant(hipStream_t s, const float* part, size_t part_stride, const int* d_pos,
+                                          int batch, int num_heads, int cmax, int8_t* codes, uint32_t* scales) {
+    if (batch <= 0 || num_heads <= 0 || cmax <= 0) return LQ8_OK;
+    const int nb = num_heads * 4, np = (nb + 1) / 2, groups = (nb + GEMM_GROUP - 1) / GEMM_GROUP;
+    hipLaunchKernelGGL(k_attn_combine_quant, dim3((unsigned)num_heads, (unsigned)batch), dim3(128), 0, s, part,
+                       part_stride, d_pos, num_heads, cmax, np, 2 * groups, codes, scales);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
