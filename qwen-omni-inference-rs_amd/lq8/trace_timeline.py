@@ -7,9 +7,10 @@ relative to the moment the layer's input is complete (the last workgroup's
 layer start, i.e. the last down tile of the previous layer).  Medians over
 the layers 4 .. L-1 of one decode step.
 
-    python -m lq8.persist_trace [--layers 28] [--prompt 128]
+    python -m lq8.trace_timeline [--layers 28] [--prompt 128]
 """
 import argparse
+import contextlib
 import os
 import sys
 
@@ -54,24 +55,53 @@ def timeline(tr: np.ndarray, n_layers: int, first: int = 4):
     return rows, period, p6_rows
 
 
+@contextlib.contextmanager
+def trace_library():
+    """Inside the block lq8's calls go to the trace build (liblq8_trace.so,
+    loaded beside liblq8.so); objects made inside belong to it."""
+    saved = lq8._lib, lq8.LIB_PATH
+    lq8._lib = None
+    lq8.LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(lq8.__file__)), "liblq8_trace.so")
+    try:
+        lq8.lib()
+        yield
+    finally:
+        lq8._lib, lq8.LIB_PATH = saved
+
+
+def collect(layers: int, prompt: int, new: int):
+    """(generate statistics, trace) of Qwen3-0.6B-shaped greedy decode with
+    ``layers`` layers through the persistent kernel of the trace build; the
+    second of two runs is the one traced."""
+    prev = os.environ.get("LQ8_PERSIST")
+    os.environ["LQ8_PERSIST"] = "1"
+    try:
+        with trace_library():
+            cfg = lq8.qwen3_0_6b(max_positions=512)
+            cfg.num_hidden_layers = layers
+            with lq8.Context(0) as ctx:
+                model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=2026)
+                ids = np.random.default_rng(2026).integers(0, cfg.vocab_size, prompt).astype(np.uint32)
+                stats = None
+                for _ in range(2):
+                    _, stats = model.generate_greedy(ids, new)
+                tr = lq8.persist_trace(ctx)
+                model.free()
+    finally:
+        if prev is None:
+            os.environ.pop("LQ8_PERSIST", None)
+        else:
+            os.environ["LQ8_PERSIST"] = prev
+    return stats, tr
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--new", type=int, default=9, help="generated tokens (the 4th decode step is traced)")
     args = ap.parse_args(argv)
-    lq8.LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(lq8.__file__)), "liblq8_trace.so")
-    os.environ["LQ8_PERSIST"] = "1"
-    cfg = lq8.qwen3_0_6b(max_positions=512)
-    cfg.num_hidden_layers = args.layers
-    with lq8.Context(0) as ctx:
-        model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=2026)
-        prompt = np.random.default_rng(2026).integers(0, cfg.vocab_size, args.prompt).astype(np.uint32)
-        stats = None
-        for _ in range(2):  # the second run is the one traced and reported
-            _, stats = model.generate_greedy(prompt, args.new)
-        tr = lq8.persist_trace(ctx)
-        model.free()
+    stats, tr = collect(args.layers, args.prompt, args.new)
     if not stats["used_persistent"]:
         print("the persistent kernel did not run", file=sys.stderr)
         return 1
