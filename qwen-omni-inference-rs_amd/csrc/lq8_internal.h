@@ -191,6 +191,13 @@ lq8_status launch_rms_quantize_act(hipStream_t s, const float* x, const float* w
                                    int8_t* codes, uint32_t* scales);
 lq8_status launch_silu_quantize_act(hipStream_t s, const float* gu, int m, int inter, int8_t* codes,
                                     uint32_t* scales);
+// Routed expert outputs y (rows t * K + j) combined into out = h2 + sum of
+// w * y (ascending expert index, the values k_moe_combine gives), then the
+// operand launch_rms_quantize_act gives for out with norm weight w.
+bool combine_rms_quant_supported(int K, int dim);
+lq8_status launch_combine_rms_quant(hipStream_t s, const float* h2, const float* eo, const uint32_t* rids,
+                                    const float* rw, int K, int m, int dim, const float* w, float eps, float* out,
+                                    int8_t* codes, uint32_t* scales);
 // The attention outputs of launch_attention_combine (head_dim 128) quantized
 // straight into the operand layout: the values launch_attention_combine
 // followed by launch_quantize_act give.

@@ -421,6 +421,7 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
     RouteArgs ra{d_scores, T, E, K, B, m->rids, m->rw, m->n_act, m->act_e, m->vbeg, m->vcnt, m->slots};
     hipLaunchKernelGGL(k_moe_route, dim3((unsigned)m->layers.size()), dim3(64 * ROUTE_WAVES), 0, s, ra);
     LQ8_HIP(hipGetLastError());
+    bool prequant = false;  // T > 1: the previous layer's combine wrote this layer's q|k|v operand
     for (size_t l = 0; l < m->layers.size(); l++) {
         MoeLayer& L = m->layers[l];
         int* n_act = m->n_act + l;
@@ -436,7 +437,9 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
                        (int)m->QKV, H, c.rms_norm_eps};
             if ((st = launch_gemv(s, XS_RMSNORM, EPI_STORE, g))) return st;
         } else {
-            if (rms_quantize_supported(H)) {
+            if (prequant) {
+                // xq / xs already hold RmsNorm(h) of this layer (the previous combine)
+            } else if (rms_quantize_supported(H)) {
                 if ((st = launch_rms_quantize_act(s, d_hidden, L.in_norm, T, H, c.rms_norm_eps, m->xq, m->xs)))
                     return st;
             } else {
@@ -496,7 +499,15 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
         d.n_prob = n_act; d.prob_id = act_e; d.vec_begin = vbeg; d.vec_count = vcnt; d.slots = slots;
         d.x = m->gu; d.x_stride = I; d.x_div = 1; d.y = m->eo; d.y_stride = H; d.max_vec = T;
         if ((st = launch_gemv_mv(s, XS_PLAIN, EPI_STORE, d, max_probs, 1))) return st;
-        // h = h2 + experts (ascending expert index)
+        // h = h2 + experts (ascending expert index); below the last layer fused
+        // with the next layer's input_layernorm + activation quantize
+        prequant = T > 1 && l + 1 < m->layers.size() && combine_rms_quant_supported(K, H);
+        if (prequant) {
+            if ((st = launch_combine_rms_quant(s, m->h2, m->eo, rids, rw, K, T, H, m->layers[l + 1].in_norm,
+                                               c.rms_norm_eps, d_hidden, m->xq, m->xs)))
+                return st;
+            continue;
+        }
         hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, s, m->h2, m->eo,
                            rids, rw, K, H, d_hidden);
         LQ8_HIP(hipGetLastError());

@@ -343,6 +343,106 @@ __global__ __launch_bounds__(256) void k_rms_quantize_act(const float* __restric
     }
 }
 
+// Routed expert outputs combined into the hidden state, then RMSNorm'd and
+// quantized for the next layer's q|k|v GEMM: one workgroup of 1024 threads
+// per padded row (rows past m repeat row m - 1 and write only the operand);
+// a thread loads its elements of every routed expert up front.  The combine is
+// k_moe_combine's arithmetic (acc = acc + w * y over the token's experts in
+// ascending index, from 0; h = h2 + acc), written to out for rows < m; the
+// rest is k_rms_quantize_act's on h (bf16(h)^2 summed in the SUM64 order by
+// wave 0, normed row staged in LDS, half-blocks quantized by neighbouring
+// lanes).  dim <= CRQ_MAX_DIM.
+constexpr int CRQ_MAX_DIM = 2048, CRQ_MAX_K = 16, CRQ_THREADS = 1024, CRQ_PER = CRQ_MAX_DIM / CRQ_THREADS;
+
+__global__ __launch_bounds__(CRQ_THREADS) void k_combine_rms_quant(
+    const float* __restrict__ h2, const float* __restrict__ eo, const uint32_t* __restrict__ rids,
+    const float* __restrict__ rw, int K, int m, int dim, const float* __restrict__ w, float eps, int np, int nbp,
+    float* __restrict__ out, int8_t* __restrict__ codes, uint32_t* __restrict__ xs) {
+    __shared__ __attribute__((aligned(16))) float hrow[CRQ_MAX_DIM];
+    __shared__ int order[CRQ_MAX_K];
+    __shared__ float inv_s;
+    const int row = blockIdx.x, t = min(row, m - 1), tid = threadIdx.x;
+    float hv[CRQ_PER], wn[CRQ_PER];  // the norm weights load with the row, off the critical path
+#pragma unroll
+    for (int e = 0; e < CRQ_PER; e++) {
+        const int ic = min(tid + e * CRQ_THREADS, dim - 1);
+        hv[e] = h2[(size_t)t * dim + ic];
+        wn[e] = w[ic];
+    }
+    if (tid < K) {
+        const uint32_t me = rids[t * K + tid];
+        int below = 0;
+        for (int r = 0; r < K; r++) below += rids[t * K + r] < me;
+        order[below] = tid;  // expert ids of a token are distinct
+    }
+    __syncthreads();
+    // every load of the row's experts in flight before the sums
+    float wv[CRQ_MAX_K], ev[CRQ_PER][CRQ_MAX_K];
+#pragma unroll
+    for (int q = 0; q < CRQ_MAX_K; q++) {
+        if (q < K) {
+            const int slot = t * K + order[q];
+            wv[q] = rw[slot];
+#pragma unroll
+            for (int e = 0; e < CRQ_PER; e++) ev[e][q] = eo[(size_t)slot * dim + min(tid + e * CRQ_THREADS, dim - 1)];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < CRQ_PER; e++) {
+        const int i = tid + e * CRQ_THREADS;
+        float acc = 0.0f;
+#pragma unroll
+        for (int q = 0; q < CRQ_MAX_K; q++)
+            if (q < K) acc = acc + wv[q] * ev[e][q];
+        const float h = hv[e] + acc;
+        if (i < dim) {
+            if (row < m) out[(size_t)t * dim + i] = h;
+            hrow[i] = h;
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        float v[CRQ_MAX_DIM / 64];  // every LDS read in flight, then the adds in order
+#pragma unroll
+        for (int u = 0; u < CRQ_MAX_DIM / 64; u++) v[u] = hrow[min(tid + 64 * u, dim - 1)];
+        float acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < CRQ_MAX_DIM / 64; u++)
+            if (tid + 64 * u < dim) {
+                const float b = bf16_round(v[u]);
+                acc = acc + b * b;
+            }
+        acc = wave_sum64(acc);
+        if (tid == 0) inv_s = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)dim) + eps));
+    }
+    __syncthreads();
+    const float inv = inv_s;
+#pragma unroll
+    for (int e = 0; e < CRQ_PER; e++) {
+        const int i = tid + e * CRQ_THREADS;
+        if (i < dim) hrow[i] = bf16_round((bf16_round(hrow[i]) * inv) * bf16_round(wn[e]));
+    }
+    __syncthreads();
+    const int nb = dim >> 5, nhb = 2 * nbp;
+    for (int hb0 = 0; hb0 < nhb; hb0 += CRQ_THREADS) {
+        const int hb = hb0 + tid, b = hb >> 1, hf = hb & 1;
+        float q[16] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        if (b < nb) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 v4 = *(const float4*)&hrow[b * 32 + hf * 16 + 4 * i];
+                q[4 * i] = v4.x;
+                q[4 * i + 1] = v4.y;
+                q[4 * i + 2] = v4.z;
+                q[4 * i + 3] = v4.w;
+            }
+        }
+        float amax = half_amax(q);
+        amax = fmaxf(amax, lane_xor<1>(amax));
+        if (hb < nhb) put_act_half(codes, xs, np, nbp >> 2, nb, row, b, hf, q, amax);
+    }
+}
+
 // act = silu(gate) * up of rows gu[m, 2 inter] (as k_silu_mul: silu(g) =
 // g / (1 + exp(-g)), src/tensor.rs:1978, mlp.rs:151-164) quantized straight
 // into the GEMM operand layout.  One wave per (padded row, group of 8
@@ -680,6 +780,128 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
 }
 
+// ---- small-M GEMM: 16 x 16 output tiles (v_mfma_i32_16x16x32_i8) -----------
+//
+// For few 32 x 32 tiles (M of a batch of sequences): one 16 (rows of x) x 16
+// (rows of W) tile per workgroup, wave s runs group s (S = the number of
+// groups, one round), the same per-block arithmetic and group order as
+// k_gemm.  A 16-row tile chunk of pair p holds in lane (r, part) the codes
+// 16 part .. 16 part + 15 of the pair (part 0, 1: block 2p; 2, 3: block
+// 2p + 1); one permlane32 swap per dword turns it into the two blocks'
+// operands (block 2p: lanes 0..31 their own low 8 bytes, lanes 32..63 the
+// high 8 bytes of lane l - 32; block 2p + 1 the mirror image), so every lane
+// group of 16 holds 8 codes of one block.  x and W are split alike, so the
+// int32 dot of each block is exact.  Scale products: one
+// v_mfma_f32_16x16x16f16 per block with dx (lanes 0..15, element 0) and dw
+// (lanes 0..15 of a real block, element 0), zero elsewhere: D = dx * dw
+// exactly, 0 past nb.  Accumulator: lane l holds column l % 16 of rows
+// 4 (l / 16) .. 4 (l / 16) + 3.
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+struct Gemm16Args {
+    const int8_t* xq;
+    const uint32_t* xs;
+    const int8_t* wc;
+    const uint16_t* ws;
+    float* y;
+    const float* resid;
+    int m, n, nb, np, nbp4, mt16, nt16;
+    int xq_bytes, xs_bytes, wc_bytes, ws_bytes;
+};
+
+__device__ __forceinline__ void split_pair(const v4i c, long& b0, long& b1) {
+    const auto p0 = __builtin_amdgcn_permlane32_swap((uint32_t)c[0], (uint32_t)c[2], false, false);
+    const auto p1 = __builtin_amdgcn_permlane32_swap((uint32_t)c[1], (uint32_t)c[3], false, false);
+    b0 = (long)((uint64_t)p0[0] | ((uint64_t)p1[0] << 32));
+    b1 = (long)((uint64_t)p0[1] | ((uint64_t)p1[1] << 32));
+}
+
+template <int S>
+__global__ __launch_bounds__(64 * S) void k_gemm16(Gemm16Args g) {
+    __shared__ v4f part[S > 1 ? S - 1 : 1][64];
+    const int lane = threadIdx.x & 63;
+    const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // workgroups of one XCD (ids congruent mod 8) take a contiguous run of
+    // tiles; the m-tiles of one n-tile are neighbours (their weight reads
+    // meet in that XCD's L2)
+    const int ntiles = g.mt16 * g.nt16;
+    const int wgi = blockIdx.x, per = ntiles >> 3, rem = ntiles & 7, xcd = wgi & 7, j8 = wgi >> 3;
+    const int tl = xcd < rem ? xcd * (per + 1) + j8 : rem * (per + 1) + (xcd - rem) * per + j8;
+    const int nt = tl / g.mt16, mt = tl - nt * g.mt16;
+    const int r = lane & 15;
+    const bool lo = lane < 16;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)g.xq, (short)0, g.xq_bytes, RSRC_CFG);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)g.wc, (short)0, g.wc_bytes, RSRC_CFG);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)g.xs, (short)0, g.xs_bytes, RSRC_CFG);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)g.ws, (short)0, g.ws_bytes, RSRC_CFG);
+    const int np = g.np, nb = g.nb;
+    // operands of group s: pairs 4 s .. 4 s + 3 (clamped to the last pair;
+    // their blocks are past nb and get zero scales)
+    v4i ac[4], wcv[4];
+    uint32_t dw[GEMM_GROUP];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int p = min(4 * s + j, np - 1);
+        ac[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, ((mt * np + p) * 64 + lane) * 16, 0, 0));
+        wcv[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, ((nt * np + p) * 64 + lane) * 16, 0, 0));
+    }
+    const int row = mt * 16 + r;  // activation row of lanes 0..15 (the operand holds every row of the tile)
+    v4i dxq[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+        dxq[q] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rx, (((row >> 5) * g.nbp4 + 2 * s + q) * 64 + (row & 31)) * 16, 0, 0));
+#pragma unroll
+    for (int i = 0; i < GEMM_GROUP; i++)
+        dw[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, ((nt * 2 * np + min(GEMM_GROUP * s + i, nb - 1)) * 16 + r) * 2, 0, 0);
+    const v4i zi = {0, 0, 0, 0};
+    const v4f zf = {0, 0, 0, 0};
+    v4f acc = zf;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        long a2[2], w2[2];
+        split_pair(ac[j], a2[0], a2[1]);
+        split_pair(wcv[j], w2[0], w2[1]);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int i = 2 * j + h, b = GEMM_GROUP * s + i;
+            const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(a2[h], w2[h], zi, 0, 0, 0);
+            const uint2 au = {lo ? (uint32_t)dxq[i >> 2][i & 3] : 0u, 0u};
+            const uint2 bu = {(lo && b < nb) ? dw[i] : 0u, 0u};
+            const v4f P = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h, au), __builtin_bit_cast(v4h, bu),
+                                                                zf, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] = fmaf((float)I[v], P[v], acc[v]);
+        }
+    }
+    // group order: y = 0 + a_0, then + a_1, ... (wave 0 sums the others' from LDS)
+    if (S > 1) {
+        if (s > 0) part[s - 1][lane] = acc;
+        __syncthreads();
+    }
+    if (s != 0) return;
+    v4f y;
+#pragma unroll
+    for (int v = 0; v < 4; v++) y[v] = 0.0f + acc[v];
+#pragma unroll
+    for (int u = 1; u < S; u++) {
+        const v4f t = part[u - 1][lane];
+#pragma unroll
+        for (int v = 0; v < 4; v++) y[v] = y[v] + t[v];
+    }
+    const int col = nt * 16 + r;
+    if (col >= g.n) return;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int m = mt * 16 + 4 * (lane >> 4) + v;
+        if (m < g.m) {
+            const size_t off = (size_t)m * g.n + col;
+            g.y[off] = g.resid ? g.resid[off] + y[v] : y[v];
+        }
+    }
+}
+
 inline unsigned grid1(size_t n, unsigned block) { return (unsigned)((n + block - 1) / block); }
 
 }  // namespace
@@ -729,6 +951,23 @@ lq8_status launch_rms_quantize_act(hipStream_t s, const float* x, const float* w
     return LQ8_OK;
 }
 
+bool combine_rms_quant_supported(int K, int dim) {
+    return K >= 1 && K <= CRQ_MAX_K && rms_quantize_supported(dim) && dim <= CRQ_MAX_DIM;
+}
+
+lq8_status launch_combine_rms_quant(hipStream_t s, const float* h2, const float* eo, const uint32_t* rids,
+                                    const float* rw, int K, int m, int dim, const float* w, float eps, float* out,
+                                    int8_t* codes, uint32_t* scales) {
+    if (!combine_rms_quant_supported(K, dim)) return fail(LQ8_ERR_SHAPE_MISMATCH, "combine_rms_quant: unsupported shape");
+    if (m <= 0) return LQ8_OK;
+    const int nb = dim / 32, np = (nb + 1) / 2, nbp = GEMM_GROUP * ((nb + GEMM_GROUP - 1) / GEMM_GROUP);
+    const unsigned grid = (unsigned)((m + 31) / 32 * 32);  // the padded rows
+    hipLaunchKernelGGL(k_combine_rms_quant, dim3(grid), dim3(CRQ_THREADS), 0, s, h2, eo, rids, rw, K, m, dim, w, eps,
+                       np, nbp, out, codes, scales);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
 lq8_status launch_silu_quantize_act(hipStream_t s, const float* gu, int m, int inter, int8_t* codes,
                                     uint32_t* scales) {
     if (inter <= 0 || inter % 32) return fail(LQ8_ERR_SHAPE_MISMATCH, "silu_quantize_act: unsupported width");
@@ -769,6 +1008,12 @@ lq8_status launch_quantize_aos(hipStream_t s, const float* x, size_t nblocks, ui
     return LQ8_OK;
 }
 
+// The 16 x 16 kernel (one round, a wave per group) when 32 x 32 tiles would
+// leave most CUs idle: a batch of up to 64 rows against fewer than 512 tiles
+// (M = 32: the 2048 x 4096 projection 14.1 -> 6.3 us, 5120 x 2048 8.8 -> 6.5
+// us per call inside the 48-layer MoE step).
+static bool gemm16_pick(int m, int groups, size_t tiles32) { return groups <= 16 && m <= 64 && tiles32 < 512; }
+
 lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const uint32_t* xs, int m, const lq8_weight* w, float* y,
                        const float* resid) {
     const size_t k = w->k_in;
@@ -805,6 +1050,27 @@ lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const uint32_t* xs, int 
     const size_t tiles = (size_t)g.ntm * ntn;
     if (tiles > lim) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemm: too many tiles");
     g.ntiles = (int)tiles;
+    if (gemm16_pick(m, g.groups, tiles)) {
+        Gemm16Args h;
+        h.xq = xq; h.xs = xs; h.wc = w->codes; h.ws = w->scales; h.y = y; h.resid = resid;
+        h.m = m; h.n = g.n; h.nb = g.nb; h.np = g.np; h.nbp4 = 2 * g.groups;
+        h.mt16 = (m + 15) / 16;
+        h.nt16 = (g.n + 15) / 16;
+        h.xq_bytes = g.xq_bytes; h.xs_bytes = g.xs_bytes; h.wc_bytes = g.wc_bytes; h.ws_bytes = g.ws_bytes;
+        const dim3 grid16((unsigned)(h.mt16 * h.nt16));
+#define LQ8_GEMM16_CASE(SS) \
+    case SS: hipLaunchKernelGGL((k_gemm16<SS>), grid16, dim3(64 * SS), 0, s, h); break;
+        switch (g.groups) {
+            LQ8_GEMM16_CASE(1) LQ8_GEMM16_CASE(2) LQ8_GEMM16_CASE(3) LQ8_GEMM16_CASE(4) LQ8_GEMM16_CASE(5)
+            LQ8_GEMM16_CASE(6) LQ8_GEMM16_CASE(7) LQ8_GEMM16_CASE(8) LQ8_GEMM16_CASE(9) LQ8_GEMM16_CASE(10)
+            LQ8_GEMM16_CASE(11) LQ8_GEMM16_CASE(12) LQ8_GEMM16_CASE(13) LQ8_GEMM16_CASE(14) LQ8_GEMM16_CASE(15)
+            LQ8_GEMM16_CASE(16)
+            default: return fail(LQ8_ERR_DEVICE, "gemm: no 16 x 16 kernel for this split");
+        }
+#undef LQ8_GEMM16_CASE
+        LQ8_HIP(hipGetLastError());
+        return LQ8_OK;
+    }
     int S;
     if (g.groups <= 16 && (g.groups <= 4 || tiles * g.groups <= 8192)) {
         S = g.groups;

@@ -259,6 +259,27 @@ def test_gemm_ragged(ctx, m, n, k):
     assert_parity(y, ref)
 
 
+@pytest.mark.parametrize("n,k", [(2048, 4096), (5120, 2048)])
+def test_gemm_small_batch_kernels_agree(ctx, n, k):
+    """A batch of 32 rows runs the 16 x 16-tile kernel, one of 96 rows the
+    32 x 32 one: both give the oracle's bits, and since an output row depends
+    only on its own activation row, the 32 rows they share are equal."""
+    blocks = oracle.quantize_q8_0(normal((n, k), 0.02, n + k))
+    x = normal((96, k), 1.0, 7)
+    w = lq8.Q8Weight.from_blocks(ctx, blocks, n, k)
+    out = {}
+    for m in (32, 96):
+        dx = lq8.DeviceBuffer.from_array(ctx, np.ascontiguousarray(x[:m]))
+        dy = lq8.DeviceBuffer(ctx, m * n * 4)
+        lq8._check(lq8.lib().lq8_gemm_q8_0_device(ctx.handle, w.handle, dx.ptr, m, dy.ptr))
+        out[m] = dy.download(np.float32, m * n).reshape(m, n)
+        dx.free(); dy.free()
+    w.free()
+    ref = oracle.gemm_q8_0(blocks, n, k, x[:32])
+    assert np.array_equal(out[32].view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(out[96][:32].view(np.uint32), out[32].view(np.uint32))
+
+
 def test_gemm_scale_edge_cases(ctx):
     """Activation and weight blocks whose f16 scales are subnormal (amax
     below 127 * 2^-14) or zero, NaN entries (ignored by amax), and a block
