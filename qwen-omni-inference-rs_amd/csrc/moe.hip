@@ -78,8 +78,9 @@ namespace {
 // larger p or an equal p and a lower index; ranks below top_k are chosen, in
 // rank order; weights p_r / (((p_0 + p_1) + p_2) + ...).  Then the routed
 // (token, rank) slots t * top_k + r are counted per expert, the active
-// experts numbered in ascending order (n_act, act_e, vbeg, vcnt) and each
-// slot placed in its expert's list (slots).  The order inside one expert's
+// experts numbered by descending vector count, then ascending index (n_act,
+// act_e, vbeg, vcnt; the expert GEMVs' workgroups follow that order), and
+// each slot placed in its expert's list (slots, by ascending expert).  The order inside one expert's
 // list is whatever the atomics give: every slot is computed on its own, so
 // results do not depend on it.
 constexpr int ROUTE_WAVES = 16;
@@ -208,17 +209,23 @@ __global__ __launch_bounds__(64 * ROUTE_WAVES) void k_moe_route(RouteArgs ra) {
             const int a1 = __shfl_up(ptot, d, 64), a2 = __shfl_up(pnz, d, 64);
             if (lane >= d) { ptot += a1; pnz += a2; }
         }
-        int off = ptot - tot, j = pnz - nz;
+        int off = ptot - tot;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int e = 4 * lane + q;
             if (e < E) {
                 beg[e] = off;
                 if (c[q]) {
+                    // problem number: experts with more vectors first (then
+                    // ascending index), so the longest workgroups start first
+                    int j = 0;
+                    for (int f = 0; f < E; f++) {
+                        const int cf = cnt[f];
+                        j += cf > c[q] || (cf == c[q] && f < e);
+                    }
                     act_e[j] = e;
                     vbeg[j] = off;
                     vcnt[j] = c[q];
-                    j++;
                 }
                 off += c[q];
             }

@@ -501,16 +501,36 @@ __global__ __launch_bounds__(128) void k_attn_combine_quant(const float* __restr
                                                             uint32_t* __restrict__ xs) {
     __shared__ __attribute__((aligned(16))) float o[128];
     const int h = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
-    const int C = min(max(d_pos[row], 0) / ATT_SEG + 1, cmax);
     const float* pb = part + row * part_stride;
+    // the first CQ segments' partials load with the position (indices
+    // clamped to the capacity: in bounds, entries past the position unused)
+    constexpr int CQ = 4;
+    float mq[CQ], lq[CQ], oq[CQ];
+#pragma unroll
+    for (int c = 0; c < CQ; c++) {
+        const float* p = pb + ((size_t)min(c, cmax - 1) * H + h) * ATT_PART_STRIDE;
+        mq[c] = p[128];
+        lq[c] = p[129];
+        oq[c] = p[d];
+    }
+    const int C = min(max(d_pos[row], 0) / ATT_SEG + 1, cmax);
     float m = -__builtin_huge_valf(), den = 0.0f, num = 0.0f;
     for (int c = 0; c < C; c++) {
-        const float* p = pb + ((size_t)c * H + h) * ATT_PART_STRIDE;
-        const float mc = p[128], lc = p[129];
+        float mc, lc, oc;
+        if (c < CQ) {
+            mc = mq[c];
+            lc = lq[c];
+            oc = oq[c];
+        } else {
+            const float* p = pb + ((size_t)c * H + h) * ATT_PART_STRIDE;
+            mc = p[128];
+            lc = p[129];
+            oc = p[d];
+        }
         const float mn = m > mc ? m : mc;
         const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
         den = den * ea + eb * lc;
-        num = num * ea + eb * p[d];
+        num = num * ea + eb * oc;
         m = mn;
     }
     o[d] = __fdiv_rn(num, den);
