@@ -800,6 +800,106 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
 }
 
+// One round, every group its own wave (S = groups): a (32 TM) x 32 output
+// block per workgroup; wave s runs group s over TM 32 x 32 MFMA tiles that
+// share each weight fragment.  The operands of block i + 1 are issued behind
+// the compute of block i (a one-block window: few registers, so many waves
+// per SIMD hide the load latency; deeper windows and issuing the whole group
+// up front measured slower).  Every wave writes its group sums to LDS and all
+// threads then finish the outputs (consecutive threads own consecutive
+// columns, so the LDS reads and the stores are coalesced), each in group
+// order: y = 0 + a_0, then + a_1, ... (the oracle's order), then y = resid + y.
+template <int S, int TM>
+__global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(3))) void k_gemm_one(GemmArgs g) {
+    extern __shared__ float gpart[];  // [S][TM][16][64]
+    const int lane = threadIdx.x & 63;
+    const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ntmb = (g.ntm + TM - 1) / TM;
+    const int wgi = blockIdx.x, per = g.ntiles >> 3, rem = g.ntiles & 7, xcd = wgi & 7, j8 = wgi >> 3;
+    const int tl = xcd < rem ? xcd * (per + 1) + j8 : rem * (per + 1) + (xcd - rem) * per + j8;
+    const int bn = tl / ntmb, bm = tl - bn * ntmb;
+    const int half = lane >> 5, r32 = lane & 31;
+    const bool lo = lane < 32;
+    const int nb = g.nb, G = g.groups;
+    const auto ra = __builtin_amdgcn_make_buffer_rsrc((void*)g.xq, (short)0, g.xq_bytes, RSRC_CFG);
+    const auto rb = __builtin_amdgcn_make_buffer_rsrc((void*)g.wc, (short)0, g.wc_bytes, RSRC_CFG);
+    const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)g.xs, (short)0, g.xs_bytes, RSRC_CFG);
+    const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)g.ws, (short)0, g.ws_bytes, RSRC_CFG);
+    int oa[TM], ox[TM], mts[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+        mts[t] = min(bm * TM + t, g.ntm - 1);
+        oa[t] = ((mts[t] * 2 + (r32 >> 4)) * g.np * 64 + half * 16 + (r32 & 15)) * 16;
+        ox[t] = (mts[t] * 2 * G * 64 + lane) * 16;
+    }
+    const int ob = ((bn * 2 + (r32 >> 4)) * g.np * 64 + half * 16 + (r32 & 15)) * 16;
+    const int ow = ((bn * 2 + (r32 >> 4)) * 2 * g.np * 16 + (r32 & 15)) * 2;
+    const int b0 = s * GEMM_GROUP;
+    v4i A[GEMM_GROUP][TM], B[GEMM_GROUP];
+    uint32_t dw[GEMM_GROUP];
+    v4i dx[2][TM];
+    // operands of block i of the group (codes of blocks past nb are read from
+    // block nb - 1 and cancelled by a zero scale below)
+    auto load_block = [&](int i) {
+        const int bc = min(b0 + i, nb - 1);
+        const int cs = (bc >> 1) * 1024 + (bc & 1) * 512;
+        if ((i & 3) == 0) {
+#pragma unroll
+            for (int t = 0; t < TM; t++)
+                dx[i >> 2][t] = __builtin_bit_cast(
+                    v4i, __builtin_amdgcn_raw_buffer_load_b128(rx, ox[t], ((b0 >> 2) + (i >> 2)) * 1024, 0));
+        }
+#pragma unroll
+        for (int t = 0; t < TM; t++)
+            A[i][t] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, oa[t], cs, 0));
+        B[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, ob, cs, 0));
+        dw[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, ow, bc * 32, 0);
+    };
+    const v16i zi = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    float acc[TM][16];
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+    load_block(0);
+    __builtin_amdgcn_sched_barrier(0);
+    // acc = fmaf((float)I_b, dw_b * dx_b, acc) per block in order (gemm_quad
+    // explains the scale MFMA)
+#pragma unroll
+    for (int i = 0; i < GEMM_GROUP; i++) {
+        const uint2 bu = {(lo && b0 + i < nb) ? dw[i] : 0u, 0u};
+#pragma unroll
+        for (int t = 0; t < TM; t++) {
+            const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i][t], B[i], zi, 0, 0, 0);
+            const uint2 au = {(uint32_t)dx[i >> 2][t][i & 3], 0u};
+            const v16f P = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, au), __builtin_bit_cast(v4h, bu),
+                                                                zf, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[t][r] = fmaf((float)I[r], P[r], acc[t][r]);
+        }
+        if (i + 1 < GEMM_GROUP) load_block(i + 1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) gpart[((s * TM + t) * 16 + r) * 64 + lane] = acc[t][r];
+    __syncthreads();
+    for (int o = threadIdx.x; o < TM * 16 * 64; o += 64 * S) {
+        const int l = o & 63, r = (o >> 6) & 15, t = o >> 10;
+        float y = 0.0f;
+        for (int u = 0; u < S; u++) y = y + gpart[((u * TM + t) * 16 + r) * 64 + l];
+        const int row = mts[t] * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+        const int col = bn * 32 + (l & 31);
+        if (bm * TM + t < g.ntm && row < g.m && col < g.n) {
+            const size_t off = (size_t)row * g.n + col;
+            if (g.resid) y = g.resid[off] + y;
+            g.y[off] = y;
+        }
+    }
+}
+
 // ---- small-M GEMM: 16 x 16 output tiles (v_mfma_i32_16x16x32_i8) -----------
 //
 // For few 32 x 32 tiles (M of a batch of sequences): one 16 (rows of x) x 16
@@ -1059,13 +1159,15 @@ lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const uint32_t* xs, int 
     g.xs_bytes = (int)xs_bytes;
     g.wc_bytes = (int)wc_bytes;
     g.ws_bytes = (int)ws_bytes;
-    // One 32 x 32 tile per workgroup, K split over S waves (one group per wave
-    // per round).  Register-blocked 2 x 1 and 2 x 2 tiles per wave (the
-    // template's TM, TN) measured slower at M = 512 and 2048: a wave's time
-    // goes to issuing its operand loads, and larger tiles give fewer waves.
-    // S: every group its own wave (one round, no running sum) when the groups
-    // are few (<= 4) or the waves that gives stay <= 8192; otherwise the
-    // fewest of 2, 3, 4, 6, 8, 12, 16 that give >= 2048 waves.
+    // K split over S waves (one group per wave per round).  S: every group its
+    // own wave (one round, no running sum: k_gemm_one) when the groups are
+    // few (<= 4) or the waves that gives stay <= 8192; otherwise the fewest of
+    // 2, 3, 4, 6, 8, 12, 16 that give >= 2048 waves (k_gemm, one 32 x 32 tile
+    // per workgroup, running sum over rounds).  k_gemm_one gives each wave two
+    // 32-row tiles sharing the weight fragment for long K (8 - 12 groups) when
+    // that still leaves >= 3072 waves (M = 512 down 8.0 -> 7.0 us); with fewer
+    // groups or waves the single tile measured faster (M = 512 gate/up 8.6
+    // against 8.7 us; M = 128 - 256 by 1 - 2 us).
     const int ntn = (g.n + 31) / 32;
     const size_t tiles = (size_t)g.ntm * ntn;
     if (tiles > lim) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemm: too many tiles");
@@ -1101,18 +1203,35 @@ lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const uint32_t* xs, int 
             if (tiles * c >= 2048) { S = c; break; }
         S = std::min(S, g.groups);
     }
-    const bool one = S == g.groups;
-    const size_t smem = S > 1 ? (size_t)(S - 1) * 4 * 64 * sizeof(float4) : 0;
+    if (S == g.groups) {
+        const size_t tiles2 = (size_t)((g.ntm + 1) / 2) * ntn;
+        const bool two = g.ntm >= 2 && S >= 8 && S <= 12 && tiles2 * S >= 3072;
+        if (two) g.ntiles = (int)tiles2;
+        const size_t smem1 = (size_t)S * (two ? 2 : 1) * 16 * 64 * sizeof(float);
+        const dim3 grid1d((unsigned)g.ntiles);
+#define LQ8_GEMM_ONE_CASE(SS)                                                                          \
+    case SS:                                                                                           \
+        if (two) hipLaunchKernelGGL((k_gemm_one<SS, 2>), grid1d, dim3(64 * SS), smem1, s, g);           \
+        else hipLaunchKernelGGL((k_gemm_one<SS, 1>), grid1d, dim3(64 * SS), smem1, s, g);               \
+        break;
+        switch (S) {
+            LQ8_GEMM_ONE_CASE(1) LQ8_GEMM_ONE_CASE(2) LQ8_GEMM_ONE_CASE(3) LQ8_GEMM_ONE_CASE(4)
+            LQ8_GEMM_ONE_CASE(5) LQ8_GEMM_ONE_CASE(6) LQ8_GEMM_ONE_CASE(7) LQ8_GEMM_ONE_CASE(8)
+            LQ8_GEMM_ONE_CASE(9) LQ8_GEMM_ONE_CASE(10) LQ8_GEMM_ONE_CASE(11) LQ8_GEMM_ONE_CASE(12)
+            LQ8_GEMM_ONE_CASE(13) LQ8_GEMM_ONE_CASE(14) LQ8_GEMM_ONE_CASE(15) LQ8_GEMM_ONE_CASE(16)
+            default: return fail(LQ8_ERR_DEVICE, "gemm: no kernel for this split");
+        }
+#undef LQ8_GEMM_ONE_CASE
+        LQ8_HIP(hipGetLastError());
+        return LQ8_OK;
+    }
+    const size_t smem = (size_t)(S - 1) * 4 * 64 * sizeof(float4);
     const dim3 grid((unsigned)g.ntiles);
 #define LQ8_GEMM_CASE(SS)                                                                          \
-    case SS:                                                                                       \
-        if (one) hipLaunchKernelGGL((k_gemm<SS, 1, 1, true>), grid, dim3(64 * SS), smem, s, g);     \
-        else hipLaunchKernelGGL((k_gemm<SS, 1, 1, false>), grid, dim3(64 * SS), smem, s, g);        \
-        break;
+    case SS: hipLaunchKernelGGL((k_gemm<SS, 1, 1, false>), grid, dim3(64 * SS), smem, s, g); break;
     switch (S) {
-        LQ8_GEMM_CASE(1) LQ8_GEMM_CASE(2) LQ8_GEMM_CASE(3) LQ8_GEMM_CASE(4) LQ8_GEMM_CASE(5) LQ8_GEMM_CASE(6)
-        LQ8_GEMM_CASE(7) LQ8_GEMM_CASE(8) LQ8_GEMM_CASE(9) LQ8_GEMM_CASE(10) LQ8_GEMM_CASE(11) LQ8_GEMM_CASE(12)
-        LQ8_GEMM_CASE(13) LQ8_GEMM_CASE(14) LQ8_GEMM_CASE(15) LQ8_GEMM_CASE(16)
+        LQ8_GEMM_CASE(2) LQ8_GEMM_CASE(3) LQ8_GEMM_CASE(4) LQ8_GEMM_CASE(6) LQ8_GEMM_CASE(8) LQ8_GEMM_CASE(12)
+        LQ8_GEMM_CASE(16)
         default: return fail(LQ8_ERR_DEVICE, "gemm: no kernel for this split");
     }
 #undef LQ8_GEMM_CASE
