@@ -107,7 +107,9 @@ __device__ __forceinline__ void seg_load_capacity(const float* __restrict__ Kc, 
     }
 }
 
-template <int NT = ATT_THREADS, bool PIN_TID = false>
+// LDS_SYNC: the barriers order LDS only (lds_sync: the caller's own global
+// stores are not waited for), for callers that keep global visibility apart.
+template <int NT = ATT_THREADS, bool PIN_TID = false, bool LDS_SYNC = false>
 __device__ __forceinline__ void seg_scores(const float4* kreg, int nj, int knew_row, const float* knew, const float* qs,
                                            int G, float scale, float* ks, float* sc, float* mlc) {
     const int tid = thread_x<PIN_TID>(), lane = tid & 63;
@@ -123,7 +125,8 @@ __device__ __forceinline__ void seg_scores(const float4* kreg, int nj, int knew_
             dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
         }
     }
-    __syncthreads();
+    if (LDS_SYNC) lds_sync();
+    else __syncthreads();
     for (int t = tid; t < G * SEG; t += NT) {
         const int h = t / SEG, j = t % SEG;
         if (j < nj) {
@@ -134,7 +137,8 @@ __device__ __forceinline__ void seg_scores(const float4* kreg, int nj, int knew_
             sc[h * SEG + j] = s * scale;
         }
     }
-    __syncthreads();
+    if (LDS_SYNC) lds_sync();
+    else __syncthreads();
     for (int h = wave; h < G; h += NT / 64) {
         const float s = lane < nj ? sc[h * SEG + lane] : -__builtin_huge_valf();
         const float mc = wave_max64(s);

@@ -6,13 +6,27 @@
 
 namespace lq8 {
 
-constexpr int PERSIST_THREADS = 256;
+constexpr int PERSIST_THREADS = 512;
+constexpr int PERSIST_FETCH = 16;  // hand-off words one thread fetches per phase, at most
+constexpr int PERSIST_NCH = 8;     // o-projection input chunks (partial sums per output row), at most
 
 // Device pointers of one decoder layer.
 struct PLayer {
     const int8_t *qkv_c, *o_c, *gu_c, *dn_c;
     const uint16_t *qkv_s, *o_s, *gu_s, *dn_s;
     const float *in_norm, *post_norm, *q_norm, *k_norm;
+};
+
+struct PersistShape {
+    int H, I, NH, NKV, head_dim, max_pos;
+};
+
+// Work split and LDS map of one shape on P workgroups (persist_layout).
+struct PersistLayout {
+    int csO, nchO;      // o projection: input chunks of csO blocks (a power of two), nchO of them
+    int fr, xs_off, gs_off, red_off, att_floats;  // LDS, in floats
+    int smem_bytes;
+    size_t words;       // tagged hand-off words of all buffers
 };
 
 struct PersistArgs {
@@ -27,15 +41,14 @@ struct PersistArgs {
     float* vc;
     int H, I, NH, NKV, max_pos, cmax, vocab;
     float eps, scale;
-    // tagged hand-off words (f32 bits | tag << 32), per layer
-    uint64_t* qkvb;   // [L][QKV]
-    uint64_t* partb;  // [L][cmax][NH][ATT_PART_STRIDE]
-    uint64_t* attnb;  // [L][NH * 128]: the combined attention output
-    uint64_t* h2b;    // [L][H]
-    uint64_t* actb;   // [L][I]
-    uint64_t* hb;     // [L][H]
+    int csO, nchO;
+    // tagged hand-off words (f32 bits | tag << 32)
+    uint64_t* qkvb;   // [L][QKV]: q|k|v projection
+    uint64_t* partb;  // [L][cmax][NH][ATT_PART_STRIDE]: attention partials per (segment, head)
+    uint64_t* resb;   // [L + 1][(1 + nchO) * H]: layer input h, then the o projection's chunk sums [nchO][H]
+    uint64_t* h2b;    // [L][H]: h + o projection (the MLP's input and residual)
+    uint64_t* actb;   // [L][I]: silu(gate) * up
     uint64_t* argb;   // [P][2]: each workgroup's greedy pick (value, index bits)
-    unsigned* cntb;   // [L][NKV][16]: per kv head, the step's segment arrivals (back to 0 after the last)
     unsigned* abort_flag;
     // steps: positions pos0 .. pos0 + steps - 1; tokens_out[step0 + s] gets step s's pick
     int pos0, steps, step0, feed_first;
@@ -44,19 +57,23 @@ struct PersistArgs {
     uint32_t* tokens_out;
     int* d_pos;
     int* d_step;
-    // LDS layout (floats) and size (bytes)
-    int xs_floats, region_a, smem_bytes;
+    // LDS map (floats) and size (bytes)
+    int fr, xs_off, gs_off, red_off, smem_bytes;
 };
 
-struct PersistShape {
-    int H, I, NH, NKV, head_dim, max_pos;
-};
-
+// false when the shape does not fit the kernel's limits on P workgroups
+bool persist_layout(const PersistShape& s, int P, PersistLayout* out);
 bool persist_supported(const PersistShape& s, int num_cus);
-size_t persist_xs_floats(const PersistShape& s);
-size_t persist_region_a(const PersistShape& s);
-size_t persist_smem_bytes(const PersistShape& s);
 // d_args: the argument block in device memory (read by the kernel throughout)
-lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg);
+// ch5: block pairs per wave group of the down tile (persist_down_group)
+lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg, int ch5);
+// block pairs per wave group of the down tile (the workgroup's waves over
+// ceil(I / 64) pairs): 1, 2, 4 or 8
+inline int persist_down_group(int I) {
+    const int np = (I / 32 + 1) / 2, pw = PERSIST_THREADS / 64;
+    int ch = 1;
+    while (ch < 8 && np > ch * pw) ch *= 2;
+    return ch;
+}
 
 }  // namespace lq8

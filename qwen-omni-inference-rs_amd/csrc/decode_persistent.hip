@@ -1,16 +1,19 @@
 // decode_persistent.hip -- greedy batch-1 Qwen3 decode as one persistent,
 // cooperatively launched kernel: every decode step of a generate() call --
 // all layers, the lm_head and the greedy pick -- with no kernel boundary in
-// between.
+// between.  One workgroup of 512 threads (8 waves) per CU.
 //
-// Work of one step (position pos), per layer:
-//   P1  RmsNorm(h) + q|k|v GEMV, one 16-row tile per item
-//   P2  attention, one (kv head, 64-position segment) per item; the last of
-//       a kv head's segment items to finish (an arrival counter) combines the
-//       segments into the head group's attention output
-//   P3  o GEMV on the attention output + residual -> h2, one tile per item
-//   P4  RmsNorm(h2) + gate and up GEMV (tile i of each) -> silu(gate) * up
-//   P5  down GEMV + residual -> h, the next layer's input
+// Work of one step (position pos), per layer l (h_l the layer's input):
+//   P1  RmsNorm(h_l) + q|k|v GEMV, one 16-row tile per item
+//   P2  attention, one (kv head, 64-position segment) per item: per query
+//       head the segment's partials (o_c, m_c, l_c)
+//   P3  o GEMV, one (16-row tile, input chunk) per item: the chunk is csO
+//       blocks of the attention output (whole heads or parts of one), whose
+//       segments the item combines itself; the item's output is the tile's
+//       partial sum over its chunk
+//   P4  h2 = h_l + o (the chunk sums meet in the GEMV block tree), then
+//       RmsNorm(h2) + gate and up GEMV (tile i of each) -> silu(gate) * up
+//   P5  down GEMV over the whole intermediate input + residual h2 -> h_l+1
 // then P6: final RmsNorm and the lm_head, one wave per 16-row tile, each
 // workgroup keeping the greedy pick of its tiles; the next step starts with
 // every workgroup reducing the workgroups' picks to the token.  Item i of a
@@ -20,21 +23,27 @@
 // Hand-off between workgroups: every value passed on is one 8-byte word (f32
 // bits, then the step's tag), stored and loaded with agent-scope atomics
 // (written through to, and read from, the device-coherent level).  A reader
-// polls until each word it needs carries its step's tag, so the data is its
-// own flag.  Buffers are per layer; a buffer is written again only one step
-// later, by a producer whose inputs depend on the outputs of every reader of
-// the earlier value.  Tags grow across launches (the host keeps the count)
-// and zeroed buffers carry tag 0, which no step uses.
+// waits until each word it needs carries its step's tag, so the data is its
+// own flag: all of a thread's words are loaded at once; while some are not
+// there yet, one lane of the wave polls one of them and, when it lands, the
+// wave loads its missing words again at once (so the polling traffic is one
+// word per wave, and the fetch ends about one memory round trip after its
+// last word lands).  Buffers are per layer; a buffer is written again only
+// one step later, by a producer whose inputs depend on the outputs of every
+// reader of the earlier value.  Tags grow across launches (the host keeps the
+// count) and zeroed buffers carry tag 0, which no step uses.
 //
-// Weights do not depend on the step's data: a workgroup issues a phase's
-// weight loads (into registers) before it waits for the phase's inputs, so
-// the weight stream overlaps the hand-offs.
+// Weights do not depend on the step's data: a workgroup issues the weight
+// loads of its next phase's item (into registers) before it waits for the
+// current phase's inputs, so the weight stream overlaps the hand-offs.
 //
 // The arithmetic of every step is that of the separate kernels (gemv.hip,
-// model_kernels.hip): the GEMV block tree, the SUM64 RmsNorm and its bf16
-// roundings, the segment attention and its combine, silu(gate) * up, the
-// residual adds, the last-index greedy pick -- so tokens and logits equal
-// the graph-replayed path's bit for bit.
+// model_kernels.hip): the GEMV block tree (an input chunk of a power-of-two
+// block count aligned to its size is a subtree, and the chunk sums meet in
+// the tree's upper levels), the SUM64 RmsNorm and its bf16 roundings, the
+// segment attention and its combine, silu(gate) * up, the residual adds, the
+// last-index greedy pick -- so tokens and logits equal the graph-replayed
+// path's bit for bit.
 //
 // Waits are bounded: a word that does not arrive within SYNC_SPIN_LIMIT
 // polls sets the abort flag; every workgroup polls that flag while it waits
@@ -67,31 +76,34 @@ __device__ __forceinline__ void ptrace_mark(int w, int s, int l, int pt) {
 #endif
 
 constexpr int PT = PERSIST_THREADS;
-constexpr int PW = PT / 64;    // waves per workgroup
-// Largest GEMV inputs: hidden (q|k|v, gate/up, lm_head), the attention
-// output (o) and the intermediate size (down).
-constexpr int K_H_MAX = 1024, K_Q_MAX = 2048, K_I_MAX = 4096;
-// groups of two block pairs a wave holds for one tile of input length k
-constexpr int groups_per_wave(int k) { return ((k / 64 + 1) / 2 + PW - 1) / PW; }
-constexpr int NG_H = groups_per_wave(K_H_MAX), NG_Q = groups_per_wave(K_Q_MAX), NG_I = groups_per_wave(K_I_MAX);
-constexpr int SLOTS = 2 * NG_I;  // weight chunks a wave holds in registers
-constexpr int LM_MAX_NP = 16;  // lm_head tiles held per wave: up to 16 block pairs (hidden <= 1024)
-constexpr int GS_TILE = PW * NG_I * 16;  // group sums of one tile (floats)
-constexpr int CNT_STRIDE = 16;  // u32 per arrival counter (one per 64 bytes)
+constexpr int PW = PT / 64;     // waves per workgroup
+// hand-off words per thread of each fetch (units t + u * PT)
+constexpr int NW_ARG = (2 * 1024 + PT - 1) / PT;                   // the picks: 2 words per workgroup (<= 1024)
+constexpr int NW_H = (1024 + PT - 1) / PT;                         // a hidden vector (hidden <= 1024)
+constexpr int NW_QKV = ((ATT_MAX_GROUP + 2) * 128 + PT - 1) / PT;  // q of a kv head's group, k, v
+constexpr int NW_RES = PERSIST_FETCH;                             // h and the o chunk sums
+constexpr int NW_ACT = (4096 + 16 + PT - 1) / PT;                  // silu(gate) * up (<= 4096) and 16 rows of h2
+constexpr int NW_PART = 16;                                       // 8 segments x 2 words per run
+constexpr int CHH = 16 / PW;    // block pairs per wave group of a hidden-long tile (hidden <= 1024: <= 16 pairs)
+constexpr int LMU = 8;         // lm_head: block pairs per streamed unit of a tile
+constexpr int RSRC_RAW = 0x00020000;  // raw buffer resource, 32-bit data format
+constexpr int AUX_NT = 2;      // buffer load cache policy: nontemporal
 
-// A value the compiler must treat as produced here: per-thread index math
-// derived from it is recomputed in each loop iteration instead of being
-// hoisted to the kernel entry and held (spilled) across the whole kernel.
-__device__ __forceinline__ int opaque(int x) {
-    asm volatile("" : "+v"(x));
-    return x;
+// The argument block and the layer table, read through the constant address
+// space: the kernel never writes them, and so their fields are scalar loads
+// (uniform values in SGPRs) even after the kernel's own global stores.
+typedef __attribute__((address_space(4))) const PersistArgs CArgs;
+typedef __attribute__((address_space(4))) const PLayer CLayer;
+
+// The argument block as a value produced here: its fields are loaded again
+// (scalar cache) where they are used instead of being held in registers
+// across the whole kernel.
+__device__ __forceinline__ CArgs* opaque_args(const PersistArgs* p) {
+    CArgs* q = (CArgs*)p;
+    asm volatile("" : "+s"(q));
+    return q;
 }
-// The same for the (uniform) argument block: its fields are loaded again
-// (scalar cache) where they are used instead of being held in registers.
-__device__ __forceinline__ const PersistArgs* opaque_args(const PersistArgs* p) {
-    asm volatile("" : "+s"(p));
-    return p;
-}
+__device__ __forceinline__ CLayer& layer_of(CArgs& a, int l) { return ((CLayer*)a.layers)[l]; }
 
 __device__ __forceinline__ void tput(uint64_t* p, float v, unsigned tag) {
     __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -101,91 +113,90 @@ __device__ __forceinline__ uint64_t traw(const uint64_t* p) {
 }
 __device__ __forceinline__ bool tok_tag(uint64_t v, unsigned tag) { return (unsigned)(v >> 32) == tag; }
 
-// The value of a tagged word once it carries `tag`, given its first load v.
-// Gives up (0, *bad set) after the poll limit or when another workgroup has
-// raised the abort flag.
-__device__ __forceinline__ float twait(const uint64_t* p, uint64_t v, unsigned tag, unsigned* abort_flag,
-                                    volatile int* bad) {
+// The workgroup's abort mark as a wave-uniform value (all lanes read the same
+// LDS word; readfirstlane tells the compiler so, keeping the branches on it
+// uniform).
+__device__ __forceinline__ bool bad_now(volatile int* bad) { return __builtin_amdgcn_readfirstlane(*bad) != 0; }
+
+// One poll of a bounded wait: false to go on polling; true (with *bad set)
+// once the poll limit is reached or another workgroup raised the abort flag.
+__device__ __forceinline__ bool poll_stop(unsigned& spins, unsigned* abort_flag, volatile int* bad) {
+    if (*bad) return true;
+    ++spins;
+    if ((spins & 63) == 0 && sync_load(abort_flag) != 0) {
+        *bad = 1;
+        return true;
+    }
+    if (spins > SYNC_SPIN_LIMIT) {
+        __hip_atomic_fetch_or(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *bad = 1;
+        return true;
+    }
+    __builtin_amdgcn_s_sleep(8);
+    return false;
+}
+
+// *dst(t, u) = the value of the tagged word src(t, u) once it carries `tag`,
+// for every unit u < NW of thread t that ok(t, u) admits.  Every
+// thread of the workgroup calls it; a lds_sync() and a look at the abort mark
+// follow.  One batch of loads per round: the first round loads every word;
+// while some have not landed, one lane of the wave polls one of them and the
+// next round loads the wave's missing words again.
+template <int NW, typename Ok, typename Src, typename Dst>
+__device__ __forceinline__ void tfetch(unsigned tag, Ok ok, Src src, Dst dst, unsigned* abort_flag, volatile int* bad) {
+    unsigned pend = 0;
+    {
+        const int tid = tid_here();
+#pragma unroll
+        for (int u = 0; u < NW; u++)
+            if (ok(tid, u)) pend |= 1u << u;
+    }
     unsigned spins = 0;
-    while (!tok_tag(v, tag)) {
-        if (*bad) return 0.0f;
-        if ((++spins & 63) == 0 && sync_load(abort_flag) != 0) {
-            *bad = 1;
-            return 0.0f;
-        }
-        if (spins > SYNC_SPIN_LIMIT) {
-            __hip_atomic_fetch_or(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *bad = 1;
-            return 0.0f;
-        }
-        __builtin_amdgcn_s_sleep(1);
-        v = traw(p);
-    }
-    return __uint_as_float((unsigned)v);
-}
-
-__device__ __forceinline__ float tget(const uint64_t* p, unsigned tag, unsigned* abort_flag, volatile int* bad) {
-    const uint64_t v = traw(p);
-    return tok_tag(v, tag) ? __uint_as_float((unsigned)v) : twait(p, v, tag, abort_flag, bad);
-}
-
-// dst[i] = src[i] for i < n (tagged words), 8 loads per thread in flight.
-__device__ __forceinline__ void tfetch(const uint64_t* src, int n, unsigned tag, float* dst, unsigned* abort_flag,
-                                       volatile int* bad) {
-    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * PT) {
-        uint64_t v[8];
+    for (;;) {
+        // indices recomputed here (not held across the wait)
+        const int tid = tid_here(), lane = tid & 63;
+        uint64_t v[NW];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = traw(src + min(i0 + u * PT, n - 1));
+        for (int u = 0; u < NW; u++)
+            if ((pend >> u) & 1) v[u] = traw(src(tid, u));
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int i = i0 + u * PT;
-            if (i < n)
-                dst[i] = tok_tag(v[u], tag) ? __uint_as_float((unsigned)v[u]) : twait(src + i, v[u], tag, abort_flag, bad);
+        for (int u = 0; u < NW; u++) {
+            if (((pend >> u) & 1) && tok_tag(v[u], tag)) {
+                *dst(tid, u) = __uint_as_float((unsigned)v[u]);
+                pend &= ~(1u << u);
+            }
         }
+        const uint64_t waiting = __ballot(pend != 0);
+        if (waiting == 0) return;
+        if (lane == (int)__builtin_ctzll(waiting)) {
+            const uint64_t* p = src(tid, (int)__builtin_ctz(pend));
+            while (!tok_tag(traw(p), tag))
+                if (poll_stop(spins, abort_flag, bad)) break;
+        }
+        if (bad_now(bad)) return;
     }
 }
+
+// The linear case: words src[0, n) into dst[0, n).
+template <int NW>
+__device__ __forceinline__ void tfetch_lin(int n, unsigned tag, const uint64_t* src, float* dst, unsigned* abort_flag,
+                                           volatile int* bad) {
+    tfetch<NW>(tag, [&](int t, int u) { return t + u * PT < n; }, [&](int t, int u) { return src + t + u * PT; },
+               [&](int t, int u) { return dst + t + u * PT; }, abort_flag, bad);
+}
+
+// A 16-byte chunk of weight codes (global memory, streamed once: nontemporal)
+// and a scale, through global-address-space pointers.
+typedef __attribute__((address_space(1))) const u32x4 gchunk;
+typedef __attribute__((address_space(1))) const uint16_t gscale;
+__device__ __forceinline__ u32x4 chunk_load(const int8_t* p) { return __builtin_nontemporal_load((gchunk*)p); }
+__device__ __forceinline__ uint16_t scale_load(const uint16_t* p) { return *(gscale*)p; }
 
 // Element j of row `row` of a tiled Q8_0 weight, dequantized (exact).
 __device__ __forceinline__ float q8_elem(const int8_t* codes, const uint16_t* scales, int np, int row, int j) {
     const int tile = row / TILE_ROWS, r = row % TILE_ROWS, b = j >> 5, hf = (j >> 4) & 1;
     const float d = f16_bits_to_f32(scales[scale_off(tile, np, b, r)]);
     return d * (float)codes[code_off(tile, np, b, hf, r) + (j & 15)];
-}
-
-// ---- GEMV of one 16-row tile by the whole workgroup ----------------------------
-// The tile's np block pairs form G = ceil(np / 2) groups of two pairs; wave w
-// takes groups w, w + PW, ... (at most NG of them: np <= 2 * PW * NG), with
-// the chunk loads of its gi-th group held in slots S0 + 2 gi, S0 + 2 gi + 1.
-// The group sums meet in the pairwise tree over the groups: together the
-// block tree of the GEMV order (gemv_tiles), bit for bit.
-struct WRegs {
-    u32x4 c[SLOTS];
-    uint16_t d[SLOTS];
-};
-
-template <int S0, int NG>
-__device__ __forceinline__ void tile_load(const int8_t* codes, const uint16_t* scales, int np, int tile, WRegs& R) {
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int G = (np + 1) >> 1;
-    const int r = lane & 15, bsel = (lane >> 4) >> 1;
-    const int8_t* cb = codes + (size_t)tile * np * CHUNK_BYTES + lane * 16;
-    const uint16_t* sb = scales + (size_t)tile * 2 * np * 16 + bsel * 16 + r;
-    // groups are taken in pairs: a wave with an odd group count also loads
-    // (a copy of) the tile's last group as its last pair's partner
-    const int ngr = G > wave ? (G - wave + PW - 1) / PW : 0;
-#pragma unroll
-    for (int gi = 0; gi < NG; gi++) {
-        if (gi < ((ngr + 1) & ~1)) {
-            const int g = min(wave + gi * PW, G - 1);
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int p = min(2 * g + i, np - 1);
-                R.c[S0 + 2 * gi + i] = __builtin_nontemporal_load((const u32x4*)(cb + (size_t)p * CHUNK_BYTES));
-                R.d[S0 + 2 * gi + i] = sb[(size_t)p * 32];
-            }
-        }
-    }
 }
 
 // The 16 codes of a chunk, unpacked only where they are used: the empty asm
@@ -196,73 +207,127 @@ __device__ __forceinline__ float dot16_pinned(u32x4 c, const float* __restrict__
     return dot16(c, x);
 }
 
-// Four chunk dots at once: the GEMV's 16-term chains (each in its order,
-// from +0, as dot16), interleaved so that the four dependency chains overlap
-// -- with one wave per SIMD nothing else hides their latency.  The codes are
-// pinned here (see dot16_pinned).
-__device__ __forceinline__ void dot16x4_pinned(u32x4 c0, u32x4 c1, u32x4 c2, u32x4 c3, const float* x0,
-                                               const float* x1, const float* x2, const float* x3, float* out) {
-    asm volatile("" : "+v"(c0.x), "+v"(c0.y), "+v"(c0.z), "+v"(c0.w), "+v"(c1.x), "+v"(c1.y), "+v"(c1.z), "+v"(c1.w),
-                      "+v"(c2.x), "+v"(c2.y), "+v"(c2.z), "+v"(c2.w), "+v"(c3.x), "+v"(c3.y), "+v"(c3.z), "+v"(c3.w));
-    const uint32_t w[4][4] = {{c0.x, c0.y, c0.z, c0.w}, {c1.x, c1.y, c1.z, c1.w}, {c2.x, c2.y, c2.z, c2.w},
-                              {c3.x, c3.y, c3.z, c3.w}};
-    const float* x[4] = {x0, x1, x2, x3};
-    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+// N chunk dots at once: N of the GEMV's 16-term fmaf chains (each in its
+// order, from +0, as dot16), interleaved step by step so that the dependent
+// chains overlap (one chain alone waits on each fma's latency).
+template <int N>
+__device__ __forceinline__ void dot16xN(const u32x4* c, const float* const* x, float* out) {
+    uint32_t w[N][4];
+#pragma unroll
+    for (int k = 0; k < N; k++) {
+        u32x4 ck = c[k];
+        asm volatile("" : "+v"(ck.x), "+v"(ck.y), "+v"(ck.z), "+v"(ck.w));
+        w[k][0] = ck.x;
+        w[k][1] = ck.y;
+        w[k][2] = ck.z;
+        w[k][3] = ck.w;
+    }
+    float p[N];
+#pragma unroll
+    for (int k = 0; k < N; k++) p[k] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        float4 xv[4];
+        float4 xv[N];
 #pragma unroll
-        for (int k = 0; k < 4; k++) xv[k] = *(const float4*)(x[k] + 4 * i);
+        for (int k = 0; k < N; k++) xv[k] = *(const float4*)(x[k] + 4 * i);
 #pragma unroll
-        for (int k = 0; k < 4; k++) p[k] = fmaf((float)(int8_t)(w[k][i] & 0xFF), xv[k].x, p[k]);
+        for (int k = 0; k < N; k++) p[k] = fmaf((float)(int8_t)(w[k][i] & 0xFF), xv[k].x, p[k]);
 #pragma unroll
-        for (int k = 0; k < 4; k++) p[k] = fmaf((float)(int8_t)((w[k][i] >> 8) & 0xFF), xv[k].y, p[k]);
+        for (int k = 0; k < N; k++) p[k] = fmaf((float)(int8_t)((w[k][i] >> 8) & 0xFF), xv[k].y, p[k]);
 #pragma unroll
-        for (int k = 0; k < 4; k++) p[k] = fmaf((float)(int8_t)((w[k][i] >> 16) & 0xFF), xv[k].z, p[k]);
+        for (int k = 0; k < N; k++) p[k] = fmaf((float)(int8_t)((w[k][i] >> 16) & 0xFF), xv[k].z, p[k]);
 #pragma unroll
-        for (int k = 0; k < 4; k++) p[k] = fmaf((float)(int8_t)(w[k][i] >> 24), xv[k].w, p[k]);
+        for (int k = 0; k < N; k++) p[k] = fmaf((float)(int8_t)(w[k][i] >> 24), xv[k].w, p[k]);
     }
 #pragma unroll
-    for (int k = 0; k < 4; k++) out[k] = p[k];
+    for (int k = 0; k < N; k++) out[k] = p[k];
 }
 
-// Group sums of the wave's groups into gs[g * 16 + row], two groups (four
-// chunks) at a time.
-template <int S0, int NG>
-__device__ __forceinline__ void tile_dot(const WRegs& R, const float* xs, int np, int nb, float* gs) {
-    static_assert(NG % 2 == 0, "groups are taken in pairs");
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int G = (np + 1) >> 1;
-    const int part = lane >> 4, bsel = part >> 1, half = part & 1;
-    const int ngr = G > wave ? (G - wave + PW - 1) / PW : 0;  // the wave's groups
+// ---- GEMV work of one workgroup in a phase ------------------------------------
+// NTL (1 or 2) 16-row tiles t0, t1 of a tiled weight (np pairs, nb blocks per
+// row) over the block pairs [p0, p0 + npv), cut into G <= PW groups of CH
+// consecutive pairs (CH a power of two); wave w takes group w of each tile,
+// slot j * CH + i holding pair p0 + w * CH + i of tile j.  The group sums
+// meet in the pairwise tree over the groups: together the block tree of the
+// GEMV order (gemv_tiles), bit for bit.
+struct Job {
+    const int8_t* codes;
+    const uint16_t* scales;
+    int np, nb, t0, t1, p0, npv, G;
+};
+
+template <int NS>
+struct WRegs {
+    u32x4 c[NS];
+    uint16_t d[NS];
+};
+
+template <int CH>
+__device__ __forceinline__ Job make_job(const int8_t* codes, const uint16_t* scales, int np, int nb, int t0, int t1,
+                                        int p0, int npv) {
+    return Job{codes, scales, np, nb, t0, t1, p0, npv, (npv + CH - 1) / CH};
+}
+
+template <int NTL, int CH>
+__device__ __forceinline__ void job_load(const Job& J, WRegs<NTL * CH>& R) {
+    const int lane = tid_here() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
+    const int r = lane & 15, bsel = (lane >> 4) >> 1;
+    if (wave >= J.G) return;
 #pragma unroll
-    for (int gi = 0; gi < NG; gi += 2) {
-        if (gi < ngr) {
-            const bool two = gi + 1 < ngr;  // else the partner is the copy tile_load took (result unused)
-            const int g0 = wave + gi * PW, g1 = min(g0 + PW, G - 1);
-            const int p[4] = {min(2 * g0, np - 1), min(2 * g0 + 1, np - 1), min(2 * g1, np - 1), min(2 * g1 + 1, np - 1)};
-            constexpr int s0 = S0 + 0;
-            float h[4];
-            dot16x4_pinned(R.c[s0 + 2 * gi], R.c[s0 + 2 * gi + 1], R.c[s0 + 2 * gi + 2], R.c[s0 + 2 * gi + 3],
-                           xs + (2 * p[0] + bsel) * 32 + half * 16, xs + (2 * p[1] + bsel) * 32 + half * 16,
-                           xs + (2 * p[2] + bsel) * 32 + half * 16, xs + (2 * p[3] + bsel) * 32 + half * 16, h);
-            float v[4];
+    for (int j = 0; j < NTL; j++) {
+        const int tile = j ? J.t1 : J.t0;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const LanePair hh = lanes16(h[k]);
-                const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(R.d[s0 + 2 * gi + k]);
-                const LanePair vv = lanes32(vb);
-                v[k] = 2 * p[k] + 1 >= nb ? vv.lo : vv.lo + vv.hi;
-            }
-            const float vg0 = 2 * g0 + 1 < np ? v[0] + v[1] : v[0];
-            const float vg1 = 2 * g1 + 1 < np ? v[2] + v[3] : v[2];
-            if (lane < 16) {
-                gs[g0 * 16 + lane] = vg0;
-                if (two) gs[g1 * 16 + lane] = vg1;
-            }
-            __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < CH; i++) {
+            const int p = J.p0 + min(wave * CH + i, J.npv - 1);
+            R.c[j * CH + i] = chunk_load(J.codes + ((size_t)tile * J.np + p) * CHUNK_BYTES + lane * 16);
+            R.d[j * CH + i] = scale_load(J.scales + (size_t)tile * 2 * J.np * 16 + bsel * 16 + r + (size_t)p * 32);
         }
+    }
+}
+
+// Group sums into gs[(j * G + wave) * 16 + row]; xs holds the input of the
+// pair range (xs[(2 (p - p0) + b) * 32 + e] = x[(2 p + b) * 32 + e]).
+template <int NTL, int CH>
+__device__ __forceinline__ void job_dot(const Job& J, const WRegs<NTL * CH>& R, const float* xs, float* gs) {
+    constexpr int NS = NTL * CH, NI = NS < 4 ? NS : 4;  // chunks, interleaved NI at a time
+    const int lane = tid_here() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
+    const int part = lane >> 4, bsel = part >> 1, half = part & 1;
+    if (wave >= J.G) return;
+    const int cnt = min(CH, J.npv - wave * CH);  // valid pairs of the wave's group
+    float v[NS];
+#pragma unroll
+    for (int s0 = 0; s0 < NS; s0 += NI) {
+        const float* xp[NI];
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            const int i = (s0 + k) % CH, pr = min(wave * CH + i, J.npv - 1);
+            xp[k] = xs + (2 * pr + bsel) * 32 + half * 16;
+        }
+        float h[NI];
+        dot16xN<NI>(&R.c[s0], xp, h);
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            const int i = (s0 + k) % CH, pr = min(wave * CH + i, J.npv - 1);
+            // h0 + h1: the half-0 lane's sum (even 16-lane row) plus the half-1 lane's
+            const LanePair hh = lanes16(h[k]);
+            const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(R.d[s0 + k]);
+            // level s = 1 of the tree: block 2p (lanes 0..31) + block 2p + 1 (lanes 32..63)
+            const LanePair vv = lanes32(vb);
+            v[s0 + k] = 2 * (J.p0 + pr) + 1 >= J.nb ? vv.lo : vv.lo + vv.hi;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = 0; j < NTL; j++) {
+        // the tree levels inside a group (as gemv_tiles: s = 1, 2, ..., i + s < cnt)
+#pragma unroll
+        for (int s = 1; s < CH; s *= 2)
+#pragma unroll
+            for (int i = 0; i + s < CH; i += 2 * s)
+                if (i + s < cnt) v[j * CH + i] = v[j * CH + i] + v[j * CH + i + s];
+        if (lane < 16) gs[(j * J.G + wave) * 16 + lane] = v[j * CH];
     }
 }
 
@@ -272,7 +337,7 @@ __device__ __forceinline__ void tile_dot(const WRegs& R, const float* xs, int np
 // additions are the same ones in the same places as one lane per row doing
 // them in order.
 __device__ __forceinline__ float tile_final(float* gs, int G) {
-    const int lane = threadIdx.x & 63, col = lane & 15, q = lane >> 4;
+    const int lane = tid_here() & 63, col = lane & 15, q = lane >> 4;
     for (int s = 1; s < G; s *= 2) {
         for (int i = 2 * s * q; i + s < G; i += 8 * s) gs[i * 16 + col] = gs[i * 16 + col] + gs[(i + s) * 16 + col];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -282,241 +347,245 @@ __device__ __forceinline__ float tile_final(float* gs, int G) {
     return gs[col];
 }
 
+// The pairwise tree over n (<= PERSIST_NCH) chunk sums v[0 .. n).
+__device__ __forceinline__ float chunk_tree(float* v, int n) {
+#pragma unroll
+    for (int s = 1; s < PERSIST_NCH; s *= 2)
+#pragma unroll
+        for (int i = 0; i + s < PERSIST_NCH; i += 2 * s)
+            if (i + s < n) v[i] = v[i] + v[i + s];
+    return v[0];
+}
+
 // RmsNorm (src/rms_norm.rs:143-176) of xs[0, k) in place, in the order of
 // the GEMV's XS_RMSNORM staging: bf16 inputs; SUM64 of squares (wave 0);
 // inv = 1 / sqrt(sum / k + eps); out = bf16((v * inv) * bf16(w)).
 __device__ __forceinline__ void stage_rmsnorm(float* xs, int k, const float* w, float eps, float* red) {
-    const int tid = threadIdx.x;
+    const int tid = tid_here();
     for (int i = tid; i < k; i += PT) xs[i] = bf16_round(xs[i]);
-    __syncthreads();
+    lds_sync();
     if (tid < 64) {
         float acc = 0.0f;
         for (int i = tid; i < k; i += 64) acc = acc + xs[i] * xs[i];
         acc = wave_sum64(acc);
         if (tid == 0) red[0] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)k) + eps));
     }
-    __syncthreads();
+    lds_sync();
     const float inv = red[0];
     for (int i = tid; i < k; i += PT) xs[i] = bf16_round((xs[i] * inv) * bf16_round(w[i]));
-    __syncthreads();
+    lds_sync();
 }
 
 // zero the padding block of an odd block count (xs[k, 64 np))
 __device__ __forceinline__ void stage_pad(float* xs, int k, int np) {
-    for (int i = k + threadIdx.x; i < np * 64; i += PT) xs[i] = 0.0f;
+    for (int i = k + tid_here(); i < np * 64; i += PT) xs[i] = 0.0f;
 }
 
-// The attention output of kv head g's query heads (g G .. g G + G - 1) from
-// the partials (o_c[128], m_c, l_c) of its C segments, in segment order: per
-// head the running max m and denominator den with the coefficients
-// a_c = exp(m - m'), b_c = exp(m_c - m'), then per element
-// num = num * a_c + b_c * o_c and out = num / den -- the combine that the
-// separate kernels do in the o GEMV's input staging.  lds: 33 G floats.
-// Not inlined: only one workgroup per kv head runs it, and its registers stay
-// out of the attention phase's allocation.
-__device__ __noinline__ void combine_group(const uint64_t* partb, uint64_t* out, int g, int C, int NH, int G,
-                                              unsigned tag, float* lds, unsigned* abort_flag, volatile int* bad) {
-    const int tid = threadIdx.x;
-    float* mcl = lds;                  // [C][G][2]
-    float* coef = mcl + 2 * 8 * G;     // [C][G][2]
-    float* dens = coef + 2 * 8 * G;    // [G]
-    for (int q = tid; q < C * G; q += PT) {
-        const uint64_t* p = partb + ((size_t)(q / G) * NH + g * G + q % G) * ATT_PART_STRIDE;
-        mcl[2 * q] = tget(p + 128, tag, abort_flag, bad);
-        mcl[2 * q + 1] = tget(p + 129, tag, abort_flag, bad);
+// Greedy pick over the workgroup: (bv, bi) of every thread -> the maximum,
+// last index on ties, in every thread.  lds: PW floats + PW ints.
+__device__ __forceinline__ void wg_argmax(float& bv, int& bi, float* pv, int* pi) {
+    const int tid = tid_here(), lane = tid & 63, wave = tid >> 6;
+    argmax_step<32>(bv, bi);
+    argmax_step<16>(bv, bi);
+    argmax_step<8>(bv, bi);
+    argmax_step<4>(bv, bi);
+    argmax_step<2>(bv, bi);
+    argmax_step<1>(bv, bi);
+    if (lane == 0) {
+        pv[wave] = bv;
+        pi[wave] = bi;
     }
-    __syncthreads();
-    if (tid < G) {
-        float m = -__builtin_huge_valf(), den = 0.0f;
-        for (int c = 0; c < C; c++) {
-            const int q = c * G + tid;
-            const float mc = mcl[2 * q], lc = mcl[2 * q + 1];
-            const float mn = m > mc ? m : mc;
-            const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
-            coef[2 * q] = ea;
-            coef[2 * q + 1] = eb;
-            den = den * ea + eb * lc;
-            m = mn;
+    lds_sync();
+    bv = pv[0];
+    bi = pi[0];
+    for (int q = 1; q < PW; q++)
+        if (pv[q] > bv || (pv[q] == bv && pi[q] > bi)) {
+            bv = pv[q];
+            bi = pi[q];
         }
-        dens[tid] = den;
-    }
-    __syncthreads();
-    for (int i = tid; i < G * 128; i += PT) {
-        const int hh = i >> 7, d = i & 127;
-        uint64_t ro[8];  // C <= 8: every segment's word in flight together
-#pragma unroll
-        for (int c = 0; c < 8; c++)
-            ro[c] = traw(partb + ((size_t)min(c, C - 1) * NH + g * G + hh) * ATT_PART_STRIDE + d);
-        float num = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            if (c < C) {
-                const uint64_t* p = partb + ((size_t)c * NH + g * G + hh) * ATT_PART_STRIDE + d;
-                const float o = tok_tag(ro[c], tag) ? __uint_as_float((unsigned)ro[c]) : twait(p, ro[c], tag, abort_flag, bad);
-                num = num * coef[2 * (c * G + hh)] + coef[2 * (c * G + hh) + 1] * o;
-            }
-        }
-        tput(out + i, __fdiv_rn(num, dens[hh]), tag);
-    }
 }
 
 struct Dims {
-    int H, I, NH, NKV, G, QD, KD, QKV, npH, nbH, GH, npQ, nbQ, GQ, npI, nbI, GI;  // G*: groups of two pairs
+    int H, I, NH, NKV, G, QD, KD, QKV, npH, nbH, npQ, nbQ, npI, nbI, T1, TH, TI, T6;
 };
 
-__device__ __forceinline__ Dims dims_of(const PersistArgs& a) {
+__device__ __forceinline__ Dims dims_of(CArgs& a) {
     Dims d;
     d.H = a.H; d.I = a.I; d.NH = a.NH; d.NKV = a.NKV; d.G = a.NH / a.NKV;
     d.QD = a.NH * 128; d.KD = a.NKV * 128; d.QKV = d.QD + 2 * d.KD;
-    d.nbH = a.H >> 5; d.npH = (d.nbH + 1) >> 1; d.GH = (d.npH + 1) >> 1;
-    d.nbQ = d.QD >> 5; d.npQ = (d.nbQ + 1) >> 1; d.GQ = (d.npQ + 1) >> 1;
-    d.nbI = a.I >> 5; d.npI = (d.nbI + 1) >> 1; d.GI = (d.npI + 1) >> 1;
+    d.nbH = a.H >> 5; d.npH = (d.nbH + 1) >> 1;
+    d.nbQ = d.QD >> 5; d.npQ = (d.nbQ + 1) >> 1;
+    d.nbI = a.I >> 5; d.npI = (d.nbI + 1) >> 1;
+    d.T1 = (d.QKV + 15) / 16; d.TH = d.H / 16; d.TI = d.I / 16; d.T6 = (a.vocab + 15) / 16;
     return d;
 }
 
-// Per-phase locals, recomputed where used (from the opaque argument block):
-// the model's dimensions, the phase item counts, the per-layer strides and
-// the LDS layout -- region A (the staged GEMV input, or the attention
-// segment and then the combine's scratch), then the group sums and the
-// RmsNorm reduction.
-#define PHASE_LOCALS                                                                                        \
-    const Dims D = dims_of(a);                                                                              \
-    const int T1 = (D.QKV + 15) / 16, TH = (D.H + 15) / 16, TI = D.I / 16, T6 = (a.vocab + 15) / 16;         \
-    const int items2 = D.NKV * a.cmax;                                                                      \
-    const size_t kv_layer = (size_t)D.NKV * a.max_pos * 128;                                                \
-    const size_t part_layer = (size_t)a.cmax * D.NH * ATT_PART_STRIDE;                                      \
-    float* xs = sm;                                                                                         \
-    float* gs = sm + a.region_a;    /* [2][GS_TILE] */                                                      \
-    float* red = gs + 2 * GS_TILE;  /* [16] */                                                              \
-    float* qs = sm;                 /* attention: [G][128] */                                               \
-    float* kn = qs + D.G * 128;     /* [128] */                                                             \
-    float* vn = kn + 128;           /* [128] */                                                             \
-    float* sc = vn + 128;           /* [G][64] */                                                           \
-    float* mlc = sc + D.G * ATT_SEG; /* [G][2] */                                                           \
-    float* ks = sm + seg_ks_off(D.G); /* [64][KPAD], later the V rows [64][128] */                           \
-    (void)T1; (void)TH; (void)TI; (void)T6; (void)items2; (void)kv_layer; (void)part_layer; (void)xs;      \
-    (void)gs; (void)red; (void)qs; (void)kn; (void)vn; (void)sc; (void)mlc; (void)ks
+// Per-phase locals of layer l, derived again in every phase from the opaque
+// argument block (so that nothing of them is held across the phases): the
+// dimensions, the layer's weights, the LDS regions and the layer's hand-off
+// buffers.
+#define LAYER_LOCALS                                                                                       \
+    CArgs& a = *opaque_args(pa);                                                               \
+    const Dims D = dims_of(a);                                                                             \
+    const int tid = tid_here(), lane = tid & 63;                                                           \
+    const int pos = a.pos0 + s;                                                                            \
+    CLayer& Lw = layer_of(a, l);                                                                        \
+    float* xs = sm + a.xs_off;                                                                             \
+    float* gs = sm + a.gs_off;                                                                             \
+    float* red = sm + a.red_off;                                                                           \
+    uint64_t* qkvb = a.qkvb + (size_t)l * D.QKV;                                                           \
+    uint64_t* partb = a.partb + (size_t)l * a.cmax * D.NH * ATT_PART_STRIDE;                               \
+    uint64_t* resl = a.resb + (size_t)l * (1 + a.nchO) * D.H; /* [h_l | o chunk sums] */                   \
+    uint64_t* resn = resl + (size_t)(1 + a.nchO) * D.H;       /* the next layer's: h_l+1 at its head */   \
+    uint64_t* h2b = a.h2b + (size_t)l * D.H;                                                               \
+    uint64_t* actb = a.actb + (size_t)l * D.I;                                                             \
+    const int n3 = D.TH * a.nchO;                                                                          \
+    (void)tid; (void)lane; (void)pos; (void)Lw; (void)xs; (void)gs; (void)red; (void)qkvb; (void)partb;    \
+    (void)resl; (void)resn; (void)h2b; (void)actb; (void)n3
 
+// The jobs of the phases' items (CH5: pairs per group of the down tile).
+__device__ __forceinline__ Job job_qkv(CArgs& a, const Dims& D, CLayer& Lw, int t) {
+    return make_job<CHH>(Lw.qkv_c, Lw.qkv_s, D.npH, D.nbH, t, t, 0, D.npH);
+}
+__device__ __forceinline__ Job job_o(CArgs& a, const Dims& D, CLayer& Lw, int it) {
+    const int t = it / a.nchO, c = it - t * a.nchO, pc = a.csO >> 1;
+    const int p0 = c * pc;
+    return make_job<CHH>(Lw.o_c, Lw.o_s, D.npQ, D.nbQ, t, t, p0, min(pc, D.npQ - p0));
+}
+__device__ __forceinline__ Job job_gu(CArgs& a, const Dims& D, CLayer& Lw, int t) {
+    return make_job<CHH>(Lw.gu_c, Lw.gu_s, D.npH, D.nbH, t, D.TI + t, 0, D.npH);
+}
+template <int CH5>
+__device__ __forceinline__ Job job_dn(CArgs& a, const Dims& D, CLayer& Lw, int t) {
+    return make_job<CH5>(Lw.dn_c, Lw.dn_s, D.npI, D.nbI, t, t, 0, D.npI);
+}
+
+template <int CH5>
 __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __restrict__ pa) {
     extern __shared__ float sm[];
     __shared__ int bad_s;
-    __shared__ int last_s;
     __shared__ float pick_v[PW];
     __shared__ int pick_i[PW];
     volatile int* bad = &bad_s;
-    const PersistArgs& a = *opaque_args(pa);
-    const int P = gridDim.x, w = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (tid == 0) bad_s = 0;
-    __syncthreads();
+    const int P = gridDim.x, w = blockIdx.x;
+    if (threadIdx.x == 0) bad_s = 0;
+    lds_sync();
 
     uint32_t tok = 0;
-    for (int s = 0; s < a.steps; s++) {
+    for (int s = 0; s < pa->steps; s++) {
+        CArgs& a = *opaque_args(pa);
+        const Dims D = dims_of(a);
         const unsigned tag = a.tag0 + (unsigned)s;
-        const int pos = a.pos0 + s;
+        // layer 0's q|k|v weights, in flight while the token arrives
+        WRegs<CHH> R1;
+        if (w < D.T1) job_load<1, CHH>(job_qkv(a, D, layer_of(a, 0), w), R1);
         // ---- the step's input token: the previous step's greedy pick (last
         // index on ties) over the workgroups' picks; the first step's from
         // the previous kernel
         if (s == 0) {
             tok = *a.d_tok;
         } else {
-            float bv = -__builtin_huge_valf();
-            int bi = -1;
-            for (int q = tid; q < P; q += PT) {
-                const float v = tget(a.argb + 2 * q, tag - 1, a.abort_flag, bad);
-                const int j = (int)__float_as_uint(tget(a.argb + 2 * q + 1, tag - 1, a.abort_flag, bad));
-                if (v > bv || (v == bv && j > bi)) { bv = v; bi = j; }
-            }
-            argmax_step<32>(bv, bi);
-            argmax_step<16>(bv, bi);
-            argmax_step<8>(bv, bi);
-            argmax_step<4>(bv, bi);
-            argmax_step<2>(bv, bi);
-            argmax_step<1>(bv, bi);
-            if (lane == 0) { pick_v[wave] = bv; pick_i[wave] = bi; }
-            __syncthreads();
-            if (*bad) goto done;
-            bv = pick_v[0];
-            bi = pick_i[0];
-            for (int q = 1; q < PW; q++)
-                if (pick_v[q] > bv || (pick_v[q] == bv && pick_i[q] > bi)) { bv = pick_v[q]; bi = pick_i[q]; }
+            float* f = sm;
+            tfetch_lin<NW_ARG>(2 * P, tag - 1, a.argb, f, a.abort_flag, bad);
+            lds_sync();
+            if (bad_now(bad)) goto done;
+            const int tid = tid_here();
+            float bv = tid < P ? f[2 * tid] : -__builtin_huge_valf();
+            int bi = tid < P ? (int)__float_as_uint(f[2 * tid + 1]) : -1;
+            wg_argmax(bv, bi, pick_v, pick_i);
             const uint32_t picked = (uint32_t)(bi < 0 ? 0 : bi);
             if (w == 0 && tid == 0) a.tokens_out[a.step0 + s - 1] = picked;
             tok = a.feed_first ? a.tokens_out[0] : picked;
-            __syncthreads();  // pick_v / pick_i are read before the next step writes them
+            lds_sync();  // f, pick_v, pick_i are read before they are written again
         }
 
         for (int l = 0; l < pa->L; l++) {
-            const PersistArgs& a = *opaque_args(pa);
-            const int tid = opaque((int)threadIdx.x), lane = tid & 63;
-            PHASE_LOCALS;
-            const PLayer Lw = a.layers[l];
-            uint64_t* qkvb = a.qkvb + (size_t)l * D.QKV;
-            uint64_t* partb = a.partb + (size_t)l * part_layer;
-            uint64_t* attnb = a.attnb + (size_t)l * D.QD;
-            unsigned* cntb = a.cntb + (size_t)l * D.NKV * CNT_STRIDE;
-            uint64_t* h2b = a.h2b + (size_t)l * D.H;
-            uint64_t* actb = a.actb + (size_t)l * D.I;
-            uint64_t* hb = a.hb + (size_t)l * D.H;
-            const uint64_t* hin = l > 0 ? a.hb + (size_t)(l - 1) * D.H : nullptr;  // layer input (else the embedding)
-            float* Kl = a.kc + l * kv_layer;
-            float* Vl = a.vc + l * kv_layer;
-
-            // ---- P1: RmsNorm(h) + q|k|v tiles
-            if (w < T1) {
+            // ---- P1: h_l, RmsNorm + q|k|v tiles
+            if (w < dims_of(*opaque_args(pa)).T1) {
+                LAYER_LOCALS;
                 PTRACE(LQ8_PT_P1_START);
-                WRegs R;
-                tile_load<0, NG_H>(Lw.qkv_c, Lw.qkv_s, D.npH, w, R);
-                if (hin) tfetch(hin, D.H, tag, xs, a.abort_flag, bad);
-                else
-                    for (int j = tid; j < D.H; j += PT) xs[j] = q8_elem(a.emb_c, a.emb_s, D.npH, (int)tok, j);
+                if (l > 0) {
+                    tfetch_lin<NW_H>(D.H, tag, resl, xs, a.abort_flag, bad);
+                } else {
+                    // the embedding row (src/embedding.rs), published as h_0
+                    const int n1 = min(D.T1, P);
+                    for (int j = tid; j < D.H; j += PT) {
+                        const float e = q8_elem(a.emb_c, a.emb_s, D.npH, (int)tok, j);
+                        xs[j] = e;
+                        if (j % n1 == w) tput(resl + j, e, tag);
+                    }
+                }
                 stage_pad(xs, D.H, D.npH);
-                __syncthreads();
-                if (*bad) goto done;
+                lds_sync();
+                if (bad_now(bad)) goto done;
                 stage_rmsnorm(xs, D.H, Lw.in_norm, a.eps, red);
                 PTRACE(LQ8_PT_P1_NORMED);
-                for (int t = w; t < T1; t += P) {
-                    if (t != w) tile_load<0, NG_H>(Lw.qkv_c, Lw.qkv_s, D.npH, t, R);
-                    tile_dot<0, NG_H>(R, xs, D.npH, D.nbH, gs);
-                    __syncthreads();
+                for (int t = w; t < D.T1; t += P) {
+                    const Job J = job_qkv(a, D, Lw, t);
+                    if (t != w) job_load<1, CHH>(J, R1);
+                    job_dot<1, CHH>(J, R1, xs, gs);
+                    lds_sync();
                     if (tid < 64) {
-                        const float y = tile_final(gs, D.GH);
+                        const float y = tile_final(gs, J.G);
                         const int row = t * 16 + tid;
                         if (tid < 16 && row < D.QKV) tput(qkvb + row, y, tag);
                     }
-                    __syncthreads();
+                    lds_sync();
                 }
+            }
+
+            // the o tile's weights, in flight through the attention phase
+            WRegs<CHH> R3;
+            {
+                LAYER_LOCALS;
+                if (w < n3) job_load<1, CHH>(job_o(a, D, Lw, w), R3);
             }
 
             // ---- P2: attention per (kv head, segment)
             PTRACE(LQ8_PT_P2_START);
             {
-                const int L1 = pos + 1, C = (L1 + ATT_SEG - 1) / ATT_SEG;
+                LAYER_LOCALS;
+                const int L1 = pos + 1, C = (L1 + ATT_SEG - 1) / ATT_SEG, G = D.G;
+                const int items2 = D.NKV * a.cmax;
+                float* qs = sm;                   // [G][128]
+                float* kn = qs + G * 128;         // [128]
+                float* vn = kn + 128;             // [128]
+                float* sc = vn + 128;             // [G][64]
+                float* mlc = sc + G * ATT_SEG;    // [G][2]
+                float* ks = sm + seg_ks_off(G);   // [64][KPAD], later the V rows [64][128]
+                float* qraw = ks;                 // the fetched q (G heads), k, v: [G + 2][128]
                 for (int it = w; it < items2; it += P) {
                     const int g = it / a.cmax, c = it % a.cmax;
                     if (c >= C) continue;
                     const int js = c * ATT_SEG, nj = min(ATT_SEG, L1 - js);
                     const bool last = c == C - 1;
                     const int newrow = last ? pos - js : -1;
-                    float* Kc = Kl + (size_t)g * a.max_pos * 128;
-                    float* Vc = Vl + (size_t)g * a.max_pos * 128;
+                    float* Kc = a.kc + l * (size_t)D.NKV * a.max_pos * 128 + (size_t)g * a.max_pos * 128;
+                    float* Vc = a.vc + l * (size_t)D.NKV * a.max_pos * 128 + (size_t)g * a.max_pos * 128;
                     float4 kreg[ATT_SEG * 32 / PT], vreg[ATT_SEG * 32 / PT];
                     seg_load<PT, true>(Kc, Vc, js, nj, kreg, vreg);
+                    // q of the group's heads; k and v only for the segment holding the position
+                    const int nq = (last ? G + 2 : G) * 128;
+                    tfetch<NW_QKV>(tag, [&](int tt, int u) { return tt + u * PT < nq; },
+                           [&](int tt, int u) {
+                               const int i = tt + u * PT, t = i >> 7, e = i & 127;
+                               return (const uint64_t*)qkvb +
+                                      (t < G ? (g * G + t) * 128 : D.QD + (t == G ? 0 : D.KD) + g * 128) + e;
+                           },
+                           [&](int tt, int u) { return qraw + tt + u * PT; }, a.abort_flag, bad);
+                    lds_sync();
+                    if (bad_now(bad)) goto done;
+                    PTRACE(LQ8_PT_P2_QKV_IN);
                     const float* cs = a.cos_t + (size_t)pos * 64;
                     const float* sn = a.sin_t + (size_t)pos * 64;
-                    for (int t = wave; t < D.G + 2; t += PW) {
-                        if (t >= D.G && !last) continue;
-                        const uint64_t* src = t < D.G ? qkvb + (g * D.G + t) * 128
-                                                      : qkvb + D.QD + (t == D.G ? 0 : D.KD) + g * 128;
-                        const uint64_t r0 = traw(src + lane), r1 = traw(src + lane + 64);
-                        const float x0 = tok_tag(r0, tag) ? __uint_as_float((unsigned)r0)
-                                                          : twait(src + lane, r0, tag, a.abort_flag, bad);
-                        const float x1 = tok_tag(r1, tag) ? __uint_as_float((unsigned)r1)
-                                                          : twait(src + lane + 64, r1, tag, a.abort_flag, bad);
-                        if (t < D.G) {
+                    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+                    for (int t = wave; t < G + 2; t += PW) {
+                        if (t >= G && !last) continue;
+                        const float x0 = qraw[t * 128 + lane], x1 = qraw[t * 128 + lane + 64];
+                        if (t < G) {
                             head_norm_rope_vals(x0, x1, Lw.q_norm[lane], Lw.q_norm[lane + 64], cs, sn, a.eps,
                                                 qs + t * 128);
-                        } else if (t == D.G) {
+                        } else if (t == G) {
                             head_norm_rope_vals(x0, x1, Lw.k_norm[lane], Lw.k_norm[lane + 64], cs, sn, a.eps, kn);
                             float* kr = Kc + (size_t)pos * 128;
                             kr[lane] = kn[lane];
@@ -529,120 +598,182 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                             vr[lane + 64] = x1;
                         }
                     }
-                    __syncthreads();
-                    if (*bad) goto done;
-                    PTRACE(LQ8_PT_P2_QKV_IN);
-                    seg_scores<PT, true>(kreg, nj, newrow, kn, qs, D.G, a.scale, ks, sc, mlc);
-                    __syncthreads();
+                    lds_sync();
+                    seg_scores<PT, true, true>(kreg, nj, newrow, kn, qs, G, a.scale, ks, sc, mlc);
+                    lds_sync();
                     PTRACE(LQ8_PT_P2_SCORES);
                     seg_stage_v<PT, true>(vreg, nj, newrow, vn, ks);
-                    __syncthreads();
-                    for (int t = tid; t < D.G * 128; t += PT) {
+                    lds_sync();
+                    for (int t = tid; t < G * 128; t += PT) {
                         const int h = t >> 7, d = t & 127;
                         const float o = pv_chain(sc + h * ATT_SEG, ks, d, nj);
-                        uint64_t* p = partb + ((size_t)c * D.NH + g * D.G + h) * ATT_PART_STRIDE;
+                        uint64_t* p = partb + ((size_t)c * D.NH + g * G + h) * ATT_PART_STRIDE;
                         tput(p + d, o, tag);
                         if (d == 0) {
                             tput(p + 128, mlc[2 * h], tag);
                             tput(p + 129, mlc[2 * h + 1], tag);
                         }
                     }
-                    // every partial of the item is stored (write-through) before
-                    // the item arrives at kv head g's counter; the C-th arrival
-                    // resets the counter for the next step and combines
                     PTRACE(LQ8_PT_P2_PARTIALS);
-                    __builtin_amdgcn_s_waitcnt(0);
-                    __syncthreads();
-                    if (tid == 0) {
-                        unsigned* cn = cntb + (size_t)g * CNT_STRIDE;
-                        const bool lastc = sync_add(cn, 1u) + 1 == (unsigned)C;
-                        if (lastc) {
-                            sync_store(cn, 0u);
-                            __builtin_amdgcn_s_waitcnt(0);  // the reset lands before the output is published
-                        }
-                        last_s = lastc ? 1 : 0;
-                    }
-                    __syncthreads();
-                    if (last_s) combine_group(partb, attnb + (size_t)g * D.G * 128, g, C, D.NH, D.G, tag, sm,
-                                              a.abort_flag, bad);
-                    __syncthreads();
+                    lds_sync();
                 }
             }
 
-            // ---- P3: o tile on the attention output, + residual -> h2
+            // ---- P3: o tile over one input chunk (the attention output of
+            // its heads, combined from the segment partials) -> chunk sums
             PTRACE(LQ8_PT_P3_START);
-            for (int t = w; t < TH; t += P) {
-                WRegs R;
-                tile_load<0, NG_Q>(Lw.o_c, Lw.o_s, D.npQ, t, R);
-                const int row = t * 16 + tid;
-                uint64_t rres = 0;  // the residual word, loaded early
-                if (tid < 16 && row < D.H && hin) rres = traw(hin + row);
-                tfetch(attnb, D.QD, tag, xs, a.abort_flag, bad);
-                stage_pad(xs, D.QD, D.npQ);
-                __syncthreads();
-                if (*bad) goto done;
-                PTRACE(LQ8_PT_P3_STAGED);
-                tile_dot<0, NG_Q>(R, xs, D.npQ, D.nbQ, gs);
-                __syncthreads();
-                if (tid < 64) {
-                    const float acc = tile_final(gs, D.GQ);
-                    if (tid < 16 && row < D.H) {
-                        const float res = hin ? (tok_tag(rres, tag) ? __uint_as_float((unsigned)rres)
-                                                                    : twait(hin + row, rres, tag, a.abort_flag, bad))
-                                              : q8_elem(a.emb_c, a.emb_s, D.npH, (int)tok, row);
-                        tput(h2b + row, res + acc, tag);
+            {
+                LAYER_LOCALS;
+                const int L1 = pos + 1, C = (L1 + ATT_SEG - 1) / ATT_SEG;
+                for (int it = w; it < n3; it += P) {
+                    const Job J = job_o(a, D, Lw, it);
+                    if (it != w) job_load<1, CHH>(J, R3);
+                    const int t = it / a.nchO, c = it - t * a.nchO;
+                    const int i0 = J.p0 * 64, rng = min(J.npv * 64, D.QD - i0);
+                    const int hA = i0 >> 7, nh = ((i0 + rng - 1) >> 7) - hA + 1;
+                    // the partials of the chunk's heads: per segment one run of
+                    // nh * ATT_PART_STRIDE words (o_c[128], m_c, l_c, 2 unused)
+                    const int R = nh * ATT_PART_STRIDE;
+                    float* pr = sm;                  // [C][R] the runs
+                    float* coef = pr + C * R;        // [C][nh][2]: a_c, b_c
+                    float* dens = coef + 2 * C * nh; // [nh]
+                    const uint64_t* run0 = partb + (size_t)hA * ATT_PART_STRIDE;
+                    const size_t seg_words = (size_t)D.NH * ATT_PART_STRIDE;
+                    // thread t: words t and t + PT of every segment's run
+                    tfetch<NW_PART>(tag,
+                           [&](int tt, int u) {
+                               const int k = tt + (u & 1) * PT;
+                               return (u >> 1) < C && k < R && k % ATT_PART_STRIDE < 130;
+                           },
+                           [&](int tt, int u) { return run0 + (size_t)(u >> 1) * seg_words + tt + (u & 1) * PT; },
+                           [&](int tt, int u) { return pr + (u >> 1) * R + tt + (u & 1) * PT; }, a.abort_flag, bad);
+                    lds_sync();
+                    if (bad_now(bad)) goto done;
+                    PTRACE(LQ8_PT_P3_STAGED);
+                    // the combine of the o GEMV's XS_ATTN staging: per head, in
+                    // segment order, m' = max(m, m_c), a_c = exp(m - m'),
+                    // b_c = exp(m_c - m'), den = den a_c + b_c l_c; per element
+                    // num = num a_c + b_c o_c, x = num / den
+                    if (tid < nh) {
+                        float m = -__builtin_huge_valf(), den = 0.0f;
+                        for (int cc = 0; cc < C; cc++) {
+                            const int q = cc * nh + tid;
+                            const float mc = pr[cc * R + tid * ATT_PART_STRIDE + 128];
+                            const float lc = pr[cc * R + tid * ATT_PART_STRIDE + 129];
+                            const float mn = m > mc ? m : mc;
+                            const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
+                            coef[2 * q] = ea;
+                            coef[2 * q + 1] = eb;
+                            den = den * ea + eb * lc;
+                            m = mn;
+                        }
+                        dens[tid] = den;
                     }
+                    lds_sync();
+                    for (int k = tid; k < rng; k += PT) {
+                        const int hh = ((i0 + k) >> 7) - hA;
+                        float num = 0.0f;
+                        for (int cc = 0; cc < C; cc++)
+                            num = num * coef[2 * (cc * nh + hh)] + coef[2 * (cc * nh + hh) + 1] *
+                                                                            pr[cc * R + hh * ATT_PART_STRIDE + ((i0 + k) & 127)];
+                        xs[k] = __fdiv_rn(num, dens[hh]);
+                    }
+                    stage_pad(xs, rng, J.npv);
+                    lds_sync();
+                    job_dot<1, CHH>(J, R3, xs, gs);
+                    lds_sync();
+                    if (tid < 64) {
+                        const float y = tile_final(gs, J.G);
+                        if (tid < 16) tput(resl + (size_t)(1 + c) * D.H + t * 16 + tid, y, tag);
+                    }
+                    lds_sync();
                 }
-                __syncthreads();
             }
 
-            // ---- P4: RmsNorm(h2) + gate / up tile pair -> silu(gate) * up
+            // the gate|up and down weights, in flight through the hand-offs
+            WRegs<2 * CHH> R4;
+            WRegs<CH5> R5;
+            {
+                LAYER_LOCALS;
+                if (w < D.TI) job_load<2, CHH>(job_gu(a, D, Lw, w), R4);
+                if (w < D.TH) job_load<1, CH5>(job_dn<CH5>(a, D, Lw, w), R5);
+            }
+
+            // ---- P4: h2 = h_l + o, RmsNorm(h2) + gate / up tile pair -> silu(gate) * up
+            {
+                LAYER_LOCALS;
             PTRACE(LQ8_PT_P4_START);
-            for (int t = w; t < TI; t += P) {
-                WRegs R;
-                tile_load<0, NG_H>(Lw.gu_c, Lw.gu_s, D.npH, t, R);
-                tile_load<2 * NG_H, NG_H>(Lw.gu_c, Lw.gu_s, D.npH, TI + t, R);
-                tfetch(h2b, D.H, tag, xs, a.abort_flag, bad);
-                stage_pad(xs, D.H, D.npH);
-                __syncthreads();
-                if (*bad) goto done;
-                PTRACE(LQ8_PT_P4_STAGED);
-                stage_rmsnorm(xs, D.H, Lw.post_norm, a.eps, red);
-                tile_dot<0, NG_H>(R, xs, D.npH, D.nbH, gs);
-                tile_dot<2 * NG_H, NG_H>(R, xs, D.npH, D.nbH, gs + GS_TILE);
-                __syncthreads();
+            for (int t = w; t < D.TI; t += P) {
+                const Job J = job_gu(a, D, Lw, t);
+                if (t != w) job_load<2, CHH>(J, R4);
+                float* f = sm;  // [1 + nchO][H]
+                if (t == w) {
+                    tfetch_lin<NW_RES>((1 + a.nchO) * D.H, tag, resl, f, a.abort_flag, bad);
+                    lds_sync();
+                    if (bad_now(bad)) goto done;
+                    PTRACE(LQ8_PT_P4_STAGED);
+                    const int n4 = min(D.TI, P);
+                    for (int r = tid; r < D.H; r += PT) {
+                        float v[PERSIST_NCH];
+#pragma unroll
+                        for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchO ? f[(1 + q) * D.H + r] : 0.0f;
+                        const float h2 = f[r] + chunk_tree(v, a.nchO);
+                        xs[r] = h2;
+                        if (r % n4 == w) tput(h2b + r, h2, tag);
+                    }
+                    stage_pad(xs, D.H, D.npH);
+                    lds_sync();
+                    stage_rmsnorm(xs, D.H, Lw.post_norm, a.eps, red);
+                }
+                job_dot<2, CHH>(J, R4, xs, gs);
+                lds_sync();
                 if (tid < 64) {
-                    const float g = tile_final(gs, D.GH), u = tile_final(gs + GS_TILE, D.GH);
+                    const float g = tile_final(gs, J.G), u = tile_final(gs + J.G * 16, J.G);
                     if (tid < 16) tput(actb + t * 16 + tid, silu_mul(g, u), tag);
                 }
-                __syncthreads();
+                lds_sync();
             }
 
-            // ---- P5: down tile + residual -> h
+            }
+
+            // the next layer's q|k|v weights, in flight through the down projection
+            {
+                LAYER_LOCALS;
+                if (l + 1 < a.L && w < D.T1) job_load<1, CHH>(job_qkv(a, D, layer_of(a, l + 1), w), R1);
+            }
+
+            // ---- P5: down tile + residual h2 -> h_l+1
+            {
+                LAYER_LOCALS;
             PTRACE(LQ8_PT_P5_START);
-            for (int t = w; t < TH; t += P) {
-                WRegs R;
-                tile_load<0, NG_I>(Lw.dn_c, Lw.dn_s, D.npI, t, R);
-                const int row = t * 16 + tid;
-                uint64_t rres = 0;
-                if (tid < 16 && row < D.H) rres = traw(h2b + row);
-                tfetch(actb, D.I, tag, xs, a.abort_flag, bad);
+            for (int t = w; t < D.TH; t += P) {
+                const Job J = job_dn<CH5>(a, D, Lw, t);
+                if (t != w) job_load<1, CH5>(J, R5);
+                float* hr = sm;  // [16] the tile's rows of h2
+                const int nI = D.I;
+                tfetch<NW_ACT>(tag, [&](int tt, int u) { return tt + u * PT < nI + 16; },
+                       [&](int tt, int u) {
+                           const int i = tt + u * PT;
+                           return i < nI ? (const uint64_t*)actb + i : (const uint64_t*)h2b + t * 16 + (i - nI);
+                       },
+                       [&](int tt, int u) {
+                           const int i = tt + u * PT;
+                           return i < nI ? xs + i : hr + (i - nI);
+                       },
+                       a.abort_flag, bad);
                 stage_pad(xs, D.I, D.npI);
-                __syncthreads();
-                if (*bad) goto done;
+                lds_sync();
+                if (bad_now(bad)) goto done;
                 PTRACE(LQ8_PT_P5_STAGED);
-                tile_dot<0, NG_I>(R, xs, D.npI, D.nbI, gs);
-                __syncthreads();
+                job_dot<1, CH5>(J, R5, xs, gs);
+                lds_sync();
                 if (tid < 64) {
-                    const float acc = tile_final(gs, D.GI);
-                    if (tid < 16 && row < D.H) {
-                        const float res = tok_tag(rres, tag) ? __uint_as_float((unsigned)rres)
-                                                             : twait(h2b + row, rres, tag, a.abort_flag, bad);
-                        tput(hb + row, res + acc, tag);
-                    }
+                    const float acc = tile_final(gs, J.G);
+                    if (tid < 16) tput(resn + t * 16 + tid, hr[tid] + acc, tag);
                 }
-                __syncthreads();
+                lds_sync();
                 PTRACE(LQ8_PT_P5_DONE);
+            }
             }
         }
 
@@ -650,74 +781,109 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
         {
             [[maybe_unused]] const int l = 0;  // the P6 marks sit in layer 0's row
             PTRACE(LQ8_PT_P6_START);
-            const PersistArgs& a = *opaque_args(pa);
-            const int tid = opaque((int)threadIdx.x), lane = tid & 63;
-            PHASE_LOCALS;
+            CArgs& a = *opaque_args(pa);
+            const Dims D = dims_of(a);
+            const int tid = tid_here(), lane = tid & 63;
+            const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+            float* xs = sm + a.xs_off;
+            float* red = sm + a.red_off;
             const int t0 = w * PW + wave, tstride = P * PW;
             const int np = D.npH, nb = D.nbH;
-            const int part = lane >> 4, bsel = part >> 1, half = part & 1, r = lane & 15;
-            u32x4 cv[LM_MAX_NP];
-            uint16_t dv[LM_MAX_NP];
-            auto load_tile = [&](int t) {
-                const int8_t* cb = a.emb_c + (size_t)t * np * CHUNK_BYTES + lane * 16;
-                const uint16_t* sb = a.emb_s + (size_t)t * 2 * np * 16 + bsel * 16 + r;
+            const int r = lane & 15;
+            // a wave streams its tiles in units of LMU block pairs, the next
+            // unit's loads in flight while the current one is summed (two
+            // register sets, A for the even units of a tile, B for the odd)
+            const int nq = (np + LMU - 1) / LMU;  // units per tile: 1 or 2
+            u32x4 cA[LMU], cB[LMU];
+            uint16_t dA[LMU], dB[LMU];
+            // buffer loads: one descriptor per table and a 32-bit lane offset,
+            // the tile and chunk offsets uniform (no per-chunk pointers)
+            const int tiles_alloc = (D.T6 + 1) & ~1;  // rows stored in multiples of 32
+            const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)a.emb_c, (short)0, (int)((size_t)tiles_alloc * np * CHUNK_BYTES), RSRC_RAW);
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)a.emb_s, (short)0, (int)((size_t)tiles_alloc * 2 * np * 16 * sizeof(uint16_t)), RSRC_RAW);
+            auto load_u = [&](int t, int q, u32x4* c, uint16_t* d) {
+                const int ln = tid_here() & 63;
+                const int vo = ln * 16, vs = (((ln >> 4) >> 1) * 16 + (ln & 15)) * 2;
 #pragma unroll
-                for (int p = 0; p < LM_MAX_NP; p++) {
-                    if (p < np) {
-                        cv[p] = __builtin_nontemporal_load((const u32x4*)(cb + (size_t)p * CHUNK_BYTES));
-                        dv[p] = sb[(size_t)p * 32];
-                    }
+                for (int i = 0; i < LMU; i++) {
+                    const int p = min(q * LMU + i, np - 1);
+                    c[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         rc, vo, (t * np + p) * CHUNK_BYTES, AUX_NT));
+                    d[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, vs, (t * 2 * np + 2 * p) * 32, 0);
                 }
             };
-            if (t0 < T6) load_tile(t0);
-            tfetch(a.hb + (size_t)(a.L - 1) * D.H, D.H, tag, xs, a.abort_flag, bad);
+            // the unit's pair values, summed by the tree levels inside the unit
+            auto dot_u = [&](int q, const u32x4* c, const uint16_t* d) {
+                const int ln = tid_here() & 63, bs = (ln >> 4) >> 1, hf = (ln >> 4) & 1;
+                float v[LMU];
+#pragma unroll
+                for (int i0 = 0; i0 < LMU; i0 += 4) {
+                    const float* xp[4];
+#pragma unroll
+                    for (int k = 0; k < 4; k++) xp[k] = xs + (2 * min(q * LMU + i0 + k, np - 1) + bs) * 32 + hf * 16;
+                    float h[4];
+                    dot16xN<4>(c + i0, xp, h);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const int pc = min(q * LMU + i0 + k, np - 1);
+                        const LanePair hh = lanes16(h[k]);
+                        const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(d[i0 + k]);
+                        const LanePair vv = lanes32(vb);
+                        v[i0 + k] = 2 * pc + 1 >= nb ? vv.lo : vv.lo + vv.hi;
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                const int cnt = np - q * LMU;
+#pragma unroll
+                for (int s2 = 1; s2 < LMU; s2 *= 2)
+#pragma unroll
+                    for (int i = 0; i + s2 < LMU; i += 2 * s2)
+                        if (i + s2 < cnt) v[i] = v[i] + v[i + s2];
+                return v[0];
+            };
+            if (t0 < D.T6) load_u(t0, 0, cA, dA);
+            const uint64_t* hL = a.resb + (size_t)a.L * (1 + a.nchO) * D.H;
+            tfetch_lin<NW_H>(D.H, tag, hL, xs, a.abort_flag, bad);
             stage_pad(xs, D.H, np);
-            __syncthreads();
-            if (*bad) goto done;
+            lds_sync();
+            if (bad_now(bad)) goto done;
             stage_rmsnorm(xs, D.H, a.final_norm, a.eps, red);
             PTRACE(LQ8_PT_P6_NORMED);
             float bv = -__builtin_huge_valf();
             int bi = -1;
-            for (int t = t0; t < T6; t += tstride) {
-                float v[LM_MAX_NP];
-#pragma unroll
-                for (int p = 0; p < LM_MAX_NP; p++) {
-                    if (p < np) {
-                        const float h = dot16_pinned(cv[p], xs + (2 * p + bsel) * 32 + half * 16);
-                        const LanePair hh = lanes16(h);
-                        const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(dv[p]);
-                        const LanePair vv = lanes32(vb);
-                        v[p] = 2 * p + 1 >= nb ? vv.lo : vv.lo + vv.hi;
-                        if (p & 1) __builtin_amdgcn_sched_barrier(0);
-                    }
+            for (int t = t0; t < D.T6; t += tstride) {
+                const bool more = t + tstride < D.T6;
+                if (nq > 1) load_u(t, 1, cB, dB);
+                float v0 = dot_u(0, cA, dA);
+                if (more) load_u(t + tstride, 0, cA, dA);
+                if (nq > 1) {
+                    // the level joining the two units (pairs 0 and LMU)
+                    const float v1 = dot_u(1, cB, dB);
+                    v0 = v0 + v1;
                 }
-                if (t + tstride < T6) load_tile(t + tstride);  // the next tile while this one reduces
-#pragma unroll
-                for (int s2 = 1; s2 < LM_MAX_NP; s2 *= 2)
-#pragma unroll
-                    for (int i = 0; i + s2 < LM_MAX_NP; i += 2 * s2)
-                        if (i + s2 < np) v[i] = v[i] + v[i + s2];
                 const int row = t * 16 + r;
                 const bool valid = lane < 16 && row < a.vocab;
-                float tv = valid ? v[0] : -__builtin_huge_valf();
+                float tv = valid ? v0 : -__builtin_huge_valf();
                 int ti = valid ? row : -1;
                 argmax_step<8>(tv, ti);
                 argmax_step<4>(tv, ti);
                 argmax_step<2>(tv, ti);
                 argmax_step<1>(tv, ti);
-                if (tv > bv || (tv == bv && ti > bi)) { bv = tv; bi = ti; }
+                if (tv > bv || (tv == bv && ti > bi)) {
+                    bv = tv;
+                    bi = ti;
+                }
             }
             // lanes 0..15 hold the wave's pick (rows of lanes 16..63 were invalid)
-            if (lane == 0) { pick_v[wave] = bv; pick_i[wave] = bi; }
-            __syncthreads();
+            wg_argmax(bv, bi, pick_v, pick_i);
             if (tid == 0) {
-                float wv = pick_v[0];
-                int wi = pick_i[0];
-                for (int q = 1; q < PW; q++)
-                    if (pick_v[q] > wv || (pick_v[q] == wv && pick_i[q] > wi)) { wv = pick_v[q]; wi = pick_i[q]; }
-                tput(a.argb + 2 * w, wv, tag);
-                tput(a.argb + 2 * w + 1, __uint_as_float((unsigned)wi), tag);
+                tput(a.argb + 2 * w, bv, tag);
+                tput(a.argb + 2 * w + 1, __uint_as_float((unsigned)bi), tag);
             }
+            // the step's one fenced barrier: the workgroup's key/value cache
+            // stores of this step are visible to its waves' loads of the next
             __syncthreads();
             PTRACE(LQ8_PT_P6_DONE);
         }
@@ -725,25 +891,17 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
 
     // the last step's token, and the decode state for the next call
     if (w == 0) {
+        CArgs& a = *opaque_args(pa);
         const unsigned tag = a.tag0 + (unsigned)a.steps - 1;
-        float bv = -__builtin_huge_valf();
-        int bi = -1;
-        for (int q = tid; q < P; q += PT) {
-            const float v = tget(a.argb + 2 * q, tag, a.abort_flag, bad);
-            const int j = (int)__float_as_uint(tget(a.argb + 2 * q + 1, tag, a.abort_flag, bad));
-            if (v > bv || (v == bv && j > bi)) { bv = v; bi = j; }
-        }
-        argmax_step<32>(bv, bi);
-        argmax_step<16>(bv, bi);
-        argmax_step<8>(bv, bi);
-        argmax_step<4>(bv, bi);
-        argmax_step<2>(bv, bi);
-        argmax_step<1>(bv, bi);
-        if (lane == 0) { pick_v[wave] = bv; pick_i[wave] = bi; }
-        __syncthreads();
-        if (tid == 0 && !*bad) {
-            for (int q = 1; q < PW; q++)
-                if (pick_v[q] > bv || (pick_v[q] == bv && pick_i[q] > bi)) { bv = pick_v[q]; bi = pick_i[q]; }
+        float* f = sm;
+        tfetch_lin<NW_ARG>(2 * P, tag, a.argb, f, a.abort_flag, bad);
+        lds_sync();
+        if (bad_now(bad)) goto done;
+        const int tid = tid_here();
+        float bv = tid < P ? f[2 * tid] : -__builtin_huge_valf();
+        int bi = tid < P ? (int)__float_as_uint(f[2 * tid + 1]) : -1;
+        wg_argmax(bv, bi, pick_v, pick_i);
+        if (tid == 0) {
             const uint32_t picked = (uint32_t)(bi < 0 ? 0 : bi);
             a.tokens_out[a.step0 + a.steps - 1] = picked;
             *a.d_tok = picked;
@@ -757,39 +915,68 @@ done:
 
 }  // namespace
 
-bool persist_supported(const PersistShape& s, int num_cus) {
-    if (s.head_dim != 128 || s.NKV <= 0 || s.NH % s.NKV) return false;
+bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
+    if (s.head_dim != 128 || s.NKV <= 0 || s.NH % s.NKV || P <= 0) return false;
     const int G = s.NH / s.NKV;
     if (G > ATT_MAX_GROUP) return false;
-    // GEMV inputs within the groups a wave holds for a tile (hidden <= 1024
-    // also lets a wave hold a whole lm_head tile, 16 block pairs); the
-    // combine: up to 8 segments
-    if (s.H % 32 || s.H > K_H_MAX || s.I % 32 || s.I > K_I_MAX || s.NH * 128 > K_Q_MAX) return false;
-    if (s.max_pos > 8 * ATT_SEG || num_cus <= 0) return false;
-    return persist_smem_bytes(s) <= 64 * 1024;
+    // hidden <= 1024 lets a wave hold a whole q|k|v, gate/up or lm_head tile
+    // group in one slot and the lm_head tile (16 block pairs) in registers;
+    // intermediate <= 4096 keeps the down tile within 4 slots per wave; at
+    // most 8 segments (the combine and the fetches are sized for them)
+    if (s.H % 32 || s.H > 1024 || s.I % 32 || s.I > 4096 || s.NH * 128 > 2048) return false;
+    const int cmax = (s.max_pos + ATT_SEG - 1) / ATT_SEG;
+    if (cmax > 8) return false;
+    const int QD = s.NH * 128, nbQ = QD / 32, TH = s.H / 16;
+    const int cap = PERSIST_FETCH * PERSIST_THREADS;  // words one fetch holds
+    // o input chunks: the smallest power-of-two block count whose items fit
+    // the workgroups (or one chunk over the whole input)
+    int csO = 2;
+    auto nch_of = [&](int cs) { return (nbQ + cs - 1) / cs; };
+    while (csO < nbQ &&
+           (TH * nch_of(csO) > P || nch_of(csO) > PERSIST_NCH || (1 + nch_of(csO)) * s.H > cap))
+        csO *= 2;
+    const int nchO = nch_of(csO);
+    // a chunk's pairs fit one group per wave (CHH pairs each)
+    if (nchO > PERSIST_NCH || (1 + nchO) * s.H > cap || std::min(csO, nbQ) > 2 * CHH * PW) return false;
+    const int pairsO = (std::min(csO, nbQ) + 1) / 2;  // pairs of the widest chunk
+    const int rng = std::min(pairsO * 64, QD);
+    const int nhc = rng / 128 + 2;  // heads a chunk touches, at most
+    if (2 * cmax * nhc + cmax * rng > cap || s.I + 16 > cap || 2 * P > cap) return false;
+    PersistLayout L{};
+    L.csO = csO;
+    L.nchO = nchO;
+    int fr = std::max((1 + nchO) * s.H, 4 * cmax * nhc + cmax * rng + nhc);
+    fr = std::max(fr, 2 * P);
+    fr = std::max(fr, 16);
+    L.fr = (fr + 3) & ~3;
+    const int npH = (s.H / 32 + 1) / 2, npI = (s.I / 32 + 1) / 2;
+    const int xsz = std::max(std::max(npH, npI), pairsO) * 64;
+    L.xs_off = L.fr;
+    L.gs_off = L.xs_off + xsz;
+    L.red_off = L.gs_off + 2 * (PERSIST_THREADS / 64) * 16;
+    const int total = L.red_off + 16;
+    L.att_floats = seg_ks_off(G) + ATT_SEG * KPAD;
+    if ((G + 2) * 128 > ATT_SEG * KPAD) return false;
+    L.smem_bytes = std::max(total, L.att_floats) * (int)sizeof(float);
+    if (L.smem_bytes > 64 * 1024) return false;
+    const size_t Ls = 1;  // per layer; the host multiplies by the layer count
+    (void)Ls;
+    L.words = 0;
+    if (out) *out = L;
+    return true;
 }
 
-size_t persist_xs_floats(const PersistShape& s) {
-    const int k = std::max(s.H, std::max(s.NH * 128, s.I));
-    return (size_t)((k + 63) / 64 * 64 + 64);
-}
+bool persist_supported(const PersistShape& s, int num_cus) { return persist_layout(s, num_cus, nullptr); }
 
-size_t persist_region_a(const PersistShape& s) {
-    const int G = s.NH / s.NKV;
-    const size_t a1 = persist_xs_floats(s);
-    // the attention segment; the combine's scratch (33 G floats) reuses it
-    const size_t a2 = std::max((size_t)seg_ks_off(G) + (size_t)ATT_SEG * KPAD, (size_t)33 * G);
-    return (std::max(a1, a2) + 3) & ~(size_t)3;
-}
-
-size_t persist_smem_bytes(const PersistShape& s) { return (persist_region_a(s) + 2 * GS_TILE + 16) * sizeof(float); }
-
-lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg) {
+lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg, int ch5) {
     const PersistArgs* args = d_args;
     void* kargs[] = {&args};
     const size_t smem = (size_t)smem_bytes;
-    hipError_t e = hipLaunchCooperativeKernel((const void*)k_decode_persistent, dim3((unsigned)num_wg), dim3(PT),
-                                              kargs, smem, st);
+    const void* k = ch5 == 1   ? (const void*)k_decode_persistent<1>
+                    : ch5 == 2 ? (const void*)k_decode_persistent<2>
+                    : ch5 == 4 ? (const void*)k_decode_persistent<4>
+                               : (const void*)k_decode_persistent<8>;
+    hipError_t e = hipLaunchCooperativeKernel(k, dim3((unsigned)num_wg), dim3(PT), kargs, smem, st);
     if (e == hipErrorCooperativeLaunchTooLarge)
         return fail(LQ8_ERR_DEVICE, "persistent decode: the grid cannot be co-resident");
     if (e != hipSuccess) return hip_fail(e, "persistent decode launch");

@@ -287,6 +287,13 @@ __device__ __forceinline__ int tid_here() {
     return x;
 }
 
+// Workgroup barrier that orders LDS only: the wave waits for its own LDS and
+// scalar memory operations (lgkmcnt) and meets the others at s_barrier, but
+// not for its global stores (a __syncthreads() also waits for those, a whole
+// memory round trip for write-through stores).  The asm's memory clobber
+// keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 constexpr int ATT_SEG = 64;
 constexpr int ATT_THREADS = 512;
 constexpr int ATT_F4 = ATT_SEG * 32 / ATT_THREADS;  // float4 of one segment's K (or V) per thread

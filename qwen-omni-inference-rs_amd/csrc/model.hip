@@ -73,7 +73,7 @@ struct lq8_model {
     // persistent greedy decode (decode_persistent.hip): per-layer weight
     // pointers, tagged hand-off buffers, the argument block, the abort flag
     PLayer* d_player = nullptr;
-    uint64_t* hand = nullptr;  // qkvb | partb | attnb | h2b | actb | hb | argb | arrival counters
+    uint64_t* hand = nullptr;  // qkvb | partb | resb | h2b | actb | argb
     size_t hand_words = 0;
     PersistArgs* d_pargs = nullptr;
     PersistArgs h_pargs{};     // host copy (the source of the argument upload)
@@ -519,11 +519,13 @@ lq8_status persist_setup(lq8_model* m) {
     if (!coop) return fail(LQ8_ERR_DEVICE, "persistent decode: no cooperative launch on this device");
     const int P = m->ctx->num_cus;
     const PersistShape sh = persist_shape(m);
+    PersistLayout lay{};
+    if (!persist_layout(sh, P, &lay)) return fail(LQ8_ERR_MODEL, "persistent decode: shape not supported");
     const size_t L = c.num_layers, H = c.hidden_size, I = c.intermediate_size, NH = c.num_heads;
     const size_t cmax = (size_t)m->cmax;
-    const size_t qkv = L * m->QKV, part = L * cmax * NH * ATT_PART_STRIDE, attn = L * NH * 128, h2 = L * H,
-                 act = L * I, h = L * H, cnt = L * c.num_kv_heads * 16 / 2;  // counters: 16 u32 each
-    m->hand_words = qkv + part + attn + h2 + act + h + 2 * (size_t)P + cnt;
+    const size_t qkv = L * m->QKV, part = L * cmax * NH * ATT_PART_STRIDE, res = (L + 1) * (1 + lay.nchO) * H,
+                 h2 = L * H, act = L * I;
+    m->hand_words = qkv + part + res + h2 + act + 2 * (size_t)P;
     std::vector<PLayer> pl(L);
     for (size_t l = 0; l < L; l++) {
         const Layer& Ly = m->layers[l];
@@ -551,18 +553,20 @@ lq8_status persist_setup(lq8_model* m) {
     a.max_pos = (int)c.max_positions; a.cmax = m->cmax; a.vocab = (int)c.vocab_size;
     a.eps = c.rms_norm_eps;
     a.scale = 1.0f / std::sqrt((float)c.head_dim);
+    a.csO = lay.csO;
+    a.nchO = lay.nchO;
     a.qkvb = m->hand;
     a.partb = a.qkvb + qkv;
-    a.attnb = a.partb + part;
-    a.h2b = a.attnb + attn;
+    a.resb = a.partb + part;
+    a.h2b = a.resb + res;
     a.actb = a.h2b + h2;
-    a.hb = a.actb + act;
-    a.argb = a.hb + h;
-    a.cntb = (unsigned*)(a.argb + 2 * (size_t)P);
+    a.argb = a.actb + act;
     a.abort_flag = m->d_abort;
-    a.xs_floats = (int)persist_xs_floats(sh);
-    a.region_a = (int)persist_region_a(sh);
-    a.smem_bytes = (int)persist_smem_bytes(sh);
+    a.fr = lay.fr;
+    a.xs_off = lay.xs_off;
+    a.gs_off = lay.gs_off;
+    a.red_off = lay.red_off;
+    a.smem_bytes = lay.smem_bytes;
     m->persist_wg = P;
     return LQ8_OK;
 }
@@ -590,7 +594,8 @@ lq8_status launch_persist(lq8_model* m, int pos0, int steps, bool feed_first) {
     m->tag += (unsigned)steps;
     LQ8_HIP(hipMemcpyAsync(m->d_pargs, &a, sizeof(PersistArgs), hipMemcpyHostToDevice, s));
     LQ8_HIP(hipMemsetAsync(m->d_abort, 0, sizeof(unsigned), s));
-    return launch_decode_persistent(s, m->d_pargs, a.smem_bytes, m->persist_wg);
+    return launch_decode_persistent(s, m->d_pargs, a.smem_bytes, m->persist_wg,
+                                    persist_down_group((int)m->c.intermediate_size));
 }
 
 // generate (src/generate.rs:611-664): greedy picks (sc null) or sampled ones;
