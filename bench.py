@@ -328,6 +328,25 @@ def gemm_sweep(ctx):
         w.free()
 
 
+def decode_only(ctx, path, new_tokens):
+    """Config-4 greedy decode alone (Qwen3-0.6B shapes, random Q8_0 weights,
+    128-token prompt) on one path: the replayed decode graph or the persistent
+    kernel; one line with the decode rate (for hardware-counter runs)."""
+    cfg = lq8.qwen3_0_6b(max_positions=512)
+    model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=2026)
+    prompt = np.random.default_rng(2026).integers(0, cfg.vocab_size, 128).astype(np.uint32)
+    if path == "persistent":
+        os.environ["LQ8_PERSIST"] = "1"
+    try:
+        model.generate_greedy(prompt, 8)
+        st = model.generate_greedy(prompt, new_tokens)[1]
+    finally:
+        os.environ.pop("LQ8_PERSIST", None)
+    print(f"decode ({path}): {st['decode_tokens_per_s']:.1f} tok/s over {new_tokens} tokens, graph {st['used_graph']}, "
+          f"persistent {st['used_persistent']}", flush=True)
+    model.free()
+
+
 def sync_bench(ctx):
     """Grid-wide synchronisation (lq8_bench_grid_sync) per kind and grid size:
     device time per synchronisation over 2000 synchronisations with a data
@@ -353,6 +372,9 @@ def main():
                     help="only the headline step and the calibration copy (for hardware-counter runs)")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="only the W8A8 GEMM at M = 512 ... 8192 (gate/up and down shapes), one line each")
+    ap.add_argument("--decode-only", choices=("graph", "persistent"),
+                    help="only the Qwen3-0.6B greedy decode on one path, one line (for hardware-counter runs)")
+    ap.add_argument("--new-tokens", type=int, default=128, help="tokens generated by --decode-only")
     ap.add_argument("--sync-bench", action="store_true",
                     help="only the grid-wide synchronisation microbenchmark, one line per kind and grid size")
     args = ap.parse_args()
@@ -361,6 +383,9 @@ def main():
         return
     if args.sync_bench:
         sync_bench(lq8.Context(0))
+        return
+    if args.decode_only:
+        decode_only(lq8.Context(0), args.decode_only, args.new_tokens)
         return
     if args.only_step:
         args.no_decode = args.no_cpu = args.no_moe = True

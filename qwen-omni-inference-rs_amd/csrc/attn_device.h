@@ -19,7 +19,9 @@ template <bool PIN>
 __device__ __forceinline__ int thread_x() {
     return PIN ? tid_here() : (int)threadIdx.x;
 }
-constexpr int KPAD = 129;  // LDS row stride of staged keys (bank-conflict free scores)
+// LDS row stride of staged keys: rows start on 16-byte boundaries (b128 reads
+// and writes) and consecutive rows 4 banks apart (conflict-free per 8 lanes)
+constexpr int KPAD = 132;
 
 // LDS float offsets of the staged K/V rows (16-byte aligned for float4 stores)
 __host__ __device__ inline int seg_ks_off(int G) { return (G * 128 + 256 + G * SEG + 2 * G + 3) & ~3; }
@@ -45,10 +47,10 @@ __device__ __forceinline__ float wave_max64(float a) {
 // RmsNorm of one head vector (src/attention.rs:350-358 with src/rms_norm.rs:143-176)
 // then RoPE (src/rope.rs:270-297) at table row cs/sn; one wave, lane l has
 // elements l and l + 64 (head_dim 128).
-__device__ __forceinline__ void head_norm_rope_vals(float s0, float s1, float w0, float w1, const float* cs,
-                                                    const float* sn, float eps, float* dst) {
+// c, s: the table entries of the lane's rotation pair (cs[lane & ~1], sn[lane & ~1]).
+__device__ __forceinline__ void head_norm_rope_cs(float s0, float s1, float w0, float w1, float c, float s, float eps,
+                                                  float* dst) {
     const int lane = threadIdx.x & 63;
-    const float c = cs[lane & ~1], s = sn[lane & ~1];
     const float x0 = bf16_round(s0), x1 = bf16_round(s1);
     float acc = 0.0f;
     acc = acc + x0 * x0;
@@ -59,6 +61,11 @@ __device__ __forceinline__ void head_norm_rope_vals(float s0, float s1, float w0
     const float y1 = bf16_round((x1 * inv) * bf16_round(w1));
     dst[lane] = y0 * c - y1 * s;
     dst[lane + 64] = y1 * c + y0 * s;
+}
+__device__ __forceinline__ void head_norm_rope_vals(float s0, float s1, float w0, float w1, const float* cs,
+                                                    const float* sn, float eps, float* dst) {
+    const int lane = threadIdx.x & 63;
+    head_norm_rope_cs(s0, s1, w0, w1, cs[lane & ~1], sn[lane & ~1], eps, dst);
 }
 __device__ __forceinline__ void head_norm_rope(const float* src, const float* w, const float* cs, const float* sn,
                                                float eps, float* dst) {
@@ -107,6 +114,23 @@ __device__ __forceinline__ void seg_load_capacity(const float* __restrict__ Kc, 
     }
 }
 
+// q . k over head_dim 128, sequential over d from +0 (s = s + q[d] * k[d]);
+// q and k 16-byte aligned in LDS, read 4 elements at a time.
+__device__ __forceinline__ float qk_dot128(const float* q, const float* k) {
+    const float4* q4 = (const float4*)q;
+    const float4* k4 = (const float4*)k;
+    float s = 0.0f;
+#pragma unroll 8
+    for (int d4 = 0; d4 < 32; d4++) {
+        const float4 a = q4[d4], b = k4[d4];
+        s = s + a.x * b.x;
+        s = s + a.y * b.y;
+        s = s + a.z * b.z;
+        s = s + a.w * b.w;
+    }
+    return s;
+}
+
 // LDS_SYNC: the barriers order LDS only (lds_sync: the caller's own global
 // stores are not waited for), for callers that keep global visibility apart.
 template <int NT = ATT_THREADS, bool PIN_TID = false, bool LDS_SYNC = false>
@@ -121,21 +145,14 @@ __device__ __forceinline__ void seg_scores(const float4* kreg, int nj, int knew_
         if (j < nj) {
             float4 v = kreg[u];
             if (j == knew_row) v = *(const float4*)(knew + c4 * 4);
-            float* dst = ks + j * KPAD + c4 * 4;
-            dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+            *(float4*)(ks + j * KPAD + c4 * 4) = v;
         }
     }
     if (LDS_SYNC) lds_sync();
     else __syncthreads();
     for (int t = tid; t < G * SEG; t += NT) {
         const int h = t / SEG, j = t % SEG;
-        if (j < nj) {
-            const float* q = qs + h * 128;
-            const float* kr = ks + j * KPAD;
-            float s = 0.0f;
-            for (int d = 0; d < 128; d++) s = s + q[d] * kr[d];
-            sc[h * SEG + j] = s * scale;
-        }
+        if (j < nj) sc[h * SEG + j] = qk_dot128(qs + h * 128, ks + j * KPAD) * scale;
     }
     if (LDS_SYNC) lds_sync();
     else __syncthreads();

@@ -85,7 +85,15 @@ constexpr int NW_RES = PERSIST_FETCH;                             // h and the o
 constexpr int NW_ACT = (4096 + 16 + PT - 1) / PT;                  // silu(gate) * up (<= 4096) and 16 rows of h2
 constexpr int NW_PART = 16;                                       // 8 segments x 2 words per run
 constexpr int CHH = 16 / PW;    // block pairs per wave group of a hidden-long tile (hidden <= 1024: <= 16 pairs)
-constexpr int LMU = 8;         // lm_head: block pairs per streamed unit of a tile
+#ifndef LQ8_LMU
+#define LQ8_LMU 4
+#endif
+#ifndef LQ8_LMS
+#define LQ8_LMS 3
+#endif
+constexpr int LMU = LQ8_LMU;   // lm_head: block pairs per streamed unit of a tile (a power of two)
+constexpr int LMS = LQ8_LMS;   // lm_head: units in a wave's ring (LMS - 1 in flight while one is summed)
+constexpr int LMQ = 16 / LMU;  // lm_head: units per tile, at most (hidden <= 1024: <= 16 pairs)
 constexpr int RSRC_RAW = 0x00020000;  // raw buffer resource, 32-bit data format
 constexpr int AUX_NT = 2;      // buffer load cache policy: nontemporal
 
@@ -360,7 +368,14 @@ __device__ __forceinline__ float chunk_tree(float* v, int n) {
 // RmsNorm (src/rms_norm.rs:143-176) of xs[0, k) in place, in the order of
 // the GEMV's XS_RMSNORM staging: bf16 inputs; SUM64 of squares (wave 0);
 // inv = 1 / sqrt(sum / k + eps); out = bf16((v * inv) * bf16(w)).
-__device__ __forceinline__ void stage_rmsnorm(float* xs, int k, const float* w, float eps, float* red) {
+// wv: the weights w[tid + j PT] (norm_prefetch), loaded before the phase's
+// hand-off so that their latency hides behind it.
+__device__ __forceinline__ void norm_prefetch(const float* w, int k, float (&wv)[NW_H]) {
+    const int tid = tid_here();
+#pragma unroll
+    for (int j = 0; j < NW_H; j++) wv[j] = tid + j * PT < k ? w[tid + j * PT] : 0.0f;
+}
+__device__ __forceinline__ void stage_rmsnorm(float* xs, int k, const float (&wv)[NW_H], float eps, float* red) {
     const int tid = tid_here();
     for (int i = tid; i < k; i += PT) xs[i] = bf16_round(xs[i]);
     lds_sync();
@@ -372,7 +387,11 @@ __device__ __forceinline__ void stage_rmsnorm(float* xs, int k, const float* w, 
     }
     lds_sync();
     const float inv = red[0];
-    for (int i = tid; i < k; i += PT) xs[i] = bf16_round((xs[i] * inv) * bf16_round(w[i]));
+#pragma unroll
+    for (int j = 0; j < NW_H; j++) {
+        const int i = tid + j * PT;
+        if (i < k) xs[i] = bf16_round((xs[i] * inv) * bf16_round(wv[j]));
+    }
     lds_sync();
 }
 
@@ -462,7 +481,7 @@ __device__ __forceinline__ Job job_dn(CArgs& a, const Dims& D, CLayer& Lw, int t
 
 template <int CH5>
 __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __restrict__ pa) {
-    extern __shared__ float sm[];
+    extern __shared__ __align__(16) float sm[];
     __shared__ int bad_s;
     __shared__ float pick_v[PW];
     __shared__ int pick_i[PW];
@@ -504,6 +523,8 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             if (w < dims_of(*opaque_args(pa)).T1) {
                 LAYER_LOCALS;
                 PTRACE(LQ8_PT_P1_START);
+                float nw[NW_H];
+                norm_prefetch(Lw.in_norm, D.H, nw);
                 if (l > 0) {
                     tfetch_lin<NW_H>(D.H, tag, resl, xs, a.abort_flag, bad);
                 } else {
@@ -518,7 +539,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 stage_pad(xs, D.H, D.npH);
                 lds_sync();
                 if (bad_now(bad)) goto done;
-                stage_rmsnorm(xs, D.H, Lw.in_norm, a.eps, red);
+                stage_rmsnorm(xs, D.H, nw, a.eps, red);
                 PTRACE(LQ8_PT_P1_NORMED);
                 for (int t = w; t < D.T1; t += P) {
                     const Job J = job_qkv(a, D, Lw, t);
@@ -564,6 +585,10 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     float* Vc = a.vc + l * (size_t)D.NKV * a.max_pos * 128 + (size_t)g * a.max_pos * 128;
                     float4 kreg[ATT_SEG * 32 / PT], vreg[ATT_SEG * 32 / PT];
                     seg_load<PT, true>(Kc, Vc, js, nj, kreg, vreg);
+                    // q/k norm weights and the position's rotation, ahead of the hand-off
+                    const float qn0 = Lw.q_norm[lane], qn1 = Lw.q_norm[lane + 64];
+                    const float kn0 = Lw.k_norm[lane], kn1 = Lw.k_norm[lane + 64];
+                    const float rc = a.cos_t[(size_t)pos * 64 + (lane & ~1)], rs = a.sin_t[(size_t)pos * 64 + (lane & ~1)];
                     // q of the group's heads; k and v only for the segment holding the position
                     const int nq = (last ? G + 2 : G) * 128;
                     tfetch<NW_QKV>(tag, [&](int tt, int u) { return tt + u * PT < nq; },
@@ -576,17 +601,14 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     lds_sync();
                     if (bad_now(bad)) goto done;
                     PTRACE(LQ8_PT_P2_QKV_IN);
-                    const float* cs = a.cos_t + (size_t)pos * 64;
-                    const float* sn = a.sin_t + (size_t)pos * 64;
                     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
                     for (int t = wave; t < G + 2; t += PW) {
                         if (t >= G && !last) continue;
                         const float x0 = qraw[t * 128 + lane], x1 = qraw[t * 128 + lane + 64];
                         if (t < G) {
-                            head_norm_rope_vals(x0, x1, Lw.q_norm[lane], Lw.q_norm[lane + 64], cs, sn, a.eps,
-                                                qs + t * 128);
+                            head_norm_rope_cs(x0, x1, qn0, qn1, rc, rs, a.eps, qs + t * 128);
                         } else if (t == G) {
-                            head_norm_rope_vals(x0, x1, Lw.k_norm[lane], Lw.k_norm[lane + 64], cs, sn, a.eps, kn);
+                            head_norm_rope_cs(x0, x1, kn0, kn1, rc, rs, a.eps, kn);
                             float* kr = Kc + (size_t)pos * 128;
                             kr[lane] = kn[lane];
                             kr[lane + 64] = kn[lane + 64];
@@ -708,6 +730,8 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 if (t != w) job_load<2, CHH>(J, R4);
                 float* f = sm;  // [1 + nchO][H]
                 if (t == w) {
+                    float nw[NW_H];
+                    norm_prefetch(Lw.post_norm, D.H, nw);
                     tfetch_lin<NW_RES>((1 + a.nchO) * D.H, tag, resl, f, a.abort_flag, bad);
                     lds_sync();
                     if (bad_now(bad)) goto done;
@@ -723,7 +747,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     }
                     stage_pad(xs, D.H, D.npH);
                     lds_sync();
-                    stage_rmsnorm(xs, D.H, Lw.post_norm, a.eps, red);
+                    stage_rmsnorm(xs, D.H, nw, a.eps, red);
                 }
                 job_dot<2, CHH>(J, R4, xs, gs);
                 lds_sync();
@@ -790,12 +814,13 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             const int t0 = w * PW + wave, tstride = P * PW;
             const int np = D.npH, nb = D.nbH;
             const int r = lane & 15;
-            // a wave streams its tiles in units of LMU block pairs, the next
-            // unit's loads in flight while the current one is summed (two
-            // register sets, A for the even units of a tile, B for the odd)
-            const int nq = (np + LMU - 1) / LMU;  // units per tile: 1 or 2
-            u32x4 cA[LMU], cB[LMU];
-            uint16_t dA[LMU], dB[LMU];
+            // a wave streams its tiles in units of LMU block pairs through a
+            // ring of LMS register sets: unit u sits in set u % LMS, and the
+            // loads of units u + 1 .. u + LMS - 1 are in flight while unit u
+            // is summed
+            const int nq = (np + LMU - 1) / LMU;  // units per tile, <= LMQ
+            u32x4 cr[LMS][LMU];
+            uint16_t dr[LMS][LMU];
             // buffer loads: one descriptor per table and a 32-bit lane offset,
             // the tile and chunk offsets uniform (no per-chunk pointers)
             const int tiles_alloc = (D.T6 + 1) & ~1;  // rows stored in multiples of 32
@@ -843,37 +868,59 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                         if (i + s2 < cnt) v[i] = v[i] + v[i + s2];
                 return v[0];
             };
-            if (t0 < D.T6) load_u(t0, 0, cA, dA);
+            const int ntw = t0 < D.T6 ? (D.T6 - t0 + tstride - 1) / tstride : 0;  // the wave's tiles
+            const int U = ntw * nq;                                                  // and units
+            auto unit_tile = [&](int u) { return t0 + (u / nq) * tstride; };
+            auto unit_q = [&](int u) { return u % nq; };
+#pragma unroll
+            for (int j = 0; j + 1 < LMS; j++)
+                if (j < U) load_u(unit_tile(j), unit_q(j), cr[j], dr[j]);
+            float nw[NW_H];
+            norm_prefetch(a.final_norm, D.H, nw);
             const uint64_t* hL = a.resb + (size_t)a.L * (1 + a.nchO) * D.H;
             tfetch_lin<NW_H>(D.H, tag, hL, xs, a.abort_flag, bad);
             stage_pad(xs, D.H, np);
             lds_sync();
             if (bad_now(bad)) goto done;
-            stage_rmsnorm(xs, D.H, a.final_norm, a.eps, red);
+            stage_rmsnorm(xs, D.H, nw, a.eps, red);
             PTRACE(LQ8_PT_P6_NORMED);
             float bv = -__builtin_huge_valf();
             int bi = -1;
-            for (int t = t0; t < D.T6; t += tstride) {
-                const bool more = t + tstride < D.T6;
-                if (nq > 1) load_u(t, 1, cB, dB);
-                float v0 = dot_u(0, cA, dA);
-                if (more) load_u(t + tstride, 0, cA, dA);
-                if (nq > 1) {
-                    // the level joining the two units (pairs 0 and LMU)
-                    const float v1 = dot_u(1, cB, dB);
-                    v0 = v0 + v1;
-                }
-                const int row = t * 16 + r;
-                const bool valid = lane < 16 && row < a.vocab;
-                float tv = valid ? v0 : -__builtin_huge_valf();
-                int ti = valid ? row : -1;
-                argmax_step<8>(tv, ti);
-                argmax_step<4>(tv, ti);
-                argmax_step<2>(tv, ti);
-                argmax_step<1>(tv, ti);
-                if (tv > bv || (tv == bv && ti > bi)) {
-                    bv = tv;
-                    bi = ti;
+            float uv[LMQ];  // the tile's unit values (subtrees of LMU pairs)
+            for (int u0 = 0; u0 < U; u0 += LMS) {
+#pragma unroll
+                for (int j = 0; j < LMS; j++) {
+                    const int u = u0 + j;
+                    if (u < U) {
+                        if (u + LMS - 1 < U)
+                            load_u(unit_tile(u + LMS - 1), unit_q(u + LMS - 1), cr[(j + LMS - 1) % LMS],
+                                   dr[(j + LMS - 1) % LMS]);
+                        const int q = unit_q(u);
+                        const float vq = dot_u(q, cr[j], dr[j]);
+#pragma unroll
+                        for (int k = 0; k < LMQ; k++)
+                            if (k == q) uv[k] = vq;
+                        if (q == nq - 1) {
+                            // the tree levels above the units (pairs LMU, 2 LMU, ... apart)
+#pragma unroll
+                            for (int s2 = 1; s2 < LMQ; s2 *= 2)
+#pragma unroll
+                                for (int i = 0; i + s2 < LMQ; i += 2 * s2)
+                                    if (i + s2 < nq) uv[i] = uv[i] + uv[i + s2];
+                            const int row = unit_tile(u) * 16 + r;
+                            const bool valid = lane < 16 && row < a.vocab;
+                            float tv = valid ? uv[0] : -__builtin_huge_valf();
+                            int ti = valid ? row : -1;
+                            argmax_step<8>(tv, ti);
+                            argmax_step<4>(tv, ti);
+                            argmax_step<2>(tv, ti);
+                            argmax_step<1>(tv, ti);
+                            if (tv > bv || (tv == bv && ti > bi)) {
+                                bv = tv;
+                                bi = ti;
+                            }
+                        }
+                    }
                 }
             }
             // lanes 0..15 hold the wave's pick (rows of lanes 16..63 were invalid)

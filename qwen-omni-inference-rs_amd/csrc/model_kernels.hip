@@ -205,9 +205,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_rows(AttnRowsLaunch a) {
             const int f = tid + u * ATT_THREADS;
             const int j = f >> 5, c4 = f & 31;
             if (j < njmax) {
-                const float4 v = kreg[u];
-                float* dst = ks + j * KPAD + c4 * 4;
-                dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+                *(float4*)(ks + j * KPAD + c4 * 4) = kreg[u];
             }
         }
         __syncthreads();
@@ -215,13 +213,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_rows(AttnRowsLaunch a) {
         for (int t = tid; t < RG * SEG; t += ATT_THREADS) {
             const int rh = t / SEG, j = t - rh * SEG, rr = rh / G;
             const int nj = min(SEG, a.pos_base + i0 + rr + 1 - js);
-            if (rr < nr && j < nj) {
-                const float* q = qs + rh * 128;
-                const float* kr = ks + j * KPAD;
-                float sv = 0.0f;
-                for (int d = 0; d < 128; d++) sv = sv + q[d] * kr[d];
-                sc[rh * SEG + j] = sv * a.scale;
-            }
+            if (rr < nr && j < nj) sc[rh * SEG + j] = qk_dot128(qs + rh * 128, ks + j * KPAD) * a.scale;
         }
         __syncthreads();
         // segment softmax per (row, head): max, exp, SUM64 denominator
