@@ -94,6 +94,10 @@ constexpr int CHH = 16 / PW;    // block pairs per wave group of a hidden-long t
 constexpr int LMU = LQ8_LMU;   // lm_head: block pairs per streamed unit of a tile (a power of two)
 constexpr int LMS = LQ8_LMS;   // lm_head: units in a wave's ring (LMS - 1 in flight while one is summed)
 constexpr int LMQ = 16 / LMU;  // lm_head: units per tile, at most (hidden <= 1024: <= 16 pairs)
+#ifndef LQ8_LMD
+#define LQ8_LMD 4
+#endif
+constexpr int LMD = LQ8_LMD;   // lm_head: chunks per interleaved dot (divides LMU)
 constexpr int RSRC_RAW = 0x00020000;  // raw buffer resource, 32-bit data format
 constexpr int AUX_NT = 2;      // buffer load cache policy: nontemporal
 
@@ -844,14 +848,14 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 const int ln = tid_here() & 63, bs = (ln >> 4) >> 1, hf = (ln >> 4) & 1;
                 float v[LMU];
 #pragma unroll
-                for (int i0 = 0; i0 < LMU; i0 += 4) {
-                    const float* xp[4];
+                for (int i0 = 0; i0 < LMU; i0 += LMD) {
+                    const float* xp[LMD];
 #pragma unroll
-                    for (int k = 0; k < 4; k++) xp[k] = xs + (2 * min(q * LMU + i0 + k, np - 1) + bs) * 32 + hf * 16;
-                    float h[4];
-                    dot16xN<4>(c + i0, xp, h);
+                    for (int k = 0; k < LMD; k++) xp[k] = xs + (2 * min(q * LMU + i0 + k, np - 1) + bs) * 32 + hf * 16;
+                    float h[LMD];
+                    dot16xN<LMD>(c + i0, xp, h);
 #pragma unroll
-                    for (int k = 0; k < 4; k++) {
+                    for (int k = 0; k < LMD; k++) {
                         const int pc = min(q * LMU + i0 + k, np - 1);
                         const LanePair hh = lanes16(h[k]);
                         const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(d[i0 + k]);
