@@ -24,6 +24,7 @@ struct PersistShape {
 // Work split and LDS map of one shape on P workgroups (persist_layout).
 struct PersistLayout {
     int csO, nchO;      // o projection: input chunks of csO blocks (a power of two), nchO of them
+    int csD, nchD;      // down projection: input chunks of csD block pairs (a power of two), nchD of them
     int fr, xs_off, gs_off, red_off, att_floats;  // LDS, in floats
     int smem_bytes;
     size_t words;       // tagged hand-off words of all buffers
@@ -42,11 +43,13 @@ struct PersistArgs {
     int H, I, NH, NKV, max_pos, cmax, vocab;
     float eps, scale;
     int csO, nchO;
+    int csD, nchD;
     // tagged hand-off words (f32 bits | tag << 32)
     uint64_t* qkvb;   // [L][QKV]: q|k|v projection
     uint64_t* partb;  // [L][cmax][NH][ATT_PART_STRIDE]: attention partials per (segment, head)
     uint64_t* resb;   // [L + 1][(1 + nchO) * H]: layer input h, then the o projection's chunk sums [nchO][H]
-    uint64_t* h2b;    // [L][H]: h + o projection (the MLP's input and residual)
+    uint64_t* h2b;    // [L][(1 + nchD) * H]: h + o projection (the MLP's input and residual), then the down
+                      // projection's chunk sums [nchD][H]
     uint64_t* actb;   // [L][I]: silu(gate) * up
     uint64_t* argb;   // [P][2]: each workgroup's greedy pick (value, index bits)
     unsigned* abort_flag;
@@ -65,15 +68,7 @@ struct PersistArgs {
 bool persist_layout(const PersistShape& s, int P, PersistLayout* out);
 bool persist_supported(const PersistShape& s, int num_cus);
 // d_args: the argument block in device memory (read by the kernel throughout)
-// ch5: block pairs per wave group of the down tile (persist_down_group)
+// ch5: block pairs per wave group of the down items (csD / waves per workgroup)
 lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg, int ch5);
-// block pairs per wave group of the down tile (the workgroup's waves over
-// ceil(I / 64) pairs): 1, 2, 4 or 8
-inline int persist_down_group(int I) {
-    const int np = (I / 32 + 1) / 2, pw = PERSIST_THREADS / 64;
-    int ch = 1;
-    while (ch < 8 && np > ch * pw) ch *= 2;
-    return ch;
-}
 
 }  // namespace lq8

@@ -459,14 +459,13 @@ __device__ __forceinline__ Dims dims_of(CArgs& a) {
     uint64_t* qkvb = a.qkvb + (size_t)l * D.QKV;                                                           \
     uint64_t* partb = a.partb + (size_t)l * a.cmax * D.NH * ATT_PART_STRIDE;                               \
     uint64_t* resl = a.resb + (size_t)l * (1 + a.nchO) * D.H; /* [h_l | o chunk sums] */                   \
-    uint64_t* resn = resl + (size_t)(1 + a.nchO) * D.H;       /* the next layer's: h_l+1 at its head */   \
-    uint64_t* h2b = a.h2b + (size_t)l * D.H;                                                               \
+    uint64_t* h2b = a.h2b + (size_t)l * (1 + a.nchD) * D.H; /* [h2 | down chunk sums] */                 \
     uint64_t* actb = a.actb + (size_t)l * D.I;                                                             \
     const int n3 = D.TH * a.nchO;                                                                          \
     (void)tid; (void)lane; (void)pos; (void)Lw; (void)xs; (void)gs; (void)red; (void)qkvb; (void)partb;    \
-    (void)resl; (void)resn; (void)h2b; (void)actb; (void)n3
+    (void)resl; (void)h2b; (void)actb; (void)n3
 
-// The jobs of the phases' items (CH5: pairs per group of the down tile).
+// The jobs of the phases' items (CH5: pairs per group of a down item).
 __device__ __forceinline__ Job job_qkv(CArgs& a, const Dims& D, CLayer& Lw, int t) {
     return make_job<CHH>(Lw.qkv_c, Lw.qkv_s, D.npH, D.nbH, t, t, 0, D.npH);
 }
@@ -479,8 +478,9 @@ __device__ __forceinline__ Job job_gu(CArgs& a, const Dims& D, CLayer& Lw, int t
     return make_job<CHH>(Lw.gu_c, Lw.gu_s, D.npH, D.nbH, t, D.TI + t, 0, D.npH);
 }
 template <int CH5>
-__device__ __forceinline__ Job job_dn(CArgs& a, const Dims& D, CLayer& Lw, int t) {
-    return make_job<CH5>(Lw.dn_c, Lw.dn_s, D.npI, D.nbI, t, t, 0, D.npI);
+__device__ __forceinline__ Job job_dn(CArgs& a, const Dims& D, CLayer& Lw, int it) {
+    const int t = it / a.nchD, c = it - t * a.nchD, p0 = c * a.csD;
+    return make_job<CH5>(Lw.dn_c, Lw.dn_s, D.npI, D.nbI, t, t, p0, min(a.csD, D.npI - p0));
 }
 
 template <int CH5>
@@ -530,7 +530,22 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 float nw[NW_H];
                 norm_prefetch(Lw.in_norm, D.H, nw);
                 if (l > 0) {
-                    tfetch_lin<NW_H>(D.H, tag, resl, xs, a.abort_flag, bad);
+                    // h_l = h2 of layer l - 1 + its down projection's chunk sums
+                    // joined in the block tree; published for this layer's h2
+                    const uint64_t* hp = a.h2b + (size_t)(l - 1) * (1 + a.nchD) * D.H;
+                    float* f = sm;  // [1 + nchD][H]
+                    tfetch_lin<NW_RES>((1 + a.nchD) * D.H, tag, hp, f, a.abort_flag, bad);
+                    lds_sync();
+                    if (bad_now(bad)) goto done;
+                    const int n1 = min(D.T1, P);
+                    for (int r = tid; r < D.H; r += PT) {
+                        float v[PERSIST_NCH];
+#pragma unroll
+                        for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchD ? f[(1 + q) * D.H + r] : 0.0f;
+                        const float h = f[r] + chunk_tree(v, a.nchD);
+                        xs[r] = h;
+                        if (r % n1 == w) tput(resl + r, h, tag);
+                    }
                 } else {
                     // the embedding row (src/embedding.rs), published as h_0
                     const int n1 = min(D.T1, P);
@@ -722,7 +737,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             {
                 LAYER_LOCALS;
                 if (w < D.TI) job_load<2, CHH>(job_gu(a, D, Lw, w), R4);
-                if (w < D.TH) job_load<1, CH5>(job_dn<CH5>(a, D, Lw, w), R5);
+                if (w < D.TH * a.nchD) job_load<1, CH5>(job_dn<CH5>(a, D, Lw, w), R5);
             }
 
             // ---- P4: h2 = h_l + o, RmsNorm(h2) + gate / up tile pair -> silu(gate) * up
@@ -770,26 +785,19 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 if (l + 1 < a.L && w < D.T1) job_load<1, CHH>(job_qkv(a, D, layer_of(a, l + 1), w), R1);
             }
 
-            // ---- P5: down tile + residual h2 -> h_l+1
+            // ---- P5: down tile over one input chunk -> chunk sums (the
+            // next layer's RMSNorm stage joins them and adds the residual h2)
             {
                 LAYER_LOCALS;
             PTRACE(LQ8_PT_P5_START);
-            for (int t = w; t < D.TH; t += P) {
-                const Job J = job_dn<CH5>(a, D, Lw, t);
-                if (t != w) job_load<1, CH5>(J, R5);
-                float* hr = sm;  // [16] the tile's rows of h2
-                const int nI = D.I;
-                tfetch<NW_ACT>(tag, [&](int tt, int u) { return tt + u * PT < nI + 16; },
-                       [&](int tt, int u) {
-                           const int i = tt + u * PT;
-                           return i < nI ? (const uint64_t*)actb + i : (const uint64_t*)h2b + t * 16 + (i - nI);
-                       },
-                       [&](int tt, int u) {
-                           const int i = tt + u * PT;
-                           return i < nI ? xs + i : hr + (i - nI);
-                       },
-                       a.abort_flag, bad);
-                stage_pad(xs, D.I, D.npI);
+            for (int it = w; it < D.TH * a.nchD; it += P) {
+                const Job J = job_dn<CH5>(a, D, Lw, it);
+                if (it != w) job_load<1, CH5>(J, R5);
+                const int t = it / a.nchD, c = it - t * a.nchD;
+                // the chunk's input: silu(gate) * up elements [64 p0, 64 (p0 + npv)) within I
+                const int i0 = J.p0 * 64, nx = min(J.npv * 64, D.I - i0);
+                tfetch_lin<NW_ACT>(nx, tag, (const uint64_t*)actb + i0, xs, a.abort_flag, bad);
+                stage_pad(xs, nx, J.npv);
                 lds_sync();
                 if (bad_now(bad)) goto done;
                 PTRACE(LQ8_PT_P5_STAGED);
@@ -797,7 +805,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 lds_sync();
                 if (tid < 64) {
                     const float acc = tile_final(gs, J.G);
-                    if (tid < 16) tput(resn + t * 16 + tid, hr[tid] + acc, tag);
+                    if (tid < 16) tput(h2b + (size_t)(1 + c) * D.H + t * 16 + tid, acc, tag);
                 }
                 lds_sync();
                 PTRACE(LQ8_PT_P5_DONE);
@@ -881,11 +889,20 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 if (j < U) load_u(unit_tile(j), unit_q(j), cr[j], dr[j]);
             float nw[NW_H];
             norm_prefetch(a.final_norm, D.H, nw);
-            const uint64_t* hL = a.resb + (size_t)a.L * (1 + a.nchO) * D.H;
-            tfetch_lin<NW_H>(D.H, tag, hL, xs, a.abort_flag, bad);
-            stage_pad(xs, D.H, np);
+            // the last layer's output: its h2 + the down projection's chunk sums
+            const uint64_t* hp = a.h2b + (size_t)(a.L - 1) * (1 + a.nchD) * D.H;
+            float* f = sm;  // [1 + nchD][H]
+            tfetch_lin<NW_RES>((1 + a.nchD) * D.H, tag, hp, f, a.abort_flag, bad);
             lds_sync();
             if (bad_now(bad)) goto done;
+            for (int r = tid; r < D.H; r += PT) {
+                float v[PERSIST_NCH];
+#pragma unroll
+                for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchD ? f[(1 + q) * D.H + r] : 0.0f;
+                xs[r] = f[r] + chunk_tree(v, a.nchD);
+            }
+            stage_pad(xs, D.H, np);
+            lds_sync();
             stage_rmsnorm(xs, D.H, nw, a.eps, red);
             PTRACE(LQ8_PT_P6_NORMED);
             float bv = -__builtin_huge_valf();
@@ -989,6 +1006,17 @@ bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
     const int nchO = nch_of(csO);
     // a chunk's pairs fit one group per wave (CHH pairs each)
     if (nchO > PERSIST_NCH || (1 + nchO) * s.H > cap || std::min(csO, nbQ) > 2 * CHH * PW) return false;
+    // down input chunks: the smallest power-of-two pair count, at least one
+    // group per wave, whose (tile, chunk) items fit the workgroups (or one
+    // chunk over the whole input); a wave's group holds <= 8 pairs
+    const int npI = (s.I / 32 + 1) / 2;
+    int csD = PERSIST_THREADS / 64;
+    auto nchd_of = [&](int cs) { return (npI + cs - 1) / cs; };
+    while (csD < npI &&
+           (TH * nchd_of(csD) > P || nchd_of(csD) > PERSIST_NCH || (1 + nchd_of(csD)) * s.H > cap))
+        csD *= 2;
+    const int nchD = nchd_of(csD);
+    if (nchD > PERSIST_NCH || (1 + nchD) * s.H > cap || csD > 8 * (PERSIST_THREADS / 64)) return false;
     const int pairsO = (std::min(csO, nbQ) + 1) / 2;  // pairs of the widest chunk
     const int rng = std::min(pairsO * 64, QD);
     const int nhc = rng / 128 + 2;  // heads a chunk touches, at most
@@ -996,11 +1024,14 @@ bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
     PersistLayout L{};
     L.csO = csO;
     L.nchO = nchO;
+    L.csD = csD;
+    L.nchD = nchD;
     int fr = std::max((1 + nchO) * s.H, 4 * cmax * nhc + cmax * rng + nhc);
+    fr = std::max(fr, (1 + nchD) * s.H);
     fr = std::max(fr, 2 * P);
     fr = std::max(fr, 16);
     L.fr = (fr + 3) & ~3;
-    const int npH = (s.H / 32 + 1) / 2, npI = (s.I / 32 + 1) / 2;
+    const int npH = (s.H / 32 + 1) / 2;
     const int xsz = std::max(std::max(npH, npI), pairsO) * 64;
     L.xs_off = L.fr;
     L.gs_off = L.xs_off + xsz;

@@ -524,7 +524,7 @@ lq8_status persist_setup(lq8_model* m) {
     const size_t L = c.num_layers, H = c.hidden_size, I = c.intermediate_size, NH = c.num_heads;
     const size_t cmax = (size_t)m->cmax;
     const size_t qkv = L * m->QKV, part = L * cmax * NH * ATT_PART_STRIDE, res = (L + 1) * (1 + lay.nchO) * H,
-                 h2 = L * H, act = L * I;
+                 h2 = L * (1 + lay.nchD) * H, act = L * I;
     m->hand_words = qkv + part + res + h2 + act + 2 * (size_t)P;
     std::vector<PLayer> pl(L);
     for (size_t l = 0; l < L; l++) {
@@ -555,6 +555,8 @@ lq8_status persist_setup(lq8_model* m) {
     a.scale = 1.0f / std::sqrt((float)c.head_dim);
     a.csO = lay.csO;
     a.nchO = lay.nchO;
+    a.csD = lay.csD;
+    a.nchD = lay.nchD;
     a.qkvb = m->hand;
     a.partb = a.qkvb + qkv;
     a.resb = a.partb + part;
@@ -594,8 +596,7 @@ lq8_status launch_persist(lq8_model* m, int pos0, int steps, bool feed_first) {
     m->tag += (unsigned)steps;
     LQ8_HIP(hipMemcpyAsync(m->d_pargs, &a, sizeof(PersistArgs), hipMemcpyHostToDevice, s));
     LQ8_HIP(hipMemsetAsync(m->d_abort, 0, sizeof(unsigned), s));
-    return launch_decode_persistent(s, m->d_pargs, a.smem_bytes, m->persist_wg,
-                                    persist_down_group((int)m->c.intermediate_size));
+    return launch_decode_persistent(s, m->d_pargs, a.smem_bytes, m->persist_wg, a.csD / (PERSIST_THREADS / 64));
 }
 
 // generate (src/generate.rs:611-664): greedy picks (sc null) or sampled ones;
