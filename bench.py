@@ -14,8 +14,9 @@ launch per GEMV replayed from a HIP graph, the lm_head alone, the single
 3072x1024 GEMV, the M = 512 W8A8 MFMA GEMM, and batch-1 decode of the
 random-init Q8_0 Qwen3-0.6B (128-token prompt, 128 new tokens; greedy, and
 sampled with temperature 0.8, top-k 50, top-p 0.95, repetition penalty 1.1)
-are reported beside it, and so are the host-pointer Linear::forward per call
-at the seven layer shapes and the opt-in persistent decode kernel.  The CPU
+are reported beside it (greedy decode on its default path, the persistent
+kernel, and on the replayed graph), and so is the host-pointer
+Linear::forward per call at the seven layer shapes.  The CPU
 baseline is a C restatement of the reference's own CPU Linear::forward (BF16
 weight, per-call transpose, BF16 -> F32 copy, naive matmul_2d) timed on one
 pinned host core over a bounded sample of the same workload; the CPU oracle's
@@ -335,13 +336,15 @@ def decode_only(ctx, path, new_tokens):
     cfg = lq8.qwen3_0_6b(max_positions=512)
     model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=2026)
     prompt = np.random.default_rng(2026).integers(0, cfg.vocab_size, 128).astype(np.uint32)
-    if path == "persistent":
-        os.environ["LQ8_PERSIST"] = "1"
+    prev = os.environ.get("LQ8_PERSIST")
+    os.environ["LQ8_PERSIST"] = "1" if path == "persistent" else "0"
     try:
         model.generate_greedy(prompt, 8)
         st = model.generate_greedy(prompt, new_tokens)[1]
     finally:
         os.environ.pop("LQ8_PERSIST", None)
+        if prev is not None:
+            os.environ["LQ8_PERSIST"] = prev
     print(f"decode ({path}): {st['decode_tokens_per_s']:.1f} tok/s over {new_tokens} tokens, graph {st['used_graph']}, "
           f"persistent {st['used_persistent']}", flush=True)
     model.free()
@@ -499,32 +502,34 @@ def main():
         model.generate(prompt, gc, seed=1)
         sruns = [model.generate(prompt, gc, seed=1 + i)[1] for i in range(3)]
         stps = sorted(r["decode_tokens_per_s"] for r in sruns)[1]
-        # the opt-in persistent kernel (one cooperative launch for all steps)
-        os.environ["LQ8_PERSIST"] = "1"
+        # the replayed decode graph (LQ8_PERSIST=0), the path before the
+        # persistent kernel became the default
+        os.environ["LQ8_PERSIST"] = "0"
         try:
             model.generate_greedy(prompt, 8)
-            pruns = [model.generate_greedy(prompt, 128)[1] for _ in range(3)]
+            gruns = [model.generate_greedy(prompt, 128)[1] for _ in range(3)]
         finally:
             del os.environ["LQ8_PERSIST"]
-        ptps = sorted(r["decode_tokens_per_s"] for r in pruns)[1] if all(r["used_persistent"] for r in pruns) else None
+        gtps = sorted(r["decode_tokens_per_s"] for r in gruns)[1] if all(r["used_graph"] for r in gruns) else None
         # every Q8_0 matrix of the model is read once per token (the tied
         # embedding as the lm_head); the step is a chain of dependent kernels
         wbytes = LAYERS * sum(n * k * 34 // 32 for _, n, k in LAYER_SHAPES) + LM_HEAD[1] * LM_HEAD[2] * 34 // 32
         chain = 5 * LAYERS + 3
-        decode = {"tokens_per_s": round(tps, 1), "us_per_token": round(1e6 / tps, 1),
+        path = "persistent" if runs[0]["used_persistent"] else ("graph" if runs[0]["used_graph"] else "plain")
+        decode = {"tokens_per_s": round(tps, 1), "us_per_token": round(1e6 / tps, 1), "path": path,
                   "weight_bytes_per_token": wbytes, "weight_gbs": round(wbytes * tps / 1e9, 1),
-                  "kernels_per_token": chain, "us_per_kernel": round(1e6 / tps / chain, 2),
-                  "bound": "latency: a chain of dependent kernels per token (5 per layer, then lm_head, pick, "
-                           "embedding row)",
-                  "prefill_ms": round(runs[0]["prefill_ms"], 2),
-                  "graph": runs[0]["used_graph"], "prompt": 128, "new_tokens": 128,
+                  "bound": "latency: one cooperative kernel for all steps of a generate() call; per layer five "
+                           "phases whose values pass between workgroups as tagged words" if path == "persistent"
+                           else "latency: a chain of dependent kernels per token",
+                  "prefill_ms": round(runs[0]["prefill_ms"], 2), "prompt": 128, "new_tokens": 128,
+                  "graph_tokens_per_s": None if gtps is None else round(gtps, 1),
+                  "graph_kernels_per_token": chain,
+                  "graph_us_per_kernel": None if gtps is None else round(1e6 / gtps / chain, 2),
                   "sampled_tokens_per_s": round(stps, 1),
                   "sampled_config": {"temperature": 0.8, "top_k": 50, "top_p": 0.95, "repetition_penalty": 1.1},
-                  "sampler_us_over_greedy": round(1e6 / stps - 1e6 / tps, 1),
-                  "persistent_tokens_per_s": None if ptps is None else round(ptps, 1)}
-        log(f"decode: {tps:.1f} tok/s (median of 3), prefill {runs[0]['prefill_ms']:.2f} ms; "
-            f"sampled {stps:.1f} tok/s ({1e6 / stps - 1e6 / tps:.1f} us/token over greedy); "
-            f"persistent kernel {ptps} tok/s")
+                  "sampler_us_over_greedy_graph": None if gtps is None else round(1e6 / stps - 1e6 / gtps, 1)}
+        log(f"decode: {tps:.1f} tok/s ({path}, median of 3), prefill {runs[0]['prefill_ms']:.2f} ms; "
+            f"graph {gtps} tok/s; sampled (graph) {stps:.1f} tok/s")
         if not args.no_cpu:
             cpu_model = (cfg, model.export_all(), prompt)
         model.free()

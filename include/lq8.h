@@ -192,7 +192,7 @@ lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t
 lq8_status lq8_bench_grid_sync(lq8_ctx* ctx, int kind, int nwg, int rounds, float* us_per_sync,
                                uint32_t* mismatches, uint32_t* gave_up);
 
-/* Phase timeline of the persistent greedy decode (LQ8_PERSIST, see
+/* Phase timeline of the persistent greedy decode (the default greedy path, see
  * lq8_generate_greedy), a diagnostic without counterpart in the reference:
  * in a library built with LQ8_PERSIST_TRACE (make trace -> liblq8_trace.so)
  * thread 0 of every workgroup stamps the 100 MHz real-time clock at the

@@ -503,10 +503,12 @@ PersistShape persist_shape(const lq8_model* m) {
                         (int)c.head_dim, (int)c.max_positions};
 }
 
-// Whether greedy decode runs as the persistent kernel: LQ8_PERSIST is set
-// and the shape is supported.
+// Whether greedy decode runs as the persistent kernel: wherever the shape is
+// supported, unless LQ8_PERSIST=0 (the replayed graph) or LQ8_NO_GRAPH (plain
+// kernel launches) asks for another path.
 bool persist_wanted(const lq8_model* m) {
-    if (std::getenv("LQ8_PERSIST") == nullptr) return false;
+    const char* e = std::getenv("LQ8_PERSIST");
+    if ((e != nullptr && e[0] == '0') || std::getenv("LQ8_NO_GRAPH") != nullptr) return false;
     return persist_supported(persist_shape(m), m->ctx->num_cus);
 }
 

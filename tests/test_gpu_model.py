@@ -71,13 +71,15 @@ def test_offset_must_match_cache(small_pair):
 
 
 def with_path(path, fn):
-    """Run fn with the greedy decode path forced: "persistent" (LQ8_PERSIST:
-    the persistent kernel), "graph" (the replayed graph, the default) or
+    """Run fn with the greedy decode path forced: "persistent" (the persistent
+    kernel, the default), "graph" (LQ8_PERSIST=0: the replayed graph) or
     "plain" (LQ8_NO_GRAPH: kernel launches)."""
     keys = ("LQ8_PERSIST", "LQ8_NO_GRAPH")
     old = {k: os.environ.pop(k, None) for k in keys}
     if path == "persistent":
         os.environ["LQ8_PERSIST"] = "1"
+    if path == "graph":
+        os.environ["LQ8_PERSIST"] = "0"
     if path == "plain":
         os.environ["LQ8_NO_GRAPH"] = "1"
     try:
@@ -266,7 +268,7 @@ def check_0_6b(ctx, cfg, tensors_model, tensors, prompt, label):
     model = tensors_model
     t0 = time.time()
     ref = oracle.Model(cfg, tensors)
-    toks, stats = model.generate_greedy(prompt, 128)
+    toks, stats = with_path("graph", lambda: model.generate_greedy(prompt, 128))
     ptoks, pstats = with_path("persistent", lambda: model.generate_greedy(prompt, 128))
     ref_toks, margins = ref.generate_greedy(prompt, 128)
     assert pstats["used_persistent"]
