@@ -504,11 +504,11 @@ PersistShape persist_shape(const lq8_model* m) {
 }
 
 // Whether greedy decode runs as the persistent kernel: wherever the shape is
-// supported, unless LQ8_PERSIST=0 (the replayed graph) or LQ8_NO_GRAPH (plain
-// kernel launches) asks for another path.
+// supported, unless LQ8_PERSIST=0 asks for the per-step kernels (replayed as
+// a graph, or as plain launches under LQ8_NO_GRAPH).
 bool persist_wanted(const lq8_model* m) {
     const char* e = std::getenv("LQ8_PERSIST");
-    if ((e != nullptr && e[0] == '0') || std::getenv("LQ8_NO_GRAPH") != nullptr) return false;
+    if (e != nullptr && e[0] == '0') return false;
     return persist_supported(persist_shape(m), m->ctx->num_cus);
 }
 
