@@ -328,3 +328,31 @@ def test_qwen3_0_6b_varied_tokens(ctx):
     toks = check_0_6b(ctx, cfg, model, tensors, prompt, "varied")
     assert len(set(toks.tolist())) >= 16
     model.free()
+
+
+# intermediate 1568 = 49 blocks: the persistent kernel cuts the down
+# projection's input into 8-pair chunks 8 + 8 + 8 + 1 pairs, the last holding
+# a single block (the odd block's padding staged in the chunk)
+ODD_DOWN = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=1568, num_hidden_layers=2,
+                           num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=96)
+
+
+def test_persistent_down_chunks_with_odd_block(ctx):
+    """The down projection as (tile, input chunk) items whose chunk sums the
+    next layer's RMSNorm stage joins (the block tree) and adds to h2: greedy
+    tokens equal to the oracle's and to the graph path's, and the prefill +
+    decode logits of the two paths' shared kernels bit-exact, on a model whose
+    tokens vary and whose last chunk holds one block."""
+    tensors = oracle.random_q8_tensors(ODD_DOWN, seed=9, layer_std=0.08, norm_jitter=0.1)
+    model = lq8.Qwen3ForCausalLM.load(ctx, ODD_DOWN, tensors)
+    ref = oracle.Model(ODD_DOWN, tensors)
+    prompt = np.random.default_rng(4).integers(0, ODD_DOWN.vocab_size, 12).astype(np.uint32)
+    ptoks, pst = with_path("persistent", lambda: model.generate_greedy(prompt, 40))
+    gtoks, gst = with_path("graph", lambda: model.generate_greedy(prompt, 40))
+    ref_toks, _ = ref.generate_greedy(prompt, 40)
+    assert pst["used_persistent"] and gst["used_graph"]
+    assert ptoks.tolist() == ref_toks.tolist()
+    assert gtoks.tolist() == ref_toks.tolist()
+    assert len(set(ref_toks.tolist())) > 4, "the tokens should vary"
+    model.free()
+    ref.close()
