@@ -46,7 +46,8 @@
  *          max / denominator (see attend()).
  *   exp    orc_expf: double-precision Cody-Waite reduction + degree-13 Taylor
  *          polynomial, rounded once to float.  Agrees with a correctly rounded
- *          expf except in rare last-bit cases.
+ *          expf except in rare last-bit cases; orc_set_libm_exp(1) uses the C
+ *          library's expf instead (the reference's f32::exp on linux-gnu).
  *
  * Build: gcc -O2 -ffp-contract=off -fno-fast-math (Rust never contracts a*b+c).
  */
@@ -62,6 +63,13 @@
 
 static int g_seq_sums = 0;
 void orc_set_sequential_sums(int on) { g_seq_sums = on ? 1 : 0; }
+
+/* 1: the decoder's exp (attention softmax, SiLU) is the host C library's
+ * expf -- on linux-gnu glibc's, the function Rust's f32::exp calls there, so
+ * together with the sequential sums this is the reference's own arithmetic.
+ * 0 (default): orc_expf, the exp the HIP kernels reproduce bit for bit. */
+static int g_libm_exp = 0;
+void orc_set_libm_exp(int on) { g_libm_exp = on ? 1 : 0; }
 
 /* 1 (default): RmsNorm rounds its input, weight and output to bf16 as the
  * reference does.  0: those roundings are skipped.  Used only by the tests
@@ -422,8 +430,11 @@ int orc_rope_apply(const float* x, size_t heads, size_t seq, size_t head_dim, co
     return 0;
 }
 
+/* exp of the decoder's softmax and SiLU (orc_set_libm_exp) */
+static float dec_exp(float x) { return g_libm_exp ? expf(x) : orc_expf(x); }
+
 /* src/tensor.rs:1967-1978 (f32 branch). */
-float orc_silu(float x) { return x / (1.0f + orc_expf(-x)); }
+float orc_silu(float x) { return x / (1.0f + dec_exp(-x)); }
 
 /* Iterator::max_by keeps the last of equal maxima (src/tensor.rs:2475-2480). */
 uint32_t orc_argmax_last(const float* x, size_t n) {
@@ -512,7 +523,7 @@ static void attend_kv(const float* K, const float* V, size_t hd, const float* q,
             if (s > mx) mx = s;
         }
         float sum = 0.0f;
-        for (size_t j = 0; j < L; j++) { sc[j] = orc_expf(sc[j] - mx); sum = sum + sc[j]; }
+        for (size_t j = 0; j < L; j++) { sc[j] = dec_exp(sc[j] - mx); sum = sum + sc[j]; }
         for (size_t j = 0; j < L; j++) sc[j] = sc[j] / sum;
         for (size_t d = 0; d < hd; d++) {
             float o = 0.0f;
@@ -534,10 +545,10 @@ static void attend_kv(const float* K, const float* V, size_t hd, const float* q,
             sc[j] = s;
             if (s > mc) mc = s;
         }
-        for (size_t j = 0; j < nj; j++) sc[j] = orc_expf(sc[j] - mc);
+        for (size_t j = 0; j < nj; j++) sc[j] = dec_exp(sc[j] - mc);
         float lc = sum64(sc, nj);
         float mn = run_m > mc ? run_m : mc;
-        float a = orc_expf(run_m - mn), b = orc_expf(mc - mn);
+        float a = dec_exp(run_m - mn), b = dec_exp(mc - mn);
         for (size_t d = 0; d < hd; d++) {
             float o = 0.0f;
             for (size_t j = 0; j < nj; j++) o = o + sc[j] * V[(js + j) * hd + d];

@@ -36,6 +36,9 @@ void orc_expf_n(const float* x, float* y, size_t n);
 /* 0 = canonical orders (what the GPU computes), 1 = the reference's plain
  * sequential sums.  Global switch, used only to compare the two. */
 void orc_set_sequential_sums(int on);
+/* 1: the decoder's softmax and SiLU use the C library's expf (the
+ * reference's f32::exp on linux-gnu); 0 (default): orc_expf. */
+void orc_set_libm_exp(int on);
 /* 1 (default) = RmsNorm's bf16 roundings as the reference; 0 = skipped (tests
  * that pin the decoder structure against a float64 restatement). */
 void orc_set_bf16_rounding(int on);

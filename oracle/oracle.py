@@ -60,6 +60,7 @@ def lib():
             "orc_bf16_round_n": (None, [vp, vp, sz]),
             "orc_expf_n": (None, [vp, vp, sz]),
             "orc_set_sequential_sums": (None, [C.c_int]),
+            "orc_set_libm_exp": (None, [C.c_int]),
             "orc_set_threads": (None, [C.c_int]),
             "orc_set_bf16_rounding": (None, [C.c_int]),
             "orc_set_activation_quantization": (None, [C.c_int]),
@@ -129,6 +130,12 @@ def expf(x) -> np.ndarray:
 
 def set_sequential_sums(on: bool) -> None:
     lib().orc_set_sequential_sums(1 if on else 0)
+
+
+def set_libm_exp(on: bool) -> None:
+    """The decoder's softmax and SiLU exp: the C library's expf (on
+    linux-gnu glibc's, which the reference's f32::exp calls) or orc_expf."""
+    lib().orc_set_libm_exp(1 if on else 0)
 
 
 def set_bf16_rounding(on: bool) -> None:

@@ -276,10 +276,14 @@ def check_0_6b(ctx, cfg, tensors_model, tensors, prompt, label):
     assert ptoks.tolist() == ref_toks.tolist()
     K = 32
     canon = chain_logits(ref, prompt, toks, K)
+    # the reference's own arithmetic: plain sequential sums and the C
+    # library's expf (Rust's f32::exp on linux-gnu) in the softmax and SiLU
     oracle.set_sequential_sums(True)
+    oracle.set_libm_exp(True)
     try:
         seq = chain_logits(ref, prompt, toks, K)
     finally:
+        oracle.set_libm_exp(False)
         oracle.set_sequential_sums(False)
     dev = np.max(np.abs(canon.astype(np.float64) - seq), axis=1)
     top2 = np.sort(canon, axis=1)[:, -2:]

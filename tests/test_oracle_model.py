@@ -1,5 +1,7 @@
 """CPU: the oracle's decoder numerics against the reference's own unit tests
 (closed forms) and invariants, and the tiny-model golden tokens."""
+import ctypes
+import ctypes.util
 import os
 
 import numpy as np
@@ -132,6 +134,37 @@ def test_sequential_sum_order_close_to_canonical():
         oracle.set_sequential_sums(False)
         m.close()
     assert np.max(np.abs(a - b)) <= 1e-3 * np.max(np.abs(b))
+
+
+def test_reference_arithmetic_mode_close_to_canonical():
+    """The reference's own arithmetic -- plain sequential sums and the C
+    library's expf for the softmax and SiLU (glibc's on linux-gnu, which
+    Rust's f32::exp calls) -- against the canonical orders and orc_expf:
+    logits within f32 rounding and the same greedy pick.  The switch is
+    pinned by SiLU: in the mode, silu(x) is x / (1 + expf(-x)) with the
+    library's expf, bit for bit."""
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    xs = np.linspace(-30.0, 30.0, 2001, dtype=np.float32)
+    m = oracle.Model(TINY, oracle.random_q8_tensors(TINY, seed=79))
+    ids = np.arange(6, dtype=np.uint32) * 13
+    a = m.forward(ids, 0)
+    oracle.set_sequential_sums(True)
+    oracle.set_libm_exp(True)
+    try:
+        for x in xs:
+            x = np.float32(x)
+            want = np.float32(x / (np.float32(1.0) + np.float32(libm.expf(-x))))
+            assert np.float32(oracle.silu(float(x))).view(np.uint32) == want.view(np.uint32), float(x)
+        m.clear_kv_cache()
+        b = m.forward(ids, 0)
+    finally:
+        oracle.set_libm_exp(False)
+        oracle.set_sequential_sums(False)
+        m.close()
+    assert np.max(np.abs(a - b)) <= 1e-3 * np.max(np.abs(b))
+    assert int(np.argmax(a)) == int(np.argmax(b))
 
 
 VARIED = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
