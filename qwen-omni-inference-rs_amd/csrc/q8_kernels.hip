@@ -811,7 +811,7 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(2))) voi
 // order: y = 0 + a_0, then + a_1, ... (the oracle's order), then y = resid + y.
 template <int S, int TM>
 __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(3))) void k_gemm_one(GemmArgs g) {
-    extern __shared__ float gpart[];  // [S][TM][16][64]
+    extern __shared__ float gpart[];  // [S][TM][16][64] floats, then [S][256] u16 (weight scales)
     const int lane = threadIdx.x & 63;
     const int s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ntmb = (g.ntm + TM - 1) / TM;
@@ -833,10 +833,19 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(3))) voi
         ox[t] = (mts[t] * 2 * G * 64 + lane) * 16;
     }
     const int ob = ((bn * 2 + (r32 >> 4)) * g.np * 64 + half * 16 + (r32 & 15)) * 16;
-    const int ow = ((bn * 2 + (r32 >> 4)) * 2 * g.np * 16 + (r32 & 15)) * 2;
     const int b0 = s * GEMM_GROUP;
+    // the weight scales of the wave's 8 blocks for the block's 32 columns in
+    // one 8-byte load per lane: the two 16-row tiles' scales of blocks
+    // b0 .. b0 + 7 are 256 contiguous bytes each (lane l: tile 2 bn + l / 32,
+    // block b0 + (l % 32) / 4, rows 4 (l % 4) .. + 3), staged in the wave's
+    // LDS words [tile][block][16 rows] and read back per block (blocks past
+    // nb read whatever lies there and get a zero scale below)
+    uint16_t* wsl = (uint16_t*)(gpart + S * TM * 16 * 64) + s * 256;
+    {
+        const int off = ((bn * 2 + (lane >> 5)) * 2 * g.np + b0) * 32 + (lane & 31) * 8;
+        *(uint2*)(wsl + lane * 4) = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, off, 0, 0));
+    }
     v4i A[GEMM_GROUP][TM], B[GEMM_GROUP];
-    uint32_t dw[GEMM_GROUP];
     v4i dx[2][TM];
     // operands of block i of the group (codes of blocks past nb are read from
     // block nb - 1 and cancelled by a zero scale below)
@@ -853,7 +862,6 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(3))) voi
         for (int t = 0; t < TM; t++)
             A[i][t] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, oa[t], cs, 0));
         B[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, ob, cs, 0));
-        dw[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, ow, bc * 32, 0);
     };
     const v16i zi = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
@@ -868,7 +876,8 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(3))) voi
     // explains the scale MFMA)
 #pragma unroll
     for (int i = 0; i < GEMM_GROUP; i++) {
-        const uint2 bu = {(lo && b0 + i < nb) ? dw[i] : 0u, 0u};
+        const uint32_t dwi = wsl[(r32 >> 4) * 128 + i * 16 + (r32 & 15)];
+        const uint2 bu = {(lo && b0 + i < nb) ? dwi : 0u, 0u};
 #pragma unroll
         for (int t = 0; t < TM; t++) {
             const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i][t], B[i], zi, 0, 0, 0);
@@ -1207,7 +1216,7 @@ lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const uint32_t* xs, int 
         const size_t tiles2 = (size_t)((g.ntm + 1) / 2) * ntn;
         const bool two = g.ntm >= 2 && S >= 8 && S <= 12 && tiles2 * S >= 3072;
         if (two) g.ntiles = (int)tiles2;
-        const size_t smem1 = (size_t)S * (two ? 2 : 1) * 16 * 64 * sizeof(float);
+        const size_t smem1 = (size_t)S * (two ? 2 : 1) * 16 * 64 * sizeof(float) + (size_t)S * 256 * sizeof(uint16_t);
         const dim3 grid1d((unsigned)g.ntiles);
 #define LQ8_GEMM_ONE_CASE(SS)                                                                          \
     case SS:                                                                                           \
