@@ -806,9 +806,10 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(2))) voi
 // the compute of block i (a one-block window: few registers, so many waves
 // per SIMD hide the load latency; deeper windows and issuing the whole group
 // up front measured slower).  Every wave writes its group sums to LDS and all
-// threads then finish the outputs (consecutive threads own consecutive
-// columns, so the LDS reads and the stores are coalesced), each in group
-// order: y = 0 + a_0, then + a_1, ... (the oracle's order), then y = resid + y.
+// waves then finish the outputs, one 64-lane output row slot per wave and
+// round (consecutive lanes own consecutive columns, so the LDS reads and the
+// stores are coalesced), each in group order: y = 0 + a_0, then + a_1, ...
+// (the oracle's order), then y = resid + y.
 template <int S, int TM>
 __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(3))) void k_gemm_one(GemmArgs g) {
     extern __shared__ float gpart[];  // [S][TM][16][64] floats, then [S][256] u16 (weight scales)
@@ -895,16 +896,24 @@ __global__ __launch_bounds__(64 * S) __attribute__((amdgpu_waves_per_eu(3))) voi
 #pragma unroll
         for (int r = 0; r < 16; r++) gpart[((s * TM + t) * 16 + r) * 64 + lane] = acc[t][r];
     __syncthreads();
-    for (int o = threadIdx.x; o < TM * 16 * 64; o += 64 * S) {
-        const int l = o & 63, r = (o >> 6) & 15, t = o >> 10;
-        float y = 0.0f;
-        for (int u = 0; u < S; u++) y = y + gpart[((u * TM + t) * 16 + r) * 64 + l];
-        const int row = mts[t] * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
-        const int col = bn * 32 + (l & 31);
-        if (bm * TM + t < g.ntm && row < g.m && col < g.n) {
-            const size_t off = (size_t)row * g.n + col;
-            if (g.resid) y = g.resid[off] + y;
-            g.y[off] = y;
+    // output row slot q = (t, r) of the block per wave and round (wave-uniform),
+    // column lane: wave s takes slots s, s + S, ...
+    constexpr int NQ = TM * 16;
+#pragma unroll
+    for (int k = 0; k < (NQ + S - 1) / S; k++) {
+        const int q = s + k * S;
+        if (q < NQ) {
+            const int r = q & 15, t = q >> 4;
+            float y = 0.0f;
+#pragma unroll
+            for (int u = 0; u < S; u++) y = y + gpart[((u * TM + t) * 16 + r) * 64 + lane];
+            const int row = mts[t] * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int col = bn * 32 + (lane & 31);
+            if (bm * TM + t < g.ntm && row < g.m && col < g.n) {
+                const size_t off = (size_t)row * g.n + col;
+                if (g.resid) y = g.resid[off] + y;
+                g.y[off] = y;
+            }
         }
     }
 }
