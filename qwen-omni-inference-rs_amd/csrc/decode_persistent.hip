@@ -4,7 +4,9 @@
 // between.  One workgroup of 512 threads (8 waves) per CU.
 //
 // Work of one step (position pos), per layer l (h_l the layer's input):
-//   P1  RmsNorm(h_l) + q|k|v GEMV, one 16-row tile per item
+//   P1  h_l = h2 of layer l - 1 + its down projection's chunk sums (joined in
+//       the GEMV block tree; published for P4), RmsNorm(h_l) + q|k|v GEMV,
+//       one 16-row tile per item
 //   P2  attention, one (kv head, 64-position segment) per item: per query
 //       head the segment's partials (o_c, m_c, l_c)
 //   P3  o GEMV, one (16-row tile, input chunk) per item: the chunk is csO
@@ -13,7 +15,9 @@
 //       partial sum over its chunk
 //   P4  h2 = h_l + o (the chunk sums meet in the GEMV block tree), then
 //       RmsNorm(h2) + gate and up GEMV (tile i of each) -> silu(gate) * up
-//   P5  down GEMV over the whole intermediate input + residual h2 -> h_l+1
+//   P5  down GEMV, one (16-row tile, input chunk of csD block pairs) per
+//       item: the tile's partial sum over its chunk (the residual h2 is
+//       added where the chunk sums meet, in the next P1 or in P6)
 // then P6: final RmsNorm and the lm_head, one wave per 16-row tile, each
 // workgroup keeping the greedy pick of its tiles; the next step starts with
 // every workgroup reducing the workgroups' picks to the token.  Item i of a
