@@ -120,7 +120,7 @@ __device__ __forceinline__ float qk_dot128(const float* q, const float* k) {
     const float4* q4 = (const float4*)q;
     const float4* k4 = (const float4*)k;
     float s = 0.0f;
-#pragma unroll 8
+#pragma unroll
     for (int d4 = 0; d4 < 32; d4++) {
         const float4 a = q4[d4], b = k4[d4];
         s = s + a.x * b.x;
