@@ -169,25 +169,26 @@ __device__ __forceinline__ void seg_scores(const float4* kreg, int nj, int knew_
     }
 }
 
-// o = sum_j e[j] * vs[j][d] for j = 0 .. nj - 1 in order, from +0.  Eight
+// o = sum_j e[j] * vs[j][d] for j = 0 .. nj - 1 in order, from +0.  Sixteen
 // steps per batch: their LDS reads go out together (e is 16-byte aligned and
 // wave-uniform), then the chain; the order of the adds is unchanged.
 __device__ __forceinline__ float pv_chain(const float* e, const float* vs, int d, int nj) {
     float o = 0.0f;
     int j = 0;
-    for (; j + 8 <= nj; j += 8) {
-        const float4 e0 = *(const float4*)(e + j), e1 = *(const float4*)(e + j + 4);
-        float v[8];
+    for (; j + 16 <= nj; j += 16) {
+        float4 ev[4];
+        float v[16];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = vs[(j + u) * 128 + d];
-        o = o + e0.x * v[0];
-        o = o + e0.y * v[1];
-        o = o + e0.z * v[2];
-        o = o + e0.w * v[3];
-        o = o + e1.x * v[4];
-        o = o + e1.y * v[5];
-        o = o + e1.z * v[6];
-        o = o + e1.w * v[7];
+        for (int q = 0; q < 4; q++) ev[q] = *(const float4*)(e + j + 4 * q);
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = vs[(j + u) * 128 + d];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            o = o + ev[q].x * v[4 * q];
+            o = o + ev[q].y * v[4 * q + 1];
+            o = o + ev[q].z * v[4 * q + 2];
+            o = o + ev[q].w * v[4 * q + 3];
+        }
     }
     for (; j < nj; j++) o = o + e[j] * vs[j * 128 + d];
     return o;
