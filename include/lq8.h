@@ -203,7 +203,7 @@ lq8_status lq8_bench_grid_sync(lq8_ctx* ctx, int kind, int nwg, int rounds, floa
  * LQ8_PTRACE_POINTS.  Other builds return LQ8_ERR_INVALID_ARG. */
 #define LQ8_PTRACE_WG 512
 #define LQ8_PTRACE_LAYERS 64
-#define LQ8_PTRACE_POINTS 16
+#define LQ8_PTRACE_POINTS 17
 enum {
     LQ8_PT_P1_START = 0,     /* RmsNorm + q|k|v: workgroup enters */
     LQ8_PT_P1_NORMED = 1,    /* the layer input has arrived and is normalised */
@@ -211,7 +211,7 @@ enum {
     LQ8_PT_P2_QKV_IN = 3,    /* the segment item's q, k, v have arrived */
     LQ8_PT_P2_SCORES = 4,    /* scores and softmax partials done */
     LQ8_PT_P2_PARTIALS = 5,  /* the segment's partials are out */
-    LQ8_PT_P3_START = 6,     /* o GEMV: workgroup enters (combine done where it ran) */
+    LQ8_PT_P3_START = 6,     /* o GEMV: workgroup enters */
     LQ8_PT_P3_STAGED = 7,    /* the attention output has arrived */
     LQ8_PT_P4_START = 8,     /* RmsNorm + gate|up: workgroup enters */
     LQ8_PT_P4_STAGED = 9,    /* h2 has arrived */
@@ -220,7 +220,8 @@ enum {
     LQ8_PT_P5_DONE = 12,     /* the down tile + residual is out */
     LQ8_PT_P6_START = 13,    /* lm_head: workgroup enters */
     LQ8_PT_P6_NORMED = 14,   /* the last layer's output has arrived and is normalised */
-    LQ8_PT_P6_DONE = 15      /* the workgroup's greedy pick is out */
+    LQ8_PT_P6_DONE = 15,     /* the workgroup's greedy pick is out */
+    LQ8_PT_P2_COMBINED = 16  /* attention: the kv head's segments are combined and out (the combining item) */
 };
 lq8_status lq8_persist_trace(lq8_ctx* ctx, uint64_t* out, size_t count);
 
@@ -275,6 +276,15 @@ typedef struct {
     uint32_t used_persistent; /* 1 if the decode steps ran as one persistent kernel (greedy) */
 } lq8_gen_stats;
 /* Greedy generation; the token loop stays on the device.  out_tokens: max_new.
+ * The decode steps run as one persistent cooperative kernel (all steps, all
+ * layers, the lm_head and the pick in one launch) when the model's shape
+ * fits it: head_dim 128, hidden_size a multiple of 32 up to 1024,
+ * intermediate_size a multiple of 32 up to 4096, num_heads * 128 <= 2048,
+ * num_heads / num_kv_heads <= 16, and a device with cooperative launch;
+ * max_positions is not limited.  lq8_persist_plan tells in advance; the
+ * environment variable LQ8_PERSIST=0 turns it off.  Other shapes run one
+ * kernel sequence per step, replayed as a HIP graph (lq8_gen_stats tells
+ * which ran).  Both give the same tokens, bit for bit the same logits.
  * Each decode step forwards the token generated last.  The reference's loop
  * as written does not: the `let next_token` in its loop body
  * (src/generate.rs:650) shadows the binding of src/generate.rs:632 only for
@@ -284,6 +294,37 @@ typedef struct {
  * the model repeats its first token. */
 lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,
                                uint32_t* out_tokens, lq8_gen_stats* stats);
+
+/* Whether lq8_generate_greedy of a model with this configuration runs as
+ * the persistent kernel on num_workgroups workgroups (the library launches
+ * one per compute unit), and the kernel's plan for it: the o and down
+ * projections' input chunks and its LDS map (in floats).  Host-only: needs
+ * no device.  A diagnostic without counterpart in the reference. */
+typedef struct {
+    uint32_t supported;          /* 1: the persistent kernel runs this shape */
+    uint32_t o_chunk_blocks;     /* the o projection's input chunks: blocks each, and how many */
+    uint32_t o_chunks;
+    uint32_t down_chunk_pairs;   /* the down projection's input chunks: block pairs each, and how many */
+    uint32_t down_chunks;
+    uint32_t lds_bytes;          /* dynamic LDS per workgroup */
+    uint32_t lds_gather_floats;  /* hand-off gathers, from 0 */
+    uint32_t lds_xs_offset;      /* the staged GEMV input */
+    uint32_t lds_gs_offset;      /* the waves' group sums */
+    uint32_t lds_red_offset;     /* reduction words (16) */
+    uint32_t lds_attention_floats; /* an attention item's region, from 0 */
+    uint32_t lds_combine_floats;   /* the segment combine's region, from 0 */
+} lq8_persist_info;
+lq8_status lq8_persist_plan(const lq8_qwen3_config* cfg, uint32_t num_workgroups, lq8_persist_info* out);
+/* The per-workgroup greedy picks of the last persistent decode step (back 0)
+ * or of the step before it (back 1) of the model's last lq8_generate_greedy
+ * call: workgroup w's largest logit over its lm_head rows (the rows of the
+ * 16-row tiles t with (t / 8) % P == w, P workgroups; the last index on
+ * ties) as f32 bits and its token index.  *count receives P; capacity must
+ * be at least P.  A diagnostic without counterpart in the reference (it lets
+ * a test compare the kernel's logits at the picked rows with another
+ * implementation's). */
+lq8_status lq8_model_persist_picks(lq8_model* m, uint32_t back, float* values, uint32_t* indices, size_t capacity,
+                                   size_t* count);
 
 /* ---- sampling ----------------------------------------------------------------
  * The fields of GenerationConfig (src/generate.rs:40-128) besides

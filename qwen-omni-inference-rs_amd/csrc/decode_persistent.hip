@@ -7,11 +7,13 @@
 //   P1  h_l = h2 of layer l - 1 + its down projection's chunk sums (joined in
 //       the GEMV block tree; published for P4), RmsNorm(h_l) + q|k|v GEMV,
 //       one 16-row tile per item
-//   P2  attention, one (kv head, 64-position segment) per item: per query
-//       head the segment's partials (o_c, m_c, l_c)
+//   P2  attention, one (64-position segment, kv head) per item: per query
+//       head the segment's partials (o_c, m_c, l_c); each item then counts
+//       itself in on its kv head's arrival counter, and the item whose
+//       arrival completes the step's count combines the kv head's segments
+//       (any number of them) and publishes its heads' attention output
 //   P3  o GEMV, one (16-row tile, input chunk) per item: the chunk is csO
-//       blocks of the attention output (whole heads or parts of one), whose
-//       segments the item combines itself; the item's output is the tile's
+//       blocks of the attention output; the item's output is the tile's
 //       partial sum over its chunk
 //   P4  h2 = h_l + o (the chunk sums meet in the GEMV block tree), then
 //       RmsNorm(h2) + gate and up GEMV (tile i of each) -> silu(gate) * up
@@ -34,8 +36,14 @@
 // word per wave, and the fetch ends about one memory round trip after its
 // last word lands).  Buffers are per layer; a buffer is written again only
 // one step later, by a producer whose inputs depend on the outputs of every
-// reader of the earlier value.  Tags grow across launches (the host keeps the
-// count) and zeroed buffers carry tag 0, which no step uses.
+// reader of the earlier value.  The greedy picks are the exception: every
+// workgroup reads them, including workgroups that produce nothing else, so
+// they alternate between two buffers by the parity of the step's tag (a
+// workgroup cannot write step s + 2's pick before every workgroup has
+// published step s + 1's, which each does after reading step s's).  Tags
+// grow across launches (the host keeps the count) and zeroed buffers carry
+// tag 0, which no step uses.  The arrival counters only grow: after a step
+// each holds arr0 plus the items of every step of the launch so far.
 //
 // Weights do not depend on the step's data: a workgroup issues the weight
 // loads of its next phase's item (into registers) before it waits for the
@@ -87,7 +95,11 @@ constexpr int NW_H = (1024 + PT - 1) / PT;                         // a hidden v
 constexpr int NW_QKV = ((ATT_MAX_GROUP + 2) * 128 + PT - 1) / PT;  // q of a kv head's group, k, v
 constexpr int NW_RES = PERSIST_FETCH;                             // h and the o chunk sums
 constexpr int NW_ACT = (4096 + 16 + PT - 1) / PT;                  // silu(gate) * up (<= 4096) and 16 rows of h2
-constexpr int NW_PART = 16;                                       // 8 segments x 2 words per run
+constexpr int NW_ATT = (2048 + PT - 1) / PT;                       // an o input chunk of the attention output (<= 2048)
+constexpr int CMB_SEGS = 64;                                       // combine: segments per batch of (m_c, l_c) words
+constexpr int NW_ML = (CMB_SEGS * ATT_MAX_GROUP * 2 + PT - 1) / PT;  // combine: a batch's (m_c, l_c) words
+constexpr int CMB_EK = (ATT_MAX_GROUP * 128 + PT - 1) / PT;        // combine: output elements per thread, at most
+constexpr int NW_OC = 16;                                          // combine: o_c words per thread and round
 constexpr int CHH = 16 / PW;    // block pairs per wave group of a hidden-long tile (hidden <= 1024: <= 16 pairs)
 #ifndef LQ8_LMU
 #define LQ8_LMU 4
@@ -432,6 +444,128 @@ __device__ __forceinline__ void wg_argmax(float& bv, int& bi, float* pv, int* pi
         }
 }
 
+// LDS writes of a wave visible to the wave's own later reads
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The segment combine of kv head g's G query heads (the order of the o GEMV's
+// XS_ATTN staging): per head, in segment order, m' = max(m, m_c),
+// a_c = exp(m - m'), b_c = exp(m_c - m'), den = den a_c + b_c l_c; per
+// element num = num a_c + b_c o_c; x = num / den, published to attl (heads
+// concatenated).  Run by the attention item whose arrival completed the kv
+// head's count for the step: the count only elects the workgroup, every
+// segment's partials are read as tagged words.  Segments go in batches of
+// CMB_SEGS: per head one wave takes the batch's running maximum in order
+// (lane 0), the coefficients in parallel (lane j: segment j), then den in
+// order (lane 0); each thread then carries up to CMB_EK output elements
+// through the batch, fetching their o_c words NW_OC at a time.
+// LDS: ml [CMB_SEGS][G][2] (m_c, l_c), cf [CMB_SEGS][G][2] (a_c, b_c),
+// st [G][2] (running m, den).  false: the launch is aborting.
+__device__ __forceinline__ bool combine_heads(unsigned tag, int C, int g, int G, int NH, const uint64_t* partb,
+                                              uint64_t* attl, float* sm, unsigned* abort_flag, volatile int* bad) {
+    const int tid = tid_here(), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float* ml = sm;
+    float* cf = ml + CMB_SEGS * 2 * G;
+    float* st = cf + CMB_SEGS * 2 * G;
+    const int GE = G * 128;                            // output elements
+    const int EK = (GE + PT - 1) / PT;                 // elements per thread (<= CMB_EK)
+    int SBs = 0;                                       // log2 of the segments per o_c round
+    while ((2 << SBs) * EK <= NW_OC) SBs++;            // (the largest power of two with EK of them <= NW_OC)
+    const int SBm = (1 << SBs) - 1;
+    const uint64_t* pb = partb + (size_t)(g * G) * ATT_PART_STRIDE;
+    const size_t segw = (size_t)NH * ATT_PART_STRIDE;  // words per segment
+    float num[CMB_EK];
+#pragma unroll
+    for (int k = 0; k < CMB_EK; k++) num[k] = 0.0f;
+    if (tid < G) {
+        st[2 * tid] = -__builtin_huge_valf();
+        st[2 * tid + 1] = 0.0f;
+    }
+    for (int cb = 0; cb < C; cb += CMB_SEGS) {
+        const int nc = min(CMB_SEGS, C - cb);
+        // (m_c, l_c) of the batch: word i = (j G + h) 2 + {0: m_c, 1: l_c}
+        tfetch<NW_ML>(tag, [&](int t, int u) { return t + u * PT < nc * G * 2; },
+                      [&](int t, int u) {
+                          const int i = t + u * PT, j = i / (2 * G), h = (i >> 1) - j * G;
+                          return pb + (size_t)(cb + j) * segw + h * ATT_PART_STRIDE + 128 + (i & 1);
+                      },
+                      [&](int t, int u) { return ml + t + u * PT; }, abort_flag, bad);
+        lds_sync();
+        if (bad_now(bad)) return false;
+        for (int h = wave; h < G; h += PW) {
+            if (lane == 0) {
+                // m before and after each segment, in order
+                float m = st[2 * h];
+                for (int j = 0; j < nc; j++) {
+                    const float mc = ml[(j * G + h) * 2];
+                    const float mn = m > mc ? m : mc;
+                    cf[(j * G + h) * 2] = m;
+                    cf[(j * G + h) * 2 + 1] = mn;
+                    m = mn;
+                }
+                st[2 * h] = m;
+            }
+            wave_sync();
+            if (lane < nc) {
+                const int q = (lane * G + h) * 2;
+                const float mp = cf[q], mn = cf[q + 1], mc = ml[q];
+                cf[q] = expf_cr(mp - mn);
+                cf[q + 1] = expf_cr(mc - mn);
+            }
+            wave_sync();
+            if (lane == 0) {
+                float den = st[2 * h + 1];
+                for (int j = 0; j < nc; j++) {
+                    const int q = (j * G + h) * 2;
+                    den = den * cf[q] + cf[q + 1] * ml[q + 1];
+                }
+                st[2 * h + 1] = den;
+            }
+        }
+        lds_sync();
+        for (int sb = 0; sb < nc; sb += SBm + 1) {
+            // unit u: element tid + (u >> SBs) PT of segment cb + sb + (u & SBm)
+            float ov[NW_OC];
+            tfetch<NW_OC>(tag,
+                          [&](int t, int u) {
+                              const int k = u >> SBs, j = u & SBm;
+                              return k < EK && t + k * PT < GE && sb + j < nc;
+                          },
+                          [&](int t, int u) {
+                              const int k = u >> SBs, j = u & SBm, e = t + k * PT;
+                              return pb + (size_t)(cb + sb + j) * segw + (e >> 7) * ATT_PART_STRIDE + (e & 127);
+                          },
+                          [&](int t, int u) { return &ov[u]; }, abort_flag, bad);
+            lds_sync();
+            if (bad_now(bad)) return false;
+            const int t = tid_here();
+#pragma unroll
+            for (int u = 0; u < NW_OC; u++) {
+                const int k = u >> SBs, j = u & SBm, e = t + k * PT;
+                if (k < EK && e < GE && sb + j < nc) {
+                    const int q = ((sb + j) * G + (e >> 7)) * 2;
+                    const float add = cf[q + 1] * ov[u];
+#pragma unroll
+                    for (int kk = 0; kk < CMB_EK; kk++)
+                        if (kk == k) num[kk] = num[kk] * cf[q] + add;
+                }
+            }
+        }
+        lds_sync();  // ml and cf are written again by the next batch
+    }
+    const int t = tid_here();
+#pragma unroll
+    for (int k = 0; k < CMB_EK; k++) {
+        const int e = t + k * PT;
+        if (k < EK && e < GE) tput(attl + (size_t)g * GE + e, __fdiv_rn(num[k], st[2 * (e >> 7) + 1]), tag);
+    }
+    return true;
+}
+
 struct Dims {
     int H, I, NH, NKV, G, QD, KD, QKV, npH, nbH, npQ, nbQ, npI, nbI, T1, TH, TI, T6;
 };
@@ -462,11 +596,13 @@ __device__ __forceinline__ Dims dims_of(CArgs& a) {
     float* red = sm + a.red_off;                                                                           \
     uint64_t* qkvb = a.qkvb + (size_t)l * D.QKV;                                                           \
     uint64_t* partb = a.partb + (size_t)l * a.cmax * D.NH * ATT_PART_STRIDE;                               \
+    uint64_t* attl = a.attb + (size_t)l * D.QD;                                                            \
     uint64_t* resl = a.resb + (size_t)l * (1 + a.nchO) * D.H; /* [h_l | o chunk sums] */                   \
     uint64_t* h2b = a.h2b + (size_t)l * (1 + a.nchD) * D.H; /* [h2 | down chunk sums] */                 \
     uint64_t* actb = a.actb + (size_t)l * D.I;                                                             \
     const int n3 = D.TH * a.nchO;                                                                          \
     (void)tid; (void)lane; (void)pos; (void)Lw; (void)xs; (void)gs; (void)red; (void)qkvb; (void)partb;    \
+    (void)attl;                                                                                            \
     (void)resl; (void)h2b; (void)actb; (void)n3
 
 // The jobs of the phases' items (CH5: pairs per group of a down item).
@@ -491,9 +627,11 @@ template <int CH5>
 __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __restrict__ pa) {
     extern __shared__ __align__(16) float sm[];
     __shared__ int bad_s;
+    __shared__ int elect_s;
     __shared__ float pick_v[PW];
     __shared__ int pick_i[PW];
     volatile int* bad = &bad_s;
+    volatile int* elect = &elect_s;
     const int P = gridDim.x, w = blockIdx.x;
     if (threadIdx.x == 0) bad_s = 0;
     lds_sync();
@@ -513,7 +651,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             tok = *a.d_tok;
         } else {
             float* f = sm;
-            tfetch_lin<NW_ARG>(2 * P, tag - 1, a.argb, f, a.abort_flag, bad);
+            tfetch_lin<NW_ARG>(2 * P, tag - 1, a.argb + (size_t)((tag - 1) & 1) * 2 * P, f, a.abort_flag, bad);
             lds_sync();
             if (bad_now(bad)) goto done;
             const int tid = tid_here();
@@ -585,12 +723,15 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 if (w < n3) job_load<1, CHH>(job_o(a, D, Lw, w), R3);
             }
 
-            // ---- P2: attention per (kv head, segment)
+            // ---- P2: attention per (segment, kv head) item; the item whose
+            // arrival completes the kv head's count combines its segments
             PTRACE(LQ8_PT_P2_START);
             {
                 LAYER_LOCALS;
                 const int L1 = pos + 1, C = (L1 + ATT_SEG - 1) / ATT_SEG, G = D.G;
-                const int items2 = D.NKV * a.cmax;
+                const int items2 = C * D.NKV;
+                // every counter's value once this step's items have all arrived
+                const uint64_t target = a.arr0 + persist_arrivals_below(pos + 1) - persist_arrivals_below(a.pos0);
                 float* qs = sm;                   // [G][128]
                 float* kn = qs + G * 128;         // [128]
                 float* vn = kn + 128;             // [128]
@@ -599,8 +740,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 float* ks = sm + seg_ks_off(G);   // [64][KPAD], later the V rows [64][128]
                 float* qraw = ks;                 // the fetched q (G heads), k, v: [G + 2][128]
                 for (int it = w; it < items2; it += P) {
-                    const int g = it / a.cmax, c = it % a.cmax;
-                    if (c >= C) continue;
+                    const int c = it / D.NKV, g = it - c * D.NKV;
                     const int js = c * ATT_SEG, nj = min(ATT_SEG, L1 - js);
                     const bool last = c == C - 1;
                     const int newrow = last ? pos - js : -1;
@@ -661,70 +801,36 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     }
                     PTRACE(LQ8_PT_P2_PARTIALS);
                     lds_sync();
+                    // count in; the item that completes the count combines
+                    if (tid == 0) {
+                        const uint64_t before = __hip_atomic_fetch_add(a.arrc + (size_t)l * D.NKV + g, (uint64_t)1,
+                                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        *elect = before + 1 == target ? 1 : 0;
+                    }
+                    lds_sync();
+                    if (__builtin_amdgcn_readfirstlane(*elect)) {
+                        if (!combine_heads(tag, C, g, G, D.NH, partb, attl, sm, a.abort_flag, bad)) goto done;
+                        PTRACE(LQ8_PT_P2_COMBINED);
+                        lds_sync();
+                    }
                 }
             }
 
-            // ---- P3: o tile over one input chunk (the attention output of
-            // its heads, combined from the segment partials) -> chunk sums
+            // ---- P3: o tile over one input chunk of the attention output
+            // -> chunk sums
             PTRACE(LQ8_PT_P3_START);
             {
                 LAYER_LOCALS;
-                const int L1 = pos + 1, C = (L1 + ATT_SEG - 1) / ATT_SEG;
                 for (int it = w; it < n3; it += P) {
                     const Job J = job_o(a, D, Lw, it);
                     if (it != w) job_load<1, CHH>(J, R3);
                     const int t = it / a.nchO, c = it - t * a.nchO;
                     const int i0 = J.p0 * 64, rng = min(J.npv * 64, D.QD - i0);
-                    const int hA = i0 >> 7, nh = ((i0 + rng - 1) >> 7) - hA + 1;
-                    // the partials of the chunk's heads: per segment one run of
-                    // nh * ATT_PART_STRIDE words (o_c[128], m_c, l_c, 2 unused)
-                    const int R = nh * ATT_PART_STRIDE;
-                    float* pr = sm;                  // [C][R] the runs
-                    float* coef = pr + C * R;        // [C][nh][2]: a_c, b_c
-                    float* dens = coef + 2 * C * nh; // [nh]
-                    const uint64_t* run0 = partb + (size_t)hA * ATT_PART_STRIDE;
-                    const size_t seg_words = (size_t)D.NH * ATT_PART_STRIDE;
-                    // thread t: words t and t + PT of every segment's run
-                    tfetch<NW_PART>(tag,
-                           [&](int tt, int u) {
-                               const int k = tt + (u & 1) * PT;
-                               return (u >> 1) < C && k < R && k % ATT_PART_STRIDE < 130;
-                           },
-                           [&](int tt, int u) { return run0 + (size_t)(u >> 1) * seg_words + tt + (u & 1) * PT; },
-                           [&](int tt, int u) { return pr + (u >> 1) * R + tt + (u & 1) * PT; }, a.abort_flag, bad);
+                    tfetch_lin<NW_ATT>(rng, tag, attl + i0, xs, a.abort_flag, bad);
+                    stage_pad(xs, rng, J.npv);
                     lds_sync();
                     if (bad_now(bad)) goto done;
                     PTRACE(LQ8_PT_P3_STAGED);
-                    // the combine of the o GEMV's XS_ATTN staging: per head, in
-                    // segment order, m' = max(m, m_c), a_c = exp(m - m'),
-                    // b_c = exp(m_c - m'), den = den a_c + b_c l_c; per element
-                    // num = num a_c + b_c o_c, x = num / den
-                    if (tid < nh) {
-                        float m = -__builtin_huge_valf(), den = 0.0f;
-                        for (int cc = 0; cc < C; cc++) {
-                            const int q = cc * nh + tid;
-                            const float mc = pr[cc * R + tid * ATT_PART_STRIDE + 128];
-                            const float lc = pr[cc * R + tid * ATT_PART_STRIDE + 129];
-                            const float mn = m > mc ? m : mc;
-                            const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
-                            coef[2 * q] = ea;
-                            coef[2 * q + 1] = eb;
-                            den = den * ea + eb * lc;
-                            m = mn;
-                        }
-                        dens[tid] = den;
-                    }
-                    lds_sync();
-                    for (int k = tid; k < rng; k += PT) {
-                        const int hh = ((i0 + k) >> 7) - hA;
-                        float num = 0.0f;
-                        for (int cc = 0; cc < C; cc++)
-                            num = num * coef[2 * (cc * nh + hh)] + coef[2 * (cc * nh + hh) + 1] *
-                                                                            pr[cc * R + hh * ATT_PART_STRIDE + ((i0 + k) & 127)];
-                        xs[k] = __fdiv_rn(num, dens[hh]);
-                    }
-                    stage_pad(xs, rng, J.npv);
-                    lds_sync();
                     job_dot<1, CHH>(J, R3, xs, gs);
                     lds_sync();
                     if (tid < 64) {
@@ -951,8 +1057,9 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             // lanes 0..15 hold the wave's pick (rows of lanes 16..63 were invalid)
             wg_argmax(bv, bi, pick_v, pick_i);
             if (tid == 0) {
-                tput(a.argb + 2 * w, bv, tag);
-                tput(a.argb + 2 * w + 1, __uint_as_float((unsigned)bi), tag);
+                uint64_t* ab = a.argb + (size_t)(tag & 1) * 2 * P;
+                tput(ab + 2 * w, bv, tag);
+                tput(ab + 2 * w + 1, __uint_as_float((unsigned)bi), tag);
             }
             // the step's one fenced barrier: the workgroup's key/value cache
             // stores of this step are visible to its waves' loads of the next
@@ -966,7 +1073,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
         CArgs& a = *opaque_args(pa);
         const unsigned tag = a.tag0 + (unsigned)a.steps - 1;
         float* f = sm;
-        tfetch_lin<NW_ARG>(2 * P, tag, a.argb, f, a.abort_flag, bad);
+        tfetch_lin<NW_ARG>(2 * P, tag, a.argb + (size_t)(tag & 1) * 2 * P, f, a.abort_flag, bad);
         lds_sync();
         if (bad_now(bad)) goto done;
         const int tid = tid_here();
@@ -988,65 +1095,71 @@ done:
 }  // namespace
 
 bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
-    if (s.head_dim != 128 || s.NKV <= 0 || s.NH % s.NKV || P <= 0) return false;
+    if (s.head_dim != 128 || s.NKV <= 0 || s.NH <= 0 || s.NH % s.NKV || s.max_pos <= 0 || P <= 0) return false;
     const int G = s.NH / s.NKV;
     if (G > ATT_MAX_GROUP) return false;
-    // hidden <= 1024 lets a wave hold a whole q|k|v, gate/up or lm_head tile
-    // group in one slot and the lm_head tile (16 block pairs) in registers;
-    // intermediate <= 4096 keeps the down tile within 4 slots per wave; at
-    // most 8 segments (the combine and the fetches are sized for them)
-    if (s.H % 32 || s.H > 1024 || s.I % 32 || s.I > 4096 || s.NH * 128 > 2048) return false;
-    const int cmax = (s.max_pos + ATT_SEG - 1) / ATT_SEG;
-    if (cmax > 8) return false;
+    // hidden <= 1024: a q|k|v, gate/up or lm_head tile (<= 16 block pairs)
+    // is one group of CHH pairs per wave, the lm_head tile fits the units
+    // of a wave's ring (LMQ * LMU pairs), and a hidden vector is NW_H words
+    // per thread; intermediate <= 4096; the attention output (NH * 128) is
+    // at most one P3 fetch (NW_ATT words per thread)
+    if (s.H % 32 || s.H < 32 || s.H > 1024 || s.I % 32 || s.I < 32 || s.I > 4096 || s.NH * 128 > 2048) return false;
     const int QD = s.NH * 128, nbQ = QD / 32, TH = s.H / 16;
-    const int cap = PERSIST_FETCH * PERSIST_THREADS;  // words one fetch holds
+    const int npH = (s.H / 32 + 1) / 2, npI = (s.I / 32 + 1) / 2;
+    if (npH > CHH * PW || npH > LMQ * LMU || s.H > NW_H * PT || QD > NW_ATT * PT) return false;
+    const int cap = NW_RES * PT;  // words of one gather of a hidden vector and its chunk sums
     // o input chunks: the smallest power-of-two block count whose items fit
-    // the workgroups (or one chunk over the whole input)
+    // the workgroups (or one chunk over the whole input, or the widest chunk
+    // a workgroup's waves hold: then a workgroup takes several items)
     int csO = 2;
     auto nch_of = [&](int cs) { return (nbQ + cs - 1) / cs; };
-    while (csO < nbQ &&
+    while (csO < nbQ && csO < 2 * CHH * PW &&
            (TH * nch_of(csO) > P || nch_of(csO) > PERSIST_NCH || (1 + nch_of(csO)) * s.H > cap))
         csO *= 2;
     const int nchO = nch_of(csO);
-    // a chunk's pairs fit one group per wave (CHH pairs each)
-    if (nchO > PERSIST_NCH || (1 + nchO) * s.H > cap || std::min(csO, nbQ) > 2 * CHH * PW) return false;
+    const int pairsO = (std::min(csO, nbQ) + 1) / 2;  // pairs of the widest o chunk
+    // P4 gathers h and the o chunk sums; a chunk's pairs are one group per wave
+    if (nchO > PERSIST_NCH || (1 + nchO) * s.H > cap || pairsO > CHH * PW) return false;
     // down input chunks: the smallest power-of-two pair count, at least one
-    // group per wave, whose (tile, chunk) items fit the workgroups (or one
-    // chunk over the whole input); a wave's group holds <= 8 pairs
-    const int npI = (s.I / 32 + 1) / 2;
-    int csD = PERSIST_THREADS / 64;
+    // pair per wave, whose (tile, chunk) items fit the workgroups (or one
+    // chunk over the whole input)
+    int csD = PW;
     auto nchd_of = [&](int cs) { return (npI + cs - 1) / cs; };
     while (csD < npI &&
            (TH * nchd_of(csD) > P || nchd_of(csD) > PERSIST_NCH || (1 + nchd_of(csD)) * s.H > cap))
         csD *= 2;
     const int nchD = nchd_of(csD);
-    if (nchD > PERSIST_NCH || (1 + nchD) * s.H > cap || csD > 8 * (PERSIST_THREADS / 64)) return false;
-    const int pairsO = (std::min(csO, nbQ) + 1) / 2;  // pairs of the widest chunk
-    const int rng = std::min(pairsO * 64, QD);
-    const int nhc = rng / 128 + 2;  // heads a chunk touches, at most
-    if (2 * cmax * nhc + cmax * rng > cap || s.I + 16 > cap || 2 * P > cap) return false;
+    // P1 and P6 gather h2 and the down chunk sums; a down item's pairs are
+    // CH5 = csD / PW per wave (a kernel variant for CH5 = 1, 2, 4, 8); its
+    // input chunk is one P5 fetch
+    if (nchD > PERSIST_NCH || (1 + nchD) * s.H > cap || csD > 8 * PW || std::min(csD, npI) * 64 > NW_ACT * PT)
+        return false;
+    // the picks (2 words per workgroup) are one fetch; an attention item's
+    // q, k, v one more; a combine batch's (m_c, l_c) and a thread's output
+    // elements fit their fetches
+    if (2 * P > NW_ARG * PT || (G + 2) * 128 > NW_QKV * PT || CMB_SEGS * G * 2 > NW_ML * PT || G * 128 > CMB_EK * PT)
+        return false;
     PersistLayout L{};
     L.csO = csO;
     L.nchO = nchO;
     L.csD = csD;
     L.nchD = nchD;
-    int fr = std::max((1 + nchO) * s.H, 4 * cmax * nhc + cmax * rng + nhc);
-    fr = std::max(fr, (1 + nchD) * s.H);
-    fr = std::max(fr, 2 * P);
-    fr = std::max(fr, 16);
+    // LDS, in floats.  From 0: the gathers (fr), the attention item's
+    // region (att_floats) and the combine's (comb_floats), never in use at
+    // once; then the staged GEMV input xs (a hidden vector, an o chunk or a
+    // down chunk), the wave group sums gs (two tiles) and red.
+    int fr = std::max(std::max((1 + nchO) * s.H, (1 + nchD) * s.H), 2 * P);
     L.fr = (fr + 3) & ~3;
-    const int npH = (s.H / 32 + 1) / 2;
-    const int xsz = std::max(std::max(npH, npI), pairsO) * 64;
+    const int xsz = std::max(std::max(npH, std::min(csD, npI)), pairsO) * 64;
     L.xs_off = L.fr;
     L.gs_off = L.xs_off + xsz;
-    L.red_off = L.gs_off + 2 * (PERSIST_THREADS / 64) * 16;
+    L.red_off = L.gs_off + 2 * PW * 16;
     const int total = L.red_off + 16;
     L.att_floats = seg_ks_off(G) + ATT_SEG * KPAD;
-    if ((G + 2) * 128 > ATT_SEG * KPAD) return false;
-    L.smem_bytes = std::max(total, L.att_floats) * (int)sizeof(float);
+    if ((G + 2) * 128 > ATT_SEG * KPAD) return false;  // the fetched q, k, v sit in the key rows' region
+    L.comb_floats = 4 * CMB_SEGS * G + 2 * G;
+    L.smem_bytes = std::max(std::max(total, L.att_floats), L.comb_floats) * (int)sizeof(float);
     if (L.smem_bytes > 64 * 1024) return false;
-    const size_t Ls = 1;  // per layer; the host multiplies by the layer count
-    (void)Ls;
     L.words = 0;
     if (out) *out = L;
     return true;
@@ -1072,6 +1185,33 @@ lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, i
 }  // namespace lq8
 
 using namespace lq8;
+
+extern "C" lq8_status lq8_persist_plan(const lq8_qwen3_config* cfg, uint32_t num_workgroups, lq8_persist_info* out) {
+    if (!cfg || !out) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (num_workgroups == 0 || num_workgroups > 65536) return fail(LQ8_ERR_INVALID_ARG, "num_workgroups must be 1 .. 65536");
+    const PersistShape sh{(int)cfg->hidden_size, (int)cfg->intermediate_size, (int)cfg->num_heads,
+                          (int)cfg->num_kv_heads, (int)cfg->head_dim, (int)cfg->max_positions};
+    *out = lq8_persist_info{};
+    PersistLayout L{};
+    // sizes beyond int range are not the kernel's
+    if (cfg->hidden_size > 65536 || cfg->intermediate_size > 65536 || cfg->num_heads > 65536 ||
+        cfg->num_kv_heads > 65536 || cfg->head_dim > 65536 || cfg->max_positions > (1u << 30) ||
+        !persist_layout(sh, (int)num_workgroups, &L))
+        return LQ8_OK;
+    out->supported = 1;
+    out->o_chunk_blocks = (uint32_t)L.csO;
+    out->o_chunks = (uint32_t)L.nchO;
+    out->down_chunk_pairs = (uint32_t)L.csD;
+    out->down_chunks = (uint32_t)L.nchD;
+    out->lds_bytes = (uint32_t)L.smem_bytes;
+    out->lds_gather_floats = (uint32_t)L.fr;
+    out->lds_xs_offset = (uint32_t)L.xs_off;
+    out->lds_gs_offset = (uint32_t)L.gs_off;
+    out->lds_red_offset = (uint32_t)L.red_off;
+    out->lds_attention_floats = (uint32_t)L.att_floats;
+    out->lds_combine_floats = (uint32_t)L.comb_floats;
+    return LQ8_OK;
+}
 
 extern "C" lq8_status lq8_persist_trace(lq8_ctx* ctx, uint64_t* out, size_t count) {
     if (!registry_has(ctx)) return fail(LQ8_ERR_INVALID_ARG, "invalid context handle");

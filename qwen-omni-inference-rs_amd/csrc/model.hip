@@ -73,8 +73,10 @@ struct lq8_model {
     // persistent greedy decode (decode_persistent.hip): per-layer weight
     // pointers, tagged hand-off buffers, the argument block, the abort flag
     PLayer* d_player = nullptr;
-    uint64_t* hand = nullptr;  // qkvb | partb | resb | h2b | actb | argb
+    uint64_t* hand = nullptr;  // qkvb | partb | attb | resb | h2b | actb | argb | arrc
     size_t hand_words = 0;
+    uint64_t arrive = 0;       // the arrival counters' value before the next persistent launch
+    int last_steps = 0;        // steps of the last persistent launch
     PersistArgs* d_pargs = nullptr;
     PersistArgs h_pargs{};     // host copy (the source of the argument upload)
     unsigned* d_abort = nullptr;
@@ -503,31 +505,53 @@ PersistShape persist_shape(const lq8_model* m) {
                         (int)c.head_dim, (int)c.max_positions};
 }
 
+// Workgroups of the persistent launch: one per compute unit, or fewer when
+// LQ8_PERSIST_WG names a smaller count (a test of the kernel's other work
+// splits).
+int persist_target_wg(const lq8_model* m) {
+    const int P = m->ctx->num_cus;
+    const char* e = std::getenv("LQ8_PERSIST_WG");
+    const int want = e != nullptr ? std::atoi(e) : 0;
+    return want > 0 && want < P ? want : P;
+}
+
 // Whether greedy decode runs as the persistent kernel: wherever the shape is
 // supported, unless LQ8_PERSIST=0 asks for the per-step kernels (replayed as
 // a graph, or as plain launches under LQ8_NO_GRAPH).
 bool persist_wanted(const lq8_model* m) {
     const char* e = std::getenv("LQ8_PERSIST");
     if (e != nullptr && e[0] == '0') return false;
-    return persist_supported(persist_shape(m), m->ctx->num_cus);
+    return persist_supported(persist_shape(m), persist_target_wg(m));
 }
 
-// Device state of the persistent decode (allocated once per model).
+// Device state of the persistent decode (allocated once per model and
+// workgroup count).
 lq8_status persist_setup(lq8_model* m) {
-    if (m->persist_wg) return LQ8_OK;
+    const int P = persist_target_wg(m);
+    if (m->persist_wg == P) return LQ8_OK;
+    if (m->persist_wg) {
+        // set up for another workgroup count: start again from zeroed words
+        LQ8_HIP(hipStreamSynchronize(m->ctx->stream));
+        LQ8_HIP(hipFree(m->d_player));
+        LQ8_HIP(hipFree(m->hand));
+        m->d_player = nullptr;
+        m->hand = nullptr;
+        m->persist_wg = 0;
+        m->tag = 1;
+        m->last_steps = 0;
+    }
     const lq8_qwen3_config& c = m->c;
     int coop = 0;
     LQ8_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, m->ctx->device));
     if (!coop) return fail(LQ8_ERR_DEVICE, "persistent decode: no cooperative launch on this device");
-    const int P = m->ctx->num_cus;
     const PersistShape sh = persist_shape(m);
     PersistLayout lay{};
     if (!persist_layout(sh, P, &lay)) return fail(LQ8_ERR_MODEL, "persistent decode: shape not supported");
     const size_t L = c.num_layers, H = c.hidden_size, I = c.intermediate_size, NH = c.num_heads;
     const size_t cmax = (size_t)m->cmax;
-    const size_t qkv = L * m->QKV, part = L * cmax * NH * ATT_PART_STRIDE, res = (L + 1) * (1 + lay.nchO) * H,
-                 h2 = L * (1 + lay.nchD) * H, act = L * I;
-    m->hand_words = qkv + part + res + h2 + act + 2 * (size_t)P;
+    const size_t qkv = L * m->QKV, part = L * cmax * NH * ATT_PART_STRIDE, att = L * NH * 128,
+                 res = (L + 1) * (1 + lay.nchO) * H, h2 = L * (1 + lay.nchD) * H, act = L * I, arg = 4 * (size_t)P;
+    m->hand_words = qkv + part + att + res + h2 + act + arg + L * c.num_kv_heads;
     std::vector<PLayer> pl(L);
     for (size_t l = 0; l < L; l++) {
         const Layer& Ly = m->layers[l];
@@ -535,11 +559,12 @@ lq8_status persist_setup(lq8_model* m) {
                        Ly.gu->scales, Ly.down->scales, Ly.in_norm, Ly.post_norm, Ly.q_norm, Ly.k_norm};
     }
     lq8_status st;
-    if ((st = dalloc(&m->d_player, L)) || (st = dalloc(&m->hand, m->hand_words)) || (st = dalloc(&m->d_pargs, 1)) ||
-        (st = dalloc(&m->d_abort, 1)))
+    if ((st = dalloc(&m->d_player, L)) || (st = dalloc(&m->hand, m->hand_words)) ||
+        (!m->d_pargs && (st = dalloc(&m->d_pargs, 1))) || (!m->d_abort && (st = dalloc(&m->d_abort, 1))))
         return st;
     LQ8_HIP(hipMemcpy(m->d_player, pl.data(), L * sizeof(PLayer), hipMemcpyHostToDevice));
-    LQ8_HIP(hipMemset(m->hand, 0, m->hand_words * sizeof(uint64_t)));  // tag 0: never a step's
+    LQ8_HIP(hipMemset(m->hand, 0, m->hand_words * sizeof(uint64_t)));  // tag 0: never a step's; counters at 0
+    m->arrive = 0;
     PersistArgs& a = m->h_pargs;
     a = PersistArgs{};
     a.layers = m->d_player;
@@ -561,10 +586,12 @@ lq8_status persist_setup(lq8_model* m) {
     a.nchD = lay.nchD;
     a.qkvb = m->hand;
     a.partb = a.qkvb + qkv;
-    a.resb = a.partb + part;
+    a.attb = a.partb + part;
+    a.resb = a.attb + att;
     a.h2b = a.resb + res;
     a.actb = a.h2b + h2;
     a.argb = a.actb + act;
+    a.arrc = a.argb + arg;
     a.abort_flag = m->d_abort;
     a.fr = lay.fr;
     a.xs_off = lay.xs_off;
@@ -584,6 +611,8 @@ lq8_status launch_persist(lq8_model* m, int pos0, int steps, bool feed_first) {
     if ((uint64_t)m->tag + (uint64_t)steps >= 0xFFFFFF00ull) {  // tags wrap: clear every word back to tag 0
         LQ8_HIP(hipMemsetAsync(m->hand, 0, m->hand_words * sizeof(uint64_t), s));
         m->tag = 1;
+        m->arrive = 0;
+        m->last_steps = 0;
     }
     PersistArgs& a = m->h_pargs;
     a.pos0 = pos0;
@@ -591,11 +620,14 @@ lq8_status launch_persist(lq8_model* m, int pos0, int steps, bool feed_first) {
     a.step0 = 1;
     a.feed_first = feed_first ? 1 : 0;
     a.tag0 = m->tag;
+    a.arr0 = m->arrive;
     a.d_tok = m->d_tok;
     a.tokens_out = m->d_tokens;
     a.d_pos = m->d_pos;
     a.d_step = m->d_step;
     m->tag += (unsigned)steps;
+    m->last_steps = steps;
+    m->arrive += persist_arrivals_below(pos0 + steps) - persist_arrivals_below(pos0);
     LQ8_HIP(hipMemcpyAsync(m->d_pargs, &a, sizeof(PersistArgs), hipMemcpyHostToDevice, s));
     LQ8_HIP(hipMemsetAsync(m->d_abort, 0, sizeof(unsigned), s));
     return launch_decode_persistent(s, m->d_pargs, a.smem_bytes, m->persist_wg, a.csD / (PERSIST_THREADS / 64));
@@ -627,6 +659,7 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     if (sc && (st = ensure_sampler(m))) return st;
     if (sc) m->s_topk = sample_topk_path(*sc);
     const bool use_persist = !sc && max_new > 1 && persist_wanted(m);
+    if (!use_persist) m->last_steps = 0;  // the picks on record are no longer this call's
     if (use_persist && (st = persist_setup(m))) return st;
     if (!use_persist && use_graph && max_new > 1 &&
         (st = sc ? capture_sample_graph(m, feed_first) : capture_decode_graph(m, feed_first)))
@@ -669,6 +702,8 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
         LQ8_HIP(hipMemsetAsync(m->hand, 0, m->hand_words * sizeof(uint64_t), s));
         LQ8_HIP(hipStreamSynchronize(s));
         m->tag = 1;
+        m->arrive = 0;
+        m->last_steps = 0;
         return fail(LQ8_ERR_DEVICE, "persistent decode: a workgroup hand-off did not arrive in time (aborted)");
     }
     m->kv_len = n_prompt + max_new - 1;
@@ -901,6 +936,32 @@ lq8_status lq8_generate_greedy(lq8_model* m, const uint32_t* prompt, size_t n_pr
                                uint32_t* out_tokens, lq8_gen_stats* stats) {
     CHECK_M(m);
     return run_generate(m, prompt, n_prompt, max_new, nullptr, false, out_tokens, stats);
+}
+
+lq8_status lq8_model_persist_picks(lq8_model* m, uint32_t back, float* values, uint32_t* indices, size_t capacity,
+                                   size_t* count) {
+    CHECK_M(m);
+    if (!values || !indices || !count) return fail(LQ8_ERR_INVALID_ARG, "null pointer");
+    if (back > 1) return fail(LQ8_ERR_INVALID_ARG, "back must be 0 (the last step) or 1 (the step before)");
+    if (!m->persist_wg || (int)back >= m->last_steps)
+        return fail(LQ8_ERR_INVALID_ARG, "no such step in the last persistent decode launch");
+    *count = (size_t)m->persist_wg;
+    if (capacity < (size_t)m->persist_wg) return fail(LQ8_ERR_SHAPE_MISMATCH, "capacity below the workgroup count");
+    LQ8_HIP(hipSetDevice(m->ctx->device));
+    const unsigned tag = m->tag - 1 - back;
+    const size_t P = (size_t)m->persist_wg;
+    std::vector<uint64_t> w(2 * P);
+    LQ8_HIP(hipStreamSynchronize(m->ctx->stream));
+    LQ8_HIP(hipMemcpy(w.data(), m->h_pargs.argb + (size_t)(tag & 1) * 2 * P, 2 * P * sizeof(uint64_t),
+                      hipMemcpyDeviceToHost));
+    for (size_t i = 0; i < 2 * P; i++)
+        if ((unsigned)(w[i] >> 32) != tag) return fail(LQ8_ERR_INVALID_ARG, "that step's picks are not recorded");
+    for (size_t i = 0; i < P; i++) {
+        const uint32_t vb = (uint32_t)w[2 * i], ib = (uint32_t)w[2 * i + 1];
+        std::memcpy(&values[i], &vb, sizeof(float));
+        indices[i] = ib;
+    }
+    return LQ8_OK;
 }
 
 lq8_status lq8_generate_ex(lq8_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new,

@@ -102,6 +102,12 @@ class GenStatsC(C.Structure):
                 ("used_graph", C.c_uint32), ("used_persistent", C.c_uint32)]
 
 
+class PersistInfoC(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in (
+        "supported", "o_chunk_blocks", "o_chunks", "down_chunk_pairs", "down_chunks", "lds_bytes", "lds_gather_floats",
+        "lds_xs_offset", "lds_gs_offset", "lds_red_offset", "lds_attention_floats", "lds_combine_floats")]
+
+
 class SamplingC(C.Structure):
     _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
                 ("repetition_penalty", C.c_float), ("seed", C.c_uint64)]
@@ -181,6 +187,9 @@ _SIGS = [
     ("lq8_bench_grid_sync", C.c_int,
      [C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
     ("lq8_persist_trace", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    ("lq8_persist_plan", C.c_int, [C.POINTER(Qwen3ConfigC), C.c_uint32, C.POINTER(PersistInfoC)]),
+    ("lq8_model_persist_picks", C.c_int,
+     [C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_size_t)]),
     ("lq8_model_free", C.c_int, [C.c_void_p]),
     ("lq8_moe_tensor_count", C.c_size_t, [C.POINTER(MoeConfigC)]),
     ("lq8_moe_tensor_bytes", C.c_int, [C.POINTER(MoeConfigC), C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -615,6 +624,19 @@ class Qwen3ForCausalLM:
                      "decode_tokens_per_s": st.decode_tokens_per_s, "used_graph": bool(st.used_graph),
                      "used_persistent": bool(st.used_persistent)}
 
+    def persist_picks(self, back: int = 0):
+        """(values f32 [P], indices uint32 [P]): each of the P workgroups'
+        greedy pick of the last persistent decode step (back 0) or the step
+        before (back 1) -- its largest logit over its lm_head rows (16-row
+        tiles t with (t // 8) % P == w), last index on ties
+        (lq8_model_persist_picks)."""
+        cap = 65536
+        v = np.empty(cap, dtype=np.float32)
+        i = np.empty(cap, dtype=np.uint32)
+        n = C.c_size_t(0)
+        _check(lib().lq8_model_persist_picks(self.handle, back, _ptr(v), _ptr(i), cap, C.byref(n)))
+        return v[:n.value].copy(), i[:n.value].copy()
+
     def generate(self, prompt: Sequence[int], config: "GenerationConfig", seed: int = 0,
                  eos_token_ids: Sequence[int] = (), feed_first: bool = False):
         """generate() (src/generate.rs:611-664) with the configuration's
@@ -809,10 +831,26 @@ def bench_grid_sync(ctx: "Context", kind: int, nwg: int, rounds: int):
     return float(us.value), int(bad.value), int(gave.value)
 
 
-PTRACE_WG, PTRACE_LAYERS, PTRACE_POINTS = 512, 64, 16
+def persist_plan(cfg: "Qwen3Config", num_workgroups: int) -> dict:
+    """lq8_persist_plan: whether greedy decode of this configuration runs as
+    the persistent kernel on num_workgroups workgroups, and its plan (input
+    chunks of the o and down projections, LDS map in floats).  No device."""
+    info = PersistInfoC()
+    c = cfg.c()
+    _check(lib().lq8_persist_plan(C.byref(c), num_workgroups, C.byref(info)))
+    out = {n: int(getattr(info, n)) for n, _ in PersistInfoC._fields_}
+    out["supported"] = bool(out["supported"])
+    return out
+
+
+PTRACE_WG, PTRACE_LAYERS, PTRACE_POINTS = 512, 64, 17
 PTRACE_MARKS = ("P1_START", "P1_NORMED", "P2_START", "P2_QKV_IN", "P2_SCORES", "P2_PARTIALS", "P3_START",
                 "P3_STAGED", "P4_START", "P4_STAGED", "P5_START", "P5_STAGED", "P5_DONE", "P6_START", "P6_NORMED",
-                "P6_DONE")
+                "P6_DONE", "P2_COMBINED")
+# the marks of a decoder layer, in phase order, and of the lm_head phase (layer 0's row)
+PTRACE_LAYER_MARKS = ("P1_START", "P1_NORMED", "P2_START", "P2_QKV_IN", "P2_SCORES", "P2_PARTIALS", "P2_COMBINED",
+                      "P3_START", "P3_STAGED", "P4_START", "P4_STAGED", "P5_START", "P5_STAGED", "P5_DONE")
+PTRACE_HEAD_MARKS = ("P6_START", "P6_NORMED", "P6_DONE")
 
 
 def persist_trace(ctx: "Context") -> np.ndarray:

@@ -32,7 +32,8 @@ def timeline(tr: np.ndarray, n_layers: int, first: int = 4):
         st = tr[:, l, lq8.PTRACE_MARKS.index("P1_START")]
         refs.append(st[st != 0].max() if (st != 0).any() else 0)
     refs = np.array(refs)
-    for m, name in enumerate(lq8.PTRACE_MARKS[:13]):
+    for name in lq8.PTRACE_LAYER_MARKS:
+        m = lq8.PTRACE_MARKS.index(name)
         per = []
         n = 0
         for l in range(first, L):
@@ -45,11 +46,11 @@ def timeline(tr: np.ndarray, n_layers: int, first: int = 4):
         if per:
             rows.append((name, n, np.median(np.array(per), axis=0) * TICK_US))
     period = np.median(np.diff(refs[first:])) * TICK_US if L > first + 1 else float("nan")
-    p6 = tr[:, 0, lq8.PTRACE_MARKS.index("P6_START"):]
+    p6 = tr[:, 0, [lq8.PTRACE_MARKS.index(n) for n in lq8.PTRACE_HEAD_MARKS]]
     p6_rows = []
     if (p6[:, 0] != 0).any():
         base = p6[p6[:, 0] != 0, 0].min()
-        for k, name in enumerate(lq8.PTRACE_MARKS[13:]):
+        for k, name in enumerate(lq8.PTRACE_HEAD_MARKS):
             v = p6[p6[:, k] != 0, k] - base
             p6_rows.append((name, v.size, np.array([v.min(), np.median(v), v.max()]) * TICK_US))
     return rows, period, p6_rows

@@ -360,3 +360,195 @@ def test_persistent_down_chunks_with_odd_block(ctx):
     assert len(set(ref_toks.tolist())) > 4, "the tokens should vary"
     model.free()
     ref.close()
+
+
+def varied_small(cfg, seed):
+    tensors = oracle.random_q8_tensors(cfg, seed=seed, layer_std=0.08, norm_jitter=0.1)
+    return tensors
+
+
+def persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, new, min_distinct=4, env=None):
+    """Greedy tokens of the persistent kernel and of the replayed graph equal
+    the oracle's; env: extra environment for the persistent run."""
+    model = lq8.Qwen3ForCausalLM.load(ctx, cfg, tensors)
+    ref = oracle.Model(cfg, tensors)
+    saved = {k: os.environ.get(k) for k in (env or {})}
+    os.environ.update(env or {})
+    try:
+        ptoks, pst = with_path("persistent", lambda: model.generate_greedy(prompt, new))
+    finally:
+        for k, v in saved.items():
+            os.environ.pop(k, None)
+            if v is not None:
+                os.environ[k] = v
+    gtoks, gst = with_path("graph", lambda: model.generate_greedy(prompt, new))
+    ref_toks, margins = ref.generate_greedy(prompt, new)
+    assert pst["used_persistent"] and gst["used_graph"]
+    assert ptoks.tolist() == ref_toks.tolist()
+    assert gtoks.tolist() == ref_toks.tolist()
+    assert len(set(ref_toks.tolist())) > min_distinct, "the tokens should vary"
+    model.free()
+    ref.close()
+    return ptoks
+
+
+@pytest.mark.parametrize("heads,kv", [(4, 2), (8, 1), (16, 1)])
+def test_persistent_segments_5_to_8(ctx, heads, kv):
+    """max_positions 512, a 300-token prompt and 200 greedy tokens: the
+    persistent kernel's decode steps run at positions 300..498, so its
+    attention items cover segments 0..7 and every kv head's combine takes 5
+    to 8 segments.  Query heads per kv head 2, 8 and 16: the combine carries
+    1, 2 and 4 output elements per thread.  Tokens equal the oracle's and the
+    graph path's."""
+    cfg = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                          num_attention_heads=heads, num_key_value_heads=kv, head_dim=128,
+                          max_position_embeddings=512)
+    tensors = varied_small(cfg, 60 + heads)
+    prompt = np.random.default_rng(heads).integers(0, cfg.vocab_size, 300).astype(np.uint32)
+    persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 200)
+
+
+def test_persistent_long_context_combine_batches(ctx):
+    """max_positions 4224 (66 segments) and a 4090-token prompt: decode steps
+    at positions 4090..4129, where a kv head's 64 or 65 segments are combined
+    in two batches of at most 64 (the second holding one segment once the
+    position reaches 4096).  Tokens equal the oracle's and the graph path's."""
+    cfg = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                          num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=4224)
+    tensors = varied_small(cfg, 77)
+    prompt = np.random.default_rng(77).integers(0, cfg.vocab_size, 4090).astype(np.uint32)
+    persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 40, min_distinct=2)
+
+
+@pytest.mark.parametrize("wg", [128, 64])
+def test_persistent_other_workgroup_counts(ctx, wg):
+    """Qwen3-0.6B layer widths (hidden 1024, intermediate 3072, 16/8 heads;
+    2 layers, vocab 4096) on fewer workgroups than compute units
+    (LQ8_PERSIST_WG): 128 workgroups cut the o projection into two 32-block
+    chunks (8 heads each) and the down projection into two 32-pair chunks (4
+    pairs per wave); 64 give every workgroup two o items and one 64-pair
+    down chunk (8 pairs per wave).  Tokens equal the oracle's and the graph
+    path's."""
+    cfg = lq8.Qwen3Config(vocab_size=4096, hidden_size=1024, intermediate_size=3072, num_hidden_layers=2,
+                          num_attention_heads=16, num_key_value_heads=8, head_dim=128, max_position_embeddings=256)
+    plan = lq8.persist_plan(cfg, wg)
+    assert plan["supported"] and plan["o_chunk_blocks"] == 32
+    assert plan["down_chunk_pairs"] == (32 if wg == 128 else 64)
+    tensors = varied_small(cfg, 90 + wg)
+    prompt = np.random.default_rng(wg).integers(0, cfg.vocab_size, 100).astype(np.uint32)
+    persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 60, env={"LQ8_PERSIST_WG": str(wg)})
+
+
+def expected_picks(logits, P, pw=8):
+    """Each workgroup's pick over its lm_head rows: rows of the 16-row tiles t
+    with (t // pw) % P == w; the largest value, the last index on ties."""
+    rows = np.arange(logits.size)
+    owner = (rows // 16 // pw) % P
+    vals = np.empty(P, np.float32)
+    idx = np.empty(P, np.int64)
+    for w in range(P):
+        r = rows[owner == w]
+        lv = logits[r]
+        j = lv.size - 1 - int(np.argmax(lv[::-1]))  # last index of the maximum
+        vals[w], idx[w] = lv[j], r[j]
+    return vals, idx
+
+
+@pytest.mark.parametrize("varied", [False, True])
+def test_persistent_pick_words_qwen3_0_6b(ctx, varied):
+    """Full Qwen3-0.6B: the persistent kernel's per-workgroup greedy picks of
+    four decode steps (positions 128..131) -- each workgroup's largest logit
+    over its lm_head rows, as f32 bits, and its index -- equal the oracle's
+    logits of the same steps at those rows, bit for bit, and the token is the
+    largest of them (last index on ties)."""
+    cfg = lq8.qwen3_0_6b(max_positions=512)
+    base = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=2028)
+    tensors = base.export_all()
+    if varied:
+        tensors = varied_0_6b_tensors(tensors, cfg)
+    base.free()
+    model = lq8.Qwen3ForCausalLM.load(ctx, cfg, tensors)
+    ref = oracle.Model(cfg, tensors)
+    prompt = np.random.default_rng(2028).integers(0, cfg.vocab_size, 128).astype(np.uint32)
+    picks = {}
+    for n in (3, 5):  # steps 0, 1 and 0 .. 3; the last two of each launch are on record
+        toks, st = with_path("persistent", lambda: model.generate_greedy(prompt, n))
+        assert st["used_persistent"]
+        for back in (0, 1):
+            picks[n - 2 - back] = model.persist_picks(back)
+    ref.clear_kv_cache()
+    ref.forward(prompt, 0)
+    for s in range(4):
+        lg = ref.forward([int(toks[s])], 128 + s)
+        vals, idx = picks[s]
+        ev, ei = expected_picks(lg, vals.size)
+        assert np.array_equal(idx.astype(np.int64), ei), f"step {s}: {np.flatnonzero(idx != ei)[:5]}"
+        assert same_bits(vals, ev), f"step {s}: values differ"
+        top = vals.size - 1 - int(np.argmax(vals[::-1]))
+        assert int(idx[top]) == int(toks[s + 1]), f"step {s}: token"
+    model.free()
+    ref.close()
+
+
+def test_reference_arithmetic_free_running_chain_0_6b(ctx):
+    """Qwen3-0.6B random-init N(0, 0.02), 128-token prompt, 128 greedy tokens,
+    free-running: the oracle in the reference's own arithmetic -- plain
+    sequential sums (matmul_2d, src/tensor.rs:2740-2750) and the C library's
+    expf (Rust's f32::exp on linux-gnu) -- produces the persistent kernel's
+    tokens up to the first step where the two chains part, and that step is a
+    near-tie: fed the same prefix, the canonical order's top-2 logit margin
+    there is below twice the largest logit difference between the two orders
+    (their ~1e-7 rounding differences, amplified by 57 bf16 roundings per
+    token, move the logits by ~1 %; the tie-break between them is the
+    summation order's, not a fault of either).  Prints the split step, its
+    margin and the orders' difference."""
+    cfg = lq8.qwen3_0_6b(max_positions=512)
+    model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=2026)
+    ref = oracle.Model(cfg, model.export_all())
+    prompt = np.random.default_rng(2026).integers(0, cfg.vocab_size, 128).astype(np.uint32)
+    toks, st = with_path("persistent", lambda: model.generate_greedy(prompt, 128))
+    assert st["used_persistent"]
+
+    def reference_arithmetic(fn):
+        oracle.set_sequential_sums(True)
+        oracle.set_libm_exp(True)
+        try:
+            return fn()
+        finally:
+            oracle.set_libm_exp(False)
+            oracle.set_sequential_sums(False)
+
+    seq_toks, margins = reference_arithmetic(lambda: ref.generate_greedy(prompt, 128))
+    split = next((i for i in range(128) if int(seq_toks[i]) != int(toks[i])), None)
+    if split is None:
+        print(f"\nreference arithmetic, free-running: all 128 tokens equal; min top-2 margin "
+              f"{float(np.min(margins)):.4g}")
+        return
+    # both orders on the common prefix: the logits that decide token `split`
+    ref.clear_kv_cache()
+    canon = ref.forward(prompt, 0) if split == 0 else None
+    if split > 0:
+        ref.forward(prompt, 0)
+        for t in range(split - 1):
+            ref.forward([int(toks[t])], 128 + t)
+        canon = ref.forward([int(toks[split - 1])], 128 + split - 1)
+
+    def seq_logits():
+        ref.clear_kv_cache()
+        lg = ref.forward(prompt, 0)
+        for t in range(split):
+            lg = ref.forward([int(toks[t])], 128 + t)
+        return lg
+
+    seq = reference_arithmetic(seq_logits)
+    dev = float(np.max(np.abs(canon.astype(np.float64) - seq)))
+    top2 = np.sort(canon)[-2:]
+    margin = float(top2[1] - top2[0])
+    print(f"\nreference arithmetic, free-running: equal through token {split - 1}, parts at token {split} "
+          f"(canonical {int(toks[split])}, reference {int(seq_toks[split])}): canonical top-2 margin "
+          f"{margin:.4g}, largest logit difference between the orders {dev:.4g} "
+          f"({dev / float(np.max(np.abs(canon))):.2%} of the largest logit)")
+    assert int(np.argmax(canon)) == int(toks[split]) or np.sum(canon == canon.max()) > 1
+    assert margin < 2 * dev, "the chains part where the canonical order's choice is clear"
+    model.free()
+    ref.close()

@@ -143,19 +143,22 @@ def test_moe_rejects_bad_calls(ctx):
         lq8.Qwen3MoeLayers.random(ctx, bad, seed=1)
 
 
-@pytest.mark.parametrize("T", [1, 32])
-def test_moe_qwen3_30b_a3b_layer(ctx, T):
+@pytest.mark.parametrize("T,pos0", [(1, 0), (32, 0), (1, 126), (32, 126)])
+def test_moe_qwen3_30b_a3b_layer(ctx, T, pos0):
     """One full-size Qwen3-30B-A3B-style layer (hidden 2048, 32/4 heads, 128
     experts, top-8, expert intermediate 768), random-init on the device,
-    exported and replayed on the oracle: two decode steps bit-exact."""
+    exported and replayed on the oracle: three decode steps bit-exact.  From
+    position 126 the steps reach positions 126..134 (T = 32: position
+    126 + t % 7 for sequence t), so attention combines three 64-position
+    segments, as at the bench's position 128."""
     cfg = MoeCfg(hidden_size=2048, num_heads=32, num_kv_heads=4, num_experts=128, top_k=8,
-                 expert_intermediate_size=768, max_positions=128, max_batch=32, num_layers=1)
+                 expert_intermediate_size=768, max_positions=256, max_batch=32, num_layers=1)
     gpu = lq8.Qwen3MoeLayers.random(ctx, lq8_cfg(cfg), seed=2026)
     tens = gpu.export_all()
     orc = oracle.MoeStack(cfg, tens)
-    rng = np.random.default_rng(31 + T)
-    pos = np.arange(T, dtype=np.int32) % 7
-    for step in range(2):
+    rng = np.random.default_rng(31 + T + pos0)
+    pos = (pos0 + np.arange(T) % 7).astype(np.int32)
+    for step in range(3):
         x = rng.standard_normal((T, cfg.hidden_size)).astype(np.float32)
         scores = rng.standard_normal((1, T, cfg.num_experts)).astype(np.float32)
         y = gpu.forward(x, scores, pos)
