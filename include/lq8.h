@@ -203,7 +203,7 @@ lq8_status lq8_bench_grid_sync(lq8_ctx* ctx, int kind, int nwg, int rounds, floa
  * LQ8_PTRACE_POINTS.  Other builds return LQ8_ERR_INVALID_ARG. */
 #define LQ8_PTRACE_WG 512
 #define LQ8_PTRACE_LAYERS 64
-#define LQ8_PTRACE_POINTS 17
+#define LQ8_PTRACE_POINTS 19
 enum {
     LQ8_PT_P1_START = 0,     /* RmsNorm + q|k|v: workgroup enters */
     LQ8_PT_P1_NORMED = 1,    /* the layer input has arrived and is normalised */
@@ -221,7 +221,9 @@ enum {
     LQ8_PT_P6_START = 13,    /* lm_head: workgroup enters */
     LQ8_PT_P6_NORMED = 14,   /* the last layer's output has arrived and is normalised */
     LQ8_PT_P6_DONE = 15,     /* the workgroup's greedy pick is out */
-    LQ8_PT_P2_COMBINED = 16  /* attention: the kv head's segments are combined and out (the combining item) */
+    LQ8_PT_P2_COMBINED = 16, /* attention: the kv head's segments are combined and out (the combining item) */
+    LQ8_PT_P2_COMB_FETCHED = 17, /* combine: the other segments' first (m_c, l_c) and o_c words have arrived */
+    LQ8_PT_P2_COMB_COEF = 18     /* combine: the first batch's coefficients are done */
 };
 lq8_status lq8_persist_trace(lq8_ctx* ctx, uint64_t* out, size_t count);
 
@@ -312,7 +314,9 @@ typedef struct {
     uint32_t lds_gs_offset;      /* the waves' group sums */
     uint32_t lds_red_offset;     /* reduction words (16) */
     uint32_t lds_attention_floats; /* an attention item's region, from 0 */
-    uint32_t lds_combine_floats;   /* the segment combine's region, from 0 */
+    uint32_t lds_combine_floats;   /* the separate segment combine's region, inside the attention item's */
+    uint32_t direct_segments;      /* steps with at most this many 64-position segments combine them in the
+                                      o projection's items; longer contexts in one combining item per kv head */
 } lq8_persist_info;
 lq8_status lq8_persist_plan(const lq8_qwen3_config* cfg, uint32_t num_workgroups, lq8_persist_info* out);
 /* The per-workgroup greedy picks of the last persistent decode step (back 0)

@@ -25,7 +25,8 @@ struct PersistShape {
 struct PersistLayout {
     int csO, nchO;      // o projection: input chunks of csO blocks (a power of two), nchO of them
     int csD, nchD;      // down projection: input chunks of csD block pairs (a power of two), nchD of them
-    int fr, xs_off, gs_off, red_off, att_floats, comb_floats;  // LDS, in floats
+    int cdir;           // steps with at most cdir segments: P3 combines the partials itself
+    int fr, xs_off, gs_off, red_off, att_floats, comb_floats;  // LDS, in floats (combine: inside att_floats)
     int smem_bytes;
     size_t words;       // tagged hand-off words of all buffers
 };
@@ -44,6 +45,7 @@ struct PersistArgs {
     float eps, scale;
     int csO, nchO;
     int csD, nchD;
+    int cdir;          // P3 combines the segment partials itself while C <= cdir
     // tagged hand-off words (f32 bits | tag << 32)
     uint64_t* qkvb;   // [L][QKV]: q|k|v projection
     uint64_t* partb;  // [L][cmax][NH][ATT_PART_STRIDE]: attention partials per (segment, head)
@@ -53,10 +55,6 @@ struct PersistArgs {
                       // projection's chunk sums [nchD][H]
     uint64_t* actb;   // [L][I]: silu(gate) * up
     uint64_t* argb;   // [2][P][2]: each workgroup's greedy pick (value, index bits), by the step tag's parity
-    // arrival counters [L][NKV] (plain counts, not tagged): the attention items of a kv head count
-    // themselves in; the item that completes a step's count combines the kv head's segments
-    uint64_t* arrc;
-    uint64_t arr0;     // the value of every counter at the launch's start
     unsigned* abort_flag;
     // steps: positions pos0 .. pos0 + steps - 1; tokens_out[step0 + s] gets step s's pick
     int pos0, steps, step0, feed_first;
@@ -69,21 +67,15 @@ struct PersistArgs {
     int fr, xs_off, gs_off, red_off, smem_bytes;
 };
 
-// Attention items of one kv head at position pos (segments 0 .. pos / ATT_SEG),
-// and their sum over the positions [0, n): every counter of arrc grows by
-// persist_arrivals(pos) at each step, so its value after a run of steps is a
-// closed form of the positions the run covered.
-__host__ __device__ inline uint64_t persist_arrivals(int pos) { return (uint64_t)(pos / ATT_SEG + 1); }
-__host__ __device__ inline uint64_t persist_arrivals_below(int n) {
-    const uint64_t k = (uint64_t)n / ATT_SEG, r = (uint64_t)n % ATT_SEG;
-    return ATT_SEG * (k * (k + 1) / 2) + r * (k + 1);
-}
-
 // false when the shape does not fit the kernel's limits on P workgroups
 bool persist_layout(const PersistShape& s, int P, PersistLayout* out);
 bool persist_supported(const PersistShape& s, int num_cus);
 // d_args: the argument block in device memory (read by the kernel throughout)
 // ch5: block pairs per wave group of the down items (csD / waves per workgroup)
-lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg, int ch5);
+// long_ctx: the instance with the combining attention items, for steps whose
+// positions have more than cdir segments (the other instance requires
+// pos0 + steps <= cdir * ATT_SEG)
+lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg, int ch5,
+                                    bool long_ctx);
 
 }  // namespace lq8

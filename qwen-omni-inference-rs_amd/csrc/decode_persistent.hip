@@ -8,13 +8,18 @@
 //       the GEMV block tree; published for P4), RmsNorm(h_l) + q|k|v GEMV,
 //       one 16-row tile per item
 //   P2  attention, one (64-position segment, kv head) per item: per query
-//       head the segment's partials (o_c, m_c, l_c); each item then counts
-//       itself in on its kv head's arrival counter, and the item whose
-//       arrival completes the step's count combines the kv head's segments
-//       (any number of them) and publishes its heads' attention output
+//       head the segment's partials (o_c, m_c, l_c).  When a step has more
+//       segments than one P3 gather holds (cdir), the item of the newest
+//       segment keeps its own partials, reads the others' and combines the
+//       kv head's segments (any number of them), publishing its heads'
+//       attention output; a combiner waits only on items of lower index,
+//       which every workgroup takes first, so the waits always end
 //   P3  o GEMV, one (16-row tile, input chunk) per item: the chunk is csO
-//       blocks of the attention output; the item's output is the tile's
-//       partial sum over its chunk
+//       blocks of the attention output (whole heads or part of one), which
+//       the item combines itself from the segment partials of its heads
+//       (C <= cdir: one hand-off fewer than a separate combine) or fetches
+//       from the combiners; the item's output is the tile's partial sum over
+//       its chunk
 //   P4  h2 = h_l + o (the chunk sums meet in the GEMV block tree), then
 //       RmsNorm(h2) + gate and up GEMV (tile i of each) -> silu(gate) * up
 //   P5  down GEMV, one (16-row tile, input chunk of csD block pairs) per
@@ -42,8 +47,7 @@
 // workgroup cannot write step s + 2's pick before every workgroup has
 // published step s + 1's, which each does after reading step s's).  Tags
 // grow across launches (the host keeps the count) and zeroed buffers carry
-// tag 0, which no step uses.  The arrival counters only grow: after a step
-// each holds arr0 plus the items of every step of the launch so far.
+// tag 0, which no step uses.
 //
 // Weights do not depend on the step's data: a workgroup issues the weight
 // loads of its next phase's item (into registers) before it waits for the
@@ -96,8 +100,9 @@ constexpr int NW_QKV = ((ATT_MAX_GROUP + 2) * 128 + PT - 1) / PT;  // q of a kv 
 constexpr int NW_RES = PERSIST_FETCH;                             // h and the o chunk sums
 constexpr int NW_ACT = (4096 + 16 + PT - 1) / PT;                  // silu(gate) * up (<= 4096) and 16 rows of h2
 constexpr int NW_ATT = (2048 + PT - 1) / PT;                       // an o input chunk of the attention output (<= 2048)
-constexpr int CMB_SEGS = 64;                                       // combine: segments per batch of (m_c, l_c) words
-constexpr int NW_ML = (CMB_SEGS * ATT_MAX_GROUP * 2 + PT - 1) / PT;  // combine: a batch's (m_c, l_c) words
+constexpr int NW_PART = 16;                                        // an o chunk's segment partials ([C][R] words)
+constexpr int CMB_SEGS = 64;                                       // combine: segments per batch, at most
+constexpr int NW_ML = 1;                                           // combine: a batch's (m_c, l_c) words per thread
 constexpr int CMB_EK = (ATT_MAX_GROUP * 128 + PT - 1) / PT;        // combine: output elements per thread, at most
 constexpr int NW_OC = 16;                                          // combine: o_c words per thread and round
 constexpr int CHH = 16 / PW;    // block pairs per wave group of a hidden-long tile (hidden <= 1024: <= 16 pairs)
@@ -455,20 +460,26 @@ __device__ __forceinline__ void wave_sync() {
 // XS_ATTN staging): per head, in segment order, m' = max(m, m_c),
 // a_c = exp(m - m'), b_c = exp(m_c - m'), den = den a_c + b_c l_c; per
 // element num = num a_c + b_c o_c; x = num / den, published to attl (heads
-// concatenated).  Run by the attention item whose arrival completed the kv
-// head's count for the step: the count only elects the workgroup, every
-// segment's partials are read as tagged words.  Segments go in batches of
-// CMB_SEGS: per head one wave takes the batch's running maximum in order
+// concatenated).  Run by the attention item of the newest segment (C - 1),
+// which holds that segment's partials itself (own_ml: its (m_c, l_c) per
+// head in LDS; own: its o_c elements in registers) and reads the other
+// segments' as tagged words.  Segments go in batches of at most CMB_SEGS,
+// as many as have their (m_c, l_c) words in NW_ML words per thread: the
+// batch's (m_c, l_c) words and the o_c words of its first round arrive in
+// one fetch; per head one wave takes the batch's running maximum in order
 // (lane 0), the coefficients in parallel (lane j: segment j), then den in
-// order (lane 0); each thread then carries up to CMB_EK output elements
-// through the batch, fetching their o_c words NW_OC at a time.
-// LDS: ml [CMB_SEGS][G][2] (m_c, l_c), cf [CMB_SEGS][G][2] (a_c, b_c),
+// order (lane 0); each thread carries up to CMB_EK output elements
+// (tid + k PT) through the batch, NW_OC o_c words per round.
+// LDS (cm): ml [CMB_SEGS][G][2] (m_c, l_c), cf [CMB_SEGS][G][2] (a_c, b_c),
 // st [G][2] (running m, den).  false: the launch is aborting.
+template <typename Mark>
 __device__ __forceinline__ bool combine_heads(unsigned tag, int C, int g, int G, int NH, const uint64_t* partb,
-                                              uint64_t* attl, float* sm, unsigned* abort_flag, volatile int* bad) {
+                                              uint64_t* attl, float* cm, const float* own_ml,
+                                              const float (&own)[CMB_EK], unsigned* abort_flag,
+                                              volatile int* bad, Mark mark) {
     const int tid = tid_here(), lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    float* ml = sm;
+    float* ml = cm;
     float* cf = ml + CMB_SEGS * 2 * G;
     float* st = cf + CMB_SEGS * 2 * G;
     const int GE = G * 128;                            // output elements
@@ -476,6 +487,8 @@ __device__ __forceinline__ bool combine_heads(unsigned tag, int C, int g, int G,
     int SBs = 0;                                       // log2 of the segments per o_c round
     while ((2 << SBs) * EK <= NW_OC) SBs++;            // (the largest power of two with EK of them <= NW_OC)
     const int SBm = (1 << SBs) - 1;
+    const int cown = C - 1;                            // the combiner's own segment
+    const int BS = min(CMB_SEGS, NW_ML * PT / (2 * G));  // segments per batch
     const uint64_t* pb = partb + (size_t)(g * G) * ATT_PART_STRIDE;
     const size_t segw = (size_t)NH * ATT_PART_STRIDE;  // words per segment
     float num[CMB_EK];
@@ -485,17 +498,59 @@ __device__ __forceinline__ bool combine_heads(unsigned tag, int C, int g, int G,
         st[2 * tid] = -__builtin_huge_valf();
         st[2 * tid + 1] = 0.0f;
     }
-    for (int cb = 0; cb < C; cb += CMB_SEGS) {
-        const int nc = min(CMB_SEGS, C - cb);
-        // (m_c, l_c) of the batch: word i = (j G + h) 2 + {0: m_c, 1: l_c}
-        tfetch<NW_ML>(tag, [&](int t, int u) { return t + u * PT < nc * G * 2; },
-                      [&](int t, int u) {
-                          const int i = t + u * PT, j = i / (2 * G), h = (i >> 1) - j * G;
-                          return pb + (size_t)(cb + j) * segw + h * ATT_PART_STRIDE + 128 + (i & 1);
-                      },
-                      [&](int t, int u) { return ml + t + u * PT; }, abort_flag, bad);
+    // o_c unit u of a round starting at segment cb + sb: element tid + (u >> SBs) PT of segment
+    // cb + sb + (u & SBm); the own segment's come from registers
+    auto oc_ok = [&](int t, int u, int cb, int sb, int nc) {
+        const int k = u >> SBs, j = u & SBm;
+        return k < EK && t + k * PT < GE && sb + j < nc && cb + sb + j != cown;
+    };
+    auto oc_src = [&](int t, int u, int cb, int sb) {
+        const int k = u >> SBs, j = u & SBm, e = t + k * PT;
+        return pb + (size_t)(cb + sb + j) * segw + (e >> 7) * ATT_PART_STRIDE + (e & 127);
+    };
+    auto oc_update = [&](const float* ov, int cb, int sb, int nc) {
+        const int t = tid_here();
+#pragma unroll
+        for (int u = 0; u < NW_OC; u++) {
+            const int k = u >> SBs, j = u & SBm, e = t + k * PT;
+            if (k < EK && e < GE && sb + j < nc) {
+                float o = ov[u];
+#pragma unroll
+                for (int kk = 0; kk < CMB_EK; kk++)
+                    if (kk == k && cb + sb + j == cown) o = own[kk];
+                const int q = ((sb + j) * G + (e >> 7)) * 2;
+                const float add = cf[q + 1] * o;
+#pragma unroll
+                for (int kk = 0; kk < CMB_EK; kk++)
+                    if (kk == k) num[kk] = num[kk] * cf[q] + add;
+            }
+        }
+    };
+    for (int cb = 0; cb < C; cb += BS) {
+        const int nc = min(BS, C - cb);
+        // the batch's (m_c, l_c) words (i = (j G + h) 2 + {0: m_c, 1: l_c}) and its first o_c round
+        float ov[NW_OC];
+        tfetch<NW_ML + NW_OC>(
+            tag,
+            [&](int t, int u) {
+                if (u < NW_ML) {
+                    const int i = t + u * PT;
+                    return i < nc * G * 2 && cb + i / (2 * G) != cown;
+                }
+                return oc_ok(t, u - NW_ML, cb, 0, nc);
+            },
+            [&](int t, int u) {
+                if (u < NW_ML) {
+                    const int i = t + u * PT, j = i / (2 * G), h = (i >> 1) - j * G;
+                    return pb + (size_t)(cb + j) * segw + h * ATT_PART_STRIDE + 128 + (i & 1);
+                }
+                return oc_src(t, u - NW_ML, cb, 0);
+            },
+            [&](int t, int u) { return u < NW_ML ? ml + t + u * PT : &ov[u - NW_ML]; }, abort_flag, bad);
+        if (tid < 2 * G && cown >= cb && cown < cb + nc) ml[(cown - cb) * 2 * G + tid] = own_ml[tid];
         lds_sync();
         if (bad_now(bad)) return false;
+        mark(LQ8_PT_P2_COMB_FETCHED);
         for (int h = wave; h < G; h += PW) {
             if (lane == 0) {
                 // m before and after each segment, in order
@@ -527,33 +582,15 @@ __device__ __forceinline__ bool combine_heads(unsigned tag, int C, int g, int G,
             }
         }
         lds_sync();
-        for (int sb = 0; sb < nc; sb += SBm + 1) {
-            // unit u: element tid + (u >> SBs) PT of segment cb + sb + (u & SBm)
-            float ov[NW_OC];
-            tfetch<NW_OC>(tag,
-                          [&](int t, int u) {
-                              const int k = u >> SBs, j = u & SBm;
-                              return k < EK && t + k * PT < GE && sb + j < nc;
-                          },
-                          [&](int t, int u) {
-                              const int k = u >> SBs, j = u & SBm, e = t + k * PT;
-                              return pb + (size_t)(cb + sb + j) * segw + (e >> 7) * ATT_PART_STRIDE + (e & 127);
-                          },
-                          [&](int t, int u) { return &ov[u]; }, abort_flag, bad);
+        mark(LQ8_PT_P2_COMB_COEF);
+        oc_update(ov, cb, 0, nc);
+        for (int sb = SBm + 1; sb < nc; sb += SBm + 1) {
+            tfetch<NW_OC>(tag, [&](int t, int u) { return oc_ok(t, u, cb, sb, nc); },
+                          [&](int t, int u) { return oc_src(t, u, cb, sb); }, [&](int t, int u) { return &ov[u]; },
+                          abort_flag, bad);
             lds_sync();
             if (bad_now(bad)) return false;
-            const int t = tid_here();
-#pragma unroll
-            for (int u = 0; u < NW_OC; u++) {
-                const int k = u >> SBs, j = u & SBm, e = t + k * PT;
-                if (k < EK && e < GE && sb + j < nc) {
-                    const int q = ((sb + j) * G + (e >> 7)) * 2;
-                    const float add = cf[q + 1] * ov[u];
-#pragma unroll
-                    for (int kk = 0; kk < CMB_EK; kk++)
-                        if (kk == k) num[kk] = num[kk] * cf[q] + add;
-                }
-            }
+            oc_update(ov, cb, sb, nc);
         }
         lds_sync();  // ml and cf are written again by the next batch
     }
@@ -623,15 +660,17 @@ __device__ __forceinline__ Job job_dn(CArgs& a, const Dims& D, CLayer& Lw, int i
     return make_job<CH5>(Lw.dn_c, Lw.dn_s, D.npI, D.nbI, t, t, p0, min(a.csD, D.npI - p0));
 }
 
-template <int CH5>
+// LONG: the kernel instance for steps with more than cdir segments (the
+// combining attention items); the other instance has no combine code at all
+// (its presence alone, never run, costs the short-context steps about 3 %
+// through register allocation), and the host launches each for its steps.
+template <int CH5, bool LONG>
 __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __restrict__ pa) {
     extern __shared__ __align__(16) float sm[];
     __shared__ int bad_s;
-    __shared__ int elect_s;
     __shared__ float pick_v[PW];
     __shared__ int pick_i[PW];
     volatile int* bad = &bad_s;
-    volatile int* elect = &elect_s;
     const int P = gridDim.x, w = blockIdx.x;
     if (threadIdx.x == 0) bad_s = 0;
     lds_sync();
@@ -648,7 +687,9 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
         // index on ties) over the workgroups' picks; the first step's from
         // the previous kernel
         if (s == 0) {
-            tok = *a.d_tok;
+            // the previous kernel's pick (the reference's loop as written:
+            // the first generated token, also after an earlier launch)
+            tok = a.feed_first ? a.tokens_out[0] : *a.d_tok;
         } else {
             float* f = sm;
             tfetch_lin<NW_ARG>(2 * P, tag - 1, a.argb + (size_t)((tag - 1) & 1) * 2 * P, f, a.abort_flag, bad);
@@ -723,15 +764,13 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 if (w < n3) job_load<1, CHH>(job_o(a, D, Lw, w), R3);
             }
 
-            // ---- P2: attention per (segment, kv head) item; the item whose
-            // arrival completes the kv head's count combines its segments
+            // ---- P2: attention per (segment, kv head) item; the item of the
+            // newest segment combines its kv head's segments
             PTRACE(LQ8_PT_P2_START);
             {
                 LAYER_LOCALS;
                 const int L1 = pos + 1, C = (L1 + ATT_SEG - 1) / ATT_SEG, G = D.G;
                 const int items2 = C * D.NKV;
-                // every counter's value once this step's items have all arrived
-                const uint64_t target = a.arr0 + persist_arrivals_below(pos + 1) - persist_arrivals_below(a.pos0);
                 float* qs = sm;                   // [G][128]
                 float* kn = qs + G * 128;         // [128]
                 float* vn = kn + 128;             // [128]
@@ -789,48 +828,122 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     PTRACE(LQ8_PT_P2_SCORES);
                     seg_stage_v<PT, true>(vreg, nj, newrow, vn, ks);
                     lds_sync();
-                    for (int t = tid; t < G * 128; t += PT) {
-                        const int h = t >> 7, d = t & 127;
-                        const float o = pv_chain(sc + h * ATT_SEG, ks, d, nj);
-                        uint64_t* p = partb + ((size_t)c * D.NH + g * G + h) * ATT_PART_STRIDE;
-                        tput(p + d, o, tag);
-                        if (d == 0) {
-                            tput(p + 128, mlc[2 * h], tag);
-                            tput(p + 129, mlc[2 * h + 1], tag);
+                    // the segment's partials: published, or kept by the
+                    // newest segment's item, which combines the kv head's
+                    // segments
+                    const bool comb = LONG && C > a.cdir && c == C - 1;
+                    float own[CMB_EK];
+#pragma unroll
+                    for (int k = 0; k < CMB_EK; k++) {
+                        const int t = tid + k * PT;
+                        own[k] = 0.0f;
+                        if (t < G * 128) {
+                            const int h = t >> 7, d = t & 127;
+                            const float o = pv_chain(sc + h * ATT_SEG, ks, d, nj);
+                            own[k] = o;
+                            if (!comb) {
+                                uint64_t* p = partb + ((size_t)c * D.NH + g * G + h) * ATT_PART_STRIDE;
+                                tput(p + d, o, tag);
+                                if (d == 0) {
+                                    tput(p + 128, mlc[2 * h], tag);
+                                    tput(p + 129, mlc[2 * h + 1], tag);
+                                }
+                            }
                         }
                     }
                     PTRACE(LQ8_PT_P2_PARTIALS);
                     lds_sync();
-                    // count in; the item that completes the count combines
-                    if (tid == 0) {
-                        const uint64_t before = __hip_atomic_fetch_add(a.arrc + (size_t)l * D.NKV + g, (uint64_t)1,
-                                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        *elect = before + 1 == target ? 1 : 0;
-                    }
-                    lds_sync();
-                    if (__builtin_amdgcn_readfirstlane(*elect)) {
-                        if (!combine_heads(tag, C, g, G, D.NH, partb, attl, sm, a.abort_flag, bad)) goto done;
-                        PTRACE(LQ8_PT_P2_COMBINED);
-                        lds_sync();
+                    if constexpr (LONG) {
+                        if (comb) {
+                            // the combine works in the key rows' region (free now); mlc stays
+                            if (!combine_heads(tag, C, g, G, D.NH, partb, attl, ks, mlc, own, a.abort_flag, bad,
+                                               [&](int pt) { (void)pt; PTRACE(pt); }))
+                                goto done;
+                            PTRACE(LQ8_PT_P2_COMBINED);
+                            lds_sync();
+                        }
                     }
                 }
             }
 
             // ---- P3: o tile over one input chunk of the attention output
-            // -> chunk sums
+            // (combined here from the segment partials of the chunk's heads
+            // while a step has at most cdir segments, else published by the
+            // combining attention items) -> chunk sums
             PTRACE(LQ8_PT_P3_START);
             {
                 LAYER_LOCALS;
+                const int L1 = pos + 1, C = (L1 + ATT_SEG - 1) / ATT_SEG;
                 for (int it = w; it < n3; it += P) {
                     const Job J = job_o(a, D, Lw, it);
                     if (it != w) job_load<1, CHH>(J, R3);
                     const int t = it / a.nchO, c = it - t * a.nchO;
                     const int i0 = J.p0 * 64, rng = min(J.npv * 64, D.QD - i0);
-                    tfetch_lin<NW_ATT>(rng, tag, attl + i0, xs, a.abort_flag, bad);
+                    if (C <= a.cdir) {
+                        const int hA = i0 >> 7, nh = ((i0 + rng - 1) >> 7) - hA + 1;
+                        // the partials of the chunk's heads: per segment one run
+                        // of R = nh * ATT_PART_STRIDE words (per head o_c[128],
+                        // m_c, l_c, 2 unused); word i of the [C][R] staging is
+                        // unit (i - tt) / PT of thread tt
+                        const int R = nh * ATT_PART_STRIDE;
+                        float* pr = sm;                   // [C][R] the runs
+                        float* coef = pr + C * R;         // [C][nh][2]: a_c, b_c
+                        float* dens = coef + 2 * C * nh;  // [nh]
+                        const uint64_t* run0 = partb + (size_t)hA * ATT_PART_STRIDE;
+                        const size_t seg_words = (size_t)D.NH * ATT_PART_STRIDE;
+                        // i / R as a multiply-high by ceil(2^32 / R): exact for
+                        // i < 2^13 and R < 2^19 (the error term stays below 1 / R)
+                        const unsigned Rm = 0xFFFFFFFFu / (unsigned)R + 1u;
+                        tfetch<NW_PART>(tag,
+                                        [&](int tt, int u) {
+                                            const int i = tt + u * PT;
+                                            const int k = i - (int)__umulhi((unsigned)i, Rm) * R;
+                                            return i < C * R && k % ATT_PART_STRIDE < 130;
+                                        },
+                                        [&](int tt, int u) {
+                                            const int i = tt + u * PT, q = (int)__umulhi((unsigned)i, Rm);
+                                            return run0 + (size_t)q * seg_words + (i - q * R);
+                                        },
+                                        [&](int tt, int u) { return pr + tt + u * PT; }, a.abort_flag, bad);
+                        lds_sync();
+                        if (bad_now(bad)) goto done;
+                        PTRACE(LQ8_PT_P3_STAGED);
+                        // the combine (combine_heads' order): per head, in
+                        // segment order, m' = max(m, m_c), a_c = exp(m - m'),
+                        // b_c = exp(m_c - m'), den = den a_c + b_c l_c; per
+                        // element num = num a_c + b_c o_c, x = num / den
+                        if (tid < nh) {
+                            float m = -__builtin_huge_valf(), den = 0.0f;
+                            for (int cc = 0; cc < C; cc++) {
+                                const int q = cc * nh + tid;
+                                const float mc = pr[cc * R + tid * ATT_PART_STRIDE + 128];
+                                const float lc = pr[cc * R + tid * ATT_PART_STRIDE + 129];
+                                const float mn = m > mc ? m : mc;
+                                const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
+                                coef[2 * q] = ea;
+                                coef[2 * q + 1] = eb;
+                                den = den * ea + eb * lc;
+                                m = mn;
+                            }
+                            dens[tid] = den;
+                        }
+                        lds_sync();
+                        for (int k = tid; k < rng; k += PT) {
+                            const int hh = ((i0 + k) >> 7) - hA;
+                            float num = 0.0f;
+                            for (int cc = 0; cc < C; cc++)
+                                num = num * coef[2 * (cc * nh + hh)] +
+                                      coef[2 * (cc * nh + hh) + 1] * pr[cc * R + hh * ATT_PART_STRIDE + ((i0 + k) & 127)];
+                            xs[k] = __fdiv_rn(num, dens[hh]);
+                        }
+                    } else {
+                        tfetch_lin<NW_ATT>(rng, tag, attl + i0, xs, a.abort_flag, bad);
+                        lds_sync();
+                        if (bad_now(bad)) goto done;
+                        PTRACE(LQ8_PT_P3_STAGED);
+                    }
                     stage_pad(xs, rng, J.npv);
                     lds_sync();
-                    if (bad_now(bad)) goto done;
-                    PTRACE(LQ8_PT_P3_STAGED);
                     job_dot<1, CHH>(J, R3, xs, gs);
                     lds_sync();
                     if (tid < 64) {
@@ -1136,19 +1249,29 @@ bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
         return false;
     // the picks (2 words per workgroup) are one fetch; an attention item's
     // q, k, v one more; a combine batch's (m_c, l_c) and a thread's output
-    // elements fit their fetches
-    if (2 * P > NW_ARG * PT || (G + 2) * 128 > NW_QKV * PT || CMB_SEGS * G * 2 > NW_ML * PT || G * 128 > CMB_EK * PT)
+    // elements fit their fetches (with a round's o_c words: at most 32)
+    if (2 * P > NW_ARG * PT || (G + 2) * 128 > NW_QKV * PT || 2 * G > NW_ML * PT || G * 128 > CMB_EK * PT ||
+        NW_ML + NW_OC > 32)
         return false;
     PersistLayout L{};
     L.csO = csO;
     L.nchO = nchO;
     L.csD = csD;
     L.nchD = nchD;
-    // LDS, in floats.  From 0: the gathers (fr), the attention item's
-    // region (att_floats) and the combine's (comb_floats), never in use at
-    // once; then the staged GEMV input xs (a hidden vector, an o chunk or a
-    // down chunk), the wave group sums gs (two tiles) and red.
+    // P3's own combine: an o chunk touches nhc heads (whole heads, or one),
+    // whose partials are R words per segment; it takes the steps with at
+    // most cdir segments, those whose [C][R] runs fit one gather
+    const int nhc = std::max(1, std::min(csO, nbQ) * 32 / 128), R = nhc * ATT_PART_STRIDE;
+    L.cdir = NW_PART * PT / R;
+    if (L.cdir < 1) return false;
+    // LDS, in floats.  From 0: the gathers (fr: a hidden vector and its
+    // chunk sums, the picks, or P3's [cdir][R] runs with their
+    // coefficients), the attention item's region (att_floats, holding the
+    // separate combine's comb_floats), never in use at once; then the staged
+    // GEMV input xs (a hidden vector, an o chunk or a down chunk), the wave
+    // group sums gs (two tiles) and red.
     int fr = std::max(std::max((1 + nchO) * s.H, (1 + nchD) * s.H), 2 * P);
+    fr = std::max(fr, L.cdir * R + 2 * L.cdir * nhc + nhc);
     L.fr = (fr + 3) & ~3;
     const int xsz = std::max(std::max(npH, std::min(csD, npI)), pairsO) * 64;
     L.xs_off = L.fr;
@@ -1156,9 +1279,11 @@ bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
     L.red_off = L.gs_off + 2 * PW * 16;
     const int total = L.red_off + 16;
     L.att_floats = seg_ks_off(G) + ATT_SEG * KPAD;
-    if ((G + 2) * 128 > ATT_SEG * KPAD) return false;  // the fetched q, k, v sit in the key rows' region
+    // the fetched q, k, v and later the combine's region sit in the key rows' region
+    if ((G + 2) * 128 > ATT_SEG * KPAD) return false;
     L.comb_floats = 4 * CMB_SEGS * G + 2 * G;
-    L.smem_bytes = std::max(std::max(total, L.att_floats), L.comb_floats) * (int)sizeof(float);
+    if (L.comb_floats > ATT_SEG * KPAD) return false;
+    L.smem_bytes = std::max(total, L.att_floats) * (int)sizeof(float);
     if (L.smem_bytes > 64 * 1024) return false;
     L.words = 0;
     if (out) *out = L;
@@ -1167,14 +1292,20 @@ bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
 
 bool persist_supported(const PersistShape& s, int num_cus) { return persist_layout(s, num_cus, nullptr); }
 
-lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg, int ch5) {
+template <bool LONG>
+const void* persist_kernel(int ch5) {
+    return ch5 == 1   ? (const void*)k_decode_persistent<1, LONG>
+           : ch5 == 2 ? (const void*)k_decode_persistent<2, LONG>
+           : ch5 == 4 ? (const void*)k_decode_persistent<4, LONG>
+                      : (const void*)k_decode_persistent<8, LONG>;
+}
+
+lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg, int ch5,
+                                    bool long_ctx) {
     const PersistArgs* args = d_args;
     void* kargs[] = {&args};
     const size_t smem = (size_t)smem_bytes;
-    const void* k = ch5 == 1   ? (const void*)k_decode_persistent<1>
-                    : ch5 == 2 ? (const void*)k_decode_persistent<2>
-                    : ch5 == 4 ? (const void*)k_decode_persistent<4>
-                               : (const void*)k_decode_persistent<8>;
+    const void* k = long_ctx ? persist_kernel<true>(ch5) : persist_kernel<false>(ch5);
     hipError_t e = hipLaunchCooperativeKernel(k, dim3((unsigned)num_wg), dim3(PT), kargs, smem, st);
     if (e == hipErrorCooperativeLaunchTooLarge)
         return fail(LQ8_ERR_DEVICE, "persistent decode: the grid cannot be co-resident");
@@ -1210,6 +1341,7 @@ extern "C" lq8_status lq8_persist_plan(const lq8_qwen3_config* cfg, uint32_t num
     out->lds_red_offset = (uint32_t)L.red_off;
     out->lds_attention_floats = (uint32_t)L.att_floats;
     out->lds_combine_floats = (uint32_t)L.comb_floats;
+    out->direct_segments = (uint32_t)L.cdir;
     return LQ8_OK;
 }
 

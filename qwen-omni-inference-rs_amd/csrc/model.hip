@@ -73,12 +73,13 @@ struct lq8_model {
     // persistent greedy decode (decode_persistent.hip): per-layer weight
     // pointers, tagged hand-off buffers, the argument block, the abort flag
     PLayer* d_player = nullptr;
-    uint64_t* hand = nullptr;  // qkvb | partb | attb | resb | h2b | actb | argb | arrc
+    uint64_t* hand = nullptr;  // qkvb | partb | attb | resb | h2b | actb | argb
     size_t hand_words = 0;
-    uint64_t arrive = 0;       // the arrival counters' value before the next persistent launch
     int last_steps = 0;        // steps of the last persistent launch
-    PersistArgs* d_pargs = nullptr;
-    PersistArgs h_pargs{};     // host copy (the source of the argument upload)
+    int persist_cdir = 0;      // the plan's direct-combine limit (segments per step)
+    PersistArgs* d_pargs = nullptr;  // [2]: the argument blocks of a call's (at most) two launches
+    PersistArgs h_pargs{};     // the model's argument block; each launch uploads a copy of it from h_launch
+    PersistArgs h_launch[2]{};
     unsigned* d_abort = nullptr;
     unsigned tag = 1;          // tag of the next persistent step (0 never used)
     int persist_wg = 0;        // workgroups of the cooperative launch (0: not set up)
@@ -551,7 +552,7 @@ lq8_status persist_setup(lq8_model* m) {
     const size_t cmax = (size_t)m->cmax;
     const size_t qkv = L * m->QKV, part = L * cmax * NH * ATT_PART_STRIDE, att = L * NH * 128,
                  res = (L + 1) * (1 + lay.nchO) * H, h2 = L * (1 + lay.nchD) * H, act = L * I, arg = 4 * (size_t)P;
-    m->hand_words = qkv + part + att + res + h2 + act + arg + L * c.num_kv_heads;
+    m->hand_words = qkv + part + att + res + h2 + act + arg;
     std::vector<PLayer> pl(L);
     for (size_t l = 0; l < L; l++) {
         const Layer& Ly = m->layers[l];
@@ -560,11 +561,10 @@ lq8_status persist_setup(lq8_model* m) {
     }
     lq8_status st;
     if ((st = dalloc(&m->d_player, L)) || (st = dalloc(&m->hand, m->hand_words)) ||
-        (!m->d_pargs && (st = dalloc(&m->d_pargs, 1))) || (!m->d_abort && (st = dalloc(&m->d_abort, 1))))
+        (!m->d_pargs && (st = dalloc(&m->d_pargs, 2))) || (!m->d_abort && (st = dalloc(&m->d_abort, 1))))
         return st;
     LQ8_HIP(hipMemcpy(m->d_player, pl.data(), L * sizeof(PLayer), hipMemcpyHostToDevice));
-    LQ8_HIP(hipMemset(m->hand, 0, m->hand_words * sizeof(uint64_t)));  // tag 0: never a step's; counters at 0
-    m->arrive = 0;
+    LQ8_HIP(hipMemset(m->hand, 0, m->hand_words * sizeof(uint64_t)));  // tag 0: never a step's
     PersistArgs& a = m->h_pargs;
     a = PersistArgs{};
     a.layers = m->d_player;
@@ -584,6 +584,8 @@ lq8_status persist_setup(lq8_model* m) {
     a.nchO = lay.nchO;
     a.csD = lay.csD;
     a.nchD = lay.nchD;
+    a.cdir = lay.cdir;
+    m->persist_cdir = lay.cdir;
     a.qkvb = m->hand;
     a.partb = a.qkvb + qkv;
     a.attb = a.partb + part;
@@ -591,7 +593,6 @@ lq8_status persist_setup(lq8_model* m) {
     a.h2b = a.resb + res;
     a.actb = a.h2b + h2;
     a.argb = a.actb + act;
-    a.arrc = a.argb + arg;
     a.abort_flag = m->d_abort;
     a.fr = lay.fr;
     a.xs_off = lay.xs_off;
@@ -602,35 +603,49 @@ lq8_status persist_setup(lq8_model* m) {
     return LQ8_OK;
 }
 
-// The decode steps of generate() at positions pos0 .. pos0 + steps - 1 as one
-// cooperative launch (the input token is in d_tok; tokens_out[1 + s] gets
-// step s's pick).  The host argument copy stays unchanged until the caller
-// synchronizes the stream.
+// The decode steps of generate() at positions pos0 .. pos0 + steps - 1 (the
+// input token is in d_tok; tokens_out[1 + s] gets step s's pick): the steps
+// whose positions have at most cdir segments as one cooperative launch of the
+// kernel instance without the combining items, the later ones as a launch of
+// the instance with them.  The host argument blocks stay unchanged until the
+// caller synchronizes the stream.
 lq8_status launch_persist(lq8_model* m, int pos0, int steps, bool feed_first) {
     hipStream_t s = m->ctx->stream;
     if ((uint64_t)m->tag + (uint64_t)steps >= 0xFFFFFF00ull) {  // tags wrap: clear every word back to tag 0
         LQ8_HIP(hipMemsetAsync(m->hand, 0, m->hand_words * sizeof(uint64_t), s));
         m->tag = 1;
-        m->arrive = 0;
         m->last_steps = 0;
     }
-    PersistArgs& a = m->h_pargs;
-    a.pos0 = pos0;
-    a.steps = steps;
-    a.step0 = 1;
-    a.feed_first = feed_first ? 1 : 0;
-    a.tag0 = m->tag;
-    a.arr0 = m->arrive;
-    a.d_tok = m->d_tok;
-    a.tokens_out = m->d_tokens;
-    a.d_pos = m->d_pos;
-    a.d_step = m->d_step;
+    // LQ8_PERSIST_CDIR lowers the direct-combine limit (0: every step through
+    // the combining attention items), a test of both paths on one shape
+    const char* e = std::getenv("LQ8_PERSIST_CDIR");
+    const int cdir = e != nullptr ? std::min(std::max(std::atoi(e), 0), m->persist_cdir) : m->persist_cdir;
+    // steps at positions below cdir * ATT_SEG have at most cdir segments
+    const int n_short = std::max(0, std::min(steps, cdir * ATT_SEG - pos0));
+    LQ8_HIP(hipMemsetAsync(m->d_abort, 0, sizeof(unsigned), s));
+    const int ch5 = m->h_pargs.csD / (PERSIST_THREADS / 64);
+    for (int part = 0; part < 2; part++) {
+        const int first = part == 0 ? 0 : n_short, n = part == 0 ? n_short : steps - n_short;
+        if (n == 0) continue;
+        PersistArgs& a = m->h_launch[part];
+        a = m->h_pargs;
+        a.cdir = cdir;
+        a.pos0 = pos0 + first;
+        a.steps = n;
+        a.step0 = 1 + first;
+        a.feed_first = feed_first ? 1 : 0;
+        a.tag0 = m->tag + (unsigned)first;
+        a.d_tok = m->d_tok;
+        a.tokens_out = m->d_tokens;
+        a.d_pos = m->d_pos;
+        a.d_step = m->d_step;
+        LQ8_HIP(hipMemcpyAsync(m->d_pargs + part, &a, sizeof(PersistArgs), hipMemcpyHostToDevice, s));
+        lq8_status st = launch_decode_persistent(s, m->d_pargs + part, a.smem_bytes, m->persist_wg, ch5, part == 1);
+        if (st) return st;
+    }
     m->tag += (unsigned)steps;
     m->last_steps = steps;
-    m->arrive += persist_arrivals_below(pos0 + steps) - persist_arrivals_below(pos0);
-    LQ8_HIP(hipMemcpyAsync(m->d_pargs, &a, sizeof(PersistArgs), hipMemcpyHostToDevice, s));
-    LQ8_HIP(hipMemsetAsync(m->d_abort, 0, sizeof(unsigned), s));
-    return launch_decode_persistent(s, m->d_pargs, a.smem_bytes, m->persist_wg, a.csD / (PERSIST_THREADS / 64));
+    return LQ8_OK;
 }
 
 // generate (src/generate.rs:611-664): greedy picks (sc null) or sampled ones;
@@ -697,12 +712,11 @@ lq8_status run_generate(lq8_model* m, const uint32_t* prompt, size_t n_prompt, s
     if (use_persist) LQ8_HIP(hipMemcpyAsync(&aborted, m->d_abort, sizeof(unsigned), hipMemcpyDeviceToHost, s));
     LQ8_HIP(hipStreamSynchronize(s));
     if (aborted) {
-        // the arrival counters and tags an aborted launch leaves are not
+        // the tags an aborted launch leaves are not
         // trusted: the next launch starts from zeroed words
         LQ8_HIP(hipMemsetAsync(m->hand, 0, m->hand_words * sizeof(uint64_t), s));
         LQ8_HIP(hipStreamSynchronize(s));
         m->tag = 1;
-        m->arrive = 0;
         m->last_steps = 0;
         return fail(LQ8_ERR_DEVICE, "persistent decode: a workgroup hand-off did not arrive in time (aborted)");
     }

@@ -105,7 +105,8 @@ class GenStatsC(C.Structure):
 class PersistInfoC(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in (
         "supported", "o_chunk_blocks", "o_chunks", "down_chunk_pairs", "down_chunks", "lds_bytes", "lds_gather_floats",
-        "lds_xs_offset", "lds_gs_offset", "lds_red_offset", "lds_attention_floats", "lds_combine_floats")]
+        "lds_xs_offset", "lds_gs_offset", "lds_red_offset", "lds_attention_floats", "lds_combine_floats",
+        "direct_segments")]
 
 
 class SamplingC(C.Structure):
@@ -843,12 +844,13 @@ def persist_plan(cfg: "Qwen3Config", num_workgroups: int) -> dict:
     return out
 
 
-PTRACE_WG, PTRACE_LAYERS, PTRACE_POINTS = 512, 64, 17
+PTRACE_WG, PTRACE_LAYERS, PTRACE_POINTS = 512, 64, 19
 PTRACE_MARKS = ("P1_START", "P1_NORMED", "P2_START", "P2_QKV_IN", "P2_SCORES", "P2_PARTIALS", "P3_START",
                 "P3_STAGED", "P4_START", "P4_STAGED", "P5_START", "P5_STAGED", "P5_DONE", "P6_START", "P6_NORMED",
-                "P6_DONE", "P2_COMBINED")
+                "P6_DONE", "P2_COMBINED", "P2_COMB_FETCHED", "P2_COMB_COEF")
 # the marks of a decoder layer, in phase order, and of the lm_head phase (layer 0's row)
-PTRACE_LAYER_MARKS = ("P1_START", "P1_NORMED", "P2_START", "P2_QKV_IN", "P2_SCORES", "P2_PARTIALS", "P2_COMBINED",
+PTRACE_LAYER_MARKS = ("P1_START", "P1_NORMED", "P2_START", "P2_QKV_IN", "P2_SCORES", "P2_PARTIALS",
+                      "P2_COMB_FETCHED", "P2_COMB_COEF", "P2_COMBINED",
                       "P3_START", "P3_STAGED", "P4_START", "P4_STAGED", "P5_START", "P5_STAGED", "P5_DONE")
 PTRACE_HEAD_MARKS = ("P6_START", "P6_NORMED", "P6_DONE")
 

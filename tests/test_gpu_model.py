@@ -392,43 +392,52 @@ def persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, new, min_distin
     return ptoks
 
 
+@pytest.mark.parametrize("combine", ["direct", "combiner"])
 @pytest.mark.parametrize("heads,kv", [(4, 2), (8, 1), (16, 1)])
-def test_persistent_segments_5_to_8(ctx, heads, kv):
+def test_persistent_segments_5_to_8(ctx, heads, kv, combine):
     """max_positions 512, a 300-token prompt and 200 greedy tokens: the
     persistent kernel's decode steps run at positions 300..498, so its
     attention items cover segments 0..7 and every kv head's combine takes 5
-    to 8 segments.  Query heads per kv head 2, 8 and 16: the combine carries
-    1, 2 and 4 output elements per thread.  Tokens equal the oracle's and the
-    graph path's."""
+    to 8 segments -- in the o projection's items ("direct", the default at
+    these lengths) or in the newest segment's item (LQ8_PERSIST_CDIR=0).
+    Query heads per kv head 2, 8 and 16: the combining item carries 1, 2 and
+    4 output elements per thread.  Tokens equal the oracle's and the graph
+    path's."""
     cfg = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
                           num_attention_heads=heads, num_key_value_heads=kv, head_dim=128,
                           max_position_embeddings=512)
     tensors = varied_small(cfg, 60 + heads)
     prompt = np.random.default_rng(heads).integers(0, cfg.vocab_size, 300).astype(np.uint32)
-    persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 200)
+    assert lq8.persist_plan(cfg, 256)["direct_segments"] >= 8
+    env = {"LQ8_PERSIST_CDIR": "0"} if combine == "combiner" else None
+    persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 200, env=env)
 
 
 def test_persistent_long_context_combine_batches(ctx):
     """max_positions 4224 (66 segments) and a 4090-token prompt: decode steps
-    at positions 4090..4129, where a kv head's 64 or 65 segments are combined
-    in two batches of at most 64 (the second holding one segment once the
-    position reaches 4096).  Tokens equal the oracle's and the graph path's."""
+    at positions 4090..4129, beyond the direct combine's 62 segments, so the
+    newest segment's item combines a kv head's 64 or 65 segments, in two
+    batches of at most 64 (the second holding one segment once the position
+    reaches 4096).  Tokens equal the oracle's and the graph path's."""
     cfg = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
                           num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=4224)
+    assert lq8.persist_plan(cfg, 256)["direct_segments"] < 64
     tensors = varied_small(cfg, 77)
     prompt = np.random.default_rng(77).integers(0, cfg.vocab_size, 4090).astype(np.uint32)
     persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 40, min_distinct=2)
 
 
+@pytest.mark.parametrize("combine", ["direct", "combiner"])
 @pytest.mark.parametrize("wg", [128, 64])
-def test_persistent_other_workgroup_counts(ctx, wg):
+def test_persistent_other_workgroup_counts(ctx, wg, combine):
     """Qwen3-0.6B layer widths (hidden 1024, intermediate 3072, 16/8 heads;
     2 layers, vocab 4096) on fewer workgroups than compute units
     (LQ8_PERSIST_WG): 128 workgroups cut the o projection into two 32-block
     chunks (8 heads each) and the down projection into two 32-pair chunks (4
     pairs per wave); 64 give every workgroup two o items and one 64-pair
     down chunk (8 pairs per wave).  Tokens equal the oracle's and the graph
-    path's."""
+    path's, with the segments combined in the o projection's items (8
+    heads' partials per item) or in the newest segment's item."""
     cfg = lq8.Qwen3Config(vocab_size=4096, hidden_size=1024, intermediate_size=3072, num_hidden_layers=2,
                           num_attention_heads=16, num_key_value_heads=8, head_dim=128, max_position_embeddings=256)
     plan = lq8.persist_plan(cfg, wg)
@@ -436,7 +445,10 @@ def test_persistent_other_workgroup_counts(ctx, wg):
     assert plan["down_chunk_pairs"] == (32 if wg == 128 else 64)
     tensors = varied_small(cfg, 90 + wg)
     prompt = np.random.default_rng(wg).integers(0, cfg.vocab_size, 100).astype(np.uint32)
-    persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 60, env={"LQ8_PERSIST_WG": str(wg)})
+    env = {"LQ8_PERSIST_WG": str(wg)}
+    if combine == "combiner":
+        env["LQ8_PERSIST_CDIR"] = "0"
+    persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 60, env=env)
 
 
 def expected_picks(logits, P, pw=8):
@@ -444,10 +456,12 @@ def expected_picks(logits, P, pw=8):
     with (t // pw) % P == w; the largest value, the last index on ties."""
     rows = np.arange(logits.size)
     owner = (rows // 16 // pw) % P
-    vals = np.empty(P, np.float32)
-    idx = np.empty(P, np.int64)
+    vals = np.full(P, -np.inf, np.float32)
+    idx = np.full(P, 0xFFFFFFFF, np.int64)  # a workgroup without rows: (-inf, index -1)
     for w in range(P):
         r = rows[owner == w]
+        if r.size == 0:
+            continue
         lv = logits[r]
         j = lv.size - 1 - int(np.argmax(lv[::-1]))  # last index of the maximum
         vals[w], idx[w] = lv[j], r[j]
@@ -550,5 +564,45 @@ def test_reference_arithmetic_free_running_chain_0_6b(ctx):
           f"({dev / float(np.max(np.abs(canon))):.2%} of the largest logit)")
     assert int(np.argmax(canon)) == int(toks[split]) or np.sum(canon == canon.max()) > 1
     assert margin < 2 * dev, "the chains part where the canonical order's choice is clear"
+    model.free()
+    ref.close()
+
+
+@pytest.mark.parametrize("feed_first", [False, True])
+def test_persistent_split_across_launches(ctx, feed_first):
+    """One greedy call whose steps run as two launches: with the direct
+    combine limited to 2 segments (LQ8_PERSIST_CDIR=2), positions 100..127
+    run on the kernel instance without the combining items and 128..158 on
+    the one with them; the second launch takes its first input token from
+    the first (or, in the reference's loop as written, the first generated
+    token).  Tokens equal the oracle's, and the last two steps' picks (both
+    in the second launch) are readable."""
+    cfg = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                          num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=192)
+    tensors = varied_small(cfg, 88)
+    model = lq8.Qwen3ForCausalLM.load(ctx, cfg, tensors)
+    ref = oracle.Model(cfg, tensors)
+    prompt = np.random.default_rng(88).integers(0, cfg.vocab_size, 100).astype(np.uint32)
+    os.environ["LQ8_PERSIST_CDIR"] = "2"
+    try:
+        toks, st = with_path("persistent", lambda: model.generate_greedy(prompt, 60, feed_first=feed_first))
+    finally:
+        os.environ.pop("LQ8_PERSIST_CDIR", None)
+    ref_toks, _ = ref.generate_greedy(prompt, 60, feed_first=feed_first)
+    assert st["used_persistent"]
+    assert toks.tolist() == ref_toks.tolist()
+    assert len(set(ref_toks.tolist())) > (1 if feed_first else 4)
+    # the last two steps (positions 157, 158) against the oracle's logits of
+    # the same fed tokens
+    ref.clear_kv_cache()
+    ref.forward(prompt, 0)
+    logits = {}
+    for t in range(59):
+        logits[t] = ref.forward([int(toks[0] if feed_first else toks[t])], 100 + t)
+    for back in (0, 1):
+        vals, idx = model.persist_picks(back)
+        ev, ei = expected_picks(logits[58 - back], vals.size)
+        assert np.array_equal(idx.astype(np.int64), ei), f"back {back}"
+        assert same_bits(vals, ev), f"back {back}"
     model.free()
     ref.close()

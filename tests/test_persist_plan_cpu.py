@@ -74,7 +74,16 @@ def check_plan(c, P, p):
     assert att >= -(-(G * 128 + 256 + G * SEG + 2 * G) // 4) * 4 + SEG * KPAD
     assert (G + 2) * 128 <= SEG * KPAD
     # (m_c, l_c) and (a_c, b_c) of 64 segments x G heads, (m, den) per head
+    # P3's own combine: an o chunk's heads (whole heads, or one) have R words
+    # of partials per segment; direct_segments of them fit one 16-word gather
+    # and the gathers' region with their coefficients
+    nhc = max(1, min(csO, nbQ) * 32 // 128)
+    R = nhc * 132
+    cdir = p["direct_segments"]
+    assert cdir >= 1 and cdir * R <= 16 * PT
+    assert fr >= cdir * R + 2 * cdir * nhc + nhc
     assert p["lds_combine_floats"] >= 4 * SEG * G + 2 * G
+    assert p["lds_combine_floats"] <= SEG * KPAD  # it works in the key rows' region
     lds = p["lds_bytes"]
     assert lds >= 4 * (red + 16) and lds >= 4 * att and lds >= 4 * p["lds_combine_floats"]
     assert lds <= 64 * 1024
@@ -111,10 +120,25 @@ def test_qwen3_0_6b_on_any_workgroup_count(P):
 
 def test_qwen3_0_6b_default_plan():
     """The plan the bench runs: 256 workgroups, o chunks of 16 blocks (4 of
-    them), down chunks of 16 pairs (3 of them)."""
+    them, 4 heads each), down chunks of 16 pairs (3 of them); the o items
+    combine up to 15 segments themselves (960 positions)."""
     p = lq8.persist_plan(lq8.qwen3_0_6b(max_positions=512), 256)
     assert p["supported"]
     assert (p["o_chunk_blocks"], p["o_chunks"], p["down_chunk_pairs"], p["down_chunks"]) == (16, 4, 16, 3)
+    assert p["direct_segments"] == 15
+
+
+def test_advisor_layouts_fit():
+    """Layouts whose o chunks cover 8 heads (32 blocks: hidden 1024 with 16
+    heads on 128-255 workgroups, hidden 512 with 16 heads on 64-127) once
+    had a P3 gather sized for 1024 words of a 1056-word run; every such plan
+    now holds its runs in full (direct_segments from the run length)."""
+    for H, P in ((1024, 128), (1024, 200), (1024, 255), (512, 64), (512, 100)):
+        c = cfg(H, 3072 if H == 1024 else 1536, 16, 8)
+        p = lq8.persist_plan(c, P)
+        assert p["supported"] and p["o_chunk_blocks"] == 32
+        assert p["direct_segments"] == 16 * PT // (8 * 132)
+        check_plan(c, P, p)
 
 
 @pytest.mark.parametrize("max_pos", [1, 64, 512, 513, 4096, 40960, 131072])
