@@ -348,6 +348,40 @@ def decode_only(ctx, path, new_tokens):
     print(f"decode ({path}): {st['decode_tokens_per_s']:.1f} tok/s over {new_tokens} tokens, graph {st['used_graph']}, "
           f"persistent {st['used_persistent']}", flush=True)
     model.free()
+    # a device copy of known size: calibrates FETCH_SIZE / WRITE_SIZE when profiled
+    src, dst = lq8.DeviceBuffer(ctx, CALIB_BYTES), lq8.DeviceBuffer(ctx, CALIB_BYTES)
+    lq8._check(lq8.lib().lq8_copy_device(ctx.handle, dst.ptr, src.ptr, CALIB_BYTES))
+    ctx.synchronize()
+    src.free()
+    dst.free()
+
+
+def floors(ctx, full=False):
+    """The hardware floors (lq8_bench_floors): the read-only streaming rate of
+    the whole chip over 1 GiB (best of the grid sizes tried), of one compute
+    unit over 64 MiB, the period of back-to-back empty launches and the
+    latency of one dependent HBM load (random lines of 1 GiB)."""
+    gib = 1 << 30
+    grids = (256, 512, 1024, 2048) if full else (256, 1024)
+    stream = {}
+    for kind, kname in ((lq8.FLOOR_STREAM, "grid-stride"), (lq8.FLOOR_STREAM_CHUNKS, "chunks")):
+        for nwg in grids:
+            lq8.bench_floor(ctx, kind, nwg, gib, 1)
+            stream[f"{kname} {nwg}"] = lq8.bench_floor(ctx, kind, nwg, gib, 5)
+    best = max(stream, key=stream.get)
+    out = {"read_peak_gbs": round(stream[best], 1), "read_peak_pattern": best,
+           "read_by_pattern_gbs": {k: round(v, 1) for k, v in stream.items()}}
+    if full:
+        # the config-1 GEMV against them: 3072 x 1024, cold (160 rotating copies), graph-replayed
+        out["gemv_3072x1024_us"] = round(rotating_gemv_us(ctx, 3072, 1024, 160), 3)
+        out["one_cu_read_gbs"] = round(lq8.bench_floor(ctx, lq8.FLOOR_STREAM, 1, 64 << 20, 3), 2)
+        out["eight_cu_read_gbs"] = round(lq8.bench_floor(ctx, lq8.FLOOR_STREAM, 8, 256 << 20, 3), 2)
+        out["empty_launch_us"] = {f"{nwg}x{thr}": round(lq8.bench_floor(ctx, lq8.FLOOR_EMPTY, nwg, thr, 2000), 3)
+                                  for nwg, thr in ((1, 64), (192, 1024), (256, 64), (256, 512), (1024, 256))}
+        out["empty_graph_node_us"] = {f"{nwg}x{thr}": round(lq8.bench_floor(ctx, lq8.FLOOR_EMPTY_GRAPH, nwg, thr, 1000), 3)
+                                      for nwg, thr in ((1, 64), (96, 1024), (192, 1024), (256, 512), (1024, 256))}
+        out["dependent_load_ns"] = round(lq8.bench_floor(ctx, lq8.FLOOR_CHASE, 1, gib, 20000), 1)
+    return out
 
 
 def sync_bench(ctx):
@@ -380,7 +414,12 @@ def main():
     ap.add_argument("--new-tokens", type=int, default=128, help="tokens generated by --decode-only")
     ap.add_argument("--sync-bench", action="store_true",
                     help="only the grid-wide synchronisation microbenchmark, one line per kind and grid size")
+    ap.add_argument("--floors", action="store_true",
+                    help="only the hardware floors (streaming read rates, launch period, HBM load latency), one line")
     args = ap.parse_args()
+    if args.floors:
+        print(json.dumps(floors(lq8.Context(0), full=True)), flush=True)
+        return
     if args.gemm_sweep:
         gemm_sweep(lq8.Context(0))
         return
@@ -454,6 +493,11 @@ def main():
         log(f"device copy 256 MiB: {copy_ms * 1e3:.1f} us, {copy_gbs:.0f} GB/s read+write")
     src.free()
     dst.free()
+    # the measured read-only streaming ceiling (the headline kernel only reads)
+    read_peak = None
+    if not args.only_step:
+        read_peak = floors(ctx)
+        log(f"read-only stream, 1 GiB: {read_peak['read_peak_gbs']} GB/s")
 
     # the single 3072 x 1024 GEMV (cold: 160 rotating copies, 535 MB)
     c1_us = float("nan")
@@ -572,7 +616,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_gemv_grouped", "launch_us": round(ms_step * 1e3, 2),
-                     "bytes_per_launch": step_bytes},
+                     "bytes_per_launch": step_bytes,
+                     "measured_read_peak_gbs": None if read_peak is None else read_peak["read_peak_gbs"],
+                     "frac_of_measured_read_peak": None if read_peak is None else
+                     round(value / read_peak["read_peak_gbs"], 4)},
         "copy_peak_gbs": None if copy_gbs is None else round(copy_gbs, 1),
         "one_launch_per_gemv_gbs": None if args.only_step else round(chain_gbs, 1),
         "one_launch_per_gemv_frac": None if args.only_step else round(chain_gbs / HBM_PEAK_GBS, 4),

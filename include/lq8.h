@@ -192,6 +192,31 @@ lq8_status lq8_bench_gemv(lq8_ctx* ctx, const lq8_gemv_problem* problems, size_t
 lq8_status lq8_bench_grid_sync(lq8_ctx* ctx, int kind, int nwg, int rounds, float* us_per_sync,
                                uint32_t* mismatches, uint32_t* gave_up);
 
+/* Hardware floors the latency-bound kernels are measured against (a
+ * diagnostic without counterpart in the reference), on the context stream:
+ *   LQ8_FLOOR_EMPTY   reps back-to-back launches of an empty kernel of nwg
+ *                     workgroups: *value = us per launch;
+ *   LQ8_FLOOR_STREAM  reps read-only passes over `bytes` of device memory by
+ *                     nwg workgroups of 512 threads (8 nontemporal 16-byte
+ *                     loads in flight per thread): *value = GB/s;
+ *   LQ8_FLOOR_CHASE   one thread following min(reps, bytes / 128) links of a
+ *                     random cycle through `bytes` (one word per 128-byte
+ *                     line): *value = ns per dependent load;
+ *   LQ8_FLOOR_STREAM_CHUNKS  as LQ8_FLOOR_STREAM, each workgroup reading one
+ *                     contiguous range: *value = GB/s;
+ *   LQ8_FLOOR_EMPTY_GRAPH  reps (<= 10000) launches of an empty kernel of nwg
+ *                     workgroups captured as one HIP graph and replayed:
+ *                     *value = us per graph node.
+ * bytes: for the streams and the chase a multiple of 4096, at most 8 GiB
+ * (allocated for the call); for the empty kernels the workgroup size in
+ * threads (a multiple of 64 up to 1024; 0: 64). */
+#define LQ8_FLOOR_EMPTY 0
+#define LQ8_FLOOR_STREAM 1
+#define LQ8_FLOOR_CHASE 2
+#define LQ8_FLOOR_STREAM_CHUNKS 3
+#define LQ8_FLOOR_EMPTY_GRAPH 4
+lq8_status lq8_bench_floors(lq8_ctx* ctx, int kind, int nwg, size_t bytes, int reps, double* value);
+
 /* Phase timeline of the persistent greedy decode (the default greedy path, see
  * lq8_generate_greedy), a diagnostic without counterpart in the reference:
  * in a library built with LQ8_PERSIST_TRACE (make trace -> liblq8_trace.so)
@@ -395,9 +420,13 @@ lq8_status lq8_model_free(lq8_model* m);
  * assembled from the reference's decoder numerics (src/transformer.rs:180-204,
  * src/attention.rs:318-403, src/mlp.rs:151-164) with a routed expert MLP.
  * A forward call decodes one token for each of T independent sequences
- * (sequence t owns KV cache slot t and writes position pos[t]); every
- * projection is applied per token (the W8A32 GEMV order), so a token's
- * result does not depend on the rest of the batch.
+ * (sequence t owns KV cache slot t and writes position pos[t]).  The
+ * attention projections follow Linear::forward on the [T, hidden] input: at
+ * T = 1 the W8A32 GEMV, at T > 1 the W8A8 GEMM (each row's activations
+ * quantized to Q8_0 on their own).  The routed experts run the per-token
+ * W8A32 GEMV order at every T.  A token's result therefore depends on
+ * whether it runs alone or in a batch (the activation quantization, about
+ * 1e-2 relative), never on the other tokens of its batch.
  * Router, from given scores s [T][num_experts] per layer: p = softmax(s)
  * (max, exp(s - max), SUM64 denominator, divide); top_k by p descending,
  * ties to the lower expert index; weights renormalised over the top_k in

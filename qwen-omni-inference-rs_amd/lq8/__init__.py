@@ -187,6 +187,7 @@ _SIGS = [
     ("lq8_linear_forward_device_noalloc", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("lq8_bench_grid_sync", C.c_int,
      [C.c_void_p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
+    ("lq8_bench_floors", C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_size_t, C.c_int, C.POINTER(C.c_double)]),
     ("lq8_persist_trace", C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     ("lq8_persist_plan", C.c_int, [C.POINTER(Qwen3ConfigC), C.c_uint32, C.POINTER(PersistInfoC)]),
     ("lq8_model_persist_picks", C.c_int,
@@ -842,6 +843,18 @@ def persist_plan(cfg: "Qwen3Config", num_workgroups: int) -> dict:
     out = {n: int(getattr(info, n)) for n, _ in PersistInfoC._fields_}
     out["supported"] = bool(out["supported"])
     return out
+
+
+FLOOR_EMPTY, FLOOR_STREAM, FLOOR_CHASE, FLOOR_STREAM_CHUNKS, FLOOR_EMPTY_GRAPH = 0, 1, 2, 3, 4
+
+
+def bench_floor(ctx: "Context", kind: int, nwg: int = 1, nbytes: int = 0, reps: int = 1) -> float:
+    """lq8_bench_floors: us per empty-kernel launch (FLOOR_EMPTY), GB/s of a
+    read-only stream (FLOOR_STREAM), or ns per dependent HBM load
+    (FLOOR_CHASE)."""
+    v = C.c_double(0.0)
+    _check(lib().lq8_bench_floors(ctx.handle, kind, nwg, nbytes, reps, C.byref(v)))
+    return float(v.value)
 
 
 PTRACE_WG, PTRACE_LAYERS, PTRACE_POINTS = 512, 64, 19
