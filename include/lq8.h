@@ -228,7 +228,7 @@ lq8_status lq8_bench_floors(lq8_ctx* ctx, int kind, int nwg, size_t bytes, int r
  * LQ8_PTRACE_POINTS.  Other builds return LQ8_ERR_INVALID_ARG. */
 #define LQ8_PTRACE_WG 512
 #define LQ8_PTRACE_LAYERS 64
-#define LQ8_PTRACE_POINTS 19
+#define LQ8_PTRACE_POINTS 25
 enum {
     LQ8_PT_P1_START = 0,     /* RmsNorm + q|k|v: workgroup enters */
     LQ8_PT_P1_NORMED = 1,    /* the layer input has arrived and is normalised */
@@ -248,7 +248,13 @@ enum {
     LQ8_PT_P6_DONE = 15,     /* the workgroup's greedy pick is out */
     LQ8_PT_P2_COMBINED = 16, /* attention: the kv head's segments are combined and out (the combining item) */
     LQ8_PT_P2_COMB_FETCHED = 17, /* combine: the other segments' first (m_c, l_c) and o_c words have arrived */
-    LQ8_PT_P2_COMB_COEF = 18     /* combine: the first batch's coefficients are done */
+    LQ8_PT_P2_COMB_COEF = 18,    /* combine: the first batch's coefficients are done */
+    LQ8_PT_P1_GATHERED = 19,     /* the layer input's words have arrived (before the join and the norm) */
+    LQ8_PT_P1_DOT = 20,          /* the q|k|v tile's group sums are in LDS */
+    LQ8_PT_P2_ROPED = 21,        /* attention: q and k normalised and rotated */
+    LQ8_PT_P3_COMBINED = 22,     /* o item: its heads' segments combined (P3's own combine) */
+    LQ8_PT_P4_NORMED = 23,       /* h2 joined and normalised */
+    LQ8_PT_P4_DOT = 24           /* the gate|up tiles' group sums are in LDS */
 };
 lq8_status lq8_persist_trace(lq8_ctx* ctx, uint64_t* out, size_t count);
 

@@ -364,20 +364,21 @@ __device__ __forceinline__ void job_dot(const Job& J, const WRegs<NTL * CH>& R, 
     }
 }
 
-// Row `lane` (< 16) of the tile: the pairwise tree over the G group sums, in
-// place in gs (column `lane` per row).  Called by a whole wave: the four
-// 16-lane quarters take the disjoint pairs of a level in turn, so the level's
-// additions are the same ones in the same places as one lane per row doing
-// them in order.
-__device__ __forceinline__ float tile_final(float* gs, int G) {
-    const int lane = tid_here() & 63, col = lane & 15, q = lane >> 4;
-    for (int s = 1; s < G; s *= 2) {
-        for (int i = 2 * s * q; i + s < G; i += 8 * s) gs[i * 16 + col] = gs[i * 16 + col] + gs[(i + s) * 16 + col];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-    return gs[col];
+// Row `lane & 15` of the tile: the pairwise tree over the G (<= PW) group
+// sums gs[i * 16 + row], in registers (all G values are read at once, then
+// v[i] = v[i] + v[i + s] for s = 1, 2, 4, ..., i + s < G: the group tree of
+// the GEMV order).
+__device__ __forceinline__ float tile_final(const float* gs, int G) {
+    const int col = tid_here() & 15;
+    float v[PW];
+#pragma unroll
+    for (int i = 0; i < PW; i++) v[i] = i < G ? gs[i * 16 + col] : 0.0f;
+#pragma unroll
+    for (int s = 1; s < PW; s *= 2)
+#pragma unroll
+        for (int i = 0; i + s < PW; i += 2 * s)
+            if (i + s < G) v[i] = v[i] + v[i + s];
+    return v[0];
 }
 
 // The pairwise tree over n (<= PERSIST_NCH) chunk sums v[0 .. n).
@@ -390,23 +391,43 @@ __device__ __forceinline__ float chunk_tree(float* v, int n) {
     return v[0];
 }
 
-// RmsNorm (src/rms_norm.rs:143-176) of xs[0, k) in place, in the order of
-// the GEMV's XS_RMSNORM staging: bf16 inputs; SUM64 of squares (wave 0);
-// inv = 1 / sqrt(sum / k + eps); out = bf16((v * inv) * bf16(w)).
-// wv: the weights w[tid + j PT] (norm_prefetch), loaded before the phase's
-// hand-off so that their latency hides behind it.
+// RmsNorm (src/rms_norm.rs:143-176) in the order of the GEMV's XS_RMSNORM
+// staging: bf16 inputs; SUM64 of squares (wave 0); inv = 1 / sqrt(sum / k +
+// eps); out = bf16((v * inv) * bf16(w)).  norm_prefetch loads the weights
+// w[tid + j PT] before the phase's hand-off, so that their latency hides
+// behind it.
 __device__ __forceinline__ void norm_prefetch(const float* w, int k, float (&wv)[NW_H]) {
     const int tid = tid_here();
 #pragma unroll
     for (int j = 0; j < NW_H; j++) wv[j] = tid + j * PT < k ? w[tid + j * PT] : 0.0f;
 }
-__device__ __forceinline__ void stage_rmsnorm(float* xs, int k, const float (&wv)[NW_H], float eps, float* red) {
+
+// The RmsNorm of the values hv[j] = v[tid + j PT] (j < NW_H) that the
+// thread holds (the caller joined them), into xs[0, k), and zero over the
+// padding [k, 64 np): the bf16 inputs go to LDS once for the reduction,
+// whose lanes read their 16 elements at once before the add chain; the
+// normalised values come from the registers.
+__device__ __forceinline__ void stage_rmsnorm_regs(float (&hv)[NW_H], float* xs, int k, int np,
+                                                   const float (&wv)[NW_H], float eps, float* red) {
     const int tid = tid_here();
-    for (int i = tid; i < k; i += PT) xs[i] = bf16_round(xs[i]);
+#pragma unroll
+    for (int j = 0; j < NW_H; j++) {
+        const int i = tid + j * PT;
+        if (i < k) {
+            hv[j] = bf16_round(hv[j]);
+            xs[i] = hv[j];
+        }
+    }
     lds_sync();
     if (tid < 64) {
+        constexpr int NL = NW_H * PT / 64;  // elements per lane, at most
+        float x[NL];
+#pragma unroll
+        for (int j = 0; j < NL; j++) x[j] = tid + 64 * j < k ? xs[tid + 64 * j] : 0.0f;
         float acc = 0.0f;
-        for (int i = tid; i < k; i += 64) acc = acc + xs[i] * xs[i];
+#pragma unroll
+        for (int j = 0; j < NL; j++)
+            if (tid + 64 * j < k) acc = acc + x[j] * x[j];
         acc = wave_sum64(acc);
         if (tid == 0) red[0] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)k) + eps));
     }
@@ -415,8 +436,9 @@ __device__ __forceinline__ void stage_rmsnorm(float* xs, int k, const float (&wv
 #pragma unroll
     for (int j = 0; j < NW_H; j++) {
         const int i = tid + j * PT;
-        if (i < k) xs[i] = bf16_round((xs[i] * inv) * bf16_round(wv[j]));
+        if (i < k) xs[i] = bf16_round((hv[j] * inv) * bf16_round(wv[j]));
     }
+    for (int i = k + tid; i < np * 64; i += PT) xs[i] = 0.0f;
     lds_sync();
 }
 
@@ -710,7 +732,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             if (w < dims_of(*opaque_args(pa)).T1) {
                 LAYER_LOCALS;
                 PTRACE(LQ8_PT_P1_START);
-                float nw[NW_H];
+                float nw[NW_H], hv[NW_H];
                 norm_prefetch(Lw.in_norm, D.H, nw);
                 if (l > 0) {
                     // h_l = h2 of layer l - 1 + its down projection's chunk sums
@@ -720,34 +742,40 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     tfetch_lin<NW_RES>((1 + a.nchD) * D.H, tag, hp, f, a.abort_flag, bad);
                     lds_sync();
                     if (bad_now(bad)) goto done;
+                    PTRACE(LQ8_PT_P1_GATHERED);
                     const int n1 = min(D.T1, P);
-                    for (int r = tid; r < D.H; r += PT) {
-                        float v[PERSIST_NCH];
 #pragma unroll
-                        for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchD ? f[(1 + q) * D.H + r] : 0.0f;
-                        const float h = f[r] + chunk_tree(v, a.nchD);
-                        xs[r] = h;
-                        if (r % n1 == w) tput(resl + r, h, tag);
+                    for (int j = 0; j < NW_H; j++) {
+                        const int r = tid + j * PT;
+                        if (r < D.H) {
+                            float v[PERSIST_NCH];
+#pragma unroll
+                            for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchD ? f[(1 + q) * D.H + r] : 0.0f;
+                            hv[j] = f[r] + chunk_tree(v, a.nchD);
+                            if (r % n1 == w) tput(resl + r, hv[j], tag);
+                        }
                     }
                 } else {
                     // the embedding row (src/embedding.rs), published as h_0
                     const int n1 = min(D.T1, P);
-                    for (int j = tid; j < D.H; j += PT) {
-                        const float e = q8_elem(a.emb_c, a.emb_s, D.npH, (int)tok, j);
-                        xs[j] = e;
-                        if (j % n1 == w) tput(resl + j, e, tag);
+#pragma unroll
+                    for (int j = 0; j < NW_H; j++) {
+                        const int r = tid + j * PT;
+                        if (r < D.H) {
+                            hv[j] = q8_elem(a.emb_c, a.emb_s, D.npH, (int)tok, r);
+                            if (r % n1 == w) tput(resl + r, hv[j], tag);
+                        }
                     }
                 }
-                stage_pad(xs, D.H, D.npH);
-                lds_sync();
                 if (bad_now(bad)) goto done;
-                stage_rmsnorm(xs, D.H, nw, a.eps, red);
+                stage_rmsnorm_regs(hv, xs, D.H, D.npH, nw, a.eps, red);
                 PTRACE(LQ8_PT_P1_NORMED);
                 for (int t = w; t < D.T1; t += P) {
                     const Job J = job_qkv(a, D, Lw, t);
                     if (t != w) job_load<1, CHH>(J, R1);
                     job_dot<1, CHH>(J, R1, xs, gs);
                     lds_sync();
+                    PTRACE(LQ8_PT_P1_DOT);
                     if (tid < 64) {
                         const float y = tile_final(gs, J.G);
                         const int row = t * 16 + tid;
@@ -823,6 +851,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                         }
                     }
                     lds_sync();
+                    PTRACE(LQ8_PT_P2_ROPED);
                     seg_scores<PT, true, true>(kreg, nj, newrow, kn, qs, G, a.scale, ks, sc, mlc);
                     lds_sync();
                     PTRACE(LQ8_PT_P2_SCORES);
@@ -912,20 +941,42 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                         // segment order, m' = max(m, m_c), a_c = exp(m - m'),
                         // b_c = exp(m_c - m'), den = den a_c + b_c l_c; per
                         // element num = num a_c + b_c o_c, x = num / den
-                        if (tid < nh) {
-                            float m = -__builtin_huge_valf(), den = 0.0f;
-                            for (int cc = 0; cc < C; cc++) {
-                                const int q = cc * nh + tid;
-                                const float mc = pr[cc * R + tid * ATT_PART_STRIDE + 128];
-                                const float lc = pr[cc * R + tid * ATT_PART_STRIDE + 129];
-                                const float mn = m > mc ? m : mc;
-                                const float ea = expf_cr(m - mn), eb = expf_cr(mc - mn);
-                                coef[2 * q] = ea;
-                                coef[2 * q + 1] = eb;
-                                den = den * ea + eb * lc;
-                                m = mn;
+                        // one wave per head (nh <= PW), lane j holding segment j
+                        // (C <= cdir < 64): every lane follows the running
+                        // maximum and then den in segment order over the
+                        // values read from their lanes, and each computes its
+                        // own segment's a_j, b_j
+                        {
+                            const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+                            if (wave < nh) {
+                                const int h = wave;
+                                const float mc = lane < C ? pr[lane * R + h * ATT_PART_STRIDE + 128] : 0.0f;
+                                const float lc = lane < C ? pr[lane * R + h * ATT_PART_STRIDE + 129] : 0.0f;
+                                float m = -__builtin_huge_valf(), mp = 0.0f, mn = 0.0f;
+                                for (int cc = 0; cc < C; cc++) {
+                                    const float mcc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mc), cc));
+                                    const float mx = m > mcc ? m : mcc;
+                                    if (lane == cc) {
+                                        mp = m;
+                                        mn = mx;
+                                    }
+                                    m = mx;
+                                }
+                                const float ea = lane < C ? expf_cr(mp - mn) : 0.0f;
+                                const float eb = lane < C ? expf_cr(mc - mn) : 0.0f;
+                                if (lane < C) {
+                                    coef[2 * (lane * nh + h)] = ea;
+                                    coef[2 * (lane * nh + h) + 1] = eb;
+                                }
+                                float den = 0.0f;
+                                for (int cc = 0; cc < C; cc++) {
+                                    const float a_c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ea), cc));
+                                    const float b_c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(eb), cc));
+                                    const float l_c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lc), cc));
+                                    den = den * a_c + b_c * l_c;
+                                }
+                                if (lane == 0) dens[h] = den;
                             }
-                            dens[tid] = den;
                         }
                         lds_sync();
                         for (int k = tid; k < rng; k += PT) {
@@ -936,6 +987,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                                       coef[2 * (cc * nh + hh) + 1] * pr[cc * R + hh * ATT_PART_STRIDE + ((i0 + k) & 127)];
                             xs[k] = __fdiv_rn(num, dens[hh]);
                         }
+                        PTRACE(LQ8_PT_P3_COMBINED);
                     } else {
                         tfetch_lin<NW_ATT>(rng, tag, attl + i0, xs, a.abort_flag, bad);
                         lds_sync();
@@ -979,20 +1031,24 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     if (bad_now(bad)) goto done;
                     PTRACE(LQ8_PT_P4_STAGED);
                     const int n4 = min(D.TI, P);
-                    for (int r = tid; r < D.H; r += PT) {
-                        float v[PERSIST_NCH];
+                    float hv[NW_H];
 #pragma unroll
-                        for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchO ? f[(1 + q) * D.H + r] : 0.0f;
-                        const float h2 = f[r] + chunk_tree(v, a.nchO);
-                        xs[r] = h2;
-                        if (r % n4 == w) tput(h2b + r, h2, tag);
+                    for (int j = 0; j < NW_H; j++) {
+                        const int r = tid + j * PT;
+                        if (r < D.H) {
+                            float v[PERSIST_NCH];
+#pragma unroll
+                            for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchO ? f[(1 + q) * D.H + r] : 0.0f;
+                            hv[j] = f[r] + chunk_tree(v, a.nchO);
+                            if (r % n4 == w) tput(h2b + r, hv[j], tag);
+                        }
                     }
-                    stage_pad(xs, D.H, D.npH);
-                    lds_sync();
-                    stage_rmsnorm(xs, D.H, nw, a.eps, red);
+                    stage_rmsnorm_regs(hv, xs, D.H, D.npH, nw, a.eps, red);
+                    PTRACE(LQ8_PT_P4_NORMED);
                 }
                 job_dot<2, CHH>(J, R4, xs, gs);
                 lds_sync();
+                PTRACE(LQ8_PT_P4_DOT);
                 if (tid < 64) {
                     const float g = tile_final(gs, J.G), u = tile_final(gs + J.G * 16, J.G);
                     if (tid < 16) tput(actb + t * 16 + tid, silu_mul(g, u), tag);
@@ -1118,15 +1174,18 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             tfetch_lin<NW_RES>((1 + a.nchD) * D.H, tag, hp, f, a.abort_flag, bad);
             lds_sync();
             if (bad_now(bad)) goto done;
-            for (int r = tid; r < D.H; r += PT) {
-                float v[PERSIST_NCH];
+            float hv[NW_H];
 #pragma unroll
-                for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchD ? f[(1 + q) * D.H + r] : 0.0f;
-                xs[r] = f[r] + chunk_tree(v, a.nchD);
+            for (int j = 0; j < NW_H; j++) {
+                const int r = tid + j * PT;
+                if (r < D.H) {
+                    float v[PERSIST_NCH];
+#pragma unroll
+                    for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchD ? f[(1 + q) * D.H + r] : 0.0f;
+                    hv[j] = f[r] + chunk_tree(v, a.nchD);
+                }
             }
-            stage_pad(xs, D.H, np);
-            lds_sync();
-            stage_rmsnorm(xs, D.H, nw, a.eps, red);
+            stage_rmsnorm_regs(hv, xs, D.H, np, nw, a.eps, red);
             PTRACE(LQ8_PT_P6_NORMED);
             float bv = -__builtin_huge_valf();
             int bi = -1;

@@ -857,14 +857,16 @@ def bench_floor(ctx: "Context", kind: int, nwg: int = 1, nbytes: int = 0, reps: 
     return float(v.value)
 
 
-PTRACE_WG, PTRACE_LAYERS, PTRACE_POINTS = 512, 64, 19
+PTRACE_WG, PTRACE_LAYERS, PTRACE_POINTS = 512, 64, 25
 PTRACE_MARKS = ("P1_START", "P1_NORMED", "P2_START", "P2_QKV_IN", "P2_SCORES", "P2_PARTIALS", "P3_START",
                 "P3_STAGED", "P4_START", "P4_STAGED", "P5_START", "P5_STAGED", "P5_DONE", "P6_START", "P6_NORMED",
-                "P6_DONE", "P2_COMBINED", "P2_COMB_FETCHED", "P2_COMB_COEF")
+                "P6_DONE", "P2_COMBINED", "P2_COMB_FETCHED", "P2_COMB_COEF", "P1_GATHERED", "P1_DOT", "P2_ROPED",
+                "P3_COMBINED", "P4_NORMED", "P4_DOT")
 # the marks of a decoder layer, in phase order, and of the lm_head phase (layer 0's row)
-PTRACE_LAYER_MARKS = ("P1_START", "P1_NORMED", "P2_START", "P2_QKV_IN", "P2_SCORES", "P2_PARTIALS",
-                      "P2_COMB_FETCHED", "P2_COMB_COEF", "P2_COMBINED",
-                      "P3_START", "P3_STAGED", "P4_START", "P4_STAGED", "P5_START", "P5_STAGED", "P5_DONE")
+PTRACE_LAYER_MARKS = ("P1_START", "P1_GATHERED", "P1_NORMED", "P1_DOT", "P2_START", "P2_QKV_IN", "P2_ROPED",
+                      "P2_SCORES", "P2_PARTIALS", "P2_COMB_FETCHED", "P2_COMB_COEF", "P2_COMBINED",
+                      "P3_START", "P3_STAGED", "P3_COMBINED", "P4_START", "P4_STAGED", "P4_NORMED", "P4_DOT",
+                      "P5_START", "P5_STAGED", "P5_DONE")
 PTRACE_HEAD_MARKS = ("P6_START", "P6_NORMED", "P6_DONE")
 
 
