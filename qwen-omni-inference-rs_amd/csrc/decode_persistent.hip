@@ -146,14 +146,23 @@ __device__ __forceinline__ uint64_t traw(const uint64_t* p) {
 }
 __device__ __forceinline__ bool tok_tag(uint64_t v, unsigned tag) { return (unsigned)(v >> 32) == tag; }
 
-// The workgroup's abort mark as a wave-uniform value (all lanes read the same
-// LDS word; readfirstlane tells the compiler so, keeping the branches on it
-// uniform).
-__device__ __forceinline__ bool bad_now(volatile int* bad) { return __builtin_amdgcn_readfirstlane(*bad) != 0; }
+// The workgroup's abort mark: an LDS word behind a generic pointer.  Its
+// reads are flat loads, after which the wave waits for vmcnt(0) -- on this
+// chip that counts the wave's outstanding stores too, so a check also waits
+// for the write-through of the hand-off words the wave has just published.
+// Measured with Qwen3-0.6B (tok/s, interleaved runs): this form 1501, the mark
+// addressed as LDS (address space 3, lgkmcnt waits only) 1485, that plus an
+// explicit vmcnt(0) drain after every publication 1367, this form without the
+// check after P1's join 1484 -- so the checks stay as they are.
+typedef volatile int* LdsFlag;
+
+// The abort mark as a wave-uniform value (all lanes read the same LDS word;
+// readfirstlane tells the compiler so, keeping the branches on it uniform).
+__device__ __forceinline__ bool bad_now(LdsFlag bad) { return __builtin_amdgcn_readfirstlane(*bad) != 0; }
 
 // One poll of a bounded wait: false to go on polling; true (with *bad set)
 // once the poll limit is reached or another workgroup raised the abort flag.
-__device__ __forceinline__ bool poll_stop(unsigned& spins, unsigned* abort_flag, volatile int* bad) {
+__device__ __forceinline__ bool poll_stop(unsigned& spins, unsigned* abort_flag, LdsFlag bad) {
     if (*bad) return true;
     ++spins;
     if ((spins & 63) == 0 && sync_load(abort_flag) != 0) {
@@ -176,7 +185,7 @@ __device__ __forceinline__ bool poll_stop(unsigned& spins, unsigned* abort_flag,
 // while some have not landed, one lane of the wave polls one of them and the
 // next round loads the wave's missing words again.
 template <int NW, typename Ok, typename Src, typename Dst>
-__device__ __forceinline__ void tfetch(unsigned tag, Ok ok, Src src, Dst dst, unsigned* abort_flag, volatile int* bad) {
+__device__ __forceinline__ void tfetch(unsigned tag, Ok ok, Src src, Dst dst, unsigned* abort_flag, LdsFlag bad) {
     unsigned pend = 0;
     {
         const int tid = tid_here();
@@ -213,7 +222,7 @@ __device__ __forceinline__ void tfetch(unsigned tag, Ok ok, Src src, Dst dst, un
 // The linear case: words src[0, n) into dst[0, n).
 template <int NW>
 __device__ __forceinline__ void tfetch_lin(int n, unsigned tag, const uint64_t* src, float* dst, unsigned* abort_flag,
-                                           volatile int* bad) {
+                                           LdsFlag bad) {
     tfetch<NW>(tag, [&](int t, int u) { return t + u * PT < n; }, [&](int t, int u) { return src + t + u * PT; },
                [&](int t, int u) { return dst + t + u * PT; }, abort_flag, bad);
 }
@@ -372,7 +381,7 @@ __device__ __forceinline__ float tile_final(const float* gs, int G) {
     const int col = tid_here() & 15;
     float v[PW];
 #pragma unroll
-    for (int i = 0; i < PW; i++) v[i] = i < G ? gs[i * 16 + col] : 0.0f;
+    for (int i = 0; i < PW; i++) v[i] = gs[min(i, G - 1) * 16 + col];  // read unconditionally, used below G
 #pragma unroll
     for (int s = 1; s < PW; s *= 2)
 #pragma unroll
@@ -423,7 +432,7 @@ __device__ __forceinline__ void stage_rmsnorm_regs(float (&hv)[NW_H], float* xs,
         constexpr int NL = NW_H * PT / 64;  // elements per lane, at most
         float x[NL];
 #pragma unroll
-        for (int j = 0; j < NL; j++) x[j] = tid + 64 * j < k ? xs[tid + 64 * j] : 0.0f;
+        for (int j = 0; j < NL; j++) x[j] = xs[min(tid + 64 * j, k - 1)];  // read unconditionally, used below k
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < NL; j++)
@@ -498,7 +507,7 @@ template <typename Mark>
 __device__ __forceinline__ bool combine_heads(unsigned tag, int C, int g, int G, int NH, const uint64_t* partb,
                                               uint64_t* attl, float* cm, const float* own_ml,
                                               const float (&own)[CMB_EK], unsigned* abort_flag,
-                                              volatile int* bad, Mark mark) {
+                                              LdsFlag bad, Mark mark) {
     const int tid = tid_here(), lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     float* ml = cm;
@@ -692,7 +701,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
     __shared__ int bad_s;
     __shared__ float pick_v[PW];
     __shared__ int pick_i[PW];
-    volatile int* bad = &bad_s;
+    const LdsFlag bad = &bad_s;
     const int P = gridDim.x, w = blockIdx.x;
     if (threadIdx.x == 0) bad_s = 0;
     lds_sync();
@@ -744,14 +753,18 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     if (bad_now(bad)) goto done;
                     PTRACE(LQ8_PT_P1_GATHERED);
                     const int n1 = min(D.T1, P);
+                    // the chunk sums are read unconditionally (an index past
+                    // nchD reads the last chunk, which chunk_tree ignores), so
+                    // all of a thread's LDS reads are in flight together
+                    const int nchD = a.nchD;
 #pragma unroll
                     for (int j = 0; j < NW_H; j++) {
                         const int r = tid + j * PT;
                         if (r < D.H) {
                             float v[PERSIST_NCH];
 #pragma unroll
-                            for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchD ? f[(1 + q) * D.H + r] : 0.0f;
-                            hv[j] = f[r] + chunk_tree(v, a.nchD);
+                            for (int q = 0; q < PERSIST_NCH; q++) v[q] = f[(1 + min(q, nchD - 1)) * D.H + r];
+                            hv[j] = f[r] + chunk_tree(v, nchD);
                             if (r % n1 == w) tput(resl + r, hv[j], tag);
                         }
                     }
@@ -1030,7 +1043,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     lds_sync();
                     if (bad_now(bad)) goto done;
                     PTRACE(LQ8_PT_P4_STAGED);
-                    const int n4 = min(D.TI, P);
+                    const int n4 = min(D.TI, P), nchO = a.nchO;
                     float hv[NW_H];
 #pragma unroll
                     for (int j = 0; j < NW_H; j++) {
@@ -1038,8 +1051,8 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                         if (r < D.H) {
                             float v[PERSIST_NCH];
 #pragma unroll
-                            for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchO ? f[(1 + q) * D.H + r] : 0.0f;
-                            hv[j] = f[r] + chunk_tree(v, a.nchO);
+                            for (int q = 0; q < PERSIST_NCH; q++) v[q] = f[(1 + min(q, nchO - 1)) * D.H + r];
+                            hv[j] = f[r] + chunk_tree(v, nchO);
                             if (r % n4 == w) tput(h2b + r, hv[j], tag);
                         }
                     }
@@ -1175,14 +1188,15 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             lds_sync();
             if (bad_now(bad)) goto done;
             float hv[NW_H];
+            const int nchD = a.nchD;
 #pragma unroll
             for (int j = 0; j < NW_H; j++) {
                 const int r = tid + j * PT;
                 if (r < D.H) {
                     float v[PERSIST_NCH];
 #pragma unroll
-                    for (int q = 0; q < PERSIST_NCH; q++) v[q] = q < a.nchD ? f[(1 + q) * D.H + r] : 0.0f;
-                    hv[j] = f[r] + chunk_tree(v, a.nchD);
+                    for (int q = 0; q < PERSIST_NCH; q++) v[q] = f[(1 + min(q, nchD - 1)) * D.H + r];
+                    hv[j] = f[r] + chunk_tree(v, nchD);
                 }
             }
             stage_rmsnorm_regs(hv, xs, D.H, np, nw, a.eps, red);
