@@ -450,7 +450,9 @@ __global__ __launch_bounds__(LONG_THREADS) void k_gemv_long(GemvArgs a) {
 // ---- multi-vector GEMV ------------------------------------------------------
 //
 // One workgroup (4 waves) per (problem, 16-row tile, vector split); with
-// EPI_SWIGLU per (problem, gate tile i) and it also runs up tile i + rows/32.
+// EPI_SWIGLU per (problem, tile pair 2i, 2i + 1) of a weight whose tiles
+// interleave gate and up by 8 rows (tile t: gate rows 8t .. 8t+7, then up
+// rows 8t .. 8t+7), which gives silu(gate) * up of rows 16i .. 16i+15.
 // Up to VB input vectors are staged in LDS at a time; a wave takes (tile,
 // group of CH pairs) items, unpacks each 16-byte code chunk to floats once
 // and runs the GEMV order of gemv_tiles for every staged vector; the group
@@ -461,12 +463,12 @@ __global__ __launch_bounds__(LONG_THREADS) void k_gemv_long(GemvArgs a) {
 template <int XS, int EPI, int CH, int VB, bool PF, int NTS>
 __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
     extern __shared__ float smem[];
-    // tiles per workgroup: gate tile i with up tile i + rows/32 (EPI_SWIGLU),
-    // else NTS consecutive tiles from `tile` (the host keeps tiles % NTS == 0)
+    // tiles per workgroup: NT consecutive tiles from `tile` (the host keeps
+    // tiles % NT == 0; EPI_SWIGLU: the pair 2i, 2i + 1)
     constexpr int NT = EPI == EPI_SWIGLU ? 2 : NTS;
     const int tiles_all = (a.rows + TILE_ROWS - 1) / TILE_ROWS;
-    const int tiles_p = tiles_all / NT, tstride = EPI == EPI_SWIGLU ? tiles_all / 2 : 1;
-    const int j = blockIdx.x / tiles_p, tile = (blockIdx.x - j * tiles_p) * (EPI == EPI_SWIGLU ? 1 : NTS);
+    const int tiles_p = tiles_all / NT;
+    const int j = blockIdx.x / tiles_p, tile = (blockIdx.x - j * tiles_p) * NT;
     if (j >= (a.n_prob ? *a.n_prob : 1)) return;
     const int e = a.prob_id ? a.prob_id[j] : j;
     const int vbeg = a.vec_begin ? a.vec_begin[j] : 0;
@@ -486,7 +488,7 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
     const size_t gt = (size_t)e * a.prob_tiles + tile;
     const int8_t* cbase = a.codes + gt * np * CHUNK_BYTES + lane * 16;
     const uint16_t* sbase = a.scales + gt * 2 * np * 16 + bsel * 16 + r;
-    const size_t cstep = (size_t)tstride * np * CHUNK_BYTES, sstep = (size_t)tstride * 2 * np * 16;
+    const size_t cstep = (size_t)np * CHUNK_BYTES, sstep = (size_t)2 * np * 16;  // the next tile
     const int items = NT * G;
     // weights of item `it` (clamped: every load in bounds and unconditional)
     u32x4 pv[CH];
@@ -726,9 +728,11 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
         if (EPI == EPI_SWIGLU) {
             __syncthreads();
             if (tid < nv * 16) {
+                // output row 8 tile + rr: gate row rr & 7 of tile tile + rr / 8, up row 8 + (rr & 7)
                 const int v = tid >> 4, rr = tid & 15;
-                const float gate = gs[(v * NT) * G * 16 + rr], up = gs[(v * NT + 1) * G * 16 + rr];
-                const int row = tile * TILE_ROWS + rr;  // < rows / 2 (a multiple of 16)
+                const float* ts = gs + (v * NT + (rr >> 3)) * G * 16;
+                const float gate = ts[rr & 7], up = ts[8 + (rr & 7)];
+                const int row = tile * 8 + rr;  // < rows / 2 (a multiple of 16)
                 const int ent = vbeg + v0 + v;
                 const int slot = a.slots ? a.slots[ent] : ent;
                 a.y[(size_t)slot * a.y_stride + row] = silu_mul(gate, up);
@@ -746,12 +750,22 @@ __global__ __launch_bounds__(256) void k_gemv_mv(MvArgs a) {
 // and over the groups) -- then h[row] = h2[row] + sum over the experts in
 // ascending index of w * y (k_moe_combine's order).  The expert outputs never
 // leave the workgroup.
+//
+// FAST (K * G <= 32 items, G <= 8 groups, the inputs in 3 float4 per
+// thread): the inputs -- which do not depend on the routing -- are loaded
+// first, the routing (experts, weights) once per lane, then every item's
+// weights (two per wave), so that no load waits behind another's round trip;
+// the rank order comes from lane exchanges, and the trees over the groups
+// and the combine run in registers of the first 16 lanes.  Otherwise the
+// weights of a wave's next item are prefetched while it computes one.
 constexpr int MOE_DOWN_THREADS = 1024;
+constexpr int MOE_DOWN_FAST_GMAX = 8;
 
-template <int CH>
+template <int CH, bool FAST>
 __global__ __launch_bounds__(MOE_DOWN_THREADS) void k_moe_down_combine(MoeDownArgs a) {
     extern __shared__ float smem[];
     __shared__ int order[MOE_DOWN_MAX_K];
+    constexpr int NW = MOE_DOWN_THREADS / 64;
     const int tile = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.K, k = a.k, k4 = k >> 2, nb = k >> 5, np = (nb + 1) >> 1;
@@ -759,53 +773,19 @@ __global__ __launch_bounds__(MOE_DOWN_THREADS) void k_moe_down_combine(MoeDownAr
     float* xs = smem;                 // [K][np * 64]
     float* gs = xs + K * np * 64;     // [K][G][16]
     const int r = lane & 15, part = lane >> 4, bsel = part >> 1, half = part & 1;
-    if (tid < K) {
-        const uint32_t me = a.rids[tid];
-        int below = 0;
-        for (int q = 0; q < K; q++) below += a.rids[q] < me;
-        order[below] = tid;  // the routed experts of a token are distinct
-    }
-    // weights of item `it` = (rank-ordered expert q, group g), clamped
-    u32x4 pv[CH];
-    uint16_t ps[CH];
-    auto load_item = [&](int it_) {
-        const int itc = min(it_, items - 1), q = itc / G, g = itc - q * G;
-        const size_t gt = (size_t)a.rids[q] * a.prob_tiles + tile;  // rank q's expert (raw rank order)
-        const int8_t* cb = a.codes + gt * np * CHUNK_BYTES + lane * 16;
-        const uint16_t* sb = a.scales + gt * 2 * np * 16 + bsel * 16 + r;
-#pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int c = min(g * CH + i, np - 1);
-            pv[i] = __builtin_nontemporal_load((const u32x4*)(cb + (size_t)c * CHUNK_BYTES));
-            ps[i] = sb[(size_t)c * 32];
-        }
-    };
-    load_item(wave);
-    // stage the K input vectors in rank order (silu(gate) * up of each expert)
-    for (int q = 0; q < K; q++) {
-        const float* x = a.x + (size_t)q * a.x_stride;
-        float* xv = xs + q * np * 64;
-        for (int i4 = tid; i4 < k4; i4 += MOE_DOWN_THREADS) *(float4*)(xv + 4 * i4) = *(const float4*)(x + 4 * i4);
-        if ((nb & 1) && tid < 32) xv[k + tid] = 0.0f;
-    }
-    __syncthreads();
-    for (int it = wave; it < items; it += MOE_DOWN_THREADS / 64) {
+    // group sum of item `it` = (rank-ordered expert q, group g) from its weights
+    auto run_item = [&](int it, const u32x4 (&cv)[CH], const uint16_t (&ds)[CH]) {
         const int q = it / G, g = it - q * G;
-        u32x4 cv[CH];
-        uint16_t ds[CH];
-#pragma unroll
-        for (int i = 0; i < CH; i++) {
-            cv[i] = pv[i];
-            ds[i] = ps[i];
-        }
-        load_item(it + MOE_DOWN_THREADS / 64);  // the next item's weights while this one computes
         const float* xv = xs + q * np * 64;
         const int cnt = min(CH, np - g * CH);
         float t[CH];
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int p = min(g * CH + i, np - 1);
-            const float h = dot16(cv[i], xv + (2 * p + bsel) * 32 + half * 16);
+            u32x4 c = cv[i];
+            // held items: the empty asm keeps the byte unpacking here
+            if constexpr (FAST) asm volatile("" : "+v"(c.x), "+v"(c.y), "+v"(c.z), "+v"(c.w));
+            const float h = dot16(c, xv + (2 * p + bsel) * 32 + half * 16);
             const LanePair hh = lanes16(h);
             const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(ds[i]);
             const LanePair vv = lanes32(vb);
@@ -817,23 +797,270 @@ __global__ __launch_bounds__(MOE_DOWN_THREADS) void k_moe_down_combine(MoeDownAr
             for (int i = 0; i + s2 < CH; i += 2 * s2)
                 if (i + s2 < cnt) t[i] = t[i] + t[i + s2];
         if (lane < 16) gs[(q * G + g) * 16 + lane] = t[0];
-    }
-    __syncthreads();
-    // tree over the group sums, one thread per (rank, row)
-    if (tid < K * 16) {
-        float* col = gs + (tid >> 4) * G * 16 + (tid & 15);
-        for (int s2 = 1; s2 < G; s2 *= 2)
-            for (int i = 0; i + s2 < G; i += 2 * s2) col[i * 16] = col[i * 16] + col[(i + s2) * 16];
-    }
-    __syncthreads();
-    if (tid < 16) {
-        const int row = tile * TILE_ROWS + tid;
-        float acc = 0.0f;
-        for (int q = 0; q < K; q++) {
-            const int rk = order[q];
-            acc = acc + a.rw[rk] * gs[rk * G * 16 + tid];
+    };
+    // weights of item `it`, clamped (every load in bounds), of expert e_of(q)
+    auto load_item = [&](int it_, uint32_t e, u32x4 (&pv)[CH], uint16_t (&ps)[CH]) {
+        const int itc = min(it_, items - 1), g = itc - (itc / G) * G;
+        const size_t gt = (size_t)e * a.prob_tiles + tile;
+        const int8_t* cb = a.codes + gt * np * CHUNK_BYTES + lane * 16;
+        const uint16_t* sb = a.scales + gt * 2 * np * 16 + bsel * 16 + r;
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int c = min(g * CH + i, np - 1);
+            pv[i] = __builtin_nontemporal_load((const u32x4*)(cb + (size_t)c * CHUNK_BYTES));
+            ps[i] = sb[(size_t)c * 32];
         }
-        if (row < a.rows) a.out[row] = a.h2[row] + acc;
+    };
+    if constexpr (FAST) {
+        // the K inputs, entry i = q * k4 + i4 (clamped: every load in bounds)
+        const int nx = K * k4;
+        auto xaddr = [&](int i) {
+            const int q = i / k4;
+            return (const float4*)(a.x + (size_t)q * a.x_stride + 4 * (i - q * k4));
+        };
+        const float4 x0 = *xaddr(min(tid, nx - 1));
+        const float4 x1 = *xaddr(min(tid + MOE_DOWN_THREADS, nx - 1));
+        const float4 x2 = *xaddr(min(tid + 2 * MOE_DOWN_THREADS, nx - 1));
+        // the routing: lane q holds rank q's expert and weight
+        const uint32_t rid = a.rids[min(lane, K - 1)];
+        const float rwt = a.rw[min(lane, K - 1)];
+        const float h2 = a.h2[min(tile * TILE_ROWS + (lane & 15), a.rows - 1)];
+        auto expert = [&](int it) {  // it wave-uniform
+            const int q = min(it, items - 1) / G;
+            return (uint32_t)__builtin_amdgcn_readlane((int)rid, q);
+        };
+        u32x4 pa[2][CH];
+        uint16_t sa[2][CH];
+        load_item(wave, expert(wave), pa[0], sa[0]);
+        load_item(wave + NW, expert(wave + NW), pa[1], sa[1]);
+        if (wave == 0 && lane < K) {
+            int below = 0;
+            for (int q = 0; q < K; q++) below += (uint32_t)__builtin_amdgcn_readlane((int)rid, q) < rid;
+            order[below] = lane;  // the routed experts of a token are distinct
+        }
+        // stage the K input vectors in rank order (silu(gate) * up of each expert)
+        auto xstore = [&](int i, float4 v) {
+            if (i < nx) {
+                const int q = i / k4;
+                *(float4*)(xs + q * np * 64 + 4 * (i - q * k4)) = v;
+            }
+        };
+        xstore(tid, x0);
+        xstore(tid + MOE_DOWN_THREADS, x1);
+        xstore(tid + 2 * MOE_DOWN_THREADS, x2);
+        if (nb & 1)
+            for (int i = tid; i < K * 32; i += MOE_DOWN_THREADS) xs[(i >> 5) * np * 64 + k + (i & 31)] = 0.0f;
+        __syncthreads();
+        if (wave < items) run_item(wave, pa[0], sa[0]);
+        if (wave + NW < items) run_item(wave + NW, pa[1], sa[1]);
+        __syncthreads();
+        // the tree over each rank's groups, then the combine in ascending expert order
+        if (tid < 16) {
+            float acc = 0.0f;
+            for (int qq = 0; qq < K; qq++) {
+                const int rk = __builtin_amdgcn_readfirstlane(order[qq]);
+                float v[MOE_DOWN_FAST_GMAX];
+#pragma unroll
+                for (int i = 0; i < MOE_DOWN_FAST_GMAX; i++) v[i] = gs[(rk * G + min(i, G - 1)) * 16 + tid];
+#pragma unroll
+                for (int s2 = 1; s2 < MOE_DOWN_FAST_GMAX; s2 *= 2)
+#pragma unroll
+                    for (int i = 0; i + s2 < MOE_DOWN_FAST_GMAX; i += 2 * s2)
+                        if (i + s2 < G) v[i] = v[i] + v[i + s2];
+                acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rwt), rk)) * v[0];
+            }
+            const int row = tile * TILE_ROWS + tid;
+            if (row < a.rows) a.out[row] = h2 + acc;
+        }
+    } else {
+        if (tid < K) {
+            const uint32_t me = a.rids[tid];
+            int below = 0;
+            for (int q = 0; q < K; q++) below += a.rids[q] < me;
+            order[below] = tid;  // the routed experts of a token are distinct
+        }
+        auto load = [&](int it_, u32x4 (&pv)[CH], uint16_t (&ps)[CH]) {
+            load_item(it_, a.rids[min(it_, items - 1) / G], pv, ps);  // rank q's expert (raw rank order)
+        };
+        u32x4 pv[CH];
+        uint16_t ps[CH];
+        load(wave, pv, ps);
+        // stage the K input vectors in rank order (silu(gate) * up of each expert)
+        for (int q = 0; q < K; q++) {
+            const float* x = a.x + (size_t)q * a.x_stride;
+            float* xv = xs + q * np * 64;
+            for (int i4 = tid; i4 < k4; i4 += MOE_DOWN_THREADS) *(float4*)(xv + 4 * i4) = *(const float4*)(x + 4 * i4);
+            if ((nb & 1) && tid < 32) xv[k + tid] = 0.0f;
+        }
+        __syncthreads();
+        for (int it = wave; it < items; it += NW) {
+            u32x4 cv[CH];
+            uint16_t ds[CH];
+#pragma unroll
+            for (int i = 0; i < CH; i++) {
+                cv[i] = pv[i];
+                ds[i] = ps[i];
+            }
+            load(it + NW, pv, ps);  // the next item's weights while this one computes
+            run_item(it, cv, ds);
+        }
+        __syncthreads();
+        // tree over the group sums, one thread per (rank, row)
+        if (tid < K * 16) {
+            float* col = gs + (tid >> 4) * G * 16 + (tid & 15);
+            for (int s2 = 1; s2 < G; s2 *= 2)
+                for (int i = 0; i + s2 < G; i += 2 * s2) col[i * 16] = col[i * 16] + col[(i + s2) * 16];
+        }
+        __syncthreads();
+        if (tid < 16) {
+            const int row = tile * TILE_ROWS + tid;
+            float acc = 0.0f;
+            for (int q = 0; q < K; q++) {
+                const int rk = order[q];
+                acc = acc + a.rw[rk] * gs[rk * G * 16 + tid];
+            }
+            if (row < a.rows) a.out[row] = a.h2[row] + acc;
+        }
+    }
+}
+
+// Routed expert gate and up projections of one token (batch 1) with the
+// RMSNorm fused.  Every tile reads the same input and, the weight's tiles
+// interleaving gate and up by 8 rows, gives silu(gate) * up of 8 rows by
+// itself, so the K ranks' tiles (2 * inter / 16 of expert rids[q] each) form
+// one list that the workgroups split evenly, GU1_TPW tiles each
+// (Qwen3-30B-A3B: 768 tiles on 256 workgroups, one per compute unit); tile
+// t of rank q stores rows 8t .. 8t+7 of y[q].  The arithmetic is k_gemv_mv's
+// (XS_RMSNORM, EPI_SWIGLU): the SUM64 norm, 16-code fmaf chains, the lane
+// pair sums, the trees over a group's pairs and over the groups.  Wave 0
+// runs the norm alone: it loads the input and the norm weights (which do
+// not depend on the routing), writes bf16(x) to LDS, reads it back in the
+// SUM64 layout (one wave's LDS operations complete in order) and writes the
+// normalised values.  Waves 1 .. 8 issue the weights of their (at most 3)
+// items at once; their registers and the norm's are live in separate
+// branches, so they do not add up, and their loads do not delay the norm
+// wave's (spreading the norm over the item waves puts their weight loads
+// ahead of it).  One barrier orders the input before the items, one the
+// group sums before the trees over the groups, which run in registers.
+constexpr int GU1_ITEM_WAVES = 8;
+constexpr int GU1_AH = 3;                          // items per item wave
+constexpr int GU1_TPW = 3;                         // tiles per workgroup
+constexpr int GU1_THREADS = 64 * (1 + GU1_ITEM_WAVES);
+constexpr int GU1_CH = 4;
+constexpr int GU1_MAX_K = 2048;                    // the norm wave holds the input: 8 float4 per lane
+constexpr int GU1_XF = GU1_MAX_K / 256;
+constexpr int GU1_GMAX = GU1_MAX_K / 64 / GU1_CH;  // groups of a tile (np <= 32)
+static_assert(GU1_TPW * GU1_GMAX <= GU1_ITEM_WAVES * GU1_AH, "a workgroup's items fit its item waves");
+static_assert(GU1_TPW * 16 <= 64, "one wave runs the trees over the groups");
+
+__global__ __launch_bounds__(GU1_THREADS) void k_moe_gate_up1(MoeGateUpArgs a) {
+    extern __shared__ float smem[];
+    constexpr int W = GU1_ITEM_WAVES, CH = GU1_CH;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ntt = a.K * a.prob_tiles, t0 = blockIdx.x * GU1_TPW, nt = min(GU1_TPW, ntt - t0);
+    const int k = a.k, k4 = k >> 2, nb = k >> 5, np = (nb + 1) >> 1;
+    const int G = (np + CH - 1) / CH, items = nt * G;
+    float* xs = smem;               // [G * CH * 64]: the normed input, zero past k
+    float* gs = xs + G * CH * 64;   // [GU1_TPW][G][16] group sums
+    if (wave == 0) {
+        float4 xv[GU1_XF], wv[GU1_XF];
+#pragma unroll
+        for (int j = 0; j < GU1_XF; j++) {
+            const int i4 = min(lane + 64 * j, k4 - 1);
+            xv[j] = *(const float4*)(a.x + 4 * i4);
+            wv[j] = *(const float4*)(a.norm_w + 4 * i4);
+        }
+        // RmsNorm (src/rms_norm.rs:143-176): v = bf16(x); the sum of squares in
+        // the SUM64 order; inv = 1 / sqrt(sum / k + eps); n = bf16((v * inv) * bf16(w))
+#pragma unroll
+        for (int j = 0; j < GU1_XF; j++)
+            if (lane + 64 * j < k4) *(float4*)(xs + 4 * (lane + 64 * j)) = bf16_round4(xv[j]);
+        float v[GU1_MAX_K / 64];
+#pragma unroll
+        for (int u = 0; u < GU1_MAX_K / 64; u++) v[u] = xs[min(lane + 64 * u, k - 1)];
+        float acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < GU1_MAX_K / 64; u++)
+            if (lane + 64 * u < k) acc = acc + v[u] * v[u];
+        acc = wave_sum64(acc);
+        const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)k) + a.eps));
+#pragma unroll
+        for (int j = 0; j < GU1_XF; j++)
+            if (lane + 64 * j < k4) {
+                float4* p = (float4*)(xs + 4 * (lane + 64 * j));
+                *p = norm4(*p, wv[j], inv);  // bf16(x) read back: xv is not held across the sum
+            }
+        // the group padding past k (read by the padding pairs, never summed)
+        for (int i = k + lane; i < G * CH * 64; i += 64) xs[i] = 0.0f;
+        __syncthreads();
+    } else {
+        const int r = lane & 15, part = lane >> 4, bsel = part >> 1, half = part & 1;
+        const int w = wave - 1;
+        const uint32_t rid = a.rids[min(lane, a.K - 1)];  // lane q: rank q's expert
+        // the weights of this wave's items (clamped: every load in bounds)
+        u32x4 pa[GU1_AH][CH];
+        uint16_t sa[GU1_AH][CH];
+#pragma unroll
+        for (int jj = 0; jj < GU1_AH; jj++) {
+            const int it = min(w + W * jj, items - 1), tt = it / G, g = it - tt * G;
+            const int q = (t0 + tt) / a.prob_tiles, lt = t0 + tt - q * a.prob_tiles;
+            const size_t gt = (size_t)(uint32_t)__builtin_amdgcn_readlane((int)rid, q) * a.prob_tiles + lt;
+            const int8_t* cb = a.codes + gt * np * CHUNK_BYTES + lane * 16;
+            const uint16_t* sb = a.scales + gt * 2 * np * 16 + bsel * 16 + r;
+#pragma unroll
+            for (int i = 0; i < CH; i++) {
+                const int c = min(g * CH + i, np - 1);
+                pa[jj][i] = __builtin_nontemporal_load((const u32x4*)(cb + (size_t)c * CHUNK_BYTES));
+                sa[jj][i] = sb[(size_t)c * 32];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int jj = 0; jj < GU1_AH; jj++) {
+            const int it = w + W * jj;
+            if (it < items) {
+                const int tt = it / G, g = it - tt * G;
+                const int cnt = min(CH, np - g * CH);
+                float t[CH];
+#pragma unroll
+                for (int i = 0; i < CH; i++) {
+                    const int p = g * CH + i;  // past np: padding, skipped by the tree
+                    u32x4 c = pa[jj][i];
+                    asm volatile("" : "+v"(c.x), "+v"(c.y), "+v"(c.z), "+v"(c.w));  // unpack here, not at the load
+                    const float h = dot16(c, xs + (2 * p + bsel) * 32 + half * 16);
+                    // h0 + h1 (half-0 lane's sum first) and v_2p + v_2p+1, v_2p alone
+                    // when block 2p + 1 is the padding of an odd nb
+                    const LanePair hh = lanes16(h);
+                    const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(sa[jj][i]);
+                    const LanePair vv = lanes32(vb);
+                    t[i] = 2 * p + 1 >= nb ? vv.lo : vv.lo + vv.hi;
+                }
+#pragma unroll
+                for (int s2 = 1; s2 < CH; s2 *= 2)
+#pragma unroll
+                    for (int i = 0; i + s2 < CH; i += 2 * s2)
+                        if (i + s2 < cnt) t[i] = t[i] + t[i + s2];
+                if (lane < 16) gs[(tt * G + g) * 16 + lane] = t[0];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // the tree over a tile's groups: lane (tile tt, row rr); the 16 lanes
+        // of a tile hold its 8 gate rows, then its 8 up rows
+        const int tt = min(lane >> 4, nt - 1), rr = lane & 15;
+        float v[GU1_GMAX];
+#pragma unroll
+        for (int i = 0; i < GU1_GMAX; i++) v[i] = gs[(tt * G + min(i, G - 1)) * 16 + rr];
+#pragma unroll
+        for (int s2 = 1; s2 < GU1_GMAX; s2 *= 2)
+#pragma unroll
+            for (int i = 0; i + s2 < GU1_GMAX; i += 2 * s2)
+                if (i + s2 < G) v[i] = v[i] + v[i + s2];
+        const float up = lane_xor<8>(v[0]);
+        const int q = (t0 + tt) / a.prob_tiles, lt = t0 + tt - q * a.prob_tiles;
+        if (lane < nt * 16 && rr < 8) a.y[(size_t)q * a.y_stride + lt * 8 + rr] = silu_mul(v[0], up);
     }
 }
 
@@ -1046,9 +1273,30 @@ lq8_status launch_moe_down_combine(hipStream_t s, const MoeDownArgs& a) {
     const int nb = a.k >> 5, np = (nb + 1) >> 1, ch = pick_ch(np, 4), G = (np + ch - 1) / ch;
     const size_t smem = ((size_t)a.K * np * 64 + (size_t)a.K * G * 16) * sizeof(float);
     const dim3 grid((unsigned)(a.rows / TILE_ROWS));
-    if (ch == 1) hipLaunchKernelGGL(k_moe_down_combine<1>, grid, dim3(MOE_DOWN_THREADS), smem, s, a);
-    else if (ch == 2) hipLaunchKernelGGL(k_moe_down_combine<2>, grid, dim3(MOE_DOWN_THREADS), smem, s, a);
-    else hipLaunchKernelGGL(k_moe_down_combine<4>, grid, dim3(MOE_DOWN_THREADS), smem, s, a);
+    // every item's weights in flight at once (two items per wave), the inputs in registers
+    const bool fast = ch == 4 && a.K * G <= 2 * (MOE_DOWN_THREADS / 64) && G <= MOE_DOWN_FAST_GMAX &&
+                      a.K * (a.k >> 2) <= 3 * MOE_DOWN_THREADS && a.K <= 64;
+    const dim3 block(MOE_DOWN_THREADS);
+    if (fast) hipLaunchKernelGGL((k_moe_down_combine<4, true>), grid, block, smem, s, a);
+    else if (ch == 1) hipLaunchKernelGGL((k_moe_down_combine<1, false>), grid, block, smem, s, a);
+    else if (ch == 2) hipLaunchKernelGGL((k_moe_down_combine<2, false>), grid, block, smem, s, a);
+    else hipLaunchKernelGGL((k_moe_down_combine<4, false>), grid, block, smem, s, a);
+    LQ8_HIP(hipGetLastError());
+    return LQ8_OK;
+}
+
+bool moe_gate_up1_supported(int K, int inter, int k) {
+    return K >= 1 && K <= 64 && inter > 0 && inter % TILE_ROWS == 0 && k > 0 && k % 32 == 0 && k <= GU1_MAX_K;
+}
+
+lq8_status launch_moe_gate_up1(hipStream_t s, const MoeGateUpArgs& a) {
+    if (!moe_gate_up1_supported(a.K, a.inter, a.k) || a.prob_tiles != 2 * a.inter / TILE_ROWS ||
+        a.y_stride < a.inter)
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe gate+up: unsupported shape");
+    const int nb = a.k >> 5, np = (nb + 1) >> 1, G = (np + GU1_CH - 1) / GU1_CH;
+    const size_t smem = ((size_t)G * GU1_CH * 64 + (size_t)GU1_TPW * G * 16) * sizeof(float);
+    const dim3 grid((unsigned)((a.K * a.prob_tiles + GU1_TPW - 1) / GU1_TPW));
+    hipLaunchKernelGGL(k_moe_gate_up1, grid, dim3(GU1_THREADS), smem, s, a);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

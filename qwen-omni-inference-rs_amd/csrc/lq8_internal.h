@@ -175,6 +175,26 @@ struct MoeDownArgs {
 bool moe_down_combine_supported(int K, int k);
 lq8_status launch_moe_down_combine(hipStream_t s, const MoeDownArgs& a);
 
+// Batch-1 routed expert gate and up projections with the RMSNorm fused:
+// y[q][row] = silu(gate_e(n)[row]) * up_e(n)[row], e = rids[q],
+// n = RmsNorm(x) -- the values launch_gemv_mv gives (XS_RMSNORM, EPI_SWIGLU)
+// for one token.  The weight interleaves gate and up by 8 rows per tile.
+struct MoeGateUpArgs {
+    const int8_t* codes;    // expert e's tiles start at tile e * prob_tiles (gate, up interleaved by 8)
+    const uint16_t* scales;
+    int inter, k;           // expert intermediate size (gate rows), hidden size
+    int prob_tiles;         // 2 * inter / 16
+    const uint32_t* rids;   // device [K]: expert of each rank
+    int K;
+    const float* x;         // the token's hidden state [k]
+    const float* norm_w;    // [k]
+    float eps;
+    float* y;               // rank q's output: y + q * y_stride (y_stride >= inter)
+    int y_stride;
+};
+bool moe_gate_up1_supported(int K, int inter, int k);
+lq8_status launch_moe_gate_up1(hipStream_t s, const MoeGateUpArgs& a);
+
 // Final greedy pick over the per-tile argmax partials: token -> *d_tok and
 // tokens_out[*d_step], then *d_pos and *d_step advance (device scalars).
 lq8_status launch_argmax_final(hipStream_t s, const float* arg_val, const int* arg_idx, int count, uint32_t* d_tok,
@@ -247,14 +267,24 @@ size_t sample_work_zero_bytes(int vocab);
 bool sample_vocab_ok(size_t vocab);  // 1 .. 2^20
 lq8_status launch_sample(hipStream_t s, const SampleLaunch& a);
 
-lq8_status launch_repack_aos(hipStream_t s, const uint8_t* aos, size_t n_rows, size_t row0, const lq8_weight* w);
-lq8_status launch_unpack_aos(hipStream_t s, const lq8_weight* w, size_t row0, size_t n_rows, uint8_t* aos);
+// A tensor's rows in a weight: row r at row0 + r, or, with run > 0, in runs of
+// `run` rows every `stride` rows (row0 + (r / run) * stride + r % run).
+struct RowRun {
+    size_t run = 0, stride = 0;
+};
+__host__ __device__ inline size_t map_row(size_t row0, size_t r, RowRun m) {
+    return m.run ? row0 + (r / m.run) * m.stride + r % m.run : row0 + r;
+}
+lq8_status launch_repack_aos(hipStream_t s, const uint8_t* aos, size_t n_rows, size_t row0, const lq8_weight* w,
+                             RowRun rr = {});
+lq8_status launch_unpack_aos(hipStream_t s, const lq8_weight* w, size_t row0, size_t n_rows, uint8_t* aos,
+                             RowRun rr = {});
 lq8_status launch_quantize_weight_f32(hipStream_t s, const float* src, size_t n_rows, size_t row0,
                                       const lq8_weight* w);
 lq8_status launch_quantize_weight_bf16(hipStream_t s, const uint16_t* src, size_t n_rows, size_t row0,
                                        const lq8_weight* w);
 lq8_status launch_random_weight(hipStream_t s, const lq8_weight* w, size_t row0, size_t n_rows, uint64_t seed,
-                                uint64_t stream, float stddev);
+                                uint64_t stream, float stddev, RowRun rr = {});
 lq8_status launch_dequant_rows(hipStream_t s, const lq8_weight* w, const uint32_t* d_ids, size_t row0,
                                size_t nrows, float* y);
 

@@ -38,7 +38,10 @@ constexpr int MOE_MAX_BATCH = 64;
 
 struct MoeLayer {
     lq8_weight *qkv = nullptr, *o = nullptr;
-    lq8_weight *gu = nullptr;    // [E * 2I, H]: expert e rows e*2I .. (gate I rows, then up I rows)
+    // [E * 2I, H]: expert e's rows from e*2I, gate and up interleaved by 8:
+    // its 16-row tile t holds gate rows 8t .. 8t+7, then up rows 8t .. 8t+7
+    // (so one tile gives silu(gate) * up of 8 rows)
+    lq8_weight *gu = nullptr;
     lq8_weight *down = nullptr;  // [E * H, I]: expert e rows e*H ..
     float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
 };
@@ -386,6 +389,7 @@ size_t per_layer(const lq8_moe_config* c) { return 8 + 3 * (size_t)c->num_expert
 struct TensorRef {
     lq8_weight* w = nullptr;
     size_t row0 = 0, rows = 0;
+    RowRun rr;  // where the tensor's rows sit in w
     float* norm = nullptr;
     size_t norm_len = 0;
 };
@@ -407,8 +411,14 @@ TensorRef tensor_ref(lq8_moe* m, size_t idx) {
         default: break;
     }
     const size_t x = k - 8, e = x % E;
-    if (x < E) { t.w = L.gu; t.row0 = e * 2 * I; t.rows = I; }
-    else if (x < 2 * E) { t.w = L.gu; t.row0 = e * 2 * I + I; t.rows = I; }
+    if (x < 2 * E) {
+        // gate (x < E) or up: runs of 8 rows, every 16 rows
+        t.w = L.gu;
+        t.row0 = e * 2 * I + (x < E ? 0 : 8);
+        t.rows = I;
+        t.rr.run = 8;
+        t.rr.stride = 16;
+    }
     else { t.w = L.down; t.row0 = e * H; t.rows = H; }
     return t;
 }
@@ -485,7 +495,12 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
         g.codes = L.gu->codes; g.scales = L.gu->scales; g.rows = 2 * I; g.k = H; g.prob_tiles = 2 * I / TILE_ROWS;
         g.n_prob = n_act; g.prob_id = act_e; g.vec_begin = vbeg; g.vec_count = vcnt; g.slots = slots;
         g.x_stride = H; g.x_div = K; g.y = m->gu; g.y_stride = I; g.max_vec = T;
-        if (T == 1) {
+        if (T == 1 && moe_gate_up1_supported(K, I, H)) {
+            // one token: the experts by rank straight from the router's list
+            const MoeGateUpArgs gu1{L.gu->codes, L.gu->scales, I, H, 2 * I / TILE_ROWS, rids, K,
+                                    m->h2, L.post_norm, c.rms_norm_eps, m->gu, I};
+            if ((st = launch_moe_gate_up1(s, gu1))) return st;
+        } else if (T == 1) {
             g.x = m->h2;
             g.norm_w = L.post_norm;
             g.eps = c.rms_norm_eps;
@@ -540,7 +555,7 @@ lq8_status upload_table(lq8_moe* m, const void* const* tensors) {
         }
         hipError_t e = hipMemcpy(tmp, tensors[i], bytes, hipMemcpyHostToDevice);
         if (e != hipSuccess) { st = hip_fail(e, "tensor upload"); break; }
-        st = launch_repack_aos(m->ctx->stream, (const uint8_t*)tmp, t.rows, t.row0, t.w);
+        st = launch_repack_aos(m->ctx->stream, (const uint8_t*)tmp, t.rows, t.row0, t.w, t.rr);
         if (!st) {
             e = hipStreamSynchronize(m->ctx->stream);
             if (e != hipSuccess) st = hip_fail(e, "tensor repack");
@@ -608,7 +623,7 @@ lq8_status lq8_moe_create_random(lq8_ctx* ctx, const lq8_moe_config* cfg, uint64
     for (size_t i = 0; i < count && !st; i++) {
         TensorRef t = tensor_ref(m, i);
         if (t.norm) st = fill_norm(t.norm, t.norm_len, nullptr);
-        else st = launch_random_weight(ctx->stream, t.w, t.row0, t.rows, seed, i, stddev);
+        else st = launch_random_weight(ctx->stream, t.w, t.row0, t.rows, seed, i, stddev, t.rr);
     }
     if (!st) {
         hipError_t e = hipStreamSynchronize(ctx->stream);
@@ -633,7 +648,7 @@ lq8_status lq8_moe_export_tensor(lq8_moe* m, size_t idx, void* host_out) {
     const size_t bytes = t.rows * t.w->nb * BLOCK_BYTES;
     void* tmp = nullptr;
     LQ8_HIP(hipMalloc(&tmp, bytes));
-    lq8_status st = launch_unpack_aos(s, t.w, t.row0, t.rows, (uint8_t*)tmp);
+    lq8_status st = launch_unpack_aos(s, t.w, t.row0, t.rows, (uint8_t*)tmp, t.rr);
     hipError_t e = hipSuccess;
     if (!st) e = hipMemcpyAsync(host_out, tmp, bytes, hipMemcpyDeviceToHost, s);
     if (!st && e == hipSuccess) e = hipStreamSynchronize(s);

@@ -77,7 +77,7 @@ __global__ void k_quantize_aos(const float* __restrict__ src, size_t nblocks, ui
 }
 
 __global__ void k_repack_aos(const uint8_t* __restrict__ aos, size_t n_rows, size_t nb, size_t np, size_t row0,
-                             int8_t* __restrict__ codes, uint16_t* __restrict__ scales) {
+                             RowRun rr, int8_t* __restrict__ codes, uint16_t* __restrict__ scales) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= n_rows * nb) return;
     const size_t r = idx / nb, b = idx % nb;
@@ -85,16 +85,16 @@ __global__ void k_repack_aos(const uint8_t* __restrict__ aos, size_t n_rows, siz
     int q[32];
 #pragma unroll
     for (int j = 0; j < 32; j++) q[j] = (int)(int8_t)blk[2 + j];
-    const size_t row = row0 + r;
+    const size_t row = map_row(row0, r, rr);
     store_tiled(codes, np, row, b, q);
     scales[scale_off(row / TILE_ROWS, np, b, (int)(row % TILE_ROWS))] = (uint16_t)(blk[0] | (blk[1] << 8));
 }
 
 __global__ void k_unpack_aos(const int8_t* __restrict__ codes, const uint16_t* __restrict__ scales, size_t row0,
-                             size_t n_rows, size_t nb, size_t np, uint8_t* __restrict__ aos) {
+                             RowRun rr, size_t n_rows, size_t nb, size_t np, uint8_t* __restrict__ aos) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= n_rows * nb) return;
-    const size_t row = row0 + idx / nb, b = idx % nb;
+    const size_t row = map_row(row0, idx / nb, rr), b = idx % nb;
     const size_t tile = row / TILE_ROWS;
     const int r = (int)(row % TILE_ROWS);
     uint8_t* o = aos + idx * BLOCK_BYTES;
@@ -141,12 +141,12 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
 // N(0, std) from a counter-based generator: each element pair (2i, 2i+1) of
 // the tensor's row-major order takes one SplitMix64 hash of (seed, stream, i)
 // through Box-Muller.
-__global__ void k_random_weight(size_t n_rows, size_t row0, size_t nb, size_t np, uint64_t key, float stddev,
-                                int8_t* __restrict__ codes, uint16_t* __restrict__ scales) {
+__global__ void k_random_weight(size_t n_rows, size_t row0, RowRun rr, size_t nb, size_t np, uint64_t key,
+                                float stddev, int8_t* __restrict__ codes, uint16_t* __restrict__ scales) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= n_rows * nb) return;
-    const size_t r = idx / nb, b = idx % nb;
-    const size_t row = row0 + r;
+    const size_t r = idx / nb, b = idx % nb;  // the values depend on (r, b), not on where row r is stored
+    const size_t row = map_row(row0, r, rr);
     float x[32];
     const size_t pair0 = (r * nb * 32 + b * 32) / 2;
 #pragma unroll 4
@@ -1257,20 +1257,22 @@ lq8_status launch_gemm(hipStream_t s, const int8_t* xq, const uint32_t* xs, int 
     return LQ8_OK;
 }
 
-lq8_status launch_repack_aos(hipStream_t s, const uint8_t* aos, size_t n_rows, size_t row0, const lq8_weight* w) {
+lq8_status launch_repack_aos(hipStream_t s, const uint8_t* aos, size_t n_rows, size_t row0, const lq8_weight* w,
+                             RowRun rr) {
     const size_t n = n_rows * w->nb;
     if (!n) return LQ8_OK;
-    hipLaunchKernelGGL(k_repack_aos, dim3(grid1(n, WG)), dim3(WG), 0, s, aos, n_rows, w->nb, w->np, row0, w->codes,
-                       w->scales);
+    hipLaunchKernelGGL(k_repack_aos, dim3(grid1(n, WG)), dim3(WG), 0, s, aos, n_rows, w->nb, w->np, row0, rr,
+                       w->codes, w->scales);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
 
-lq8_status launch_unpack_aos(hipStream_t s, const lq8_weight* w, size_t row0, size_t n_rows, uint8_t* aos) {
+lq8_status launch_unpack_aos(hipStream_t s, const lq8_weight* w, size_t row0, size_t n_rows, uint8_t* aos,
+                             RowRun rr) {
     const size_t n = n_rows * w->nb;
     if (!n) return LQ8_OK;
-    hipLaunchKernelGGL(k_unpack_aos, dim3(grid1(n, WG)), dim3(WG), 0, s, w->codes, w->scales, row0, n_rows, w->nb,
-                       w->np, aos);
+    hipLaunchKernelGGL(k_unpack_aos, dim3(grid1(n, WG)), dim3(WG), 0, s, w->codes, w->scales, row0, rr, n_rows,
+                       w->nb, w->np, aos);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
@@ -1296,12 +1298,12 @@ lq8_status launch_quantize_weight_bf16(hipStream_t s, const uint16_t* src, size_
 }
 
 lq8_status launch_random_weight(hipStream_t s, const lq8_weight* w, size_t row0, size_t n_rows, uint64_t seed,
-                                uint64_t stream, float stddev) {
+                                uint64_t stream, float stddev, RowRun rr) {
     const size_t n = n_rows * w->nb;
     if (!n) return LQ8_OK;
     const uint64_t key = seed * 0x9E3779B97F4A7C15ull ^ (stream + 1) * 0xC2B2AE3D27D4EB4Full;
-    hipLaunchKernelGGL(k_random_weight, dim3(grid1(n, WG)), dim3(WG), 0, s, n_rows, row0, w->nb, w->np, key, stddev,
-                       w->codes, w->scales);
+    hipLaunchKernelGGL(k_random_weight, dim3(grid1(n, WG)), dim3(WG), 0, s, n_rows, row0, rr, w->nb, w->np, key,
+                       stddev, w->codes, w->scales);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

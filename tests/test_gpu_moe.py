@@ -143,6 +143,21 @@ def test_moe_rejects_bad_calls(ctx):
         lq8.Qwen3MoeLayers.random(ctx, bad, seed=1)
 
 
+def test_moe_expert_weights_round_trip(ctx):
+    """The expert gate and up weights are stored interleaved by 8 rows per
+    16-row tile; loading host tensors and exporting them gives the same
+    bytes (intermediate size 96: 12 such tiles per expert, 2 layers)."""
+    cfg = MoeCfg(num_experts=8, top_k=2, expert_intermediate_size=96, max_positions=64, max_batch=2,
+                 num_layers=2)
+    tens = moe_tensors(cfg, 41)
+    gpu = lq8.Qwen3MoeLayers.load(ctx, lq8_cfg(cfg), tens)
+    back = gpu.export_all()
+    assert len(back) == len(tens)
+    for i, (a, b) in enumerate(zip(tens, back)):
+        assert np.array_equal(np.asarray(a).view(np.uint8).ravel(), np.asarray(b).view(np.uint8).ravel()), f"tensor {i}"
+    gpu.free()
+
+
 @pytest.mark.parametrize("T,pos0", [(1, 0), (32, 0), (1, 126), (32, 126)])
 def test_moe_qwen3_30b_a3b_layer(ctx, T, pos0):
     """One full-size Qwen3-30B-A3B-style layer (hidden 2048, 32/4 heads, 128
