@@ -765,6 +765,7 @@ template <int CH, bool FAST>
 __global__ __launch_bounds__(MOE_DOWN_THREADS) void k_moe_down_combine(MoeDownArgs a) {
     extern __shared__ float smem[];
     __shared__ int order[MOE_DOWN_MAX_K];
+    __shared__ float ys[FAST ? MOE_DOWN_MAX_K * 16 : 1];  // FAST: rank q's outputs of the tile's rows
     constexpr int NW = MOE_DOWN_THREADS / 64;
     const int tile = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -854,21 +855,31 @@ __global__ __launch_bounds__(MOE_DOWN_THREADS) void k_moe_down_combine(MoeDownAr
         if (wave < items) run_item(wave, pa[0], sa[0]);
         if (wave + NW < items) run_item(wave + NW, pa[1], sa[1]);
         __syncthreads();
-        // the tree over each rank's groups, then the combine in ascending expert order
+        // the tree over each rank's groups, thread (rank, row) ...
+        if (tid < K * 16) {
+            float v[MOE_DOWN_FAST_GMAX];
+#pragma unroll
+            for (int i = 0; i < MOE_DOWN_FAST_GMAX; i++) v[i] = gs[((tid >> 4) * G + min(i, G - 1)) * 16 + (tid & 15)];
+#pragma unroll
+            for (int s2 = 1; s2 < MOE_DOWN_FAST_GMAX; s2 *= 2)
+#pragma unroll
+                for (int i = 0; i + s2 < MOE_DOWN_FAST_GMAX; i += 2 * s2)
+                    if (i + s2 < G) v[i] = v[i] + v[i + s2];
+            ys[tid] = v[0];
+        }
+        __syncthreads();
+        // ... then the combine in ascending expert order (every LDS read issued at once)
         if (tid < 16) {
+            int rk[MOE_DOWN_MAX_K];
+            float y[MOE_DOWN_MAX_K];
+#pragma unroll
+            for (int qq = 0; qq < MOE_DOWN_MAX_K; qq++) rk[qq] = __builtin_amdgcn_readfirstlane(order[min(qq, K - 1)]);
+#pragma unroll
+            for (int qq = 0; qq < MOE_DOWN_MAX_K; qq++) y[qq] = ys[rk[qq] * 16 + tid];
             float acc = 0.0f;
-            for (int qq = 0; qq < K; qq++) {
-                const int rk = __builtin_amdgcn_readfirstlane(order[qq]);
-                float v[MOE_DOWN_FAST_GMAX];
 #pragma unroll
-                for (int i = 0; i < MOE_DOWN_FAST_GMAX; i++) v[i] = gs[(rk * G + min(i, G - 1)) * 16 + tid];
-#pragma unroll
-                for (int s2 = 1; s2 < MOE_DOWN_FAST_GMAX; s2 *= 2)
-#pragma unroll
-                    for (int i = 0; i + s2 < MOE_DOWN_FAST_GMAX; i += 2 * s2)
-                        if (i + s2 < G) v[i] = v[i] + v[i + s2];
-                acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rwt), rk)) * v[0];
-            }
+            for (int qq = 0; qq < MOE_DOWN_MAX_K; qq++)
+                if (qq < K) acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rwt), rk[qq])) * y[qq];
             const int row = tile * TILE_ROWS + tid;
             if (row < a.rows) a.out[row] = h2 + acc;
         }

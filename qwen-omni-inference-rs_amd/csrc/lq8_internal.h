@@ -352,6 +352,9 @@ struct AttnSegLaunch {
     // owns k/v_cache + b * kv_stride and writes part + b * part_stride
     int batch = 1;
     size_t qkv_stride = 0, kv_stride = 0, part_stride = 0;
+    // query heads per workgroup (0: the num_heads / num_kv_heads of a kv head;
+    // a divisor of it spreads one kv head's heads over several workgroups)
+    int head_group = 0;
 };
 lq8_status launch_attention_seg(hipStream_t s, const AttnSegLaunch& a);
 // Attention outputs from the per-segment partials of launch_attention_seg,

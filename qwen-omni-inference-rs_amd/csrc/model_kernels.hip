@@ -42,17 +42,19 @@ __global__ __launch_bounds__(64) void k_qk_rope_kv(QkRopeLaunch a) {
 }
 
 
-// Decode attention, one workgroup per (kv head, segment of 64 positions).
-// Every workgroup normalizes and rotates its G query heads; the workgroup of
-// the last segment also normalizes and rotates the new key, appends key and
-// value at the position and uses them from LDS.  Output: per (segment, q
-// head) o_c[128], m_c, l_c at part[(c * H + h) * ATT_PART_STRIDE].
+// Decode attention, one workgroup per (kv head, group of HG of its G query
+// heads, segment of 64 positions).  Every workgroup normalizes and rotates
+// its HG query heads; the workgroups of the last segment also normalize and
+// rotate the new key and use key and value from LDS, and the one of head
+// group 0 appends them to the cache at the position.  Output: per (segment,
+// q head) o_c[128], m_c, l_c at part[(c * H + h) * ATT_PART_STRIDE].
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     extern __shared__ float sm[];
-    const int kvh = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int G = a.num_heads / a.num_kv_heads, HG = a.head_group, NG = G / HG;
+    const int kvh = blockIdx.x / NG, hg = blockIdx.x - kvh * NG, c = blockIdx.y, b = blockIdx.z;
+    const int h0 = kvh * G + hg * HG;  // this workgroup's first query head
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int G = a.num_heads / a.num_kv_heads;
     const int QD = a.num_heads * 128, KD = a.num_kv_heads * 128;
     a.qkv += b * a.qkv_stride;
     a.k_cache += b * a.kv_stride;
@@ -69,14 +71,14 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     float4 kreg[ATT_F4], vreg[ATT_F4];
     const bool early = c < ATT_EARLY_SEGS && gridDim.z == 1;
     if (early) seg_load_capacity(Kc, Vc, js, a.max_pos, kreg, vreg);
-    float h0 = 0.0f, h1 = 0.0f, n0 = 0.0f, n1 = 0.0f;
-    if (wave < G + 2) {
-        const float* src = wave < G ? a.qkv + (kvh * G + wave) * 128
-                                    : a.qkv + QD + (wave == G ? 0 : KD) + kvh * 128;
-        h0 = src[lane];
-        h1 = src[lane + 64];
-        if (wave <= G) {
-            const float* w = wave < G ? a.q_norm : a.k_norm;
+    float x0 = 0.0f, x1 = 0.0f, n0 = 0.0f, n1 = 0.0f;
+    if (wave < HG + 2) {
+        const float* src = wave < HG ? a.qkv + (h0 + wave) * 128
+                                     : a.qkv + QD + (wave == HG ? 0 : KD) + kvh * 128;
+        x0 = src[lane];
+        x1 = src[lane + 64];
+        if (wave <= HG) {
+            const float* w = wave < HG ? a.q_norm : a.k_norm;
             n0 = w[lane];
             n1 = w[lane + 64];
         }
@@ -90,44 +92,48 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     const int nj = min(SEG, L - js);
     const bool last = c == C - 1;
     const int newrow = last ? pos - js : -1;
-    float* qs = sm;                      // [G][128]
-    float* kn = qs + G * 128;            // [128]
+    float* qs = sm;                      // [HG][128]
+    float* kn = qs + HG * 128;           // [128]
     float* vn = kn + 128;                // [128]
-    float* sc = vn + 128;                // [G][64]
-    float* mlc = sc + G * SEG;           // [G][2]
-    float* ks = sm + seg_ks_off(G);      // [64][KPAD], later vs [64][128]
+    float* sc = vn + 128;                // [HG][64]
+    float* mlc = sc + HG * SEG;          // [HG][2]
+    float* ks = sm + seg_ks_off(HG);     // [64][KPAD], later vs [64][128]
     if (!early) seg_load(Kc, Vc, js, nj, kreg, vreg);
     const float* cs = a.cos_t + (size_t)pos * 64;
     const float* sn = a.sin_t + (size_t)pos * 64;
-    for (int t = wave; t < G + 2; t += ATT_THREADS / 64) {
-        if (t < G) {
-            if (t == wave) head_norm_rope_vals(h0, h1, n0, n1, cs, sn, a.eps, qs + t * 128);
-            else head_norm_rope(a.qkv + (kvh * G + t) * 128, a.q_norm, cs, sn, a.eps, qs + t * 128);
-        } else if (t == G && last) {
-            if (t == wave) head_norm_rope_vals(h0, h1, n0, n1, cs, sn, a.eps, kn);
+    for (int t = wave; t < HG + 2; t += ATT_THREADS / 64) {
+        if (t < HG) {
+            if (t == wave) head_norm_rope_vals(x0, x1, n0, n1, cs, sn, a.eps, qs + t * 128);
+            else head_norm_rope(a.qkv + (h0 + t) * 128, a.q_norm, cs, sn, a.eps, qs + t * 128);
+        } else if (t == HG && last) {
+            if (t == wave) head_norm_rope_vals(x0, x1, n0, n1, cs, sn, a.eps, kn);
             else head_norm_rope(a.qkv + QD + kvh * 128, a.k_norm, cs, sn, a.eps, kn);
-            float* kr = a.k_cache + ((size_t)kvh * a.max_pos + pos) * 128;
-            kr[lane] = kn[lane];
-            kr[lane + 64] = kn[lane + 64];
-        } else if (t == G + 1 && last) {
+            if (hg == 0) {
+                float* kr = a.k_cache + ((size_t)kvh * a.max_pos + pos) * 128;
+                kr[lane] = kn[lane];
+                kr[lane + 64] = kn[lane + 64];
+            }
+        } else if (t == HG + 1 && last) {
             const float* v = a.qkv + QD + KD + kvh * 128;
-            float* vr = a.v_cache + ((size_t)kvh * a.max_pos + pos) * 128;
-            const float v0 = t == wave ? h0 : v[lane], v1 = t == wave ? h1 : v[lane + 64];
+            const float v0 = t == wave ? x0 : v[lane], v1 = t == wave ? x1 : v[lane + 64];
             vn[lane] = v0;
             vn[lane + 64] = v1;
-            vr[lane] = v0;
-            vr[lane + 64] = v1;
+            if (hg == 0) {
+                float* vr = a.v_cache + ((size_t)kvh * a.max_pos + pos) * 128;
+                vr[lane] = v0;
+                vr[lane + 64] = v1;
+            }
         }
     }
     __syncthreads();
-    seg_scores(kreg, nj, newrow, kn, qs, G, a.scale, ks, sc, mlc);
+    seg_scores(kreg, nj, newrow, kn, qs, HG, a.scale, ks, sc, mlc);
     __syncthreads();
     seg_stage_v(vreg, nj, newrow, vn, ks);
     __syncthreads();
-    for (int t = tid; t < G * 128; t += ATT_THREADS) {
+    for (int t = tid; t < HG * 128; t += ATT_THREADS) {
         const int h = t >> 7, d = t & 127;
         const float o = pv_chain(sc + h * SEG, ks, d, nj);
-        float* p = a.part + ((size_t)c * a.num_heads + kvh * G + h) * ATT_PART_STRIDE;
+        float* p = a.part + ((size_t)c * a.num_heads + h0 + h) * ATT_PART_STRIDE;
         p[d] = o;
         if (d == 0) {
             p[128] = mlc[2 * h];
@@ -377,8 +383,11 @@ lq8_status launch_attention_seg(hipStream_t s, const AttnSegLaunch& a) {
     const int G = a.num_heads / a.num_kv_heads;
     const int cmax = (a.max_pos + SEG - 1) / SEG;
     if (a.batch <= 0) return fail(LQ8_ERR_INVALID_ARG, "attention: batch must be positive");
-    hipLaunchKernelGGL(k_attn_seg, dim3((unsigned)a.num_kv_heads, (unsigned)cmax, (unsigned)a.batch), dim3(ATT_THREADS),
-                       seg_smem(G), s, a);
+    AttnSegLaunch b = a;
+    if (b.head_group <= 0 || G % b.head_group) b.head_group = G;
+    const int NG = G / b.head_group;
+    hipLaunchKernelGGL(k_attn_seg, dim3((unsigned)(a.num_kv_heads * NG), (unsigned)cmax, (unsigned)a.batch),
+                       dim3(ATT_THREADS), seg_smem(b.head_group), s, b);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }

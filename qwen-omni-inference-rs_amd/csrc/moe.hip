@@ -472,6 +472,7 @@ lq8_status enqueue_forward(lq8_moe* m, float* d_hidden, const float* d_scores, c
         at.qkv_stride = m->QKV;
         at.kv_stride = seq_kv;
         at.part_stride = part_stride;
+        at.head_group = T == 1 ? 2 : 0;  // one sequence: a kv head's query heads over G / 2 workgroups
         if ((st = launch_attention_seg(s, at))) return st;
         // o_proj on the attention output, + residual -> h2
         if (T == 1) {
