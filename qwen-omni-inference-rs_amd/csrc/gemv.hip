@@ -36,7 +36,7 @@ constexpr int MAX_CH = 4;
 constexpr int MAX_WAVES = 16;
 constexpr int SP = 4;  // input float4s per thread held in registers (the rest load-and-use)
 constexpr int CU = 4;  // attention segments held in registers (256 positions)
-constexpr int EA = 2;  // attention outputs per thread held in registers
+constexpr int EA = 4;  // attention outputs per thread held in registers (k = 4096 on 1024 threads)
 
 // Input staging, split into the loads (issued before the weights) and the
 // transform into LDS xs[0, k) (ends with a barrier).
@@ -160,6 +160,58 @@ struct Stage {
             const int C = min(max(a.d_pos ? *a.d_pos : a.pos_base, 0) / ATT_SEG + 1, a.attn_cmax);
             float* coef = red + 4;                     // [C][H][2]
             float* dens = coef + a.attn_cmax * H * 2;  // [H]
+            if (C <= CU && H <= nt && k <= EA * nt) {
+                // every partial this thread uses is in its registers: the same
+                // steps with no global load, so that no wait joins them to the
+                // weights issued after the staging's loads
+                if (tid < H) {
+                    const int h = tid;
+                    float m = -__builtin_huge_valf(), den = 0.0f;
+                    float mp[CU], mn[CU], ea[CU], eb[CU];
+#pragma unroll
+                    for (int c = 0; c < CU; c++) {
+                        mp[c] = m;
+                        if (c < C) m = m > mcs[c] ? m : mcs[c];
+                        mn[c] = m;
+                    }
+#pragma unroll
+                    for (int c = 0; c < CU; c++) {
+                        ea[c] = expf_cr(mp[c] - mn[c]);
+                        eb[c] = expf_cr(mcs[c] - mn[c]);
+                    }
+#pragma unroll
+                    for (int c = 0; c < CU; c++) {
+                        if (c < C) {
+                            coef[(c * H + h) * 2] = ea[c];
+                            coef[(c * H + h) * 2 + 1] = eb[c];
+                            den = den * ea[c] + eb[c] * lcs[c];
+                        }
+                    }
+                    dens[h] = den;
+                }
+                __syncthreads();
+#pragma unroll
+                for (int e = 0; e < EA; e++) {
+                    const int i = tid + e * nt;
+                    if (i < k) {
+                        const int h = i >> 7;
+                        float ca[CU], cb[CU];
+#pragma unroll
+                        for (int c = 0; c < CU; c++) {
+                            const int cc = min(c, C - 1);
+                            ca[c] = coef[(cc * H + h) * 2];
+                            cb[c] = coef[(cc * H + h) * 2 + 1];
+                        }
+                        float num = 0.0f;
+#pragma unroll
+                        for (int c = 0; c < CU; c++)
+                            if (c < C) num = num * ca[c] + cb[c] * ov[e][c];
+                        xs[i] = __fdiv_rn(num, dens[h]);
+                    }
+                }
+                __syncthreads();
+                return;
+            }
             for (int h = tid; h < H; h += nt) {
                 float m = -__builtin_huge_valf(), den = 0.0f;
                 for (int c0 = 0; c0 < C; c0 += CU) {
