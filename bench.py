@@ -416,7 +416,12 @@ def main():
                     help="only the grid-wide synchronisation microbenchmark, one line per kind and grid size")
     ap.add_argument("--floors", action="store_true",
                     help="only the hardware floors (streaming read rates, launch period, HBM load latency), one line")
+    ap.add_argument("--moe-only", action="store_true",
+                    help="only the 48-layer MoE stack at batch 1 and 32, one line (for kernel traces)")
     args = ap.parse_args()
+    if args.moe_only:
+        print(json.dumps(moe_stack(lq8.Context(0))), flush=True)
+        return
     if args.floors:
         print(json.dumps(floors(lq8.Context(0), full=True)), flush=True)
         return

@@ -36,7 +36,7 @@ constexpr int MAX_CH = 4;
 constexpr int MAX_WAVES = 16;
 constexpr int SP = 4;  // input float4s per thread held in registers (the rest load-and-use)
 constexpr int CU = 4;  // attention segments held in registers (256 positions)
-constexpr int EA = 4;  // attention outputs per thread held in registers (k = 4096 on 1024 threads)
+constexpr int EA = 2;  // attention outputs per thread held in registers
 
 // Input staging, split into the loads (issued before the weights) and the
 // transform into LDS xs[0, k) (ends with a barrier).
@@ -45,6 +45,7 @@ struct Stage {
     float4 xv[SP] = {}, wv[SP] = {};
     float mcs[CU] = {}, lcs[CU] = {};
     float ov[EA][CU] = {};
+    float4 ov4[CU] = {};  // k <= 4 * threads: outputs 4 t .. 4 t + 3 (one head) of the first CU segments
 
     // Only waves whose 64 threads reach into the input issue its loads (a
     // wave-uniform condition, so no lane-divergent branch around a load).
@@ -76,13 +77,25 @@ struct Stage {
                     lcs[c] = p[129];
                 }
             }
-#pragma unroll
-            for (int e = 0; e < EA; e++) {
-                if (wave * 64 + e * nt < a.k) {
-                    const int i = min(tid + e * nt, a.k - 1);
+            if (a.k <= 4 * nt) {
+                // one float4 per segment and thread (a 16-byte load: each vector
+                // memory instruction costs the texture path the same whatever
+                // its width)
+                if (wave * 64 < k4) {
+                    const int i = 4 * min(tid, k4 - 1);
 #pragma unroll
                     for (int c = 0; c < CU; c++)
-                        ov[e][c] = x[((size_t)min(c, cl) * H + (i >> 7)) * ATT_PART_STRIDE + (i & 127)];
+                        ov4[c] = *(const float4*)(x + ((size_t)min(c, cl) * H + (i >> 7)) * ATT_PART_STRIDE + (i & 127));
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < EA; e++) {
+                    if (wave * 64 + e * nt < a.k) {
+                        const int i = min(tid + e * nt, a.k - 1);
+#pragma unroll
+                        for (int c = 0; c < CU; c++)
+                            ov[e][c] = x[((size_t)min(c, cl) * H + (i >> 7)) * ATT_PART_STRIDE + (i & 127)];
+                    }
                 }
             }
         }
@@ -160,7 +173,7 @@ struct Stage {
             const int C = min(max(a.d_pos ? *a.d_pos : a.pos_base, 0) / ATT_SEG + 1, a.attn_cmax);
             float* coef = red + 4;                     // [C][H][2]
             float* dens = coef + a.attn_cmax * H * 2;  // [H]
-            if (C <= CU && H <= nt && k <= EA * nt) {
+            if (C <= CU && H <= nt && k <= 4 * nt) {
                 // every partial this thread uses is in its registers: the same
                 // steps with no global load, so that no wait joins them to the
                 // weights issued after the staging's loads
@@ -190,24 +203,27 @@ struct Stage {
                     dens[h] = den;
                 }
                 __syncthreads();
+                if (tid < k4) {
+                    const int i = 4 * tid, h = i >> 7;
+                    float ca[CU], cb[CU];
 #pragma unroll
-                for (int e = 0; e < EA; e++) {
-                    const int i = tid + e * nt;
-                    if (i < k) {
-                        const int h = i >> 7;
-                        float ca[CU], cb[CU];
-#pragma unroll
-                        for (int c = 0; c < CU; c++) {
-                            const int cc = min(c, C - 1);
-                            ca[c] = coef[(cc * H + h) * 2];
-                            cb[c] = coef[(cc * H + h) * 2 + 1];
-                        }
-                        float num = 0.0f;
-#pragma unroll
-                        for (int c = 0; c < CU; c++)
-                            if (c < C) num = num * ca[c] + cb[c] * ov[e][c];
-                        xs[i] = __fdiv_rn(num, dens[h]);
+                    for (int c = 0; c < CU; c++) {
+                        const int cc = min(c, C - 1);
+                        ca[c] = coef[(cc * H + h) * 2];
+                        cb[c] = coef[(cc * H + h) * 2 + 1];
                     }
+                    float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < CU; c++)
+                        if (c < C) {
+                            n0 = n0 * ca[c] + cb[c] * ov4[c].x;
+                            n1 = n1 * ca[c] + cb[c] * ov4[c].y;
+                            n2 = n2 * ca[c] + cb[c] * ov4[c].z;
+                            n3 = n3 * ca[c] + cb[c] * ov4[c].w;
+                        }
+                    const float den = dens[h];
+                    *(float4*)(xs + i) = make_float4(__fdiv_rn(n0, den), __fdiv_rn(n1, den), __fdiv_rn(n2, den),
+                                                     __fdiv_rn(n3, den));
                 }
                 __syncthreads();
                 return;
@@ -265,7 +281,8 @@ struct Stage {
 #pragma unroll
                             for (int c = 0; c < CU; c++) {
                                 const int cc = min(c0 + c, C - 1);
-                                o[c] = (c0 == 0 && e0 == 0) ? ov[e][c] : x[((size_t)cc * H + h) * ATT_PART_STRIDE + d];
+                                o[c] = (c0 == 0 && e0 == 0 && k > 4 * nt) ? ov[e][c]
+                                                                          : x[((size_t)cc * H + h) * ATT_PART_STRIDE + d];
                                 ca[c] = coef[(cc * H + h) * 2];  // coefficients read before the chain
                                 cb[c] = coef[(cc * H + h) * 2 + 1];
                             }
