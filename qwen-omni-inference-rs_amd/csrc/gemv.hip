@@ -68,8 +68,11 @@ struct Stage {
             // position (entries past it are loaded and never used)
             const int H = a.attn_heads;
             const int cl = a.attn_cmax - 1;
-            const int h = min(tid, H - 1);
-            if (wave * 64 < H) {
+            // thread t < CU * H (or < H): (m_c, l_c) of every segment c < CU of
+            // head t % H (threads t < H: head t)
+            const int nml = CU * H <= nt ? CU * H : H;
+            const int h = min(tid, nml - 1) % H;
+            if (wave * 64 < nml) {
 #pragma unroll
                 for (int c = 0; c < CU; c++) {
                     const float* p = x + ((size_t)min(c, cl) * H + h) * ATT_PART_STRIDE;
@@ -173,61 +176,59 @@ struct Stage {
             const int C = min(max(a.d_pos ? *a.d_pos : a.pos_base, 0) / ATT_SEG + 1, a.attn_cmax);
             float* coef = red + 4;                     // [C][H][2]
             float* dens = coef + a.attn_cmax * H * 2;  // [H]
-            if (C <= CU && H <= nt && k <= 4 * nt) {
+            if (C <= CU && CU * H <= nt && k <= 4 * nt) {
                 // every partial this thread uses is in its registers: the same
                 // steps with no global load, so that no wait joins them to the
-                // weights issued after the staging's loads
-                if (tid < H) {
-                    const int h = tid;
-                    float m = -__builtin_huge_valf(), den = 0.0f;
-                    float mp[CU], mn[CU], ea[CU], eb[CU];
+                // weights issued after the staging's loads.  Thread (segment
+                // c, head h) = c * H + h runs its head's running maximum up to
+                // c and the two exps of segment c; the combine threads run the
+                // denominator chain as they read the coefficients.
+                float* lsh = dens + H;  // [CU][H] l_c
+                if (tid < CU * H) {
+                    const int c = tid / H, h = tid - c * H;
+                    float m = -__builtin_huge_valf(), mpc = m, mnc = m, mcc = 0.0f, lcc = 0.0f;
 #pragma unroll
-                    for (int c = 0; c < CU; c++) {
-                        mp[c] = m;
-                        if (c < C) m = m > mcs[c] ? m : mcs[c];
-                        mn[c] = m;
+                    for (int cc = 0; cc < CU; cc++) {
+                        const float mp = m, mv = mcs[cc], lv = lcs[cc];
+                        if (cc < C) m = m > mv ? m : mv;
+                        const bool me = cc == c;
+                        mpc = me ? mp : mpc;
+                        mnc = me ? m : mnc;
+                        mcc = me ? mv : mcc;
+                        lcc = me ? lv : lcc;
                     }
-#pragma unroll
-                    for (int c = 0; c < CU; c++) {
-                        ea[c] = expf_cr(mp[c] - mn[c]);
-                        eb[c] = expf_cr(mcs[c] - mn[c]);
+                    if (c < C) {
+                        coef[(c * H + h) * 2] = expf_cr(mpc - mnc);
+                        coef[(c * H + h) * 2 + 1] = expf_cr(mcc - mnc);
+                        lsh[c * H + h] = lcc;
                     }
-#pragma unroll
-                    for (int c = 0; c < CU; c++) {
-                        if (c < C) {
-                            coef[(c * H + h) * 2] = ea[c];
-                            coef[(c * H + h) * 2 + 1] = eb[c];
-                            den = den * ea[c] + eb[c] * lcs[c];
-                        }
-                    }
-                    dens[h] = den;
                 }
                 __syncthreads();
                 if (tid < k4) {
                     const int i = 4 * tid, h = i >> 7;
-                    float ca[CU], cb[CU];
+                    float ca[CU], cb[CU], lc[CU];
 #pragma unroll
                     for (int c = 0; c < CU; c++) {
                         const int cc = min(c, C - 1);
                         ca[c] = coef[(cc * H + h) * 2];
                         cb[c] = coef[(cc * H + h) * 2 + 1];
+                        lc[c] = lsh[cc * H + h];
                     }
-                    float n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
+                    float den = 0.0f, n0 = 0.0f, n1 = 0.0f, n2 = 0.0f, n3 = 0.0f;
 #pragma unroll
                     for (int c = 0; c < CU; c++)
                         if (c < C) {
+                            den = den * ca[c] + cb[c] * lc[c];
                             n0 = n0 * ca[c] + cb[c] * ov4[c].x;
                             n1 = n1 * ca[c] + cb[c] * ov4[c].y;
                             n2 = n2 * ca[c] + cb[c] * ov4[c].z;
                             n3 = n3 * ca[c] + cb[c] * ov4[c].w;
                         }
-                    const float den = dens[h];
                     *(float4*)(xs + i) = make_float4(__fdiv_rn(n0, den), __fdiv_rn(n1, den), __fdiv_rn(n2, den),
                                                      __fdiv_rn(n3, den));
                 }
                 __syncthreads();
-                return;
-            }
+            } else {
             for (int h = tid; h < H; h += nt) {
                 float m = -__builtin_huge_valf(), den = 0.0f;
                 for (int c0 = 0; c0 < C; c0 += CU) {
@@ -295,6 +296,7 @@ struct Stage {
                 }
             }
             __syncthreads();
+            }
         }
     }
 };
@@ -1209,7 +1211,7 @@ lq8_status launch_one(hipStream_t s, const GemvArgs& a) {
     const int G = (np + ch - 1) / ch;
     waves = max(tpw, min(wmax, tpw * G));
     size_t smem = ((size_t)np * 64 + (size_t)tpw * G * 16 + 4) * sizeof(float);
-    if (XS == XS_ATTN) smem += ((size_t)a.attn_cmax * a.attn_heads * 2 + a.attn_heads) * sizeof(float);
+    if (XS == XS_ATTN) smem += ((size_t)a.attn_cmax * a.attn_heads * 2 + (1 + CU) * a.attn_heads) * sizeof(float);
     if (smem > 64 * 1024) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: input staging exceeds 64 KiB of LDS");
     const dim3 grid((unsigned)((tiles + tpw - 1) / tpw)), block(64 * waves);
     if (ch == 1) hipLaunchKernelGGL((k_gemv<XS, EPI, 1>), grid, block, smem, s, a, tpw);
