@@ -71,6 +71,7 @@ struct lq8_ctx {
     // grown on demand (never per call)
     void* io_dev = nullptr;
     void* io_host = nullptr;
+    void* io_host_dev = nullptr;  // io_host as the device addresses it (mapped pinned memory)
     size_t io_bytes = 0;
 };
 

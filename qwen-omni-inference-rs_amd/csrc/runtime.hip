@@ -595,6 +595,22 @@ lq8_status lq8_linear_forward_device_noalloc(lq8_ctx* ctx, const lq8_weight* w, 
     return launch_gemm(ctx->stream, xq, xs, (int)m, w, d_y, nullptr);
 }
 
+namespace {
+// n16 16-byte words from src to dst, one workgroup (the GEMV's input, 4-48
+// KiB, out of the mapped pinned staging: one PCIe round trip per load batch).
+__global__ __launch_bounds__(1024) void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16) {
+    constexpr int U = 4;
+    for (size_t i0 = threadIdx.x; i0 < n16; i0 += 1024 * U) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = i0 + u * 1024 < n16 ? src[i0 + u * 1024] : uint4{0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (i0 + u * 1024 < n16) dst[i0 + u * 1024] = v[u];
+    }
+}
+}  // namespace
+
 // Device and pinned host staging for the host-pointer entry points: grows
 // (after a synchronize) only when a call needs more than any call before.
 static lq8_status ctx_io(lq8_ctx* ctx, size_t bytes) {
@@ -602,11 +618,12 @@ static lq8_status ctx_io(lq8_ctx* ctx, size_t bytes) {
     LQ8_HIP(hipStreamSynchronize(ctx->stream));
     if (ctx->io_dev) LQ8_HIP(hipFree(ctx->io_dev));
     if (ctx->io_host) LQ8_HIP(hipHostFree(ctx->io_host));
-    ctx->io_dev = ctx->io_host = nullptr;
+    ctx->io_dev = ctx->io_host = ctx->io_host_dev = nullptr;
     ctx->io_bytes = 0;
     const size_t want = std::max(bytes, (size_t)1 << 20);
     LQ8_HIP(hipMalloc(&ctx->io_dev, want));
     LQ8_HIP(hipHostMalloc(&ctx->io_host, want, hipHostMallocDefault));
+    LQ8_HIP(hipHostGetDevicePointer(&ctx->io_host_dev, ctx->io_host, 0));
     ctx->io_bytes = want;
     return LQ8_OK;
 }
@@ -626,13 +643,23 @@ lq8_status lq8_linear_forward(lq8_ctx* ctx, const lq8_weight* w, const float* x,
     char* dio = (char*)ctx->io_dev;
     char* hio = (char*)ctx->io_host;
     std::memcpy(hio, x, xb);
-    LQ8_HIP(hipMemcpyAsync(dio, hio, xb, hipMemcpyHostToDevice, ctx->stream));
-    st = lq8_linear_forward_device(ctx, w, (const float*)dio, m, (float*)(dio + yoff));
+    if (m == 1) {
+        // one vector: a one-workgroup kernel copies x out of the mapped pinned
+        // buffer and the GEMV stores y into it (no copy engine between the
+        // compute queue's steps)
+        char* hdev = (char*)ctx->io_host_dev;
+        hipLaunchKernelGGL(k_copy16, dim3(1), dim3(1024), 0, ctx->stream, (const uint4*)hdev, (uint4*)dio, xb / 16);
+        LQ8_HIP(hipGetLastError());
+        st = lq8_gemv_q8_0_device(ctx, w, (const float*)dio, (float*)(hdev + yoff));
+    } else {
+        LQ8_HIP(hipMemcpyAsync(dio, hio, xb, hipMemcpyHostToDevice, ctx->stream));
+        st = lq8_linear_forward_device(ctx, w, (const float*)dio, m, (float*)(dio + yoff));
+        if (!st) LQ8_HIP(hipMemcpyAsync(hio + yoff, dio + yoff, yb, hipMemcpyDeviceToHost, ctx->stream));
+    }
     if (st) {
         (void)hipStreamSynchronize(ctx->stream);
         return st;
     }
-    LQ8_HIP(hipMemcpyAsync(hio + yoff, dio + yoff, yb, hipMemcpyDeviceToHost, ctx->stream));
     LQ8_HIP(hipStreamSynchronize(ctx->stream));
     std::memcpy(y, hio + yoff, yb);
     return LQ8_OK;
