@@ -76,6 +76,26 @@ def test_moe_partial_groups_odd_blocks(ctx, hidden):
     run_steps(ctx, cfg, tens, 8, [3] * 8, 1, 43)
 
 
+@pytest.mark.parametrize("hidden,inter,nh,nkv,ne,k", [
+    (288, 160, 6, 2, 8, 2),    # gate|up: 40 tiles, the last workgroup takes one; odd block counts; 3 q heads per kv head
+    (256, 1536, 4, 2, 16, 8),  # down: 8 ranks x 6 groups = 48 items, the prefetching path
+    (320, 64, 4, 4, 4, 1),     # one routed expert, 8 tiles (3, 3, 2); one q head per kv head
+    (288, 672, 4, 2, 6, 4),    # down with every item in flight, 21 blocks (11 pairs in groups of 4, a padding block)
+])
+def test_moe_batch1_shapes(ctx, hidden, inter, nh, nkv, ne, k):
+    """Batch 1 through shapes at the edges of its kernels: the gate|up tile
+    list (3 tiles per workgroup) ending part-way, block counts with a padding
+    block, the down kernel within and past its every-item-in-flight limits
+    (groups of 4 pairs, at most 32 items), and the
+    attention's head groups falling back to whole kv-head groups (an odd or a
+    single query head per kv head); bit-exact with the oracle across a
+    segment edge."""
+    cfg = MoeCfg(hidden_size=hidden, expert_intermediate_size=inter, num_heads=nh, num_kv_heads=nkv,
+                 num_experts=ne, top_k=k, max_positions=96, max_batch=2, num_layers=2)
+    tens = moe_tensors(cfg, 61 + inter)
+    run_steps(ctx, cfg, tens, 1, [61], 4, 62 + hidden)
+
+
 def test_moe_batch_invariance(ctx):
     """A token's bits do not depend on the other tokens of its batch: each
     sequence of a batch of 6 equals its result in a batch of 2 with another
