@@ -265,6 +265,35 @@ def linear_forward_host(ctx, calls=200):
     return out
 
 
+def decode_larger(ctx, cfg, label):
+    """Greedy decode of a larger Qwen3 shape (random Q8_0 weights, 128-token
+    prompt, 128 new tokens) on the default path and on the replayed graph:
+    tok/s, medians of 3; the tokens of the two paths must agree."""
+    model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=2026)
+    prompt = np.random.default_rng(2026).integers(0, cfg.vocab_size, 128).astype(np.uint32)
+    model.generate_greedy(prompt, 8)
+    runs = [model.generate_greedy(prompt, 128) for _ in range(3)]
+    os.environ["LQ8_PERSIST"] = "0"
+    try:
+        model.generate_greedy(prompt, 8)
+        gruns = [model.generate_greedy(prompt, 128) for _ in range(3)]
+    finally:
+        del os.environ["LQ8_PERSIST"]
+    model.free()
+    tps = sorted(st["decode_tokens_per_s"] for _, st in runs)[1]
+    gtps = sorted(st["decode_tokens_per_s"] for _, st in gruns)[1]
+    st0 = runs[0][1]
+    out = {"tokens_per_s": round(tps, 1),
+           "path": "persistent" if st0["used_persistent"] else ("graph" if st0["used_graph"] else "plain"),
+           "graph_tokens_per_s": round(gtps, 1),
+           "tokens_agree": all(np.array_equal(t, runs[0][0]) for t, _ in runs + gruns),
+           "config": {"hidden": cfg.hidden_size, "intermediate": cfg.intermediate_size,
+                      "layers": cfg.num_hidden_layers, "heads": cfg.num_attention_heads,
+                      "kv_heads": cfg.num_key_value_heads, "vocab": cfg.vocab_size}}
+    log(f"decode {label}: {tps:.1f} tok/s ({out['path']}), graph {gtps:.1f} tok/s, tokens agree: {out['tokens_agree']}")
+    return out
+
+
 def moe_stack(ctx, layers=48, reps=10):
     """Qwen3-30B-A3B-style MoE decoder stack (48 layers, ~31.8 GB of Q8_0
     weights resident), one decode step for T = 1 and T = 32 sequences at
@@ -582,6 +611,7 @@ def main():
         if not args.no_cpu:
             cpu_model = (cfg, model.export_all(), prompt)
         model.free()
+        decode["qwen3_1_7b"] = decode_larger(ctx, lq8.qwen3_1_7b(max_positions=512), "Qwen3-1.7B")
 
     moe = None if args.no_moe else moe_stack(ctx)
     ctx.close()

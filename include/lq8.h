@@ -311,8 +311,10 @@ typedef struct {
 /* Greedy generation; the token loop stays on the device.  out_tokens: max_new.
  * The decode steps run as one persistent cooperative kernel (all steps, all
  * layers, the lm_head and the pick in one launch) when the model's shape
- * fits it: head_dim 128, hidden_size a multiple of 32 up to 1024,
- * intermediate_size a multiple of 32 up to 4096, num_heads * 128 <= 2048,
+ * fits it: head_dim 128, hidden_size a multiple of 32 up to 2048 (one
+ * kernel instance up to 1024, another above), intermediate_size a multiple
+ * of 32 whose down-projection split fits (up to 8192 at hidden 2048 on 256
+ * workgroups, Qwen3-1.7B's 6144 included), num_heads * 128 <= 2048,
  * num_heads / num_kv_heads <= 16, and a device with cooperative launch;
  * max_positions is not limited.  lq8_persist_plan tells in advance; the
  * environment variable LQ8_PERSIST=0 turns it off.  Other shapes run one

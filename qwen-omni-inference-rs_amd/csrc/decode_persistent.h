@@ -23,6 +23,7 @@ struct PersistShape {
 
 // Work split and LDS map of one shape on P workgroups (persist_layout).
 struct PersistLayout {
+    int hc;             // block pairs per wave group of a hidden-long tile (2: hidden <= 1024, 4: <= 2048)
     int csO, nchO;      // o projection: input chunks of csO blocks (a power of two), nchO of them
     int csD, nchD;      // down projection: input chunks of csD block pairs (a power of two), nchD of them
     int cdir;           // steps with at most cdir segments: P3 combines the partials itself
@@ -70,12 +71,15 @@ struct PersistArgs {
 // false when the shape does not fit the kernel's limits on P workgroups
 bool persist_layout(const PersistShape& s, int P, PersistLayout* out);
 bool persist_supported(const PersistShape& s, int num_cus);
+// the kernel instance's block pairs per wave group of a hidden-long tile
+int persist_pairs_per_wave(int hidden);
 // d_args: the argument block in device memory (read by the kernel throughout)
 // ch5: block pairs per wave group of the down items (csD / waves per workgroup)
+// hc: persist_pairs_per_wave(hidden)
 // long_ctx: the instance with the combining attention items, for steps whose
 // positions have more than cdir segments (the other instance requires
 // pos0 + steps <= cdir * ATT_SEG)
 lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg, int ch5,
-                                    bool long_ctx);
+                                    int hc, bool long_ctx);
 
 }  // namespace lq8

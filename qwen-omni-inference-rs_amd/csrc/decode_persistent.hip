@@ -95,9 +95,15 @@ constexpr int PT = PERSIST_THREADS;
 constexpr int PW = PT / 64;     // waves per workgroup
 // hand-off words per thread of each fetch (units t + u * PT)
 constexpr int NW_ARG = (2 * 1024 + PT - 1) / PT;                   // the picks: 2 words per workgroup (<= 1024)
-constexpr int NW_H = (1024 + PT - 1) / PT;                         // a hidden vector (hidden <= 1024)
 constexpr int NW_QKV = ((ATT_MAX_GROUP + 2) * 128 + PT - 1) / PT;  // q of a kv head's group, k, v
 constexpr int NW_RES = PERSIST_FETCH;                             // h and the o chunk sums
+// the instance for hidden above 1024 (HC = 4) gathers a hidden vector and
+// its chunk sums in NW_RES4 words per thread and joins at most NCH4 chunk
+// sums per element (fewer registers held across its phases)
+constexpr int NW_RES4 = 12;
+constexpr int NCH4 = 2;
+template <int HC> constexpr int nw_res() { return HC == 4 ? NW_RES4 : NW_RES; }
+template <int HC> constexpr int nch_max() { return HC == 4 ? NCH4 : PERSIST_NCH; }
 constexpr int NW_ACT = (4096 + 16 + PT - 1) / PT;                  // silu(gate) * up (<= 4096) and 16 rows of h2
 constexpr int NW_ATT = (2048 + PT - 1) / PT;                       // an o input chunk of the attention output (<= 2048)
 constexpr int NW_PART = 16;                                        // an o chunk's segment partials ([C][R] words)
@@ -105,7 +111,9 @@ constexpr int CMB_SEGS = 64;                                       // combine: s
 constexpr int NW_ML = 1;                                           // combine: a batch's (m_c, l_c) words per thread
 constexpr int CMB_EK = (ATT_MAX_GROUP * 128 + PT - 1) / PT;        // combine: output elements per thread, at most
 constexpr int NW_OC = 16;                                          // combine: o_c words per thread and round
-constexpr int CHH = 16 / PW;    // block pairs per wave group of a hidden-long tile (hidden <= 1024: <= 16 pairs)
+// HC (a kernel parameter, 2 or 4): block pairs per wave group of a
+// hidden-long tile (q|k|v, gate/up, lm_head; K = hidden), so hidden <= 64 HC
+// PW (1024 or 2048), and the words of a hidden vector per thread.
 #ifndef LQ8_LMU
 #define LQ8_LMU 4
 #endif
@@ -114,7 +122,6 @@ constexpr int CHH = 16 / PW;    // block pairs per wave group of a hidden-long t
 #endif
 constexpr int LMU = LQ8_LMU;   // lm_head: block pairs per streamed unit of a tile (a power of two)
 constexpr int LMS = LQ8_LMS;   // lm_head: units in a wave's ring (LMS - 1 in flight while one is summed)
-constexpr int LMQ = 16 / LMU;  // lm_head: units per tile, at most (hidden <= 1024: <= 16 pairs)
 #ifndef LQ8_LMD
 #define LQ8_LMD 4
 #endif
@@ -252,7 +259,7 @@ __device__ __forceinline__ float dot16_pinned(u32x4 c, const float* __restrict__
 // N chunk dots at once: N of the GEMV's 16-term fmaf chains (each in its
 // order, from +0, as dot16), interleaved step by step so that the dependent
 // chains overlap (one chain alone waits on each fma's latency).
-template <int N>
+template <int N, bool LEAN = false>
 __device__ __forceinline__ void dot16xN(const u32x4* c, const float* const* x, float* out) {
     uint32_t w[N][4];
 #pragma unroll
@@ -269,6 +276,7 @@ __device__ __forceinline__ void dot16xN(const u32x4* c, const float* const* x, f
     for (int k = 0; k < N; k++) p[k] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
+        if (LEAN) __builtin_amdgcn_sched_barrier(0);
         float4 xv[N];
 #pragma unroll
         for (int k = 0; k < N; k++) xv[k] = *(const float4*)(x[k] + 4 * i);
@@ -304,6 +312,18 @@ struct WRegs {
     uint16_t d[NS];
 };
 
+// A register set that a workgroup or wave has no item for: zeros, so that
+// every load site ends the life of the set's earlier values (a set kept
+// only on some paths stays allocated through every phase in between).
+template <int NS>
+__device__ __forceinline__ void wregs_clear(WRegs<NS>& R) {
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        R.c[i] = u32x4{0u, 0u, 0u, 0u};
+        R.d[i] = 0;
+    }
+}
+
 template <int CH>
 __device__ __forceinline__ Job make_job(const int8_t* codes, const uint16_t* scales, int np, int nb, int t0, int t1,
                                         int p0, int npv) {
@@ -315,7 +335,10 @@ __device__ __forceinline__ void job_load(const Job& J, WRegs<NTL * CH>& R) {
     const int lane = tid_here() & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
     const int r = lane & 15, bsel = (lane >> 4) >> 1;
-    if (wave >= J.G) return;
+    if (wave >= J.G) {
+        if constexpr (CH >= 4) wregs_clear(R);
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < NTL; j++) {
         const int tile = j ? J.t1 : J.t0;
@@ -328,11 +351,26 @@ __device__ __forceinline__ void job_load(const Job& J, WRegs<NTL * CH>& R) {
     }
 }
 
+// The chunks of one tile of the job into slots S0 .. S0 + CH - 1.
+template <int CH, int S0, int NSR>
+__device__ __forceinline__ void job_load_tile(const Job& J, int tile, WRegs<NSR>& R) {
+    const int lane = tid_here() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
+    const int r = lane & 15, bsel = (lane >> 4) >> 1;
+    if (wave >= J.G) return;
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const int p = J.p0 + min(wave * CH + i, J.npv - 1);
+        R.c[S0 + i] = chunk_load(J.codes + ((size_t)tile * J.np + p) * CHUNK_BYTES + lane * 16);
+        R.d[S0 + i] = scale_load(J.scales + (size_t)tile * 2 * J.np * 16 + bsel * 16 + r + (size_t)p * 32);
+    }
+}
+
 // Group sums into gs[(j * G + wave) * 16 + row]; xs holds the input of the
 // pair range (xs[(2 (p - p0) + b) * 32 + e] = x[(2 p + b) * 32 + e]).
 template <int NTL, int CH>
 __device__ __forceinline__ void job_dot(const Job& J, const WRegs<NTL * CH>& R, const float* xs, float* gs) {
-    constexpr int NS = NTL * CH, NI = NS < 4 ? NS : 4;  // chunks, interleaved NI at a time
+    constexpr int NS = NTL * CH, NI = NS < 4 ? NS : (CH >= 4 ? 2 : 4);  // chunks, interleaved NI at a time
     const int lane = tid_here() & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid_here() >> 6);
     const int part = lane >> 4, bsel = part >> 1, half = part & 1;
@@ -348,7 +386,7 @@ __device__ __forceinline__ void job_dot(const Job& J, const WRegs<NTL * CH>& R, 
             xp[k] = xs + (2 * pr + bsel) * 32 + half * 16;
         }
         float h[NI];
-        dot16xN<NI>(&R.c[s0], xp, h);
+        dot16xN<NI, (CH >= 4)>(&R.c[s0], xp, h);
 #pragma unroll
         for (int k = 0; k < NI; k++) {
             const int i = (s0 + k) % CH, pr = min(wave * CH + i, J.npv - 1);
@@ -390,12 +428,13 @@ __device__ __forceinline__ float tile_final(const float* gs, int G) {
     return v[0];
 }
 
-// The pairwise tree over n (<= PERSIST_NCH) chunk sums v[0 .. n).
-__device__ __forceinline__ float chunk_tree(float* v, int n) {
+// The pairwise tree over n (<= N) chunk sums v[0 .. n).
+template <int N>
+__device__ __forceinline__ float chunk_tree_n(float* v, int n) {
 #pragma unroll
-    for (int s = 1; s < PERSIST_NCH; s *= 2)
+    for (int s = 1; s < N; s *= 2)
 #pragma unroll
-        for (int i = 0; i + s < PERSIST_NCH; i += 2 * s)
+        for (int i = 0; i + s < N; i += 2 * s)
             if (i + s < n) v[i] = v[i] + v[i + s];
     return v[0];
 }
@@ -405,22 +444,24 @@ __device__ __forceinline__ float chunk_tree(float* v, int n) {
 // eps); out = bf16((v * inv) * bf16(w)).  norm_prefetch loads the weights
 // w[tid + j PT] before the phase's hand-off, so that their latency hides
 // behind it.
-__device__ __forceinline__ void norm_prefetch(const float* w, int k, float (&wv)[NW_H]) {
+template <int NWV>
+__device__ __forceinline__ void norm_prefetch(const float* w, int k, float (&wv)[NWV]) {
     const int tid = tid_here();
 #pragma unroll
-    for (int j = 0; j < NW_H; j++) wv[j] = tid + j * PT < k ? w[tid + j * PT] : 0.0f;
+    for (int j = 0; j < NWV; j++) wv[j] = tid + j * PT < k ? w[tid + j * PT] : 0.0f;
 }
 
-// The RmsNorm of the values hv[j] = v[tid + j PT] (j < NW_H) that the
+// The RmsNorm of the values hv[j] = v[tid + j PT] (j < NWV) that the
 // thread holds (the caller joined them), into xs[0, k), and zero over the
 // padding [k, 64 np): the bf16 inputs go to LDS once for the reduction,
 // whose lanes read their 16 elements at once before the add chain; the
 // normalised values come from the registers.
-__device__ __forceinline__ void stage_rmsnorm_regs(float (&hv)[NW_H], float* xs, int k, int np,
-                                                   const float (&wv)[NW_H], float eps, float* red) {
+template <int NWV>
+__device__ __forceinline__ void stage_rmsnorm_regs(float (&hv)[NWV], float* xs, int k, int np,
+                                                   const float (&wv)[NWV], float eps, float* red) {
     const int tid = tid_here();
 #pragma unroll
-    for (int j = 0; j < NW_H; j++) {
+    for (int j = 0; j < NWV; j++) {
         const int i = tid + j * PT;
         if (i < k) {
             hv[j] = bf16_round(hv[j]);
@@ -429,21 +470,25 @@ __device__ __forceinline__ void stage_rmsnorm_regs(float (&hv)[NW_H], float* xs,
     }
     lds_sync();
     if (tid < 64) {
-        constexpr int NL = NW_H * PT / 64;  // elements per lane, at most
-        float x[NL];
-#pragma unroll
-        for (int j = 0; j < NL; j++) x[j] = xs[min(tid + 64 * j, k - 1)];  // read unconditionally, used below k
+        constexpr int NL = NWV * PT / 64;  // elements per lane, at most
+        constexpr int NB = NL < 16 ? NL : 16;  // read in batches of NB
         float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < NL; j++)
-            if (tid + 64 * j < k) acc = acc + x[j] * x[j];
+        for (int j0 = 0; j0 < NL; j0 += NB) {
+            float x[NB];
+#pragma unroll
+            for (int j = 0; j < NB; j++) x[j] = xs[min(tid + 64 * (j0 + j), k - 1)];  // read unconditionally, used below k
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+                if (tid + 64 * (j0 + j) < k) acc = acc + x[j] * x[j];
+        }
         acc = wave_sum64(acc);
         if (tid == 0) red[0] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(acc, (float)k) + eps));
     }
     lds_sync();
     const float inv = red[0];
 #pragma unroll
-    for (int j = 0; j < NW_H; j++) {
+    for (int j = 0; j < NWV; j++) {
         const int i = tid + j * PT;
         if (i < k) xs[i] = bf16_round((hv[j] * inv) * bf16_round(wv[j]));
     }
@@ -673,17 +718,21 @@ __device__ __forceinline__ Dims dims_of(CArgs& a) {
     (void)attl;                                                                                            \
     (void)resl; (void)h2b; (void)actb; (void)n3
 
-// The jobs of the phases' items (CH5: pairs per group of a down item).
+// The jobs of the phases' items (HC: pairs per group of a hidden-long tile and
+// of an o item; CH5: pairs per group of a down item).
+template <int HC>
 __device__ __forceinline__ Job job_qkv(CArgs& a, const Dims& D, CLayer& Lw, int t) {
-    return make_job<CHH>(Lw.qkv_c, Lw.qkv_s, D.npH, D.nbH, t, t, 0, D.npH);
+    return make_job<HC>(Lw.qkv_c, Lw.qkv_s, D.npH, D.nbH, t, t, 0, D.npH);
 }
+template <int HC>
 __device__ __forceinline__ Job job_o(CArgs& a, const Dims& D, CLayer& Lw, int it) {
     const int t = it / a.nchO, c = it - t * a.nchO, pc = a.csO >> 1;
     const int p0 = c * pc;
-    return make_job<CHH>(Lw.o_c, Lw.o_s, D.npQ, D.nbQ, t, t, p0, min(pc, D.npQ - p0));
+    return make_job<HC>(Lw.o_c, Lw.o_s, D.npQ, D.nbQ, t, t, p0, min(pc, D.npQ - p0));
 }
+template <int HC>
 __device__ __forceinline__ Job job_gu(CArgs& a, const Dims& D, CLayer& Lw, int t) {
-    return make_job<CHH>(Lw.gu_c, Lw.gu_s, D.npH, D.nbH, t, D.TI + t, 0, D.npH);
+    return make_job<HC>(Lw.gu_c, Lw.gu_s, D.npH, D.nbH, t, D.TI + t, 0, D.npH);
 }
 template <int CH5>
 __device__ __forceinline__ Job job_dn(CArgs& a, const Dims& D, CLayer& Lw, int it) {
@@ -691,12 +740,191 @@ __device__ __forceinline__ Job job_dn(CArgs& a, const Dims& D, CLayer& Lw, int i
     return make_job<CH5>(Lw.dn_c, Lw.dn_s, D.npI, D.nbI, t, t, p0, min(a.csD, D.npI - p0));
 }
 
+// P6 of step s: the final RmsNorm, the lm_head tiles (one wave each) and
+// the workgroup's greedy pick, published for the next step.  false: the
+// launch is aborting.
+template <int HC>
+__device__ __forceinline__ bool lm_head_phase(const PersistArgs* __restrict__ pa, int w, int s, unsigned tag, float* sm,
+                                              LdsFlag bad, float* pick_v, int* pick_i) {
+    constexpr int LMQ = HC * PW / LMU;  // lm_head: units per tile, at most
+    constexpr int NWG = nw_res<HC>(), NCJ = nch_max<HC>();  // gather words per thread, chunk sums joined
+    const int P = gridDim.x;
+    [[maybe_unused]] const int l = 0;  // the P6 marks sit in layer 0's row
+    PTRACE(LQ8_PT_P6_START);
+    CArgs& a = *opaque_args(pa);
+    const Dims D = dims_of(a);
+    const int tid = tid_here(), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float* xs = sm + a.xs_off;
+    float* red = sm + a.red_off;
+    const int t0 = w * PW + wave, tstride = P * PW;
+    const int np = D.npH, nb = D.nbH;
+    const int r = lane & 15;
+    // a wave streams its tiles in units of LMU block pairs through a
+    // ring of LMS register sets: unit u sits in set u % LMS, and the
+    // loads of units u + 1 .. u + LMS - 1 are in flight while unit u
+    // is summed
+    const int nq = (np + LMU - 1) / LMU;  // units per tile, <= LMQ
+    u32x4 cr[LMS][LMU];
+    uint16_t dr[LMS][LMU];
+    // buffer loads: one descriptor per table and a 32-bit lane offset,
+    // the tile and chunk offsets uniform (no per-chunk pointers)
+    const int tiles_alloc = (D.T6 + 1) & ~1;  // rows stored in multiples of 32
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.emb_c, (short)0, (int)((size_t)tiles_alloc * np * CHUNK_BYTES), RSRC_RAW);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.emb_s, (short)0, (int)((size_t)tiles_alloc * 2 * np * 16 * sizeof(uint16_t)), RSRC_RAW);
+    auto load_u = [&](int t, int q, u32x4* c, uint16_t* d) {
+        const int ln = tid_here() & 63;
+        const int vo = ln * 16, vs = (((ln >> 4) >> 1) * 16 + (ln & 15)) * 2;
+#pragma unroll
+        for (int i = 0; i < LMU; i++) {
+            const int p = min(q * LMU + i, np - 1);
+            c[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rc, vo, (t * np + p) * CHUNK_BYTES, AUX_NT));
+            d[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, vs, (t * 2 * np + 2 * p) * 32, 0);
+        }
+    };
+    // the unit's pair values, summed by the tree levels inside the unit
+    auto dot_u = [&](int q, const u32x4* c, const uint16_t* d) {
+        const int ln = tid_here() & 63, bs = (ln >> 4) >> 1, hf = (ln >> 4) & 1;
+        float v[LMU];
+#pragma unroll
+        for (int i0 = 0; i0 < LMU; i0 += LMD) {
+            const float* xp[LMD];
+#pragma unroll
+            for (int k = 0; k < LMD; k++) xp[k] = xs + (2 * min(q * LMU + i0 + k, np - 1) + bs) * 32 + hf * 16;
+            float h[LMD];
+            dot16xN<LMD, HC == 4>(c + i0, xp, h);
+#pragma unroll
+            for (int k = 0; k < LMD; k++) {
+                const int pc = min(q * LMU + i0 + k, np - 1);
+                const LanePair hh = lanes16(h[k]);
+                const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(d[i0 + k]);
+                const LanePair vv = lanes32(vb);
+                v[i0 + k] = 2 * pc + 1 >= nb ? vv.lo : vv.lo + vv.hi;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const int cnt = np - q * LMU;
+#pragma unroll
+        for (int s2 = 1; s2 < LMU; s2 *= 2)
+#pragma unroll
+            for (int i = 0; i + s2 < LMU; i += 2 * s2)
+                if (i + s2 < cnt) v[i] = v[i] + v[i + s2];
+        return v[0];
+    };
+    const int ntw = t0 < D.T6 ? (D.T6 - t0 + tstride - 1) / tstride : 0;  // the wave's tiles
+    const int U = ntw * nq;                                                  // and units
+    auto unit_tile = [&](int u) { return t0 + (u / nq) * tstride; };
+    auto unit_q = [&](int u) { return u % nq; };
+    if constexpr (HC == 2) {
+#pragma unroll
+        for (int j = 0; j + 1 < LMS; j++)
+            if (j < U) load_u(unit_tile(j), unit_q(j), cr[j], dr[j]);
+    }
+    float nw[HC];
+    norm_prefetch(a.final_norm, D.H, nw);
+    // the last layer's output: its h2 + the down projection's chunk sums
+    const uint64_t* hp = a.h2b + (size_t)(a.L - 1) * (1 + a.nchD) * D.H;
+    float* f = sm;  // [1 + nchD][H]
+    tfetch_lin<NWG>((1 + a.nchD) * D.H, tag, hp, f, a.abort_flag, bad);
+    lds_sync();
+    if (bad_now(bad)) return false;
+    float hv[HC];
+    const int nchD = a.nchD;
+#pragma unroll
+    for (int j = 0; j < HC; j++) {
+        const int r = tid + j * PT;
+        if (r < D.H) {
+            float v[NCJ];
+#pragma unroll
+            for (int q = 0; q < NCJ; q++) v[q] = f[(1 + min(q, nchD - 1)) * D.H + r];
+            hv[j] = f[r] + chunk_tree_n<NCJ>(v, nchD);
+        }
+    }
+    stage_rmsnorm_regs(hv, xs, D.H, np, nw, a.eps, red);
+    if constexpr (HC == 4) {
+#pragma unroll
+        for (int j = 0; j + 1 < LMS; j++)
+            if (j < U) load_u(unit_tile(j), unit_q(j), cr[j], dr[j]);
+    }
+    PTRACE(LQ8_PT_P6_NORMED);
+    float bv = -__builtin_huge_valf();
+    int bi = -1;
+    float uv[LMQ];  // the tile's unit values (subtrees of LMU pairs)
+    for (int u0 = 0; u0 < U; u0 += LMS) {
+#pragma unroll
+        for (int j = 0; j < LMS; j++) {
+            const int u = u0 + j;
+            if (u < U) {
+                if (u + LMS - 1 < U)
+                    load_u(unit_tile(u + LMS - 1), unit_q(u + LMS - 1), cr[(j + LMS - 1) % LMS],
+                           dr[(j + LMS - 1) % LMS]);
+                const int q = unit_q(u);
+                const float vq = dot_u(q, cr[j], dr[j]);
+#pragma unroll
+                for (int k = 0; k < LMQ; k++)
+                    if (k == q) uv[k] = vq;
+                if (q == nq - 1) {
+                    // the tree levels above the units (pairs LMU, 2 LMU, ... apart)
+#pragma unroll
+                    for (int s2 = 1; s2 < LMQ; s2 *= 2)
+#pragma unroll
+                        for (int i = 0; i + s2 < LMQ; i += 2 * s2)
+                            if (i + s2 < nq) uv[i] = uv[i] + uv[i + s2];
+                    const int row = unit_tile(u) * 16 + r;
+                    const bool valid = lane < 16 && row < a.vocab;
+                    float tv = valid ? uv[0] : -__builtin_huge_valf();
+                    int ti = valid ? row : -1;
+                    argmax_step<8>(tv, ti);
+                    argmax_step<4>(tv, ti);
+                    argmax_step<2>(tv, ti);
+                    argmax_step<1>(tv, ti);
+                    if (tv > bv || (tv == bv && ti > bi)) {
+                        bv = tv;
+                        bi = ti;
+                    }
+                }
+            }
+        }
+    }
+    // lanes 0..15 hold the wave's pick (rows of lanes 16..63 were invalid)
+    wg_argmax(bv, bi, pick_v, pick_i);
+    if (tid == 0) {
+        uint64_t* ab = a.argb + (size_t)(tag & 1) * 2 * P;
+        tput(ab + 2 * w, bv, tag);
+        tput(ab + 2 * w + 1, __uint_as_float((unsigned)bi), tag);
+    }
+    // the step's one fenced barrier: the workgroup's key/value cache
+    // stores of this step are visible to its waves' loads of the next
+    __syncthreads();
+    PTRACE(LQ8_PT_P6_DONE);
+    return true;
+}
+
+// The lm_head phase as a call of its own: its registers are allocated apart
+// from the layer phases' (the kernel instance for hidden above 1024 holds
+// too many of them across the layers for the phase's load ring).
+template <int HC>
+__device__ __noinline__ bool lm_head_phase_call(const PersistArgs* __restrict__ pa, int w, int s, unsigned tag,
+                                                float* sm, LdsFlag bad, float* pick_v, int* pick_i) {
+    // the arguments arrive in vector registers: wave-uniform values again
+    const uint64_t pu = (uint64_t)(uintptr_t)pa;
+    const uint32_t plo = __builtin_amdgcn_readfirstlane((uint32_t)pu);
+    const uint32_t phi = __builtin_amdgcn_readfirstlane((uint32_t)(pu >> 32));
+    const PersistArgs* pa_u = (const PersistArgs*)(uintptr_t)(((uint64_t)phi << 32) | plo);
+    return lm_head_phase<HC>(pa_u, __builtin_amdgcn_readfirstlane(w), __builtin_amdgcn_readfirstlane(s),
+                             __builtin_amdgcn_readfirstlane(tag), sm, bad, pick_v, pick_i);
+}
+
 // LONG: the kernel instance for steps with more than cdir segments (the
 // combining attention items); the other instance has no combine code at all
 // (its presence alone, never run, costs the short-context steps about 3 %
 // through register allocation), and the host launches each for its steps.
-template <int CH5, bool LONG>
+template <int CH5, bool LONG, int HC>
 __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __restrict__ pa) {
+    constexpr int NWG = nw_res<HC>(), NCJ = nch_max<HC>();  // gather words per thread, chunk sums joined
     extern __shared__ __align__(16) float sm[];
     __shared__ int bad_s;
     __shared__ float pick_v[PW];
@@ -712,8 +940,9 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
         const Dims D = dims_of(a);
         const unsigned tag = a.tag0 + (unsigned)s;
         // layer 0's q|k|v weights, in flight while the token arrives
-        WRegs<CHH> R1;
-        if (w < D.T1) job_load<1, CHH>(job_qkv(a, D, layer_of(a, 0), w), R1);
+        WRegs<HC> R1;
+        if (w < D.T1) job_load<1, HC>(job_qkv<HC>(a, D, layer_of(a, 0), w), R1);
+        else if constexpr (HC == 4) wregs_clear(R1);
         // ---- the step's input token: the previous step's greedy pick (last
         // index on ties) over the workgroups' picks; the first step's from
         // the previous kernel
@@ -741,30 +970,30 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             if (w < dims_of(*opaque_args(pa)).T1) {
                 LAYER_LOCALS;
                 PTRACE(LQ8_PT_P1_START);
-                float nw[NW_H], hv[NW_H];
+                float nw[HC], hv[HC];
                 norm_prefetch(Lw.in_norm, D.H, nw);
                 if (l > 0) {
                     // h_l = h2 of layer l - 1 + its down projection's chunk sums
                     // joined in the block tree; published for this layer's h2
                     const uint64_t* hp = a.h2b + (size_t)(l - 1) * (1 + a.nchD) * D.H;
                     float* f = sm;  // [1 + nchD][H]
-                    tfetch_lin<NW_RES>((1 + a.nchD) * D.H, tag, hp, f, a.abort_flag, bad);
+                    tfetch_lin<NWG>((1 + a.nchD) * D.H, tag, hp, f, a.abort_flag, bad);
                     lds_sync();
                     if (bad_now(bad)) goto done;
                     PTRACE(LQ8_PT_P1_GATHERED);
                     const int n1 = min(D.T1, P);
                     // the chunk sums are read unconditionally (an index past
-                    // nchD reads the last chunk, which chunk_tree ignores), so
+                    // nchD reads the last chunk, which chunk_tree_n ignores), so
                     // all of a thread's LDS reads are in flight together
                     const int nchD = a.nchD;
 #pragma unroll
-                    for (int j = 0; j < NW_H; j++) {
+                    for (int j = 0; j < HC; j++) {
                         const int r = tid + j * PT;
                         if (r < D.H) {
-                            float v[PERSIST_NCH];
+                            float v[NCJ];
 #pragma unroll
-                            for (int q = 0; q < PERSIST_NCH; q++) v[q] = f[(1 + min(q, nchD - 1)) * D.H + r];
-                            hv[j] = f[r] + chunk_tree(v, nchD);
+                            for (int q = 0; q < NCJ; q++) v[q] = f[(1 + min(q, nchD - 1)) * D.H + r];
+                            hv[j] = f[r] + chunk_tree_n<NCJ>(v, nchD);
                             if (r % n1 == w) tput(resl + r, hv[j], tag);
                         }
                     }
@@ -772,7 +1001,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     // the embedding row (src/embedding.rs), published as h_0
                     const int n1 = min(D.T1, P);
 #pragma unroll
-                    for (int j = 0; j < NW_H; j++) {
+                    for (int j = 0; j < HC; j++) {
                         const int r = tid + j * PT;
                         if (r < D.H) {
                             hv[j] = q8_elem(a.emb_c, a.emb_s, D.npH, (int)tok, r);
@@ -784,9 +1013,9 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 stage_rmsnorm_regs(hv, xs, D.H, D.npH, nw, a.eps, red);
                 PTRACE(LQ8_PT_P1_NORMED);
                 for (int t = w; t < D.T1; t += P) {
-                    const Job J = job_qkv(a, D, Lw, t);
-                    if (t != w) job_load<1, CHH>(J, R1);
-                    job_dot<1, CHH>(J, R1, xs, gs);
+                    const Job J = job_qkv<HC>(a, D, Lw, t);
+                    if (t != w) job_load<1, HC>(J, R1);
+                    job_dot<1, HC>(J, R1, xs, gs);
                     lds_sync();
                     PTRACE(LQ8_PT_P1_DOT);
                     if (tid < 64) {
@@ -799,10 +1028,10 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             }
 
             // the o tile's weights, in flight through the attention phase
-            WRegs<CHH> R3;
+            WRegs<HC> R3;
             {
                 LAYER_LOCALS;
-                if (w < n3) job_load<1, CHH>(job_o(a, D, Lw, w), R3);
+                if (w < n3) job_load<1, HC>(job_o<HC>(a, D, Lw, w), R3);
             }
 
             // ---- P2: attention per (segment, kv head) item; the item of the
@@ -917,8 +1146,8 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 LAYER_LOCALS;
                 const int L1 = pos + 1, C = (L1 + ATT_SEG - 1) / ATT_SEG;
                 for (int it = w; it < n3; it += P) {
-                    const Job J = job_o(a, D, Lw, it);
-                    if (it != w) job_load<1, CHH>(J, R3);
+                    const Job J = job_o<HC>(a, D, Lw, it);
+                    if (it != w) job_load<1, HC>(J, R3);
                     const int t = it / a.nchO, c = it - t * a.nchO;
                     const int i0 = J.p0 * 64, rng = min(J.npv * 64, D.QD - i0);
                     if (C <= a.cdir) {
@@ -1009,7 +1238,7 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                     }
                     stage_pad(xs, rng, J.npv);
                     lds_sync();
-                    job_dot<1, CHH>(J, R3, xs, gs);
+                    job_dot<1, HC>(J, R3, xs, gs);
                     lds_sync();
                     if (tid < 64) {
                         const float y = tile_final(gs, J.G);
@@ -1020,12 +1249,16 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             }
 
             // the gate|up and down weights, in flight through the hand-offs
-            WRegs<2 * CHH> R4;
+            WRegs<2 * HC> R4;
             WRegs<CH5> R5;
             {
                 LAYER_LOCALS;
-                if (w < D.TI) job_load<2, CHH>(job_gu(a, D, Lw, w), R4);
-                if (w < D.TH * a.nchD) job_load<1, CH5>(job_dn<CH5>(a, D, Lw, w), R5);
+                if (w < D.TI) {
+                    const Job J = job_gu<HC>(a, D, Lw, w);
+                    if constexpr (HC == 4) job_load_tile<HC, 0>(J, J.t0, R4);  // the up half after the hand-off
+                    else job_load<2, HC>(J, R4);
+                }
+                if (HC == 2 && w < D.TH * a.nchD) job_load<1, CH5>(job_dn<CH5>(a, D, Lw, w), R5);
             }
 
             // ---- P4: h2 = h_l + o, RmsNorm(h2) + gate / up tile pair -> silu(gate) * up
@@ -1033,33 +1266,34 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 LAYER_LOCALS;
             PTRACE(LQ8_PT_P4_START);
             for (int t = w; t < D.TI; t += P) {
-                const Job J = job_gu(a, D, Lw, t);
-                if (t != w) job_load<2, CHH>(J, R4);
+                const Job J = job_gu<HC>(a, D, Lw, t);
+                if (t != w) job_load<2, HC>(J, R4);
                 float* f = sm;  // [1 + nchO][H]
                 if (t == w) {
-                    float nw[NW_H];
+                    float nw[HC];
                     norm_prefetch(Lw.post_norm, D.H, nw);
-                    tfetch_lin<NW_RES>((1 + a.nchO) * D.H, tag, resl, f, a.abort_flag, bad);
+                    tfetch_lin<NWG>((1 + a.nchO) * D.H, tag, resl, f, a.abort_flag, bad);
                     lds_sync();
                     if (bad_now(bad)) goto done;
+                    if constexpr (HC == 4) job_load_tile<HC, HC>(J, J.t1, R4);
                     PTRACE(LQ8_PT_P4_STAGED);
                     const int n4 = min(D.TI, P), nchO = a.nchO;
-                    float hv[NW_H];
+                    float hv[HC];
 #pragma unroll
-                    for (int j = 0; j < NW_H; j++) {
+                    for (int j = 0; j < HC; j++) {
                         const int r = tid + j * PT;
                         if (r < D.H) {
-                            float v[PERSIST_NCH];
+                            float v[NCJ];
 #pragma unroll
-                            for (int q = 0; q < PERSIST_NCH; q++) v[q] = f[(1 + min(q, nchO - 1)) * D.H + r];
-                            hv[j] = f[r] + chunk_tree(v, nchO);
+                            for (int q = 0; q < NCJ; q++) v[q] = f[(1 + min(q, nchO - 1)) * D.H + r];
+                            hv[j] = f[r] + chunk_tree_n<NCJ>(v, nchO);
                             if (r % n4 == w) tput(h2b + r, hv[j], tag);
                         }
                     }
                     stage_rmsnorm_regs(hv, xs, D.H, D.npH, nw, a.eps, red);
                     PTRACE(LQ8_PT_P4_NORMED);
                 }
-                job_dot<2, CHH>(J, R4, xs, gs);
+                job_dot<2, HC>(J, R4, xs, gs);
                 lds_sync();
                 PTRACE(LQ8_PT_P4_DOT);
                 if (tid < 64) {
@@ -1074,7 +1308,8 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
             // the next layer's q|k|v weights, in flight through the down projection
             {
                 LAYER_LOCALS;
-                if (l + 1 < a.L && w < D.T1) job_load<1, CHH>(job_qkv(a, D, layer_of(a, l + 1), w), R1);
+                if (HC == 4 && w < D.TH * a.nchD) job_load<1, CH5>(job_dn<CH5>(a, D, Lw, w), R5);
+                if (HC == 2 && l + 1 < a.L && w < D.T1) job_load<1, HC>(job_qkv<HC>(a, D, layer_of(a, l + 1), w), R1);
             }
 
             // ---- P5: down tile over one input chunk -> chunk sums (the
@@ -1103,154 +1338,19 @@ __global__ __launch_bounds__(PT) void k_decode_persistent(const PersistArgs* __r
                 PTRACE(LQ8_PT_P5_DONE);
             }
             }
+            if constexpr (HC == 4) {
+                // the next layer's q|k|v weights, in flight through its hand-off
+                LAYER_LOCALS;
+                if (l + 1 < a.L && w < D.T1) job_load<1, HC>(job_qkv<HC>(a, D, layer_of(a, l + 1), w), R1);
+                else wregs_clear(R1);
+            }
         }
 
         // ---- P6: final RmsNorm, lm_head tiles (one wave each), greedy pick
-        {
-            [[maybe_unused]] const int l = 0;  // the P6 marks sit in layer 0's row
-            PTRACE(LQ8_PT_P6_START);
-            CArgs& a = *opaque_args(pa);
-            const Dims D = dims_of(a);
-            const int tid = tid_here(), lane = tid & 63;
-            const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-            float* xs = sm + a.xs_off;
-            float* red = sm + a.red_off;
-            const int t0 = w * PW + wave, tstride = P * PW;
-            const int np = D.npH, nb = D.nbH;
-            const int r = lane & 15;
-            // a wave streams its tiles in units of LMU block pairs through a
-            // ring of LMS register sets: unit u sits in set u % LMS, and the
-            // loads of units u + 1 .. u + LMS - 1 are in flight while unit u
-            // is summed
-            const int nq = (np + LMU - 1) / LMU;  // units per tile, <= LMQ
-            u32x4 cr[LMS][LMU];
-            uint16_t dr[LMS][LMU];
-            // buffer loads: one descriptor per table and a 32-bit lane offset,
-            // the tile and chunk offsets uniform (no per-chunk pointers)
-            const int tiles_alloc = (D.T6 + 1) & ~1;  // rows stored in multiples of 32
-            const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-                (void*)a.emb_c, (short)0, (int)((size_t)tiles_alloc * np * CHUNK_BYTES), RSRC_RAW);
-            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                (void*)a.emb_s, (short)0, (int)((size_t)tiles_alloc * 2 * np * 16 * sizeof(uint16_t)), RSRC_RAW);
-            auto load_u = [&](int t, int q, u32x4* c, uint16_t* d) {
-                const int ln = tid_here() & 63;
-                const int vo = ln * 16, vs = (((ln >> 4) >> 1) * 16 + (ln & 15)) * 2;
-#pragma unroll
-                for (int i = 0; i < LMU; i++) {
-                    const int p = min(q * LMU + i, np - 1);
-                    c[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         rc, vo, (t * np + p) * CHUNK_BYTES, AUX_NT));
-                    d[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, vs, (t * 2 * np + 2 * p) * 32, 0);
-                }
-            };
-            // the unit's pair values, summed by the tree levels inside the unit
-            auto dot_u = [&](int q, const u32x4* c, const uint16_t* d) {
-                const int ln = tid_here() & 63, bs = (ln >> 4) >> 1, hf = (ln >> 4) & 1;
-                float v[LMU];
-#pragma unroll
-                for (int i0 = 0; i0 < LMU; i0 += LMD) {
-                    const float* xp[LMD];
-#pragma unroll
-                    for (int k = 0; k < LMD; k++) xp[k] = xs + (2 * min(q * LMU + i0 + k, np - 1) + bs) * 32 + hf * 16;
-                    float h[LMD];
-                    dot16xN<LMD>(c + i0, xp, h);
-#pragma unroll
-                    for (int k = 0; k < LMD; k++) {
-                        const int pc = min(q * LMU + i0 + k, np - 1);
-                        const LanePair hh = lanes16(h[k]);
-                        const float vb = (hh.lo + hh.hi) * f16_bits_to_f32(d[i0 + k]);
-                        const LanePair vv = lanes32(vb);
-                        v[i0 + k] = 2 * pc + 1 >= nb ? vv.lo : vv.lo + vv.hi;
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                const int cnt = np - q * LMU;
-#pragma unroll
-                for (int s2 = 1; s2 < LMU; s2 *= 2)
-#pragma unroll
-                    for (int i = 0; i + s2 < LMU; i += 2 * s2)
-                        if (i + s2 < cnt) v[i] = v[i] + v[i + s2];
-                return v[0];
-            };
-            const int ntw = t0 < D.T6 ? (D.T6 - t0 + tstride - 1) / tstride : 0;  // the wave's tiles
-            const int U = ntw * nq;                                                  // and units
-            auto unit_tile = [&](int u) { return t0 + (u / nq) * tstride; };
-            auto unit_q = [&](int u) { return u % nq; };
-#pragma unroll
-            for (int j = 0; j + 1 < LMS; j++)
-                if (j < U) load_u(unit_tile(j), unit_q(j), cr[j], dr[j]);
-            float nw[NW_H];
-            norm_prefetch(a.final_norm, D.H, nw);
-            // the last layer's output: its h2 + the down projection's chunk sums
-            const uint64_t* hp = a.h2b + (size_t)(a.L - 1) * (1 + a.nchD) * D.H;
-            float* f = sm;  // [1 + nchD][H]
-            tfetch_lin<NW_RES>((1 + a.nchD) * D.H, tag, hp, f, a.abort_flag, bad);
-            lds_sync();
-            if (bad_now(bad)) goto done;
-            float hv[NW_H];
-            const int nchD = a.nchD;
-#pragma unroll
-            for (int j = 0; j < NW_H; j++) {
-                const int r = tid + j * PT;
-                if (r < D.H) {
-                    float v[PERSIST_NCH];
-#pragma unroll
-                    for (int q = 0; q < PERSIST_NCH; q++) v[q] = f[(1 + min(q, nchD - 1)) * D.H + r];
-                    hv[j] = f[r] + chunk_tree(v, nchD);
-                }
-            }
-            stage_rmsnorm_regs(hv, xs, D.H, np, nw, a.eps, red);
-            PTRACE(LQ8_PT_P6_NORMED);
-            float bv = -__builtin_huge_valf();
-            int bi = -1;
-            float uv[LMQ];  // the tile's unit values (subtrees of LMU pairs)
-            for (int u0 = 0; u0 < U; u0 += LMS) {
-#pragma unroll
-                for (int j = 0; j < LMS; j++) {
-                    const int u = u0 + j;
-                    if (u < U) {
-                        if (u + LMS - 1 < U)
-                            load_u(unit_tile(u + LMS - 1), unit_q(u + LMS - 1), cr[(j + LMS - 1) % LMS],
-                                   dr[(j + LMS - 1) % LMS]);
-                        const int q = unit_q(u);
-                        const float vq = dot_u(q, cr[j], dr[j]);
-#pragma unroll
-                        for (int k = 0; k < LMQ; k++)
-                            if (k == q) uv[k] = vq;
-                        if (q == nq - 1) {
-                            // the tree levels above the units (pairs LMU, 2 LMU, ... apart)
-#pragma unroll
-                            for (int s2 = 1; s2 < LMQ; s2 *= 2)
-#pragma unroll
-                                for (int i = 0; i + s2 < LMQ; i += 2 * s2)
-                                    if (i + s2 < nq) uv[i] = uv[i] + uv[i + s2];
-                            const int row = unit_tile(u) * 16 + r;
-                            const bool valid = lane < 16 && row < a.vocab;
-                            float tv = valid ? uv[0] : -__builtin_huge_valf();
-                            int ti = valid ? row : -1;
-                            argmax_step<8>(tv, ti);
-                            argmax_step<4>(tv, ti);
-                            argmax_step<2>(tv, ti);
-                            argmax_step<1>(tv, ti);
-                            if (tv > bv || (tv == bv && ti > bi)) {
-                                bv = tv;
-                                bi = ti;
-                            }
-                        }
-                    }
-                }
-            }
-            // lanes 0..15 hold the wave's pick (rows of lanes 16..63 were invalid)
-            wg_argmax(bv, bi, pick_v, pick_i);
-            if (tid == 0) {
-                uint64_t* ab = a.argb + (size_t)(tag & 1) * 2 * P;
-                tput(ab + 2 * w, bv, tag);
-                tput(ab + 2 * w + 1, __uint_as_float((unsigned)bi), tag);
-            }
-            // the step's one fenced barrier: the workgroup's key/value cache
-            // stores of this step are visible to its waves' loads of the next
-            __syncthreads();
-            PTRACE(LQ8_PT_P6_DONE);
+        if constexpr (HC == 4) {
+            if (!lm_head_phase_call<HC>(pa, w, s, tag, sm, bad, pick_v, pick_i)) goto done;
+        } else {
+            if (!lm_head_phase<HC>(pa, w, s, tag, sm, bad, pick_v, pick_i)) goto done;
         }
     }
 
@@ -1284,41 +1384,44 @@ bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
     if (s.head_dim != 128 || s.NKV <= 0 || s.NH <= 0 || s.NH % s.NKV || s.max_pos <= 0 || P <= 0) return false;
     const int G = s.NH / s.NKV;
     if (G > ATT_MAX_GROUP) return false;
-    // hidden <= 1024: a q|k|v, gate/up or lm_head tile (<= 16 block pairs)
-    // is one group of CHH pairs per wave, the lm_head tile fits the units
-    // of a wave's ring (LMQ * LMU pairs), and a hidden vector is NW_H words
-    // per thread; intermediate <= 4096; the attention output (NH * 128) is
-    // at most one P3 fetch (NW_ATT words per thread)
-    if (s.H % 32 || s.H < 32 || s.H > 1024 || s.I % 32 || s.I < 32 || s.I > 4096 || s.NH * 128 > 2048) return false;
+    // hidden <= 2048: a q|k|v, gate/up or lm_head tile (<= 32 block pairs)
+    // is one group of hc pairs per wave (the kernel instance's HC: 2 up to
+    // hidden 1024, else 4), the lm_head tile fits the units of a wave's
+    // ring (hc PW pairs), and a hidden vector is hc words per thread; the
+    // attention output (NH * 128) is at most one P3 fetch (NW_ATT words per
+    // thread)
+    if (s.H % 32 || s.H < 32 || s.H > 2048 || s.I % 32 || s.I < 32 || s.I > 65536 || s.NH * 128 > 2048) return false;
+    const int hc = persist_pairs_per_wave(s.H);
     const int QD = s.NH * 128, nbQ = QD / 32, TH = s.H / 16;
     const int npH = (s.H / 32 + 1) / 2, npI = (s.I / 32 + 1) / 2;
-    if (npH > CHH * PW || npH > LMQ * LMU || s.H > NW_H * PT || QD > NW_ATT * PT) return false;
-    const int cap = NW_RES * PT;  // words of one gather of a hidden vector and its chunk sums
+    if (npH > hc * PW || s.H > hc * PT || QD > NW_ATT * PT) return false;
+    const int cap = (hc == 4 ? NW_RES4 : NW_RES) * PT;  // words of one gather of a hidden vector and its chunk sums
+    const int nchm = hc == 4 ? NCH4 : PERSIST_NCH;       // chunk sums one element joins, at most
     // o input chunks: the smallest power-of-two block count whose items fit
     // the workgroups (or one chunk over the whole input, or the widest chunk
     // a workgroup's waves hold: then a workgroup takes several items)
     int csO = 2;
     auto nch_of = [&](int cs) { return (nbQ + cs - 1) / cs; };
-    while (csO < nbQ && csO < 2 * CHH * PW &&
-           (TH * nch_of(csO) > P || nch_of(csO) > PERSIST_NCH || (1 + nch_of(csO)) * s.H > cap))
+    while (csO < nbQ && csO < 2 * hc * PW &&
+           (TH * nch_of(csO) > P || nch_of(csO) > nchm || (1 + nch_of(csO)) * s.H > cap))
         csO *= 2;
     const int nchO = nch_of(csO);
     const int pairsO = (std::min(csO, nbQ) + 1) / 2;  // pairs of the widest o chunk
     // P4 gathers h and the o chunk sums; a chunk's pairs are one group per wave
-    if (nchO > PERSIST_NCH || (1 + nchO) * s.H > cap || pairsO > CHH * PW) return false;
+    if (nchO > nchm || (1 + nchO) * s.H > cap || pairsO > hc * PW) return false;
     // down input chunks: the smallest power-of-two pair count, at least one
     // pair per wave, whose (tile, chunk) items fit the workgroups (or one
     // chunk over the whole input)
     int csD = PW;
     auto nchd_of = [&](int cs) { return (npI + cs - 1) / cs; };
     while (csD < npI &&
-           (TH * nchd_of(csD) > P || nchd_of(csD) > PERSIST_NCH || (1 + nchd_of(csD)) * s.H > cap))
+           (TH * nchd_of(csD) > P || nchd_of(csD) > nchm || (1 + nchd_of(csD)) * s.H > cap))
         csD *= 2;
     const int nchD = nchd_of(csD);
     // P1 and P6 gather h2 and the down chunk sums; a down item's pairs are
     // CH5 = csD / PW per wave (a kernel variant for CH5 = 1, 2, 4, 8); its
     // input chunk is one P5 fetch
-    if (nchD > PERSIST_NCH || (1 + nchD) * s.H > cap || csD > 8 * PW || std::min(csD, npI) * 64 > NW_ACT * PT)
+    if (nchD > nchm || (1 + nchD) * s.H > cap || csD > 8 * PW || std::min(csD, npI) * 64 > NW_ACT * PT)
         return false;
     // the picks (2 words per workgroup) are one fetch; an attention item's
     // q, k, v one more; a combine batch's (m_c, l_c) and a thread's output
@@ -1327,6 +1430,7 @@ bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
         NW_ML + NW_OC > 32)
         return false;
     PersistLayout L{};
+    L.hc = hc;
     L.csO = csO;
     L.nchO = nchO;
     L.csD = csD;
@@ -1365,20 +1469,24 @@ bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
 
 bool persist_supported(const PersistShape& s, int num_cus) { return persist_layout(s, num_cus, nullptr); }
 
-template <bool LONG>
+template <bool LONG, int HC>
 const void* persist_kernel(int ch5) {
-    return ch5 == 1   ? (const void*)k_decode_persistent<1, LONG>
-           : ch5 == 2 ? (const void*)k_decode_persistent<2, LONG>
-           : ch5 == 4 ? (const void*)k_decode_persistent<4, LONG>
-                      : (const void*)k_decode_persistent<8, LONG>;
+    return ch5 == 1   ? (const void*)k_decode_persistent<1, LONG, HC>
+           : ch5 == 2 ? (const void*)k_decode_persistent<2, LONG, HC>
+           : ch5 == 4 ? (const void*)k_decode_persistent<4, LONG, HC>
+                      : (const void*)k_decode_persistent<8, LONG, HC>;
 }
 
+int persist_pairs_per_wave(int hidden) { return hidden > 64 * 2 * PW ? 4 : 2; }
+
 lq8_status launch_decode_persistent(hipStream_t st, const PersistArgs* d_args, int smem_bytes, int num_wg, int ch5,
-                                    bool long_ctx) {
+                                    int hc, bool long_ctx) {
     const PersistArgs* args = d_args;
     void* kargs[] = {&args};
     const size_t smem = (size_t)smem_bytes;
-    const void* k = long_ctx ? persist_kernel<true>(ch5) : persist_kernel<false>(ch5);
+    if (hc != 2 && hc != 4) return fail(LQ8_ERR_INVALID_ARG, "persistent decode: no kernel for this hidden size");
+    const void* k = hc == 2 ? (long_ctx ? persist_kernel<true, 2>(ch5) : persist_kernel<false, 2>(ch5))
+                            : (long_ctx ? persist_kernel<true, 4>(ch5) : persist_kernel<false, 4>(ch5));
     hipError_t e = hipLaunchCooperativeKernel(k, dim3((unsigned)num_wg), dim3(PT), kargs, smem, st);
     if (e == hipErrorCooperativeLaunchTooLarge)
         return fail(LQ8_ERR_DEVICE, "persistent decode: the grid cannot be co-resident");

@@ -640,7 +640,8 @@ lq8_status launch_persist(lq8_model* m, int pos0, int steps, bool feed_first) {
         a.d_pos = m->d_pos;
         a.d_step = m->d_step;
         LQ8_HIP(hipMemcpyAsync(m->d_pargs + part, &a, sizeof(PersistArgs), hipMemcpyHostToDevice, s));
-        lq8_status st = launch_decode_persistent(s, m->d_pargs + part, a.smem_bytes, m->persist_wg, ch5, part == 1);
+        lq8_status st = launch_decode_persistent(s, m->d_pargs + part, a.smem_bytes, m->persist_wg, ch5,
+                                                 persist_pairs_per_wave(a.H), part == 1);
         if (st) return st;
     }
     m->tag += (unsigned)steps;

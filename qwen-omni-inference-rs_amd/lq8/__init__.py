@@ -464,6 +464,13 @@ def qwen3_0_6b(max_positions: int = 4096) -> Qwen3Config:
     return Qwen3Config(max_position_embeddings=max_positions)
 
 
+def qwen3_1_7b(max_positions: int = 4096) -> Qwen3Config:
+    """Qwen3-1.7B's shapes (its config.json): hidden 2048, intermediate 6144,
+    28 layers, 16 query and 8 kv heads of 128, vocab 151936, tied embedding;
+    the other fields as Qwen3-0.6B's."""
+    return Qwen3Config(hidden_size=2048, intermediate_size=6144, max_position_embeddings=max_positions)
+
+
 class Qwen3ForCausalLM:
     """src/model.rs:245-398 on Q8_0 weights."""
 

@@ -1,13 +1,13 @@
 """Phase timeline of the persistent greedy decode kernel.
 
-Runs Qwen3-0.6B-shaped greedy decode (random Q8_0 weights, a 128-token
-prompt) through the persistent kernel of the trace build (``make trace`` ->
+Runs Qwen3-0.6B-shaped (or, with --shape 1.7b, Qwen3-1.7B-shaped) greedy
+decode (random Q8_0 weights, a 128-token prompt) through the persistent kernel of the trace build (``make trace`` ->
 liblq8_trace.so) and prints, per phase mark, when the workgroups pass it
 relative to the moment the layer's input is complete (the last workgroup's
 layer start, i.e. the last down tile of the previous layer).  Medians over
 the layers 4 .. L-1 of one decode step.
 
-    python -m lq8.trace_timeline [--layers 28] [--prompt 128]
+    python -m lq8.trace_timeline [--layers 28] [--prompt 128] [--shape 0.6b|1.7b]
 """
 import argparse
 import contextlib
@@ -70,15 +70,15 @@ def trace_library():
         lq8._lib, lq8.LIB_PATH = saved
 
 
-def collect(layers: int, prompt: int, new: int):
-    """(generate statistics, trace) of Qwen3-0.6B-shaped greedy decode with
+def collect(layers: int, prompt: int, new: int, shape: str = "0.6b"):
+    """(generate statistics, trace) of Qwen3-0.6B- or 1.7B-shaped greedy decode with
     ``layers`` layers through the persistent kernel of the trace build; the
     second of two runs is the one traced."""
     prev = os.environ.get("LQ8_PERSIST")
     os.environ["LQ8_PERSIST"] = "1"
     try:
         with trace_library():
-            cfg = lq8.qwen3_0_6b(max_positions=512)
+            cfg = (lq8.qwen3_1_7b if shape == "1.7b" else lq8.qwen3_0_6b)(max_positions=512)
             cfg.num_hidden_layers = layers
             with lq8.Context(0) as ctx:
                 model = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=2026)
@@ -101,8 +101,9 @@ def main(argv=None) -> int:
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--new", type=int, default=9, help="generated tokens (the 4th decode step is traced)")
+    ap.add_argument("--shape", choices=("0.6b", "1.7b"), default="0.6b", help="the model's layer shapes")
     args = ap.parse_args(argv)
-    stats, tr = collect(args.layers, args.prompt, args.new)
+    stats, tr = collect(args.layers, args.prompt, args.new, args.shape)
     if not stats["used_persistent"]:
         print("the persistent kernel did not run", file=sys.stderr)
         return 1

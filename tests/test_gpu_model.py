@@ -451,6 +451,61 @@ def test_persistent_other_workgroup_counts(ctx, wg, combine):
     persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 60, env=env)
 
 
+@pytest.mark.parametrize("combine", ["direct", "combiner"])
+@pytest.mark.parametrize("hidden,inter,heads,kv", [(2048, 6144, 16, 8), (1536, 4160, 12, 4), (1056, 2720, 8, 2)])
+def test_persistent_hidden_above_1024(ctx, hidden, inter, heads, kv, combine):
+    """Hidden sizes above 1024 run the kernel instance with 4 block pairs per
+    wave group of a hidden-long tile: Qwen3-1.7B layer widths (hidden 2048:
+    32 pairs, 8 full groups; intermediate 6144: 384 gate|up tiles, so half
+    the workgroups take two, and down chunks of 64 pairs), hidden 1536 (24
+    pairs, 6 groups) with intermediate 4160 (65 pairs: a last down chunk of
+    one pair), and hidden 1056 (33 blocks: 17 pairs, the last a single
+    block, 5 groups, the last partial) with intermediate 2720.  2 layers,
+    vocab 4096, 100-token prompt, 60 greedy tokens at positions 100..159
+    (3 segments): tokens equal the oracle's and the graph path's, with the
+    segments combined in the o items or in the newest segment's item."""
+    cfg = lq8.Qwen3Config(vocab_size=4096, hidden_size=hidden, intermediate_size=inter, num_hidden_layers=2,
+                          num_attention_heads=heads, num_key_value_heads=kv, head_dim=128, max_position_embeddings=256)
+    assert lq8.persist_plan(cfg, 256)["supported"]
+    tensors = varied_small(cfg, hidden + heads)
+    prompt = np.random.default_rng(hidden).integers(0, cfg.vocab_size, 100).astype(np.uint32)
+    env = {"LQ8_PERSIST_CDIR": "0"} if combine == "combiner" else None
+    persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 60, env=env)
+
+
+def test_qwen3_1_7b_greedy(ctx):
+    """Qwen3-1.7B shapes at full size (28 layers, hidden 2048, intermediate
+    6144, 16 / 8 heads, vocab 151936), random Q8_0 weights with the decoder
+    layers at N(0, 0.08) so that the tokens vary: 64 prompt ids and 64
+    greedy tokens on the persistent kernel (its hidden-2048 instance) and on
+    the replayed graph, both identical to the oracle's; one decode step's
+    logits bit-identical."""
+    cfg = lq8.Qwen3Config(vocab_size=151936, hidden_size=2048, intermediate_size=6144, num_hidden_layers=28,
+                          num_attention_heads=16, num_key_value_heads=8, head_dim=128, max_position_embeddings=256)
+    base = lq8.Qwen3ForCausalLM.random(ctx, cfg, seed=17)
+    tensors = varied_0_6b_tensors(base.export_all(), cfg)
+    base.free()
+    model = lq8.Qwen3ForCausalLM.load(ctx, cfg, tensors)
+    ref = oracle.Model(cfg, tensors)
+    prompt = np.random.default_rng(17).integers(0, cfg.vocab_size, 64).astype(np.uint32)
+    ptoks, pst = with_path("persistent", lambda: model.generate_greedy(prompt, 64))
+    gtoks, gst = with_path("graph", lambda: model.generate_greedy(prompt, 64))
+    ref_toks, margins = ref.generate_greedy(prompt, 64)
+    print(f"\nQwen3-1.7B shapes: persistent {pst}; graph {gst}; distinct tokens {len(set(ref_toks.tolist()))}; "
+          f"min top-2 margin {float(margins.min()):.3g}")
+    assert pst["used_persistent"] and gst["used_graph"]
+    assert ptoks.tolist() == ref_toks.tolist()
+    assert gtoks.tolist() == ref_toks.tolist()
+    assert len(set(ref_toks.tolist())) >= 8
+    model.clear_kv_cache()
+    ref.clear_kv_cache()
+    assert same_bits(model.forward(prompt, 0), ref.forward(prompt, 0))
+    lg, lr = model.forward([int(ptoks[0])], 64), ref.forward([int(ptoks[0])], 64)
+    assert same_bits(lg, lr), f"decode step: max|d| {np.max(np.abs(lg - lr))}"
+    model.free()
+    ref.close()
+
+
 def expected_picks(logits, P, pw=8):
     """Each workgroup's pick over its lm_head rows: rows of the 16-row tiles t
     with (t // pw) % P == w; the largest value, the last index on ties."""

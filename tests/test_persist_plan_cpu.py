@@ -6,12 +6,13 @@ shapes outside the kernel's stated limits must be refused.
 
 The capacities below are facts of csrc/decode_persistent.hip, written out
 here as numbers: 512 threads (8 waves) per workgroup; a hidden-vector gather
-of 16 words per thread; a down-input fetch of 9 words per thread; the
+of 16 words per thread (12 in the instance for hidden above 1024); a down-input fetch of 9 words per thread; the
 attention output chunk of the o projection 4 words per thread; an attention
 item's q, k, v 5 words per thread; the picks 4 words per thread; a segment
-combine's (m_c, l_c) batch 4 words per thread; block pairs per wave group 2
-(hidden-long tiles and o chunks) or 1, 2, 4, 8 (down chunks); at most 8 input
-chunks per projection; LDS at most 64 KiB."""
+combine's (m_c, l_c) batch 4 words per thread; block pairs per wave group
+of hidden-long tiles and o chunks 2 (hidden <= 1024) or 4 (hidden <= 2048,
+the second kernel instance), of down chunks 1, 2, 4, 8; at most 8 input
+chunks per projection (2 in the second instance); LDS at most 64 KiB."""
 import itertools
 
 import pytest
@@ -32,29 +33,32 @@ def check_plan(c, P, p):
     """The kernel's assumptions about an accepted plan."""
     H, I, NH, NKV = c.hidden_size, c.intermediate_size, c.num_attention_heads, c.num_key_value_heads
     G = NH // NKV
+    hc = 2 if H <= 1024 else 4  # block pairs per wave group of the instance
+    nw, nchm = (16, 8) if hc == 2 else (12, 2)  # gather words per thread, chunk sums joined
     QD = NH * 128
     nbQ, npH, npI, TH = QD // 32, (H // 32 + 1) // 2, (I // 32 + 1) // 2, H // 16
     csO, nchO = p["o_chunk_blocks"], p["o_chunks"]
     csD, nchD = p["down_chunk_pairs"], p["down_chunks"]
     # o chunks: a power of two of blocks; the chunks cover the input exactly
-    # once; each is at most 16 pairs (one 2-pair group per wave); <= 8 chunk
+    # once; each is at most hc * 8 pairs (one hc-pair group per wave); <= 8 chunk
     # sums per row; their items fit the workgroups unless one chunk holds all
     # or the chunks are the widest (32 blocks)
     assert csO >= 2 and csO & (csO - 1) == 0
-    assert nchO == -(-nbQ // csO) and nchO <= 8
+    assert nchO == -(-nbQ // csO) and nchO <= nchm
     pairsO = (min(csO, nbQ) + 1) // 2
-    assert pairsO <= 2 * PW
+    assert pairsO <= hc * PW
     assert TH * nchO <= P or nchO == 1 or csO == 32
     # down chunks: 8, 16, 32 or 64 pairs (1, 2, 4, 8 per wave); <= 8 chunks;
     # a chunk's input is one fetch of <= 9 words per thread
     assert csD in (8, 16, 32, 64)
-    assert nchD == -(-npI // csD) and nchD <= 8
+    assert nchD == -(-npI // csD) and nchD <= nchm
     assert min(csD, npI) * 64 <= 9 * PT
     assert TH * nchD <= P or nchD == 1
     # gathers: h and the o chunk sums (P4); h2 and the down chunk sums (P1, P6)
-    assert (1 + nchO) * H <= 16 * PT and (1 + nchD) * H <= 16 * PT
-    # hidden-long tiles: <= 16 pairs, one 2-pair group per wave
-    assert npH <= 2 * PW
+    assert (1 + nchO) * H <= nw * PT and (1 + nchD) * H <= nw * PT
+    # hidden-long tiles: <= hc * 8 pairs, one hc-pair group per wave; a
+    # hidden vector is hc words per thread
+    assert npH <= hc * PW and H <= hc * PT
     # the P3 fetch of an o chunk's attention output, an attention item's
     # q, k, v, the picks, a combine batch
     assert min(csO, nbQ) * 32 <= 4 * PT
@@ -89,8 +93,8 @@ def check_plan(c, P, p):
     assert lds <= 64 * 1024
 
 
-HIDDEN = (32, 64, 96, 128, 224, 256, 320, 512, 768, 1024)
-INTER = (32, 64, 352, 512, 768, 1568, 3072, 4096)
+HIDDEN = (32, 64, 96, 128, 224, 256, 320, 512, 768, 1024, 1056, 1536, 2048)
+INTER = (32, 64, 352, 512, 768, 1568, 3072, 4096, 6144, 8192)
 HEADS = ((1, 1), (2, 1), (4, 2), (8, 1), (8, 8), (12, 4), (16, 8), (16, 1), (16, 16))
 WGS = (1, 8, 32, 48, 64, 100, 128, 160, 192, 200, 255, 256, 304, 512, 1024)
 
@@ -103,7 +107,8 @@ def test_accepted_plans_fit_the_kernel():
         if p["supported"]:
             check_plan(c, P, p)
             accepted += 1
-    # most of the sweep is inside the limits (hidden <= 1024, inter <= 4096)
+    # most of the sweep is inside the limits (hidden <= 2048, a down chunk of
+    # at most 64 pairs)
     assert accepted > 0.8 * len(HIDDEN) * len(INTER) * len(HEADS) * len(WGS)
 
 
@@ -141,6 +146,19 @@ def test_advisor_layouts_fit():
         check_plan(c, P, p)
 
 
+def test_qwen3_1_7b_plan():
+    """Qwen3-1.7B (hidden 2048, intermediate 6144, 16 / 8 heads) on 256
+    workgroups: the hidden-2048 instance (4 pairs per wave group), o chunks
+    of 32 blocks (2, 8 heads each), down chunks of 64 pairs (2, 8 pairs per
+    wave); the o items combine up to 7 segments themselves."""
+    c = cfg(2048, 6144, 16, 8, max_pos=40960)
+    p = lq8.persist_plan(c, 256)
+    assert p["supported"]
+    assert (p["o_chunk_blocks"], p["o_chunks"], p["down_chunk_pairs"], p["down_chunks"]) == (32, 2, 64, 2)
+    assert p["direct_segments"] == 7
+    check_plan(c, 256, p)
+
+
 @pytest.mark.parametrize("max_pos", [1, 64, 512, 513, 4096, 40960, 131072])
 def test_positions_do_not_limit_the_kernel(max_pos):
     """The segment combine runs once per kv head and streams any number of
@@ -152,8 +170,8 @@ def test_positions_do_not_limit_the_kernel(max_pos):
 
 
 @pytest.mark.parametrize("H,I,NH,NKV,hd", [
-    (1056, 3072, 16, 8, 128),   # hidden above 1024
-    (1024, 4128, 16, 8, 128),   # intermediate above 4096
+    (2080, 6144, 16, 8, 128),   # hidden above 2048
+    (2048, 8256, 16, 8, 128),   # a down chunk above 64 pairs (8 per wave)
     (1024, 3072, 32, 4, 128),   # 32 heads: attention output above 2048
     (1040, 3072, 16, 8, 128),   # hidden not a multiple of 32
     (1024, 3072, 16, 8, 64),    # head_dim 64
