@@ -260,7 +260,7 @@ __device__ __forceinline__ void put_act_half(int8_t* __restrict__ codes, uint32_
 
 __global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ x, int m, int k, int waves, int np8,
                                                       int8_t* __restrict__ codes, uint32_t* __restrict__ xs) {
-    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (gw >= waves) return;
     const int lane = threadIdx.x & 63;
     const int tile = gw / np8, p = gw - tile * np8;
@@ -1060,7 +1060,9 @@ lq8_status launch_quantize_act(hipStream_t s, const float* x, int m, int k, int8
     const int groups = (k / 32 + GEMM_GROUP - 1) / GEMM_GROUP;
     const size_t waves = (size_t)((m + 31) / 32) * 2 * (4 * groups);
     if (!waves) return LQ8_OK;
-    hipLaunchKernelGGL(k_quantize_act, dim3(grid1(waves, 4)), dim3(256), 0, s, x, m, k, (int)waves, 4 * groups,
+    // two waves per workgroup: at M = 512 the gate/up and down operands end
+    // to end 12.20 -> 12.09 and 13.89 -> 13.41 us against four
+    hipLaunchKernelGGL(k_quantize_act, dim3(grid1(waves, 2)), dim3(128), 0, s, x, m, k, (int)waves, 4 * groups,
                        codes, scales);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
