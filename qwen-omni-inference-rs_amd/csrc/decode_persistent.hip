@@ -258,7 +258,9 @@ __device__ __forceinline__ float dot16_pinned(u32x4 c, const float* __restrict__
 
 // N chunk dots at once: N of the GEMV's 16-term fmaf chains (each in its
 // order, from +0, as dot16), interleaved step by step so that the dependent
-// chains overlap (one chain alone waits on each fma's latency).
+// chains overlap (one chain alone waits on each fma's latency).  LEAN: a
+// scheduling barrier before each step's input reads, so that the compiler
+// does not hoist all 4 N of them (for the register-bound instances).
 template <int N, bool LEAN = false>
 __device__ __forceinline__ void dot16xN(const u32x4* c, const float* const* x, float* out) {
     uint32_t w[N][4];
