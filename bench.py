@@ -15,7 +15,8 @@ launch per GEMV replayed from a HIP graph, the lm_head alone, the single
 random-init Q8_0 Qwen3-0.6B (128-token prompt, 128 new tokens; greedy, and
 sampled with temperature 0.8, top-k 50, top-p 0.95, repetition penalty 1.1)
 are reported beside it (greedy decode on its default path, the persistent
-kernel, and on the replayed graph), and so is the host-pointer
+kernel, and on the replayed graph; the same greedy decode at Qwen3-1.7B and
+Qwen3-4B shapes, random weights), and so is the host-pointer
 Linear::forward per call at the seven layer shapes.  The CPU
 baseline is a C restatement of the reference's own CPU Linear::forward (BF16
 weight, per-call transpose, BF16 -> F32 copy, naive matmul_2d) timed on one
@@ -283,7 +284,9 @@ def decode_larger(ctx, cfg, label):
     tps = sorted(st["decode_tokens_per_s"] for _, st in runs)[1]
     gtps = sorted(st["decode_tokens_per_s"] for _, st in gruns)[1]
     st0 = runs[0][1]
-    out = {"tokens_per_s": round(tps, 1),
+    H, I, QD, KD = cfg.hidden_size, cfg.intermediate_size, cfg.num_attention_heads * 128, cfg.num_key_value_heads * 128
+    wbytes = (cfg.num_hidden_layers * ((QD + 2 * KD) * H + H * QD + 3 * I * H) + cfg.vocab_size * H) * 34 // 32
+    out = {"tokens_per_s": round(tps, 1), "weight_bytes_per_token": wbytes, "weight_gbs": round(wbytes * tps / 1e9, 1),
            "path": "persistent" if st0["used_persistent"] else ("graph" if st0["used_graph"] else "plain"),
            "graph_tokens_per_s": round(gtps, 1),
            "tokens_agree": all(np.array_equal(t, runs[0][0]) for t, _ in runs + gruns),
@@ -612,6 +615,7 @@ def main():
             cpu_model = (cfg, model.export_all(), prompt)
         model.free()
         decode["qwen3_1_7b"] = decode_larger(ctx, lq8.qwen3_1_7b(max_positions=512), "Qwen3-1.7B")
+        decode["qwen3_4b"] = decode_larger(ctx, lq8.qwen3_4b(max_positions=512), "Qwen3-4B")
 
     moe = None if args.no_moe else moe_stack(ctx)
     ctx.close()

@@ -471,6 +471,14 @@ def qwen3_1_7b(max_positions: int = 4096) -> Qwen3Config:
     return Qwen3Config(hidden_size=2048, intermediate_size=6144, max_position_embeddings=max_positions)
 
 
+def qwen3_4b(max_positions: int = 4096) -> Qwen3Config:
+    """Qwen3-4B's shapes (its config.json): hidden 2560, intermediate 9728,
+    36 layers, 32 query and 8 kv heads of 128, vocab 151936, tied embedding;
+    the other fields as Qwen3-0.6B's."""
+    return Qwen3Config(hidden_size=2560, intermediate_size=9728, num_hidden_layers=36, num_attention_heads=32,
+                       num_key_value_heads=8, max_position_embeddings=max_positions)
+
+
 class Qwen3ForCausalLM:
     """src/model.rs:245-398 on Q8_0 weights."""
 

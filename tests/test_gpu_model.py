@@ -506,6 +506,33 @@ def test_qwen3_1_7b_greedy(ctx):
     ref.close()
 
 
+def test_qwen3_4b_layer_widths_graph_path(ctx):
+    """Qwen3-4B layer widths (hidden 2560, intermediate 9728, 32 query and 8
+    kv heads; 2 layers, vocab 4096): outside the persistent kernel (hidden
+    above 2048), so greedy decode runs the per-step kernels replayed as a
+    graph; 100 prompt ids and 48 greedy tokens identical to the oracle's,
+    and a KV-cached decode step's logits bit-identical."""
+    cfg = lq8.Qwen3Config(vocab_size=4096, hidden_size=2560, intermediate_size=9728, num_hidden_layers=2,
+                          num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=256)
+    assert not lq8.persist_plan(cfg, 256)["supported"]
+    tensors = varied_small(cfg, 2560)
+    model = lq8.Qwen3ForCausalLM.load(ctx, cfg, tensors)
+    ref = oracle.Model(cfg, tensors)
+    prompt = np.random.default_rng(2560).integers(0, cfg.vocab_size, 100).astype(np.uint32)
+    toks, st = model.generate_greedy(prompt, 48)
+    ref_toks, _ = ref.generate_greedy(prompt, 48)
+    assert st["used_graph"] and not st["used_persistent"]
+    assert toks.tolist() == ref_toks.tolist()
+    assert len(set(ref_toks.tolist())) > 4, "the tokens should vary"
+    model.clear_kv_cache()
+    ref.clear_kv_cache()
+    assert same_bits(model.forward(prompt, 0), ref.forward(prompt, 0))
+    lg, lr = model.forward([int(toks[0])], 100), ref.forward([int(toks[0])], 100)
+    assert same_bits(lg, lr), f"decode step: max|d| {np.max(np.abs(lg - lr))}"
+    model.free()
+    ref.close()
+
+
 def expected_picks(logits, P, pw=8):
     """Each workgroup's pick over its lm_head rows: rows of the 16-row tiles t
     with (t // pw) % P == w; the largest value, the last index on ties."""
