@@ -1401,16 +1401,18 @@ bool persist_layout(const PersistShape& s, int P, PersistLayout* out) {
     const int nchm = hc == 4 ? NCH4 : PERSIST_NCH;       // chunk sums one element joins, at most
     // o input chunks: the smallest power-of-two block count whose items fit
     // the workgroups (or one chunk over the whole input, or the widest chunk
-    // a workgroup's waves hold: then a workgroup takes several items)
+    // a workgroup's waves hold: then a workgroup takes several items).  A
+    // chunk covers at most PW heads (4 PW blocks): P3's own segment combine
+    // runs one wave per head of the chunk.
     int csO = 2;
     auto nch_of = [&](int cs) { return (nbQ + cs - 1) / cs; };
-    while (csO < nbQ && csO < 2 * hc * PW &&
+    while (csO < nbQ && csO < std::min(2 * hc * PW, 4 * PW) &&
            (TH * nch_of(csO) > P || nch_of(csO) > nchm || (1 + nch_of(csO)) * s.H > cap))
         csO *= 2;
     const int nchO = nch_of(csO);
     const int pairsO = (std::min(csO, nbQ) + 1) / 2;  // pairs of the widest o chunk
     // P4 gathers h and the o chunk sums; a chunk's pairs are one group per wave
-    if (nchO > nchm || (1 + nchO) * s.H > cap || pairsO > hc * PW) return false;
+    if (nchO > nchm || (1 + nchO) * s.H > cap || pairsO > hc * PW || std::min(csO, nbQ) > 4 * PW) return false;
     // down input chunks: the smallest power-of-two pair count, at least one
     // pair per wave, whose (tile, chunk) items fit the workgroups (or one
     // chunk over the whole input)

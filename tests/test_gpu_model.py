@@ -473,6 +473,27 @@ def test_persistent_hidden_above_1024(ctx, hidden, inter, heads, kv, combine):
     persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 60, env=env)
 
 
+@pytest.mark.parametrize("combine", ["direct", "combiner"])
+@pytest.mark.parametrize("wg", [128, 64])
+def test_persistent_hidden_2048_other_workgroup_counts(ctx, wg, combine):
+    """The hidden-2048 instance on fewer workgroups (LQ8_PERSIST_WG): hidden
+    2048, intermediate 4096, 16 / 8 heads, so every workgroup takes 2 (128)
+    or 4 (64) q|k|v tiles, gate|up tile pairs and o items (two 32-block
+    chunks, 8 heads' partials per item), reloading the weights of each item
+    after the first, and one 64-pair down chunk; tokens equal the oracle's
+    and the graph path's, both combine paths."""
+    cfg = lq8.Qwen3Config(vocab_size=4096, hidden_size=2048, intermediate_size=4096, num_hidden_layers=2,
+                          num_attention_heads=16, num_key_value_heads=8, head_dim=128, max_position_embeddings=256)
+    plan = lq8.persist_plan(cfg, wg)
+    assert plan["supported"] and plan["o_chunk_blocks"] == 32 and plan["down_chunk_pairs"] == 64
+    tensors = varied_small(cfg, 300 + wg)
+    prompt = np.random.default_rng(wg + 1).integers(0, cfg.vocab_size, 100).astype(np.uint32)
+    env = {"LQ8_PERSIST_WG": str(wg)}
+    if combine == "combiner":
+        env["LQ8_PERSIST_CDIR"] = "0"
+    persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 60, env=env)
+
+
 def test_qwen3_1_7b_greedy(ctx):
     """Qwen3-1.7B shapes at full size (28 layers, hidden 2048, intermediate
     6144, 16 / 8 heads, vocab 151936), random Q8_0 weights with the decoder

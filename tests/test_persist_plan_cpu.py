@@ -47,6 +47,7 @@ def check_plan(c, P, p):
     assert nchO == -(-nbQ // csO) and nchO <= nchm
     pairsO = (min(csO, nbQ) + 1) // 2
     assert pairsO <= hc * PW
+    assert min(csO, nbQ) <= 4 * PW  # at most PW heads: P3's combine runs one wave per head
     assert TH * nchO <= P or nchO == 1 or csO == 32
     # down chunks: 8, 16, 32 or 64 pairs (1, 2, 4, 8 per wave); <= 8 chunks;
     # a chunk's input is one fetch of <= 9 words per thread
