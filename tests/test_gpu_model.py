@@ -494,6 +494,20 @@ def test_persistent_hidden_2048_other_workgroup_counts(ctx, wg, combine):
     persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 60, env=env)
 
 
+def test_persistent_hidden_2048_across_the_direct_combine_limit(ctx):
+    """Hidden 2048 (16 heads: the o items combine at most 7 segments, 448
+    positions, themselves): a 420-token prompt and 60 greedy tokens, so one
+    generate() runs the steps below position 448 on the kernel instance
+    without the combining items and the rest on the one with them (7 and 8
+    segments).  Tokens equal the oracle's and the graph path's."""
+    cfg = lq8.Qwen3Config(vocab_size=4096, hidden_size=2048, intermediate_size=4096, num_hidden_layers=2,
+                          num_attention_heads=16, num_key_value_heads=8, head_dim=128, max_position_embeddings=512)
+    assert lq8.persist_plan(cfg, 256)["direct_segments"] == 7
+    tensors = varied_small(cfg, 448)
+    prompt = np.random.default_rng(448).integers(0, cfg.vocab_size, 420).astype(np.uint32)
+    persistent_and_graph_equal_oracle(ctx, cfg, tensors, prompt, 60)
+
+
 def test_qwen3_1_7b_greedy(ctx):
     """Qwen3-1.7B shapes at full size (28 layers, hidden 2048, intermediate
     6144, 16 / 8 heads, vocab 151936), random Q8_0 weights with the decoder
