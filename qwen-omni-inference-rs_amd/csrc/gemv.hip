@@ -46,20 +46,40 @@ struct Stage {
     float mcs[CU] = {}, lcs[CU] = {};
     float ov[EA][CU] = {};
     float4 ov4[CU] = {};  // k <= 4 * threads: outputs 4 t .. 4 t + 3 (one head) of the first CU segments
+    float4 pv[4] = {};    // XS_RMSNORM_JOIN: the chunk sums of the thread's first float4
+
+    // XS_RMSNORM_JOIN: base + the pairwise tree over the n (<= 4) chunk sums
+    // p[0 .. n) of 4 consecutive elements (the GEMV block tree's upper levels)
+    static __device__ __forceinline__ float4 join4(float4 base, float4 (&p)[4], int n) {
+#pragma unroll
+        for (int st = 1; st < 4; st *= 2)
+#pragma unroll
+            for (int i = 0; i + st < 4; i += 2 * st)
+                if (i + st < n)
+                    p[i] = make_float4(p[i].x + p[i + st].x, p[i].y + p[i + st].y, p[i].z + p[i + st].z,
+                                       p[i].w + p[i + st].w);
+        return make_float4(base.x + p[0].x, base.y + p[0].y, base.z + p[0].z, base.w + p[0].w);
+    }
 
     // Only waves whose 64 threads reach into the input issue its loads (a
     // wave-uniform condition, so no lane-divergent branch around a load).
     __device__ __forceinline__ void load(const GemvArgs& a, int wave) {
         const int tid = threadIdx.x, nt = blockDim.x, k4 = a.k >> 2;
         const float* __restrict__ x = a.x;
-        if (XS == XS_PLAIN || XS == XS_RMSNORM || XS == XS_SILU) {
+        if (XS == XS_PLAIN || XS == XS_RMSNORM || XS == XS_SILU || XS == XS_RMSNORM_JOIN || XS == XS_SILU_PART) {
 #pragma unroll
             for (int e = 0; e < SP; e++) {
                 if (wave * 64 + e * nt < k4) {
                     const int i4 = min(tid + e * nt, k4 - 1);
                     xv[e] = *(const float4*)(x + 4 * i4);
-                    if (XS == XS_RMSNORM) wv[e] = *(const float4*)(a.norm_w + 4 * i4);
+                    if (XS == XS_RMSNORM || XS == XS_RMSNORM_JOIN) wv[e] = *(const float4*)(a.norm_w + 4 * i4);
                     if (XS == XS_SILU) wv[e] = *(const float4*)(x + a.k + 4 * i4);
+                    if (XS == XS_SILU_PART) wv[e] = *(const float4*)(x + a.xk + 4 * i4);
+                    if (XS == XS_RMSNORM_JOIN && e == 0) {
+#pragma unroll
+                        for (int c = 0; c < 4; c++)
+                            if (c < a.nparts) pv[c] = *(const float4*)(a.parts + (size_t)c * a.k + 4 * i4);
+                    }
                 }
             }
         } else {
@@ -116,8 +136,9 @@ struct Stage {
                 }
             for (int i4 = tid + SP * nt; i4 < k4; i4 += nt) *(float4*)(xs + 4 * i4) = *(const float4*)(x + 4 * i4);
             __syncthreads();
-        } else if (XS == XS_SILU) {
+        } else if (XS == XS_SILU || XS == XS_SILU_PART) {
             // silu(gate) * up (src/mlp.rs:151-164; silu src/tensor.rs:1978)
+            const int uo = XS == XS_SILU ? k : a.xk;  // up's offset from gate
 #pragma unroll
             for (int e = 0; e < SP; e++)
                 if (wave * 64 + e * nt < k4 && tid + e * nt < k4) {
@@ -126,20 +147,49 @@ struct Stage {
                         make_float4(silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w));
                 }
             for (int i4 = tid + SP * nt; i4 < k4; i4 += nt) {
-                const float4 g = *(const float4*)(x + 4 * i4), u = *(const float4*)(x + k + 4 * i4);
+                const float4 g = *(const float4*)(x + 4 * i4), u = *(const float4*)(x + uo + 4 * i4);
                 *(float4*)(xs + 4 * i4) =
                     make_float4(silu_mul(g.x, u.x), silu_mul(g.y, u.y), silu_mul(g.z, u.z), silu_mul(g.w, u.w));
             }
             __syncthreads();
-        } else if (XS == XS_RMSNORM) {
+        } else if (XS == XS_RMSNORM || XS == XS_RMSNORM_JOIN) {
             // RmsNorm (src/rms_norm.rs:143-176): input rounded to bf16; sum of
             // squares in the SUM64 order (lane l adds elements l, l + 64, ... in
             // order; the 64 partials fold at distances 32, 16, 8, 4, 2, 1);
             // inv = 1 / sqrt(sum / k + eps); out = bf16((v * inv) * bf16(w)).
+            // XS_RMSNORM_JOIN: the input is x + the tree over the chunk sums,
+            // stored to h_out by workgroup 0 (the residual of the next steps).
+            if constexpr (XS == XS_RMSNORM_JOIN) {
+                const bool keep = blockIdx.x == 0 && blockIdx.y == 0;
 #pragma unroll
-            for (int e = 0; e < SP; e++)
-                if (wave * 64 + e * nt < k4 && tid + e * nt < k4) *(float4*)(xs + 4 * (tid + e * nt)) = bf16_round4(xv[e]);
-            for (int i4 = tid + SP * nt; i4 < k4; i4 += nt) *(float4*)(xs + 4 * i4) = bf16_round4(*(const float4*)(x + 4 * i4));
+                for (int e = 0; e < SP; e++)
+                    if (wave * 64 + e * nt < k4 && tid + e * nt < k4) {
+                        float4 p[4];
+#pragma unroll
+                        for (int c = 0; c < 4; c++) {
+                            if (e == 0) p[c] = pv[c];
+                            else if (c < a.nparts) p[c] = *(const float4*)(a.parts + (size_t)c * k + 4 * (tid + e * nt));
+                            else p[c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                        }
+                        const float4 v = join4(xv[e], p, a.nparts);
+                        if (keep) *(float4*)(a.h_out + 4 * (tid + e * nt)) = v;
+                        *(float4*)(xs + 4 * (tid + e * nt)) = bf16_round4(v);
+                    }
+                for (int i4 = tid + SP * nt; i4 < k4; i4 += nt) {
+                    float4 p[4];
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        p[c] = c < a.nparts ? *(const float4*)(a.parts + (size_t)c * k + 4 * i4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    const float4 v = join4(*(const float4*)(x + 4 * i4), p, a.nparts);
+                    if (keep) *(float4*)(a.h_out + 4 * i4) = v;
+                    *(float4*)(xs + 4 * i4) = bf16_round4(v);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < SP; e++)
+                    if (wave * 64 + e * nt < k4 && tid + e * nt < k4) *(float4*)(xs + 4 * (tid + e * nt)) = bf16_round4(xv[e]);
+                for (int i4 = tid + SP * nt; i4 < k4; i4 += nt) *(float4*)(xs + 4 * i4) = bf16_round4(*(const float4*)(x + 4 * i4));
+            }
             __syncthreads();
             if (tid < 64) {
                 float acc = 0.0f;
@@ -317,14 +367,18 @@ __device__ __forceinline__ void gemv_tiles(const GemvArgs& a, int tile0, int nti
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar control flow
     const int W = blockDim.x >> 6;
     const int nb = a.k >> 5, np = (nb + 1) >> 1;
+    // EPI_PART: the input is one chunk of the weight's rows, from pair pw0
+    // of npw (the chunk's sums are subtrees of the GEMV block tree)
+    const int npw = EPI == EPI_PART ? a.npw : np;
+    const int pw0 = EPI == EPI_PART ? a.p0 : 0;
     const int G = (np + CH - 1) / CH;
     const int items = ntiles * G;
     float* xs = sm;
     float* gs = sm + np * 64;
     float* red = gs + items * 16;
     const int r = lane & 15, part = lane >> 4, bsel = part >> 1, half = part & 1;
-    const int8_t* cbase = a.codes + (size_t)tile0 * np * CHUNK_BYTES + lane * 16;
-    const uint16_t* sbase = a.scales + (size_t)tile0 * 2 * np * 16 + bsel * 16 + r;
+    const int8_t* cbase = a.codes + ((size_t)tile0 * npw + pw0) * CHUNK_BYTES + lane * 16;
+    const uint16_t* sbase = a.scales + (size_t)tile0 * 2 * npw * 16 + (size_t)pw0 * 32 + bsel * 16 + r;
     Stage<XS> st;
     st.load(a, wave);
     if ((nb & 1) && threadIdx.x < 32) xs[a.k + threadIdx.x] = 0.0f;  // ordered by the staging barriers
@@ -336,7 +390,7 @@ __device__ __forceinline__ void gemv_tiles(const GemvArgs& a, int tile0, int nti
         const int t0 = it0 / G, g0 = it0 - t0 * G;
 #pragma unroll
         for (int i = 0; i < CH; i++) {
-            const int c = t0 * np + min(g0 * CH + i, np - 1);  // chunk of (tile t0, group g0)
+            const int c = t0 * npw + min(g0 * CH + i, np - 1);  // chunk of (tile t0, group g0)
             nv[i] = __builtin_nontemporal_load((const u32x4*)(cbase + (size_t)c * CHUNK_BYTES));
             ns[i] = sbase[(size_t)c * 32];
         }
@@ -352,7 +406,7 @@ __device__ __forceinline__ void gemv_tiles(const GemvArgs& a, int tile0, int nti
             const int tn = (item + W) / G, gn = item + W - tn * G;
 #pragma unroll
             for (int i = 0; i < CH; i++) {
-                const int c = tn * np + min(gn * CH + i, np - 1);
+                const int c = tn * npw + min(gn * CH + i, np - 1);
                 nv[i] = __builtin_nontemporal_load((const u32x4*)(cbase + (size_t)c * CHUNK_BYTES));
                 ns[i] = sbase[(size_t)c * 32];
             }
@@ -429,7 +483,21 @@ __global__ __launch_bounds__(1024) void k_gemv(GemvArgs a, int tpw) {
     extern __shared__ float smem[];
     const int tiles = (a.n + TILE_ROWS - 1) / TILE_ROWS;
     const int tile0 = blockIdx.x * tpw;
-    gemv_tiles<XS, EPI, CH>(a, tile0, min(tpw, tiles - tile0), smem);
+    if constexpr (EPI == EPI_PART) {
+        // chunk blockIdx.y: pairs p0 .. p0 + part_pairs - 1 of the input
+        const int npf = ((a.k >> 5) + 1) >> 1, c = blockIdx.y, p0 = c * a.part_pairs;
+        const int npv = min(a.part_pairs, npf - p0), e0 = 64 * p0;
+        GemvArgs ac = a;
+        ac.x = a.x + e0;
+        ac.k = min(64 * npv, a.k - e0);
+        ac.npw = npf;
+        ac.p0 = p0;
+        ac.xk = a.k;
+        ac.y = a.y + (size_t)c * a.n;
+        gemv_tiles<XS, EPI, CH>(ac, tile0, min(tpw, tiles - tile0), smem);
+    } else {
+        gemv_tiles<XS, EPI, CH>(a, tile0, min(tpw, tiles - tile0), smem);
+    }
 }
 
 __global__ __launch_bounds__(256) void k_gemv_grouped(const GemvProblemDev* __restrict__ probs, int count) {
@@ -1191,7 +1259,10 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__
 
 template <int XS, int EPI>
 lq8_status launch_one(hipStream_t s, const GemvArgs& a) {
-    const int nb = a.k >> 5, np = (nb + 1) >> 1;
+    const int nb = a.k >> 5, npf = (nb + 1) >> 1;
+    // EPI_PART: a workgroup stages one chunk of part_pairs pairs
+    const int np = EPI == EPI_PART ? std::min(npf, a.part_pairs) : npf;
+    const int nch = EPI == EPI_PART ? (npf + a.part_pairs - 1) / a.part_pairs : 1;
     const int tiles = (a.n + TILE_ROWS - 1) / TILE_ROWS;
     // Many tiles (lm_head): 4 pairs per item, 4-wave workgroups with the next
     // item's weights prefetched; a plain input takes one tile per workgroup,
@@ -1213,7 +1284,7 @@ lq8_status launch_one(hipStream_t s, const GemvArgs& a) {
     size_t smem = ((size_t)np * 64 + (size_t)tpw * G * 16 + 4) * sizeof(float);
     if (XS == XS_ATTN) smem += ((size_t)a.attn_cmax * a.attn_heads * 2 + (1 + CU) * a.attn_heads) * sizeof(float);
     if (smem > 64 * 1024) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: input staging exceeds 64 KiB of LDS");
-    const dim3 grid((unsigned)((tiles + tpw - 1) / tpw)), block(64 * waves);
+    const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)nch), block(64 * waves);
     if (ch == 1) hipLaunchKernelGGL((k_gemv<XS, EPI, 1>), grid, block, smem, s, a, tpw);
     else if (ch == 2) hipLaunchKernelGGL((k_gemv<XS, EPI, 2>), grid, block, smem, s, a, tpw);
     else hipLaunchKernelGGL((k_gemv<XS, EPI, 4>), grid, block, smem, s, a, tpw);
@@ -1250,6 +1321,19 @@ lq8_status launch_gemv(hipStream_t s, XSource xs, Epilogue epi, const GemvArgs& 
     if (epi == EPI_ARGMAX && (!a.arg_val || !a.arg_idx)) return fail(LQ8_ERR_INVALID_ARG, "gemv: argmax buffers are null");
     if (xs == XS_ATTN && (a.attn_heads * 128 != a.k || a.attn_cmax <= 0))
         return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: attention input layout does not match k");
+    if (xs == XS_SILU_PART || epi == EPI_PART) {
+        const int pp = a.part_pairs;
+        if (xs != XS_SILU_PART || epi != EPI_PART || pp <= 0 || (pp & (pp - 1)))
+            return fail(LQ8_ERR_INVALID_ARG, "gemv: input chunks need the chunked silu input and a power-of-two pair count");
+        return launch_one<XS_SILU_PART, EPI_PART>(s, a);
+    }
+    if (xs == XS_RMSNORM_JOIN) {
+        if (!a.parts || a.nparts < 1 || a.nparts > 4 || !a.h_out || !a.norm_w)
+            return fail(LQ8_ERR_INVALID_ARG, "gemv: the join needs 1 to 4 chunk-sum vectors, h_out and the norm weight");
+        if (epi == EPI_STORE) return launch_one<XS_RMSNORM_JOIN, EPI_STORE>(s, a);
+        if (epi == EPI_ARGMAX) return launch_one<XS_RMSNORM_JOIN, EPI_ARGMAX>(s, a);
+        return fail(LQ8_ERR_INVALID_ARG, "gemv: the join stages a plain or argmax GEMV only");
+    }
     switch (xs) {
         case XS_PLAIN: return launch_epi<XS_PLAIN>(s, epi, a);
         case XS_RMSNORM: return launch_epi<XS_RMSNORM>(s, epi, a);

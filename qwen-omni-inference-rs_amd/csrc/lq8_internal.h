@@ -91,13 +91,26 @@ lq8_status ctx_scratch(lq8_ctx* ctx, size_t bytes, void** out);
 // Input x of a GEMV: plain f32 vector, RmsNorm of a hidden vector,
 // silu(gate) * up of a concatenated [gate | up] vector, or the attention
 // output combined from per-segment partials (x = partials, see AttnSegLaunch).
-enum XSource : int { XS_PLAIN = 0, XS_RMSNORM = 1, XS_SILU = 2, XS_ATTN = 3 };
+enum XSource : int {
+    XS_PLAIN = 0, XS_RMSNORM = 1, XS_SILU = 2, XS_ATTN = 3,
+    // RMSNorm of x + the pairwise tree over nparts chunk sums (the input of
+    // a GEMV whose producer wrote chunk sums, EPI_PART); workgroup 0 stores
+    // the joined vector to h_out
+    XS_RMSNORM_JOIN = 4,
+    // silu(gate) * up over one input chunk (EPI_PART): gate at x, up at x + xk
+    XS_SILU_PART = 5
+};
 // Output: y = W x, y = resid + W x, or y = W x plus the per-tile argmax
 // (value, index; last index on ties) of the logits.
 // EPI_SWIGLU (multi-vector GEMV only): rows = [gate | up] halves; the
 // workgroup of gate tile i also runs up tile i and stores silu(gate) * up
 // (rows / 2 outputs per vector).
-enum Epilogue : int { EPI_STORE = 0, EPI_RESID = 1, EPI_ARGMAX = 2, EPI_SWIGLU = 3 };
+enum Epilogue : int {
+    EPI_STORE = 0, EPI_RESID = 1, EPI_ARGMAX = 2, EPI_SWIGLU = 3,
+    // input chunks of part_pairs block pairs (a power of two; workgroup
+    // column blockIdx.y = chunk): y[chunk * n + row] receives the chunk sums
+    EPI_PART = 4
+};
 
 struct GemvArgs {
     const int8_t* codes;
@@ -113,6 +126,16 @@ struct GemvArgs {
     // XS_ATTN: position (device scalar or base), heads, partial rows per segment capacity
     const int* d_pos = nullptr;
     int pos_base = 0, attn_heads = 0, attn_cmax = 0;
+    // EPI_PART: pairs per input chunk (the launch has ceil(pairs / part_pairs) chunks)
+    int part_pairs = 0;
+    // XS_RMSNORM_JOIN: parts[nparts][k] chunk sums added to x by the pairwise
+    // tree; h_out[k] receives x + that sum
+    const float* parts = nullptr;
+    int nparts = 0;
+    float* h_out = nullptr;
+    // set by the kernel for a chunk: pairs per weight row, the chunk's first
+    // pair, the offset of up from gate (XS_SILU_PART)
+    int npw = 0, p0 = 0, xk = 0;
 };
 lq8_status launch_gemv(hipStream_t s, XSource xs, Epilogue epi, const GemvArgs& a);
 

@@ -46,6 +46,11 @@ struct lq8_model {
     size_t kv_len = 0;
     // single-position buffers
     float *h = nullptr, *h2 = nullptr, *qkv = nullptr, *gu = nullptr, *apart = nullptr, *logits = nullptr;
+    // decode's down projection in input chunks of down_cs pairs (down_nch >= 2
+    // of them; 0: whole rows): dpart[down_nch][hidden] holds the chunk sums,
+    // which the next RMSNorm GEMV joins with the residual
+    float* dpart = nullptr;
+    int down_cs = 0, down_nch = 0;
     float* arg_val = nullptr;
     int* arg_idx = nullptr;
     uint32_t* d_ids = nullptr;
@@ -133,7 +138,7 @@ void release(lq8_model* m) {
         F(L.in_norm); F(L.post_norm); F(L.q_norm); F(L.k_norm);
     }
     F(m->cos_t); F(m->sin_t); F(m->kc); F(m->vc);
-    F(m->h); F(m->h2); F(m->qkv); F(m->gu); F(m->apart); F(m->logits); F(m->arg_val); F(m->arg_idx);
+    F(m->h); F(m->h2); F(m->qkv); F(m->gu); F(m->apart); F(m->logits); F(m->arg_val); F(m->arg_idx); F(m->dpart);
     F(m->d_ids); F(m->d_pos); F(m->d_step); F(m->d_tok); F(m->d_tokens);
     F(m->P_h); F(m->P_x); F(m->P_qkv); F(m->P_qr); F(m->P_attn); F(m->P_gu); F(m->P_xs); F(m->P_xq);
     F(m->d_scfg); F(m->d_counts); F(m->s_work);
@@ -186,8 +191,22 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_qwen3_config* c, lq8_model* m)
         (st = dalloc(&m->gu, 2 * I)) || (st = dalloc(&m->apart, (size_t)m->cmax * c->num_heads * ATT_PART_STRIDE)) ||
         (st = dalloc(&m->logits, c->vocab_size)) || (st = dalloc(&m->arg_val, m->embed->tiles)) ||
         (st = dalloc(&m->arg_idx, m->embed->tiles)) || (st = dalloc(&m->d_pos, 1)) || (st = dalloc(&m->d_step, 1)) ||
-        (st = dalloc(&m->d_tok, 1)))
+        (st = dalloc(&m->d_tok, 1)) || (st = dalloc(&m->dpart, 4 * (size_t)Hd)))
         return st;
+    {
+        // the down projection's 16-row tiles leave compute units idle: input
+        // chunks (an aligned power-of-two pair count, at most 4 of them) put
+        // (tile, chunk) items on them
+        const int tilesH = Hd / TILE_ROWS, npI = (int)((I / 32 + 1) / 2);
+        if (tilesH < m->ctx->num_cus && npI > 8) {
+            int cs = 8;
+            while ((npI + cs - 1) / cs > 4) cs *= 2;
+            if ((npI + cs - 1) / cs >= 2) {
+                m->down_cs = cs;
+                m->down_nch = (npI + cs - 1) / cs;
+            }
+        }
+    }
     LQ8_HIP(hipEventCreate(&m->e0));
     LQ8_HIP(hipEventCreate(&m->e1));
     LQ8_HIP(hipEventCreate(&m->e2));
@@ -291,15 +310,27 @@ lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, 
     const size_t layer_kv = (size_t)c.num_kv_heads * c.head_dim * c.max_positions;
     const float scale = 1.0f / std::sqrt((float)c.head_dim);
     lq8_status st;
+    // down in input chunks (not while tracing the layers' outputs, which the
+    // chunk sums would only give one launch later); LQ8_DOWN_CHUNKS=0: whole rows
+    const char* dce = std::getenv("LQ8_DOWN_CHUNKS");
+    const bool chunks = m->down_nch >= 2 && !trace && !(dce && dce[0] == '0');
     if ((st = launch_dequant_rows(s, m->embed, d_id, 0, 1, m->h))) return st;
     if ((st = trace_copy(m, trace, m->h, Hd))) return st;
     for (size_t l = 0; l < m->layers.size(); l++) {
         Layer& L = m->layers[l];
-        // input_layernorm + q|k|v projection (src/transformer.rs:190; src/attention.rs:330-332)
-        GemvArgs g1 = gemv_args(L.qkv, m->h, m->qkv);
+        // input_layernorm + q|k|v projection (src/transformer.rs:190; src/attention.rs:330-332);
+        // after a chunked down projection the layer input h = h2 + its chunk
+        // sums (joined here, in the GEMV block tree, and stored to h)
+        const bool join = chunks && l > 0;
+        GemvArgs g1 = gemv_args(L.qkv, join ? m->h2 : m->h, m->qkv);
         g1.norm_w = L.in_norm;
         g1.eps = c.rms_norm_eps;
-        if ((st = launch_gemv(s, XS_RMSNORM, EPI_STORE, g1))) return st;
+        if (join) {
+            g1.parts = m->dpart;
+            g1.nparts = m->down_nch;
+            g1.h_out = m->h;
+        }
+        if ((st = launch_gemv(s, join ? XS_RMSNORM_JOIN : XS_RMSNORM, EPI_STORE, g1))) return st;
         // q/k norm, RoPE, KV append, attention per segment (src/attention.rs:336-399)
         AttnSegLaunch at{m->qkv, L.q_norm, L.k_norm, m->cos_t, m->sin_t, m->kc + l * layer_kv, m->vc + l * layer_kv,
                          m->apart, d_pos, pos_base, (int)c.num_heads, (int)c.num_kv_heads, (int)c.max_positions,
@@ -318,21 +349,36 @@ lq8_status enqueue_decode(lq8_model* m, const uint32_t* d_id, const int* d_pos, 
         g3.norm_w = L.post_norm;
         g3.eps = c.rms_norm_eps;
         if ((st = launch_gemv(s, XS_RMSNORM, EPI_STORE, g3))) return st;
-        // down(silu(gate) * up) + residual (src/mlp.rs:163; src/transformer.rs:203)
-        GemvArgs g4 = gemv_args(L.down, m->gu, m->h);
-        g4.resid = m->h2;
-        if ((st = launch_gemv(s, XS_SILU, EPI_RESID, g4))) return st;
+        // down(silu(gate) * up) + residual (src/mlp.rs:163; src/transformer.rs:203):
+        // whole rows, or the chunk sums that the next RMSNorm GEMV joins
+        if (chunks) {
+            GemvArgs g4 = gemv_args(L.down, m->gu, m->dpart);
+            g4.part_pairs = m->down_cs;
+            if ((st = launch_gemv(s, XS_SILU_PART, EPI_PART, g4))) return st;
+        } else {
+            GemvArgs g4 = gemv_args(L.down, m->gu, m->h);
+            g4.resid = m->h2;
+            if ((st = launch_gemv(s, XS_SILU, EPI_RESID, g4))) return st;
+        }
         if ((st = trace_copy(m, trace ? trace + (l + 1) * Hd : nullptr, m->h, Hd))) return st;
     }
-    if (final_hidden)
+    if (final_hidden && !chunks)
         LQ8_HIP(hipMemcpyAsync(final_hidden, m->h, Hd * sizeof(float), hipMemcpyDeviceToDevice, s));
     // final norm -> lm_head logits + per-tile argmax (src/model.rs:357-371)
-    GemvArgs g5 = gemv_args(m->embed, m->h, m->logits);
+    GemvArgs g5 = gemv_args(m->embed, chunks ? m->h2 : m->h, m->logits);
     g5.norm_w = m->final_norm;
     g5.eps = c.rms_norm_eps;
     g5.arg_val = m->arg_val;
     g5.arg_idx = m->arg_idx;
-    return launch_gemv(s, XS_RMSNORM, EPI_ARGMAX, g5);
+    if (chunks) {
+        g5.parts = m->dpart;
+        g5.nparts = m->down_nch;
+        g5.h_out = m->h;
+    }
+    if ((st = launch_gemv(s, chunks ? XS_RMSNORM_JOIN : XS_RMSNORM, EPI_ARGMAX, g5))) return st;
+    if (final_hidden && chunks)
+        LQ8_HIP(hipMemcpyAsync(final_hidden, m->h, Hd * sizeof(float), hipMemcpyDeviceToDevice, s));
+    return LQ8_OK;
 }
 
 lq8_status quant_gemm(lq8_model* m, const float* x, int n, const lq8_weight* w, float* y, const float* resid) {

@@ -568,6 +568,49 @@ def test_qwen3_4b_layer_widths_graph_path(ctx):
     ref.close()
 
 
+@pytest.mark.parametrize("hidden,inter", [
+    (256, 768),    # 12 input pairs of down: 2 chunks of 8
+    (512, 1568),   # 49 blocks, 25 pairs: 4 chunks of 8, the last one pair of one block
+    (256, 4096),   # 64 pairs: 4 chunks of 16
+    (1024, 3072),  # Qwen3-0.6B widths: 3 chunks of 16
+    (128, 352),    # 6 pairs: whole rows
+])
+def test_graph_path_down_chunks(ctx, hidden, inter):
+    """The per-step kernels' down projection in input chunks (their sums
+    joined with the residual by the next layer's RMSNorm GEMV and by the
+    lm_head's): a KV-cached decode step's logits bit-identical to the
+    oracle's and to the whole-row down's (LQ8_DOWN_CHUNKS=0), and greedy
+    tokens of the replayed graph equal to the oracle's."""
+    cfg = lq8.Qwen3Config(vocab_size=2048, hidden_size=hidden, intermediate_size=inter, num_hidden_layers=3,
+                          num_attention_heads=8, num_key_value_heads=2, head_dim=128, max_position_embeddings=128)
+    tensors = varied_small(cfg, hidden + inter)
+    model = lq8.Qwen3ForCausalLM.load(ctx, cfg, tensors)
+    ref = oracle.Model(cfg, tensors)
+    prompt = np.random.default_rng(inter).integers(0, cfg.vocab_size, 30).astype(np.uint32)
+    ref_prefill = ref.forward(prompt, 0)
+    tok = int(np.argmax(ref_prefill))
+    lr = ref.forward([tok], 30)
+    steps = {}
+    for chunks in ("on", "0"):
+        if chunks == "0":
+            os.environ["LQ8_DOWN_CHUNKS"] = "0"
+        try:
+            model.clear_kv_cache()
+            assert same_bits(model.forward(prompt, 0), ref_prefill)
+            steps[chunks] = model.forward([tok], 30)
+        finally:
+            os.environ.pop("LQ8_DOWN_CHUNKS", None)
+    assert same_bits(steps["on"], lr), f"decode step: max|d| {np.max(np.abs(steps['on'] - lr))}"
+    assert same_bits(steps["0"], lr)
+    ref.clear_kv_cache()
+    toks, st = with_path("graph", lambda: model.generate_greedy(prompt, 24))
+    ref_toks, _ = ref.generate_greedy(prompt, 24)
+    assert st["used_graph"]
+    assert toks.tolist() == ref_toks.tolist()
+    model.free()
+    ref.close()
+
+
 def expected_picks(logits, P, pw=8):
     """Each workgroup's pick over its lm_head rows: rows of the 16-row tiles t
     with (t // pw) % P == w; the largest value, the last index on ties."""
