@@ -316,10 +316,12 @@ typedef struct {
  * of 32 whose down-projection split fits (up to 8192 at hidden 2048 on 256
  * workgroups, Qwen3-1.7B's 6144 included), num_heads * 128 <= 2048,
  * num_heads / num_kv_heads <= 16, and a device with cooperative launch;
- * max_positions is not limited.  lq8_persist_plan tells in advance; the
- * environment variable LQ8_PERSIST=0 turns it off.  Other shapes run one
- * kernel sequence per step, replayed as a HIP graph (lq8_gen_stats tells
- * which ran).  Both give the same tokens, bit for bit the same logits.
+ * max_positions is not limited.  lq8_persist_plan tells in advance.  By
+ * default the kernel runs up to hidden_size 1024 (above, the per-step
+ * kernels are faster); the environment variable LQ8_PERSIST=1 runs it
+ * wherever the shape fits, LQ8_PERSIST=0 never.  Otherwise one kernel
+ * sequence per step runs, replayed as a HIP graph (lq8_gen_stats tells which
+ * ran).  Both give the same tokens, bit for bit the same logits.
  * Each decode step forwards the token generated last.  The reference's loop
  * as written does not: the `let next_token` in its loop body
  * (src/generate.rs:650) shadows the binding of src/generate.rs:632 only for

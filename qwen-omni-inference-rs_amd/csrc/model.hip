@@ -195,13 +195,17 @@ lq8_status build_skeleton(lq8_ctx* ctx, const lq8_qwen3_config* c, lq8_model* m)
         return st;
     {
         // the down projection's 16-row tiles leave compute units idle: input
-        // chunks (an aligned power-of-two pair count, at most 4 of them) put
-        // (tile, chunk) items on them
-        const int tilesH = Hd / TILE_ROWS, npI = (int)((I / 32 + 1) / 2);
-        if (tilesH < m->ctx->num_cus && npI > 8) {
+        // chunks (an aligned power-of-two pair count of at most 128, at most 4
+        // chunks) put (tile, chunk) workgroups on them -- the fewest chunks
+        // that still give every CU one (each chunk sum is one more vector for
+        // the joining GEMV to read): Qwen3-0.6B 3 chunks of 16 pairs, 1.7B 2
+        // of 64, 4B 2 of 128
+        const int tilesH = Hd / TILE_ROWS, npI = (int)((I / 32 + 1) / 2), ncu = m->ctx->num_cus;
+        if (tilesH < ncu && npI > 8) {
             int cs = 8;
             while ((npI + cs - 1) / cs > 4) cs *= 2;
-            if ((npI + cs - 1) / cs >= 2) {
+            while (2 * cs <= 128 && 2 * cs < npI && tilesH * ((npI + 2 * cs - 1) / (2 * cs)) >= ncu) cs *= 2;
+            if (cs <= 128 && (npI + cs - 1) / cs >= 2) {
                 m->down_cs = cs;
                 m->down_nch = (npI + cs - 1) / cs;
             }
@@ -562,12 +566,16 @@ int persist_target_wg(const lq8_model* m) {
     return want > 0 && want < P ? want : P;
 }
 
-// Whether greedy decode runs as the persistent kernel: wherever the shape is
-// supported, unless LQ8_PERSIST=0 asks for the per-step kernels (replayed as
-// a graph, or as plain launches under LQ8_NO_GRAPH).
+// Whether greedy decode runs as the persistent kernel: by default where the
+// shape is supported up to hidden 1024 (its first instance; above, the
+// replayed per-step kernels with the down projection in input chunks are
+// faster: Qwen3-1.7B shapes 1037 against 1011 tok/s); LQ8_PERSIST=1 wherever
+// the shape is supported, LQ8_PERSIST=0 never (the per-step kernels,
+// replayed as a graph, or as plain launches under LQ8_NO_GRAPH).
 bool persist_wanted(const lq8_model* m) {
     const char* e = std::getenv("LQ8_PERSIST");
     if (e != nullptr && e[0] == '0') return false;
+    if (!(e != nullptr && e[0] == '1') && m->c.hidden_size > 1024) return false;
     return persist_supported(persist_shape(m), persist_target_wg(m));
 }
 
