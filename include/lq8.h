@@ -264,7 +264,7 @@ lq8_status lq8_persist_trace(lq8_ctx* ctx, uint64_t* out, size_t count);
  * sampling (src/generate.rs:611-664, 153-174). */
 typedef struct {
     uint32_t vocab_size, hidden_size, intermediate_size, num_layers;
-    uint32_t num_heads, num_kv_heads, head_dim, max_positions;
+    uint32_t num_heads, num_kv_heads, head_dim, max_positions; /* max_positions <= 1048576 */
     float rms_norm_eps;
     double rope_theta;
 } lq8_qwen3_config;
@@ -446,7 +446,7 @@ typedef struct lq8_moe lq8_moe;
 typedef struct {
     uint32_t hidden_size, num_heads, num_kv_heads, head_dim;
     uint32_t num_experts, top_k, expert_intermediate_size;
-    uint32_t max_positions; /* KV capacity per sequence */
+    uint32_t max_positions; /* KV capacity per sequence, 1 .. 1048576 */
     uint32_t max_batch;     /* sequences per forward call */
     uint32_t num_layers;
     float rms_norm_eps;

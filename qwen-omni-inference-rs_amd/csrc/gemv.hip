@@ -36,6 +36,7 @@ constexpr int MAX_CH = 4;
 constexpr int MAX_WAVES = 16;
 constexpr int SP = 4;  // input float4s per thread held in registers (the rest load-and-use)
 constexpr int CU = 4;  // attention segments held in registers (256 positions)
+constexpr int ATT_CB = 64;  // attention segments whose combine coefficients are in LDS at once (4096 positions)
 constexpr int EA = 2;  // attention outputs per thread held in registers
 
 // Input staging, split into the loads (issued before the weights) and the
@@ -224,8 +225,8 @@ struct Stage {
             // num = num * a + b * o_c, den = den * a + b * l_c; x = num / den.
             const int H = a.attn_heads;
             const int C = min(max(a.d_pos ? *a.d_pos : a.pos_base, 0) / ATT_SEG + 1, a.attn_cmax);
-            float* coef = red + 4;                     // [C][H][2]
-            float* dens = coef + a.attn_cmax * H * 2;  // [H]
+            float* coef = red + 4;                     // [min(C, ATT_CB)][H][2]
+            float* dens = coef + min(a.attn_cmax, ATT_CB) * H * 2;  // [H]
             if (C <= CU && CU * H <= nt && k <= 4 * nt) {
                 // every partial this thread uses is in its registers: the same
                 // steps with no global load, so that no wait joins them to the
@@ -279,73 +280,84 @@ struct Stage {
                 }
                 __syncthreads();
             } else {
-            for (int h = tid; h < H; h += nt) {
-                float m = -__builtin_huge_valf(), den = 0.0f;
-                for (int c0 = 0; c0 < C; c0 += CU) {
-                    float mc[CU], lc[CU];
+            // batches of ATT_CB segments (the coefficients of one batch in LDS):
+            // each head's running maximum and denominator, and each element's
+            // running numerator (in xs), carry from batch to batch, so the
+            // chain is the one above whatever the number of segments
+            float* mrun = dens + H;  // [H]
+            for (int b0 = 0; b0 < C; b0 += ATT_CB) {
+                const int b1 = min(b0 + ATT_CB, C);
+                for (int h = tid; h < H; h += nt) {
+                    float m = b0 == 0 ? -__builtin_huge_valf() : mrun[h], den = b0 == 0 ? 0.0f : dens[h];
+                    for (int c0 = b0; c0 < b1; c0 += CU) {
+                        float mc[CU], lc[CU];
 #pragma unroll
-                    for (int c = 0; c < CU; c++) {
-                        if (c0 == 0 && h == tid) {
-                            mc[c] = mcs[c];
-                            lc[c] = lcs[c];
-                        } else {
-                            const float* p = x + ((size_t)min(c0 + c, C - 1) * H + h) * ATT_PART_STRIDE;
-                            mc[c] = p[128];
-                            lc[c] = p[129];
-                        }
-                    }
-                    // the running maxima first, then the exps of every segment
-                    // (independent of each other), then the denominator chain
-                    float mp[CU], mn[CU], ea[CU], eb[CU];
-#pragma unroll
-                    for (int c = 0; c < CU; c++) {
-                        mp[c] = m;
-                        if (c0 + c < C) m = m > mc[c] ? m : mc[c];
-                        mn[c] = m;
-                    }
-#pragma unroll
-                    for (int c = 0; c < CU; c++) {
-                        ea[c] = expf_cr(mp[c] - mn[c]);
-                        eb[c] = expf_cr(mc[c] - mn[c]);
-                    }
-#pragma unroll
-                    for (int c = 0; c < CU; c++) {
-                        if (c0 + c < C) {
-                            coef[((c0 + c) * H + h) * 2] = ea[c];
-                            coef[((c0 + c) * H + h) * 2 + 1] = eb[c];
-                            den = den * ea[c] + eb[c] * lc[c];
-                        }
-                    }
-                }
-                dens[h] = den;
-            }
-            __syncthreads();
-            for (int e0 = 0; tid + e0 * nt < k; e0 += EA) {
-#pragma unroll
-                for (int e = 0; e < EA; e++) {
-                    const int i = tid + (e0 + e) * nt;
-                    if (i < k) {
-                        const int h = i >> 7, d = i & 127;
-                        float num = 0.0f;
-                        for (int c0 = 0; c0 < C; c0 += CU) {
-                            float o[CU], ca[CU], cb[CU];
-#pragma unroll
-                            for (int c = 0; c < CU; c++) {
-                                const int cc = min(c0 + c, C - 1);
-                                o[c] = (c0 == 0 && e0 == 0 && k > 4 * nt) ? ov[e][c]
-                                                                          : x[((size_t)cc * H + h) * ATT_PART_STRIDE + d];
-                                ca[c] = coef[(cc * H + h) * 2];  // coefficients read before the chain
-                                cb[c] = coef[(cc * H + h) * 2 + 1];
+                        for (int c = 0; c < CU; c++) {
+                            if (c0 == 0 && h == tid) {
+                                mc[c] = mcs[c];
+                                lc[c] = lcs[c];
+                            } else {
+                                const float* p = x + ((size_t)min(c0 + c, C - 1) * H + h) * ATT_PART_STRIDE;
+                                mc[c] = p[128];
+                                lc[c] = p[129];
                             }
-#pragma unroll
-                            for (int c = 0; c < CU; c++)
-                                if (c0 + c < C) num = num * ca[c] + cb[c] * o[c];
                         }
-                        xs[i] = __fdiv_rn(num, dens[h]);
+                        // the running maxima first, then the exps of every segment
+                        // (independent of each other), then the denominator chain
+                        float mp[CU], mn[CU], ea[CU], eb[CU];
+#pragma unroll
+                        for (int c = 0; c < CU; c++) {
+                            mp[c] = m;
+                            if (c0 + c < b1) m = m > mc[c] ? m : mc[c];
+                            mn[c] = m;
+                        }
+#pragma unroll
+                        for (int c = 0; c < CU; c++) {
+                            ea[c] = expf_cr(mp[c] - mn[c]);
+                            eb[c] = expf_cr(mc[c] - mn[c]);
+                        }
+#pragma unroll
+                        for (int c = 0; c < CU; c++) {
+                            if (c0 + c < b1) {
+                                coef[((c0 - b0 + c) * H + h) * 2] = ea[c];
+                                coef[((c0 - b0 + c) * H + h) * 2 + 1] = eb[c];
+                                den = den * ea[c] + eb[c] * lc[c];
+                            }
+                        }
+                    }
+                    mrun[h] = m;
+                    dens[h] = den;
+                }
+                __syncthreads();
+                const bool last = b1 == C;
+                for (int e0 = 0; tid + e0 * nt < k; e0 += EA) {
+#pragma unroll
+                    for (int e = 0; e < EA; e++) {
+                        const int i = tid + (e0 + e) * nt;
+                        if (i < k) {
+                            const int h = i >> 7, d = i & 127;
+                            float num = b0 == 0 ? 0.0f : xs[i];
+                            for (int c0 = b0; c0 < b1; c0 += CU) {
+                                float o[CU], ca[CU], cb[CU];
+#pragma unroll
+                                for (int c = 0; c < CU; c++) {
+                                    const int cc = min(c0 + c, b1 - 1);
+                                    o[c] = (c0 == 0 && e0 == 0 && k > 4 * nt)
+                                               ? ov[e][c]
+                                               : x[((size_t)cc * H + h) * ATT_PART_STRIDE + d];
+                                    ca[c] = coef[((cc - b0) * H + h) * 2];  // coefficients read before the chain
+                                    cb[c] = coef[((cc - b0) * H + h) * 2 + 1];
+                                }
+#pragma unroll
+                                for (int c = 0; c < CU; c++)
+                                    if (c0 + c < b1) num = num * ca[c] + cb[c] * o[c];
+                            }
+                            xs[i] = last ? __fdiv_rn(num, dens[h]) : num;
+                        }
                     }
                 }
+                __syncthreads();
             }
-            __syncthreads();
             }
         }
     }
@@ -1282,7 +1294,8 @@ lq8_status launch_one(hipStream_t s, const GemvArgs& a) {
     const int G = (np + ch - 1) / ch;
     waves = max(tpw, min(wmax, tpw * G));
     size_t smem = ((size_t)np * 64 + (size_t)tpw * G * 16 + 4) * sizeof(float);
-    if (XS == XS_ATTN) smem += ((size_t)a.attn_cmax * a.attn_heads * 2 + (1 + CU) * a.attn_heads) * sizeof(float);
+    if (XS == XS_ATTN)
+        smem += ((size_t)std::min(a.attn_cmax, ATT_CB) * a.attn_heads * 2 + (1 + CU) * a.attn_heads) * sizeof(float);
     if (smem > 64 * 1024) return fail(LQ8_ERR_SHAPE_MISMATCH, "gemv: input staging exceeds 64 KiB of LDS");
     const dim3 grid((unsigned)((tiles + tpw - 1) / tpw), (unsigned)nch), block(64 * waves);
     if (ch == 1) hipLaunchKernelGGL((k_gemv<XS, EPI, 1>), grid, block, smem, s, a, tpw);

@@ -110,7 +110,9 @@ lq8_status validate(const lq8_qwen3_config* c) {
         return fail(LQ8_ERR_MODEL, "hidden and intermediate sizes must be multiples of 32 (Q8_0 blocks)");
     if (!attention_supported((int)c->num_heads, (int)c->num_kv_heads, (int)c->head_dim))
         return fail(LQ8_ERR_MODEL, "attention needs head_dim 128 and at most 16 query heads per kv head");
-    if (c->max_positions > 8192) return fail(LQ8_ERR_MODEL, "max_positions > 8192 not supported");
+    // the KV cache holds layers * kv heads * max_positions * 128 floats twice
+    // (Qwen3's 40960 positions: 9.4 GB at 0.6B); every position index is 64-bit
+    if (c->max_positions > (1u << 20)) return fail(LQ8_ERR_MODEL, "max_positions > 1048576 not supported");
     if (c->hidden_size > (uint32_t)GEMV_MAX_K || c->intermediate_size > (uint32_t)GEMV_MAX_K ||
         c->num_heads * c->head_dim > (uint32_t)GEMV_MAX_K)
         return fail(LQ8_ERR_MODEL, "dimensions above 12288 not supported");

@@ -43,15 +43,16 @@ __global__ __launch_bounds__(64) void k_qk_rope_kv(QkRopeLaunch a) {
 
 
 // Decode attention, one workgroup per (kv head, group of HG of its G query
-// heads, segment of 64 positions).  Every workgroup normalizes and rotates
-// its HG query heads; the workgroups of the last segment also normalize and
-// rotate the new key and use key and value from LDS, and the one of head
-// group 0 appends them to the cache at the position.  Output: per (segment,
-// q head) o_c[128], m_c, l_c at part[(c * H + h) * ATT_PART_STRIDE].
+// heads, segment slot y), which takes the segments of 64 positions y, y +
+// gridDim.y, ... in use.  Every workgroup normalizes and rotates its HG query
+// heads; the workgroups of the last segment also normalize and rotate the
+// new key and use key and value from LDS, and the one of head group 0
+// appends them to the cache at the position.  Output: per (segment, q head)
+// o_c[128], m_c, l_c at part[(c * H + h) * ATT_PART_STRIDE].
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     extern __shared__ float sm[];
     const int G = a.num_heads / a.num_kv_heads, HG = a.head_group, NG = G / HG;
-    const int kvh = blockIdx.x / NG, hg = blockIdx.x - kvh * NG, c = blockIdx.y, b = blockIdx.z;
+    const int kvh = blockIdx.x / NG, hg = blockIdx.x - kvh * NG, c0 = blockIdx.y, b = blockIdx.z;
     const int h0 = kvh * G + hg * HG;  // this workgroup's first query head
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -62,15 +63,14 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     a.part += b * a.part_stride;
     const float* Kc = a.k_cache + (size_t)kvh * a.max_pos * 128;
     const float* Vc = a.v_cache + (size_t)kvh * a.max_pos * 128;
-    const int js = c * SEG;
     // Loads that do not depend on the position go out before it arrives: the
     // K/V rows of the first ATT_EARLY_SEGS segments of a single sequence
     // (almost always in use; later segments, and batches, whose idle
     // workgroups would multiply the waste, wait) and this wave's first head
     // vector (q head `wave`, or the new k / v).
     float4 kreg[ATT_F4], vreg[ATT_F4];
-    const bool early = c < ATT_EARLY_SEGS && gridDim.z == 1;
-    if (early) seg_load_capacity(Kc, Vc, js, a.max_pos, kreg, vreg);
+    const bool early = c0 < ATT_EARLY_SEGS && gridDim.z == 1;
+    if (early) seg_load_capacity(Kc, Vc, c0 * SEG, a.max_pos, kreg, vreg);
     float x0 = 0.0f, x1 = 0.0f, n0 = 0.0f, n1 = 0.0f;
     if (wave < HG + 2) {
         const float* src = wave < HG ? a.qkv + (h0 + wave) * 128
@@ -88,56 +88,63 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     const int C = (L + SEG - 1) / SEG;
     // before any barrier: the whole workgroup leaves (a position outside the
     // cache writes nothing)
-    if (c >= C || pos < 0 || pos >= a.max_pos) return;
-    const int nj = min(SEG, L - js);
-    const bool last = c == C - 1;
-    const int newrow = last ? pos - js : -1;
+    if (c0 >= C || pos < 0 || pos >= a.max_pos) return;
     float* qs = sm;                      // [HG][128]
     float* kn = qs + HG * 128;           // [128]
     float* vn = kn + 128;                // [128]
     float* sc = vn + 128;                // [HG][64]
     float* mlc = sc + HG * SEG;          // [HG][2]
     float* ks = sm + seg_ks_off(HG);     // [64][KPAD], later vs [64][128]
-    if (!early) seg_load(Kc, Vc, js, nj, kreg, vreg);
     const float* cs = a.cos_t + (size_t)pos * 64;
     const float* sn = a.sin_t + (size_t)pos * 64;
-    for (int t = wave; t < HG + 2; t += ATT_THREADS / 64) {
-        if (t < HG) {
-            if (t == wave) head_norm_rope_vals(x0, x1, n0, n1, cs, sn, a.eps, qs + t * 128);
-            else head_norm_rope(a.qkv + (h0 + t) * 128, a.q_norm, cs, sn, a.eps, qs + t * 128);
-        } else if (t == HG && last) {
-            if (t == wave) head_norm_rope_vals(x0, x1, n0, n1, cs, sn, a.eps, kn);
-            else head_norm_rope(a.qkv + QD + kvh * 128, a.k_norm, cs, sn, a.eps, kn);
-            if (hg == 0) {
-                float* kr = a.k_cache + ((size_t)kvh * a.max_pos + pos) * 128;
-                kr[lane] = kn[lane];
-                kr[lane + 64] = kn[lane + 64];
-            }
-        } else if (t == HG + 1 && last) {
-            const float* v = a.qkv + QD + KD + kvh * 128;
-            const float v0 = t == wave ? x0 : v[lane], v1 = t == wave ? x1 : v[lane + 64];
-            vn[lane] = v0;
-            vn[lane + 64] = v1;
-            if (hg == 0) {
-                float* vr = a.v_cache + ((size_t)kvh * a.max_pos + pos) * 128;
-                vr[lane] = v0;
-                vr[lane + 64] = v1;
+    // segments c0, c0 + gridDim.y, ... (every workgroup of the launch takes
+    // the same number of rounds of its own; the rounds after the first wait
+    // for the previous one's reads of the LDS regions)
+    for (int c = c0; c < C; c += gridDim.y) {
+        if (c != c0) __syncthreads();
+        const int js = c * SEG;
+        const int nj = min(SEG, L - js);
+        const bool last = c == C - 1;
+        const int newrow = last ? pos - js : -1;
+        if (!(early && c == c0)) seg_load(Kc, Vc, js, nj, kreg, vreg);
+        for (int t = wave; t < HG + 2; t += ATT_THREADS / 64) {
+            if (t < HG) {
+                if (t == wave) head_norm_rope_vals(x0, x1, n0, n1, cs, sn, a.eps, qs + t * 128);
+                else head_norm_rope(a.qkv + (h0 + t) * 128, a.q_norm, cs, sn, a.eps, qs + t * 128);
+            } else if (t == HG && last) {
+                if (t == wave) head_norm_rope_vals(x0, x1, n0, n1, cs, sn, a.eps, kn);
+                else head_norm_rope(a.qkv + QD + kvh * 128, a.k_norm, cs, sn, a.eps, kn);
+                if (hg == 0) {
+                    float* kr = a.k_cache + ((size_t)kvh * a.max_pos + pos) * 128;
+                    kr[lane] = kn[lane];
+                    kr[lane + 64] = kn[lane + 64];
+                }
+            } else if (t == HG + 1 && last) {
+                const float* v = a.qkv + QD + KD + kvh * 128;
+                const float v0 = t == wave ? x0 : v[lane], v1 = t == wave ? x1 : v[lane + 64];
+                vn[lane] = v0;
+                vn[lane + 64] = v1;
+                if (hg == 0) {
+                    float* vr = a.v_cache + ((size_t)kvh * a.max_pos + pos) * 128;
+                    vr[lane] = v0;
+                    vr[lane + 64] = v1;
+                }
             }
         }
-    }
-    __syncthreads();
-    seg_scores(kreg, nj, newrow, kn, qs, HG, a.scale, ks, sc, mlc);
-    __syncthreads();
-    seg_stage_v(vreg, nj, newrow, vn, ks);
-    __syncthreads();
-    for (int t = tid; t < HG * 128; t += ATT_THREADS) {
-        const int h = t >> 7, d = t & 127;
-        const float o = pv_chain(sc + h * SEG, ks, d, nj);
-        float* p = a.part + ((size_t)c * a.num_heads + h0 + h) * ATT_PART_STRIDE;
-        p[d] = o;
-        if (d == 0) {
-            p[128] = mlc[2 * h];
-            p[129] = mlc[2 * h + 1];
+        __syncthreads();
+        seg_scores(kreg, nj, newrow, kn, qs, HG, a.scale, ks, sc, mlc);
+        __syncthreads();
+        seg_stage_v(vreg, nj, newrow, vn, ks);
+        __syncthreads();
+        for (int t = tid; t < HG * 128; t += ATT_THREADS) {
+            const int h = t >> 7, d = t & 127;
+            const float o = pv_chain(sc + h * SEG, ks, d, nj);
+            float* p = a.part + ((size_t)c * a.num_heads + h0 + h) * ATT_PART_STRIDE;
+            p[d] = o;
+            if (d == 0) {
+                p[128] = mlc[2 * h];
+                p[129] = mlc[2 * h + 1];
+            }
         }
     }
 }
@@ -359,6 +366,9 @@ __global__ void k_silu(const float* __restrict__ x, size_t n, float* __restrict_
 
 inline unsigned grid1(size_t n, unsigned block) { return (unsigned)((n + block - 1) / block); }
 
+constexpr int ATT_WG_TARGET = 512;  // decode attention workgroups sought per launch (2 per CU)
+constexpr int ATT_MIN_SLOTS = 8;    // segment slots at least (512 positions without a second round)
+
 size_t seg_smem(int G) { return ((size_t)seg_ks_off(G) + (size_t)SEG * KPAD) * sizeof(float); }
 size_t rows_smem(int G) { return ((size_t)rows_ks_off(G) + (size_t)SEG * KPAD) * sizeof(float); }
 
@@ -386,7 +396,13 @@ lq8_status launch_attention_seg(hipStream_t s, const AttnSegLaunch& a) {
     AttnSegLaunch b = a;
     if (b.head_group <= 0 || G % b.head_group) b.head_group = G;
     const int NG = G / b.head_group;
-    hipLaunchKernelGGL(k_attn_seg, dim3((unsigned)(a.num_kv_heads * NG), (unsigned)cmax, (unsigned)a.batch),
+    // segment slots: all cmax segments up to about ATT_WG_TARGET workgroups
+    // (at least ATT_MIN_SLOTS slots); a long max_positions (Qwen3's 40960:
+    // 640 segments) no longer launches a workgroup per segment of capacity,
+    // almost all of them idle, and a workgroup loops over its segments
+    const int per_slot = a.num_kv_heads * NG * a.batch;
+    const int slots = std::min(cmax, std::max(ATT_MIN_SLOTS, (ATT_WG_TARGET + per_slot - 1) / per_slot));
+    hipLaunchKernelGGL(k_attn_seg, dim3((unsigned)(a.num_kv_heads * NG), (unsigned)slots, (unsigned)a.batch),
                        dim3(ATT_THREADS), seg_smem(b.head_group), s, b);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;

@@ -301,8 +301,8 @@ lq8_status validate(const lq8_moe_config* c) {
         return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: top_k must be 1..min(num_experts, 16)");
     if (c->max_batch == 0 || c->max_batch > MOE_MAX_BATCH)
         return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: max_batch must be 1..64");
-    if (c->max_positions == 0 || c->max_positions > 8192)
-        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: max_positions must be 1..8192");
+    if (c->max_positions == 0 || c->max_positions > (1u << 20))
+        return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: max_positions must be 1..1048576");
     if (c->num_layers == 0) return fail(LQ8_ERR_SHAPE_MISMATCH, "moe: num_layers must be positive");
     return LQ8_OK;
 }

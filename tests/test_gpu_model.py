@@ -611,6 +611,47 @@ def test_graph_path_down_chunks(ctx, hidden, inter):
     ref.close()
 
 
+@pytest.mark.parametrize("heads,kv,max_pos,n_prompt", [
+    (16, 8, 40960, 40),    # Qwen3-0.6B / 1.7B heads at Qwen3's max_position_embeddings (640 segments)
+    (32, 8, 40960, 40),    # Qwen3-4B heads
+    (4, 2, 8192, 4160),    # decode at 66 segments: the combine's coefficients in two batches
+    (16, 8, 16384, 4100),  # 65 segments with 16 heads
+])
+def test_graph_path_long_positions(ctx, heads, kv, max_pos, n_prompt):
+    """The per-step kernels at long max_positions: the o projection's
+    attention-combine staging holds the coefficients of at most 64 segments
+    in LDS at a time (each head's running maximum and denominator, each
+    element's running numerator carried between batches), so any
+    max_positions fits its LDS and a position beyond 4096 combines in
+    batches.  Prompt, two KV-cached decode steps bit-identical to the
+    oracle's logits; greedy and sampled tokens of the replayed graph equal
+    to the oracle's."""
+    cfg = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                          num_attention_heads=heads, num_key_value_heads=kv, head_dim=128,
+                          max_position_embeddings=max_pos)
+    tensors = varied_small(cfg, heads * 1000 + n_prompt)
+    model = lq8.Qwen3ForCausalLM.load(ctx, cfg, tensors)
+    ref = oracle.Model(cfg, tensors)
+    prompt = np.random.default_rng(n_prompt).integers(0, cfg.vocab_size, n_prompt).astype(np.uint32)
+    lg = ref.forward(prompt, 0)
+    assert same_bits(model.forward(prompt, 0), lg)
+    for t in range(2):
+        tok = int(np.argmax(lg))
+        lg = ref.forward([tok], n_prompt + t)
+        step = model.forward([tok], n_prompt + t)
+        assert same_bits(step, lg), f"decode step at {n_prompt + t}: max|d| {np.max(np.abs(step - lg))}"
+    ref.clear_kv_cache()
+    toks, st = with_path("graph", lambda: model.generate_greedy(prompt, 12))
+    ref_toks, _ = ref.generate_greedy(prompt, 12)
+    assert st["used_graph"]
+    assert toks.tolist() == ref_toks.tolist()
+    ref.clear_kv_cache()
+    stoks, _ = model.generate(prompt, lq8.GenerationConfig(12, 0.8, 50, 0.95, 1.1), seed=7)
+    assert stoks.tolist() == ref.generate_sampled(prompt, 12, 0.8, 50, 0.95, 1.1, 7).tolist()
+    model.free()
+    ref.close()
+
+
 def expected_picks(logits, P, pw=8):
     """Each workgroup's pick over its lm_head rows: rows of the 16-row tiles t
     with (t // pw) % P == w; the largest value, the last index on ties."""

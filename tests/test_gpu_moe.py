@@ -53,6 +53,18 @@ def test_moe_batch1_across_segments(ctx):
     run_steps(ctx, cfg, tens, 1, [62], 4, 22)      # positions 62..65 cross the 64-position segment edge
 
 
+@pytest.mark.parametrize("pos0,T", [([100], 1), ([4150], 1), ([4150, 90], 2)])
+def test_moe_long_max_positions(ctx, pos0, T):
+    """Qwen3-30B-A3B's heads (32 query, 4 kv) at max_positions 40960 (640
+    attention segments): the batch-1 o projection's segment combine holds the
+    coefficients of at most 64 segments in LDS at a time, so it fits; position
+    4150 combines 65 segments in two batches (batch 1) or through the combine
+    kernel (batch 2)."""
+    cfg = MoeCfg(num_heads=32, num_kv_heads=4, num_experts=16, top_k=4, max_positions=40960, max_batch=2,
+                 num_layers=2)
+    run_steps(ctx, cfg, moe_tensors(cfg, 31), T, pos0, 2, 32)
+
+
 def test_moe_batched_decode(ctx):
     cfg = MoeCfg(num_experts=16, top_k=4, max_positions=200, max_batch=8, num_layers=2)
     tens = moe_tensors(cfg, 23)
