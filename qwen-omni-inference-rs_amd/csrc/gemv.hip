@@ -1269,6 +1269,8 @@ __global__ __launch_bounds__(1024) void k_argmax_final(const float* __restrict__
     }
 }
 
+constexpr int MANY_TILES = 512;  // 16-row tiles from which a GEMV takes the many-tiles launch shape
+
 template <int XS, int EPI>
 lq8_status launch_one(hipStream_t s, const GemvArgs& a) {
     const int nb = a.k >> 5, npf = (nb + 1) >> 1;
@@ -1276,15 +1278,18 @@ lq8_status launch_one(hipStream_t s, const GemvArgs& a) {
     const int np = EPI == EPI_PART ? std::min(npf, a.part_pairs) : npf;
     const int nch = EPI == EPI_PART ? (npf + a.part_pairs - 1) / a.part_pairs : 1;
     const int tiles = (a.n + TILE_ROWS - 1) / TILE_ROWS;
-    // Many tiles (lm_head): 4 pairs per item, 4-wave workgroups with the next
-    // item's weights prefetched; a plain input takes one tile per workgroup,
-    // a transformed one (RMSNorm) is staged once for 2 tiles (151936 x 1024:
-    // 26.8 / 27.9 / 29.2 us plain and 1246 / 1248 / 1244 decode tok/s at 1 / 2
-    // / 4 tiles).  Few tiles: one tile per workgroup and up to 16 waves to
-    // spread it over the CU.
+    // Many tiles (lm_head, and from two per CU: MANY_TILES): 4 pairs per
+    // item, 4-wave workgroups with the next item's weights prefetched; a plain
+    // input takes one tile per workgroup, a transformed one (RMSNorm) is
+    // staged once for 2 tiles (151936 x 1024: 26.8 / 27.9 / 29.2 us plain and
+    // 1246 / 1248 / 1244 decode tok/s at 1 / 2 / 4 tiles).  Few tiles: one
+    // tile per workgroup and up to 16 waves to spread it over the CU.  The
+    // boundary, measured on greedy decode: Qwen3-1.7B's gate|up (768 tiles)
+    // 1036 -> 1079 tok/s as many, Qwen3-4B's q|k|v (384 tiles, K 2560) 575 ->
+    // 565 and its gate|up (1216 tiles) 575 -> 519 as few.
     int ch, tpw, waves;
-    const int wmax = tiles >= 1024 ? 4 : MAX_WAVES;
-    if (tiles >= 1024) {
+    const int wmax = tiles >= MANY_TILES ? 4 : MAX_WAVES;
+    if (tiles >= MANY_TILES) {
         ch = MAX_CH;
         tpw = XS == XS_PLAIN ? 1 : 2;
     } else {

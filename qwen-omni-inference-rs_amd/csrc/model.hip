@@ -571,7 +571,7 @@ int persist_target_wg(const lq8_model* m) {
 // Whether greedy decode runs as the persistent kernel: by default where the
 // shape is supported up to hidden 1024 (its first instance; above, the
 // replayed per-step kernels with the down projection in input chunks are
-// faster: Qwen3-1.7B shapes 1037 against 1011 tok/s); LQ8_PERSIST=1 wherever
+// faster: Qwen3-1.7B shapes 1075 against 1007 tok/s); LQ8_PERSIST=1 wherever
 // the shape is supported, LQ8_PERSIST=0 never (the per-step kernels,
 // replayed as a graph, or as plain launches under LQ8_NO_GRAPH).
 bool persist_wanted(const lq8_model* m) {
