@@ -44,11 +44,14 @@ __global__ __launch_bounds__(64) void k_qk_rope_kv(QkRopeLaunch a) {
 
 // Decode attention, one workgroup per (kv head, group of HG of its G query
 // heads, segment slot y), which takes the segments of 64 positions y, y +
-// gridDim.y, ... in use.  Every workgroup normalizes and rotates its HG query
+// gridDim.y, ... in use (ROUNDS; otherwise there are as many slots as
+// segments of capacity, and the instance without the loop keeps its
+// registers: 73 VGPRs against 148).  Every workgroup normalizes and rotates its HG query
 // heads; the workgroups of the last segment also normalize and rotate the
 // new key and use key and value from LDS, and the one of head group 0
 // appends them to the cache at the position.  Output: per (segment, q head)
 // o_c[128], m_c, l_c at part[(c * H + h) * ATT_PART_STRIDE].
+template <bool ROUNDS>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     extern __shared__ float sm[];
     const int G = a.num_heads / a.num_kv_heads, HG = a.head_group, NG = G / HG;
@@ -100,8 +103,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
     // segments c0, c0 + gridDim.y, ... (every workgroup of the launch takes
     // the same number of rounds of its own; the rounds after the first wait
     // for the previous one's reads of the LDS regions)
-    for (int c = c0; c < C; c += gridDim.y) {
-        if (c != c0) __syncthreads();
+    for (int c = c0;;) {
         const int js = c * SEG;
         const int nj = min(SEG, L - js);
         const bool last = c == C - 1;
@@ -146,6 +148,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_seg(AttnSegLaunch a) {
                 p[129] = mlc[2 * h + 1];
             }
         }
+        if (!ROUNDS) break;
+        c += gridDim.y;
+        if (c >= C) break;
+        __syncthreads();  // the next round's writes wait for this round's reads of the LDS regions
     }
 }
 
@@ -402,8 +408,9 @@ lq8_status launch_attention_seg(hipStream_t s, const AttnSegLaunch& a) {
     // almost all of them idle, and a workgroup loops over its segments
     const int per_slot = a.num_kv_heads * NG * a.batch;
     const int slots = std::min(cmax, std::max(ATT_MIN_SLOTS, (ATT_WG_TARGET + per_slot - 1) / per_slot));
-    hipLaunchKernelGGL(k_attn_seg, dim3((unsigned)(a.num_kv_heads * NG), (unsigned)slots, (unsigned)a.batch),
-                       dim3(ATT_THREADS), seg_smem(b.head_group), s, b);
+    const dim3 grid((unsigned)(a.num_kv_heads * NG), (unsigned)slots, (unsigned)a.batch);
+    if (slots < cmax) hipLaunchKernelGGL(k_attn_seg<true>, grid, dim3(ATT_THREADS), seg_smem(b.head_group), s, b);
+    else hipLaunchKernelGGL(k_attn_seg<false>, grid, dim3(ATT_THREADS), seg_smem(b.head_group), s, b);
     LQ8_HIP(hipGetLastError());
     return LQ8_OK;
 }
