@@ -18,7 +18,8 @@ are reported beside it (greedy decode on its default path, the persistent
 kernel, and on the replayed graph; the same greedy decode at Qwen3-1.7B and
 Qwen3-4B shapes, random weights, on the default path -- the replayed graph
 above hidden 1024 --, the graph, and the persistent kernel where the shape
-fits it), and so is the host-pointer
+fits it; Qwen3-0.6B again with its own max_positions, 40960), and so is the
+host-pointer
 Linear::forward per call at the seven layer shapes.  The CPU
 baseline is a C restatement of the reference's own CPU Linear::forward (BF16
 weight, per-call transpose, BF16 -> F32 copy, naive matmul_2d) timed on one
@@ -625,6 +626,10 @@ def main():
         if not args.no_cpu:
             cpu_model = (cfg, model.export_all(), prompt)
         model.free()
+        # the same model with Qwen3-0.6B's own max_position_embeddings (a 9.4 GB
+        # KV cache; 640 attention segments of capacity, 3 in use)
+        decode["qwen3_0_6b_max_positions_40960"] = decode_larger(ctx, lq8.qwen3_0_6b(max_positions=40960),
+                                                                 "Qwen3-0.6B, max_positions 40960")
         decode["qwen3_1_7b"] = decode_larger(ctx, lq8.qwen3_1_7b(max_positions=512), "Qwen3-1.7B")
         decode["qwen3_4b"] = decode_larger(ctx, lq8.qwen3_4b(max_positions=512), "Qwen3-4B")
 
