@@ -624,7 +624,8 @@ def test_graph_path_long_positions(ctx, heads, kv, max_pos, n_prompt):
     element's running numerator carried between batches), so any
     max_positions fits its LDS and a position beyond 4096 combines in
     batches.  Prompt, two KV-cached decode steps bit-identical to the
-    oracle's logits; greedy and sampled tokens of the replayed graph equal
+    oracle's logits; greedy and sampled tokens of the replayed graph, and the
+    persistent kernel's greedy tokens where its plan takes the shape, equal
     to the oracle's."""
     cfg = lq8.Qwen3Config(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
                           num_attention_heads=heads, num_key_value_heads=kv, head_dim=128,
@@ -645,6 +646,12 @@ def test_graph_path_long_positions(ctx, heads, kv, max_pos, n_prompt):
     ref_toks, _ = ref.generate_greedy(prompt, 12)
     assert st["used_graph"]
     assert toks.tolist() == ref_toks.tolist()
+    if lq8.persist_plan(cfg, 256)["supported"]:
+        # the persistent kernel at the same max_positions (its partials sized
+        # for every segment of capacity, its combine streaming the ones in use)
+        ptoks, pst = with_path("persistent", lambda: model.generate_greedy(prompt, 12))
+        assert pst["used_persistent"]
+        assert ptoks.tolist() == ref_toks.tolist()
     ref.clear_kv_cache()
     stoks, _ = model.generate(prompt, lq8.GenerationConfig(12, 0.8, 50, 0.95, 1.1), seed=7)
     assert stoks.tolist() == ref.generate_sampled(prompt, 12, 0.8, 50, 0.95, 1.1, 7).tolist()
