@@ -71,9 +71,10 @@ def test_offset_must_match_cache(small_pair):
 
 
 def with_path(path, fn):
-    """Run fn with the greedy decode path forced: "persistent" (the persistent
-    kernel, the default), "graph" (LQ8_PERSIST=0: the replayed graph) or
-    "plain" (LQ8_PERSIST=0 and LQ8_NO_GRAPH: kernel launches)."""
+    """Run fn with the greedy decode path forced: "persistent" (LQ8_PERSIST=1:
+    the persistent kernel, the default up to hidden 1024), "graph"
+    (LQ8_PERSIST=0: the replayed graph) or "plain" (LQ8_PERSIST=0 and
+    LQ8_NO_GRAPH: kernel launches)."""
     keys = ("LQ8_PERSIST", "LQ8_NO_GRAPH")
     old = {k: os.environ.pop(k, None) for k in keys}
     if path == "persistent":
